@@ -1,0 +1,135 @@
+"""CPU oracle for the quantized linear-layer path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this package, and only as the checker or the timed
+CPU baseline.  The product (``unillm_amd``) never imports it.
+
+It wraps ``oracle/liboracle.so`` (built from ``oracle/oracle.c`` by
+``oracle/Makefile``) with numpy-friendly functions.  What each function
+restates, and what pins it, is documented in ``oracle/oracle.h``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+Q4_0 = 2
+Q8_0 = 8
+QK = 32
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34}
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+
+def build() -> None:
+    """Compile liboracle.so with the committed Makefile."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        l = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        I64 = ctypes.c_int64
+        l.oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+        l.oracle_f16_to_f32.restype = ctypes.c_float
+        l.oracle_f32_to_f16.argtypes = [ctypes.c_float]
+        l.oracle_f32_to_f16.restype = ctypes.c_uint16
+        l.oracle_quantize.argtypes = [ctypes.c_int, P, I64, I64, P]
+        l.oracle_dequant.argtypes = [ctypes.c_int, P, I64, I64, P]
+        l.oracle_qmatmul_f64.argtypes = [ctypes.c_int, P, P, I64, I64, I64, P, ctypes.c_int]
+        l.oracle_candle_qmatmul.argtypes = [ctypes.c_int, P, P, I64, I64, I64, P, ctypes.c_int]
+        l.oracle_fill_normal.argtypes = [P, I64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double]
+        l.oracle_fill_normal.restype = None
+        _lib = l
+    return _lib
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def f16_to_f32(h: int) -> float:
+    return lib().oracle_f16_to_f32(h)
+
+
+def f32_to_f16(f: float) -> int:
+    return lib().oracle_f32_to_f16(f)
+
+
+def normal(count: int, seed: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(count, dtype=np.float32)
+    lib().oracle_fill_normal(_ptr(out), count, seed, mean, std)
+    return out
+
+
+def quantize(qtype: int, w: np.ndarray) -> np.ndarray:
+    """f32 [n, k] -> GGUF block bytes (uint8 [n, k/32 * block_bytes])."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, k = w.shape
+    out = np.empty((n, (k // QK) * BLOCK_BYTES[qtype]), dtype=np.uint8)
+    if lib().oracle_quantize(qtype, _ptr(w), n, k, _ptr(out)) != 0:
+        raise ValueError(f"oracle_quantize rejected qtype={qtype} n={n} k={k}")
+    return out
+
+
+def dequant(qtype: int, blocks: np.ndarray, n: int, k: int) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    assert blocks.size == n * (k // QK) * BLOCK_BYTES[qtype]
+    out = np.empty((n, k), dtype=np.float32)
+    if lib().oracle_dequant(qtype, _ptr(blocks), n, k, _ptr(out)) != 0:
+        raise ValueError("oracle_dequant rejected its arguments")
+    return out
+
+
+def qmatmul_f64(qtype: int, blocks: np.ndarray, x: np.ndarray, n: int, k: int,
+                nthreads: int = 0) -> np.ndarray:
+    """The parity oracle: x[m, k] . dequant(W)[n, k]^T accumulated in f64."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, k)
+    m = x.shape[0]
+    y = np.empty((m, n), dtype=np.float64)
+    if lib().oracle_qmatmul_f64(qtype, _ptr(blocks), _ptr(x), m, n, k, _ptr(y), nthreads) != 0:
+        raise ValueError("oracle_qmatmul_f64 rejected its arguments")
+    return y
+
+
+def candle_qmatmul(qtype: int, blocks: np.ndarray, x: np.ndarray, n: int, k: int,
+                   nthreads: int = 0) -> np.ndarray:
+    """candle CPU QMatMul semantics (Q8_0 activations, integer block dots)."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, k)
+    m = x.shape[0]
+    y = np.empty((m, n), dtype=np.float32)
+    if lib().oracle_candle_qmatmul(qtype, _ptr(blocks), _ptr(x), m, n, k, _ptr(y), nthreads) != 0:
+        raise ValueError("oracle_candle_qmatmul rejected its arguments")
+    return y
+
+
+def normwise_error(y: np.ndarray, ref: np.ndarray) -> float:
+    """max|y - r| / max|r|, the tolerance measure used by every parity test."""
+    ref = np.asarray(ref, dtype=np.float64)
+    denom = float(np.max(np.abs(ref))) if ref.size else 0.0
+    err = float(np.max(np.abs(np.asarray(y, dtype=np.float64) - ref))) if ref.size else 0.0
+    return err / denom if denom > 0 else err
+
+
+def elementwise_error(y: np.ndarray, ref: np.ndarray, floor: float = 1e-3) -> float:
+    """max relative error over elements with |r| > floor * max|r|."""
+    ref = np.asarray(ref, dtype=np.float64)
+    if ref.size == 0:
+        return 0.0
+    big = np.abs(ref) > floor * np.max(np.abs(ref))
+    if not big.any():
+        return 0.0
+    d = np.abs(np.asarray(y, dtype=np.float64)[big] - ref[big]) / np.abs(ref[big])
+    return float(d.max())

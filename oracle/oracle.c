@@ -1,0 +1,274 @@
+/*
+ * oracle.c -- CPU restatement of unillm's Q4_0 / Q8_0 linear-layer path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see oracle.h): the checker for the HIP kernels and
+ * the timed CPU baseline.  The product never links or calls it.
+ *
+ * Each function names the reference code it follows.  The arithmetic of the
+ * live path is in candle-core 0.8 (external, un-vendored); its GGML block
+ * formats are restated from their published definition.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+size_t oracle_block_bytes(int qtype) {
+    /* Q4_0: {f16 d; u8 qs[16]} = 18 B; Q8_0: {f16 d; i8 qs[32]} = 34 B.
+     * (The reference's in-repo Q4_0Block is 32 B because of align(32),
+     * crates/runtime/src/simd/quant/block.rs:27 -- not the GGUF stride.) */
+    if (qtype == ORACLE_Q4_0) return 18;
+    if (qtype == ORACLE_Q8_0) return 34;
+    return 0;
+}
+
+static inline uint32_t f32_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float bits_f32(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* binary16 -> binary32, exact for every code (half::f16::to_f32 semantics,
+ * used by candle's BlockQ4_0/BlockQ8_0::to_float). */
+float oracle_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1Fu;
+    uint32_t man = h & 0x3FFu;
+    if (exp == 0) {
+        if (man == 0) return bits_f32(sign);
+        /* subnormal: man * 2^-24, exact in f32 */
+        float v = (float)man * 5.9604644775390625e-08f;
+        return sign ? -v : v;
+    }
+    if (exp == 31) return bits_f32(sign | 0x7F800000u | (man << 13));
+    return bits_f32(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+/* binary32 -> binary16, round to nearest even (half::f16::from_f32 and
+ * x86 F16C _cvtss_sh(.., 0), which GGML_FP32_TO_FP16 uses). */
+uint16_t oracle_f32_to_f16(float f) {
+    uint32_t x = f32_bits(f);
+    uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) {                       /* inf or nan */
+        if (ax == 0x7F800000u) return sign | 0x7C00u;
+        return sign | 0x7E00u | (uint16_t)((ax >> 13) & 0x3FFu);
+    }
+    if (ax >= 0x477FF000u) return sign | 0x7C00u;  /* rounds to >= 65520 -> inf */
+    if (ax < 0x38800000u) {                        /* below 2^-14: subnormal or 0 */
+        if (ax < 0x33000000u) return sign;         /* < 2^-25: rounds to 0 */
+        uint32_t e = ax >> 23;
+        uint32_t m = (ax & 0x7FFFFFu) | 0x800000u;
+        uint32_t shift = 126u - e;                 /* 14..24 */
+        uint32_t q = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return sign | (uint16_t)q;
+    }
+    uint32_t e = (ax >> 23) - 112u;                /* 1..30 */
+    uint32_t m = ax & 0x7FFFFFu;
+    uint32_t q = (e << 10) | (m >> 13);
+    uint32_t rem = m & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++;  /* carries into exp */
+    return sign | (uint16_t)q;
+}
+
+static inline uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+static inline void wr16(uint8_t* p, uint16_t v) { p[0] = (uint8_t)v; p[1] = (uint8_t)(v >> 8); }
+
+/* GGML quantize_row_q4_0_reference, as candle's BlockQ4_0::from_float restates
+ * it (candle-core 0.8 quantized/k_quants.rs, external): d = max / -8 where max
+ * is the signed element of largest magnitude; q = min(15, trunc(x/d + 8.5));
+ * low nibble of qs[j] holds element j, high nibble element j + 16. */
+static void quantize_block_q4_0(const float* x, uint8_t* out) {
+    float amax = 0.0f, max = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+        float v = x[j];
+        if (amax < fabsf(v)) { amax = fabsf(v); max = v; }
+    }
+    const float d = max / -8.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    wr16(out, oracle_f32_to_f16(d));
+    for (int j = 0; j < 16; ++j) {
+        const float x0 = x[j] * id;
+        const float x1 = x[j + 16] * id;
+        int q0 = (int)(int8_t)(x0 + 8.5f);
+        int q1 = (int)(int8_t)(x1 + 8.5f);
+        if (q0 > 15) q0 = 15;
+        if (q1 > 15) q1 = 15;
+        out[2 + j] = (uint8_t)(q0 | (q1 << 4));
+    }
+}
+
+/* GGML quantize_row_q8_0_reference / candle BlockQ8_0::from_float:
+ * d = amax / 127; q = round-half-away(x / d). */
+static void quantize_block_q8_0(const float* x, uint8_t* out) {
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+        float a = fabsf(x[j]);
+        if (a > amax) amax = a;
+    }
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    wr16(out, oracle_f32_to_f16(d));
+    for (int j = 0; j < 32; ++j) out[2 + j] = (uint8_t)(int8_t)roundf(x[j] * id);
+}
+
+int oracle_quantize(int qtype, const float* w, int64_t n, int64_t k, uint8_t* blocks) {
+    const size_t bb = oracle_block_bytes(qtype);
+    if (!bb || k % 32 || n < 0 || k < 0) return -1;
+    const int64_t kb = k / 32;
+    for (int64_t r = 0; r < n; ++r)
+        for (int64_t b = 0; b < kb; ++b) {
+            const float* src = w + r * k + b * 32;
+            uint8_t* dst = blocks + (size_t)(r * kb + b) * bb;
+            if (qtype == ORACLE_Q4_0) quantize_block_q4_0(src, dst);
+            else quantize_block_q8_0(src, dst);
+        }
+    return 0;
+}
+
+/* BlockQ4_0::to_float / BlockQ8_0::to_float (candle, external), reached from
+ * qtensor.dequantize at crates/runtime/src/weight_loader_core.rs:579.  The
+ * products are exact in f32 (<= 8-bit integer times an 11-bit significand). */
+static void dequant_block(int qtype, const uint8_t* blk, float* y) {
+    const float d = oracle_f16_to_f32(rd16(blk));
+    const uint8_t* qs = blk + 2;
+    if (qtype == ORACLE_Q4_0) {
+        for (int j = 0; j < 16; ++j) {
+            y[j] = (float)((int)(qs[j] & 0x0F) - 8) * d;
+            y[j + 16] = (float)((int)(qs[j] >> 4) - 8) * d;
+        }
+    } else {
+        for (int j = 0; j < 32; ++j) y[j] = (float)(int8_t)qs[j] * d;
+    }
+}
+
+int oracle_dequant(int qtype, const uint8_t* blocks, int64_t n, int64_t k, float* out) {
+    const size_t bb = oracle_block_bytes(qtype);
+    if (!bb || k % 32 || n < 0 || k < 0) return -1;
+    const int64_t kb = k / 32;
+    for (int64_t r = 0; r < n; ++r)
+        for (int64_t b = 0; b < kb; ++b)
+            dequant_block(qtype, blocks + (size_t)(r * kb + b) * bb, out + r * k + b * 32);
+    return 0;
+}
+
+/* The parity oracle: the f32-fallback semantics of quantized_matmul
+ * (crates/runtime/src/models_v2/llama.rs:1193 -> ops_fn::matmul ->
+ * CpuTensorOpsImpl::matmul, crates/runtime/src/tensor_core.rs:843-892):
+ * y = x . dequant(W)^T, here accumulated in f64 so it is a reference for any
+ * f32 summation order.  x is [m, k] row-major (the 3-D [B, T, K] case of
+ * tensor_core.rs:857-871 reshapes to [B*T, K]), W is [n, k] blocks. */
+int oracle_qmatmul_f64(int qtype, const uint8_t* blocks, const float* x,
+                       int64_t m, int64_t n, int64_t k, double* y, int nthreads) {
+    const size_t bb = oracle_block_bytes(qtype);
+    if (!bb || k % 32 || n < 0 || k < 0 || m < 0) return -1;
+    const int64_t kb = k / 32;
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel
+#endif
+    {
+        float* wrow = (float*)malloc(sizeof(float) * (size_t)(k ? k : 1));
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+        for (int64_t c = 0; c < n; ++c) {
+            for (int64_t b = 0; b < kb; ++b)
+                dequant_block(qtype, blocks + (size_t)(c * kb + b) * bb, wrow + b * 32);
+            for (int64_t r = 0; r < m; ++r) {
+                const float* xr = x + r * k;
+                double acc = 0.0;
+                for (int64_t i = 0; i < k; ++i) acc += (double)xr[i] * (double)wrow[i];
+                y[r * n + c] = acc;
+            }
+        }
+        free(wrow);
+    }
+    return 0;
+}
+
+/* ---- candle CPU QMatMul semantics (the timing baseline) -------------------
+ * QMatMul::forward -> QTensor CustomOp1 cpu_fwd -> k_quants::matmul
+ * (candle-core 0.8, external; called at llama.rs:1188, 1329, 399):
+ *   1. each activation row is quantized to Q8_0 (VecDotType of Q4_0 and Q8_0);
+ *   2. for each row, a rayon parallel-for over the N output columns
+ *      (with_min_len 128, with_max_len 512) runs vec_dot over K/32 blocks:
+ *      integer block dot, then sumf += isum * f32(d_w) * f32(d_x).
+ * Restated with OpenMP dynamic chunks of 256 columns. */
+static float vec_dot_q4_0_q8_0(const uint8_t* w, const uint8_t* xq, int64_t kb) {
+    float sumf = 0.0f;
+    for (int64_t b = 0; b < kb; ++b, w += 18, xq += 34) {
+        const uint8_t* qs = w + 2;
+        const int8_t* ys = (const int8_t*)(xq + 2);
+        int isum = 0;
+        for (int j = 0; j < 16; ++j) {
+            isum += ((int)(qs[j] & 0x0F) - 8) * ys[j];
+            isum += ((int)(qs[j] >> 4) - 8) * ys[j + 16];
+        }
+        sumf += (float)isum * oracle_f16_to_f32(rd16(w)) * oracle_f16_to_f32(rd16(xq));
+    }
+    return sumf;
+}
+
+static float vec_dot_q8_0_q8_0(const uint8_t* w, const uint8_t* xq, int64_t kb) {
+    float sumf = 0.0f;
+    for (int64_t b = 0; b < kb; ++b, w += 34, xq += 34) {
+        const int8_t* qs = (const int8_t*)(w + 2);
+        const int8_t* ys = (const int8_t*)(xq + 2);
+        int isum = 0;
+        for (int j = 0; j < 32; ++j) isum += qs[j] * ys[j];
+        sumf += (float)isum * oracle_f16_to_f32(rd16(w)) * oracle_f16_to_f32(rd16(xq));
+    }
+    return sumf;
+}
+
+int oracle_candle_qmatmul(int qtype, const uint8_t* blocks, const float* x,
+                          int64_t m, int64_t n, int64_t k, float* y, int nthreads) {
+    const size_t bb = oracle_block_bytes(qtype);
+    if (!bb || k % 32 || n < 0 || k < 0 || m < 0) return -1;
+    const int64_t kb = k / 32;
+    uint8_t* xq = (uint8_t*)malloc((size_t)(m * kb * 34) + 1);
+    if (!xq) return -2;
+    oracle_quantize(ORACLE_Q8_0, x, m, k, xq);
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#endif
+    for (int64_t r = 0; r < m; ++r) {
+        const uint8_t* xr = xq + (size_t)(r * kb * 34);
+        float* yr = y + r * n;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 256)
+#endif
+        for (int64_t c = 0; c < n; ++c) {
+            const uint8_t* wc = blocks + (size_t)(c * kb) * bb;
+            yr[c] = qtype == ORACLE_Q4_0 ? vec_dot_q4_0_q8_0(wc, xr, kb)
+                                         : vec_dot_q8_0_q8_0(wc, xr, kb);
+        }
+    }
+    free(xq);
+    return 0;
+}
+
+/* ---- synthetic inputs ------------------------------------------------------ */
+static inline uint64_t splitmix64(uint64_t* s) {
+    uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+void oracle_fill_normal(float* out, int64_t count, uint64_t seed, double mean, double std) {
+    uint64_t s = seed;
+    const double two_pi = 6.283185307179586476925286766559;
+    for (int64_t i = 0; i < count; i += 2) {
+        double u1 = ((double)(splitmix64(&s) >> 11) + 0.5) * 0x1.0p-53;
+        double u2 = ((double)(splitmix64(&s) >> 11) + 0.5) * 0x1.0p-53;
+        double r = sqrt(-2.0 * log(u1));
+        out[i] = (float)(mean + std * r * cos(two_pi * u2));
+        if (i + 1 < count) out[i + 1] = (float)(mean + std * r * sin(two_pi * u2));
+    }
+}

@@ -1,0 +1,82 @@
+/*
+ * oracle.h -- CPU restatement of unillm's quantized linear-layer path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (unillm_amd/, include/)
+ * links, loads or calls this code.  Only tests/, __graft_entry__.smoke() and
+ * the cpu_baseline leg of bench.py use it, and only as the checker / the timed
+ * CPU baseline.
+ *
+ * The reference (cognisoc/unillm) runs this path through candle-core 0.8
+ * (crates/runtime/Cargo.toml:35, un-vendored, patch version unpinned because
+ * Cargo.lock is not committed, .gitignore:4).  Candle implements the GGML
+ * block formats; this file restates the published GGML definitions:
+ *
+ *   Q4_0 block (18 B / 32 weights): { f16 d; u8 qs[16]; }
+ *        w[j]    = ((qs[j] & 0xF) - 8) * d      j = 0..15
+ *        w[j+16] = ((qs[j] >>  4) - 8) * d
+ *   Q8_0 block (34 B / 32 weights): { f16 d; i8 qs[32]; }   w[j] = qs[j] * d
+ *
+ * Call sites in the reference that this path serves:
+ *   crates/runtime/src/weight_loader_core.rs:543-584  (GGUF read, QMatMul::from_arc)
+ *   crates/runtime/src/models_v2/llama.rs:1184-1195, 1325-1336, 396-405 (forward)
+ *   crates/runtime/src/tensor_core.rs:843-892  (the f32 fallback matmul whose
+ *       semantics -- y = x . W^T in f32 with exactly dequantized W -- define parity)
+ *
+ * Parity pinning (all exercised by tests/test_oracle.py):
+ *   f16<->f32          : numpy's float16 conversions, exhaustive over 65536 codes
+ *   dequant            : closed form, exhaustive over all scales x all codes;
+ *                        the reference's layout-neutral known answers
+ *                        (simd/quant/block.rs:398-423, q4_0.rs:131-178)
+ *   quantizers         : invariants (max-magnitude element -> code 0 for Q4_0,
+ *                        round-trip error <= d/2 for Q8_0), hand-computed blocks,
+ *                        and an independent numpy restatement (tests/golden)
+ *   f64 matmul         : numpy float64 matmul (library routine), known answers
+ *                        6.3984375 / 12.796875 / 32 (simd/matmul/gemv.rs:91-113,
+ *                        simd/matmul/gemm.rs:404-429, simd/arch/avx2.rs:569-594)
+ *   candle-semantics   : loose bound (~1e-2 normwise) against the f64 oracle;
+ *   CPU path             bit-identity with candle's SIMD summation order is
+ *                        not claimed (timing baseline only).
+ */
+#ifndef UNILLM_ORACLE_H
+#define UNILLM_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORACLE_QK 32
+#define ORACLE_Q4_0 2
+#define ORACLE_Q8_0 8
+
+/* bytes per 32-weight block: 18 (Q4_0) or 34 (Q8_0); 0 for unknown types */
+size_t oracle_block_bytes(int qtype);
+
+/* IEEE binary16 <-> binary32 (round to nearest even, subnormals, inf, nan) */
+float oracle_f16_to_f32(uint16_t h);
+uint16_t oracle_f32_to_f16(float f);
+
+/* GGML reference quantizers, weights [n, k] row-major -> GGUF block bytes */
+int oracle_quantize(int qtype, const float* w, int64_t n, int64_t k, uint8_t* blocks);
+
+/* exact dequant, GGUF block bytes -> f32 [n, k] */
+int oracle_dequant(int qtype, const uint8_t* blocks, int64_t n, int64_t k, float* out);
+
+/* the parity oracle: y[m, n] = sum_k x[m, k] * dequant(W)[n, k], accumulated in f64 */
+int oracle_qmatmul_f64(int qtype, const uint8_t* blocks, const float* x,
+                       int64_t m, int64_t n, int64_t k, double* y, int nthreads);
+
+/* candle CPU semantics (timing baseline): x rows -> Q8_0, integer block dots,
+ * f32 accumulation of isum * d_w * d_x, parallel over N in column chunks */
+int oracle_candle_qmatmul(int qtype, const uint8_t* blocks, const float* x,
+                          int64_t m, int64_t n, int64_t k, float* y, int nthreads);
+
+/* deterministic N(mean, std) generator: SplitMix64 -> Box-Muller (f64) -> f32 */
+void oracle_fill_normal(float* out, int64_t count, uint64_t seed, double mean, double std);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,328 @@
+"""Benchmark of the MI355X quantized linear-layer path (one GPU).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+
+Headline: Q4_0 decode GEMV at m = 1 on the
+Llama-2-7B projection shapes.  One step is one decode pass over the linear
+layers of a 32-layer Llama-2-7B in Q4_0: per layer QKV 4096x12288,
+o_proj 4096x4096, gate 4096x11008, up 4096x11008, down 11008x4096 -- 160
+GEMV launches over 3.64 GB of distinct weights, so every launch streams its
+weights from HBM (the working set is 14x the 256 MB Infinity Cache).  The
+launches of one step are captured once in a HIP graph and replayed.
+
+value = algorithmic bytes (weights + x + y) / wall time per step, in GB/s.
+roofline.achieved uses the same bytes over the GEMV kernel's average duration,
+measured with HIP events on the stream the kernels run on.
+
+The other BASELINE configs are reported under "extra" (Q8_0 TinyLlama GEMV,
+batched decode, prefill TFLOP/s, full stack with lm_head); they are not the
+headline.  Synthetic data: weights N(0, 0.02) from torch's generator,
+quantized on the device with the GGML quantizer; activations N(0, 1).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6
+Q4_0, Q8_0 = 2, 8
+BPB = {Q4_0: 18, Q8_0: 34}
+
+LLAMA2_7B = [("qkv", 4096, 12288), ("o_proj", 4096, 4096), ("gate", 4096, 11008),
+             ("up", 4096, 11008), ("down", 11008, 4096)]
+
+
+def wbytes(qtype, n, k):
+    return n * (k // 32) * BPB[qtype]
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--only", default="", help="comma list of extra configs to run "
+                    "(q8_gemv,batched,prefill,stack) -- for profiling")
+    return ap.parse_args()
+
+
+class Timer:
+    """HIP events on the stream the kernels run on."""
+
+    def __init__(self, torch, stream):
+        self.torch = torch
+        self.stream = stream
+
+    def run(self, fn, reps):
+        t = self.torch
+        a = t.cuda.Event(enable_timing=True)
+        b = t.cuda.Event(enable_timing=True)
+        a.record(self.stream)
+        for _ in range(reps):
+            fn()
+        b.record(self.stream)
+        b.synchronize()
+        return a.elapsed_time(b) / reps  # ms
+
+
+def make_weights(torch, QuantLinear, qtype, n, k, copies, gen):
+    out = []
+    for _ in range(copies):
+        w = torch.empty(n, k, device="cuda", dtype=torch.float32)
+        w.normal_(0.0, 0.02, generator=gen)
+        out.append(QuantLinear.quantize(qtype, w))
+        del w
+    torch.cuda.synchronize()
+    return out
+
+
+def decode_stack(torch, QuantLinear, args, gen, stream):
+    """The headline: 32 layers x 5 Q4_0 GEMVs at m = 1, graph-replayed."""
+    layers = []
+    for _ in range(args.layers):
+        layer = []
+        for name, k, n in LLAMA2_7B:
+            layer.append(make_weights(torch, QuantLinear, Q4_0, n, k, 1, gen)[0])
+        layers.append(layer)
+    xs = {k: torch.empty(1, k, device="cuda").normal_(generator=gen) for _, k, _ in LLAMA2_7B}
+    ys = {n: torch.empty(1, n, device="cuda") for _, _, n in LLAMA2_7B}
+    nbytes = 0
+    for layer in layers:
+        for ql, (name, k, n) in zip(layer, LLAMA2_7B):
+            nbytes += wbytes(Q4_0, n, k) + 4 * k + 4 * n
+    launches = len(layers) * len(LLAMA2_7B)
+    path = layers[0][0].select_path(1)
+
+    def step():
+        for layer in layers:
+            for ql, (name, k, n) in zip(layer, LLAMA2_7B):
+                ql.forward(xs[k], out=ys[n], stream=stream)
+
+    with torch.cuda.stream(stream):
+        step()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
+            step()
+    torch.cuda.synchronize()
+    return layers, g, nbytes, launches, path
+
+
+def cpu_baseline():
+    """The reference CPU path (candle QMatMul semantics: Q8_0 activations,
+    integer block dots, OpenMP over columns), restated in oracle/oracle.c and
+    timed on this host on one layer's five GEMVs (a bounded sample)."""
+    import oracle
+
+    threads = len(os.sched_getaffinity(0))
+    # same distribution and shapes as the device weights (drawn on the host)
+    rng = np.random.default_rng(1234)
+    host = []
+    for name, k, n in LLAMA2_7B:
+        w = rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)
+        host.append((oracle.quantize(Q4_0, w), np.ascontiguousarray(
+            rng.standard_normal((1, k), dtype=np.float32)), n, k))
+    nbytes = sum(wbytes(Q4_0, n, k) + 4 * k + 4 * n for _, _, n, k in host)
+
+    def one_pass():
+        for b, x, n, k in host:
+            oracle.candle_qmatmul(Q4_0, b, x, n, k, nthreads=threads)
+
+    for _ in range(3):
+        one_pass()
+    times = []
+    t_end = time.perf_counter() + 10.0
+    while len(times) < 20 or (time.perf_counter() < t_end and len(times) < 200):
+        t0 = time.perf_counter()
+        one_pass()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 20 and time.perf_counter() > t_end:
+            break
+    med = float(np.median(times))
+    return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"one Llama-2-7B layer's 5 Q4_0 GEMVs at m=1 ({nbytes / 1e6:.1f} MB), "
+                      f"median of {len(times)} passes after 3 warm-ups, "
+                      "candle QMatMul semantics restated in C (oracle/oracle.c), OpenMP",
+            "ms_per_pass": round(med * 1e3, 3)}
+
+
+def extra_configs(torch, QuantLinear, gen, stream, only):
+    """The other BASELINE configs, each timed with HIP events (median of 3
+    rounds), weights rotated over >= 1 GB where the op is HBM-bound."""
+    from unillm_amd import PATH_DECODE_MFMA, PATH_PREFILL_MFMA
+
+    timer = Timer(torch, stream)
+    res = {}
+
+    def rotate(qtype, n, k, min_bytes=1 << 30, max_copies=96):
+        copies = max(1, min(max_copies, -(-min_bytes // wbytes(qtype, n, k))))
+        return make_weights(torch, QuantLinear, qtype, n, k, copies, gen)
+
+    def timed(ws, x, y, reps_per_copy=2, path=0):
+        def call_all():
+            for ql in ws:
+                ql.forward(x, out=y, path=path, stream=stream)
+        with torch.cuda.stream(stream):
+            call_all()
+            ts = [timer.run(call_all, reps_per_copy) / len(ws) for _ in range(3)]
+        return float(np.median(ts))
+
+    want = set(only.split(",")) if only else {"q8_gemv", "batched", "prefill", "stack"}
+    if "q8_gemv" in want:
+        n, k = 5632, 2048
+        ws = rotate(Q8_0, n, k)
+        x = torch.empty(1, k, device="cuda").normal_(generator=gen)
+        y = torch.empty(1, n, device="cuda")
+        ms = timed(ws, x, y)
+        b = wbytes(Q8_0, n, k) + 4 * k + 4 * n
+        res["q8_0_gemv_m1_k2048_n5632"] = {"GB/s": round(b / ms / 1e6, 1),
+                                           "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 3),
+                                           "us": round(ms * 1e3, 2), "copies": len(ws)}
+        del ws
+    if "batched" in want:
+        for n in (4096, 14336):
+            ws = rotate(Q4_0, n, 4096, max_copies=64)
+            for m in (4, 16, 64):
+                x = torch.empty(m, 4096, device="cuda").normal_(generator=gen)
+                y = torch.empty(m, n, device="cuda")
+                ms = timed(ws, x, y)
+                b = wbytes(Q4_0, n, 4096) + 4 * m * 4096 + 4 * m * n
+                res[f"q4_0_batched_m{m}_k4096_n{n}"] = {
+                    "GB/s": round(b / ms / 1e6, 1), "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 3),
+                    "TFLOP/s": round(2 * m * n * 4096 / ms / 1e9, 2), "us": round(ms * 1e3, 2),
+                    "path": ws[0].select_path(m)}
+            del ws
+    if "prefill" in want:
+        for qtype in (Q4_0, Q8_0):
+            for k, n in ((4096, 14336), (14336, 4096)):
+                ws = make_weights(torch, QuantLinear, qtype, n, k, 2, gen)
+                for m in (512, 2048):
+                    x = torch.empty(m, k, device="cuda").normal_(generator=gen)
+                    y = torch.empty(m, n, device="cuda")
+                    ms = timed(ws, x, y, reps_per_copy=2, path=PATH_PREFILL_MFMA)
+                    tf = 2 * m * n * k / ms / 1e9
+                    res[f"{'q4_0' if qtype == Q4_0 else 'q8_0'}_prefill_m{m}_k{k}_n{n}"] = {
+                        "TFLOP/s": round(tf, 1), "frac_bf16": round(tf / BF16_PEAK_TFLOPS, 3),
+                        "us": round(ms * 1e3, 1)}
+                del ws
+    if "stack" in want:
+        # config 5: 32 layers (QKV, o, gate+up fused 22016, down) + Q8_0 lm_head
+        shapes = [(Q4_0, 4096, 12288), (Q4_0, 4096, 4096), (Q4_0, 4096, 22016),
+                  (Q4_0, 11008, 4096)]
+        layers = [[make_weights(torch, QuantLinear, q, n, k, 1, gen)[0] for q, k, n in shapes]
+                  for _ in range(32)]
+        head = make_weights(torch, QuantLinear, Q8_0, 32000, 4096, 1, gen)[0]
+        total_w = 32 * sum(wbytes(q, n, k) for q, k, n in shapes) + wbytes(Q8_0, 32000, 4096)
+        for m in (1, 16):
+            xs = {k: torch.empty(m, k, device="cuda").normal_(generator=gen) for k in (4096, 11008)}
+            ys = {n: torch.empty(m, n, device="cuda") for n in (12288, 4096, 22016, 32000)}
+
+            def step():
+                for layer in layers:
+                    for ql, (q, k, n) in zip(layer, shapes):
+                        ql.forward(xs[k], out=ys[n], stream=stream)
+                head.forward(xs[4096], out=ys[32000], stream=stream)
+
+            with torch.cuda.stream(stream):
+                step()
+                ms = float(np.median([timer.run(step, 3) for _ in range(3)]))
+            b = total_w + 4 * m * (32 * (3 * 4096 + 11008) + 4096) + 4 * m * (
+                32 * (12288 + 4096 + 22016 + 4096) + 32000)
+            res[f"llama2_7b_stack_q4_0_m{m}"] = {
+                "GB/s": round(b / ms / 1e6, 1), "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 3),
+                "ms_per_step": round(ms, 4), "tokens/s": round(m * 1e3 / ms, 1),
+                "weight_bytes": total_w}
+        del layers, head
+    torch.cuda.synchronize()
+    return res
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(sharding is a design note, not code); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from unillm_amd import QuantLinear
+    from unillm_amd import _capi
+
+    _capi.check(_capi.lib().unillm_hip_init(0))
+    torch.cuda.set_device(0)
+    stream = torch.cuda.Stream()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(20240601)
+    timer = Timer(torch, stream)
+
+    layers, graph, nbytes, launches, path = decode_stack(torch, QuantLinear, args, gen, stream)
+
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    # timed region: exactly K steps, synchronised on both sides
+    t0 = time.perf_counter()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    with torch.cuda.stream(stream):
+        for _ in range(args.steps):
+            graph.replay()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / args.steps
+    kern_ms = ev0.elapsed_time(ev1) / (args.steps * launches)  # average GEMV launch
+    value = nbytes / (wall / args.steps) / 1e9
+    achieved = (nbytes / launches) / (kern_ms * 1e-3) / 1e9
+
+    extra = {}
+    if not args.no_extra:
+        extra = extra_configs(torch, QuantLinear, gen, stream, args.only)
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline()
+
+    line = {
+        "metric": "Q4_0 decode GEMV GB/s (% HBM peak) at 7B shapes; prefill GEMM TFLOP/s",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_0 weights, f32 activations, fp32 accumulate",
+        "data": "synthetic: weights N(0,0.02) quantized on device with the GGML Q4_0 "
+                "quantizer, x N(0,1); random-init Llama-2-7B projection shapes",
+        "config": {"workload": "Q4_0 decode GEMV, m=1, Llama-2-7B shapes (QKV 4096x12288, "
+                               "o 4096x4096, gate/up 4096x11008, down 11008x4096), "
+                               f"{args.layers} distinct layers per step, HIP-graph replay",
+                   "global_batch": 1, "seq_len": 1, "parallelism": "none (1 GPU)",
+                   "launches_per_step": launches, "bytes_per_step": nbytes,
+                   "kernel_path": {1: "gemv", 2: "decode_mfma", 3: "prefill_mfma"}[path]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "gemv_kernel<Q4_0, M=1>",
+                     "avg_launch_us": round(kern_ms * 1e3, 3),
+                     "bytes_per_launch": nbytes // launches},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,124 @@
+/*
+ * unillm_hip.h -- C ABI of the MI355X (gfx950) quantized linear-layer device.
+ *
+ * This is the drop-in boundary for unillm's quantized matmul: the matmul that
+ * candle's QMatMul::forward runs today on GGUF Q4_0 / Q8_0 weights loaded by
+ * WeightLoaderCore.  Plain C types only (pointers, sizes, int status) so that
+ * a Rust `extern "C"` block, ctypes or C++ can bind it unchanged.
+ *
+ * Conventions
+ *   - Status: 0 = OK, negative = error; unillm_hip_last_error() returns the
+ *     message of the last failing call on the calling thread.  (The reference
+ *     reports errors as anyhow::Result strings, e.g. "QMatMul forward failed:
+ *     ..." at crates/runtime/src/models_v2/llama.rs:1189; a binding maps a
+ *     negative status plus this message onto that.)
+ *   - Layout: W is [n, k] (n = out features, k = in features), row-major GGUF
+ *     blocks along k, exactly as GGUF stores a tensor with ne = [k, n]
+ *     (candle reverses ne into shape [n, k]).  x is [m, k] f32 row-major and
+ *     y = x . dequant(W)^T is [m, n] f32 row-major.
+ *   - Preconditions checked on the host before any launch: k % 32 == 0,
+ *     n >= 1, k >= 32, m >= 0, non-null pointers, known qtype.
+ *   - Streams: a `void* stream` is a hipStream_t (NULL = the null stream).
+ *     Compute calls are asynchronous on that stream and never synchronise.
+ *   - Ownership: a qweight owns its device copy of the weights and is
+ *     immutable after create, so it may be shared across threads.  The caller
+ *     owns x, y and the stream.
+ */
+#ifndef UNILLM_HIP_H
+#define UNILLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGML type ids as GGUF stores them (candle GgmlDType::Q4_0 / Q8_0). */
+#define UNILLM_QTYPE_Q4_0 2
+#define UNILLM_QTYPE_Q8_0 8
+
+#define UNILLM_OK 0
+#define UNILLM_ERR_INVALID_ARG (-1)
+#define UNILLM_ERR_UNSUPPORTED (-2)
+#define UNILLM_ERR_HIP (-3)
+#define UNILLM_ERR_OUT_OF_MEMORY (-4)
+#define UNILLM_ERR_NOT_INITIALIZED (-5)
+
+/* Kernel path for unillm_hip_qmatmul_path (AUTO is what qmatmul uses). */
+#define UNILLM_PATH_AUTO 0
+#define UNILLM_PATH_GEMV 1         /* fused dequant + GEMV, fp32 VALU, m <= 2 */
+#define UNILLM_PATH_DECODE_MFMA 2  /* batched decode, f16 MFMA, fp32 accumulate */
+#define UNILLM_PATH_PREFILL_MFMA 3 /* prefill, LDS-staged bf16 MFMA, fp32 accumulate */
+
+typedef struct unillm_qweight unillm_qweight;
+
+/* Select and check the device (must be gfx950).  Replaces the device choice the
+ * reference makes with `Device` (crates/runtime/src/tensor_core.rs:39-44), to
+ * which a binding adds HIP(usize).  Calls on other entry points made before
+ * init use device 0 after an implicit init. */
+int unillm_hip_init(int device);
+
+/* Message of the last error on the calling thread ("" if none). */
+const char* unillm_hip_last_error(void);
+
+/* Upload one GGUF Q4_0 / Q8_0 tensor ([n, k], n * k/32 blocks of 18 / 34 B)
+ * to the device, repacked there into the kernels' layout.  Replaces
+ * `QMatMul::from_arc(Arc::new(qtensor))` at
+ * crates/runtime/src/weight_loader_core.rs:569-571 (the QTensor read at :545).
+ * layout_flags must be 0 (reserved). */
+int unillm_hip_qweight_create(int qtype, int64_t n, int64_t k, const void* host_blocks,
+                              size_t nbytes, int layout_flags, unillm_qweight** out);
+
+/* As unillm_hip_qweight_create, from GGUF block bytes already in device memory
+ * (e.g. produced by unillm_hip_quantize).  Runs on `stream` and synchronises it
+ * before returning, so the source may be freed afterwards. */
+int unillm_hip_qweight_create_device(int qtype, int64_t n, int64_t k, const void* dev_blocks,
+                                     size_t nbytes, int layout_flags, void* stream,
+                                     unillm_qweight** out);
+
+/* Free a weight (NULL is a no-op).  Drop of the Arc<QMatMul> in ModelWeights
+ * (crates/runtime/src/model_core.rs:134). */
+int unillm_hip_qweight_destroy(unillm_qweight* w);
+
+/* Shape and footprint of a weight; any out-pointer may be NULL. */
+int unillm_hip_qweight_info(const unillm_qweight* w, int* qtype, int64_t* n, int64_t* k,
+                            size_t* device_bytes);
+
+/* y[m, n] = x[m, k] . dequant(W)^T, f32 in and out.  Replaces
+ * QMatMul::forward as called from LlamaAttention/LlamaMLP::quantized_matmul
+ * (crates/runtime/src/models_v2/llama.rs:1184-1195, 1325-1336) and
+ * LlamaModelV2::lm_head_forward (llama.rs:396-405); the m rows are the
+ * flattened leading dims of the [.., k] input.  m == 0 is a no-op. */
+int unillm_hip_qmatmul(const unillm_qweight* w, const float* x_dev, int64_t m, float* y_dev,
+                       void* stream);
+
+/* As unillm_hip_qmatmul with an explicit kernel path (UNILLM_PATH_*), for
+ * tests and benchmarks; AUTO picks what unillm_hip_qmatmul picks. */
+int unillm_hip_qmatmul_path(const unillm_qweight* w, const float* x_dev, int64_t m,
+                            float* y_dev, int path, void* stream);
+
+/* Kernel path that unillm_hip_qmatmul selects for m rows (UNILLM_PATH_*). */
+int unillm_hip_select_path(const unillm_qweight* w, int64_t m);
+
+/* out[n, k] = dequant(W) in f32, bit-exact with GGML's to_float.  Replaces
+ * `qtensor.dequantize(&device)` at crates/runtime/src/weight_loader_core.rs:579. */
+int unillm_hip_dequant(const unillm_qweight* w, float* out_dev, void* stream);
+
+/* GGML reference quantizer on the device: w[n, k] f32 -> GGUF block bytes
+ * (n * k/32 blocks of 18 / 34 B), bit-exact with GGML quantize_row_q4_0/q8_0
+ * (candle QTensor::quantize; used by the reference only to make GGUF files). */
+int unillm_hip_quantize(int qtype, const float* w_dev, int64_t n, int64_t k, void* blocks_dev,
+                        void* stream);
+
+/* Device memory helpers for bindings without their own allocator. */
+int unillm_hip_malloc(void** ptr, size_t bytes);
+int unillm_hip_free(void* ptr);
+int unillm_hip_memcpy_htod(void* dst_dev, const void* src_host, size_t bytes);
+int unillm_hip_memcpy_dtoh(void* dst_host, const void* src_dev, size_t bytes);
+int unillm_hip_synchronize(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* UNILLM_HIP_H */

@@ -1,0 +1,227 @@
+// test_host.cpp -- tests of the C++ host layer (unillm_amd/host), run by
+// tests/test_host_cpp.py.
+//
+//   test_host cpu <file.gguf> <file.expect>   parsing, name map, plan, errors
+//   test_host gpu <file.gguf> <file.expect>   load to the device + forward parity
+//
+// The .gguf / .expect pair is written by tests/golden/make_gguf.py.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "../../unillm_amd/host/unillm_host.hpp"
+
+using namespace unillm;
+
+static int g_fail = 0, g_pass = 0;
+
+#define CHECK(cond)                                                                     \
+    do {                                                                                \
+        if (cond) {                                                                     \
+            ++g_pass;                                                                   \
+        } else {                                                                        \
+            ++g_fail;                                                                   \
+            std::fprintf(stderr, "FAIL %s:%d: %s\n", __FILE__, __LINE__, #cond);        \
+        }                                                                               \
+    } while (0)
+
+template <typename F>
+static bool throws_with(F&& f, const std::string& needle) {
+    try {
+        f();
+    } catch (const std::exception& e) {
+        if (std::string(e.what()).find(needle) != std::string::npos) return true;
+        std::fprintf(stderr, "  unexpected message: %s\n", e.what());
+        return false;
+    }
+    return false;
+}
+
+struct Expect {
+    std::string gguf_name, hf_name;
+    uint32_t type, quantized, m, n, k;
+    std::vector<float> x;
+    std::vector<double> y;
+};
+
+static std::vector<Expect> read_expect(const std::string& path) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) throw std::runtime_error("cannot open " + path);
+    auto u32 = [&]() {
+        uint32_t v;
+        f.read(reinterpret_cast<char*>(&v), 4);
+        return v;
+    };
+    auto str = [&]() {
+        std::string s(u32(), '\0');
+        f.read(s.data(), (std::streamsize)s.size());
+        return s;
+    };
+    char magic[4];
+    f.read(magic, 4);
+    if (std::memcmp(magic, "UXPT", 4) != 0) throw std::runtime_error("bad expect file");
+    std::vector<Expect> out(u32());
+    for (Expect& e : out) {
+        e.gguf_name = str();
+        e.hf_name = str();
+        e.type = u32();
+        e.quantized = u32();
+        e.m = u32();
+        e.n = u32();
+        e.k = u32();
+        e.x.resize((size_t)e.m * e.k);
+        e.y.resize((size_t)e.m * e.n);
+        f.read(reinterpret_cast<char*>(e.x.data()), (std::streamsize)(e.x.size() * 4));
+        f.read(reinterpret_cast<char*>(e.y.data()), (std::streamsize)(e.y.size() * 8));
+    }
+    if (!f) throw std::runtime_error("truncated expect file");
+    return out;
+}
+
+static std::string write_tmp(const std::string& name, const std::vector<char>& bytes) {
+    const std::string path = "/tmp/unillm_host_test_" + name;
+    std::ofstream o(path, std::ios::binary);
+    o.write(bytes.data(), (std::streamsize)bytes.size());
+    return path;
+}
+
+static std::vector<char> slurp(const std::string& path) {
+    std::ifstream f(path, std::ios::binary);
+    return std::vector<char>(std::istreambuf_iterator<char>(f), {});
+}
+
+static void test_cpu(const std::string& gguf, const std::vector<Expect>& ex) {
+    // name map: the reference's own examples and its ordering hazards
+    CHECK(gguf_to_hf_name("blk.3.attn_output.weight") == "model.layers.3.self_attn.o_proj.weight");
+    CHECK(gguf_to_hf_name("output.weight") == "lm_head.weight");
+    CHECK(gguf_to_hf_name("output_norm.weight") == "model.norm.weight");
+    CHECK(gguf_to_hf_name("token_embd.weight") == "model.embed_tokens.weight");
+    CHECK(gguf_to_hf_name("blk.0.ffn_down.weight") == "model.layers.0.mlp.down_proj.weight");
+    CHECK(gguf_to_hf_name("blk.12.attn_norm.weight") ==
+          "model.layers.12.input_layernorm.weight");
+    CHECK(is_quantized_weight_name("model.layers.0.mlp.up_proj.weight"));
+    CHECK(is_quantized_weight_name("lm_head.weight"));
+    CHECK(!is_quantized_weight_name("model.embed_tokens.weight"));
+    CHECK(!is_quantized_weight_name("model.layers.0.input_layernorm.weight"));
+
+    const GgufFile f = GgufFile::open(gguf);
+    CHECK(f.version() == 3);
+    CHECK(f.alignment() == 32);
+    CHECK(f.data_offset() % 32 == 0);
+    CHECK(f.tensors().size() == ex.size());
+    const GgufModelConfig c = GgufWeightLoader::config_from(f);
+    CHECK(c.architecture == "llama");
+    CHECK(c.hidden_size == 64 && c.intermediate_size == 96 && c.num_hidden_layers == 2);
+    CHECK(c.num_attention_heads == 4 && c.num_key_value_heads == 2);
+    CHECK(c.vocab_size == 8);  // from tokenizer.ggml.tokens
+
+    GgufWeightLoader loader;
+    CHECK(loader.supports("model.gguf") && !loader.supports("model.safetensors"));
+    const auto plan = loader.plan(f);
+    size_t nq = 0;
+    for (size_t i = 0; i < plan.size() && i < ex.size(); ++i) {
+        CHECK(plan[i].gguf_name == ex[i].gguf_name);
+        CHECK(plan[i].hf_name == ex[i].hf_name);
+        CHECK(plan[i].type == ex[i].type);
+        CHECK(plan[i].quantized == (ex[i].quantized != 0));
+        if (plan[i].quantized) {
+            ++nq;
+            CHECK(plan[i].shape.size() == 2 && plan[i].shape[0] == ex[i].n &&
+                  plan[i].shape[1] == ex[i].k);  // ne reversed: [n, k]
+        }
+    }
+    CHECK(nq == 2 * 7 + 1);  // 7 projections per layer + lm_head
+
+    // raw bytes of a Q4_0 tensor: 18 B per block
+    const GgufTensorInfo* q = nullptr;
+    for (const auto& t : f.tensors())
+        if (t.name == "blk.0.attn_q.weight") q = &t;
+    CHECK(q && q->type == GGML_Q4_0 && q->nbytes == 64 * 2 * 18);
+    if (q) CHECK(f.read(*q).size() == q->nbytes);
+
+    // malformed files
+    std::vector<char> bytes = slurp(gguf);
+    std::vector<char> bad = bytes;
+    bad[0] = 'X';
+    CHECK(throws_with([&] { GgufFile::open(write_tmp("magic.gguf", bad)); }, "bad magic"));
+    bad = bytes;
+    bad[4] = 7;  // version 7
+    CHECK(throws_with([&] { GgufFile::open(write_tmp("ver.gguf", bad)); }, "version"));
+    std::vector<char> cut(bytes.begin(), bytes.begin() + (long)bytes.size() / 2);
+    CHECK(throws_with([&] { GgufFile::open(write_tmp("cut.gguf", cut)); }, "past the end"));
+    std::vector<char> hdr(bytes.begin(), bytes.begin() + 40);
+    CHECK(throws_with([&] { GgufFile::open(write_tmp("hdr.gguf", hdr)); }, "end of file"));
+    CHECK(throws_with([&] { GgufFile::open("/nonexistent/x.gguf"); }, "cannot open"));
+
+    // shape rules of QMatMul::forward are checked before any device work
+    Device d = Device::hip(0);
+    CHECK(d.to_string() == "HIP(0)" && d != Device::cpu());
+}
+
+static double normwise(const std::vector<float>& y, const std::vector<double>& r) {
+    double num = 0, den = 0;
+    for (size_t i = 0; i < r.size(); ++i) {
+        num = std::max(num, std::fabs((double)y[i] - r[i]));
+        den = std::max(den, std::fabs(r[i]));
+    }
+    return den > 0 ? num / den : num;
+}
+
+static void test_gpu(const std::string& gguf, const std::vector<Expect>& ex) {
+    GgufWeightLoader loader;
+    const ModelWeights w = loader.load_weights(gguf);
+    CHECK(w.quantized_tensors.size() == 15);
+    CHECK(w.get_quantized("model.layers.1.mlp.down_proj.weight") != nullptr);
+    CHECK(w.get_quantized("model.embed_tokens.weight") == nullptr);
+    CHECK(w.tensors.count("model.embed_tokens.weight") == 1);
+    CHECK(w.tensors.at("model.embed_tokens.weight").shape() == std::vector<int64_t>({128, 64}));
+    HipTensorOps ops;
+    for (const Expect& e : ex) {
+        if (!e.quantized) continue;
+        auto q = w.get_quantized(e.hf_name);
+        CHECK(q != nullptr);
+        if (!q) continue;
+        CHECK(q->n() == (int64_t)e.n && q->k() == (int64_t)e.k);
+        const Tensor x = Tensor::from_host(e.x, {(int64_t)e.m, (int64_t)e.k}, Device::hip(0));
+        const std::vector<float> y = q->forward(x).to_host();
+        const double err = normwise(y, e.y);
+        if (err >= 1e-3) std::fprintf(stderr, "  %s: normwise %.3g\n", e.hf_name.c_str(), err);
+        CHECK(err < 1e-3);
+        // TensorOps dispatch gives the same answer; a 3-D input keeps its leading dims
+        const std::vector<float> y2 = ops.matmul(x, *q).to_host();
+        CHECK(y2 == y);
+        const Tensor x3 = x.reshape({1, (int64_t)e.m, (int64_t)e.k});
+        const Tensor y3 = q->forward(x3);
+        CHECK(y3.shape() == std::vector<int64_t>({1, (int64_t)e.m, (int64_t)e.n}));
+    }
+    auto q = w.get_quantized("lm_head.weight");
+    CHECK(throws_with([&] { q->forward(Tensor::empty({3, 32}, Device::hip(0))); },
+                      "QMatMul forward failed: input last dim 32"));
+    CHECK(throws_with([&] { q->forward(Tensor::empty({64}, Device::hip(0))); },
+                      "QMatMul forward failed: rank 1"));
+    CHECK(throws_with([&] { q->forward(Tensor::empty({2, 64}, Device::cpu())); },
+                      "QMatMul forward failed: input is on CPU"));
+}
+
+int main(int argc, char** argv) {
+    if (argc != 4) {
+        std::fprintf(stderr, "usage: %s cpu|gpu file.gguf file.expect\n", argv[0]);
+        return 2;
+    }
+    const std::string mode = argv[1];
+    try {
+        const std::vector<Expect> ex = read_expect(argv[3]);
+        if (mode == "cpu") test_cpu(argv[2], ex);
+        else if (mode == "gpu") test_gpu(argv[2], ex);
+        else return 2;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "FAIL: uncaught exception: %s\n", e.what());
+        return 1;
+    }
+    std::printf("%s: %d passed, %d failed\n", mode.c_str(), g_pass, g_fail);
+    return g_fail ? 1 : 0;
+}

@@ -1,0 +1,186 @@
+"""Write tests/golden/tiny_llama_q4_0.gguf and its expected outputs.
+
+A minimal GGUF v3 file in the layout llama.cpp writes for a Llama model:
+2 blocks of attn_q/k/v/output + ffn_gate/up/down (Q4_0), token_embd (Q8_0),
+output (lm_head, Q8_0), attn_norm/ffn_norm/output_norm (F32).  No gguf
+package exists offline, so the writer follows the published GGUF v3 spec:
+
+  header   : magic "GGUF", u32 version = 3, u64 n_tensors, u64 n_kv
+  kv       : gguf string key (u64 len + bytes), u32 value type, value
+  tensors  : name, u32 n_dims, u64 ne[n_dims] (ne[0] = innermost = k),
+             u32 ggml type, u64 offset (from the data section, aligned)
+  data     : starts at the next multiple of general.alignment (32)
+
+Expected values (tiny_llama_q4_0.npz): for every projection, x and
+y = x . dequant(W)^T in f64 (numpy), the names after the reference's
+gguf_to_hf_name map (crates/runtime/src/weight_loader_core.rs:760-798), and
+which tensors stay quantized (weight_loader_core.rs:554).
+"""
+from __future__ import annotations
+
+import os
+import struct
+
+import numpy as np
+
+from make_golden import dequant, quantize_q4_0, quantize_q8_0
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ALIGN = 32
+T_F32, T_F16, T_Q4_0, T_Q8_0 = 0, 1, 2, 8
+V_UINT32, V_FLOAT32, V_STRING, V_ARRAY = 4, 6, 8, 9
+
+HIDDEN, INTER, VOCAB, LAYERS = 64, 96, 128, 2
+
+
+def gstr(s: str) -> bytes:
+    b = s.encode()
+    return struct.pack("<Q", len(b)) + b
+
+
+def kv(key: str, vtype: int, value) -> bytes:
+    out = gstr(key) + struct.pack("<I", vtype)
+    if vtype == V_UINT32:
+        out += struct.pack("<I", value)
+    elif vtype == V_FLOAT32:
+        out += struct.pack("<f", value)
+    elif vtype == V_STRING:
+        out += gstr(value)
+    elif vtype == V_ARRAY:
+        etype, items = value
+        out += struct.pack("<IQ", etype, len(items))
+        for it in items:
+            out += gstr(it) if etype == V_STRING else struct.pack("<I", it)
+    return out
+
+
+def main() -> None:
+    rng = np.random.default_rng(7)
+    tensors = []  # (gguf name, ggml type, [n, k] shape, raw bytes, dequantized f32 or None)
+
+    def add_q(name, qtype, n, k):
+        w = rng.normal(0.0, 0.02, size=(n, k)).astype(np.float32)
+        blocks = quantize_q4_0(w) if qtype == T_Q4_0 else quantize_q8_0(w)
+        tensors.append((name, qtype, (n, k), blocks.tobytes(), dequant(qtype, blocks, n, k)))
+
+    def add_f32(name, n):
+        v = (1.0 + rng.normal(0, 0.1, size=n)).astype(np.float32)
+        tensors.append((name, T_F32, (n,), v.tobytes(), v))
+
+    add_q("token_embd.weight", T_Q8_0, VOCAB, HIDDEN)
+    for i in range(LAYERS):
+        p = f"blk.{i}."
+        add_f32(p + "attn_norm.weight", HIDDEN)
+        add_q(p + "attn_q.weight", T_Q4_0, HIDDEN, HIDDEN)
+        add_q(p + "attn_k.weight", T_Q4_0, HIDDEN // 2, HIDDEN)
+        add_q(p + "attn_v.weight", T_Q4_0, HIDDEN // 2, HIDDEN)
+        add_q(p + "attn_output.weight", T_Q4_0, HIDDEN, HIDDEN)
+        add_f32(p + "ffn_norm.weight", HIDDEN)
+        add_q(p + "ffn_gate.weight", T_Q4_0, INTER, HIDDEN)
+        add_q(p + "ffn_up.weight", T_Q4_0, INTER, HIDDEN)
+        add_q(p + "ffn_down.weight", T_Q4_0, HIDDEN, INTER)
+    add_f32("output_norm.weight", HIDDEN)
+    add_q("output.weight", T_Q8_0, VOCAB, HIDDEN)
+
+    kvs = [
+        kv("general.architecture", V_STRING, "llama"),
+        kv("general.name", V_STRING, "tiny-llama-test"),
+        kv("general.alignment", V_UINT32, ALIGN),
+        kv("llama.embedding_length", V_UINT32, HIDDEN),
+        kv("llama.feed_forward_length", V_UINT32, INTER),
+        kv("llama.block_count", V_UINT32, LAYERS),
+        kv("llama.attention.head_count", V_UINT32, 4),
+        kv("llama.attention.head_count_kv", V_UINT32, 2),
+        kv("llama.attention.layer_norm_rms_epsilon", V_FLOAT32, 1e-5),
+        kv("tokenizer.ggml.tokens", V_ARRAY, (V_STRING, [f"t{i}" for i in range(8)])),
+    ]
+    header = b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(kvs)) + b"".join(kvs)
+
+    infos = b""
+    data = b""
+    for name, ttype, shape, raw, _ in tensors:
+        pad = (-len(data)) % ALIGN
+        data += b"\0" * pad
+        ne = list(reversed(shape))  # ggml ne[0] is the innermost (k) dimension
+        infos += gstr(name) + struct.pack("<I", len(ne)) + struct.pack(f"<{len(ne)}Q", *ne)
+        infos += struct.pack("<IQ", ttype, len(data))
+        data += raw
+    meta = header + infos
+    meta += b"\0" * ((-len(meta)) % ALIGN)
+    with open(os.path.join(HERE, "tiny_llama_q4_0.gguf"), "wb") as f:
+        f.write(meta + data)
+
+    # expected outputs for every tensor the loader keeps quantized
+    out = {}
+    hf = []
+    names = []
+    for name, ttype, shape, raw, deq in tensors:
+        mapped = hf_name(name)
+        names.append(name)
+        hf.append(mapped)
+        if ttype in (T_Q4_0, T_Q8_0) and ("_proj.weight" in mapped or "lm_head.weight" in mapped):
+            n, k = shape
+            x = rng.normal(0, 1, size=(3, k)).astype(np.float32)
+            key = mapped.replace(".", "_")
+            out["x__" + key] = x
+            out["y__" + key] = x.astype(np.float64) @ deq.astype(np.float64).T
+    out["gguf_names"] = np.array(names)
+    out["hf_names"] = np.array(hf)
+    np.savez_compressed(os.path.join(HERE, "tiny_llama_q4_0.npz"), **out)
+    # the same expectations in a flat binary the C++ host test reads:
+    # "UXPT", u32 count; per tensor: u32 len + gguf name, u32 len + hf name,
+    # u32 type, u32 quantized, u32 m, u32 n, u32 k, f32 x[m*k], f64 y[m*n]
+    blob = b"UXPT" + struct.pack("<I", len(tensors))
+    for name, ttype, shape, raw, deq in tensors:
+        mapped = hf_name(name)
+        quant = "_proj.weight" in mapped or "lm_head.weight" in mapped
+        key = mapped.replace(".", "_")
+        blob += struct.pack("<I", len(name)) + name.encode()
+        blob += struct.pack("<I", len(mapped)) + mapped.encode()
+        if quant:
+            x, y = out["x__" + key], out["y__" + key]
+            blob += struct.pack("<5I", ttype, 1, x.shape[0], y.shape[1], x.shape[1])
+            blob += x.astype("<f4").tobytes() + y.astype("<f8").tobytes()
+        else:
+            blob += struct.pack("<5I", ttype, 0, 0, 0, 0)
+    with open(os.path.join(HERE, "tiny_llama_q4_0.expect"), "wb") as f:
+        f.write(blob)
+    print(f"wrote tiny_llama_q4_0.gguf ({len(meta) + len(data)} B), {len(tensors)} tensors")
+
+
+def hf_name(name: str) -> str:
+    """The reference's GGUF -> HuggingFace name map, as a table of ordered
+    substring replacements (weight_loader_core.rs:760-798)."""
+    for a, b in HF_MAP:
+        name = name.replace(a, b)
+    return name
+
+
+HF_MAP = [
+    ("token_embd.weight", "model.embed_tokens.weight"),
+    ("blk.", "model.layers."),
+    (".attn_output.weight", ".self_attn.o_proj.weight"),
+    (".attn_q.weight", ".self_attn.q_proj.weight"),
+    (".attn_k.weight", ".self_attn.k_proj.weight"),
+    (".attn_v.weight", ".self_attn.v_proj.weight"),
+    (".attn_output.bias", ".self_attn.o_proj.bias"),
+    (".attn_q.bias", ".self_attn.q_proj.bias"),
+    (".attn_k.bias", ".self_attn.k_proj.bias"),
+    (".attn_v.bias", ".self_attn.v_proj.bias"),
+    ("output_norm.weight", "model.norm.weight"),
+    ("output.weight", "lm_head.weight"),
+    (".ffn_gate.weight", ".mlp.gate_proj.weight"),
+    (".ffn_up.weight", ".mlp.up_proj.weight"),
+    (".ffn_down.weight", ".mlp.down_proj.weight"),
+    (".ffn_gate.bias", ".mlp.gate_proj.bias"),
+    (".ffn_up.bias", ".mlp.up_proj.bias"),
+    (".ffn_down.bias", ".mlp.down_proj.bias"),
+    (".attn_norm.weight", ".input_layernorm.weight"),
+    (".ffn_norm.weight", ".post_attention_layernorm.weight"),
+    (".attn_norm.bias", ".input_layernorm.bias"),
+    (".ffn_norm.bias", ".post_attention_layernorm.bias"),
+]
+
+
+if __name__ == "__main__":
+    main()

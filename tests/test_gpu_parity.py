@@ -1,0 +1,232 @@
+"""GPU parity: the HIP kernels, called through the C ABI, against the CPU oracle.
+
+Bars: dequant bit-exact; GEMV / batched decode within
+1e-3 and bf16 prefill within 2e-2 of the f64 matmul of the exactly
+dequantized weights, measured normwise as max|y - r| / max|r|.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import Q4_0, Q8_0
+from unillm_amd import (PATH_AUTO, PATH_DECODE_MFMA, PATH_GEMV, PATH_PREFILL_MFMA, HipError,
+                        QuantLinear, quantize_blocks)
+
+pytestmark = pytest.mark.gpu
+
+TOL = {PATH_GEMV: 1e-3, PATH_DECODE_MFMA: 1e-3, PATH_PREFILL_MFMA: 2e-2}
+
+
+def _dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _case(qtype, m, n, k, seed):
+    w = oracle.normal(n * k, seed=seed, std=0.02).reshape(n, k)
+    x = oracle.normal(m * k, seed=seed + 1).reshape(m, k)
+    return oracle.quantize(qtype, w), x
+
+
+def _run(ql: QuantLinear, x: np.ndarray, path: int) -> np.ndarray:
+    y = ql.forward(_dev(x), path=path)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+# ---- dequant: bit-exact ------------------------------------------------------------------
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_dequant_bit_exact_all_scales_all_codes(qtype):
+    codes = np.arange(65536, dtype=np.uint16)
+    if qtype == Q4_0:  # one block holds every code in both nibble positions
+        nblk = 1
+        blocks = np.zeros((65536, nblk, 18), np.uint8)
+        blocks[:, 0, 2:] = np.array([j | ((15 - j) << 4) for j in range(16)], np.uint8)
+    else:  # eight blocks hold all 256 byte values
+        nblk = 8
+        blocks = np.zeros((65536, nblk, 34), np.uint8)
+        blocks[:, :, 2:] = np.arange(256, dtype=np.uint8).reshape(8, 32)
+    blocks[:, :, 0:2] = codes.view(np.uint8).reshape(-1, 1, 2)
+    k = 32 * nblk
+    ql = QuantLinear.from_blocks(qtype, 65536, k, blocks)
+    got = ql.dequantize().cpu().numpy()
+    want = oracle.dequant(qtype, blocks, 65536, k)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype,n,k", [(Q4_0, 37, 96), (Q4_0, 300, 4096), (Q8_0, 41, 160),
+                                       (Q8_0, 128, 2048)])
+def test_dequant_bit_exact_random(qtype, n, k):
+    blocks, _ = _case(qtype, 1, n, k, seed=100 + n)
+    got = QuantLinear.from_blocks(qtype, n, k, blocks).dequantize().cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), oracle.dequant(qtype, blocks, n, k).view(np.uint32))
+
+
+def test_dequant_golden(golden_cases):
+    for name, c in golden_cases.items():
+        ql = QuantLinear.from_blocks(int(c["qtype"]), int(c["n"]), int(c["k"]), c["blocks"])
+        got = ql.dequantize().cpu().numpy()
+        want = oracle.dequant(int(c["qtype"]), c["blocks"], int(c["n"]), int(c["k"]))
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), name
+
+
+# ---- device quantizer: bit-exact with GGML ---------------------------------------------------
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_device_quantizer_bit_exact(qtype, golden_cases):
+    for name, c in golden_cases.items():
+        got = quantize_blocks(qtype, _dev(c["w"])).cpu().numpy()
+        assert np.array_equal(got, oracle.quantize(qtype, c["w"]).reshape(-1)), name
+    w = oracle.normal(512 * 1024, seed=3, std=0.02).reshape(512, 1024)
+    w[0, :64] = 0.0
+    w[1, 5] = 1e-6
+    got = quantize_blocks(qtype, _dev(w)).cpu().numpy()
+    assert np.array_equal(got, oracle.quantize(qtype, w).reshape(-1))
+
+
+# ---- the reference's known answers --------------------------------------------------------
+
+@pytest.mark.parametrize("path,m", [(PATH_GEMV, 1), (PATH_GEMV, 2), (PATH_DECODE_MFMA, 3),
+                                    (PATH_DECODE_MFMA, 8)])
+def test_known_answer_6p3984375(path, m):
+    # simd/matmul/gemv.rs:91-113, gemm.rs:377-402: d = f16(0.1), 0x99, x = 1
+    blk = np.zeros(18, np.uint8)
+    blk[0:2] = np.array([0.1], np.float16).view(np.uint8)
+    blk[2:] = 0x99
+    blocks = np.tile(blk, 4)
+    y = _run(QuantLinear.from_blocks(Q4_0, 2, 64, blocks), np.ones((m, 64), np.float32), path)
+    assert np.all(y == np.float32(6.3984375))
+
+
+def test_known_answer_12p796875_prefill_close():
+    # gemm.rs:404-429, 8 tokens x 4 rows x 128; bf16 rounds d, so within 2e-2
+    blk = np.zeros(18, np.uint8)
+    blk[0:2] = np.array([0.1], np.float16).view(np.uint8)
+    blk[2:] = 0x99
+    y = _run(QuantLinear.from_blocks(Q4_0, 4, 128, np.tile(blk, 16)),
+             np.ones((8, 128), np.float32), PATH_PREFILL_MFMA)
+    assert np.allclose(y, 12.796875, rtol=2e-2)
+
+
+# ---- matmul parity vs the f64 oracle -------------------------------------------------------
+
+SHAPES = [(37, 96), (33, 4128), (64, 2048), (300, 4096), (129, 11008), (70, 14336)]
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+@pytest.mark.parametrize("n,k", SHAPES)
+@pytest.mark.parametrize("path,m", [(PATH_GEMV, 1), (PATH_GEMV, 2), (PATH_DECODE_MFMA, 2),
+                                    (PATH_DECODE_MFMA, 5), (PATH_DECODE_MFMA, 16),
+                                    (PATH_DECODE_MFMA, 33), (PATH_DECODE_MFMA, 64),
+                                    (PATH_PREFILL_MFMA, 65), (PATH_PREFILL_MFMA, 130)])
+def test_qmatmul_parity(qtype, n, k, path, m):
+    blocks, x = _case(qtype, m, n, k, seed=n * 7 + k)
+    ql = QuantLinear.from_blocks(qtype, n, k, blocks)
+    y = _run(ql, x, path)
+    ref = oracle.qmatmul_f64(qtype, blocks, x, n, k)
+    assert y.shape == (m, n)
+    e = oracle.normwise_error(y, ref)
+    assert e < TOL[path], f"normwise {e:.3g}"
+    if path == PATH_GEMV:
+        assert e < 1e-5  # fp32 with exact products: far inside the bar
+
+
+def test_golden_fixtures_auto_path(golden_cases):
+    for name, c in golden_cases.items():
+        qtype, m, n, k = (int(c[f]) for f in ("qtype", "m", "n", "k"))
+        ql = QuantLinear.from_blocks(qtype, n, k, c["blocks"])
+        path = ql.select_path(m)
+        y = _run(ql, c["x"], PATH_AUTO)
+        assert oracle.normwise_error(y, c["y"]) < TOL[path], name
+
+
+def test_auto_path_selection():
+    blocks, _ = _case(Q4_0, 1, 16, 4096, seed=1)
+    ql = QuantLinear.from_blocks(Q4_0, 16, 4096, blocks)
+    assert ql.select_path(1) == PATH_GEMV
+    assert ql.select_path(2) == PATH_GEMV
+    assert ql.select_path(3) == PATH_DECODE_MFMA
+    assert ql.select_path(64) == PATH_DECODE_MFMA
+    assert ql.select_path(65) == PATH_PREFILL_MFMA
+
+
+# ---- BASELINE shapes -----------------------------------------------------------------------
+
+@pytest.mark.parametrize("qtype,k,n", [(Q8_0, 2048, 5632), (Q4_0, 4096, 12288),
+                                       (Q4_0, 4096, 4096), (Q4_0, 4096, 11008),
+                                       (Q4_0, 11008, 4096)])
+def test_baseline_decode_shapes_m1(qtype, k, n):
+    blocks, x = _case(qtype, 1, n, k, seed=k + n)
+    y = _run(QuantLinear.from_blocks(qtype, n, k, blocks), x, PATH_AUTO)
+    assert oracle.normwise_error(y, oracle.qmatmul_f64(qtype, blocks, x, n, k)) < 1e-5
+
+
+@pytest.mark.parametrize("m", [4, 16, 64])
+@pytest.mark.parametrize("n", [4096, 14336])
+def test_baseline_batched_decode(m, n):
+    k = 4096
+    blocks, x = _case(Q4_0, m, n, k, seed=m + n)
+    y = _run(QuantLinear.from_blocks(Q4_0, n, k, blocks), x, PATH_AUTO)
+    assert oracle.normwise_error(y, oracle.qmatmul_f64(Q4_0, blocks, x, n, k)) < 1e-3
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+@pytest.mark.parametrize("m,k,n", [(512, 4096, 14336), (512, 14336, 4096)])
+def test_baseline_prefill_rows_sampled(qtype, m, k, n):
+    # full-size prefill; the f64 oracle checks a sample of rows, plus linearity
+    blocks, x = _case(qtype, m, n, k, seed=m + k)
+    ql = QuantLinear.from_blocks(qtype, n, k, blocks)
+    y = _run(ql, x, PATH_AUTO)
+    rows = np.array([0, 1, 255, 256, 511])
+    ref = oracle.qmatmul_f64(qtype, blocks, x[rows], n, k)
+    assert oracle.normwise_error(y[rows], ref) < 2e-2
+    xd = _dev(x)
+    y2 = ql.forward(xd * 2.0)
+    torch.cuda.synchronize()
+    # scaling by 2 is exact in bf16 and f32: outputs scale exactly
+    assert np.array_equal(y2.cpu().numpy(), 2.0 * y)
+
+
+# ---- edges -----------------------------------------------------------------------------------
+
+def test_m_zero_is_noop():
+    blocks, _ = _case(Q4_0, 1, 8, 64, seed=2)
+    ql = QuantLinear.from_blocks(Q4_0, 8, 64, blocks)
+    y = ql.forward(torch.empty(0, 64, device="cuda"))
+    assert y.shape == (0, 8)
+
+
+def test_3d_input_flattens_leading_dims():
+    # tensor_core.rs:857-871: [B, T, K] is treated as [B*T, K]
+    blocks, x = _case(Q4_0, 6, 40, 128, seed=4)
+    ql = QuantLinear.from_blocks(Q4_0, 40, 128, blocks)
+    y = ql.forward(_dev(x).reshape(2, 3, 128))
+    torch.cuda.synchronize()
+    assert y.shape == (2, 3, 40)
+    ref = oracle.qmatmul_f64(Q4_0, blocks, x, 40, 128).reshape(2, 3, 40)
+    assert oracle.normwise_error(y.cpu().numpy(), ref) < 1e-3
+
+
+def test_forward_argument_errors():
+    blocks, _ = _case(Q4_0, 1, 8, 64, seed=2)
+    ql = QuantLinear.from_blocks(Q4_0, 8, 64, blocks)
+    with pytest.raises(RuntimeError, match="QMatMul forward failed"):
+        ql.forward(torch.zeros(1, 32, device="cuda"))
+    with pytest.raises(RuntimeError, match="QMatMul forward failed"):
+        ql.forward(torch.zeros(64, device="cuda"))
+    with pytest.raises(RuntimeError, match="QMatMul forward failed"):
+        ql.forward(torch.zeros(1, 64, device="cuda", dtype=torch.float16))
+    with pytest.raises(HipError, match="16-byte aligned"):
+        ql.forward(torch.zeros(2 * 64 + 1, device="cuda")[1:65].view(1, 64))
+    with pytest.raises(HipError, match="m <= 2"):
+        ql.forward(torch.zeros(3, 64, device="cuda"), path=PATH_GEMV)
+
+
+def test_repeat_calls_deterministic():
+    blocks, x = _case(Q4_0, 16, 4096, 4096, seed=9)
+    ql = QuantLinear.from_blocks(Q4_0, 4096, 4096, blocks)
+    xd = _dev(x)
+    a = ql.forward(xd).cpu().numpy()
+    for _ in range(3):
+        assert np.array_equal(ql.forward(xd).cpu().numpy(), a)

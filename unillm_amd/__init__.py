@@ -1,0 +1,24 @@
+"""unillm_amd -- MI355X (gfx950) device for unillm's quantized linear layer.
+
+The product is libunillm_hip.so (HIP kernels behind the C ABI declared in
+include/unillm_hip.h).  This package builds it (``unillm_amd.build``), binds
+it with ctypes (``unillm_amd._capi``) and mirrors the reference's call
+surface for this path (``QuantLinear``, the `Arc<QMatMul>` of
+crates/runtime/src/model_core.rs:134).
+"""
+from ._capi import (BLOCK_BYTES, ERR_HIP, ERR_INVALID_ARG, ERR_UNSUPPORTED, OK, PATH_AUTO,
+                    PATH_DECODE_MFMA, PATH_GEMV, PATH_PREFILL_MFMA, QK, Q4_0, Q8_0, HipError)
+
+__all__ = [
+    "BLOCK_BYTES", "ERR_HIP", "ERR_INVALID_ARG", "ERR_UNSUPPORTED", "OK", "PATH_AUTO",
+    "PATH_DECODE_MFMA", "PATH_GEMV", "PATH_PREFILL_MFMA", "QK", "Q4_0", "Q8_0", "HipError",
+    "QuantLinear", "quantize_blocks",
+]
+
+
+def __getattr__(name):
+    # QuantLinear needs torch; import it lazily so the ABI binding loads without it.
+    if name in ("QuantLinear", "quantize_blocks"):
+        from . import quant_linear
+        return getattr(quant_linear, name)
+    raise AttributeError(name)

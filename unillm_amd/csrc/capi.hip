@@ -1,0 +1,335 @@
+// capi.hip -- the extern "C" boundary (include/unillm_hip.h): argument checks,
+// error reporting, weight lifetime and kernel-path dispatch.
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <new>
+#include <string>
+
+#include <hip/hip_fp16.h>
+#include <math.h>
+
+#include "internal.hpp"
+
+namespace unillm {
+namespace {
+
+thread_local std::string g_last_error;
+std::once_flag g_init_once;
+int g_init_status = UNILLM_ERR_NOT_INITIALIZED;
+int g_device = -1;
+DeviceInfo g_info{};
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int fail_hip(hipError_t e, const char* what) {
+    return fail(UNILLM_ERR_HIP, std::string(what) + ": " + hipGetErrorName(e) + " (" +
+                                    hipGetErrorString(e) + ")");
+}
+
+int do_init(int device) {
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return fail_hip(e, "hipGetDeviceCount");
+    if (device < 0 || device >= count)
+        return fail(UNILLM_ERR_INVALID_ARG, "device " + std::to_string(device) +
+                                                " out of range (have " + std::to_string(count) +
+                                                ")");
+    hipDeviceProp_t prop;
+    if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess)
+        return fail_hip(e, "hipGetDeviceProperties");
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(UNILLM_ERR_UNSUPPORTED,
+                    std::string("unillm_hip requires gfx950 (MI355X); device reports ") +
+                        prop.gcnArchName);
+    if ((e = hipSetDevice(device)) != hipSuccess) return fail_hip(e, "hipSetDevice");
+    g_info.cu_count = prop.multiProcessorCount;
+    g_info.max_lds = (int)prop.sharedMemPerBlock;
+    g_device = device;
+    return UNILLM_OK;
+}
+
+int ensure_init() {
+    if (g_device >= 0) {
+        hipError_t e = hipSetDevice(g_device);
+        return e == hipSuccess ? UNILLM_OK : fail_hip(e, "hipSetDevice");
+    }
+    std::call_once(g_init_once, [] { g_init_status = do_init(0); });
+    return g_init_status;
+}
+
+bool valid_qtype(int q) { return q == UNILLM_QTYPE_Q4_0 || q == UNILLM_QTYPE_Q8_0; }
+
+int check_shape(int qtype, int64_t n, int64_t k) {
+    if (!valid_qtype(qtype))
+        return fail(UNILLM_ERR_UNSUPPORTED,
+                    "unsupported qtype " + std::to_string(qtype) + " (want 2 = Q4_0, 8 = Q8_0)");
+    if (n < 1 || k < QK || k % QK != 0)
+        return fail(UNILLM_ERR_INVALID_ARG, "bad weight shape [" + std::to_string(n) + ", " +
+                                                std::to_string(k) +
+                                                "]: need n >= 1 and k a positive multiple of 32");
+    if (n > (int64_t)INT32_MAX || k / QK > (int64_t)INT32_MAX / 4)
+        return fail(UNILLM_ERR_INVALID_ARG, "weight shape too large");
+    return UNILLM_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int alloc_weight(int qtype, int64_t n, int64_t k, QWeight** out) {
+    QWeight* w = new (std::nothrow) QWeight{};
+    if (!w) return fail(UNILLM_ERR_OUT_OF_MEMORY, "host allocation failed");
+    w->qtype = qtype;
+    w->device = g_device;
+    w->n = n;
+    w->k = k;
+    w->kb = k / QK;
+    const size_t qs_bytes = (size_t)(n * w->kb) * qbytes(qtype);
+    const size_t d_off = (qs_bytes + 255) & ~(size_t)255;
+    // + a 256-byte tail slot for the scale reduction run at create
+    w->bytes = ((d_off + (size_t)(n * w->kb) * 2 + 255) & ~(size_t)255) + 256;
+    hipError_t e = hipMalloc(&w->base, w->bytes);
+    if (e != hipSuccess) {
+        delete w;
+        return e == hipErrorOutOfMemory ? fail(UNILLM_ERR_OUT_OF_MEMORY, "hipMalloc of weight")
+                                        : fail_hip(e, "hipMalloc");
+    }
+    w->qs = static_cast<uint8_t*>(w->base);
+    w->d = reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(w->base) + d_off);
+    *out = w;
+    return UNILLM_OK;
+}
+
+// After repack: find max|d| and the f16 exponent offset E the decode MFMA path
+// applies, so that every (q - 8) * d * 2^-E (or q * d * 2^-E) fits f16.
+// Synchronises `s`.
+int finish_weight(QWeight* w, hipStream_t s) {
+    uint32_t* slot = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(w->base) + w->bytes - 256);
+    uint32_t bits = 0;
+    hipError_t e;
+    if ((e = hipMemsetAsync(slot, 0, sizeof(uint32_t), s)) != hipSuccess)
+        return fail_hip(e, "hipMemsetAsync");
+    if ((e = launch_scale_absmax(*w, slot, s)) != hipSuccess) return fail_hip(e, "scale scan");
+    if ((e = hipMemcpyAsync(&bits, slot, sizeof(bits), hipMemcpyDeviceToHost, s)) != hipSuccess)
+        return fail_hip(e, "hipMemcpyAsync");
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return fail_hip(e, "weight upload");
+    // |code| <= 8 (Q4_0) or 128 (Q8_0); f16 holds magnitudes up to 65504
+    const float dmax = __half2float(__ushort_as_half((unsigned short)(bits > 0x7BFFu ? 0x7BFFu
+                                                                                    : bits)));
+    const float wmax = dmax * (w->qtype == UNILLM_QTYPE_Q4_0 ? 8.0f : 128.0f);
+    int E = 0;
+    while (E < 30 && wmax * ldexpf(1.0f, -E) > 65504.0f) ++E;
+    w->f16_exp = E;
+    return UNILLM_OK;
+}
+
+}  // namespace
+
+const DeviceInfo& device_info() { return g_info; }
+
+}  // namespace unillm
+
+using namespace unillm;
+
+extern "C" {
+
+int unillm_hip_init(int device) {
+    int rc = UNILLM_OK;
+    std::call_once(g_init_once, [&] { g_init_status = do_init(device); });
+    rc = g_init_status;
+    if (rc == UNILLM_OK && device != g_device)
+        return fail(UNILLM_ERR_INVALID_ARG, "already initialised on device " +
+                                                std::to_string(g_device));
+    return rc;
+}
+
+const char* unillm_hip_last_error(void) { return g_last_error.c_str(); }
+
+int unillm_hip_qweight_create(int qtype, int64_t n, int64_t k, const void* host_blocks,
+                              size_t nbytes, int layout_flags, unillm_qweight** out) {
+    if (!out) return fail(UNILLM_ERR_INVALID_ARG, "out is NULL");
+    *out = nullptr;
+    if (int rc = check_shape(qtype, n, k)) return rc;
+    if (!host_blocks) return fail(UNILLM_ERR_INVALID_ARG, "host_blocks is NULL");
+    if (layout_flags != 0) return fail(UNILLM_ERR_INVALID_ARG, "layout_flags must be 0");
+    const size_t want = (size_t)(n * (k / QK)) * gguf_block_bytes(qtype);
+    if (nbytes != want)
+        return fail(UNILLM_ERR_INVALID_ARG, "nbytes " + std::to_string(nbytes) + " != " +
+                                                std::to_string(want) + " for this shape");
+    if (int rc = ensure_init()) return rc;
+    void* staging = nullptr;
+    hipError_t e = hipMalloc(&staging, want);
+    if (e != hipSuccess) return fail_hip(e, "hipMalloc (staging)");
+    QWeight* w = nullptr;
+    int rc = alloc_weight(qtype, n, k, &w);
+    if (rc == UNILLM_OK) {
+        if ((e = hipMemcpy(staging, host_blocks, want, hipMemcpyHostToDevice)) != hipSuccess)
+            rc = fail_hip(e, "hipMemcpy (upload)");
+        else if ((e = launch_repack(*w, static_cast<const uint8_t*>(staging), nullptr)) !=
+                 hipSuccess)
+            rc = fail_hip(e, "repack launch");
+        else
+            rc = finish_weight(w, nullptr);
+    }
+    (void)hipFree(staging);
+    if (rc != UNILLM_OK) {
+        if (w) {
+            (void)hipFree(w->base);
+            delete w;
+        }
+        return rc;
+    }
+    *out = w;
+    return UNILLM_OK;
+}
+
+int unillm_hip_qweight_create_device(int qtype, int64_t n, int64_t k, const void* dev_blocks,
+                                     size_t nbytes, int layout_flags, void* stream,
+                                     unillm_qweight** out) {
+    if (!out) return fail(UNILLM_ERR_INVALID_ARG, "out is NULL");
+    *out = nullptr;
+    if (int rc = check_shape(qtype, n, k)) return rc;
+    if (!dev_blocks) return fail(UNILLM_ERR_INVALID_ARG, "dev_blocks is NULL");
+    if (layout_flags != 0) return fail(UNILLM_ERR_INVALID_ARG, "layout_flags must be 0");
+    const size_t want = (size_t)(n * (k / QK)) * gguf_block_bytes(qtype);
+    if (nbytes != want)
+        return fail(UNILLM_ERR_INVALID_ARG, "nbytes " + std::to_string(nbytes) + " != " +
+                                                std::to_string(want) + " for this shape");
+    if (((uintptr_t)dev_blocks & 1u) != 0)
+        return fail(UNILLM_ERR_INVALID_ARG, "dev_blocks must be 2-byte aligned");
+    if (int rc = ensure_init()) return rc;
+    QWeight* w = nullptr;
+    if (int rc = alloc_weight(qtype, n, k, &w)) return rc;
+    hipError_t e = launch_repack(*w, static_cast<const uint8_t*>(dev_blocks),
+                                 static_cast<hipStream_t>(stream));
+    int rc = e == hipSuccess ? finish_weight(w, static_cast<hipStream_t>(stream))
+                             : fail_hip(e, "repack launch");
+    if (rc != UNILLM_OK) {
+        (void)hipFree(w->base);
+        delete w;
+        return rc;
+    }
+    *out = w;
+    return UNILLM_OK;
+}
+
+int unillm_hip_qweight_destroy(unillm_qweight* w) {
+    if (!w) return UNILLM_OK;
+    hipError_t e = hipFree(w->base);
+    delete w;
+    return e == hipSuccess ? UNILLM_OK : fail_hip(e, "hipFree (weight)");
+}
+
+int unillm_hip_qweight_info(const unillm_qweight* w, int* qtype, int64_t* n, int64_t* k,
+                            size_t* device_bytes) {
+    if (!w) return fail(UNILLM_ERR_INVALID_ARG, "weight is NULL");
+    if (qtype) *qtype = w->qtype;
+    if (n) *n = w->n;
+    if (k) *k = w->k;
+    if (device_bytes) *device_bytes = w->bytes;
+    return UNILLM_OK;
+}
+
+int unillm_hip_select_path(const unillm_qweight* w, int64_t m) {
+    if (!w || m < 0) return fail(UNILLM_ERR_INVALID_ARG, "bad arguments to select_path");
+    if (m <= kGemvMaxM && w->kb <= gemv_max_kb(m)) return UNILLM_PATH_GEMV;
+    if (m <= kDecodeMaxM) return UNILLM_PATH_DECODE_MFMA;
+    return UNILLM_PATH_PREFILL_MFMA;
+}
+
+int unillm_hip_qmatmul_path(const unillm_qweight* w, const float* x_dev, int64_t m,
+                            float* y_dev, int path, void* stream) {
+    if (!w) return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: weight is NULL");
+    if (m < 0) return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: m < 0");
+    if (m == 0) return UNILLM_OK;
+    if (!x_dev || !y_dev)
+        return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: x or y is NULL");
+    if (!aligned16(x_dev))
+        return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: x must be 16-byte aligned");
+    if (m > (int64_t)INT32_MAX / 2)
+        return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: m too large");
+    if (path == UNILLM_PATH_AUTO) path = unillm_hip_select_path(w, m);
+    if (int rc = ensure_init()) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e;
+    switch (path) {
+        case UNILLM_PATH_GEMV:
+            if (m > kGemvMaxM || w->kb > gemv_max_kb(m))
+                return fail(UNILLM_ERR_UNSUPPORTED,
+                            "GEMV path takes m <= 2 and k <= " +
+                                std::to_string(gemv_max_kb(m) * QK) + " at this m");
+            e = launch_gemv(*w, x_dev, m, y_dev, s);
+            break;
+        case UNILLM_PATH_DECODE_MFMA:
+            if (m > kDecodeMaxM)
+                return fail(UNILLM_ERR_UNSUPPORTED, "decode MFMA path takes m <= 64");
+            e = launch_decode_mfma(*w, x_dev, m, y_dev, s);
+            break;
+        case UNILLM_PATH_PREFILL_MFMA:
+            e = launch_prefill_mfma(*w, x_dev, m, y_dev, s);
+            break;
+        default:
+            return fail(UNILLM_ERR_INVALID_ARG, "unknown path " + std::to_string(path));
+    }
+    return e == hipSuccess ? UNILLM_OK : fail_hip(e, "QMatMul forward failed: kernel launch");
+}
+
+int unillm_hip_qmatmul(const unillm_qweight* w, const float* x_dev, int64_t m, float* y_dev,
+                       void* stream) {
+    return unillm_hip_qmatmul_path(w, x_dev, m, y_dev, UNILLM_PATH_AUTO, stream);
+}
+
+int unillm_hip_dequant(const unillm_qweight* w, float* out_dev, void* stream) {
+    if (!w || !out_dev) return fail(UNILLM_ERR_INVALID_ARG, "weight or out is NULL");
+    if (!aligned16(out_dev)) return fail(UNILLM_ERR_INVALID_ARG, "out must be 16-byte aligned");
+    if (int rc = ensure_init()) return rc;
+    hipError_t e = launch_dequant(*w, out_dev, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? UNILLM_OK : fail_hip(e, "dequant launch");
+}
+
+int unillm_hip_quantize(int qtype, const float* w_dev, int64_t n, int64_t k, void* blocks_dev,
+                        void* stream) {
+    if (int rc = check_shape(qtype, n, k)) return rc;
+    if (!w_dev || !blocks_dev) return fail(UNILLM_ERR_INVALID_ARG, "w or blocks is NULL");
+    if (!aligned16(w_dev)) return fail(UNILLM_ERR_INVALID_ARG, "w must be 16-byte aligned");
+    if (int rc = ensure_init()) return rc;
+    hipError_t e = launch_quantize(qtype, w_dev, n, k, static_cast<uint8_t*>(blocks_dev),
+                                   static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? UNILLM_OK : fail_hip(e, "quantize launch");
+}
+
+int unillm_hip_malloc(void** ptr, size_t bytes) {
+    if (!ptr) return fail(UNILLM_ERR_INVALID_ARG, "ptr is NULL");
+    if (int rc = ensure_init()) return rc;
+    hipError_t e = hipMalloc(ptr, bytes);
+    if (e == hipErrorOutOfMemory) return fail(UNILLM_ERR_OUT_OF_MEMORY, "hipMalloc");
+    return e == hipSuccess ? UNILLM_OK : fail_hip(e, "hipMalloc");
+}
+
+int unillm_hip_free(void* ptr) {
+    hipError_t e = hipFree(ptr);
+    return e == hipSuccess ? UNILLM_OK : fail_hip(e, "hipFree");
+}
+
+int unillm_hip_memcpy_htod(void* dst_dev, const void* src_host, size_t bytes) {
+    if (int rc = ensure_init()) return rc;
+    hipError_t e = hipMemcpy(dst_dev, src_host, bytes, hipMemcpyHostToDevice);
+    return e == hipSuccess ? UNILLM_OK : fail_hip(e, "hipMemcpy H2D");
+}
+
+int unillm_hip_memcpy_dtoh(void* dst_host, const void* src_dev, size_t bytes) {
+    if (int rc = ensure_init()) return rc;
+    hipError_t e = hipMemcpy(dst_host, src_dev, bytes, hipMemcpyDeviceToHost);
+    return e == hipSuccess ? UNILLM_OK : fail_hip(e, "hipMemcpy D2H");
+}
+
+int unillm_hip_synchronize(void) {
+    if (int rc = ensure_init()) return rc;
+    hipError_t e = hipDeviceSynchronize();
+    return e == hipSuccess ? UNILLM_OK : fail_hip(e, "hipDeviceSynchronize");
+}
+
+}  // extern "C"

@@ -1,0 +1,65 @@
+// internal.hpp -- shared definitions of the gfx950 quantized-matmul library.
+//
+// Device layout of a weight (written once by the repack kernel at upload):
+//   qs plane : [n][kb][QB] bytes, QB = 16 (Q4_0 nibbles) or 32 (Q8_0 int8),
+//              the block payloads of a row back to back, so a 128-bit load is
+//              exactly one Q4_0 block payload (or half a Q8_0 one);
+//   d plane  : [n][kb] f16 scales, at a 256-byte aligned offset after qs.
+// The byte count is the GGUF one (18 or 34 B per 32 weights); only the order
+// differs, and dequant of this layout is bit-exact with the GGUF bytes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/unillm_hip.h"
+
+// The opaque handle of the C ABI is the weight descriptor itself.
+struct unillm_qweight {
+    int qtype;
+    int device;
+    int64_t n, k, kb;      // kb = k / 32
+    uint8_t* qs;           // [n][kb][qbytes]
+    uint16_t* d;           // [n][kb]
+    void* base;            // single allocation holding both planes
+    size_t bytes;
+    int f16_exp;           // E >= 0 with 8 * max|d| * 2^-E <= 65504 (f16 range)
+};
+
+namespace unillm {
+
+constexpr int QK = 32;  // weights per block
+using QWeight = ::unillm_qweight;
+
+int64_t gemv_max_kb(int64_t m);
+
+inline int qbytes(int qtype) { return qtype == UNILLM_QTYPE_Q4_0 ? 16 : 32; }
+inline int gguf_block_bytes(int qtype) { return qtype == UNILLM_QTYPE_Q4_0 ? 18 : 34; }
+
+// Per-device properties cached at init.
+struct DeviceInfo {
+    int cu_count;
+    int max_lds;
+};
+const DeviceInfo& device_info();
+
+// ---- launchers (each in the translation unit that holds its kernel) ----------
+// All return a hipError_t from the launch; shapes are validated by the caller.
+hipError_t launch_repack(const QWeight& w, const uint8_t* gguf, hipStream_t s);
+hipError_t launch_dequant(const QWeight& w, float* out, hipStream_t s);
+// max over the scale plane of (f16 bits & 0x7FFF), atomically max-ed into *out
+hipError_t launch_scale_absmax(const QWeight& w, uint32_t* out, hipStream_t s);
+hipError_t launch_quantize(int qtype, const float* w, int64_t n, int64_t k, uint8_t* out,
+                           hipStream_t s);
+hipError_t launch_gemv(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t s);
+hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float* y,
+                              hipStream_t s);
+hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, float* y,
+                               hipStream_t s);
+
+constexpr int64_t kGemvMaxM = 2;
+constexpr int64_t kDecodeMaxM = 64;
+
+}  // namespace unillm

@@ -1,0 +1,204 @@
+// weights.hip -- load-time kernels: GGUF repack, exact dequant, GGML quantizer.
+//
+// None of these is on the per-token path; they run once per weight (repack)
+// or in tests and tooling (dequant, quantize).  All are HBM-bound byte work.
+#include <hip/hip_fp16.h>
+
+#include <algorithm>
+
+#include "internal.hpp"
+
+namespace unillm {
+namespace {
+
+__device__ __forceinline__ uint16_t ld_u16(const uint8_t* p) {
+    return (uint16_t)(p[0] | ((uint16_t)p[1] << 8));
+}
+
+// One thread per block: GGUF {f16 d; qs[QB]} (18 / 34 B, only 2-byte aligned)
+// -> qs plane (16-byte aligned rows of payloads) + d plane.
+template <int QB>
+__global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__ src,
+                                                     uint8_t* __restrict__ qs,
+                                                     uint16_t* __restrict__ d,
+                                                     int64_t nblocks) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const uint8_t* b = src + i * (QB + 2);
+    d[i] = ld_u16(b);
+    uint32_t words[QB / 4];
+#pragma unroll
+    for (int w = 0; w < QB / 4; ++w) {
+        const uint8_t* p = b + 2 + 4 * w;
+        words[w] = (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) |
+                   ((uint32_t)p[3] << 24);
+    }
+    uint4* dst = reinterpret_cast<uint4*>(qs + i * QB);
+#pragma unroll
+    for (int v = 0; v < QB / 16; ++v)
+        dst[v] = make_uint4(words[4 * v], words[4 * v + 1], words[4 * v + 2], words[4 * v + 3]);
+}
+
+// Exact dequant (GGML to_float): Q4_0 w[j] = (lo(qs[j]) - 8) * d,
+// w[j + 16] = (hi(qs[j]) - 8) * d; Q8_0 w[j] = qs[j] * d.  One thread per
+// block.  Every product is exact in f32, so any evaluation order is bit-exact.
+template <int QT>
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ qs,
+                                                      const uint16_t* __restrict__ dsc,
+                                                      float* __restrict__ out,
+                                                      int64_t nblocks) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const float d = __half2float(__ushort_as_half(dsc[i]));
+    float4* o = reinterpret_cast<float4*>(out + i * QK);
+    if constexpr (QT == UNILLM_QTYPE_Q4_0) {
+        const uint4 q = *reinterpret_cast<const uint4*>(qs + i * 16);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            float lo[4], hi[4];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const uint32_t byte = (w[t] >> (8 * b)) & 0xFFu;
+                lo[b] = (float)((int)(byte & 0xF) - 8) * d;
+                hi[b] = (float)((int)(byte >> 4) - 8) * d;
+            }
+            o[t] = make_float4(lo[0], lo[1], lo[2], lo[3]);
+            o[4 + t] = make_float4(hi[0], hi[1], hi[2], hi[3]);
+        }
+    } else {
+        const uint4* q = reinterpret_cast<const uint4*>(qs + i * 32);
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+            const uint4 qq = q[v];
+            const uint32_t w[4] = {qq.x, qq.y, qq.z, qq.w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                float f[4];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) f[b] = (float)(int8_t)(w[t] >> (8 * b)) * d;
+                o[4 * v + t] = make_float4(f[0], f[1], f[2], f[3]);
+            }
+        }
+    }
+}
+
+// GGML reference quantizers (quantize_row_q4_0_ref / q8_0_ref, which candle's
+// BlockQ4_0/BlockQ8_0::from_float restate).  Explicit _rn intrinsics keep the
+// multiply and the add separately rounded, as the reference does: a fused
+// multiply-add here would change which side of x.5 some values fall on.
+template <int QT>
+__global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__ w,
+                                                       uint8_t* __restrict__ out,
+                                                       int64_t nblocks) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const float4* src = reinterpret_cast<const float4*>(w + i * QK);
+    float x[QK];
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+        const float4 f = src[v];
+        x[4 * v] = f.x; x[4 * v + 1] = f.y; x[4 * v + 2] = f.z; x[4 * v + 3] = f.w;
+    }
+    constexpr int BB = QT == UNILLM_QTYPE_Q4_0 ? 18 : 34;
+    uint8_t* o = out + i * BB;
+    if constexpr (QT == UNILLM_QTYPE_Q4_0) {
+        float amax = 0.0f, mx = 0.0f;
+#pragma unroll
+        for (int j = 0; j < QK; ++j) {  // first element of largest magnitude, signed
+            const float a = fabsf(x[j]);
+            if (amax < a) { amax = a; mx = x[j]; }
+        }
+        // d = mx / -8 is exact in f32.  An all-zero block keeps mx = +0, so GGML
+        // stores d = -0.0 (f16 0x8000); that case is written explicitly because
+        // the compiler folds the product into the f16 conversion as
+        // fma(mx, -0.125, +0), whose zero result is +0.
+        const float d = __fmul_rn(mx, -0.125f);
+        const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+        const uint16_t dh = amax == 0.0f ? (uint16_t)0x8000u
+                                         : __half_as_ushort(__float2half_rn(d));
+        o[0] = (uint8_t)dh;
+        o[1] = (uint8_t)(dh >> 8);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            int q0 = (int)(int8_t)(int)__fadd_rn(__fmul_rn(x[j], id), 8.5f);
+            int q1 = (int)(int8_t)(int)__fadd_rn(__fmul_rn(x[j + 16], id), 8.5f);
+            q0 = q0 > 15 ? 15 : q0;
+            q1 = q1 > 15 ? 15 : q1;
+            o[2 + j] = (uint8_t)(q0 | (q1 << 4));
+        }
+    } else {
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < QK; ++j) amax = fmaxf(amax, fabsf(x[j]));
+        const float d = __fdiv_rn(amax, 127.0f);
+        const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+        const uint16_t dh = __half_as_ushort(__float2half_rn(d));
+        o[0] = (uint8_t)dh;
+        o[1] = (uint8_t)(dh >> 8);
+#pragma unroll
+        for (int j = 0; j < QK; ++j) o[2 + j] = (uint8_t)(int8_t)roundf(__fmul_rn(x[j], id));
+    }
+}
+
+// max |d| over the scale plane, as f16 magnitude bits (monotone in |d| for
+// finite values).  Used once per weight to pick the f16 exponent offset.
+__global__ __launch_bounds__(256) void scale_absmax_kernel(const uint16_t* __restrict__ d,
+                                                           int64_t count,
+                                                           uint32_t* __restrict__ out) {
+    __shared__ uint32_t part[256];
+    uint32_t m = 0;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += (int64_t)gridDim.x * blockDim.x)
+        m = max(m, (uint32_t)(d[i] & 0x7FFFu));
+    part[threadIdx.x] = m;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) part[threadIdx.x] = max(part[threadIdx.x], part[threadIdx.x + s]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) atomicMax(out, part[0]);
+}
+
+inline unsigned grid_for(int64_t items, int block) {
+    return (unsigned)((items + block - 1) / block);
+}
+
+}  // namespace
+
+hipError_t launch_repack(const QWeight& w, const uint8_t* gguf, hipStream_t s) {
+    const int64_t nb = w.n * w.kb;
+    if (w.qtype == UNILLM_QTYPE_Q4_0)
+        repack_kernel<16><<<grid_for(nb, 256), 256, 0, s>>>(gguf, w.qs, w.d, nb);
+    else
+        repack_kernel<32><<<grid_for(nb, 256), 256, 0, s>>>(gguf, w.qs, w.d, nb);
+    return hipGetLastError();
+}
+
+hipError_t launch_scale_absmax(const QWeight& w, uint32_t* out, hipStream_t s) {
+    const int64_t nb = w.n * w.kb;
+    const unsigned grid = (unsigned)std::min<int64_t>(1024, (nb + 255) / 256);
+    scale_absmax_kernel<<<grid, 256, 0, s>>>(w.d, nb, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant(const QWeight& w, float* out, hipStream_t s) {
+    const int64_t nb = w.n * w.kb;
+    if (w.qtype == UNILLM_QTYPE_Q4_0)
+        dequant_kernel<UNILLM_QTYPE_Q4_0><<<grid_for(nb, 256), 256, 0, s>>>(w.qs, w.d, out, nb);
+    else
+        dequant_kernel<UNILLM_QTYPE_Q8_0><<<grid_for(nb, 256), 256, 0, s>>>(w.qs, w.d, out, nb);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize(int qtype, const float* w, int64_t n, int64_t k, uint8_t* out,
+                           hipStream_t s) {
+    const int64_t nb = n * (k / QK);
+    if (qtype == UNILLM_QTYPE_Q4_0)
+        quantize_kernel<UNILLM_QTYPE_Q4_0><<<grid_for(nb, 256), 256, 0, s>>>(w, out, nb);
+    else
+        quantize_kernel<UNILLM_QTYPE_Q8_0><<<grid_for(nb, 256), 256, 0, s>>>(w, out, nb);
+    return hipGetLastError();
+}
+
+}  // namespace unillm

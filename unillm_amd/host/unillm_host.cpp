@@ -1,0 +1,331 @@
+// unillm_host.cpp -- implementation of the C++ host layer (see unillm_host.hpp).
+#include "unillm_host.hpp"
+
+#include <cstring>
+
+namespace unillm {
+
+namespace {
+
+void check(int rc, const char* what) {
+    if (rc != UNILLM_OK)
+        throw Error(std::string(what) + ": " + unillm_hip_last_error());
+}
+
+int64_t product(const std::vector<int64_t>& shape) {
+    int64_t p = 1;
+    for (int64_t d : shape) {
+        if (d < 0) throw Error("negative dimension");
+        p *= d;
+    }
+    return p;
+}
+
+// IEEE binary16 / bfloat16 -> binary32 (exact) for F16 / BF16 GGUF tensors.
+float half_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t exp = (h >> 10) & 0x1Fu;
+    const uint32_t man = h & 0x3FFu;
+    uint32_t bits;
+    if (exp == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else {
+            float v = (float)man * (1.0f / 16777216.0f);  // man * 2^-24, exact
+            std::memcpy(&bits, &v, 4);
+            bits |= sign;
+        }
+    } else if (exp == 31) {
+        bits = sign | 0x7F800000u | (man << 13);
+    } else {
+        bits = sign | ((exp + 112u) << 23) | (man << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+float bf16_to_float(uint16_t h) {
+    const uint32_t bits = (uint32_t)h << 16;
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+}  // namespace
+
+std::string Device::to_string() const {
+    switch (kind) {
+        case DeviceKind::CPU: return "CPU";
+        case DeviceKind::CUDA: return "CUDA(" + std::to_string(id) + ")";
+        case DeviceKind::Metal: return "Metal(" + std::to_string(id) + ")";
+        case DeviceKind::HIP: return "HIP(" + std::to_string(id) + ")";
+    }
+    return "?";
+}
+
+// ---- HipStorage ----------------------------------------------------------------------------
+HipStorage::HipStorage(size_t bytes, Device device) : bytes_(bytes), device_(device) {
+    if (!device.is_hip()) throw Error("HipStorage on " + device.to_string());
+    check(unillm_hip_init((int)device.id), "unillm_hip_init");
+    if (bytes) check(unillm_hip_malloc(&ptr_, bytes), "unillm_hip_malloc");
+}
+
+HipStorage::~HipStorage() {
+    if (ptr_) unillm_hip_free(ptr_);
+}
+
+// ---- Tensor --------------------------------------------------------------------------------
+Tensor Tensor::empty(std::vector<int64_t> shape, const Device& device) {
+    Tensor t;
+    const int64_t n = product(shape);
+    t.shape_ = std::move(shape);
+    t.device_ = device;
+    if (device.is_hip())
+        t.dev_ = std::make_shared<HipStorage>((size_t)n * sizeof(float), device);
+    else if (device.kind == DeviceKind::CPU)
+        t.host_ = std::make_shared<std::vector<float>>((size_t)n);
+    else
+        throw Error("tensors on " + device.to_string() + " are not supported by this build");
+    return t;
+}
+
+Tensor Tensor::from_host(const std::vector<float>& data, std::vector<int64_t> shape,
+                         const Device& device) {
+    if ((int64_t)data.size() != product(shape)) throw Error("data size does not match shape");
+    Tensor t = empty(std::move(shape), device);
+    if (device.is_hip()) {
+        if (!data.empty())
+            check(unillm_hip_memcpy_htod(t.dev_->data_ptr(), data.data(),
+                                         data.size() * sizeof(float)),
+                  "copy to device");
+    } else {
+        *t.host_ = data;
+    }
+    return t;
+}
+
+int64_t Tensor::numel() const { return product(shape_); }
+
+int64_t Tensor::dim(int i) const {
+    const int r = (int)shape_.size();
+    if (i < 0) i += r;
+    if (i < 0 || i >= r) throw Error("dimension index out of range");
+    return shape_[(size_t)i];
+}
+
+const float* Tensor::data() const {
+    if (dev_) return static_cast<const float*>(dev_->data_ptr());
+    return host_ ? host_->data() : nullptr;
+}
+
+float* Tensor::data_mut() {
+    if (dev_) return static_cast<float*>(dev_->data_ptr());
+    return host_ ? host_->data() : nullptr;
+}
+
+std::vector<float> Tensor::to_host() const {
+    if (host_) return *host_;
+    std::vector<float> out((size_t)numel());
+    if (!out.empty())
+        check(unillm_hip_memcpy_dtoh(out.data(), dev_->data_ptr(), out.size() * sizeof(float)),
+              "copy to host");
+    return out;
+}
+
+Tensor Tensor::to_device(const Device& device) const {
+    if (device == device_) return *this;
+    return from_host(to_host(), shape_, device);
+}
+
+Tensor Tensor::reshape(std::vector<int64_t> shape) const {
+    if (product(shape) != numel()) throw Error("reshape changes the element count");
+    Tensor t = *this;
+    t.shape_ = std::move(shape);
+    return t;
+}
+
+// ---- QuantLinear ---------------------------------------------------------------------------
+std::shared_ptr<QuantLinear> QuantLinear::from_blocks(int qtype, int64_t n, int64_t k,
+                                                      const void* blocks, size_t nbytes) {
+    std::shared_ptr<QuantLinear> q(new QuantLinear());
+    check(unillm_hip_qweight_create(qtype, n, k, blocks, nbytes, 0, &q->w_),
+          "Failed to create QMatMul");
+    q->qtype_ = qtype;
+    q->n_ = n;
+    q->k_ = k;
+    return q;
+}
+
+QuantLinear::~QuantLinear() { unillm_hip_qweight_destroy(w_); }
+
+Tensor QuantLinear::forward(const Tensor& x, void* stream) const {
+    // candle QMatMul::forward rules (called at llama.rs:1188): f32, rank >= 2,
+    // last dim == k; output [.., n], freshly allocated.
+    if (x.shape().size() < 2)
+        throw Error("QMatMul forward failed: rank " + std::to_string(x.shape().size()) +
+                    " input, need rank >= 2");
+    if (x.dim(-1) != k_)
+        throw Error("QMatMul forward failed: input last dim " + std::to_string(x.dim(-1)) +
+                    " != k " + std::to_string(k_));
+    if (!x.device().is_hip())
+        throw Error("QMatMul forward failed: input is on " + x.device().to_string() +
+                    ", weight is on HIP");
+    std::vector<int64_t> oshape = x.shape();
+    oshape.back() = n_;
+    Tensor y = Tensor::empty(oshape, x.device());
+    const int64_t m = x.numel() / k_;
+    check(unillm_hip_qmatmul(w_, x.data(), m, y.data_mut(), stream), "QMatMul forward failed");
+    return y;
+}
+
+Tensor QuantLinear::dequantize(void* stream) const {
+    Tensor out = Tensor::empty({n_, k_}, Device::hip(0));
+    check(unillm_hip_dequant(w_, out.data_mut(), stream), "Failed to dequantize");
+    check(unillm_hip_synchronize(), "Failed to dequantize");
+    return out;
+}
+
+Tensor HipTensorOps::matmul(const Tensor& a, const QuantLinear& b) {
+    return b.forward(a, stream_);
+}
+
+// ---- ModelWeights / loader -----------------------------------------------------------------
+std::shared_ptr<QuantLinear> ModelWeights::get_quantized(const std::string& name) const {
+    auto it = quantized_tensors.find(name);
+    return it == quantized_tensors.end() ? nullptr : it->second;
+}
+
+std::string gguf_to_hf_name(const std::string& gguf_name) {
+    // The reference's ordered replacement table (weight_loader_core.rs:764-795):
+    // the order matters (".attn_output.weight" before "output.weight").
+    static const char* const kMap[][2] = {
+        {"token_embd.weight", "model.embed_tokens.weight"},
+        {"blk.", "model.layers."},
+        {".attn_output.weight", ".self_attn.o_proj.weight"},
+        {".attn_q.weight", ".self_attn.q_proj.weight"},
+        {".attn_k.weight", ".self_attn.k_proj.weight"},
+        {".attn_v.weight", ".self_attn.v_proj.weight"},
+        {".attn_output.bias", ".self_attn.o_proj.bias"},
+        {".attn_q.bias", ".self_attn.q_proj.bias"},
+        {".attn_k.bias", ".self_attn.k_proj.bias"},
+        {".attn_v.bias", ".self_attn.v_proj.bias"},
+        {"output_norm.weight", "model.norm.weight"},
+        {"output.weight", "lm_head.weight"},
+        {".ffn_gate.weight", ".mlp.gate_proj.weight"},
+        {".ffn_up.weight", ".mlp.up_proj.weight"},
+        {".ffn_down.weight", ".mlp.down_proj.weight"},
+        {".ffn_gate.bias", ".mlp.gate_proj.bias"},
+        {".ffn_up.bias", ".mlp.up_proj.bias"},
+        {".ffn_down.bias", ".mlp.down_proj.bias"},
+        {".attn_norm.weight", ".input_layernorm.weight"},
+        {".ffn_norm.weight", ".post_attention_layernorm.weight"},
+        {".attn_norm.bias", ".input_layernorm.bias"},
+        {".ffn_norm.bias", ".post_attention_layernorm.bias"},
+    };
+    std::string s = gguf_name;
+    for (const auto& m : kMap) {
+        const std::string from = m[0], to = m[1];
+        std::string out;
+        size_t pos = 0, hit;
+        while ((hit = s.find(from, pos)) != std::string::npos) {  // Rust str::replace: all, left to right
+            out.append(s, pos, hit - pos);
+            out += to;
+            pos = hit + from.size();
+        }
+        out.append(s, pos, std::string::npos);
+        s = std::move(out);
+    }
+    return s;
+}
+
+bool is_quantized_weight_name(const std::string& hf_name) {
+    return hf_name.find("_proj.weight") != std::string::npos ||
+           hf_name.find("lm_head.weight") != std::string::npos;
+}
+
+bool GgufWeightLoader::supports(const std::string& path) const {
+    return path.size() >= 5 && path.compare(path.size() - 5, 5, ".gguf") == 0;
+}
+
+GgufModelConfig GgufWeightLoader::config_from(const GgufFile& f) {
+    // GGUFModelConfig::from_gguf_metadata (weight_loader_core.rs:35-98):
+    // "{arch}.key" first, then the llama key.
+    GgufModelConfig c;
+    c.architecture = f.get_string("general.architecture", "llama");
+    auto get = [&](const std::string& key) {
+        return f.get_uint(c.architecture + "." + key, f.get_uint("llama." + key, 0));
+    };
+    c.hidden_size = get("embedding_length");
+    c.intermediate_size = get("feed_forward_length");
+    c.num_hidden_layers = get("block_count");
+    c.num_attention_heads = get("attention.head_count");
+    c.num_key_value_heads = f.get_uint(c.architecture + ".attention.head_count_kv",
+                                       f.get_uint("llama.attention.head_count_kv",
+                                                  c.num_attention_heads));
+    c.vocab_size = get("vocab_size");
+    if (c.vocab_size == 0)
+        if (const GgufValue* t = f.find("tokenizer.ggml.tokens"))
+            if (t->kind == GgufValue::ARRAY) c.vocab_size = t->items.size();
+    return c;
+}
+
+std::vector<GgufWeightLoader::Plan> GgufWeightLoader::plan(const GgufFile& f) const {
+    std::vector<Plan> out;
+    for (const GgufTensorInfo& t : f.tensors()) {
+        Plan p;
+        p.gguf_name = t.name;
+        p.hf_name = gguf_to_hf_name(t.name);
+        p.shape = t.shape();
+        p.type = t.type;
+        p.quantized = is_quantized_weight_name(p.hf_name);
+        out.push_back(std::move(p));
+    }
+    return out;
+}
+
+ModelWeights GgufWeightLoader::load_weights(const std::string& path) const {
+    const GgufFile f = GgufFile::open(path);
+    ModelWeights w;
+    w.config = config_from(f);
+    for (const GgufTensorInfo& t : f.tensors()) {
+        const std::string hf = gguf_to_hf_name(t.name);
+        const std::vector<uint8_t> bytes = f.read(t);
+        const std::vector<uint64_t> shp = t.shape();
+        if (is_quantized_weight_name(hf)) {
+            if (t.ne.size() != 2 || (t.type != GGML_Q4_0 && t.type != GGML_Q8_0))
+                throw Error("Failed to create QMatMul for '" + t.name + "': " +
+                            ggml_type_name(t.type) + " " + std::to_string(t.ne.size()) +
+                            "-D weights are not supported on the HIP device (Q4_0 / Q8_0 only)");
+            w.quantized_tensors[hf] = QuantLinear::from_blocks(
+                (int)t.type, (int64_t)t.ne[1], (int64_t)t.ne[0], bytes.data(), bytes.size());
+            continue;
+        }
+        // embeddings, norms: dequantize to f32 on the host (weight_loader_core.rs:579)
+        std::vector<int64_t> shape(shp.begin(), shp.end());
+        int64_t elems = 1;
+        for (int64_t d : shape) elems *= d;
+        std::vector<float> v((size_t)elems);
+        if (t.type == GGML_F32) {
+            std::memcpy(v.data(), bytes.data(), v.size() * 4);
+        } else if (t.type == GGML_F16 || t.type == GGML_BF16) {
+            for (size_t i = 0; i < v.size(); ++i) {
+                uint16_t h;
+                std::memcpy(&h, bytes.data() + 2 * i, 2);
+                v[i] = t.type == GGML_F16 ? half_to_float(h) : bf16_to_float(h);
+            }
+        } else if (t.type == GGML_Q4_0 || t.type == GGML_Q8_0) {
+            const int64_t k = (int64_t)t.ne[0];
+            const int64_t n = elems / k;
+            auto q = QuantLinear::from_blocks((int)t.type, n, k, bytes.data(), bytes.size());
+            v = q->dequantize().to_host();
+        } else {
+            throw Error("Failed to dequantize tensor '" + t.name + "': " +
+                        ggml_type_name(t.type) + " is not supported by this build");
+        }
+        w.tensors[hf] = Tensor::from_host(v, shape, Device::cpu());
+    }
+    return w;
+}
+
+}  // namespace unillm

@@ -1,0 +1,178 @@
+// unillm_host.hpp -- C++ host side of the HIP quantized linear-layer device.
+//
+// The reference is Rust (cognisoc/unillm); no Rust toolchain exists in this
+// build environment, so the host layer above the C ABI is C++ that mirrors
+// the reference's interface for this path, name for name:
+//
+//   reference (crates/runtime/src/...)              here
+//   tensor_core.rs:39-44   enum Device {CPU, CUDA, Metal}   Device (+ HIP(id))
+//   tensor_core.rs:47-70   trait TensorStorage             HipStorage
+//   tensor_core.rs:13-24   struct Tensor                   Tensor (f32, host or HIP)
+//   tensor_core.rs:179-296 trait TensorOps::matmul         TensorOps / HipTensorOps
+//   model_core.rs:124-138  ModelWeights{tensors, quantized_tensors}   ModelWeights
+//   model_core.rs:469-471  ModelWeights::get_quantized     ModelWeights::get_quantized
+//   candle QMatMul (Arc)   used at llama.rs:1184-1195       QuantLinear
+//   weight_loader_core.rs:504-608  GGUFWeightLoader       GgufWeightLoader
+//   weight_loader_core.rs:760-798  gguf_to_hf_name        gguf_to_hf_name
+//
+// Errors are exceptions carrying the reference's anyhow text ("QMatMul
+// forward failed: ...").  All device work goes through include/unillm_hip.h.
+#pragma once
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/unillm_hip.h"
+#include "gguf.hpp"
+
+namespace unillm {
+
+struct Error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+// ---- Device ------------------------------------------------------------------------------
+enum class DeviceKind { CPU, CUDA, Metal, HIP };
+
+struct Device {
+    DeviceKind kind = DeviceKind::CPU;
+    size_t id = 0;
+    static Device cpu() { return {DeviceKind::CPU, 0}; }
+    static Device hip(size_t id) { return {DeviceKind::HIP, id}; }
+    bool is_hip() const { return kind == DeviceKind::HIP; }
+    bool operator==(const Device& o) const { return kind == o.kind && id == o.id; }
+    bool operator!=(const Device& o) const { return !(*this == o); }
+    std::string to_string() const;
+};
+
+// ---- Storage -----------------------------------------------------------------------------
+// Device memory owned through the C ABI's allocator (TensorStorage on HIP).
+class HipStorage {
+public:
+    HipStorage(size_t bytes, Device device);
+    ~HipStorage();
+    HipStorage(const HipStorage&) = delete;
+    HipStorage& operator=(const HipStorage&) = delete;
+    void* data_ptr() const { return ptr_; }
+    size_t size_bytes() const { return bytes_; }
+    const Device& device() const { return device_; }
+
+private:
+    void* ptr_ = nullptr;
+    size_t bytes_ = 0;
+    Device device_;
+};
+
+// ---- Tensor (f32 only: the dtype of this path's activations and outputs) ------------------
+class Tensor {
+public:
+    Tensor() = default;
+    static Tensor from_host(const std::vector<float>& data, std::vector<int64_t> shape,
+                            const Device& device);
+    static Tensor empty(std::vector<int64_t> shape, const Device& device);
+
+    const std::vector<int64_t>& shape() const { return shape_; }
+    int64_t numel() const;
+    int64_t dim(int i) const;  // negative i counts from the end
+    const Device& device() const { return device_; }
+    const float* data() const;       // host or device pointer, per device()
+    float* data_mut();
+    Tensor to_device(const Device& device) const;
+    std::vector<float> to_host() const;
+    Tensor reshape(std::vector<int64_t> shape) const;
+
+private:
+    std::vector<int64_t> shape_;
+    Device device_;
+    std::shared_ptr<std::vector<float>> host_;
+    std::shared_ptr<HipStorage> dev_;
+};
+
+// ---- the quantized projection --------------------------------------------------------------
+// Holds one GGUF Q4_0 / Q8_0 weight [n, k] resident on the HIP device; the
+// slot `Arc<QMatMul>` occupies in ModelWeights.
+class QuantLinear {
+public:
+    static std::shared_ptr<QuantLinear> from_blocks(int qtype, int64_t n, int64_t k,
+                                                    const void* blocks, size_t nbytes);
+    ~QuantLinear();
+    QuantLinear(const QuantLinear&) = delete;
+    QuantLinear& operator=(const QuantLinear&) = delete;
+
+    // QMatMul::forward: [.., k] f32 -> [.., n] f32 (rank >= 2, last dim k).
+    Tensor forward(const Tensor& x, void* stream = nullptr) const;
+    // qtensor.dequantize: f32 [n, k] on the device, bit-exact with GGML.
+    Tensor dequantize(void* stream = nullptr) const;
+
+    int qtype() const { return qtype_; }
+    int64_t n() const { return n_; }
+    int64_t k() const { return k_; }
+    const unillm_qweight* handle() const { return w_; }
+
+private:
+    QuantLinear() = default;
+    unillm_qweight* w_ = nullptr;
+    int qtype_ = 0;
+    int64_t n_ = 0, k_ = 0;
+};
+
+// ---- ops dispatch ----------------------------------------------------------------------------
+class TensorOps {
+public:
+    virtual ~TensorOps() = default;
+    // out = a . b^T where b is a quantized [n, k] weight (the call
+    // quantized_matmul makes); f32 x f32 matmul is not part of this device.
+    virtual Tensor matmul(const Tensor& a, const QuantLinear& b) = 0;
+};
+
+class HipTensorOps : public TensorOps {
+public:
+    explicit HipTensorOps(void* stream = nullptr) : stream_(stream) {}
+    Tensor matmul(const Tensor& a, const QuantLinear& b) override;
+
+private:
+    void* stream_;
+};
+
+// ---- weights and loading --------------------------------------------------------------------
+struct GgufModelConfig {
+    std::string architecture;
+    uint64_t hidden_size = 0, intermediate_size = 0, num_hidden_layers = 0;
+    uint64_t num_attention_heads = 0, num_key_value_heads = 0, vocab_size = 0;
+};
+
+struct ModelWeights {
+    std::map<std::string, Tensor> tensors;                                  // f32, host
+    std::map<std::string, std::shared_ptr<QuantLinear>> quantized_tensors;  // HIP
+    GgufModelConfig config;
+    std::shared_ptr<QuantLinear> get_quantized(const std::string& name) const;
+};
+
+// weight_loader_core.rs:760-798: ordered substring replacements.
+std::string gguf_to_hf_name(const std::string& gguf_name);
+// weight_loader_core.rs:554: which tensors stay quantized.
+bool is_quantized_weight_name(const std::string& hf_name);
+
+class GgufWeightLoader {
+public:
+    bool supports(const std::string& path) const;
+    // Parses the file, uploads every *_proj / lm_head tensor to the device as
+    // a QuantLinear and dequantizes the rest to host f32.
+    ModelWeights load_weights(const std::string& path) const;
+    // What load_weights would do, without any device work: hf name, shape,
+    // type and whether it would be quantized, per tensor.
+    struct Plan {
+        std::string gguf_name, hf_name;
+        std::vector<uint64_t> shape;
+        uint32_t type;
+        bool quantized;
+    };
+    std::vector<Plan> plan(const GgufFile& file) const;
+    static GgufModelConfig config_from(const GgufFile& file);
+};
+
+}  // namespace unillm

@@ -1,0 +1,152 @@
+"""QuantLinear: a device-resident GGUF Q4_0 / Q8_0 weight and its forward.
+
+It takes the slot that `Arc<QMatMul>` holds in unillm's
+`ModelWeights.quantized_tensors` (crates/runtime/src/model_core.rs:134) and
+mirrors the call the model makes on it:
+
+    qmatmul.forward(&input)   -> QuantLinear.forward(x)
+      (crates/runtime/src/models_v2/llama.rs:1184-1195, 1325-1336, 396-405)
+
+with candle's argument rules (f32, contiguous, rank >= 2, last dim == k,
+output [..., n]) and its error text ("QMatMul forward failed: ...").  Torch is
+used only for device memory and the current stream; all arithmetic runs in
+libunillm_hip.so.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _capi
+from ._capi import BLOCK_BYTES, QK, Q4_0, Q8_0, HipError
+
+
+def _stream_ptr(stream: torch.cuda.Stream | None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return int(s.cuda_stream)
+
+
+class QuantLinear:
+    """One quantized projection (W is [n, k] = [out_features, in_features])."""
+
+    def __init__(self, handle: int, qtype: int, n: int, k: int):
+        self._h = ctypes.c_void_p(handle)
+        self.qtype = qtype
+        self.n = n
+        self.k = k
+
+    # ---- construction (WeightLoaderCore's QMatMul::from_arc, weight_loader_core.rs:569)
+    @classmethod
+    def from_blocks(cls, qtype: int, n: int, k: int, blocks) -> "QuantLinear":
+        """From GGUF block bytes in host memory (n * k/32 blocks of 18 / 34 B)."""
+        buf = np.ascontiguousarray(np.frombuffer(memoryview(blocks), dtype=np.uint8))
+        h = ctypes.c_void_p()
+        _capi.check(_capi.lib().unillm_hip_qweight_create(
+            qtype, n, k, buf.ctypes.data, buf.nbytes, 0, ctypes.byref(h)))
+        return cls(h.value, qtype, n, k)
+
+    @classmethod
+    def from_device_blocks(cls, qtype: int, n: int, k: int, blocks: torch.Tensor,
+                           stream: torch.cuda.Stream | None = None) -> "QuantLinear":
+        """From GGUF block bytes already on the device (a uint8 CUDA tensor)."""
+        if blocks.dtype != torch.uint8 or not blocks.is_cuda or not blocks.is_contiguous():
+            raise ValueError("blocks must be a contiguous uint8 device tensor")
+        h = ctypes.c_void_p()
+        _capi.check(_capi.lib().unillm_hip_qweight_create_device(
+            qtype, n, k, blocks.data_ptr(), blocks.numel(), 0, _stream_ptr(stream),
+            ctypes.byref(h)))
+        return cls(h.value, qtype, n, k)
+
+    @classmethod
+    def quantize(cls, qtype: int, w: torch.Tensor,
+                 stream: torch.cuda.Stream | None = None) -> "QuantLinear":
+        """Quantize an f32 [n, k] device tensor with the GGML quantizer, then load it."""
+        blocks = quantize_blocks(qtype, w, stream)
+        return cls.from_device_blocks(qtype, w.shape[0], w.shape[1], blocks, stream)
+
+    # ---- queries -----------------------------------------------------------------------
+    @property
+    def shape(self) -> tuple[int, int]:
+        return (self.n, self.k)
+
+    @property
+    def device_bytes(self) -> int:
+        nb = ctypes.c_size_t()
+        _capi.check(_capi.lib().unillm_hip_qweight_info(self._h, None, None, None,
+                                                        ctypes.byref(nb)))
+        return nb.value
+
+    @property
+    def gguf_bytes(self) -> int:
+        return self.n * (self.k // QK) * BLOCK_BYTES[self.qtype]
+
+    def select_path(self, m: int) -> int:
+        return _capi.lib().unillm_hip_select_path(self._h, m)
+
+    # ---- compute -------------------------------------------------------------------------
+    def forward(self, x: torch.Tensor, path: int = _capi.PATH_AUTO,
+                out: torch.Tensor | None = None,
+                stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        """y[..., n] = x[..., k] . dequant(W)^T (QMatMul::forward)."""
+        if x.dtype != torch.float32:
+            raise RuntimeError(f"QMatMul forward failed: expected f32 input, got {x.dtype}")
+        if x.dim() < 2:
+            raise RuntimeError(f"QMatMul forward failed: rank {x.dim()} input, need rank >= 2")
+        if x.shape[-1] != self.k:
+            raise RuntimeError(
+                f"QMatMul forward failed: input last dim {x.shape[-1]} != k {self.k}")
+        if not x.is_cuda:
+            raise RuntimeError("QMatMul forward failed: input is not on the HIP device")
+        if not x.is_contiguous():
+            raise RuntimeError("QMatMul forward failed: input is not contiguous")
+        m = x.numel() // self.k
+        if out is None:
+            out = torch.empty(*x.shape[:-1], self.n, dtype=torch.float32, device=x.device)
+        elif (out.dtype != torch.float32 or not out.is_contiguous()
+              or out.numel() != m * self.n):
+            raise RuntimeError("QMatMul forward failed: bad output tensor")
+        rc = _capi.lib().unillm_hip_qmatmul_path(self._h, x.data_ptr(), m, out.data_ptr(), path,
+                                                 _stream_ptr(stream))
+        if rc != _capi.OK:
+            raise HipError(rc, _capi.last_error())
+        return out
+
+    __call__ = forward
+
+    def dequantize(self, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        """f32 [n, k], bit-exact with GGML's to_float (weight_loader_core.rs:579)."""
+        out = torch.empty(self.n, self.k, dtype=torch.float32, device="cuda")
+        _capi.check(_capi.lib().unillm_hip_dequant(self._h, out.data_ptr(), _stream_ptr(stream)))
+        return out
+
+    # ---- lifetime ------------------------------------------------------------------------
+    def close(self) -> None:
+        if self._h is not None and self._h.value:
+            _capi.lib().unillm_hip_qweight_destroy(self._h)
+        self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __repr__(self) -> str:
+        name = {Q4_0: "Q4_0", Q8_0: "Q8_0"}.get(self.qtype, str(self.qtype))
+        return f"QuantLinear({name}, n={self.n}, k={self.k})"
+
+
+def quantize_blocks(qtype: int, w: torch.Tensor,
+                    stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """GGML quantizer on the device: f32 [n, k] -> uint8 GGUF block bytes."""
+    if w.dtype != torch.float32 or not w.is_cuda or not w.is_contiguous() or w.dim() != 2:
+        raise ValueError("w must be a contiguous f32 [n, k] device tensor")
+    n, k = w.shape
+    if k % QK:
+        raise ValueError(f"k = {k} is not a multiple of 32")
+    out = torch.empty(n * (k // QK) * BLOCK_BYTES[qtype], dtype=torch.uint8, device=w.device)
+    _capi.check(_capi.lib().unillm_hip_quantize(qtype, w.data_ptr(), n, k, out.data_ptr(),
+                                                _stream_ptr(stream)))
+    return out

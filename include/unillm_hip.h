@@ -47,7 +47,7 @@ extern "C" {
 
 /* Kernel path for unillm_hip_qmatmul_path (AUTO is what qmatmul uses). */
 #define UNILLM_PATH_AUTO 0
-#define UNILLM_PATH_GEMV 1         /* fused dequant + GEMV, fp32 VALU, m <= 2 */
+#define UNILLM_PATH_GEMV 1         /* fused dequant + GEMV (VALU int8 dot), m <= 4 */
 #define UNILLM_PATH_DECODE_MFMA 2  /* batched decode, f16 MFMA, fp32 accumulate */
 #define UNILLM_PATH_PREFILL_MFMA 3 /* prefill, LDS-staged bf16 MFMA, fp32 accumulate */
 

@@ -87,7 +87,8 @@ def test_device_quantizer_bit_exact(qtype, golden_cases):
 
 # ---- the reference's known answers --------------------------------------------------------
 
-@pytest.mark.parametrize("path,m", [(PATH_GEMV, 1), (PATH_GEMV, 2), (PATH_DECODE_MFMA, 3),
+@pytest.mark.parametrize("path,m", [(PATH_GEMV, 1), (PATH_GEMV, 2), (PATH_GEMV, 3),
+                                    (PATH_GEMV, 4), (PATH_DECODE_MFMA, 3),
                                     (PATH_DECODE_MFMA, 8)])
 def test_known_answer_6p3984375(path, m):
     # simd/matmul/gemv.rs:91-113, gemm.rs:377-402: d = f16(0.1), 0x99, x = 1
@@ -116,20 +117,23 @@ SHAPES = [(37, 96), (33, 4128), (64, 2048), (300, 4096), (129, 11008), (70, 1433
 
 @pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
 @pytest.mark.parametrize("n,k", SHAPES)
-@pytest.mark.parametrize("path,m", [(PATH_GEMV, 1), (PATH_GEMV, 2), (PATH_DECODE_MFMA, 2),
+@pytest.mark.parametrize("path,m", [(PATH_GEMV, 1), (PATH_GEMV, 2), (PATH_GEMV, 3),
+                                    (PATH_GEMV, 4), (PATH_DECODE_MFMA, 2),
                                     (PATH_DECODE_MFMA, 5), (PATH_DECODE_MFMA, 16),
                                     (PATH_DECODE_MFMA, 33), (PATH_DECODE_MFMA, 64),
                                     (PATH_PREFILL_MFMA, 65), (PATH_PREFILL_MFMA, 130)])
 def test_qmatmul_parity(qtype, n, k, path, m):
     blocks, x = _case(qtype, m, n, k, seed=n * 7 + k)
     ql = QuantLinear.from_blocks(qtype, n, k, blocks)
+    if path == PATH_GEMV and ql.select_path(m) != PATH_GEMV:
+        pytest.skip("k beyond the GEMV path's register budget at this m")
     y = _run(ql, x, path)
     ref = oracle.qmatmul_f64(qtype, blocks, x, n, k)
     assert y.shape == (m, n)
     e = oracle.normwise_error(y, ref)
     assert e < TOL[path], f"normwise {e:.3g}"
     if path == PATH_GEMV:
-        assert e < 1e-5  # fp32 with exact products: far inside the bar
+        assert e < 1e-4  # two int8 digits of x: ~3e-5, far inside the bar
 
 
 def test_golden_fixtures_auto_path(golden_cases):
@@ -146,8 +150,12 @@ def test_auto_path_selection():
     ql = QuantLinear.from_blocks(Q4_0, 16, 4096, blocks)
     assert ql.select_path(1) == PATH_GEMV
     assert ql.select_path(2) == PATH_GEMV
-    assert ql.select_path(3) == PATH_DECODE_MFMA
+    assert ql.select_path(4) == PATH_GEMV
+    assert ql.select_path(5) == PATH_DECODE_MFMA
     assert ql.select_path(64) == PATH_DECODE_MFMA
+    big = QuantLinear.from_blocks(Q4_0, 16, 11008, _case(Q4_0, 1, 16, 11008, seed=1)[0])
+    # 344 blocks per row: the x digits fit the registers at m = 1 only
+    assert big.select_path(1) == PATH_GEMV and big.select_path(2) == PATH_DECODE_MFMA
     assert ql.select_path(65) == PATH_PREFILL_MFMA
 
 
@@ -158,8 +166,12 @@ def test_auto_path_selection():
                                        (Q4_0, 11008, 4096)])
 def test_baseline_decode_shapes_m1(qtype, k, n):
     blocks, x = _case(qtype, 1, n, k, seed=k + n)
-    y = _run(QuantLinear.from_blocks(qtype, n, k, blocks), x, PATH_AUTO)
-    assert oracle.normwise_error(y, oracle.qmatmul_f64(qtype, blocks, x, n, k)) < 1e-5
+    ql = QuantLinear.from_blocks(qtype, n, k, blocks)
+    y = _run(ql, x, PATH_AUTO)
+    assert oracle.normwise_error(y, oracle.qmatmul_f64(qtype, blocks, x, n, k)) < 1e-4
+    # size-independent properties: power-of-two scaling and negation are exact
+    assert np.array_equal(_run(ql, x * np.float32(4.0), PATH_AUTO), 4.0 * y)
+    assert np.array_equal(_run(ql, -x, PATH_AUTO), -y)
 
 
 @pytest.mark.parametrize("m", [4, 16, 64])
@@ -219,8 +231,8 @@ def test_forward_argument_errors():
         ql.forward(torch.zeros(1, 64, device="cuda", dtype=torch.float16))
     with pytest.raises(HipError, match="16-byte aligned"):
         ql.forward(torch.zeros(2 * 64 + 1, device="cuda")[1:65].view(1, 64))
-    with pytest.raises(HipError, match="m <= 2"):
-        ql.forward(torch.zeros(3, 64, device="cuda"), path=PATH_GEMV)
+    with pytest.raises(HipError, match="m <= 4"):
+        ql.forward(torch.zeros(5, 64, device="cuda"), path=PATH_GEMV)
 
 
 def test_repeat_calls_deterministic():

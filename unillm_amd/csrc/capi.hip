@@ -87,18 +87,24 @@ int alloc_weight(int qtype, int64_t n, int64_t k, QWeight** out) {
     w->n = n;
     w->k = k;
     w->kb = k / QK;
-    const size_t qs_bytes = (size_t)(n * w->kb) * qbytes(qtype);
-    const size_t d_off = (qs_bytes + 255) & ~(size_t)255;
+    w->row_bytes = row_bytes_for(qtype, w->kb);
     // + a 256-byte tail slot for the scale reduction run at create
-    w->bytes = ((d_off + (size_t)(n * w->kb) * 2 + 255) & ~(size_t)255) + 256;
-    hipError_t e = hipMalloc(&w->base, w->bytes);
+    w->bytes = (((size_t)n * (size_t)w->row_bytes + 255) & ~(size_t)255) + 256;
+    void* mem = nullptr;
+    hipError_t e = hipMalloc(&mem, w->bytes);
     if (e != hipSuccess) {
         delete w;
         return e == hipErrorOutOfMemory ? fail(UNILLM_ERR_OUT_OF_MEMORY, "hipMalloc of weight")
                                         : fail_hip(e, "hipMalloc");
     }
-    w->qs = static_cast<uint8_t*>(w->base);
-    w->d = reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(w->base) + d_off);
+    w->base = static_cast<uint8_t*>(mem);
+    // row padding is never read as data; zero it anyway so device memory
+    // holds only defined bytes
+    if ((e = hipMemset(mem, 0, w->bytes)) != hipSuccess) {
+        (void)hipFree(mem);
+        delete w;
+        return fail_hip(e, "hipMemset");
+    }
     *out = w;
     return UNILLM_OK;
 }
@@ -107,7 +113,7 @@ int alloc_weight(int qtype, int64_t n, int64_t k, QWeight** out) {
 // applies, so that every (q - 8) * d * 2^-E (or q * d * 2^-E) fits f16.
 // Synchronises `s`.
 int finish_weight(QWeight* w, hipStream_t s) {
-    uint32_t* slot = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(w->base) + w->bytes - 256);
+    uint32_t* slot = reinterpret_cast<uint32_t*>(w->base + w->bytes - 256);
     uint32_t bits = 0;
     hipError_t e;
     if ((e = hipMemsetAsync(slot, 0, sizeof(uint32_t), s)) != hipSuccess)
@@ -235,7 +241,7 @@ int unillm_hip_qweight_info(const unillm_qweight* w, int* qtype, int64_t* n, int
 
 int unillm_hip_select_path(const unillm_qweight* w, int64_t m) {
     if (!w || m < 0) return fail(UNILLM_ERR_INVALID_ARG, "bad arguments to select_path");
-    if (m <= kGemvMaxM && w->kb <= gemv_max_kb(m)) return UNILLM_PATH_GEMV;
+    if (m <= kGemvMaxM && w->kb <= gemv_max_kb(m, w->qtype)) return UNILLM_PATH_GEMV;
     if (m <= kDecodeMaxM) return UNILLM_PATH_DECODE_MFMA;
     return UNILLM_PATH_PREFILL_MFMA;
 }
@@ -257,10 +263,10 @@ int unillm_hip_qmatmul_path(const unillm_qweight* w, const float* x_dev, int64_t
     hipError_t e;
     switch (path) {
         case UNILLM_PATH_GEMV:
-            if (m > kGemvMaxM || w->kb > gemv_max_kb(m))
+            if (m > kGemvMaxM || w->kb > gemv_max_kb(m, w->qtype))
                 return fail(UNILLM_ERR_UNSUPPORTED,
-                            "GEMV path takes m <= 2 and k <= " +
-                                std::to_string(gemv_max_kb(m) * QK) + " at this m");
+                            "GEMV path takes m <= 4 and k <= " +
+                                std::to_string(gemv_max_kb(m, w->qtype) * QK) + " at this m");
             e = launch_gemv(*w, x_dev, m, y_dev, s);
             break;
         case UNILLM_PATH_DECODE_MFMA:

@@ -1,37 +1,57 @@
-// gemv.hip -- fused dequant + GEMV for decode (m = 1, 2), fp32 VALU.
+// gemv.hip -- fused dequant + GEMV for decode (m <= 4).
 //
 // What it computes: y[m, n] = sum_k x[m, k] * dequant(W)[n, k], the decode
-// step of QMatMul::forward (crates/runtime/src/models_v2/llama.rs:1188) on one
-// token (m = 1) or two.  Bound: HBM -- every weight byte is read exactly once
-// and the arithmetic intensity is ~3.6 flop/B (Q4_0), far below the ridge.
+// step of QMatMul::forward (crates/runtime/src/models_v2/llama.rs:1188) for
+// one to four tokens.  Bound: HBM -- each weight byte is read once; the
+// arithmetic intensity is ~3.6 flop/B per token (Q4_0).
 //
-// Mapping (MI355X, wave64):
-//   - a wave owns a K-slice of at most 64 * NB blocks; lane l takes blocks
-//     l, l + 64, ... of the slice, so one wave-wide 128-bit load reads 1 KiB of
-//     contiguous Q4_0 payload (or half of that many Q8_0 blocks);
-//   - the lane keeps its slice of x in registers for all rows it visits
-//     (x[j] for the low nibbles, x[j + 16] / 16 for the high nibbles, so the
-//     masked byte 16*q converts with one v_cvt_f32_ubyte), and -8 * sum(x) of
-//     each block seeds the block accumulator, which folds the Q4_0 offset
-//     (Q8_0: bytes are biased by 128 and -128 * sum(x) seeds it);
-//   - R rows are loaded before any is used, so each wave has R * NB 128-bit
-//     loads in flight; the per-row partials are reduced with DPP row
-//     rotations plus two cross-row swizzles;
-//   - when K needs S > 1 slices, the S waves of a workgroup share the rows
-//     and combine their partials through LDS.
-// Numerics: every product (q - 8) * x is formed exactly in an fp32 FMA; block
-// sums are scaled by d in fp32.  Error vs the f64 oracle is ~1e-6 normwise.
+// Arithmetic.  Each 32-element block of x is written as two signed int8
+// digits over a per-block power-of-two scale s, max|x| / 127 < s <= 2 max|x| / 127:
+//     x[j] ~= s * (d0[j] + d1[j] / 254),  d0 = rint(x/s), d1 = rint((x/s - d0) * 254)
+// (|error| <= s / 508 <= max|x| / 32258 per element; x / s is exact, so
+// scaling x by a power of two scales y exactly).  The weight codes are exact
+// small integers, so each block's dot products are exact int32 sums computed
+// with v_dot4_i32_i8 (four products per instruction, ~1 VALU op per weight):
+//     Q4_0: sum_j (q_j - 8) x_j = s * ((D0 - 8 S0) + (D1 - 8 S1) / 254),
+//     D_i = sum_j q_j d_i[j], S_i = sum_j d_i[j]  (the -8 S_i seeds the sum);
+//     Q8_0: the same with signed codes and no offset.
+// Block results are scaled by d_w * s and summed in fp32.  Normwise error vs
+// the f64 oracle is ~3e-5 (bound 1e-3).
+//
+// Mapping (MI355X, wave64).  One 1024-thread workgroup per CU (two of 512
+// where a lane needs more than 128 VGPRs):
+//   1. every wave requests its first chunk of weights at once (they do not
+//      depend on x);
+//   2. the workgroup turns x into digits in LDS, four threads per 32-block,
+//      so each CU does this once, hidden under the latency of step 1;
+//   3. each wave owns a contiguous, balanced range of rows and walks it in
+//      chunks of R rows (lane l owns blocks l, l + 64, ... of every row),
+//      two chunks at a time; a wave-wide 128-bit load reads 1 KiB of
+//      contiguous Q4_0 payload.  Every load is branch-free (indices are
+//      clamped, validity is applied through the scale), so the in-order
+//      memory counter lets the x digits be built while the weights stream.  Row partials are reduced with DPP rotations and two
+//      cross-row shuffles.
 #include <hip/hip_fp16.h>
+
+#include <stdlib.h>
+
+#include <algorithm>
 
 #include "internal.hpp"
 
 namespace unillm {
 namespace {
 
+constexpr int kXWords = 20;             // LDS dwords per x block (19 used; conflict-free)
+constexpr float kRound = 12582912.0f;   // 1.5 * 2^23: t + kRound rounds t to an integer
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
-    return __builtin_bit_cast(
-        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+    return __builtin_bit_cast(float, dpp_i32<CTRL>(__builtin_bit_cast(int, v)));
 }
 
 // Sum over the 64 lanes; every lane receives the total.
@@ -45,210 +65,351 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+__device__ __forceinline__ int sdot4(int a, int b, int c) {
+    return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+// Low bytes of four registers -> one dword (v_perm_b32 selects bytes; 0x0C = zero).
+__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a0, uint32_t a1, uint32_t a2,
+                                                   uint32_t a3) {
+    return __builtin_amdgcn_perm(a1, a0, 0x0C0C0400u) | __builtin_amdgcn_perm(a3, a2, 0x04000C0Cu);
+}
+
+// ---- x digits -----------------------------------------------------------------------------
+// LDS record of one 32-element x block, in the byte order of the weight payload:
+// dwords 0-7 digit 0 of elements 4t..4t+3, 8-15 digit 1, 16 / 17 the seeds
+// c0 / c1 (-8 S_i for Q4_0, 0 for Q8_0), 18 the scale s.  (For Q4_0, payload
+// dword t meets digit dwords t (low nibbles) and 4 + t (high nibbles).)
+//
+// One thread builds one quarter (8 elements) of a block; the four threads of a
+// block are one DPP quad, so the block max and digit sums are quad reductions.
+// The math runs on every thread and only the stores are conditional, so the
+// compiler keeps the x loads where they are issued (ahead of the weights).
 template <int QT>
-struct Payload;
-template <>
-struct Payload<UNILLM_QTYPE_Q4_0> {
-    static constexpr int V = 1;  // uint4 loads per block
-};
-template <>
-struct Payload<UNILLM_QTYPE_Q8_0> {
-    static constexpr int V = 2;
-};
-
-template <int QT, int M, int NB, int R>
-__global__ __launch_bounds__(512) void gemv_kernel(const uint8_t* __restrict__ qs,
-                                                   const uint16_t* __restrict__ dsc,
-                                                   const float* __restrict__ x,
-                                                   float* __restrict__ y, int N, int KB, int S,
-                                                   int SB, int G) {
-    constexpr int V = Payload<QT>::V;
-    constexpr int QB = 16 * V;
-    __shared__ float red[8 * R * M];
-
-    const int lane = threadIdx.x & 63;
-    const int wv = threadIdx.x >> 6;
-    const int s = wv % S;
-    const int g = wv / S;
-    const int row0 = (blockIdx.x * G + g) * R;
-    const int64_t K = (int64_t)KB * QK;
-
-    int bidx[NB];
-    bool bval[NB];
-    const int slice_len = min(SB, KB - s * SB);
+__device__ __forceinline__ void prep_quarter(const float (&v)[8], int u, bool store,
+                                             uint32_t* __restrict__ dst) {
+    float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < NB; ++i) {
-        const int lb = i * 64 + lane;
-        bval[i] = lb < slice_len;
-        bidx[i] = bval[i] ? s * SB + lb : 0;
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    amax = fmaxf(amax, dpp_f32<0xB1>(amax));
+    amax = fmaxf(amax, dpp_f32<0x4E>(amax));
+    // s = 2^e with amax / 127 < s: frexp gives amax / 127 = f * 2^e, f in [0.5, 1)
+    int e = 0;
+    (void)frexpf(amax * (1.0f / 127.0f), &e);
+    const float inv = amax > 0.0f ? ldexpf(1.0f, -e) : 0.0f;
+    uint32_t b0[8], b1[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float t = v[j] * inv;                     // exact, |t| < 127
+        const float a = t + kRound;                     // low byte: rint(t) as int8
+        const float r = t - (a - kRound);               // exact, |r| <= 1/2
+        b0[j] = __float_as_uint(a);
+        b1[j] = __float_as_uint(fmaf(r, 254.0f, kRound));  // low byte: rint(254 r)
     }
+    const uint32_t p00 = pack_low_bytes(b0[0], b0[1], b0[2], b0[3]);
+    const uint32_t p01 = pack_low_bytes(b0[4], b0[5], b0[6], b0[7]);
+    const uint32_t p10 = pack_low_bytes(b1[0], b1[1], b1[2], b1[3]);
+    const uint32_t p11 = pack_low_bytes(b1[4], b1[5], b1[6], b1[7]);
+    int s0 = sdot4((int)p00, 0x01010101, sdot4((int)p01, 0x01010101, 0));
+    int s1 = sdot4((int)p10, 0x01010101, sdot4((int)p11, 0x01010101, 0));
+    s0 += dpp_i32<0xB1>(s0);
+    s0 += dpp_i32<0x4E>(s0);
+    s1 += dpp_i32<0xB1>(s1);
+    s1 += dpp_i32<0x4E>(s1);
+    if (!store) return;
+    dst[2 * u] = p00;
+    dst[2 * u + 1] = p01;
+    dst[8 + 2 * u] = p10;
+    dst[8 + 2 * u + 1] = p11;
+    if (u == 0) {
+        dst[16] = (uint32_t)(QT == UNILLM_QTYPE_Q4_0 ? -8 * s0 : 0);
+        dst[17] = (uint32_t)(QT == UNILLM_QTYPE_Q4_0 ? -8 * s1 : 0);
+        dst[18] = __float_as_uint(amax > 0.0f ? ldexpf(1.0f, e) : 0.0f);
+    }
+}
 
-    // x slice in registers: xa[m][i][0..31], seed c[m][i]
-    float xa[M][NB][QK];
-    float c[M][NB];
-#pragma unroll
-    for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            float sum = 0.0f;
-            if (bval[i]) {
-                const float4* xp = reinterpret_cast<const float4*>(x + m * K + (int64_t)bidx[i] * QK);
-#pragma unroll
-                for (int v = 0; v < 8; ++v) {
-                    const float4 f = xp[v];
-                    xa[m][i][4 * v + 0] = f.x;
-                    xa[m][i][4 * v + 1] = f.y;
-                    xa[m][i][4 * v + 2] = f.z;
-                    xa[m][i][4 * v + 3] = f.w;
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < QK; ++j) xa[m][i][j] = 0.0f;
-            }
-#pragma unroll
-            for (int j = 0; j < QK; ++j) sum += xa[m][i][j];
-            if constexpr (QT == UNILLM_QTYPE_Q4_0) {
-                c[m][i] = -8.0f * sum;
-#pragma unroll
-                for (int j = 16; j < QK; ++j) xa[m][i][j] *= 0.0625f;  // exact
-            } else {
-                c[m][i] = -128.0f * sum;
-            }
-        }
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-    // issue every load of the R rows first
-    uint4 q[R][NB][V];
-    float dd[R][NB];
+struct XBlock {
+    u32x4 d0[2], d1[2];  // 8 dwords each
+    int c0, c1;
+    float s;
+};
+
+__device__ __forceinline__ void load_xblock(const uint32_t* __restrict__ src, XBlock& o) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(src);
+    o.d0[0] = p[0];
+    o.d0[1] = p[1];
+    o.d1[0] = p[2];
+    o.d1[1] = p[3];
+    const u32x4 e = p[4];
+    o.c0 = (int)e.x;
+    o.c1 = (int)e.y;
+    o.s = __uint_as_float(e.z);
+}
+
+// ---- weights --------------------------------------------------------------------------------
+template <int QT>
+struct Payload {
+    static constexpr int V = QT == UNILLM_QTYPE_Q4_0 ? 1 : 2;  // 128-bit loads per block
+};
+
+template <int QT, int NB, int R>
+struct Chunk {
+    u32x4 q[R][NB][Payload<QT>::V];
+    uint16_t d[R][NB];
+};
+
+// Branch-free: indices are clamped into the matrix and validity is applied
+// later through the scale (d = 0), so no divergent branch sits around a load.
+// (A load under a divergent branch whose other side writes the same register
+// makes the compiler wait for the load at the join, serialising the loads.)
+template <int QT, int NB, int R>
+__device__ __forceinline__ void load_chunk(Chunk<QT, NB, R>& c, const uint8_t* __restrict__ base,
+                                           int64_t rb, int row0, int last, int KB,
+                                           const int* bidx) {
+    constexpr int V = Payload<QT>::V;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int row = row0 + r;
+        const int row = min(row0 + r, last);  // rows past the wave's range: its last row again
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
-            if (row < N && bval[i]) {
-                const int64_t blk = (int64_t)row * KB + bidx[i];
-                const uint4* p = reinterpret_cast<const uint4*>(qs + blk * QB);
+            // streamed once: non-temporal, so it does not evict x from the caches
+            const u32x4* p =
+                reinterpret_cast<const u32x4*>(blk_payload<16 * V>(base, rb, row, bidx[i]));
 #pragma unroll
-                for (int v = 0; v < V; ++v) q[r][i][v] = p[v];
-                dd[r][i] = __half2float(__ushort_as_half(dsc[blk]));
-            } else {
-#pragma unroll
-                for (int v = 0; v < V; ++v) q[r][i][v] = make_uint4(0, 0, 0, 0);
-                dd[r][i] = 0.0f;
-            }
+            for (int v = 0; v < V; ++v) c.q[r][i][v] = __builtin_nontemporal_load(p + v);
+            c.d[r][i] = *blk_scale<16 * V>(base, rb, KB, row, bidx[i]);
         }
     }
+}
 
+template <int QT, int M, int NB, int R>
+__device__ __forceinline__ void compute_chunk(const Chunk<QT, NB, R>& c, const XBlock (&xbs)[M][NB],
+                                              const bool* bval, float* __restrict__ y, int row0,
+                                              int row_end, int N, int lane, int m_real) {
     float part[M][R];
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
         for (int r = 0; r < R; ++r) part[m][r] = 0.0f;
-
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+    for (int i = 0; i < NB; ++i)
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            float acc[M];
+        for (int m = 0; m < M; ++m) {
+            const XBlock& xb = xbs[m][i];
 #pragma unroll
-            for (int m = 0; m < M; ++m) acc[m] = c[m][i];
-            if constexpr (QT == UNILLM_QTYPE_Q4_0) {
-                const uint32_t w4[4] = {q[r][i][0].x, q[r][i][0].y, q[r][i][0].z, q[r][i][0].w};
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const uint32_t lo = w4[t] & 0x0F0F0F0Fu;
-                    const uint32_t hi = w4[t] & 0xF0F0F0F0u;
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        const float fl = (float)((lo >> (8 * b)) & 0xFFu);
-                        const float fh = (float)((hi >> (8 * b)) & 0xFFu);
-#pragma unroll
-                        for (int m = 0; m < M; ++m) {
-                            acc[m] = fmaf(fl, xa[m][i][4 * t + b], acc[m]);
-                            acc[m] = fmaf(fh, xa[m][i][16 + 4 * t + b], acc[m]);
-                        }
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int v = 0; v < 2; ++v) {
-                    const uint32_t w4[4] = {q[r][i][v].x, q[r][i][v].y, q[r][i][v].z,
-                                            q[r][i][v].w};
+            for (int r = 0; r < R; ++r) {
+                int a0 = xb.c0, a1 = xb.c1;
+                if constexpr (QT == UNILLM_QTYPE_Q4_0) {
+                    const u32x4 w4 = c.q[r][i][0];
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
-                        const uint32_t u = w4[t] ^ 0x80808080u;  // q + 128 per byte
+                        const int lo = (int)(w4[t] & 0x0F0F0F0Fu);
+                        const int hi = (int)((w4[t] >> 4) & 0x0F0F0F0Fu);
+                        a0 = sdot4(lo, (int)xb.d0[0][t], a0);
+                        a0 = sdot4(hi, (int)xb.d0[1][t], a0);
+                        a1 = sdot4(lo, (int)xb.d1[0][t], a1);
+                        a1 = sdot4(hi, (int)xb.d1[1][t], a1);
+                    }
+                } else {
 #pragma unroll
-                        for (int b = 0; b < 4; ++b) {
-                            const float f = (float)((u >> (8 * b)) & 0xFFu);
+                    for (int v = 0; v < 2; ++v) {
+                        const u32x4 w4 = c.q[r][i][v];
 #pragma unroll
-                            for (int m = 0; m < M; ++m)
-                                acc[m] = fmaf(f, xa[m][i][16 * v + 4 * t + b], acc[m]);
+                        for (int t = 0; t < 4; ++t) {
+                            a0 = sdot4((int)w4[t], (int)xb.d0[v][t], a0);
+                            a1 = sdot4((int)w4[t], (int)xb.d1[v][t], a1);
                         }
                     }
                 }
+                // lanes past the row end (clamped duplicates) contribute nothing
+                const float dw = bval[i] ? __half2float(__ushort_as_half(c.d[r][i])) : 0.0f;
+                const float blk = fmaf((float)a1, 1.0f / 254.0f, (float)a0);
+                part[m][r] = fmaf(dw * xb.s, blk, part[m][r]);
             }
-#pragma unroll
-            for (int m = 0; m < M; ++m) part[m][r] = fmaf(dd[r][i], acc[m], part[m][r]);
         }
-
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
         for (int r = 0; r < R; ++r) part[m][r] = wave_sum(part[m][r]);
-
-    if (S == 1) {
-        if (lane == 0) {
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (row0 + r < N)
-#pragma unroll
-                    for (int m = 0; m < M; ++m) y[(int64_t)m * N + row0 + r] = part[m][r];
-        }
-        return;
-    }
-    // S slices of one row group combine through LDS (uniform control flow:
-    // every wave of the workgroup reaches the barrier exactly once).
     if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
+            if (row0 + r < row_end)
 #pragma unroll
-            for (int m = 0; m < M; ++m) red[(wv * R + r) * M + m] = part[m][r];
-    }
-    __syncthreads();
-    if (s == 0 && lane < R * M) {
-        const int r = lane / M;
-        const int m = lane % M;
-        float tot = 0.0f;
-        for (int t = 0; t < S; ++t) tot += red[((g * S + t) * R + r) * M + m];
-        if (row0 + r < N) y[(int64_t)m * N + row0 + r] = tot;
+                for (int m = 0; m < M; ++m)
+                    if (m < m_real) y[(int64_t)m * N + row0 + r] = part[m][r];
     }
 }
 
-constexpr int kRows = 4;  // rows in flight per wave
-
+// Workgroup size: 1024 threads (one workgroup per CU, 128 VGPRs per lane)
+// when a chunk and one x block fit that budget, else 512 (two per CU, 256).
 template <int QT, int M, int NB>
-hipError_t launch_t(const QWeight& w, const float* x, float* y, hipStream_t st) {
-    const int KB = (int)w.kb;
-    const int S = (KB + 64 * NB - 1) / (64 * NB);
-    const int SB = (KB + S - 1) / S;
-    const int G = S >= 4 ? 1 : 4 / S;
-    const int64_t rows_per_wg = (int64_t)G * kRows;
-    const unsigned grid = (unsigned)((w.n + rows_per_wg - 1) / rows_per_wg);
-    gemv_kernel<QT, M, NB, kRows><<<grid, 64 * S * G, 0, st>>>(w.qs, w.d, x, y, (int)w.n, KB, S,
-                                                               SB, G);
+constexpr int gemv_threads() {
+    return M * NB * Payload<QT>::V <= 2 ? 1024 : 512;
+}
+
+// m_real <= M rows of x are used; rows m >= m_real repeat row m_real - 1 and
+// are not written.  Dynamic LDS: M * KB * kXWords dwords of x digits.
+// M * KB * 4 <= 2048, so a thread builds at most 2048 / THREADS quarter-blocks.
+template <int QT, int M, int NB, int R, int THREADS>
+__global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict__ base,
+                                                       int64_t rb,
+                                                       const float* __restrict__ x,
+                                                       float* __restrict__ y, int N, int KB,
+                                                       int m_real) {
+    constexpr int WAVES = THREADS / 64;
+    constexpr int PASSES = 2048 / THREADS;
+    extern __shared__ uint32_t xlds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * WAVES + (threadIdx.x >> 6));
+    const int waves = gridDim.x * WAVES;
+    const int64_t K = (int64_t)KB * QK;
+    // balanced contiguous row range per wave (sizes differ by at most one row);
+    // wave-uniform, so every branch on it is a scalar branch
+    const int per = N / waves, extra = N % waves;
+    const int row_begin = wave * per + min(wave, extra);
+    const int row_end = row_begin + per + (wave < extra ? 1 : 0);
+
+    int bidx[NB];
+    bool bval[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const int b = i * 64 + lane;
+        bval[i] = b < KB;
+        bidx[i] = min(b, KB - 1);
+    }
+
+    // 1. x for the digits first (its loads are the oldest, so waiting for them
+    //    does not wait for the weights), then the first two weight chunks
+    const int nq = M * KB * 4;
+    float v[PASSES][8];
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        const int q = threadIdx.x + p * THREADS;
+        const int blk = min(q, nq - 1) >> 2;
+        const int m = blk / KB;
+        const float4* src = reinterpret_cast<const float4*>(
+            x + (int64_t)min(m, m_real - 1) * K + (int64_t)(blk - m * KB) * QK) + 2 * (q & 3);
+        float4 f0 = make_float4(0.f, 0.f, 0.f, 0.f), f1 = f0;
+        if (q < nq) {  // only the quarters that exist are fetched
+            f0 = src[0];
+            f1 = src[1];
+        }
+        v[p][0] = f0.x; v[p][1] = f0.y; v[p][2] = f0.z; v[p][3] = f0.w;
+        v[p][4] = f1.x; v[p][5] = f1.y; v[p][6] = f1.z; v[p][7] = f1.w;
+    }
+    // Unconditional (indices clamped into the matrix): a load under a branch
+    // would make the waits that follow it conservative.
+    // (clamped to the wave's own last row, so padding loads repeat an address
+    // the wave reads anyway; a wave without rows reads row N - 1)
+    const int last = row_end > row_begin ? row_end - 1 : N - 1;
+    Chunk<QT, NB, R> a, b;
+    load_chunk<QT, NB, R>(a, base, rb, row_begin, last, KB, bidx);
+    load_chunk<QT, NB, R>(b, base, rb, row_begin + R, last, KB, bidx);
+
+    // 2. x digits for all M * KB blocks, four threads per block (threads past
+    //    nq compute on a clamped copy and store nothing; nq is a multiple of 4,
+    //    so a DPP quad is either all real or all clamped)
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        const int q = threadIdx.x + p * THREADS;
+        prep_quarter<QT>(v[p], q & 3, q < nq, xlds + (size_t)(min(q, nq - 1) >> 2) * kXWords);
+    }
+    __syncthreads();
+
+    // 3. this lane's x digits, read once from LDS into registers for all rows
+    XBlock xb[M][NB];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int i = 0; i < NB; ++i) load_xblock(xlds + ((size_t)m * KB + bidx[i]) * kXWords, xb[m][i]);
+
+    // 4. the first two chunks, then (for ranges longer than 2R rows) two
+    //    chunks per step
+    compute_chunk<QT, M, NB, R>(a, xb, bval, y, row_begin, row_end, N, lane, m_real);
+    compute_chunk<QT, M, NB, R>(b, xb, bval, y, row_begin + R, row_end, N, lane, m_real);
+    for (int c = row_begin + 2 * R; c < row_end; c += 2 * R) {
+        load_chunk<QT, NB, R>(a, base, rb, c, last, KB, bidx);
+        load_chunk<QT, NB, R>(b, base, rb, c + R, last, KB, bidx);
+        compute_chunk<QT, M, NB, R>(a, xb, bval, y, c, row_end, N, lane, m_real);
+        compute_chunk<QT, M, NB, R>(b, xb, bval, y, c + R, row_end, N, lane, m_real);
+    }
+}
+
+template <int QT, int M, int NB, int R>
+hipError_t launch_r(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st,
+                    int waves) {
+    constexpr int THREADS = gemv_threads<QT, M, NB>();
+    constexpr int WAVES = THREADS / 64;
+    const size_t lds = (size_t)M * w.kb * kXWords * sizeof(uint32_t);
+    const int grid = (waves + WAVES - 1) / WAVES;
+    gemv_kernel<QT, M, NB, R, THREADS><<<grid, THREADS, lds, st>>>(w.base, w.row_bytes, x, y,
+                                                                  (int)w.n, (int)w.kb, (int)m);
     return hipGetLastError();
+}
+
+// Launch shape.  Every workgroup is resident at once (the occupancy the
+// registers and LDS allow), each wave gets at least two rows, and the chunk
+// size R (rows) is the smallest that lets the two chunks a wave requests up
+// front cover its rows -- so no wave loads rows it does not own -- capped by
+// the registers a chunk may take (at most 4 payload loads per lane).
+template <int QT, int M, int NB>
+hipError_t launch_nb(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st) {
+    constexpr int V = Payload<QT>::V;
+    constexpr int RMAX = NB * V >= 4 ? 1 : 4 / (NB * V);
+    constexpr int THREADS = gemv_threads<QT, M, NB>();
+    constexpr int WAVES = THREADS / 64;
+    int per_cu = 0;
+    const size_t lds = (size_t)M * w.kb * kXWords * sizeof(uint32_t);
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &per_cu, gemv_kernel<QT, M, NB, RMAX, THREADS>, THREADS, lds);
+    if (e != hipSuccess) return e;
+    const int64_t resident = (int64_t)device_info().cu_count * std::max(per_cu, 1) * WAVES;
+    const int64_t waves = std::max<int64_t>(1, std::min(resident, w.n / 2));
+    const int64_t rows = (w.n + waves - 1) / waves;  // per wave, at most
+    if (RMAX >= 4 && rows > 4) return launch_r<QT, M, NB, RMAX>(w, x, m, y, st, (int)waves);
+    if (RMAX >= 2 && rows > 2) return launch_r<QT, M, NB, (RMAX >= 2 ? 2 : 1)>(w, x, m, y, st, (int)waves);
+    return launch_r<QT, M, NB, 1>(w, x, m, y, st, (int)waves);
+}
+
+template <int QT, int M>
+hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st) {
+    switch ((int)((w.kb + 63) / 64)) {
+        case 1: return launch_nb<QT, M, 1>(w, x, m, y, st);
+        case 2: return launch_nb<QT, M, 2>(w, x, m, y, st);
+        case 3: if constexpr (M <= 2) return launch_nb<QT, M, 3>(w, x, m, y, st); break;
+        case 4: if constexpr (M <= 2) return launch_nb<QT, M, 4>(w, x, m, y, st); break;
+        case 5: if constexpr (M == 1 && QT == UNILLM_QTYPE_Q4_0) return launch_nb<QT, M, 5>(w, x, m, y, st); break;
+        case 6: if constexpr (M == 1 && QT == UNILLM_QTYPE_Q4_0) return launch_nb<QT, M, 6>(w, x, m, y, st); break;
+        case 7: if constexpr (M == 1 && QT == UNILLM_QTYPE_Q4_0) return launch_nb<QT, M, 7>(w, x, m, y, st); break;
+        default: break;
+    }
+    return hipErrorInvalidValue;
 }
 
 }  // namespace
 
-// Largest K (in blocks) the GEMV path takes: 8 waves x 64 lanes x NB blocks.
-int64_t gemv_max_kb(int64_t m) { return m == 1 ? 8 * 64 * 2 : 8 * 64; }
+// Largest K (in blocks) the GEMV path takes at m rows, set by the registers
+// two chunks of NB blocks per lane need (NB = ceil(KB / 64)): Q4_0 up to
+// NB = 7 at one row (K = 14336), 4 at two, 2 at four; Q8_0 payloads are twice
+// as wide, so it stops at NB = 4.  M * KB <= 512 also bounds the LDS (40 KiB).
+int64_t gemv_max_kb(int64_t m, int qtype) {
+    if (m <= 1) return qtype == UNILLM_QTYPE_Q8_0 ? 256 : 448;
+    if (m <= 2) return 256;
+    return 128;
+}
 
 hipError_t launch_gemv(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t s) {
-    if (w.qtype == UNILLM_QTYPE_Q4_0)
-        return m == 1 ? launch_t<UNILLM_QTYPE_Q4_0, 1, 2>(w, x, y, s)
-                      : launch_t<UNILLM_QTYPE_Q4_0, 2, 1>(w, x, y, s);
-    return m == 1 ? launch_t<UNILLM_QTYPE_Q8_0, 1, 2>(w, x, y, s)
-                  : launch_t<UNILLM_QTYPE_Q8_0, 2, 1>(w, x, y, s);
+    if (w.qtype == UNILLM_QTYPE_Q4_0) {
+        if (m == 1) return launch_m<UNILLM_QTYPE_Q4_0, 1>(w, x, m, y, s);
+        if (m == 2) return launch_m<UNILLM_QTYPE_Q4_0, 2>(w, x, m, y, s);
+        return launch_m<UNILLM_QTYPE_Q4_0, 4>(w, x, m, y, s);
+    }
+    if (m == 1) return launch_m<UNILLM_QTYPE_Q8_0, 1>(w, x, m, y, s);
+    if (m == 2) return launch_m<UNILLM_QTYPE_Q8_0, 2>(w, x, m, y, s);
+    return launch_m<UNILLM_QTYPE_Q8_0, 4>(w, x, m, y, s);
 }
 
 }  // namespace unillm

@@ -1,12 +1,14 @@
 // internal.hpp -- shared definitions of the gfx950 quantized-matmul library.
 //
-// Device layout of a weight (written once by the repack kernel at upload):
-//   qs plane : [n][kb][QB] bytes, QB = 16 (Q4_0 nibbles) or 32 (Q8_0 int8),
-//              the block payloads of a row back to back, so a 128-bit load is
-//              exactly one Q4_0 block payload (or half a Q8_0 one);
-//   d plane  : [n][kb] f16 scales, at a 256-byte aligned offset after qs.
-// The byte count is the GGUF one (18 or 34 B per 32 weights); only the order
-// differs, and dequant of this layout is bit-exact with the GGUF bytes.
+// Device layout of a weight (written once by the repack kernel at upload).
+// Row n occupies `row_bytes` = align16(kb * (QB + 2)) bytes at n * row_bytes:
+//   [kb x QB payload bytes][kb x f16 scales][pad to 16 B]
+// QB = 16 (Q4_0 nibbles) or 32 (Q8_0 int8).  The payloads of a row are back
+// to back, so a 128-bit load is exactly one Q4_0 block payload (or half a
+// Q8_0 one), and the row's scales sit in the same DRAM pages right after
+// them (measured: cheaper to stream than a separate scale plane).  The byte
+// count is GGUF's (18 or 34 B per 32 weights) plus at most 15 B of row
+// padding; dequant of this layout is bit-exact with the GGUF bytes.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -21,9 +23,8 @@ struct unillm_qweight {
     int qtype;
     int device;
     int64_t n, k, kb;      // kb = k / 32
-    uint8_t* qs;           // [n][kb][qbytes]
-    uint16_t* d;           // [n][kb]
-    void* base;            // single allocation holding both planes
+    int64_t row_bytes;     // bytes per row: payloads, scales, padding
+    uint8_t* base;         // n * row_bytes, then a 256-byte scratch slot
     size_t bytes;
     int f16_exp;           // E >= 0 with 8 * max|d| * 2^-E <= 65504 (f16 range)
 };
@@ -33,9 +34,24 @@ namespace unillm {
 constexpr int QK = 32;  // weights per block
 using QWeight = ::unillm_qweight;
 
-int64_t gemv_max_kb(int64_t m);
+int64_t gemv_max_kb(int64_t m, int qtype);
 
 inline int qbytes(int qtype) { return qtype == UNILLM_QTYPE_Q4_0 ? 16 : 32; }
+inline int64_t row_bytes_for(int qtype, int64_t kb) {
+    return (kb * (qbytes(qtype) + 2) + 15) / 16 * 16;
+}
+
+// Addresses inside a row (QB = payload bytes per block).
+template <int QB>
+__host__ __device__ __forceinline__ const uint8_t* blk_payload(const uint8_t* base, int64_t rb,
+                                                                int64_t row, int64_t b) {
+    return base + row * rb + b * QB;
+}
+template <int QB>
+__host__ __device__ __forceinline__ const uint16_t* blk_scale(const uint8_t* base, int64_t rb,
+                                                               int64_t kb, int64_t row, int64_t b) {
+    return reinterpret_cast<const uint16_t*>(base + row * rb + kb * QB) + b;
+}
 inline int gguf_block_bytes(int qtype) { return qtype == UNILLM_QTYPE_Q4_0 ? 18 : 34; }
 
 // Per-device properties cached at init.
@@ -59,7 +75,7 @@ hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float
 hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, float* y,
                                hipStream_t s);
 
-constexpr int64_t kGemvMaxM = 2;
+constexpr int64_t kGemvMaxM = 4;
 constexpr int64_t kDecodeMaxM = 64;
 
 }  // namespace unillm

@@ -48,8 +48,7 @@ constexpr int BK = 64;        // k per tile (two blocks)
 constexpr int LDK = BK + 8;   // padded LDS row (elements): breaks power-of-two strides
 
 template <typename T, int QT, int BM, int BN, int WM, int WN>
-__global__ __launch_bounds__(256) void mfma_kernel(const uint8_t* __restrict__ qs,
-                                                   const uint16_t* __restrict__ dsc,
+__global__ __launch_bounds__(256) void mfma_kernel(const uint8_t* __restrict__ base, int64_t rb,
                                                    const float* __restrict__ x,
                                                    float* __restrict__ y, int M, int N,
                                                    int KB, float wscale, float oscale) {
@@ -105,9 +104,10 @@ __global__ __launch_bounds__(256) void mfma_kernel(const uint8_t* __restrict__ q
                 const int kblk = kt * 2 + b;
                 T lo[8], hi[8];
                 if (n0 + col < N && kblk < KB) {
-                    const int64_t blk = (int64_t)(n0 + col) * KB + kblk;
-                    const uint2 p = *reinterpret_cast<const uint2*>(qs + blk * 16 + 8 * h);
-                    const float d = __half2float(__ushort_as_half(dsc[blk]));
+                    const uint2 p = *reinterpret_cast<const uint2*>(
+                        blk_payload<16>(base, rb, n0 + col, kblk) + 8 * h);
+                    const float d =
+                        __half2float(__ushort_as_half(*blk_scale<16>(base, rb, KB, n0 + col, kblk)));
                     const uint32_t w2[2] = {p.x, p.y};
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
@@ -136,9 +136,10 @@ __global__ __launch_bounds__(256) void mfma_kernel(const uint8_t* __restrict__ q
                 const int kblk = kt * 2 + b;
                 T v8[8];
                 if (n0 + col < N && kblk < KB) {
-                    const int64_t blk = (int64_t)(n0 + col) * KB + kblk;
-                    const uint2 p = *reinterpret_cast<const uint2*>(qs + blk * 32 + 8 * e);
-                    const float d = __half2float(__ushort_as_half(dsc[blk]));
+                    const uint2 p = *reinterpret_cast<const uint2*>(
+                        blk_payload<32>(base, rb, n0 + col, kblk) + 8 * e);
+                    const float d =
+                        __half2float(__ushort_as_half(*blk_scale<32>(base, rb, KB, n0 + col, kblk)));
                     const uint32_t w2[2] = {p.x, p.y};
 #pragma unroll
                     for (int j = 0; j < 8; ++j)
@@ -200,10 +201,10 @@ hipError_t launch_cfg(const QWeight& w, const float* x, int64_t m, float* y, hip
     const float wscale = ldexpf(1.0f, -E), oscale = ldexpf(1.0f, E);
     if (w.qtype == UNILLM_QTYPE_Q4_0)
         mfma_kernel<T, UNILLM_QTYPE_Q4_0, BM, BN, WM, WN><<<grid, 256, 0, s>>>(
-            w.qs, w.d, x, y, (int)m, (int)w.n, (int)w.kb, wscale, oscale);
+            w.base, w.row_bytes, x, y, (int)m, (int)w.n, (int)w.kb, wscale, oscale);
     else
         mfma_kernel<T, UNILLM_QTYPE_Q8_0, BM, BN, WM, WN><<<grid, 256, 0, s>>>(
-            w.qs, w.d, x, y, (int)m, (int)w.n, (int)w.kb, wscale, oscale);
+            w.base, w.row_bytes, x, y, (int)m, (int)w.n, (int)w.kb, wscale, oscale);
     return hipGetLastError();
 }
 

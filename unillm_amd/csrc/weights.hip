@@ -16,16 +16,16 @@ __device__ __forceinline__ uint16_t ld_u16(const uint8_t* p) {
 }
 
 // One thread per block: GGUF {f16 d; qs[QB]} (18 / 34 B, only 2-byte aligned)
-// -> qs plane (16-byte aligned rows of payloads) + d plane.
+// -> the row layout [kb payloads][kb scales] (payloads 16-byte aligned).
 template <int QB>
 __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__ src,
-                                                     uint8_t* __restrict__ qs,
-                                                     uint16_t* __restrict__ d,
-                                                     int64_t nblocks) {
+                                                     uint8_t* __restrict__ base, int64_t rb,
+                                                     int64_t kb, int64_t nblocks) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nblocks) return;
+    const int64_t row = i / kb, blk = i - row * kb;
     const uint8_t* b = src + i * (QB + 2);
-    d[i] = ld_u16(b);
+    *const_cast<uint16_t*>(blk_scale<QB>(base, rb, kb, row, blk)) = ld_u16(b);
     uint32_t words[QB / 4];
 #pragma unroll
     for (int w = 0; w < QB / 4; ++w) {
@@ -33,7 +33,7 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
         words[w] = (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) |
                    ((uint32_t)p[3] << 24);
     }
-    uint4* dst = reinterpret_cast<uint4*>(qs + i * QB);
+    uint4* dst = reinterpret_cast<uint4*>(const_cast<uint8_t*>(blk_payload<QB>(base, rb, row, blk)));
 #pragma unroll
     for (int v = 0; v < QB / 16; ++v)
         dst[v] = make_uint4(words[4 * v], words[4 * v + 1], words[4 * v + 2], words[4 * v + 3]);
@@ -43,16 +43,19 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
 // w[j + 16] = (hi(qs[j]) - 8) * d; Q8_0 w[j] = qs[j] * d.  One thread per
 // block.  Every product is exact in f32, so any evaluation order is bit-exact.
 template <int QT>
-__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ qs,
-                                                      const uint16_t* __restrict__ dsc,
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ base,
+                                                      int64_t rb, int64_t kb,
                                                       float* __restrict__ out,
                                                       int64_t nblocks) {
+    constexpr int QB = QT == UNILLM_QTYPE_Q4_0 ? 16 : 32;
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nblocks) return;
-    const float d = __half2float(__ushort_as_half(dsc[i]));
+    const int64_t row = i / kb, blk = i - row * kb;
+    const float d = __half2float(__ushort_as_half(*blk_scale<QB>(base, rb, kb, row, blk)));
+    const uint8_t* qs = blk_payload<QB>(base, rb, row, blk);
     float4* o = reinterpret_cast<float4*>(out + i * QK);
     if constexpr (QT == UNILLM_QTYPE_Q4_0) {
-        const uint4 q = *reinterpret_cast<const uint4*>(qs + i * 16);
+        const uint4 q = *reinterpret_cast<const uint4*>(qs);
         const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -67,7 +70,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
             o[4 + t] = make_float4(hi[0], hi[1], hi[2], hi[3]);
         }
     } else {
-        const uint4* q = reinterpret_cast<const uint4*>(qs + i * 32);
+        const uint4* q = reinterpret_cast<const uint4*>(qs);
 #pragma unroll
         for (int v = 0; v < 2; ++v) {
             const uint4 qq = q[v];
@@ -143,14 +146,17 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
 
 // max |d| over the scale plane, as f16 magnitude bits (monotone in |d| for
 // finite values).  Used once per weight to pick the f16 exponent offset.
-__global__ __launch_bounds__(256) void scale_absmax_kernel(const uint16_t* __restrict__ d,
-                                                           int64_t count,
+template <int QB>
+__global__ __launch_bounds__(256) void scale_absmax_kernel(const uint8_t* __restrict__ base,
+                                                           int64_t rb, int64_t kb, int64_t count,
                                                            uint32_t* __restrict__ out) {
     __shared__ uint32_t part[256];
     uint32_t m = 0;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
-         i += (int64_t)gridDim.x * blockDim.x)
-        m = max(m, (uint32_t)(d[i] & 0x7FFFu));
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = i / kb;
+        m = max(m, (uint32_t)(*blk_scale<QB>(base, rb, kb, row, i - row * kb) & 0x7FFFu));
+    }
     part[threadIdx.x] = m;
     __syncthreads();
     for (int s = 128; s > 0; s >>= 1) {
@@ -169,25 +175,30 @@ inline unsigned grid_for(int64_t items, int block) {
 hipError_t launch_repack(const QWeight& w, const uint8_t* gguf, hipStream_t s) {
     const int64_t nb = w.n * w.kb;
     if (w.qtype == UNILLM_QTYPE_Q4_0)
-        repack_kernel<16><<<grid_for(nb, 256), 256, 0, s>>>(gguf, w.qs, w.d, nb);
+        repack_kernel<16><<<grid_for(nb, 256), 256, 0, s>>>(gguf, w.base, w.row_bytes, w.kb, nb);
     else
-        repack_kernel<32><<<grid_for(nb, 256), 256, 0, s>>>(gguf, w.qs, w.d, nb);
+        repack_kernel<32><<<grid_for(nb, 256), 256, 0, s>>>(gguf, w.base, w.row_bytes, w.kb, nb);
     return hipGetLastError();
 }
 
 hipError_t launch_scale_absmax(const QWeight& w, uint32_t* out, hipStream_t s) {
     const int64_t nb = w.n * w.kb;
     const unsigned grid = (unsigned)std::min<int64_t>(1024, (nb + 255) / 256);
-    scale_absmax_kernel<<<grid, 256, 0, s>>>(w.d, nb, out);
+    if (w.qtype == UNILLM_QTYPE_Q4_0)
+        scale_absmax_kernel<16><<<grid, 256, 0, s>>>(w.base, w.row_bytes, w.kb, nb, out);
+    else
+        scale_absmax_kernel<32><<<grid, 256, 0, s>>>(w.base, w.row_bytes, w.kb, nb, out);
     return hipGetLastError();
 }
 
 hipError_t launch_dequant(const QWeight& w, float* out, hipStream_t s) {
     const int64_t nb = w.n * w.kb;
     if (w.qtype == UNILLM_QTYPE_Q4_0)
-        dequant_kernel<UNILLM_QTYPE_Q4_0><<<grid_for(nb, 256), 256, 0, s>>>(w.qs, w.d, out, nb);
+        dequant_kernel<UNILLM_QTYPE_Q4_0><<<grid_for(nb, 256), 256, 0, s>>>(w.base, w.row_bytes,
+                                                                            w.kb, out, nb);
     else
-        dequant_kernel<UNILLM_QTYPE_Q8_0><<<grid_for(nb, 256), 256, 0, s>>>(w.qs, w.d, out, nb);
+        dequant_kernel<UNILLM_QTYPE_Q8_0><<<grid_for(nb, 256), 256, 0, s>>>(w.base, w.row_bytes,
+                                                                            w.kb, out, nb);
     return hipGetLastError();
 }
 

@@ -1,6 +1,7 @@
 // capi.hip -- the extern "C" boundary (include/unillm_hip.h): argument checks,
 // error reporting, weight lifetime and kernel-path dispatch.
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <mutex>
@@ -135,6 +136,14 @@ int finish_weight(QWeight* w, hipStream_t s) {
 }  // namespace
 
 const DeviceInfo& device_info() { return g_info; }
+
+bool debug_launch() {
+    static const bool on = [] {
+        const char* e = getenv("UNILLM_DEBUG_LAUNCH");
+        return e && e[0] == '1';
+    }();
+    return on;
+}
 
 }  // namespace unillm
 

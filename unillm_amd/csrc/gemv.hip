@@ -20,11 +20,13 @@
 //
 // Mapping (MI355X, wave64).  One 1024-thread workgroup per CU (two of 512
 // where a lane needs more than 128 VGPRs):
-//   1. every wave requests its first chunk of weights at once (they do not
-//      depend on x);
-//   2. the workgroup turns x into digits in LDS, four threads per 32-block,
-//      so each CU does this once, hidden under the latency of step 1;
-//   3. each wave owns a contiguous, balanced range of rows and walks it in
+//   1. the workgroup turns x into digits in LDS, four threads per 32-block,
+//      so each CU does this once -- before any weight load, because
+//      instructions issue in order and weight loads that fill the memory
+//      pipeline would hold back everything behind them;
+//   2. every wave then requests its first two chunks of weights at once;
+//   3. wave w owns rows w, w + W, w + 2W, ... (so the rows requested at one
+//      moment form one contiguous stretch of the matrix) and walks them in
 //      chunks of R rows (lane l owns blocks l, l + 64, ... of every row),
 //      two chunks at a time; a wave-wide 128-bit load reads 1 KiB of
 //      contiguous Q4_0 payload.  Every load is branch-free (indices are
@@ -33,6 +35,7 @@
 //      cross-row shuffles.
 #include <hip/hip_fp16.h>
 
+#include <stdio.h>
 #include <stdlib.h>
 
 #include <algorithm>
@@ -164,14 +167,18 @@ struct Chunk {
 // later through the scale (d = 0), so no divergent branch sits around a load.
 // (A load under a divergent branch whose other side writes the same register
 // makes the compiler wait for the load at the join, serialising the loads.)
+// Rows of a wave: w, w + W, w + 2W, ... (W = waves), so the rows the whole
+// grid requests at one moment form one contiguous stretch of the matrix.
+// Chunk j0 holds the wave's rows j0 .. j0 + R - 1; rows past the wave's last
+// are clamped to that last row (an address the wave reads anyway).
 template <int QT, int NB, int R>
 __device__ __forceinline__ void load_chunk(Chunk<QT, NB, R>& c, const uint8_t* __restrict__ base,
-                                           int64_t rb, int row0, int last, int KB,
+                                           int64_t rb, int w, int W, int j0, int jlast, int KB,
                                            const int* bidx) {
     constexpr int V = Payload<QT>::V;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int row = min(row0 + r, last);  // rows past the wave's range: its last row again
+        const int row = w + min(j0 + r, jlast) * W;
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             // streamed once: non-temporal, so it does not evict x from the caches
@@ -186,8 +193,9 @@ __device__ __forceinline__ void load_chunk(Chunk<QT, NB, R>& c, const uint8_t* _
 
 template <int QT, int M, int NB, int R>
 __device__ __forceinline__ void compute_chunk(const Chunk<QT, NB, R>& c, const XBlock (&xbs)[M][NB],
-                                              const bool* bval, float* __restrict__ y, int row0,
-                                              int row_end, int N, int lane, int m_real) {
+                                              const bool* bval, float* __restrict__ y, int w,
+                                              int W, int j0, int jcount, int N, int lane,
+                                              int m_real) {
     float part[M][R];
 #pragma unroll
     for (int m = 0; m < M; ++m)
@@ -236,10 +244,10 @@ __device__ __forceinline__ void compute_chunk(const Chunk<QT, NB, R>& c, const X
     if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
-            if (row0 + r < row_end)
+            if (j0 + r < jcount)
 #pragma unroll
                 for (int m = 0; m < M; ++m)
-                    if (m < m_real) y[(int64_t)m * N + row0 + r] = part[m][r];
+                    if (m < m_real) y[(int64_t)m * N + w + (j0 + r) * W] = part[m][r];
     }
 }
 
@@ -266,11 +274,11 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * WAVES + (threadIdx.x >> 6));
     const int waves = gridDim.x * WAVES;
     const int64_t K = (int64_t)KB * QK;
-    // balanced contiguous row range per wave (sizes differ by at most one row);
-    // wave-uniform, so every branch on it is a scalar branch
-    const int per = N / waves, extra = N % waves;
-    const int row_begin = wave * per + min(wave, extra);
-    const int row_end = row_begin + per + (wave < extra ? 1 : 0);
+    // this wave's rows: wave, wave + waves, ... (counts differ by at most one);
+    // wave-uniform, so every branch on them is a scalar branch
+    const int jcount = wave < N ? (N - 1 - wave) / waves + 1 : 0;
+    const int jlast = max(jcount - 1, 0);
+    const int wrow = min(wave, N - 1);  // a wave without rows reads row N - 1
 
     int bidx[NB];
     bool bval[NB];
@@ -281,8 +289,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
         bidx[i] = min(b, KB - 1);
     }
 
-    // 1. x for the digits first (its loads are the oldest, so waiting for them
-    //    does not wait for the weights), then the first two weight chunks
+    // 1. x for the digits
     const int nq = M * KB * 4;
     float v[PASSES][8];
 #pragma unroll
@@ -302,16 +309,12 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     }
     // Unconditional (indices clamped into the matrix): a load under a branch
     // would make the waits that follow it conservative.
-    // (clamped to the wave's own last row, so padding loads repeat an address
-    // the wave reads anyway; a wave without rows reads row N - 1)
-    const int last = row_end > row_begin ? row_end - 1 : N - 1;
-    Chunk<QT, NB, R> a, b;
-    load_chunk<QT, NB, R>(a, base, rb, row_begin, last, KB, bidx);
-    load_chunk<QT, NB, R>(b, base, rb, row_begin + R, last, KB, bidx);
-
     // 2. x digits for all M * KB blocks, four threads per block (threads past
     //    nq compute on a clamped copy and store nothing; nq is a multiple of 4,
-    //    so a DPP quad is either all real or all clamped)
+    //    so a DPP quad is either all real or all clamped).  This comes before
+    //    the weight loads: instructions issue in order, and once the weight
+    //    loads fill the memory pipeline, anything behind them waits until they
+    //    are accepted -- the digits would then be late for every row.
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
         const int q = threadIdx.x + p * THREADS;
@@ -320,21 +323,30 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     __syncthreads();
 
     // 3. this lane's x digits, read once from LDS into registers for all rows
+    //    (also ahead of the weight loads, for the same in-order reason)
     XBlock xb[M][NB];
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
         for (int i = 0; i < NB; ++i) load_xblock(xlds + ((size_t)m * KB + bidx[i]) * kXWords, xb[m][i]);
+    __builtin_amdgcn_sched_barrier(0);  // keep the reads above the weight loads
 
-    // 4. the first two chunks, then (for ranges longer than 2R rows) two
+    // 4. the weights: the first two chunks at once (unconditional, indices
+    //    clamped: a load under a branch would make the waits that follow it
+    //    conservative)
+    Chunk<QT, NB, R> a, b;
+    load_chunk<QT, NB, R>(a, base, rb, wrow, waves, 0, jlast, KB, bidx);
+    load_chunk<QT, NB, R>(b, base, rb, wrow, waves, R, jlast, KB, bidx);
+
+    // 5. the first two chunks, then (for ranges longer than 2R rows) two
     //    chunks per step
-    compute_chunk<QT, M, NB, R>(a, xb, bval, y, row_begin, row_end, N, lane, m_real);
-    compute_chunk<QT, M, NB, R>(b, xb, bval, y, row_begin + R, row_end, N, lane, m_real);
-    for (int c = row_begin + 2 * R; c < row_end; c += 2 * R) {
-        load_chunk<QT, NB, R>(a, base, rb, c, last, KB, bidx);
-        load_chunk<QT, NB, R>(b, base, rb, c + R, last, KB, bidx);
-        compute_chunk<QT, M, NB, R>(a, xb, bval, y, c, row_end, N, lane, m_real);
-        compute_chunk<QT, M, NB, R>(b, xb, bval, y, c + R, row_end, N, lane, m_real);
+    compute_chunk<QT, M, NB, R>(a, xb, bval, y, wrow, waves, 0, jcount, N, lane, m_real);
+    compute_chunk<QT, M, NB, R>(b, xb, bval, y, wrow, waves, R, jcount, N, lane, m_real);
+    for (int j = 2 * R; j < jcount; j += 2 * R) {
+        load_chunk<QT, NB, R>(a, base, rb, wrow, waves, j, jlast, KB, bidx);
+        load_chunk<QT, NB, R>(b, base, rb, wrow, waves, j + R, jlast, KB, bidx);
+        compute_chunk<QT, M, NB, R>(a, xb, bval, y, wrow, waves, j, jcount, N, lane, m_real);
+        compute_chunk<QT, M, NB, R>(b, xb, bval, y, wrow, waves, j + R, jcount, N, lane, m_real);
     }
 }
 
@@ -369,6 +381,10 @@ hipError_t launch_nb(const QWeight& w, const float* x, int64_t m, float* y, hipS
     const int64_t resident = (int64_t)device_info().cu_count * std::max(per_cu, 1) * WAVES;
     const int64_t waves = std::max<int64_t>(1, std::min(resident, w.n / 2));
     const int64_t rows = (w.n + waves - 1) / waves;  // per wave, at most
+    if (debug_launch())
+        fprintf(stderr, "unillm gemv: n=%lld kb=%lld m=%lld threads=%d per_cu=%d waves=%lld rows=%lld\n",
+                (long long)w.n, (long long)w.kb, (long long)m, THREADS, per_cu, (long long)waves,
+                (long long)rows);
     if (RMAX >= 4 && rows > 4) return launch_r<QT, M, NB, RMAX>(w, x, m, y, st, (int)waves);
     if (RMAX >= 2 && rows > 2) return launch_r<QT, M, NB, (RMAX >= 2 ? 2 : 1)>(w, x, m, y, st, (int)waves);
     return launch_r<QT, M, NB, 1>(w, x, m, y, st, (int)waves);

@@ -60,6 +60,8 @@ struct DeviceInfo {
     int max_lds;
 };
 const DeviceInfo& device_info();
+// UNILLM_DEBUG_LAUNCH=1 prints each kernel's launch shape to stderr.
+bool debug_launch();
 
 // ---- launchers (each in the translation unit that holds its kernel) ----------
 // All return a hipError_t from the launch; shapes are validated by the caller.

@@ -5,23 +5,33 @@
 // one to four tokens.  Bound: HBM -- each weight byte is read once; the
 // arithmetic intensity is ~3.6 flop/B per token (Q4_0).
 //
-// Arithmetic.  Each 32-element block of x is written as two signed int8
-// digits over a per-block power-of-two scale s, max|x| / 127 < s <= 2 max|x| / 127:
-//     x[j] ~= s * (d0[j] + d1[j] / 254),  d0 = rint(x/s), d1 = rint((x/s - d0) * 254)
-// (|error| <= s / 508 <= max|x| / 32258 per element; x / s is exact, so
-// scaling x by a power of two scales y exactly).  The weight codes are exact
-// small integers, so each block's dot products are exact int32 sums computed
-// with v_dot4_i32_i8 (four products per instruction, ~1 VALU op per weight):
-//     Q4_0: sum_j (q_j - 8) x_j = s * ((D0 - 8 S0) + (D1 - 8 S1) / 254),
-//     D_i = sum_j q_j d_i[j], S_i = sum_j d_i[j]  (the -8 S_i seeds the sum);
-//     Q8_0: the same with signed codes and no offset.
-// Block results are scaled by d_w * s and summed in fp32.  Normwise error vs
-// the f64 oracle is ~3e-5 (bound 1e-3).
+// Arithmetic.  The weight codes are exact small integers, so each block's dot
+// product with x is computed as an exact int32 sum and scaled once.  x is
+// turned, per 32-element block, into integers T_j over a power-of-two scale:
+//   Q4_0: x_j ~= sx * T_j, T_j = rint(x_j / s * 2^12), max|x| / 7 < s <= 2 max|x| / 7,
+//         sx = s * 2^-12 (|T_j| <= 7 * 2^12; error <= s * 2^-13 <= max|x| / 28672).
+//         T_j is written as four balanced base-16 digits in [-8, 7], so with the
+//         weight nibbles stored as the signed values q - 8 one v_dot8_i32_i4
+//         takes eight weights against one digit of eight x values, with no
+//         unpacking: A = sum_j (q_j - 8) T_j = sum_k 16^k sum_j (q_j - 8) d_kj
+//         (16 dot8 per block, |A| < 2^24).
+//   Q8_0: x_j ~= sx * (254 d0_j + d1_j), d0 = rint(x / s), d1 = rint((x / s - d0) * 254),
+//         max|x| / 127 < s <= 2 max|x| / 127, sx = s / 254; v_dot4_i32_i8 against each
+//         int8 digit, A = 254 sum q d0 + sum q d1 (error <= s / 508 <= max|x| / 32258).
+// x / s is exact (a power-of-two scale), so scaling x by a power of two scales
+// y exactly.  Block results are scaled by d_w * sx and summed in fp32;
+// normwise error vs the f64 oracle is ~3e-5 (bound 1e-3).
+//
+// Why integers: a wave64 VALU instruction occupies a gfx950 SIMD for about
+// four cycles (fp32 FMA and the dot instructions alike, measured), so the
+// decode GEMV is VALU-heavy unless each instruction covers many weights.
+// dot8 covers 8 Q4_0 weights per digit; the inner loop is ~22 instructions per
+// 32-weight block (vs ~64 for an fp32 dequant-FMA).
 //
 // Mapping (MI355X, wave64).  One 1024-thread workgroup per CU (two of 512
 // where a lane needs more than 128 VGPRs):
-//   1. the workgroup turns x into digits in LDS, four threads per 32-block,
-//      so each CU does this once -- before any weight load, because
+//   1. the workgroup turns x into digit records in LDS, four threads per
+//      32-block, so each CU does this once -- before any weight load, because
 //      instructions issue in order and weight loads that fill the memory
 //      pipeline would hold back everything behind them;
 //   2. every wave then requests its first two chunks of weights at once;
@@ -31,8 +41,8 @@
 //      two chunks at a time; a wave-wide 128-bit load reads 1 KiB of
 //      contiguous Q4_0 payload.  Every load is branch-free (indices are
 //      clamped, validity is applied through the scale), so the in-order
-//      memory counter lets the x digits be built while the weights stream.  Row partials are reduced with DPP rotations and two
-//      cross-row shuffles.
+//      memory counter never makes a wait cover more loads than it needs.
+//      Row partials are reduced with DPP rotations and two cross-row shuffles.
 #include <hip/hip_fp16.h>
 
 #include <stdio.h>
@@ -45,8 +55,12 @@
 namespace unillm {
 namespace {
 
-constexpr int kXWords = 20;             // LDS dwords per x block (19 used; conflict-free)
+// LDS dwords per x block: 16 digit dwords + sx (17 used; 20 keeps the
+// 128-bit reads of the 64 lanes of a wave spread over the banks)
+constexpr int kXWords = 20;
 constexpr float kRound = 12582912.0f;   // 1.5 * 2^23: t + kRound rounds t to an integer
+// kRound + 0x8888: the low 16 bits of (t + kRound4) are rint(t) + 0x8888
+constexpr float kRound4 = 12582912.0f + 34952.0f;
 
 template <int CTRL>
 __device__ __forceinline__ int dpp_i32(int v) {
@@ -71,6 +85,9 @@ __device__ __forceinline__ float wave_sum(float v) {
 __device__ __forceinline__ int sdot4(int a, int b, int c) {
     return __builtin_amdgcn_sdot4(a, b, c, false);
 }
+__device__ __forceinline__ int sdot8(int a, int b, int c) {
+    return __builtin_amdgcn_sdot8(a, b, c, false);
+}
 
 // Low bytes of four registers -> one dword (v_perm_b32 selects bytes; 0x0C = zero).
 __device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a0, uint32_t a1, uint32_t a2,
@@ -78,27 +95,82 @@ __device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a0, uint32_t a1, uin
     return __builtin_amdgcn_perm(a1, a0, 0x0C0C0400u) | __builtin_amdgcn_perm(a3, a2, 0x04000C0Cu);
 }
 
-// ---- x digits -----------------------------------------------------------------------------
-// LDS record of one 32-element x block, in the byte order of the weight payload:
-// dwords 0-7 digit 0 of elements 4t..4t+3, 8-15 digit 1, 16 / 17 the seeds
-// c0 / c1 (-8 S_i for Q4_0, 0 for Q8_0), 18 the scale s.  (For Q4_0, payload
-// dword t meets digit dwords t (low nibbles) and 4 + t (high nibbles).)
-//
-// One thread builds one quarter (8 elements) of a block; the four threads of a
-// block are one DPP quad, so the block max and digit sums are quad reductions.
-// The math runs on every thread and only the stores are conditional, so the
-// compiler keeps the x loads where they are issued (ahead of the weights).
-template <int QT>
-__device__ __forceinline__ void prep_quarter(const float (&v)[8], int u, bool store,
-                                             uint32_t* __restrict__ dst) {
+// Bits of a where m is set, of b elsewhere (v_bfi_b32).
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
+    return (m & a) | (~m & b);
+}
+
+// Max of |v| over the 8 values of this thread and its DPP quad.
+__device__ __forceinline__ float quad_absmax(const float (&v)[8]) {
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
     amax = fmaxf(amax, dpp_f32<0xB1>(amax));
-    amax = fmaxf(amax, dpp_f32<0x4E>(amax));
-    // s = 2^e with amax / 127 < s: frexp gives amax / 127 = f * 2^e, f in [0.5, 1)
+    return fmaxf(amax, dpp_f32<0x4E>(amax));
+}
+
+// ---- x digit records -------------------------------------------------------------------------
+// One record per 32-element x block (kXWords dwords in LDS), built by the four
+// threads of a DPP quad (one per weight-payload dword t = 0..3), in the
+// operand order of the weight payload so that payload dword t meets digit
+// dword t:
+//   Q4_0: dwords 4L + t (L = 0..3) hold digit 3 - L of the eight elements of
+//         payload dword t, in its nibble order 4t, 4t+16, 4t+1, 4t+17, ...;
+//         dword 16 = sx.
+//   Q8_0: dwords 0-7 digit d0 of elements 4t..4t+3 (t = 0..7), 8-15 digit d1,
+//         dword 16 = sx.
+//
+// The math runs on every thread and only the stores are conditional, so the
+// compiler keeps the x loads where they are issued.
+
+// Q4_0: v[2i] = x[4t + i], v[2i + 1] = x[16 + 4t + i] (i = 0..3).
+__device__ __forceinline__ void prep_q4(const float (&v)[8], int t, bool store,
+                                        uint32_t* __restrict__ dst) {
+    const float amax = quad_absmax(v);
+    // s = 2^e with max|x| / 7 < s: frexp gives max|x| / 7 = f * 2^e, f in [0.5, 1);
+    // e >= -100 keeps 2^(12 - e) finite (blocks below 2^-100 round to zero)
+    int e = 0;
+    (void)frexpf(amax * (1.0f / 7.0f), &e);
+    e = max(e, -100);
+    const float inv = amax > 0.0f ? ldexpf(1.0f, 12 - e) : 0.0f;
+    // low 16 bits of a[j]: U_j = T_j + 0x8888, T_j = rint(x_j * 2^12 / s) (one rounding:
+    // the product is exact).  For balanced digits, U = sum_k (d_k + 8) 16^k, so
+    // nibble k of U is digit k XOR 8 (its 4-bit two's complement pattern, XOR 8).
+    uint32_t a[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a[j] = __float_as_uint(fmaf(v[j], inv, kRound4));
+    // nibble transpose: P[i] byte 0 = nibble 0 of a[2i] | nibble 0 of a[2i+1] << 4,
+    // byte 1 = the same for nibble 2; Q[i] the same for nibbles 1 and 3
+    uint32_t P[4], Q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        P[i] = bfi(0x0F0Fu, a[2 * i], a[2 * i + 1] << 4);
+        Q[i] = bfi(0x0F0Fu, a[2 * i] >> 4, a[2 * i + 1]);
+    }
+    const uint32_t P01 = __builtin_amdgcn_perm(P[1], P[0], 0x05010400u);
+    const uint32_t P23 = __builtin_amdgcn_perm(P[3], P[2], 0x05010400u);
+    const uint32_t Q01 = __builtin_amdgcn_perm(Q[1], Q[0], 0x05010400u);
+    const uint32_t Q23 = __builtin_amdgcn_perm(Q[3], Q[2], 0x05010400u);
+    const uint32_t d0 = __builtin_amdgcn_perm(P23, P01, 0x05040100u) ^ 0x88888888u;
+    const uint32_t d2 = __builtin_amdgcn_perm(P23, P01, 0x07060302u) ^ 0x88888888u;
+    const uint32_t d1 = __builtin_amdgcn_perm(Q23, Q01, 0x05040100u) ^ 0x88888888u;
+    const uint32_t d3 = __builtin_amdgcn_perm(Q23, Q01, 0x07060302u) ^ 0x88888888u;
+    if (!store) return;
+    dst[t] = d3;
+    dst[4 + t] = d2;
+    dst[8 + t] = d1;
+    dst[12 + t] = d0;
+    if (t == 0) dst[16] = __float_as_uint(amax > 0.0f ? ldexpf(1.0f, e - 12) : 0.0f);
+}
+
+// Q8_0: v[j] = x[8u + j], u = quarter 0..3.
+__device__ __forceinline__ void prep_q8(const float (&v)[8], int u, bool store,
+                                        uint32_t* __restrict__ dst) {
+    const float amax = quad_absmax(v);
+    // s = 2^e with max|x| / 127 < s
     int e = 0;
     (void)frexpf(amax * (1.0f / 127.0f), &e);
+    e = max(e, -100);
     const float inv = amax > 0.0f ? ldexpf(1.0f, -e) : 0.0f;
     uint32_t b0[8], b1[8];
 #pragma unroll
@@ -109,46 +181,39 @@ __device__ __forceinline__ void prep_quarter(const float (&v)[8], int u, bool st
         b0[j] = __float_as_uint(a);
         b1[j] = __float_as_uint(fmaf(r, 254.0f, kRound));  // low byte: rint(254 r)
     }
-    const uint32_t p00 = pack_low_bytes(b0[0], b0[1], b0[2], b0[3]);
-    const uint32_t p01 = pack_low_bytes(b0[4], b0[5], b0[6], b0[7]);
-    const uint32_t p10 = pack_low_bytes(b1[0], b1[1], b1[2], b1[3]);
-    const uint32_t p11 = pack_low_bytes(b1[4], b1[5], b1[6], b1[7]);
-    int s0 = sdot4((int)p00, 0x01010101, sdot4((int)p01, 0x01010101, 0));
-    int s1 = sdot4((int)p10, 0x01010101, sdot4((int)p11, 0x01010101, 0));
-    s0 += dpp_i32<0xB1>(s0);
-    s0 += dpp_i32<0x4E>(s0);
-    s1 += dpp_i32<0xB1>(s1);
-    s1 += dpp_i32<0x4E>(s1);
     if (!store) return;
-    dst[2 * u] = p00;
-    dst[2 * u + 1] = p01;
-    dst[8 + 2 * u] = p10;
-    dst[8 + 2 * u + 1] = p11;
-    if (u == 0) {
-        dst[16] = (uint32_t)(QT == UNILLM_QTYPE_Q4_0 ? -8 * s0 : 0);
-        dst[17] = (uint32_t)(QT == UNILLM_QTYPE_Q4_0 ? -8 * s1 : 0);
-        dst[18] = __float_as_uint(amax > 0.0f ? ldexpf(1.0f, e) : 0.0f);
+    dst[2 * u] = pack_low_bytes(b0[0], b0[1], b0[2], b0[3]);
+    dst[2 * u + 1] = pack_low_bytes(b0[4], b0[5], b0[6], b0[7]);
+    dst[8 + 2 * u] = pack_low_bytes(b1[0], b1[1], b1[2], b1[3]);
+    dst[8 + 2 * u + 1] = pack_low_bytes(b1[4], b1[5], b1[6], b1[7]);
+    if (u == 0) dst[16] = __float_as_uint(amax > 0.0f ? ldexpf(1.0f, e) * (1.0f / 254.0f) : 0.0f);
+}
+
+// The x elements a prep thread handles (q = 4 * block + quarter), as two float4 offsets.
+template <int QT>
+__device__ __forceinline__ void quarter_offsets(int quarter, int& o0, int& o1) {
+    if constexpr (QT == UNILLM_QTYPE_Q4_0) {
+        o0 = 4 * quarter;       // x[4t .. 4t+3]
+        o1 = 16 + 4 * quarter;  // x[16+4t .. 16+4t+3]
+    } else {
+        o0 = 8 * quarter;       // x[8u .. 8u+7]
+        o1 = 8 * quarter + 4;
     }
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct XBlock {
-    u32x4 d0[2], d1[2];  // 8 dwords each
-    int c0, c1;
-    float s;
+    u32x4 dg[4];  // 16 digit dwords, in record order
+    float sx;     // 0 for a lane's clamped (duplicate) block
 };
 
-__device__ __forceinline__ void load_xblock(const uint32_t* __restrict__ src, XBlock& o) {
+__device__ __forceinline__ void load_xblock(const uint32_t* __restrict__ src, bool valid,
+                                            XBlock& o) {
     const u32x4* p = reinterpret_cast<const u32x4*>(src);
-    o.d0[0] = p[0];
-    o.d0[1] = p[1];
-    o.d1[0] = p[2];
-    o.d1[1] = p[3];
-    const u32x4 e = p[4];
-    o.c0 = (int)e.x;
-    o.c1 = (int)e.y;
-    o.s = __uint_as_float(e.z);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o.dg[i] = p[i];
+    o.sx = valid ? __uint_as_float(src[16]) : 0.0f;
 }
 
 // ---- weights --------------------------------------------------------------------------------
@@ -193,9 +258,8 @@ __device__ __forceinline__ void load_chunk(Chunk<QT, NB, R>& c, const uint8_t* _
 
 template <int QT, int M, int NB, int R>
 __device__ __forceinline__ void compute_chunk(const Chunk<QT, NB, R>& c, const XBlock (&xbs)[M][NB],
-                                              const bool* bval, float* __restrict__ y, int w,
-                                              int W, int j0, int jcount, int N, int lane,
-                                              int m_real) {
+                                              float* __restrict__ y, int w, int W, int j0,
+                                              int jcount, int N, int lane, int m_real) {
     float part[M][R];
 #pragma unroll
     for (int m = 0; m < M; ++m)
@@ -208,33 +272,31 @@ __device__ __forceinline__ void compute_chunk(const Chunk<QT, NB, R>& c, const X
             const XBlock& xb = xbs[m][i];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                int a0 = xb.c0, a1 = xb.c1;
+                int acc;
                 if constexpr (QT == UNILLM_QTYPE_Q4_0) {
+                    // digit levels 3..0: A = ((a3 * 16 + a2) * 16 + a1) * 16 + a0
                     const u32x4 w4 = c.q[r][i][0];
+                    int lv[4] = {0, 0, 0, 0};
 #pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        const int lo = (int)(w4[t] & 0x0F0F0F0Fu);
-                        const int hi = (int)((w4[t] >> 4) & 0x0F0F0F0Fu);
-                        a0 = sdot4(lo, (int)xb.d0[0][t], a0);
-                        a0 = sdot4(hi, (int)xb.d0[1][t], a0);
-                        a1 = sdot4(lo, (int)xb.d1[0][t], a1);
-                        a1 = sdot4(hi, (int)xb.d1[1][t], a1);
-                    }
+                    for (int t = 0; t < 4; ++t)
+#pragma unroll
+                        for (int L = 0; L < 4; ++L) lv[L] = sdot8((int)w4[t], (int)xb.dg[L][t], lv[L]);
+                    acc = ((lv[0] * 16 + lv[1]) * 16 + lv[2]) * 16 + lv[3];
                 } else {
+                    int a0 = 0, a1 = 0;
 #pragma unroll
                     for (int v = 0; v < 2; ++v) {
                         const u32x4 w4 = c.q[r][i][v];
 #pragma unroll
                         for (int t = 0; t < 4; ++t) {
-                            a0 = sdot4((int)w4[t], (int)xb.d0[v][t], a0);
-                            a1 = sdot4((int)w4[t], (int)xb.d1[v][t], a1);
+                            a0 = sdot4((int)w4[t], (int)xb.dg[v][t], a0);
+                            a1 = sdot4((int)w4[t], (int)xb.dg[2 + v][t], a1);
                         }
                     }
+                    acc = a0 * 254 + a1;
                 }
-                // lanes past the row end (clamped duplicates) contribute nothing
-                const float dw = bval[i] ? __half2float(__ushort_as_half(c.d[r][i])) : 0.0f;
-                const float blk = fmaf((float)a1, 1.0f / 254.0f, (float)a0);
-                part[m][r] = fmaf(dw * xb.s, blk, part[m][r]);
+                const float dw = __half2float(__ushort_as_half(c.d[r][i]));
+                part[m][r] = fmaf(dw, (float)acc * xb.sx, part[m][r]);
             }
         }
 #pragma unroll
@@ -260,7 +322,7 @@ constexpr int gemv_threads() {
 
 // m_real <= M rows of x are used; rows m >= m_real repeat row m_real - 1 and
 // are not written.  Dynamic LDS: M * KB * kXWords dwords of x digits.
-// M * KB * 4 <= 2048, so a thread builds at most 2048 / THREADS quarter-blocks.
+// KB <= NB * 64, so a thread builds at most PASSES = ceil(M * NB * 256 / THREADS) quarter-blocks.
 template <int QT, int M, int NB, int R, int THREADS>
 __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict__ base,
                                                        int64_t rb,
@@ -268,7 +330,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
                                                        float* __restrict__ y, int N, int KB,
                                                        int m_real) {
     constexpr int WAVES = THREADS / 64;
-    constexpr int PASSES = 2048 / THREADS;
+    constexpr int PASSES = (M * NB * 256 + THREADS - 1) / THREADS;  // quarter-blocks per thread
     extern __shared__ uint32_t xlds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * WAVES + (threadIdx.x >> 6));
@@ -289,46 +351,50 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
         bidx[i] = min(b, KB - 1);
     }
 
-    // 1. x for the digits
+    // 1. x for the digits (indices clamped into x; every thread loads)
     const int nq = M * KB * 4;
     float v[PASSES][8];
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
-        const int q = threadIdx.x + p * THREADS;
-        const int blk = min(q, nq - 1) >> 2;
+        const int q = min((int)threadIdx.x + p * THREADS, nq - 1);
+        const int blk = q >> 2;
         const int m = blk / KB;
-        const float4* src = reinterpret_cast<const float4*>(
-            x + (int64_t)min(m, m_real - 1) * K + (int64_t)(blk - m * KB) * QK) + 2 * (q & 3);
-        float4 f0 = make_float4(0.f, 0.f, 0.f, 0.f), f1 = f0;
-        if (q < nq) {  // only the quarters that exist are fetched
-            f0 = src[0];
-            f1 = src[1];
+        const float* xb = x + (int64_t)min(m, m_real - 1) * K + (int64_t)(blk - m * KB) * QK;
+        int o0, o1;
+        quarter_offsets<QT>(q & 3, o0, o1);
+        const float4 f0 = *reinterpret_cast<const float4*>(xb + o0);
+        const float4 f1 = *reinterpret_cast<const float4*>(xb + o1);
+        if constexpr (QT == UNILLM_QTYPE_Q4_0) {  // payload nibble order
+            v[p][0] = f0.x; v[p][1] = f1.x; v[p][2] = f0.y; v[p][3] = f1.y;
+            v[p][4] = f0.z; v[p][5] = f1.z; v[p][6] = f0.w; v[p][7] = f1.w;
+        } else {
+            v[p][0] = f0.x; v[p][1] = f0.y; v[p][2] = f0.z; v[p][3] = f0.w;
+            v[p][4] = f1.x; v[p][5] = f1.y; v[p][6] = f1.z; v[p][7] = f1.w;
         }
-        v[p][0] = f0.x; v[p][1] = f0.y; v[p][2] = f0.z; v[p][3] = f0.w;
-        v[p][4] = f1.x; v[p][5] = f1.y; v[p][6] = f1.z; v[p][7] = f1.w;
     }
-    // Unconditional (indices clamped into the matrix): a load under a branch
-    // would make the waits that follow it conservative.
-    // 2. x digits for all M * KB blocks, four threads per block (threads past
-    //    nq compute on a clamped copy and store nothing; nq is a multiple of 4,
-    //    so a DPP quad is either all real or all clamped).  This comes before
-    //    the weight loads: instructions issue in order, and once the weight
-    //    loads fill the memory pipeline, anything behind them waits until they
-    //    are accepted -- the digits would then be late for every row.
+
+    // 2. x digit records for all M * KB blocks, four threads per block (threads
+    //    past nq compute on a clamped copy and store nothing; nq is a multiple
+    //    of 4, so a DPP quad is either all real or all clamped).  This comes
+    //    before the weight loads: instructions issue in order, and once the
+    //    weight loads fill the memory pipeline, anything behind them waits
+    //    until they are accepted -- the digits would then be late for every row.
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
         const int q = threadIdx.x + p * THREADS;
-        prep_quarter<QT>(v[p], q & 3, q < nq, xlds + (size_t)(min(q, nq - 1) >> 2) * kXWords);
+        uint32_t* dst = xlds + (size_t)(min(q, nq - 1) >> 2) * kXWords;
+        if constexpr (QT == UNILLM_QTYPE_Q4_0) prep_q4(v[p], q & 3, q < nq, dst);
+        else prep_q8(v[p], q & 3, q < nq, dst);
     }
     __syncthreads();
 
-    // 3. this lane's x digits, read once from LDS into registers for all rows
-    //    (also ahead of the weight loads, for the same in-order reason)
+
+    // 3. this lane's records, read once from LDS into registers for all rows
     XBlock xb[M][NB];
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
-        for (int i = 0; i < NB; ++i) load_xblock(xlds + ((size_t)m * KB + bidx[i]) * kXWords, xb[m][i]);
+        for (int i = 0; i < NB; ++i) load_xblock(xlds + ((size_t)m * KB + bidx[i]) * kXWords, bval[i], xb[m][i]);
     __builtin_amdgcn_sched_barrier(0);  // keep the reads above the weight loads
 
     // 4. the weights: the first two chunks at once (unconditional, indices
@@ -340,13 +406,13 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
 
     // 5. the first two chunks, then (for ranges longer than 2R rows) two
     //    chunks per step
-    compute_chunk<QT, M, NB, R>(a, xb, bval, y, wrow, waves, 0, jcount, N, lane, m_real);
-    compute_chunk<QT, M, NB, R>(b, xb, bval, y, wrow, waves, R, jcount, N, lane, m_real);
+    compute_chunk<QT, M, NB, R>(a, xb, y, wrow, waves, 0, jcount, N, lane, m_real);
+    compute_chunk<QT, M, NB, R>(b, xb, y, wrow, waves, R, jcount, N, lane, m_real);
     for (int j = 2 * R; j < jcount; j += 2 * R) {
         load_chunk<QT, NB, R>(a, base, rb, wrow, waves, j, jlast, KB, bidx);
         load_chunk<QT, NB, R>(b, base, rb, wrow, waves, j + R, jlast, KB, bidx);
-        compute_chunk<QT, M, NB, R>(a, xb, bval, y, wrow, waves, j, jcount, N, lane, m_real);
-        compute_chunk<QT, M, NB, R>(b, xb, bval, y, wrow, waves, j + R, jcount, N, lane, m_real);
+        compute_chunk<QT, M, NB, R>(a, xb, y, wrow, waves, j, jcount, N, lane, m_real);
+        compute_chunk<QT, M, NB, R>(b, xb, y, wrow, waves, j + R, jcount, N, lane, m_real);
     }
 }
 

@@ -3,7 +3,10 @@
 // Device layout of a weight (written once by the repack kernel at upload).
 // Row n occupies `row_bytes` = align16(kb * (QB + 2)) bytes at n * row_bytes:
 //   [kb x QB payload bytes][kb x f16 scales][pad to 16 B]
-// QB = 16 (Q4_0 nibbles) or 32 (Q8_0 int8).  The payloads of a row are back
+// QB = 16 (Q4_0 nibbles) or 32 (Q8_0 int8).  Q4_0 nibbles are stored as the
+// signed 4-bit value q - 8 (the GGUF byte XOR 0x88), the operand form of
+// v_dot8_i32_i4; the GGUF nibble order is kept (low nibble of byte j = element
+// j, high nibble = element j + 16).  The payloads of a row are back
 // to back, so a 128-bit load is exactly one Q4_0 block payload (or half a
 // Q8_0 one), and the row's scales sit in the same DRAM pages right after
 // them (measured: cheaper to stream than a separate scale plane).  The byte

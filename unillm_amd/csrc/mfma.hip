@@ -112,8 +112,9 @@ __global__ __launch_bounds__(256) void mfma_kernel(const uint8_t* __restrict__ b
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
                         const uint32_t byte = (w2[j / 4] >> (8 * (j % 4))) & 0xFFu;
-                        lo[j] = (T)((float)((int)(byte & 0xF) - 8) * d * wscale);
-                        hi[j] = (T)((float)((int)(byte >> 4) - 8) * d * wscale);
+                        // signed nibbles q - 8
+                        lo[j] = (T)((float)(((int)(byte << 28)) >> 28) * d * wscale);
+                        hi[j] = (T)((float)(((int)(byte << 24)) >> 28) * d * wscale);
                     }
                 } else {
 #pragma unroll

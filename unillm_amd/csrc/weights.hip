@@ -26,12 +26,14 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
     const int64_t row = i / kb, blk = i - row * kb;
     const uint8_t* b = src + i * (QB + 2);
     *const_cast<uint16_t*>(blk_scale<QB>(base, rb, kb, row, blk)) = ld_u16(b);
+    // Q4_0 codes are stored as signed nibbles q - 8 (two's complement: q ^ 8)
+    constexpr uint32_t kFlip = QB == 16 ? 0x88888888u : 0u;
     uint32_t words[QB / 4];
 #pragma unroll
     for (int w = 0; w < QB / 4; ++w) {
         const uint8_t* p = b + 2 + 4 * w;
-        words[w] = (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) |
-                   ((uint32_t)p[3] << 24);
+        words[w] = ((uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) |
+                    ((uint32_t)p[3] << 24)) ^ kFlip;
     }
     uint4* dst = reinterpret_cast<uint4*>(const_cast<uint8_t*>(blk_payload<QB>(base, rb, row, blk)));
 #pragma unroll
@@ -40,7 +42,8 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
 }
 
 // Exact dequant (GGML to_float): Q4_0 w[j] = (lo(qs[j]) - 8) * d,
-// w[j + 16] = (hi(qs[j]) - 8) * d; Q8_0 w[j] = qs[j] * d.  One thread per
+// w[j + 16] = (hi(qs[j]) - 8) * d (stored here as the signed nibbles q - 8);
+// Q8_0 w[j] = qs[j] * d.  One thread per
 // block.  Every product is exact in f32, so any evaluation order is bit-exact.
 template <int QT>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ base,
@@ -63,8 +66,8 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
                 const uint32_t byte = (w[t] >> (8 * b)) & 0xFFu;
-                lo[b] = (float)((int)(byte & 0xF) - 8) * d;
-                hi[b] = (float)((int)(byte >> 4) - 8) * d;
+                lo[b] = (float)(((int)(byte << 28)) >> 28) * d;  // signed nibble q - 8
+                hi[b] = (float)(((int)(byte << 24)) >> 28) * d;
             }
             o[t] = make_float4(lo[0], lo[1], lo[2], lo[3]);
             o[4 + t] = make_float4(hi[0], hi[1], hi[2], hi[3]);

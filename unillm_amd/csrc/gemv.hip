@@ -351,11 +351,15 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
         bidx[i] = min(b, KB - 1);
     }
 
-    // 1. x for the digits (indices clamped into x; every thread loads)
+    // 1. x for the digits.  A wave whose quarters of a pass all lie past nq
+    //    neither loads nor builds anything in that pass (a wave-uniform, scalar
+    //    branch); inside a wave, indices are clamped into x.
     const int nq = M * KB * 4;
+    const int wave0 = __builtin_amdgcn_readfirstlane((int)threadIdx.x & ~63);
     float v[PASSES][8];
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
+        if (wave0 + p * THREADS >= nq) continue;
         const int q = min((int)threadIdx.x + p * THREADS, nq - 1);
         const int blk = q >> 2;
         const int m = blk / KB;
@@ -373,14 +377,20 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
         }
     }
 
-    // 2. x digit records for all M * KB blocks, four threads per block (threads
+    // 2. the first chunk of weights: one chunk per wave keeps the memory
+    //    pipeline busy while x arrives and is turned into digits, without
+    //    filling it -- instructions issue in order, and once weight loads back
+    //    up, everything behind them (here: the digit work every row needs)
+    //    waits until they are accepted.
+    Chunk<QT, NB, R> a, b;
+    load_chunk<QT, NB, R>(a, base, rb, wrow, waves, 0, jlast, KB, bidx);
+
+    // 3. x digit records for all M * KB blocks, four threads per block (threads
     //    past nq compute on a clamped copy and store nothing; nq is a multiple
-    //    of 4, so a DPP quad is either all real or all clamped).  This comes
-    //    before the weight loads: instructions issue in order, and once the
-    //    weight loads fill the memory pipeline, anything behind them waits
-    //    until they are accepted -- the digits would then be late for every row.
+    //    of 4, so a DPP quad is either all real or all clamped).
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
+        if (wave0 + p * THREADS >= nq) continue;
         const int q = threadIdx.x + p * THREADS;
         uint32_t* dst = xlds + (size_t)(min(q, nq - 1) >> 2) * kXWords;
         if constexpr (QT == UNILLM_QTYPE_Q4_0) prep_q4(v[p], q & 3, q < nq, dst);
@@ -389,22 +399,19 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     __syncthreads();
 
 
-    // 3. this lane's records, read once from LDS into registers for all rows
+    // 4. this lane's records, read once from LDS into registers for all rows
     XBlock xb[M][NB];
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
         for (int i = 0; i < NB; ++i) load_xblock(xlds + ((size_t)m * KB + bidx[i]) * kXWords, bval[i], xb[m][i]);
-    __builtin_amdgcn_sched_barrier(0);  // keep the reads above the weight loads
+    __builtin_amdgcn_sched_barrier(0);  // keep the reads above the second chunk's loads
 
-    // 4. the weights: the first two chunks at once (unconditional, indices
-    //    clamped: a load under a branch would make the waits that follow it
-    //    conservative)
-    Chunk<QT, NB, R> a, b;
-    load_chunk<QT, NB, R>(a, base, rb, wrow, waves, 0, jlast, KB, bidx);
+    // 5. the second chunk (loads are unconditional, indices clamped: a load
+    //    under a branch would make the waits that follow it conservative)
     load_chunk<QT, NB, R>(b, base, rb, wrow, waves, R, jlast, KB, bidx);
 
-    // 5. the first two chunks, then (for ranges longer than 2R rows) two
+    // 6. the first two chunks, then (for ranges longer than 2R rows) two
     //    chunks per step
     compute_chunk<QT, M, NB, R>(a, xb, y, wrow, waves, 0, jcount, N, lane, m_real);
     compute_chunk<QT, M, NB, R>(b, xb, y, wrow, waves, R, jcount, N, lane, m_real);

@@ -52,7 +52,37 @@ def parse():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default="", help="comma list of extra configs to run "
                     "(q8_gemv,batched,prefill,stack) -- for profiling")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only copy 64 MiB once (device to device) and exit: the known-size "
+                    "kernel that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
+
+
+COPY_PROBE_BYTES = 64 << 20
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "gemv_q4_0_decode_traffic.json")
+
+
+def copy_probe():
+    import torch
+    src = torch.full((COPY_PROBE_BYTES,), 7, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": COPY_PROBE_BYTES}), flush=True)
+
+
+def measured_traffic():
+    """HBM bytes per GEMV launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by what the counter reads for the
+    64 MiB copy probe), or None if it is absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return t["bytes_per_launch"], t
+    except (OSError, ValueError, KeyError):
+        return None, None
 
 
 class Timer:
@@ -249,6 +279,9 @@ def extra_configs(torch, QuantLinear, gen, stream, only):
 
 def main():
     args = parse()
+    if args.copy_probe:
+        copy_probe()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(sharding is a design note, not code); run with --gpus 1", file=sys.stderr)
@@ -293,6 +326,13 @@ def main():
     if not args.no_cpu_baseline:
         cpu = cpu_baseline()
 
+    traffic, tinfo = measured_traffic()
+    traffic_src = None
+    if tinfo is not None:
+        traffic_src = (f"rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over the same decode step "
+                       f"({os.path.relpath(TRAFFIC_FILE, os.path.dirname(TRAFFIC_FILE) + '/..')}), "
+                       f"scale factors {tinfo.get('fetch_factor')} / {tinfo.get('write_factor')} "
+                       "from the 64 MiB copy probe")
     line = {
         "metric": "Q4_0 decode GEMV GB/s (% HBM peak) at 7B shapes; prefill GEMM TFLOP/s",
         "value": round(value, 1),
@@ -315,9 +355,10 @@ def main():
                    "kernel_path": {1: "gemv", 2: "decode_mfma", 3: "prefill_mfma"}[path]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "gemv_kernel<Q4_0, M=1>",
+                     "traffic": traffic, "kernel": "gemv_kernel<Q4_0, M=1>",
                      "avg_launch_us": round(kern_ms * 1e3, 3),
-                     "bytes_per_launch": nbytes // launches},
+                     "bytes_per_launch": nbytes // launches,
+                     "traffic_source": traffic_src},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -250,7 +250,7 @@ int unillm_hip_qweight_info(const unillm_qweight* w, int* qtype, int64_t* n, int
 
 int unillm_hip_select_path(const unillm_qweight* w, int64_t m) {
     if (!w || m < 0) return fail(UNILLM_ERR_INVALID_ARG, "bad arguments to select_path");
-    if (m <= kGemvMaxM && w->kb <= gemv_max_kb(m, w->qtype)) return UNILLM_PATH_GEMV;
+    if (gemv_supports(*w, m)) return UNILLM_PATH_GEMV;
     if (m <= kDecodeMaxM) return UNILLM_PATH_DECODE_MFMA;
     return UNILLM_PATH_PREFILL_MFMA;
 }
@@ -272,10 +272,11 @@ int unillm_hip_qmatmul_path(const unillm_qweight* w, const float* x_dev, int64_t
     hipError_t e;
     switch (path) {
         case UNILLM_PATH_GEMV:
-            if (m > kGemvMaxM || w->kb > gemv_max_kb(m, w->qtype))
+            if (!gemv_supports(*w, m))
                 return fail(UNILLM_ERR_UNSUPPORTED,
-                            "GEMV path takes m <= 4 and k <= " +
-                                std::to_string(gemv_max_kb(m, w->qtype) * QK) + " at this m");
+                            "GEMV path takes m <= 4, k <= " +
+                                std::to_string(gemv_max_kb(m, w->qtype) * QK) +
+                                " at this m and weights under 4 GiB");
             e = launch_gemv(*w, x_dev, m, y_dev, s);
             break;
         case UNILLM_PATH_DECODE_MFMA:

@@ -38,6 +38,7 @@ constexpr int QK = 32;  // weights per block
 using QWeight = ::unillm_qweight;
 
 int64_t gemv_max_kb(int64_t m, int qtype);
+bool gemv_supports(const unillm_qweight& w, int64_t m);
 
 inline int qbytes(int qtype) { return qtype == UNILLM_QTYPE_Q4_0 ? 16 : 32; }
 inline int64_t row_bytes_for(int qtype, int64_t kb) {

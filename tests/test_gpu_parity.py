@@ -200,6 +200,21 @@ def test_baseline_prefill_rows_sampled(qtype, m, k, n):
     assert np.array_equal(y2.cpu().numpy(), 2.0 * y)
 
 
+@pytest.mark.parametrize("qtype,m,k,n", [(Q4_0, 2048, 4096, 14336), (Q8_0, 1100, 4128, 14000),
+                                         (Q4_0, 1100, 4128, 14000)])
+def test_prefill_large_tiles(qtype, m, k, n):
+    # enough tiles for the 256-row tile shape; ragged m and n, odd blocks per row
+    blocks, x = _case(qtype, m, n, k, seed=m + n + k)
+    ql = QuantLinear.from_blocks(qtype, n, k, blocks)
+    y = _run(ql, x, PATH_AUTO)
+    rows = np.array([0, 1, 255, 256, 1023, m - 77, m - 1])
+    ref = oracle.qmatmul_f64(qtype, blocks, x[rows], n, k)
+    assert oracle.normwise_error(y[rows], ref) < 2e-2
+    y2 = ql.forward(_dev(x) * 2.0)
+    torch.cuda.synchronize()
+    assert np.array_equal(y2.cpu().numpy(), 2.0 * y)
+
+
 # ---- edges -----------------------------------------------------------------------------------
 
 def test_m_zero_is_noop():

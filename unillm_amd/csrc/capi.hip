@@ -50,6 +50,13 @@ int do_init(int device) {
     if ((e = hipSetDevice(device)) != hipSuccess) return fail_hip(e, "hipSetDevice");
     g_info.cu_count = prop.multiProcessorCount;
     g_info.max_lds = (int)prop.sharedMemPerBlock;
+    // the prefill path takes its bf16 copy of x from the stream-ordered pool:
+    // keep freed memory in the pool between calls instead of returning it
+    hipMemPool_t pool;
+    if (hipDeviceGetDefaultMemPool(&pool, device) == hipSuccess) {
+        uint64_t keep = UINT64_MAX;
+        (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+    }
     g_device = device;
     return UNILLM_OK;
 }

@@ -217,9 +217,5 @@ hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float
     return launch_cfg<_Float16, 64, 64, 2, 2>(w, x, m, y, s);
 }
 
-hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, float* y,
-                               hipStream_t s) {
-    return launch_cfg<__bf16, 128, 128, 2, 2>(w, x, m, y, s);
-}
 
 }  // namespace unillm

@@ -7,21 +7,28 @@
 // matrix cores (v_mfma_f32_16x16x32_bf16).  Bound: MFMA (2 m n k flops over
 // ~n k / 32 * 18 + 4 m k + 4 m n bytes).
 //
+// x is first rounded to bf16 once (x_to_bf16_kernel, into a stream-ordered
+// workspace): the GEMM re-reads x once per 256-column tile, so half the bytes,
+// and no conversion sits in its inner loop.
+//
 // Tile per workgroup: BM rows of x (BM = 256 or 128) x 256 weight rows
-// (output columns), k in steps of 64 (two blocks).  Four waves; wave w owns
-// output columns [64 w, 64 w + 64) for all BM rows: BM / 16 x 4 MFMA tiles,
-// 4 fp32 accumulators each (256 per lane at BM = 256; one wave per SIMD).
-//   A (x): BM x 64 f32 per step, loaded into registers one step ahead,
-//     rounded to bf16 and written to a double-buffered LDS tile; every wave
-//     reads all BM rows of it.
-//   B (weights): no LDS.  Each wave's 64 columns are its own, so each lane
-//     loads exactly the 8 payload bytes behind its MFMA B fragment (column
-//     l % 16 of a 16-column tile, elements 8 (l / 16) .. +7 of a 32-block)
-//     plus the block scale, one step ahead, and dequantizes them in
-//     registers; nothing is dequantized twice within a workgroup.
-// LDS traffic per CU per 32-wide k slice: reads 4 x BM x 32 x 2 B, writes
-// BM x 32 x 2 B -- 80 B/clk at BM = 256 against ~128 B/clk available, with the
-// MFMAs of the slice taking BM x 256 x 32 x 2 / 4096 flop/clk cycles.
+// (output columns), k in steps of 64 (two blocks).  Eight waves (two per
+// SIMD) in a 2 x 4 grid: wave (rw, cw) owns BM / 2 rows x 64 columns,
+// BM / 32 x 4 MFMA tiles of 16 x 16, fp32 accumulators in registers.
+//   - Operands reach LDS by direct global -> LDS loads through a 3-stage ring
+//     (two k steps in flight, no VGPR staging): A as bf16 rows with an XOR
+//     swizzle of 16-byte chunks, B as the raw Q4_0 / Q8_0 payload bytes and
+//     scales of the tile's 256 weight rows.
+//   - Each lane reads the 8 payload bytes behind its MFMA B fragment and
+//     dequantizes them in registers; a column group's weights are dequantized
+//     by its two waves (a 1 x 8 split would halve that but double the A reads).
+//   - The LDS reads are inline asm with explicit waits, so the compiler never
+//     drains the ring's later stages before them; a step waits for its own
+//     stage (vmcnt in issue order) and meets the other waves at a bare
+//     s_barrier.
+// Measured limits (rocprofv3 counters): VALU (the dequant, ~2.9 instructions
+// per weight per pass) and MFMA each occupy ~45 % of a SIMD's cycles with
+// little co-issue; the 2 x 4 split keeps LDS traffic at ~70 % of its rate.
 //
 // Workgroup -> tile: workgroups are dealt round-robin over the 8 XCDs, so
 // workgroup b takes tile (b % 8) * (T / 8) + b / 8 (T tiles, padded to a
@@ -32,6 +39,8 @@
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
+#include <type_traits>
+#include <utility>
 
 #include "internal.hpp"
 
@@ -49,16 +58,14 @@ constexpr int PLD = PBK + 8;     // LDS row stride in bf16 (144 B): spreads rows
 #define PREFILL_WAVES 8
 #endif
 constexpr int kWaves = PREFILL_WAVES;  // waves per workgroup (8: two per SIMD)
-#ifndef PREFILL_DEPTH
-#define PREFILL_DEPTH 1
-#endif
-constexpr int kDepth = PREFILL_DEPTH;  // k steps of weight loads in flight
 
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
     // round to nearest even; the pair in one dword, lo in the low half
-    const __bf16 a = (__bf16)lo, b = (__bf16)hi;
-    return (uint32_t)__builtin_bit_cast(uint16_t, a) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+    // (v_cvt_pk_bf16_f32 directly: two scalar conversions compile to two of them
+    // plus a shift and an or)
+    uint32_t r;
+    asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(lo), "v"(hi));
+    return r;
 }
 
 // One lane's B fragment of one 32-block: 8 codes (4 per dword of `raw`, in
@@ -77,9 +84,15 @@ __device__ __forceinline__ bf16x8 dequant8(u32x2 raw, int shift, float d) {
     float f[8];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
+        // v_cvt_f32_ubyte{0..3} directly: the compiler otherwise rewrites the byte
+        // masks (the codes are known to be < 16) into bit-field extracts plus ubyte0
+        float c[4];
+        asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(c[0]) : "v"(u[h]));
+        asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(c[1]) : "v"(u[h]));
+        asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(c[2]) : "v"(u[h]));
+        asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(c[3]) : "v"(u[h]));
 #pragma unroll
-        for (int e = 0; e < 4; ++e)  // v_cvt_f32_ubyte{e}
-            f[4 * h + e] = fmaf((float)((u[h] >> (8 * e)) & 0xFFu), d, off);
+        for (int e = 0; e < 4; ++e) f[4 * h + e] = fmaf(c[e], d, off);
     }
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     const u32x4 p = {pack_bf16(f[0], f[1]), pack_bf16(f[2], f[3]), pack_bf16(f[4], f[5]),
@@ -99,110 +112,174 @@ __global__ __launch_bounds__(256) void x_to_bf16_kernel(const float* __restrict_
     }
 }
 
-// Register-staged operands of one k step (64 k): the bf16 A slice this thread
-// copies into LDS (A comes from L2 -- the XCD's CUs share it -- and is loaded
-// one step ahead), and this lane's raw B fragments with their scales (B comes
-// from HBM and is loaded D steps ahead).
-template <int BM, int NW>
-struct AStage {
-    static constexpr int APASS = BM * 8 / (64 * NW);  // 16-byte A chunks per thread
-    uint4 a[APASS];
-};
-template <int TJ>
-struct BStage {
-    u32x2 b[TJ][2];    // [16-column tile j][block of the step]
-    uint32_t sc[TJ];   // the two f16 scales of the step's blocks, per j
+// ---- LDS ring ------------------------------------------------------------------------------
+// S stages, each one k step (64 k) of both operands, filled by direct
+// global -> LDS loads (global_load_lds_dwordx4: each lane's 16 bytes land at
+// lane * 16 of the instruction's 1 KiB destination; no VGPRs involved):
+//   A  [BM rows][128 B]  bf16 x, swizzled: the 16-byte chunk c of row r sits in
+//                        slot c ^ (r % 8), so the 16 rows an MFMA fragment read
+//                        touches spread over the banks;
+//   Bp [256 cols][32 B]  the step's two payloads of each weight row;
+//   Bs [256 cols][4 B]   their two f16 scales (x2: each wave loads 32 columns'
+//                        scales with all 64 lanes, the upper half a duplicate).
+// The compiler is kept out of the LDS reads (inline asm) so it never inserts
+// its conservative "wait for every direct load" before them; the kernel waits
+// for exactly the stage it reads (vmcnt counts a wave's loads in issue order)
+// and then meets the other waves at a bare s_barrier (no fence: a fence would
+// also drain the stages still in flight).
+constexpr int kStages = 3;
+
+template <int QT, int BM>
+struct Ring {
+    static constexpr int QB = QT == UNILLM_QTYPE_Q4_0 ? 16 : 32;  // payload bytes per block
+    static constexpr int A = BM * 128;
+    static constexpr int BP = PBN * 2 * QB;
+    static constexpr int BS = 2 * PBN * 4;
+    static constexpr int STAGE = A + BP + BS;
+    static constexpr int BYTES = kStages * STAGE;
+    static constexpr int CPB = 2 * QB / 16;            // 16-byte payload chunks per column
+    static constexpr int AQ = BM / 8 / 8;              // A loads (8 rows each) per wave
+    static constexpr int DMA = AQ + CPB / 2 + 1;       // direct loads per wave per stage
 };
 
-template <int QT, int BM, int NW, int D>
+// Calls f(integral_constant<int, I>) for I = 0 .. N - 1 (compile-time indices).
+template <int N, class F, int... I>
+__device__ __forceinline__ void constexpr_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void constexpr_for(F&& f) {
+    constexpr_for_impl<N>(f, std::make_integer_sequence<int, N>{});
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+typedef const __attribute__((address_space(1))) void* gbl_ptr;
+
+__device__ __forceinline__ void dma16(const void* g, uint8_t* l) {
+    __builtin_amdgcn_global_load_lds((gbl_ptr)g, (lds_ptr)l, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* g, uint8_t* l) {
+    __builtin_amdgcn_global_load_lds((gbl_ptr)g, (lds_ptr)l, 4, 0, 0);
+}
+
+// LDS reads the compiler does not see (so it adds no wait for the direct loads
+// before them); lds_wait<N>() waits until at most N of this wave's LDS reads are
+// outstanding and ties the given registers to that point.
+template <int OFF>
+__device__ __forceinline__ bf16x8 lds_read128(uint32_t addr) {
+    bf16x8 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_read64(uint32_t addr) {
+    u32x2 v;
+    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t lds_read32(uint32_t addr) {
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return v;
+}
+
+template <int QT, int BM, int NW>
 __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __restrict__ base,
                                                               int64_t rb,
                                                               const __bf16* __restrict__ xb,
                                                               float* __restrict__ y, int M, int N,
                                                               int KB, int tiles_n, int tiles,
                                                               int tiles_pad) {
+    static_assert(NW == 8, "the ring's load split assumes 8 waves");
     constexpr int QB = QT == UNILLM_QTYPE_Q4_0 ? 16 : 32;  // payload bytes per block
-    constexpr int TI = BM / 16;                            // MFMA tiles along m per wave
-    constexpr int WC = PBN / NW;                           // output columns per wave
-    constexpr int TJ = WC / 16;                            // MFMA tiles along n per wave
-    constexpr int NT = NW * 64;                            // threads
-    constexpr int AROWS = NT / 8;                          // rows one pass of A chunks covers
-    constexpr int APASS = AStage<BM, NW>::APASS;
-    __shared__ __attribute__((aligned(16))) __bf16 As[2][BM * PLD];
+    // waves: 2 row groups x 4 column groups; wave (rw, cw) owns rows BM / 2 * rw .. and
+    // columns 64 cw .. 64 cw + 63 of the tile (each column group's weights are
+    // dequantized by both of its waves: half the A traffic of a 1 x 8 split)
+    constexpr int RW = 2, CW = 4;
+    constexpr int WR = BM / RW;                            // rows per wave
+    constexpr int WC = PBN / CW;                           // output columns per wave (64)
+    constexpr int TI = WR / 16;                            // MFMA tiles along m per wave
+    constexpr int TJ = WC / 16;                            // MFMA tiles along n per wave (4)
+    using R = Ring<QT, BM>;
+    constexpr int AQ = R::AQ;
+    constexpr int CPB = R::CPB;
+    extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
 
     // ---- tile (XCD-aware) ----
     const int per_xcd = tiles_pad / 8;
     const int t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     if (t >= tiles) return;  // padding workgroups (uniform: the whole workgroup leaves)
     const int mt = t / tiles_n, nt = t % tiles_n;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int m0 = mt * BM;
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int m0 = mt * BM, n0 = nt * PBN;
     const uint32_t K = (uint32_t)KB * QK;
     const int ksteps = (KB + 1) / 2;
 
-    // ---- A: thread -> 16-byte chunk (tid % 8) of rows tid / 8 + AROWS p (bf16, 32-bit
-    // element offsets: the launcher keeps m * k below 2^30); rows past m read row m - 1
-    // and are never stored
-    const int arow = tid / 8, ach = tid % 8;
+    // ---- this lane's direct-load sources (k-independent parts) ----
+    // A: load q covers tile rows 8 q .. 8 q + 7; lane -> row 8 q + lane / 8, slot lane % 8,
+    // global chunk (lane % 8) ^ (row % 8).  Rows past m read row m - 1 (never stored).
+    uint32_t arow_off[AQ], achunk[AQ];
+#pragma unroll
+    for (int q = 0; q < AQ; ++q) {
+        const int r = 8 * (wv * AQ + q) + lane / 8;
+        achunk[q] = (uint32_t)(((lane % 8) ^ (r % 8)) * 8);
+        arow_off[q] = (uint32_t)min(m0 + r, M - 1) * K;
+    }
+    // B payload: wave wv covers tile columns 32 wv .. +31, CPB chunks each; load u: lane ->
+    // column 32 wv + u (64 / CPB) + lane / CPB, chunk c = lane % CPB (block c / (QB / 16),
+    // 16-byte half c % (QB / 16)).  Scales: lane -> column 32 wv + lane % 32 (upper half of
+    // the wave writes a duplicate).
+    uint32_t pcol_off[CPB / 2];
+#pragma unroll
+    for (int u = 0; u < CPB / 2; ++u)
+        pcol_off[u] = (uint32_t)min(n0 + 32 * wv + u * (64 / CPB) + lane / CPB, N - 1) * (uint32_t)rb;
+    const int pblk = (lane % CPB) / (QB / 16);
+    const uint32_t phalf = (uint32_t)((lane % CPB) % (QB / 16)) * 16;
+    const uint32_t ssrc = (uint32_t)min(n0 + 32 * wv + lane % 32, N - 1) * (uint32_t)rb +
+                          (uint32_t)KB * QB;
 
-    // ---- B: lane -> column (l % 16) of each 16-column tile, elements 8 g .. +7 of a
-    // block (g = l / 16): Q4_0 payload bytes 8 (g & 1) .. +7, low nibbles for g < 2,
-    // high for g >= 2; Q8_0 bytes 8 g .. +7.  32-bit byte offsets (weights < 4 GiB).
-    const int g = lane / 16;
+    auto issue = [&](int ks) {  // this wave's R::DMA direct loads of step ks
+        uint8_t* st = ring + (ks % kStages) * R::STAGE;
+        // k chunks past the end (an odd KB's last step) re-read the row's last chunk: x
+        // is finite and those k have zero weights
+#pragma unroll
+        for (int q = 0; q < AQ; ++q)
+            dma16(xb + arow_off[q] + min((uint32_t)ks * PBK + achunk[q], K - 8),
+                  st + (wv * AQ + q) * 1024);
+        const uint32_t kb = (uint32_t)min(2 * ks + pblk, KB - 1);
+#pragma unroll
+        for (int u = 0; u < CPB / 2; ++u)
+            dma16(base + pcol_off[u] + kb * QB + phalf, st + R::A + wv * (CPB / 2) * 1024 + u * 1024);
+        // the step's two scales (2 ks is even: one aligned dword; an odd KB's last step
+        // reads two bytes past the scales, inside the row padding or the weight's tail slot)
+        dma4(base + ssrc + 4u * ks, st + R::A + R::BP + wv * 256);
+    };
+
+    // ---- B fragment geometry: lane -> column 16 j + l % 16 of the wave's 32, elements
+    // 8 g .. +7 of a block (g = l / 16): Q4_0 payload bytes 8 (g & 1) .. +7, low nibbles
+    // for g < 2, high for g >= 2; Q8_0 bytes 8 g .. +7
+    const int g = lane / 16, fr = lane % 16;
     const uint32_t boff = QT == UNILLM_QTYPE_Q4_0 ? 8 * (g & 1) : 8 * g;
     const int bshift = QT == UNILLM_QTYPE_Q4_0 ? 4 * (g >> 1) : 0;
-    uint32_t bcol[TJ];
+    const int rw = wv / CW, cw = wv % CW;
     bool bval[TJ];
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-        const int c = nt * PBN + wv * WC + j * 16 + (lane % 16);
-        bval[j] = c < N;
-        bcol[j] = (uint32_t)min(c, N - 1) * (uint32_t)rb;
-    }
-    const uint32_t sbase = (uint32_t)KB * QB;  // scales follow the row's payloads
-
-    auto load_a = [&](AStage<BM, NW>& st, int ks) {
-        // k chunks past the end (an odd KB's last step) re-read the row's last chunk
-        const uint32_t kk = min((uint32_t)ks * PBK + ach * 8, K - 8);
+    for (int j = 0; j < TJ; ++j) bval[j] = n0 + WC * cw + 16 * j + fr < N;
+    // LDS byte offsets (within a stage) of this lane's reads; the row tile i and the
+    // column tile j enter as immediate offsets.  A: row WR rw + 16 i + fr, chunk
+    // 4 kk + g in slot (4 kk + g) ^ (row % 8), and row % 8 == fr % 8.
+    uint32_t aoff[2];
 #pragma unroll
-        for (int p = 0; p < APASS; ++p) {
-            const uint32_t row = (uint32_t)min(m0 + arow + AROWS * p, M - 1);
-            st.a[p] = *reinterpret_cast<const uint4*>(xb + row * K + kk);
-        }
-    };
-    auto load_b = [&](BStage<TJ>& st, int ks) {
-        const int kb0 = 2 * ks, kb1 = min(2 * ks + 1, KB - 1);
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-            st.b[j][0] = *reinterpret_cast<const u32x2*>(base + bcol[j] + (uint32_t)kb0 * QB + boff);
-            st.b[j][1] = *reinterpret_cast<const u32x2*>(base + bcol[j] + (uint32_t)kb1 * QB + boff);
-            // scales kb0, kb0 + 1 in one dword (kb0 is even; an odd KB's last step reads
-            // two bytes past the scales, inside the row padding or the weight's tail slot)
-            st.sc[j] = *reinterpret_cast<const uint32_t*>(base + bcol[j] + sbase + 2u * kb0);
-        }
-    };
-    auto store_a = [&](const AStage<BM, NW>& st, int ks, int buf) {
-        const uint32_t keep = 0u - (uint32_t)((uint32_t)ks * PBK + ach * 8 < K);
-#pragma unroll
-        for (int p = 0; p < APASS; ++p) {
-            const uint4 v = make_uint4(st.a[p].x & keep, st.a[p].y & keep, st.a[p].z & keep,
-                                       st.a[p].w & keep);
-            *reinterpret_cast<uint4*>(&As[buf][(arow + AROWS * p) * PLD + ach * 8]) = v;
-        }
-    };
-    bf16x8 bfrag[TJ][2];
-    auto dequant_b = [&](const BStage<TJ>& st, int ks) {
-        const bool b1ok = 2 * ks + 1 < KB;
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-            const float d0 = bval[j] ? __half2float(__ushort_as_half((uint16_t)st.sc[j])) : 0.0f;
-            const float d1 = bval[j] && b1ok
-                                 ? __half2float(__ushort_as_half((uint16_t)(st.sc[j] >> 16)))
-                                 : 0.0f;
-            bfrag[j][0] = dequant8<QT>(st.b[j][0], bshift, d0);
-            bfrag[j][1] = dequant8<QT>(st.b[j][1], bshift, d1);
-        }
-    };
+    for (int kk = 0; kk < 2; ++kk)
+        aoff[kk] = (uint32_t)((WR * rw + fr) * 128 + (((4 * kk + g) ^ (fr % 8)) * 16));
+    // B payload of column WC cw + 16 j + fr: block b at b * QB + boff; its scales
+    // (column c at (c / 32) * 256 + (c % 32) * 4)
+    const int bc0 = WC * cw + fr;
+    const uint32_t boff0 = (uint32_t)(R::A + bc0 * (2 * QB) + boff);
+    const uint32_t soff0 = (uint32_t)(R::A + R::BP + (bc0 / 32) * 256 + (bc0 % 32) * 4);
+    const uint32_t ring0 = (uint32_t)(uintptr_t)ring;
 
     f32x4 acc[TI][TJ];
 #pragma unroll
@@ -210,69 +287,94 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
 #pragma unroll
         for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int fr = lane % 16, fk = (lane / 16) * 8;
-    auto mfma_step = [&](int buf) {
+    // prologue: stages 0 .. kStages - 2 in flight
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-            for (int i = 0; i < TI; ++i) {
-                const bf16x8 a = *reinterpret_cast<const bf16x8*>(
-                    &As[buf][(16 * i + fr) * PLD + 32 * kk + fk]);
-#pragma unroll
-                for (int j = 0; j < TJ; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bfrag[j][kk],
-                                                                        acc[i][j], 0, 0, 0);
-            }
-        // schedule: one A fragment read, then its TJ MFMAs (a fragment is live for
-        // one group only; the SIMD's other wave covers the LDS latency)
-#pragma unroll
-        for (int g2 = 0; g2 < 2 * TI; ++g2) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-            __builtin_amdgcn_sched_group_barrier(0x008, TJ, 0);  // MFMA
-        }
-    };
+    for (int d = 0; d < kStages - 1; ++d)
+        if (d < ksteps) issue(d);
 
-    // A one step ahead, B D steps ahead.  Steady state: every step loads (no
-    // conditions); the last steps run in a separate tail.
-    AStage<BM, NW> sa;
-    BStage<TJ> sb[D];
-    load_a(sa, 0);
+    for (int ks = 0; ks < ksteps; ++ks) {
+        // wait for this wave's loads of step ks: the loads of later steps already
+        // issued (at most kStages - 2 of them) may stay in flight.  s_waitcnt on
+        // gfx950: vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 at their
+        // maxima (no wait)
+        constexpr int kWaitLater = 0x0F70 | (R::DMA & 0xF) | (((R::DMA >> 4) & 3) << 14);
+        if (ks + 1 < ksteps) __builtin_amdgcn_s_waitcnt(kWaitLater);
+        else __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        if (ks + kStages - 1 < ksteps) issue(ks + kStages - 1);
+
+        const uint32_t st = ring0 + (uint32_t)((ks % kStages) * R::STAGE);
+        // B: raw bytes and scales of this wave's columns -> bf16 fragments
+        u32x2 raw[TJ][2];
+        uint32_t sc[TJ];
+        static_assert(TJ == 4, "unrolled for four column tiles");
+        raw[0][0] = lds_read64<0 * 16 * 2 * QB>(st + boff0);
+        raw[0][1] = lds_read64<0 * 16 * 2 * QB + QB>(st + boff0);
+        raw[1][0] = lds_read64<1 * 16 * 2 * QB>(st + boff0);
+        raw[1][1] = lds_read64<1 * 16 * 2 * QB + QB>(st + boff0);
+        raw[2][0] = lds_read64<2 * 16 * 2 * QB>(st + boff0);
+        raw[2][1] = lds_read64<2 * 16 * 2 * QB + QB>(st + boff0);
+        raw[3][0] = lds_read64<3 * 16 * 2 * QB>(st + boff0);
+        raw[3][1] = lds_read64<3 * 16 * 2 * QB + QB>(st + boff0);
+        // column tiles j and j + 2 are 32 columns apart: the next 256-byte scale group
+        sc[0] = lds_read32<0>(st + soff0);
+        sc[1] = lds_read32<64>(st + soff0);
+        sc[2] = lds_read32<256>(st + soff0);
+        sc[3] = lds_read32<256 + 64>(st + soff0);
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(raw[0][0]), "+v"(raw[0][1]), "+v"(raw[1][0]), "+v"(raw[1][1]),
+                       "+v"(raw[2][0]), "+v"(raw[2][1]), "+v"(raw[3][0]), "+v"(raw[3][1]),
+                       "+v"(sc[0]), "+v"(sc[1]), "+v"(sc[2]), "+v"(sc[3]));
+        const bool b1ok = 2 * ks + 1 < KB;
+        float d0[TJ], d1[TJ];
 #pragma unroll
-    for (int d = 0; d < D; ++d) load_b(sb[d], min(d, ksteps - 1));
-    auto step = [&](BStage<TJ>& b_, int ks, bool more_a, bool more_b) {
-        store_a(sa, ks, ks & 1);
-        dequant_b(b_, ks);
-        if (more_a) load_a(sa, ks + 1);
-        // A's loads stay older than B's: the wait for A next step then leaves
-        // B's D-step-ahead loads in flight (vmcnt counts in issue order)
-        __builtin_amdgcn_sched_barrier(0);
-        if (more_b) load_b(b_, ks + D);
-        __syncthreads();
-        mfma_step(ks & 1);
-    };
-    int k0 = 0;
-    for (; k0 + 2 * D <= ksteps; k0 += D) {
+        for (int j = 0; j < TJ; ++j) {
+            d0[j] = bval[j] ? __half2float(__ushort_as_half((uint16_t)sc[j])) : 0.0f;
+            d1[j] = bval[j] && b1ok ? __half2float(__ushort_as_half((uint16_t)(sc[j] >> 16)))
+                                    : 0.0f;
+        }
+        // block 0's fragments first; block 1's are dequantized between the MFMAs of
+        // the first 32 k (one column tile after every TI / TJ row tiles), so the
+        // VALU work overlaps the matrix cores instead of following them
+        bf16x8 bfrag[TJ][2];
 #pragma unroll
-        for (int d = 0; d < D; ++d) step(sb[d], k0 + d, true, true);
+        for (int j = 0; j < TJ; ++j) bfrag[j][0] = dequant8<QT>(raw[j][0], bshift, d0[j]);
+        // A fragments, one ahead: fragment f = kk * TI + i at aoff[kk] + 2048 i
+        bf16x8 afr[2 * TI];
+        afr[0] = lds_read128<0>(st + aoff[0]);
+#pragma unroll
+        for (int f = 0; f < 2 * TI; ++f) {
+            if (f + 1 < 2 * TI) {
+                constexpr_for<2 * TI>([&](auto F) {
+                    if (F.value == f + 1)
+                        afr[F.value] = lds_read128<(F.value % TI) * 2048>(st + aoff[F.value / TI]);
+                });
+                asm volatile("s_waitcnt lgkmcnt(1)" : "+v"(afr[f]));
+            } else {
+                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(afr[f]));
+            }
+            const int kk = f / TI, i = f % TI;
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr[f], bfrag[j][kk], acc[i][j],
+                                                                    0, 0, 0);
+            if (kk == 0 && (i + 1) % (TI / TJ) == 0) {
+                const int j = (i + 1) / (TI / TJ) - 1;
+                bfrag[j][1] = dequant8<QT>(raw[j][1], bshift, d1[j]);
+            }
+        }
     }
-    // tail: fewer than 2 D steps left
-#pragma unroll
-    for (int d = 0; d < D; ++d)
-        if (k0 + d < ksteps) step(sb[d], k0 + d, k0 + d + 1 < ksteps, k0 + d + D < ksteps);
-#pragma unroll
-    for (int d = 0; d < D; ++d)
-        if (k0 + D + d < ksteps) step(sb[d], k0 + D + d, k0 + D + d + 1 < ksteps, false);
 
     // ---- epilogue: lane holds C[4 (l / 16) + e][l % 16] of each 16 x 16 tile ----
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
-        const int col = nt * PBN + wv * WC + j * 16 + fr;
+        const int col = n0 + WC * cw + 16 * j + fr;
         if (col >= N) continue;
 #pragma unroll
         for (int i = 0; i < TI; ++i)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int row = m0 + 16 * i + 4 * (lane / 16) + e;
+                const int row = m0 + WR * rw + 16 * i + 4 * g + e;
                 if (row < M) y[(int64_t)row * N + col] = acc[i][j][e];
             }
     }
@@ -289,11 +391,17 @@ hipError_t launch_bm(const QWeight& w, const __bf16* xb, int64_t m, float* y, hi
         }
         return hipSuccess;
     }
+    static bool attr = [] {
+        return hipFuncSetAttribute((const void*)prefill_kernel<QT, BM, kWaves>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   Ring<QT, BM>::BYTES) == hipSuccess;
+    }();
+    if (!attr) return hipErrorInvalidValue;
     const int tiles_m = (int)((m + BM - 1) / BM);
     const int tiles_n = (int)((w.n + PBN - 1) / PBN);
     const int tiles = tiles_m * tiles_n;
     const int tiles_pad = (tiles + 7) / 8 * 8;
-    prefill_kernel<QT, BM, kWaves, kDepth><<<tiles_pad, kWaves * 64, 0, s>>>(
+    prefill_kernel<QT, BM, kWaves><<<tiles_pad, kWaves * 64, Ring<QT, BM>::BYTES, s>>>(
         w.base, w.row_bytes, xb, y, (int)m, (int)w.n, (int)w.kb, tiles_n, tiles, tiles_pad);
     return hipGetLastError();
 }

@@ -43,6 +43,7 @@
 #include <utility>
 
 #include "internal.hpp"
+#include "lds.hpp"
 
 namespace unillm {
 namespace {
@@ -141,48 +142,6 @@ struct Ring {
     static constexpr int AQ = BM / 8 / 8;              // A loads (8 rows each) per wave
     static constexpr int DMA = AQ + CPB / 2 + 1;       // direct loads per wave per stage
 };
-
-// Calls f(integral_constant<int, I>) for I = 0 .. N - 1 (compile-time indices).
-template <int N, class F, int... I>
-__device__ __forceinline__ void constexpr_for_impl(F&& f, std::integer_sequence<int, I...>) {
-    (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, class F>
-__device__ __forceinline__ void constexpr_for(F&& f) {
-    constexpr_for_impl<N>(f, std::make_integer_sequence<int, N>{});
-}
-
-typedef __attribute__((address_space(3))) void* lds_ptr;
-typedef const __attribute__((address_space(1))) void* gbl_ptr;
-
-__device__ __forceinline__ void dma16(const void* g, uint8_t* l) {
-    __builtin_amdgcn_global_load_lds((gbl_ptr)g, (lds_ptr)l, 16, 0, 0);
-}
-__device__ __forceinline__ void dma4(const void* g, uint8_t* l) {
-    __builtin_amdgcn_global_load_lds((gbl_ptr)g, (lds_ptr)l, 4, 0, 0);
-}
-
-// LDS reads the compiler does not see (so it adds no wait for the direct loads
-// before them); lds_wait<N>() waits until at most N of this wave's LDS reads are
-// outstanding and ties the given registers to that point.
-template <int OFF>
-__device__ __forceinline__ bf16x8 lds_read128(uint32_t addr) {
-    bf16x8 v;
-    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
-    return v;
-}
-template <int OFF>
-__device__ __forceinline__ u32x2 lds_read64(uint32_t addr) {
-    u32x2 v;
-    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
-    return v;
-}
-template <int OFF>
-__device__ __forceinline__ uint32_t lds_read32(uint32_t addr) {
-    uint32_t v;
-    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
-    return v;
-}
 
 template <int QT, int BM, int NW>
 __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __restrict__ base,
@@ -294,12 +253,9 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
 
     for (int ks = 0; ks < ksteps; ++ks) {
         // wait for this wave's loads of step ks: the loads of later steps already
-        // issued (at most kStages - 2 of them) may stay in flight.  s_waitcnt on
-        // gfx950: vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 at their
-        // maxima (no wait)
-        constexpr int kWaitLater = 0x0F70 | (R::DMA & 0xF) | (((R::DMA >> 4) & 3) << 14);
-        if (ks + 1 < ksteps) __builtin_amdgcn_s_waitcnt(kWaitLater);
-        else __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        // issued (at most kStages - 2 of them) may stay in flight
+        if (ks + 1 < ksteps) wait_vmcnt<R::DMA>();
+        else wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
         if (ks + kStages - 1 < ksteps) issue(ks + kStages - 1);
 
@@ -308,14 +264,14 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
         u32x2 raw[TJ][2];
         uint32_t sc[TJ];
         static_assert(TJ == 4, "unrolled for four column tiles");
-        raw[0][0] = lds_read64<0 * 16 * 2 * QB>(st + boff0);
-        raw[0][1] = lds_read64<0 * 16 * 2 * QB + QB>(st + boff0);
-        raw[1][0] = lds_read64<1 * 16 * 2 * QB>(st + boff0);
-        raw[1][1] = lds_read64<1 * 16 * 2 * QB + QB>(st + boff0);
-        raw[2][0] = lds_read64<2 * 16 * 2 * QB>(st + boff0);
-        raw[2][1] = lds_read64<2 * 16 * 2 * QB + QB>(st + boff0);
-        raw[3][0] = lds_read64<3 * 16 * 2 * QB>(st + boff0);
-        raw[3][1] = lds_read64<3 * 16 * 2 * QB + QB>(st + boff0);
+        raw[0][0] = (u32x2)lds_read64<0 * 16 * 2 * QB>(st + boff0);
+        raw[0][1] = (u32x2)lds_read64<0 * 16 * 2 * QB + QB>(st + boff0);
+        raw[1][0] = (u32x2)lds_read64<1 * 16 * 2 * QB>(st + boff0);
+        raw[1][1] = (u32x2)lds_read64<1 * 16 * 2 * QB + QB>(st + boff0);
+        raw[2][0] = (u32x2)lds_read64<2 * 16 * 2 * QB>(st + boff0);
+        raw[2][1] = (u32x2)lds_read64<2 * 16 * 2 * QB + QB>(st + boff0);
+        raw[3][0] = (u32x2)lds_read64<3 * 16 * 2 * QB>(st + boff0);
+        raw[3][1] = (u32x2)lds_read64<3 * 16 * 2 * QB + QB>(st + boff0);
         // column tiles j and j + 2 are 32 columns apart: the next 256-byte scale group
         sc[0] = lds_read32<0>(st + soff0);
         sc[1] = lds_read32<64>(st + soff0);
@@ -341,13 +297,14 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
         for (int j = 0; j < TJ; ++j) bfrag[j][0] = dequant8<QT>(raw[j][0], bshift, d0[j]);
         // A fragments, one ahead: fragment f = kk * TI + i at aoff[kk] + 2048 i
         bf16x8 afr[2 * TI];
-        afr[0] = lds_read128<0>(st + aoff[0]);
+        afr[0] = __builtin_bit_cast(bf16x8, lds_read128<0>(st + aoff[0]));
 #pragma unroll
         for (int f = 0; f < 2 * TI; ++f) {
             if (f + 1 < 2 * TI) {
                 constexpr_for<2 * TI>([&](auto F) {
                     if (F.value == f + 1)
-                        afr[F.value] = lds_read128<(F.value % TI) * 2048>(st + aoff[F.value / TI]);
+                        afr[F.value] = __builtin_bit_cast(
+                            bf16x8, lds_read128<(F.value % TI) * 2048>(st + aoff[F.value / TI]));
                 });
                 asm volatile("s_waitcnt lgkmcnt(1)" : "+v"(afr[f]));
             } else {

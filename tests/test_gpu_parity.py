@@ -251,9 +251,18 @@ def test_forward_argument_errors():
 
 
 def test_repeat_calls_deterministic():
-    blocks, x = _case(Q4_0, 16, 4096, 4096, seed=9)
-    ql = QuantLinear.from_blocks(Q4_0, 4096, 4096, blocks)
-    xd = _dev(x)
-    a = ql.forward(xd).cpu().numpy()
-    for _ in range(3):
-        assert np.array_equal(ql.forward(xd).cpu().numpy(), a)
+    # GEMV (m <= 4) and prefill compute every output in one fixed order: bitwise
+    # repeatable.  Batched decode splits k over workgroups whose partial sums
+    # meet in y by f32 atomic adds, so the order of those few adds (at most 4)
+    # can vary between calls: repeatable to f32 rounding, not bitwise.
+    for m, exact in ((1, True), (130, True), (16, False), (64, False)):
+        blocks, x = _case(Q4_0, m, 4096, 4096, seed=9)
+        ql = QuantLinear.from_blocks(Q4_0, 4096, 4096, blocks)
+        xd = _dev(x)
+        a = ql.forward(xd).cpu().numpy()
+        for _ in range(3):
+            b = ql.forward(xd).cpu().numpy()
+            if exact:
+                assert np.array_equal(b, a), m
+            else:
+                assert oracle.normwise_error(b, a) < 1e-6, m

@@ -4,9 +4,11 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <new>
 #include <string>
+#include <unordered_map>
 
 #include <hip/hip_fp16.h>
 #include <math.h>
@@ -50,8 +52,10 @@ int do_init(int device) {
     if ((e = hipSetDevice(device)) != hipSuccess) return fail_hip(e, "hipSetDevice");
     g_info.cu_count = prop.multiProcessorCount;
     g_info.max_lds = (int)prop.sharedMemPerBlock;
-    // the prefill path takes its bf16 copy of x from the stream-ordered pool:
-    // keep freed memory in the pool between calls instead of returning it
+    g_info.max_lds_cu = (int)prop.maxSharedMemoryPerMultiProcessor;
+    if (g_info.max_lds_cu <= 0) g_info.max_lds_cu = 160 * 1024;
+    // workspaces come from the stream-ordered pool: keep freed memory in the
+    // pool instead of returning it
     hipMemPool_t pool;
     if (hipDeviceGetDefaultMemPool(&pool, device) == hipSuccess) {
         uint64_t keep = UINT64_MAX;
@@ -140,9 +144,42 @@ int finish_weight(QWeight* w, hipStream_t s) {
     return UNILLM_OK;
 }
 
+// stream -> workspace: see stream_workspace
+struct StreamWs {
+    void* buf = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+std::unordered_map<hipStream_t, StreamWs> g_ws;
+
 }  // namespace
 
 const DeviceInfo& device_info() { return g_info; }
+
+hipError_t stream_workspace(hipStream_t s, size_t bytes, void** out) {
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    StreamWs& w = g_ws[s];
+    if (w.bytes < bytes) {
+        // grow in stream order: earlier work on s that uses the old buffer runs
+        // before the free, later work uses the new one
+        if (w.buf) {
+            hipError_t e = hipFreeAsync(w.buf, s);
+            w.buf = nullptr;
+            w.bytes = 0;
+            if (e != hipSuccess) return e;
+        }
+        const size_t want = std::max(bytes, (size_t)1 << 20);
+        hipError_t e = hipMallocAsync(&w.buf, want, s);
+        if (e != hipSuccess) {
+            w.buf = nullptr;
+            return e;
+        }
+        w.bytes = want;
+    }
+    *out = w.buf;
+    return hipSuccess;
+}
+
 
 bool debug_launch() {
     static const bool on = [] {

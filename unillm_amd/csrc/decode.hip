@@ -1,30 +1,41 @@
-// decode.hip -- batched decode (5 <= m <= 64): fused dequant + f16 MFMA.
+// decode.hip -- batched decode (m <= 64 off the GEMV path): fused dequant + f16 MFMA.
 //
 // y[m, n] = x[m, k] . dequant(W)[n, k]^T for continuous-batching widths, the
 // QMatMul::forward call of llama.rs:1188 / 1329 with a few tokens per step.
-// Bound: HBM for the weights (each byte read once) with the dequant VALU
-// close behind; the tokens are few, so the matrix cores have slack.
+// Bound: HBM for the weights (each byte read once).  The dequant VALU and the
+// matrix cores share the rest of the time; x is re-read from L2 by every row
+// group, so a workgroup owns enough rows to keep that below the weight bytes.
 //
-// Orientation: the weights are the MFMA A operand (16 weight rows x 32 k, one
-// Q4_0 / Q8_0 block per row and fragment) and the tokens the B operand, so
-// C = W . x^T is [16 rows][16 tokens] per tile (v_mfma_f32_16x16x32_f16).
-//   - A workgroup of 4 waves owns 64 weight rows; wave w owns rows 16 w ..
-//     16 w + 15 over all of k.  Each lane loads exactly the 8 payload bytes
-//     behind its A fragment (row l % 16, elements 8 (l / 16) .. +7 of the
-//     block) and the row's scales, three 256-k chunks ahead, and dequantizes them
-//     in registers to f16 with packed f16 arithmetic:
-//       (code | 0x6400) is the f16 1024 + code (exact), minus 1024 + offset
-//       gives the signed code exactly, times d 2^-E rounds once
-//     -- the same single rounding as (q - 8) d 2^-E computed in fp32 and
-//     rounded to f16.  Codes are taken two at a time from bytes (0, 2) and
-//     (1, 3) of a dword, so a fragment holds its 8 elements in the order
-//     0 2 1 3 4 6 5 7; x is staged in that same order, which leaves every dot
-//     product unchanged.
-//   - x (f32) is rounded to f16 and staged per 256-k chunk in LDS, shared by
-//     the workgroup's 4 waves (double-buffered, loaded one chunk ahead).
-//   - E is the weight's f16 exponent offset (8 max|d| 2^-E <= 65504), undone
-//     on the output: both scalings are exact.
-// Normwise error vs the f64 oracle ~3e-4 (f16 operands; bound 1e-3).
+// Two kernels on the caller's stream:
+//   1. xprep_kernel rounds x to f16 (round to nearest even) into a stream-ordered
+//      workspace, each aligned group of 8 k stored in the order 0 2 1 3 4 6 5 7
+//      (the order the dequant below produces), and zeroes y when k is split.
+//   2. decode_kernel: v_mfma_f32_32x32x16_f16 with the tokens as the A operand
+//      (32 tokens x 16 k) and the weights as B (16 k x 32 weight rows), so a
+//      lane's accumulator column is one weight row and the output stores and
+//      atomics are 128-byte rows.
+//        - A workgroup (4 waves) owns 128 weight rows and a contiguous slice of
+//          the k chunks (64 k = 2 blocks each); the k range is split over S
+//          workgroups when the row groups alone cannot fill the chip, and the S
+//          partial sums meet in y by f32 atomic adds.
+//        - Every operand comes through a D-stage LDS ring filled by direct
+//          global -> LDS loads (no VGPRs): the chunk's x rows (f16), its weight
+//          payloads (2 blocks per row) and its f16 scales.  Step j waits for
+//          its own chunk (exact vmcnt: younger chunks stay in flight), meets
+//          the other waves, issues chunk j + D - 1 and computes chunk j.
+//        - Dequant, per lane and block: Q4_0 -- 8 payload bytes (16 signed
+//          nibbles, flipped back to q) become two B fragments, the low nibbles
+//          (elements 8h .. 8h + 7) and the high nibbles (16 + 8h ..), h = lane / 32;
+//          Q8_0 -- 16 bytes (elements 16h .. 16h + 15) become two fragments.
+//          (code | 0x6400) is the f16 1024 + code exactly; minus 1024 + offset
+//          gives the signed code exactly, times d 2^-E rounds once -- the same
+//          single rounding as (q - 8) d 2^-E computed in f32 and rounded to f16.
+//          Codes go two at a time from bytes (0, 2) and (1, 3) of a dword, hence
+//          the element order 0 2 1 3 within each 8, matched by x's layout.
+//   E is the weight's f16 exponent offset (8 max|d| 2^-E <= 65504), undone on
+//   the output: both scalings are exact.
+// Normwise error vs the f64 oracle ~3e-4 (f16 operands, f32 accumulation;
+// bound 1e-3).  x must lie in the f16 range (|x| <= 65504).
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
@@ -37,11 +48,12 @@ namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int DROWS = 64;       // weight rows per workgroup (4 waves x 16)
+constexpr int DROWS = 128;  // weight rows per workgroup (4 waves x 32)
+constexpr int DCK = 128;    // k per chunk (4 blocks)
 
 __device__ __forceinline__ uint32_t pk_f16(float a, float b) {
     uint32_t r;  // round to nearest even, a in the low half
@@ -49,207 +61,404 @@ __device__ __forceinline__ uint32_t pk_f16(float a, float b) {
     return r;
 }
 
-// Two codes (bytes 0 and 2 of `sel`, already masked to the code bits) -> f16 pair
-// (code - bias) * dh: 0x6400 | code is 1024 + code exactly.
-__device__ __forceinline__ uint32_t codes2(uint32_t sel, f16x2 bias, f16x2 dh) {
-    const f16x2 v = __builtin_bit_cast(f16x2, sel | 0x64006400u);
-    return __builtin_bit_cast(uint32_t, (v - bias) * dh);
+// (a & mask) | bits in one instruction (the compiler splits it in two).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(bits));
+    return r;
 }
 
-// One lane's A fragment of one block: 8 bytes of payload -> 8 f16 in the order
-// 0 2 1 3 4 6 5 7.  Q4_0: nibbles at bit offset `shift` of each byte (signed
-// codes stored as q - 8, flipped back to q); Q8_0: whole bytes (flipped to q + 128).
-template <int QT>
-__device__ __forceinline__ f16x8 dequant_frag(u32x2 raw, int shift, f16x2 dh) {
-    constexpr uint32_t kFlip = QT == UNILLM_QTYPE_Q4_0 ? 0x88888888u : 0x80808080u;
-    constexpr uint32_t kMask = QT == UNILLM_QTYPE_Q4_0 ? 0x000F000Fu : 0x00FF00FFu;
-    const _Float16 b = QT == UNILLM_QTYPE_Q4_0 ? (_Float16)1032.0f : (_Float16)1152.0f;
-    const f16x2 bias = {b, b};
-    u32x4 out;
+// f16 pair (v - bias) * dh, v holding two f16 1024 + code: exact but the last step.
+__device__ __forceinline__ uint32_t scale2(uint32_t v, f16x2 bias, f16x2 dh) {
+    return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, v) - bias) * dh);
+}
+
+// Q4_0: 8 payload bytes (signed nibbles of elements 8h .. 8h + 7 low, 16 + 8h .. high)
+// -> lo / hi fragments, each in the order 0 2 1 3 4 6 5 7.
+__device__ __forceinline__ void dequant_q4(u32x2 raw, f16x2 dh, f16x8& lo, f16x8& hi) {
+    const f16x2 bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+    const uint32_t magic = 0x64006400u;
+    u32x4 l, h;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const uint32_t w = (raw[h] ^ kFlip) >> shift;
-        out[2 * h] = codes2(w & kMask, bias, dh);               // bytes 0, 2
-        out[2 * h + 1] = codes2((w >> 8) & kMask, bias, dh);    // bytes 1, 3
+    for (int d = 0; d < 2; ++d) {
+        const uint32_t w = raw[d] ^ 0x88888888u;  // signed nibble -> q
+        l[2 * d] = scale2(and_or(w, 0x000F000Fu, magic), bias, dh);            // bytes 0, 2 low
+        l[2 * d + 1] = scale2(and_or(w >> 8, 0x000F000Fu, magic), bias, dh);   // bytes 1, 3 low
+        h[2 * d] = scale2(and_or(w >> 4, 0x000F000Fu, magic), bias, dh);       // bytes 0, 2 high
+        h[2 * d + 1] = scale2(and_or(w >> 12, 0x000F000Fu, magic), bias, dh);  // bytes 1, 3 high
     }
-    return __builtin_bit_cast(f16x8, out);
+    lo = __builtin_bit_cast(f16x8, l);
+    hi = __builtin_bit_cast(f16x8, h);
 }
 
-// x ring: S stages of one 128-k chunk of TOK token rows in f32 (512 B per row),
-// filled by direct global -> LDS loads (a 1 KiB load covers two rows).  The
-// 16-byte chunk c of row r sits in slot c ^ (r % 16), so the 16 rows a
-// fragment read touches fall on distinct banks.
-constexpr int DKC = 128;  // k per chunk (4 blocks)
-constexpr int DS = 3;     // stages: chunks ch + 1, ch + 2 in flight while ch is used
+// Q8_0: 16 payload bytes (elements 16h .. 16h + 15) -> two fragments (elements
+// 16h .. +7 and 16h + 8 .. +7), each in the order 0 2 1 3 4 6 5 7.
+__device__ __forceinline__ void dequant_q8(u32x4 raw, f16x2 dh, f16x8& f0, f16x8& f1) {
+    const f16x2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const uint32_t magic = 0x64646464u;
+    u32x4 a, b;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const uint32_t w = raw[d] ^ 0x80808080u;  // int8 -> q + 128
+        // bytes (0, 2) and (1, 3) each under a 0x64 byte: f16 1024 + byte
+        const uint32_t p02 = __builtin_amdgcn_perm(magic, w, 0x04020400u);
+        const uint32_t p13 = __builtin_amdgcn_perm(magic, w, 0x04030401u);
+        u32x4& o = d < 2 ? a : b;
+        o[2 * (d & 1)] = scale2(p02, bias, dh);
+        o[2 * (d & 1) + 1] = scale2(p13, bias, dh);
+    }
+    f0 = __builtin_bit_cast(f16x8, a);
+    f1 = __builtin_bit_cast(f16x8, b);
+}
 
-template <int MT>
-struct XRing {
-    static constexpr int TOK = MT * 16;
-    static constexpr int STAGE = TOK * DKC * 4;
-    static constexpr int BYTES = DS * STAGE;
-    static constexpr int DMA = TOK * DKC * 4 / 1024 / 4;  // direct loads per wave per chunk
+// x (f32 [m, k]) -> f16 in the fragment order; y[0, ny) <- 0 (a split k range
+// adds into it).
+__global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x,
+                                                    uint4* __restrict__ xh, int64_t n8,
+                                                    float* __restrict__ y, int64_t ny) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += stride) {
+        const float4 a = reinterpret_cast<const float4*>(x)[2 * i];
+        const float4 b = reinterpret_cast<const float4*>(x)[2 * i + 1];
+        xh[i] = make_uint4(pk_f16(a.x, a.z), pk_f16(a.y, a.w), pk_f16(b.x, b.z), pk_f16(b.y, b.w));
+    }
+    // y: scalar stores up to a 16-byte boundary, then float4, then the tail
+    const int64_t head = std::min<int64_t>(ny, (int64_t)((16 - ((uintptr_t)y & 15)) & 15) / 4);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < head; i += stride) y[i] = 0.0f;
+    float4* y4 = reinterpret_cast<float4*>(y + head);
+    const int64_t n4 = (ny - head) / 4;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride)
+        y4[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int64_t i = head + 4 * n4 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < ny; i += stride)
+        y[i] = 0.0f;
+}
+
+// LDS: a D-stage ring, each stage one 128-k chunk of
+//   x   [TOK rows][256 B] f16; the 16-byte group g of row r sits in slot g ^ (r % 8);
+//   W   [128 rows][4 QB] payloads of the chunk's 4 blocks; the 16-byte piece c
+//       of row r sits in slot c ^ swz(r) (Q4_0 (r / 2) % 4, Q8_0 r % 8),
+// then the workgroup's k-slice scales, per wave [32 rows][8 nch B] (at most
+// kMaxSliceChunks chunks: 2 KiB a wave), loaded once before the ring starts.
+// The swizzles spread an MFMA fragment's 16 rows / 8 tokens over distinct banks.
+constexpr int kMaxSliceChunks = 8;
+#ifndef DECODE_MAX_SPLIT
+#define DECODE_MAX_SPLIT 4
+#endif
+// at most this many k slices add into one output (more slices contend on the
+// same y lines with their atomics)
+constexpr int kMaxSplit = DECODE_MAX_SPLIT;
+
+template <int QT, int MT2>
+struct Stage {
+    static constexpr int QB = QT == UNILLM_QTYPE_Q4_0 ? 16 : 32;
+    static constexpr int TOK = 32 * MT2;
+    static constexpr int X = TOK * 256;
+    static constexpr int P = DROWS * 4 * QB;
+    static constexpr int BYTES = X + P;
+    static constexpr int XD = TOK * 256 / 1024 / 4;  // x direct loads per wave per chunk
+    static constexpr int PD = 32 * 4 * QB / 1024;    // payload direct loads per wave (2 / 4)
+    static constexpr int LPC = XD + PD;
+    static constexpr int LPR = 4 * QB / 16;          // payload lanes per row (4 / 8)
+    static constexpr int RPI = 64 / LPR;             // payload rows per direct load
+    static constexpr int SCALES = 4 * 32 * 8 * kMaxSliceChunks;
+    // depth: as deep as keeps two workgroups per CU, where the stage allows
+    static constexpr int D = BYTES <= 16384 ? 4 : 3;
+    static constexpr int LDS = D * BYTES + SCALES;
 };
 
-template <int QT, int MT>
+// s_waitcnt vmcnt(rem * LPC) for a wave-uniform rem in [0, R].
+template <int LPC, int R>
+__device__ __forceinline__ void wait_chunks(int rem) {
+    if constexpr (R == 0) {
+        wait_vmcnt<0>();
+    } else {
+        if (rem >= R) wait_vmcnt<R * LPC>();
+        else wait_chunks<LPC, R - 1>(rem);
+    }
+}
+
+// The LDS reads for two blocks of a chunk and the wait for them in ONE asm
+// statement: the outputs are early-clobber and defined only once the statement
+// ends, so the compiler cannot copy a destination register before its data has
+// landed (with separate asm reads it may, and the copy reads a stale register).
+//   x: for each block the two fragment groups (a0, a1 | a2, a3), tile 1 at +8192;
+//   payload: Q4_0 8 bytes, Q8_0 16 bytes per block (p0, p1); the chunk's four
+//   f16 scales (8 bytes at sa).
+#define UNILLM_DS128(o, a, off) "ds_read_b128 %" #o ", %" #a " offset:" #off "\n"
+#define UNILLM_DS64(o, a, off) "ds_read_b64 %" #o ", %" #a " offset:" #off "\n"
+template <bool Q4, int MT2>
+__device__ __forceinline__ void read_pair(lds_u32x4 (&xa)[MT2][4], u32x4 (&pw)[2],
+                                          lds_u32x2& scp, uint32_t a0, uint32_t a1, uint32_t a2,
+                                          uint32_t a3, uint32_t p0, uint32_t p1, uint32_t sa) {
+    if constexpr (Q4 && MT2 == 1) {
+        lds_u32x2 w0, w1;
+        asm volatile(UNILLM_DS128(0, 7, 0) UNILLM_DS128(1, 8, 0) UNILLM_DS128(2, 9, 0)
+                         UNILLM_DS128(3, 10, 0) UNILLM_DS64(4, 11, 0) UNILLM_DS64(5, 12, 0)
+                             UNILLM_DS64(6, 13, 0) "s_waitcnt lgkmcnt(0)"
+                     : "=&v"(xa[0][0]), "=&v"(xa[0][1]), "=&v"(xa[0][2]), "=&v"(xa[0][3]),
+                       "=&v"(w0), "=&v"(w1), "=&v"(scp)
+                     : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(p0), "v"(p1), "v"(sa));
+        pw[0] = u32x4{w0[0], w0[1], 0u, 0u};
+        pw[1] = u32x4{w1[0], w1[1], 0u, 0u};
+    } else if constexpr (Q4) {
+        lds_u32x2 w0, w1;
+        asm volatile(UNILLM_DS128(0, 11, 0) UNILLM_DS128(1, 12, 0) UNILLM_DS128(2, 13, 0)
+                         UNILLM_DS128(3, 14, 0) UNILLM_DS128(4, 11, 8192) UNILLM_DS128(5, 12, 8192)
+                             UNILLM_DS128(6, 13, 8192) UNILLM_DS128(7, 14, 8192)
+                                 UNILLM_DS64(8, 15, 0) UNILLM_DS64(9, 16, 0)
+                                     UNILLM_DS64(10, 17, 0) "s_waitcnt lgkmcnt(0)"
+                     : "=&v"(xa[0][0]), "=&v"(xa[0][1]), "=&v"(xa[0][2]), "=&v"(xa[0][3]),
+                       "=&v"(xa[MT2 - 1][0]), "=&v"(xa[MT2 - 1][1]), "=&v"(xa[MT2 - 1][2]),
+                       "=&v"(xa[MT2 - 1][3]), "=&v"(w0), "=&v"(w1), "=&v"(scp)
+                     : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(p0), "v"(p1), "v"(sa));
+        pw[0] = u32x4{w0[0], w0[1], 0u, 0u};
+        pw[1] = u32x4{w1[0], w1[1], 0u, 0u};
+    } else if constexpr (MT2 == 1) {
+        lds_u32x4 w0, w1;
+        asm volatile(UNILLM_DS128(0, 7, 0) UNILLM_DS128(1, 8, 0) UNILLM_DS128(2, 9, 0)
+                         UNILLM_DS128(3, 10, 0) UNILLM_DS128(4, 11, 0) UNILLM_DS128(5, 12, 0)
+                             UNILLM_DS64(6, 13, 0) "s_waitcnt lgkmcnt(0)"
+                     : "=&v"(xa[0][0]), "=&v"(xa[0][1]), "=&v"(xa[0][2]), "=&v"(xa[0][3]),
+                       "=&v"(w0), "=&v"(w1), "=&v"(scp)
+                     : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(p0), "v"(p1), "v"(sa));
+        pw[0] = __builtin_bit_cast(u32x4, w0);
+        pw[1] = __builtin_bit_cast(u32x4, w1);
+    } else {
+        lds_u32x4 w0, w1;
+        asm volatile(UNILLM_DS128(0, 11, 0) UNILLM_DS128(1, 12, 0) UNILLM_DS128(2, 13, 0)
+                         UNILLM_DS128(3, 14, 0) UNILLM_DS128(4, 11, 8192) UNILLM_DS128(5, 12, 8192)
+                             UNILLM_DS128(6, 13, 8192) UNILLM_DS128(7, 14, 8192)
+                                 UNILLM_DS128(8, 15, 0) UNILLM_DS128(9, 16, 0)
+                                     UNILLM_DS64(10, 17, 0) "s_waitcnt lgkmcnt(0)"
+                     : "=&v"(xa[0][0]), "=&v"(xa[0][1]), "=&v"(xa[0][2]), "=&v"(xa[0][3]),
+                       "=&v"(xa[MT2 - 1][0]), "=&v"(xa[MT2 - 1][1]), "=&v"(xa[MT2 - 1][2]),
+                       "=&v"(xa[MT2 - 1][3]), "=&v"(w0), "=&v"(w1), "=&v"(scp)
+                     : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(p0), "v"(p1), "v"(sa));
+        pw[0] = __builtin_bit_cast(u32x4, w0);
+        pw[1] = __builtin_bit_cast(u32x4, w1);
+    }
+}
+#undef UNILLM_DS128
+#undef UNILLM_DS64
+
+template <int QT, int MT2>
 __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__ base, int64_t rb,
-                                                     const float* __restrict__ x,
+                                                     const _Float16* __restrict__ xh,
                                                      float* __restrict__ y, int M, int N, int KB,
-                                                     float wscale, float oscale) {
-    constexpr int QB = QT == UNILLM_QTYPE_Q4_0 ? 16 : 32;  // payload bytes per block
-    using XR = XRing<MT>;
-    constexpr int LPC = XR::DMA + 5;  // a wave's loads per chunk: x + 4 payloads + scales
-    extern __shared__ __attribute__((aligned(16))) uint8_t xring[];
+                                                     int S, float wscale, float oscale) {
+    using ST = Stage<QT, MT2>;
+    constexpr int QB = ST::QB, D = ST::D, LPC = ST::LPC;
+    constexpr bool Q4 = QT == UNILLM_QTYPE_Q4_0;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    uint8_t* const ring = lds;
+    uint8_t* const scl = lds + D * ST::BYTES;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int g = lane / 16, fr = lane % 16;
+    const int h = lane >> 5, col = lane & 31;
     const uint32_t K = (uint32_t)KB * QK;
+
+    // workgroup -> (row group, k slice); the slice is chunks [c0, c1), at most
+    // kMaxSliceChunks of them (the host picks S so)
+    const int rg = blockIdx.x / S, sp = blockIdx.x % S;
     const int chunks = (KB + 3) / 4;
+    const int c0 = (int)((int64_t)sp * chunks / S), c1 = (int)((int64_t)(sp + 1) * chunks / S);
+    const int nch = c1 - c0;
+    const int row0 = rg * DROWS + 32 * wv;  // this wave's 32 weight rows
+    const uint32_t sbase = (uint32_t)KB * QB;  // the scales follow the payloads in a row
 
-    // ---- weights: row 64 blockIdx + 16 wv + fr; bytes 8 (g & 1) .. +7 of each block
-    // (Q4_0, nibble shift 4 (g >> 1)) or 8 g .. +7 (Q8_0).  32-bit byte offsets.
-    const int row = blockIdx.x * DROWS + wv * 16 + fr;
-    const bool rval = row < N;
-    const uint32_t roff = (uint32_t)min(row, N - 1) * (uint32_t)rb;
-    const uint32_t boff = QT == UNILLM_QTYPE_Q4_0 ? 8 * (g & 1) : 8 * g;
-    const int bshift = QT == UNILLM_QTYPE_Q4_0 ? 4 * (g >> 1) : 0;
-    const uint32_t sbase = (uint32_t)KB * QB;
-
-    // ---- x: this wave's direct loads q = XR::DMA wv .. : rows 2 q + lane / 32, slot
-    // lane % 32 <- global chunk (lane % 32) ^ (row % 16).  Rows past m read row m - 1
-    // and k past K the row's last chunk (finite values against zero weights).
-    uint32_t xrow[XR::DMA], xchunk[XR::DMA];
-#pragma unroll
-    for (int q = 0; q < XR::DMA; ++q) {
-        const int r = 2 * (XR::DMA * wv + q) + lane / 32;
-        xrow[q] = (uint32_t)min(r, M - 1) * K;
-        xchunk[q] = (uint32_t)(((lane % 32) ^ (r % 16)) * 4);
+    // ---- the slice's scales: 8 nch bytes a row, nch dword loads per wave; lane
+    // -> flat dword f = 64 i + lane = row r, dword f % (2 nch) (past the last
+    // block: the row's padding, the next row or the tail slot; zeroed below) ----
+    for (int i = 0; i < nch; ++i) {
+        const int f = 64 * i + lane;
+        const int r = f / (2 * nch), dw = f - r * (2 * nch);
+        const uint32_t g = (uint32_t)min(row0 + r, N - 1) * (uint32_t)rb + sbase +
+                           8u * (uint32_t)c0 + 4u * (uint32_t)dw;
+        dma4(base + g, scl + wv * 2048 + i * 256);
     }
 
-    struct WChunk {
-        u32x2 p[4];  // the 4 blocks' fragment bytes
-        u32x2 s;     // the 4 blocks' f16 scales
+    // ---- per-chunk direct-load sources (32-bit offsets; the host checks sizes) ----
+    // x: load q = XD wv + i covers token rows 4q .. 4q + 3; lane -> row 4q + lane / 16,
+    // slot lane % 16 <- group (lane % 16) ^ (row % 8).  Rows past m read row m - 1
+    // and k past K the row's last group (finite values against zero weights).
+    uint32_t xoff[ST::XD], xgrp[ST::XD];
+#pragma unroll
+    for (int i = 0; i < ST::XD; ++i) {
+        const int r = 4 * (ST::XD * wv + i) + (lane >> 4);
+        xoff[i] = (uint32_t)min(r, M - 1) * K;
+        xgrp[i] = (uint32_t)(((lane & 15) ^ (r & 7)) * 8);
+    }
+    // payload: load i covers wave rows RPI i ..; lane -> row RPI i + lane / LPR,
+    // slot lane % LPR <- piece (lane % LPR) ^ swz(row)
+    auto swz = [](int r) { return Q4 ? (r >> 1) & 3 : r & 7; };
+    uint32_t poff[ST::PD];
+#pragma unroll
+    for (int i = 0; i < ST::PD; ++i) {
+        const int r = ST::RPI * i + lane / ST::LPR;
+        const int piece = (lane % ST::LPR) ^ swz(r);
+        poff[i] = (uint32_t)min(row0 + r, N - 1) * (uint32_t)rb + (uint32_t)(16 * piece);
+    }
+    auto issue = [&](int j) {  // this wave's LPC loads of chunk c0 + j into stage j % D
+        const uint32_t c = (uint32_t)(c0 + j);
+        uint8_t* st = ring + (j % D) * ST::BYTES;
+#pragma unroll
+        for (int i = 0; i < ST::XD; ++i)
+            dma16(xh + xoff[i] + min(c * DCK + xgrp[i], K - 8), st + (ST::XD * wv + i) * 1024);
+#pragma unroll
+        for (int i = 0; i < ST::PD; ++i)
+            dma16(base + poff[i] + c * (4 * QB), st + ST::X + (ST::PD * wv + i) * 1024);
     };
-    auto issue = [&](WChunk& c, int ch) {  // this wave's LPC loads of chunk ch
-        uint8_t* st = xring + (ch % DS) * XR::STAGE;
+
+    f32x16 acc[MT2];
 #pragma unroll
-        for (int q = 0; q < XR::DMA; ++q)
-            dma16(x + xrow[q] + min((uint32_t)ch * DKC + xchunk[q], K - 4),
-                  st + (XR::DMA * wv + q) * 1024);
+    for (int t = 0; t < MT2; ++t)
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const uint32_t kb = (uint32_t)min(4 * ch + b, KB - 1);
-            c.p[b] = *reinterpret_cast<const u32x2*>(base + roff + kb * QB + boff);
+        for (int e = 0; e < 16; ++e) acc[t][e] = 0.0f;
+
+    // ---- LDS offsets within a stage (chunk-independent) ----
+    // x groups of block i: Q4_0 low nibbles 4i + h, high 4i + 2 + h; Q8_0 4i + 2h, 4i + 2h + 1
+    uint32_t xo[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+            const int g = Q4 ? 4 * i + 2 * f + h : 4 * i + 2 * h + f;
+            xo[2 * i + f] = (uint32_t)(col * 256 + 16 * (g ^ (col & 7)));
         }
-        // scales of blocks 4 ch .. 4 ch + 3 (8-byte aligned); a partial last chunk
-        // reads past the row's scales only inside the row padding, the next row or
-        // the weight's tail slot, and those blocks get d = 0
-        c.s = *reinterpret_cast<const u32x2*>(base + roff + sbase + 8u * ch);
-    };
+    // payload of block i: Q4_0 piece i, bytes 8h ..; Q8_0 piece 2i + h
+    uint32_t po[4];
+    const int prow = 32 * wv + col;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int piece = Q4 ? i : 2 * i + h;
+        po[i] = (uint32_t)(ST::X + prow * 4 * QB + 16 * (piece ^ swz(col)) + (Q4 ? 8 * h : 0));
+    }
+    const uint32_t ring0 = (uint32_t)(uintptr_t)ring;
+    const uint32_t srow = (uint32_t)(uintptr_t)scl + (uint32_t)(wv * 2048 + col * 8 * nch);
 
-    f32x4 acc[MT];
+    auto compute = [&](int j) {
+        const uint32_t st = ring0 + (uint32_t)((j % D) * ST::BYTES);
+        const int kb0 = 4 * (c0 + j);
 #pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // LDS byte offset of this lane's x fragment (token 16 t + fr, k 32 b + 8 g, i.e.
-    // chunks 8 b + 2 g and 8 b + 2 g + 1 of the row): row and the pair of slots
-    const uint32_t ring0 = (uint32_t)(uintptr_t)xring;
-    auto compute = [&](const WChunk& c, int ch) {
-        const uint32_t st = ring0 + (uint32_t)((ch % DS) * XR::STAGE);
+        for (int hp = 0; hp < 2; ++hp) {
+            lds_u32x4 xa[MT2][4];
+            u32x4 pw[2];
+            lds_u32x2 scp;
+            read_pair<Q4, MT2>(xa, pw, scp, st + xo[4 * hp], st + xo[4 * hp + 1],
+                               st + xo[4 * hp + 2], st + xo[4 * hp + 3], st + po[2 * hp],
+                               st + po[2 * hp + 1], srow + 8 * j);
+            const uint32_t sc = scp[hp];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const bool bok = rval && 4 * ch + b < KB;
-            const uint16_t sb = (uint16_t)(c.s[b / 2] >> (16 * (b % 2)));
-            const _Float16 d = bok ? (_Float16)(__half2float(__ushort_as_half(sb)) * wscale)
-                                   : (_Float16)0.0f;
-            const f16x2 dh = {d, d};
-            const f16x8 a = dequant_frag<QT>(c.p[b], bshift, dh);
-            const uint32_t c0 = (uint32_t)(((8 * b + 2 * g) ^ fr) * 16);
-            const uint32_t c1 = (uint32_t)(((8 * b + 2 * g + 1) ^ fr) * 16);
-            lds_u32x4 lo[MT], hi[MT];
-            constexpr_for<MT>([&](auto T) {
-                constexpr int t = T.value;
-                lo[t] = lds_read128<t * 16 * 512>(st + fr * 512 + c0);
-                hi[t] = lds_read128<t * 16 * 512>(st + fr * 512 + c1);
-            });
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            for (int bi = 0; bi < 2; ++bi) {
+                const uint16_t sb = (uint16_t)(sc >> (16 * bi));
+                const float dv =
+                    kb0 + 2 * hp + bi < KB ? __half2float(__ushort_as_half(sb)) * wscale : 0.0f;
+                const _Float16 d = (_Float16)dv;
+                const f16x2 dh = {d, d};
+                f16x8 b0, b1;
+                if constexpr (Q4) dequant_q4(u32x2{pw[bi][0], pw[bi][1]}, dh, b0, b1);
+                else dequant_q8(pw[bi], dh, b0, b1);
 #pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                asm volatile("" : "+v"(lo[t]), "+v"(hi[t]));
-                const float* f0 = reinterpret_cast<const float*>(&lo[t]);
-                const float* f1 = reinterpret_cast<const float*>(&hi[t]);
-                const u32x4 h = {pk_f16(f0[0], f0[2]), pk_f16(f0[1], f0[3]),
-                                 pk_f16(f1[0], f1[2]), pk_f16(f1[1], f1[3])};
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, h),
-                                                                acc[t], 0, 0, 0);
+                for (int t = 0; t < MT2; ++t) {
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                        __builtin_bit_cast(f16x8, xa[t][2 * bi]), b0, acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                        __builtin_bit_cast(f16x8, xa[t][2 * bi + 1]), b1, acc[t], 0, 0, 0);
+                }
             }
         }
     };
 
-    // chunks 0 .. DS - 2 in flight; step ch waits for its own loads (the later chunk
-    // may stay in flight), meets the other waves (its x chunk is then complete),
-    // issues chunk ch + DS - 1 and computes.  Steady state unconditionally; the
-    // last chunks in a separate tail.
-    WChunk wc[DS];
-#pragma unroll
-    for (int d = 0; d < DS - 1; ++d) issue(wc[d], min(d, chunks - 1));
-    auto step = [&](WChunk& cur, WChunk& next, int ch, bool last) {
-        if (last) wait_vmcnt<0>();
-        else wait_vmcnt<LPC * (DS - 2)>();
+    // chunks 0 .. D - 2 in flight before the first step; step j waits for its own
+    // chunk (the min(D - 2, nch - 1 - j) younger ones may stay in flight; the
+    // scale loads are older than all), meets the other waves (its x rows are then
+    // complete and stage (j - 1) % D is free), issues chunk j + D - 1 and computes
+    // chunk j.  The last step waits for everything: no direct load outlives the loop.
+    for (int j = 0; j < D - 1 && j < nch; ++j) issue(j);
+    for (int j = 0; j < nch; ++j) {
+        wait_chunks<LPC, D - 2>(min(D - 2, nch - 1 - j));
         __builtin_amdgcn_s_barrier();
-        if (ch + DS - 1 < chunks) issue(next, ch + DS - 1);
-        compute(cur, ch);
-    };
-    int c0 = 0;
-    for (; c0 + 2 * DS <= chunks; c0 += DS) {
-#pragma unroll
-        for (int d = 0; d < DS; ++d) step(wc[d], wc[(d + DS - 1) % DS], c0 + d, false);
+        if (j + D - 1 < nch) issue(j + D - 1);
+        compute(j);
     }
-#pragma unroll
-    for (int d = 0; d < 2 * DS; ++d)
-        if (c0 + d < chunks)
-            step(wc[d % DS], wc[(d + DS - 1) % DS], c0 + d, c0 + d + 1 >= chunks);
 
-    // ---- epilogue: lane holds C[4 g + e][fr] = y[token 16 t + fr][row 4 g + e] ----
-    const int rbase = blockIdx.x * DROWS + wv * 16 + 4 * g;
+    // ---- epilogue: acc[t][r] = C[token 32 t + 8 (r / 4) + 4 h + r % 4][row row0 + col] ----
+    // A split k range (S > 1) meets in y by f32 atomic adds onto zeros.
+    const int n = row0 + col;
+    if (n < N) {
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-        const int m = 16 * t + fr;
-        if (m >= M) continue;
+        for (int t = 0; t < MT2; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (rbase + e < N) y[(int64_t)m * N + rbase + e] = acc[t][e] * oscale;
+            for (int r = 0; r < 16; ++r) {
+                const int m = 32 * t + 8 * (r / 4) + 4 * h + (r % 4);
+                if (m < M) {
+                    float* dst = y + (int64_t)m * N + n;
+                    if (S == 1) *dst = acc[t][r] * oscale;
+                    else unsafeAtomicAdd(dst, acc[t][r] * oscale);
+                }
+            }
     }
 }
 
-template <int QT, int MT>
-hipError_t launch_mt(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t s) {
-    static const bool attr = hipFuncSetAttribute((const void*)decode_kernel<QT, MT>,
+template <int QT, int MT2>
+hipError_t launch_mt(const QWeight& w, const _Float16* xh, int64_t m, float* y, int S,
+                     hipStream_t s) {
+    using ST = Stage<QT, MT2>;
+    static const bool attr = hipFuncSetAttribute((const void*)decode_kernel<QT, MT2>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 XRing<MT>::BYTES) == hipSuccess;
+                                                 ST::LDS) == hipSuccess;
     if (!attr) return hipErrorInvalidValue;
     const float wscale = ldexpf(1.0f, -w.f16_exp), oscale = ldexpf(1.0f, w.f16_exp);
-    const int grid = (int)((w.n + DROWS - 1) / DROWS);
-    decode_kernel<QT, MT><<<grid, 256, XRing<MT>::BYTES, s>>>(w.base, w.row_bytes, x, y, (int)m,
-                                                              (int)w.n, (int)w.kb, wscale, oscale);
+    const int groups = (int)((w.n + DROWS - 1) / DROWS);
+    decode_kernel<QT, MT2><<<groups * S, 256, ST::LDS, s>>>(
+        w.base, w.row_bytes, xh, y, (int)m, (int)w.n, (int)w.kb, S, wscale, oscale);
     return hipGetLastError();
 }
 
-template <int QT>
-hipError_t launch_qt(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t s) {
-    if (m <= 16) return launch_mt<QT, 1>(w, x, m, y, s);
-    if (m <= 32) return launch_mt<QT, 2>(w, x, m, y, s);
-    if (m <= 48) return launch_mt<QT, 3>(w, x, m, y, s);
-    return launch_mt<QT, 4>(w, x, m, y, s);
+// k split S: the fewest slices of at most kMaxSliceChunks chunks, then more
+// while the workgroups still fit the CUs at once (lds_bytes each).
+int choose_split(const QWeight& w, int lds_bytes) {
+    const int64_t groups = (w.n + DROWS - 1) / DROWS;
+    const int64_t chunks = (w.kb + 3) / 4;
+    const int64_t per_cu = std::max(1, device_info().max_lds_cu / lds_bytes);
+    const int64_t slots = (int64_t)device_info().cu_count * per_cu;
+    int64_t S = (chunks + kMaxSliceChunks - 1) / kMaxSliceChunks;
+    while (S < std::min<int64_t>(chunks, kMaxSplit) && groups * (S + 1) <= slots) ++S;
+#ifdef FORCE_S
+    S = std::min<int64_t>(std::max<int64_t>(FORCE_S, (chunks + kMaxSliceChunks - 1) / kMaxSliceChunks), chunks);
+#endif
+    return (int)S;
 }
 
 }  // namespace
 
-// m in [1, 64]; x is addressed with 32-bit offsets (m k < 2^30 always holds here).
 hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float* y,
                               hipStream_t s) {
-    if (w.qtype == UNILLM_QTYPE_Q4_0) return launch_qt<UNILLM_QTYPE_Q4_0>(w, x, m, y, s);
-    return launch_qt<UNILLM_QTYPE_Q8_0>(w, x, m, y, s);
+    // 32-bit offsets: x in f16 elements, weight bytes
+    if ((uint64_t)m * (uint64_t)w.k >= (1ull << 31) ||
+        (uint64_t)w.n * (uint64_t)w.row_bytes >= (1ull << 32))
+        return hipErrorInvalidValue;
+    const bool q4 = w.qtype == UNILLM_QTYPE_Q4_0, wide = m > 32;
+    const int lds = q4 ? (wide ? Stage<UNILLM_QTYPE_Q4_0, 2>::LDS : Stage<UNILLM_QTYPE_Q4_0, 1>::LDS)
+                       : (wide ? Stage<UNILLM_QTYPE_Q8_0, 2>::LDS : Stage<UNILLM_QTYPE_Q8_0, 1>::LDS);
+    const int S = choose_split(w, lds);
+    void* ws = nullptr;
+    hipError_t e = stream_workspace(s, (size_t)m * (size_t)w.k * 2, &ws);
+    if (e != hipSuccess) return e;
+    const int64_t n8 = m * w.k / 8;  // k % 32 == 0
+    const int64_t ny = S > 1 ? m * w.n : 0;
+    const int64_t work = std::max(n8, ny / 4);
+    const int grid =
+        (int)std::min<int64_t>((work + 255) / 256, (int64_t)device_info().cu_count * 8);
+    xprep_kernel<<<grid, 256, 0, s>>>(x, static_cast<uint4*>(ws), n8, y, ny);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    const _Float16* xh = static_cast<const _Float16*>(ws);
+    if (!wide)
+        return q4 ? launch_mt<UNILLM_QTYPE_Q4_0, 1>(w, xh, m, y, S, s)
+                  : launch_mt<UNILLM_QTYPE_Q8_0, 1>(w, xh, m, y, S, s);
+    return q4 ? launch_mt<UNILLM_QTYPE_Q4_0, 2>(w, xh, m, y, S, s)
+              : launch_mt<UNILLM_QTYPE_Q8_0, 2>(w, xh, m, y, S, s);
 }
 
 }  // namespace unillm

@@ -61,9 +61,16 @@ inline int gguf_block_bytes(int qtype) { return qtype == UNILLM_QTYPE_Q4_0 ? 18 
 // Per-device properties cached at init.
 struct DeviceInfo {
     int cu_count;
-    int max_lds;
+    int max_lds;     // per workgroup
+    int max_lds_cu;  // per CU
 };
 const DeviceInfo& device_info();
+// A device buffer of at least `bytes` for work on stream s, kept and reused by
+// later calls on the same stream (stream order makes the reuse safe: a call's
+// kernels finish before the next call's start).  Grows stream-ordered; the
+// memory is held until the process ends.  Calls on one stream from several
+// host threads are ordered by the stream, the map by a mutex.
+hipError_t stream_workspace(hipStream_t s, size_t bytes, void** out);
 // UNILLM_DEBUG_LAUNCH=1 prints each kernel's launch shape to stderr.
 bool debug_launch();
 

@@ -59,6 +59,12 @@ __device__ __forceinline__ uint32_t lds_read32(uint32_t addr) {
     asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
     return v;
 }
+template <int OFF>
+__device__ __forceinline__ uint32_t lds_read_u16(uint32_t addr) {
+    uint32_t v;
+    asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return v;
+}
 
 // s_waitcnt with only vmcnt = n (gfx950: vmcnt in bits 3:0 and 15:14; expcnt 6:4
 // and lgkmcnt 11:8 at their maxima, i.e. no wait on them).

@@ -7,7 +7,7 @@
 // matrix cores (v_mfma_f32_16x16x32_bf16).  Bound: MFMA (2 m n k flops over
 // ~n k / 32 * 18 + 4 m k + 4 m n bytes).
 //
-// x is first rounded to bf16 once (x_to_bf16_kernel, into a stream-ordered
+// x is first rounded to bf16 once (x_to_bf16_kernel, into the stream's
 // workspace): the GEMM re-reads x once per 256-column tile, so half the bytes,
 // and no conversion sits in its inner loop.
 //
@@ -376,24 +376,21 @@ hipError_t launch_qt(const QWeight& w, const __bf16* xb, int64_t m, float* y, hi
 
 hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, float* y,
                                hipStream_t s) {
-    // x in bf16 (the operand precision) in a stream-ordered workspace: the GEMM
+    // x in bf16 (the operand precision) in the stream's workspace: the GEMM
     // re-reads x once per 256-column tile, so it reads half the bytes, and no
-    // conversion sits in its inner loop.  The pool keeps the memory between calls.
+    // conversion sits in its inner loop.
     const int64_t n = m * w.k;  // k % 32 == 0, so n % 8 == 0
     void* ws = nullptr;
-    hipError_t e = hipMallocAsync(&ws, (size_t)n * sizeof(__bf16), s);
+    hipError_t e = stream_workspace(s, (size_t)n * sizeof(__bf16), &ws);
     if (e != hipSuccess) return e;
     const int64_t n8 = n / 8;
     const int grid = (int)std::min<int64_t>((n8 + 255) / 256, (int64_t)device_info().cu_count * 16);
     x_to_bf16_kernel<<<grid, 256, 0, s>>>(x, static_cast<uint4*>(ws), n8);
     e = hipGetLastError();
-    if (e == hipSuccess) {
-        const __bf16* xb = static_cast<const __bf16*>(ws);
-        e = w.qtype == UNILLM_QTYPE_Q4_0 ? launch_qt<UNILLM_QTYPE_Q4_0>(w, xb, m, y, s)
-                                         : launch_qt<UNILLM_QTYPE_Q8_0>(w, xb, m, y, s);
-    }
-    hipError_t f = hipFreeAsync(ws, s);
-    return e != hipSuccess ? e : f;
+    if (e != hipSuccess) return e;
+    const __bf16* xb = static_cast<const __bf16*>(ws);
+    return w.qtype == UNILLM_QTYPE_Q4_0 ? launch_qt<UNILLM_QTYPE_Q4_0>(w, xb, m, y, s)
+                                        : launch_qt<UNILLM_QTYPE_Q8_0>(w, xb, m, y, s);
 }
 
 }  // namespace unillm

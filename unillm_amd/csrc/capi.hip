@@ -138,8 +138,11 @@ int finish_weight(QWeight* w, hipStream_t s) {
     const float dmax = __half2float(__ushort_as_half((unsigned short)(bits > 0x7BFFu ? 0x7BFFu
                                                                                     : bits)));
     const float wmax = dmax * (w->qtype == UNILLM_QTYPE_Q4_0 ? 8.0f : 128.0f);
+    // the largest power-of-two scaling that keeps every dequantized weight in
+    // f16 range: small scales stay normal in f16 (also divided by 16)
     int E = 0;
     while (E < 30 && wmax * ldexpf(1.0f, -E) > 65504.0f) ++E;
+    while (wmax > 0.0f && E > -30 && wmax * ldexpf(1.0f, -(E - 1)) <= 65504.0f) --E;
     w->f16_exp = E;
     return UNILLM_OK;
 }

@@ -23,10 +23,12 @@
 //          payloads (2 blocks per row) and its f16 scales.  Step j waits for
 //          its own chunk (exact vmcnt: younger chunks stay in flight), meets
 //          the other waves, issues chunk j + D - 1 and computes chunk j.
-//        - Dequant, per lane and block: Q4_0 -- 8 payload bytes (16 signed
-//          nibbles, flipped back to q) become two B fragments, the low nibbles
-//          (elements 8h .. 8h + 7) and the high nibbles (16 + 8h ..), h = lane / 32;
-//          Q8_0 -- 16 bytes (elements 16h .. 16h + 15) become two fragments.
+//        - Dequant, per lane (h = lane / 32): Q4_0 -- a lane takes one whole
+//          block (16 payload bytes, 32 signed nibbles flipped back to q), the
+//          two blocks of a pair on the two lane halves, and makes four B
+//          fragments of 8 elements; MFMA q then runs over elements 8q .. 8q + 7
+//          of both blocks, each lane with its own block's scale.  Q8_0 -- a lane
+//          takes 16 bytes of a block (elements 16h .. 16h + 15): two fragments.
 //          (code | 0x6400) is the f16 1024 + code exactly; minus 1024 + offset
 //          gives the signed code exactly, times d 2^-E rounds once -- the same
 //          single rounding as (q - 8) d 2^-E computed in f32 and rounded to f16.
@@ -73,22 +75,29 @@ __device__ __forceinline__ uint32_t scale2(uint32_t v, f16x2 bias, f16x2 dh) {
     return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, v) - bias) * dh);
 }
 
-// Q4_0: 8 payload bytes (signed nibbles of elements 8h .. 8h + 7 low, 16 + 8h .. high)
-// -> lo / hi fragments, each in the order 0 2 1 3 4 6 5 7.
-__device__ __forceinline__ void dequant_q4(u32x2 raw, f16x2 dh, f16x8& lo, f16x8& hi) {
-    const f16x2 bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+// Q4_0: one block's 16 payload bytes (signed nibbles: low = elements 0 .. 15,
+// high = 16 .. 31) -> four fragments, elements 8q .. 8q + 7 for q = 0 .. 3, each
+// in the order 0 2 1 3 4 6 5 7.  A low nibble u lands in an f16 as 1024 + u
+// (minus 1032, times d); a high nibble in place, bits 4 .. 7, as 1024 + 16 u
+// (minus 1152, times d / 16): one shift per dword instead of three.  dh16 = d / 16
+// is exact (the weight's exponent offset keeps the scales normal in f16).
+__device__ __forceinline__ void dequant_q4(u32x4 raw, f16x2 dh, f16x2 dh16, f16x8 (&f)[4]) {
+    const f16x2 blo = {(_Float16)1032.0f, (_Float16)1032.0f};
+    const f16x2 bhi = {(_Float16)1152.0f, (_Float16)1152.0f};
     const uint32_t magic = 0x64006400u;
-    u32x4 l, h;
+    u32x4 o[4];
 #pragma unroll
-    for (int d = 0; d < 2; ++d) {
+    for (int d = 0; d < 4; ++d) {  // bytes 4d .. 4d + 3: elements 4d .. (low), 16 + 4d .. (high)
         const uint32_t w = raw[d] ^ 0x88888888u;  // signed nibble -> q
-        l[2 * d] = scale2(and_or(w, 0x000F000Fu, magic), bias, dh);            // bytes 0, 2 low
-        l[2 * d + 1] = scale2(and_or(w >> 8, 0x000F000Fu, magic), bias, dh);   // bytes 1, 3 low
-        h[2 * d] = scale2(and_or(w >> 4, 0x000F000Fu, magic), bias, dh);       // bytes 0, 2 high
-        h[2 * d + 1] = scale2(and_or(w >> 12, 0x000F000Fu, magic), bias, dh);  // bytes 1, 3 high
+        const uint32_t w8 = w >> 8;
+        const int lo = d / 2, e = 2 * (d % 2);
+        o[lo][e] = scale2(and_or(w, 0x000F000Fu, magic), blo, dh);          // bytes 0, 2 low
+        o[lo][e + 1] = scale2(and_or(w8, 0x000F000Fu, magic), blo, dh);     // bytes 1, 3 low
+        o[2 + lo][e] = scale2(and_or(w, 0x00F000F0u, magic), bhi, dh16);    // bytes 0, 2 high
+        o[2 + lo][e + 1] = scale2(and_or(w8, 0x00F000F0u, magic), bhi, dh16);  // bytes 1, 3 high
     }
-    lo = __builtin_bit_cast(f16x8, l);
-    hi = __builtin_bit_cast(f16x8, h);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) f[q] = __builtin_bit_cast(f16x8, o[q]);
 }
 
 // Q8_0: 16 payload bytes (elements 16h .. 16h + 15) -> two fragments (elements
@@ -134,12 +143,14 @@ __global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x,
 }
 
 // LDS: a D-stage ring, each stage one 128-k chunk of
-//   x   [TOK rows][256 B] f16; the 16-byte group g of row r sits in slot g ^ (r % 8);
+//   x   [TOK rows][256 B] f16; the 16-byte group g of row r sits in slot g ^ (r % 16);
 //   W   [128 rows][4 QB] payloads of the chunk's 4 blocks; the 16-byte piece c
-//       of row r sits in slot c ^ swz(r) (Q4_0 (r / 2) % 4, Q8_0 r % 8),
-// then the workgroup's k-slice scales, per wave [32 rows][8 nch B] (at most
-// kMaxSliceChunks chunks: 2 KiB a wave), loaded once before the ring starts.
-// The swizzles spread an MFMA fragment's 16 rows / 8 tokens over distinct banks.
+//       of row r sits in slot c ^ swz(r),
+// then the workgroup's k-slice scales, per wave [32 rows][8 x 8 B] (at most
+// kMaxSliceChunks = 8 chunks: 2 KiB a wave), chunk j of row r at position
+// (j + r) % 8, loaded once before the ring starts.  The swizzles and the
+// rotation put the rows (tokens) that one LDS read pass serves -- 8 or 16
+// consecutive lanes -- on distinct banks.
 constexpr int kMaxSliceChunks = 8;
 #ifndef DECODE_MAX_SPLIT
 #define DECODE_MAX_SPLIT 4
@@ -177,54 +188,47 @@ __device__ __forceinline__ void wait_chunks(int rem) {
     }
 }
 
-// The LDS reads for two blocks of a chunk and the wait for them in ONE asm
+// The LDS reads for half a chunk (two blocks) and the wait for them in ONE asm
 // statement: the outputs are early-clobber and defined only once the statement
 // ends, so the compiler cannot copy a destination register before its data has
 // landed (with separate asm reads it may, and the copy reads a stale register).
-//   x: for each block the two fragment groups (a0, a1 | a2, a3), tile 1 at +8192;
-//   payload: Q4_0 8 bytes, Q8_0 16 bytes per block (p0, p1); the chunk's four
-//   f16 scales (8 bytes at sa).
+//   x: four fragment groups (a0 .. a3), tile 1 at +8192; payload: Q4_0 one
+//   block (16 bytes at p0), Q8_0 half of each of two blocks (16 bytes at p0, p1);
+//   the chunk's four f16 scales (8 bytes at sa).
 #define UNILLM_DS128(o, a, off) "ds_read_b128 %" #o ", %" #a " offset:" #off "\n"
 #define UNILLM_DS64(o, a, off) "ds_read_b64 %" #o ", %" #a " offset:" #off "\n"
 template <bool Q4, int MT2>
-__device__ __forceinline__ void read_pair(lds_u32x4 (&xa)[MT2][4], u32x4 (&pw)[2],
+__device__ __forceinline__ void read_half(lds_u32x4 (&xa)[MT2][4], u32x4 (&pw)[2],
                                           lds_u32x2& scp, uint32_t a0, uint32_t a1, uint32_t a2,
                                           uint32_t a3, uint32_t p0, uint32_t p1, uint32_t sa) {
+    lds_u32x4 w0, w1;
     if constexpr (Q4 && MT2 == 1) {
-        lds_u32x2 w0, w1;
-        asm volatile(UNILLM_DS128(0, 7, 0) UNILLM_DS128(1, 8, 0) UNILLM_DS128(2, 9, 0)
-                         UNILLM_DS128(3, 10, 0) UNILLM_DS64(4, 11, 0) UNILLM_DS64(5, 12, 0)
-                             UNILLM_DS64(6, 13, 0) "s_waitcnt lgkmcnt(0)"
+        asm volatile(UNILLM_DS128(0, 6, 0) UNILLM_DS128(1, 7, 0) UNILLM_DS128(2, 8, 0)
+                         UNILLM_DS128(3, 9, 0) UNILLM_DS128(4, 10, 0) UNILLM_DS64(5, 11, 0)
+                             "s_waitcnt lgkmcnt(0)"
                      : "=&v"(xa[0][0]), "=&v"(xa[0][1]), "=&v"(xa[0][2]), "=&v"(xa[0][3]),
-                       "=&v"(w0), "=&v"(w1), "=&v"(scp)
-                     : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(p0), "v"(p1), "v"(sa));
-        pw[0] = u32x4{w0[0], w0[1], 0u, 0u};
-        pw[1] = u32x4{w1[0], w1[1], 0u, 0u};
+                       "=&v"(w0), "=&v"(scp)
+                     : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(p0), "v"(sa));
+        w1 = w0;
     } else if constexpr (Q4) {
-        lds_u32x2 w0, w1;
-        asm volatile(UNILLM_DS128(0, 11, 0) UNILLM_DS128(1, 12, 0) UNILLM_DS128(2, 13, 0)
-                         UNILLM_DS128(3, 14, 0) UNILLM_DS128(4, 11, 8192) UNILLM_DS128(5, 12, 8192)
-                             UNILLM_DS128(6, 13, 8192) UNILLM_DS128(7, 14, 8192)
-                                 UNILLM_DS64(8, 15, 0) UNILLM_DS64(9, 16, 0)
-                                     UNILLM_DS64(10, 17, 0) "s_waitcnt lgkmcnt(0)"
+        asm volatile(UNILLM_DS128(0, 10, 0) UNILLM_DS128(1, 11, 0) UNILLM_DS128(2, 12, 0)
+                         UNILLM_DS128(3, 13, 0) UNILLM_DS128(4, 10, 8192) UNILLM_DS128(5, 11, 8192)
+                             UNILLM_DS128(6, 12, 8192) UNILLM_DS128(7, 13, 8192)
+                                 UNILLM_DS128(8, 14, 0) UNILLM_DS64(9, 15, 0)
+                                     "s_waitcnt lgkmcnt(0)"
                      : "=&v"(xa[0][0]), "=&v"(xa[0][1]), "=&v"(xa[0][2]), "=&v"(xa[0][3]),
                        "=&v"(xa[MT2 - 1][0]), "=&v"(xa[MT2 - 1][1]), "=&v"(xa[MT2 - 1][2]),
-                       "=&v"(xa[MT2 - 1][3]), "=&v"(w0), "=&v"(w1), "=&v"(scp)
-                     : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(p0), "v"(p1), "v"(sa));
-        pw[0] = u32x4{w0[0], w0[1], 0u, 0u};
-        pw[1] = u32x4{w1[0], w1[1], 0u, 0u};
+                       "=&v"(xa[MT2 - 1][3]), "=&v"(w0), "=&v"(scp)
+                     : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(p0), "v"(sa));
+        w1 = w0;
     } else if constexpr (MT2 == 1) {
-        lds_u32x4 w0, w1;
         asm volatile(UNILLM_DS128(0, 7, 0) UNILLM_DS128(1, 8, 0) UNILLM_DS128(2, 9, 0)
                          UNILLM_DS128(3, 10, 0) UNILLM_DS128(4, 11, 0) UNILLM_DS128(5, 12, 0)
                              UNILLM_DS64(6, 13, 0) "s_waitcnt lgkmcnt(0)"
                      : "=&v"(xa[0][0]), "=&v"(xa[0][1]), "=&v"(xa[0][2]), "=&v"(xa[0][3]),
                        "=&v"(w0), "=&v"(w1), "=&v"(scp)
                      : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(p0), "v"(p1), "v"(sa));
-        pw[0] = __builtin_bit_cast(u32x4, w0);
-        pw[1] = __builtin_bit_cast(u32x4, w1);
     } else {
-        lds_u32x4 w0, w1;
         asm volatile(UNILLM_DS128(0, 11, 0) UNILLM_DS128(1, 12, 0) UNILLM_DS128(2, 13, 0)
                          UNILLM_DS128(3, 14, 0) UNILLM_DS128(4, 11, 8192) UNILLM_DS128(5, 12, 8192)
                              UNILLM_DS128(6, 13, 8192) UNILLM_DS128(7, 14, 8192)
@@ -234,9 +238,9 @@ __device__ __forceinline__ void read_pair(lds_u32x4 (&xa)[MT2][4], u32x4 (&pw)[2
                        "=&v"(xa[MT2 - 1][0]), "=&v"(xa[MT2 - 1][1]), "=&v"(xa[MT2 - 1][2]),
                        "=&v"(xa[MT2 - 1][3]), "=&v"(w0), "=&v"(w1), "=&v"(scp)
                      : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(p0), "v"(p1), "v"(sa));
-        pw[0] = __builtin_bit_cast(u32x4, w0);
-        pw[1] = __builtin_bit_cast(u32x4, w1);
     }
+    pw[0] = __builtin_bit_cast(u32x4, w0);
+    pw[1] = __builtin_bit_cast(u32x4, w1);
 }
 #undef UNILLM_DS128
 #undef UNILLM_DS64
@@ -267,31 +271,37 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
     const int row0 = rg * DROWS + 32 * wv;  // this wave's 32 weight rows
     const uint32_t sbase = (uint32_t)KB * QB;  // the scales follow the payloads in a row
 
-    // ---- the slice's scales: 8 nch bytes a row, nch dword loads per wave; lane
-    // -> flat dword f = 64 i + lane = row r, dword f % (2 nch) (past the last
-    // block: the row's padding, the next row or the tail slot; zeroed below) ----
-    for (int i = 0; i < nch; ++i) {
+    // ---- the slice's scales: 8 positions of 8 bytes a row (kMaxSliceChunks), 8
+    // dword loads per wave; lane -> flat dword f = 64 i + lane = row f / 16,
+    // position f % 16 / 2, which holds chunk (position - row) % 8 (positions past
+    // the slice repeat its last chunk; past the last block: the row's padding, the
+    // next row or the tail slot, zeroed below) ----
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
         const int f = 64 * i + lane;
-        const int r = f / (2 * nch), dw = f - r * (2 * nch);
+        const int r = f >> 4, dw = f & 15;
+        const int jj = min(((dw >> 1) - r) & 7, nch - 1);
         const uint32_t g = (uint32_t)min(row0 + r, N - 1) * (uint32_t)rb + sbase +
-                           8u * (uint32_t)c0 + 4u * (uint32_t)dw;
+                           8u * (uint32_t)(c0 + jj) + 4u * (uint32_t)(dw & 1);
         dma4(base + g, scl + wv * 2048 + i * 256);
     }
 
     // ---- per-chunk direct-load sources (32-bit offsets; the host checks sizes) ----
     // x: load q = XD wv + i covers token rows 4q .. 4q + 3; lane -> row 4q + lane / 16,
-    // slot lane % 16 <- group (lane % 16) ^ (row % 8).  Rows past m read row m - 1
+    // slot lane % 16 <- group (lane % 16) ^ (row % 16).  Rows past m read row m - 1
     // and k past K the row's last group (finite values against zero weights).
     uint32_t xoff[ST::XD], xgrp[ST::XD];
 #pragma unroll
     for (int i = 0; i < ST::XD; ++i) {
         const int r = 4 * (ST::XD * wv + i) + (lane >> 4);
         xoff[i] = (uint32_t)min(r, M - 1) * K;
-        xgrp[i] = (uint32_t)(((lane & 15) ^ (r & 7)) * 8);
+        xgrp[i] = (uint32_t)(((lane & 15) ^ (r & 15)) * 8);
     }
     // payload: load i covers wave rows RPI i ..; lane -> row RPI i + lane / LPR,
     // slot lane % LPR <- piece (lane % LPR) ^ swz(row)
-    auto swz = [](int r) { return Q4 ? (r >> 1) & 3 : r & 7; };
+    //   Q4_0 ((r / 2) % 4) ^ (r / 8 % 2), Q8_0 (r % 8) ^ (r / 8 % 2): distinct (row
+    //   parity, slot) pairs over any 8 and any aligned 16 consecutive rows
+    auto swz = [](int r) { return (Q4 ? (r >> 1) & 3 : r & 7) ^ ((r >> 3) & 1); };
     uint32_t poff[ST::PD];
 #pragma unroll
     for (int i = 0; i < ST::PD; ++i) {
@@ -299,12 +309,19 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
         const int piece = (lane % ST::LPR) ^ swz(r);
         poff[i] = (uint32_t)min(row0 + r, N - 1) * (uint32_t)rb + (uint32_t)(16 * piece);
     }
-    auto issue = [&](int j) {  // this wave's LPC loads of chunk c0 + j into stage j % D
+    // A wave whose x rows all lie past m loads none: padded token rows only feed
+    // the outputs of padded tokens (never stored), so their LDS rows may hold
+    // anything.  Its loads per chunk are then PD, not LPC.
+    const bool xw = 4 * ST::XD * wv < M;
+    auto issue = [&](int j) {  // this wave's loads of chunk c0 + j into stage j % D
         const uint32_t c = (uint32_t)(c0 + j);
         uint8_t* st = ring + (j % D) * ST::BYTES;
+        if (xw) {
 #pragma unroll
-        for (int i = 0; i < ST::XD; ++i)
-            dma16(xh + xoff[i] + min(c * DCK + xgrp[i], K - 8), st + (ST::XD * wv + i) * 1024);
+            for (int i = 0; i < ST::XD; ++i)
+                dma16(xh + xoff[i] + min(c * DCK + xgrp[i], K - 8),
+                      st + (ST::XD * wv + i) * 1024);
+        }
 #pragma unroll
         for (int i = 0; i < ST::PD; ++i)
             dma16(base + poff[i] + c * (4 * QB), st + ST::X + (ST::PD * wv + i) * 1024);
@@ -317,54 +334,75 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
         for (int e = 0; e < 16; ++e) acc[t][e] = 0.0f;
 
     // ---- LDS offsets within a stage (chunk-independent) ----
-    // x groups of block i: Q4_0 low nibbles 4i + h, high 4i + 2 + h; Q8_0 4i + 2h, 4i + 2h + 1
+    // Q4_0: half p of the chunk is blocks 2p (h = 0) and 2p + 1 (h = 1); a lane
+    // reads its block (piece 2p + h) and feeds four MFMAs, the q-th with elements
+    // 8q .. 8q + 7 of that block (x group 4 (2p + h) + q).  Q8_0: half p is blocks
+    // 2p, 2p + 1; a lane reads half h of each (piece 2i + h), elements 16h .. +15
+    // (x groups 4i + 2h, 4i + 2h + 1).
     uint32_t xo[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int hp = 0; hp < 2; ++hp)
 #pragma unroll
-        for (int f = 0; f < 2; ++f) {
-            const int g = Q4 ? 4 * i + 2 * f + h : 4 * i + 2 * h + f;
-            xo[2 * i + f] = (uint32_t)(col * 256 + 16 * (g ^ (col & 7)));
+        for (int q = 0; q < 4; ++q) {
+            const int i = 2 * hp + q / 2;  // Q8_0 block
+            const int g = Q4 ? 8 * hp + 4 * h + q : 4 * i + 2 * h + (q & 1);
+            xo[4 * hp + q] = (uint32_t)(col * 256 + 16 * (g ^ (col & 15)));
         }
-    // payload of block i: Q4_0 piece i, bytes 8h ..; Q8_0 piece 2i + h
     uint32_t po[4];
     const int prow = 32 * wv + col;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int piece = Q4 ? i : 2 * i + h;
-        po[i] = (uint32_t)(ST::X + prow * 4 * QB + 16 * (piece ^ swz(col)) + (Q4 ? 8 * h : 0));
+        const int piece = Q4 ? (2 * (i & 1) + h) : 2 * i + h;  // Q4_0 uses po[0], po[1]
+        po[i] = (uint32_t)(ST::X + prow * 4 * QB + 16 * (piece ^ swz(col)));
     }
     const uint32_t ring0 = (uint32_t)(uintptr_t)ring;
-    const uint32_t srow = (uint32_t)(uintptr_t)scl + (uint32_t)(wv * 2048 + col * 8 * nch);
+    const uint32_t srow = (uint32_t)(uintptr_t)scl + (uint32_t)(wv * 2048 + col * 64);
 
     auto compute = [&](int j) {
         const uint32_t st = ring0 + (uint32_t)((j % D) * ST::BYTES);
         const int kb0 = 4 * (c0 + j);
+        const uint32_t sa = srow + 8 * ((j + col) & 7);
 #pragma unroll
         for (int hp = 0; hp < 2; ++hp) {
             lds_u32x4 xa[MT2][4];
             u32x4 pw[2];
             lds_u32x2 scp;
-            read_pair<Q4, MT2>(xa, pw, scp, st + xo[4 * hp], st + xo[4 * hp + 1],
-                               st + xo[4 * hp + 2], st + xo[4 * hp + 3], st + po[2 * hp],
-                               st + po[2 * hp + 1], srow + 8 * j);
-            const uint32_t sc = scp[hp];
-#pragma unroll
-            for (int bi = 0; bi < 2; ++bi) {
-                const uint16_t sb = (uint16_t)(sc >> (16 * bi));
+            read_half<Q4, MT2>(xa, pw, scp, st + xo[4 * hp], st + xo[4 * hp + 1],
+                               st + xo[4 * hp + 2], st + xo[4 * hp + 3],
+                               st + po[Q4 ? hp : 2 * hp], st + po[Q4 ? hp : 2 * hp + 1], sa);
+            if constexpr (Q4) {
+                // this lane's block 2 hp + h and its scale
+                const uint16_t sb = (uint16_t)(scp[hp] >> (16 * h));
                 const float dv =
-                    kb0 + 2 * hp + bi < KB ? __half2float(__ushort_as_half(sb)) * wscale : 0.0f;
-                const _Float16 d = (_Float16)dv;
-                const f16x2 dh = {d, d};
-                f16x8 b0, b1;
-                if constexpr (Q4) dequant_q4(u32x2{pw[bi][0], pw[bi][1]}, dh, b0, b1);
-                else dequant_q8(pw[bi], dh, b0, b1);
+                    kb0 + 2 * hp + h < KB ? __half2float(__ushort_as_half(sb)) * wscale : 0.0f;
+                const _Float16 d = (_Float16)dv, d16 = (_Float16)(dv * 0.0625f);
+                const f16x2 dh = {d, d}, dh16 = {d16, d16};
+                f16x8 b[4];
+                dequant_q4(pw[0], dh, dh16, b);
 #pragma unroll
-                for (int t = 0; t < MT2; ++t) {
-                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                        __builtin_bit_cast(f16x8, xa[t][2 * bi]), b0, acc[t], 0, 0, 0);
-                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                        __builtin_bit_cast(f16x8, xa[t][2 * bi + 1]), b1, acc[t], 0, 0, 0);
+                for (int t = 0; t < MT2; ++t)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            __builtin_bit_cast(f16x8, xa[t][q]), b[q], acc[t], 0, 0, 0);
+            } else {
+#pragma unroll
+                for (int bi = 0; bi < 2; ++bi) {
+                    const uint16_t sb = (uint16_t)(scp[hp] >> (16 * bi));
+                    const float dv = kb0 + 2 * hp + bi < KB
+                                         ? __half2float(__ushort_as_half(sb)) * wscale
+                                         : 0.0f;
+                    const _Float16 d = (_Float16)dv;
+                    const f16x2 dh = {d, d};
+                    f16x8 b0, b1;
+                    dequant_q8(pw[bi], dh, b0, b1);
+#pragma unroll
+                    for (int t = 0; t < MT2; ++t) {
+                        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            __builtin_bit_cast(f16x8, xa[t][2 * bi]), b0, acc[t], 0, 0, 0);
+                        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            __builtin_bit_cast(f16x8, xa[t][2 * bi + 1]), b1, acc[t], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -377,27 +415,42 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
     // chunk j.  The last step waits for everything: no direct load outlives the loop.
     for (int j = 0; j < D - 1 && j < nch; ++j) issue(j);
     for (int j = 0; j < nch; ++j) {
-        wait_chunks<LPC, D - 2>(min(D - 2, nch - 1 - j));
+        if (xw) wait_chunks<LPC, D - 2>(min(D - 2, nch - 1 - j));
+        else wait_chunks<ST::PD, D - 2>(min(D - 2, nch - 1 - j));
         __builtin_amdgcn_s_barrier();
         if (j + D - 1 < nch) issue(j + D - 1);
         compute(j);
     }
 
     // ---- epilogue: acc[t][r] = C[token 32 t + 8 (r / 4) + 4 h + r % 4][row row0 + col] ----
-    // A split k range (S > 1) meets in y by f32 atomic adds onto zeros.
+    // A split k range (S > 1) meets in y by f32 atomic adds onto zeros.  With
+    // m % 8 == 0 a token block (t, r / 4) is valid for all lanes or none.
     const int n = row0 + col;
     if (n < N) {
+        float* yb = y + (int64_t)(4 * h) * N + n;
+        auto put = [&](float* dst, float v) {
+            if (S == 1) *dst = v * oscale;
+            else unsafeAtomicAdd(dst, v * oscale);
+        };
+        if (M % 8 == 0) {
 #pragma unroll
-        for (int t = 0; t < MT2; ++t)
+            for (int t = 0; t < MT2; ++t)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = 32 * t + 8 * (r / 4) + 4 * h + (r % 4);
-                if (m < M) {
-                    float* dst = y + (int64_t)m * N + n;
-                    if (S == 1) *dst = acc[t][r] * oscale;
-                    else unsafeAtomicAdd(dst, acc[t][r] * oscale);
+                for (int rb4 = 0; rb4 < 4; ++rb4) {
+                    if (32 * t + 8 * rb4 >= M) break;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        put(yb + (int64_t)(32 * t + 8 * rb4 + e) * N, acc[t][4 * rb4 + e]);
                 }
-            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < MT2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m0 = 32 * t + 8 * (r / 4) + (r % 4);
+                    if (m0 + 4 * h < M) put(yb + (int64_t)m0 * N, acc[t][r]);
+                }
+        }
     }
 }
 

@@ -29,7 +29,7 @@ struct unillm_qweight {
     int64_t row_bytes;     // bytes per row: payloads, scales, padding
     uint8_t* base;         // n * row_bytes, then a 256-byte scratch slot
     size_t bytes;
-    int f16_exp;           // E >= 0 with 8 * max|d| * 2^-E <= 65504 (f16 range)
+    int f16_exp;           // smallest E with max|q d| 2^-E <= 65504 (f16 range)
 };
 
 namespace unillm {

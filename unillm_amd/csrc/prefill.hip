@@ -13,22 +13,25 @@
 //
 // Tile per workgroup: BM rows of x (BM = 256 or 128) x 256 weight rows
 // (output columns), k in steps of 64 (two blocks).  Eight waves (two per
-// SIMD) in a 2 x 4 grid: wave (rw, cw) owns BM / 2 rows x 64 columns,
-// BM / 32 x 4 MFMA tiles of 16 x 16, fp32 accumulators in registers.
+// SIMD) side by side: wave w owns all BM rows x columns 32 w .. 32 w + 31,
+// BM / 16 x 2 MFMA tiles of 16 x 16, fp32 accumulators in registers.
 //   - Operands reach LDS by direct global -> LDS loads through a 3-stage ring
 //     (two k steps in flight, no VGPR staging): A as bf16 rows with an XOR
 //     swizzle of 16-byte chunks, B as the raw Q4_0 / Q8_0 payload bytes and
 //     scales of the tile's 256 weight rows.
 //   - Each lane reads the 8 payload bytes behind its MFMA B fragment and
-//     dequantizes them in registers; a column group's weights are dequantized
-//     by its two waves (a 1 x 8 split would halve that but double the A reads).
+//     dequantizes them in registers; every weight is dequantized once (a 2 x 4
+//     grid of waves halves the A reads from LDS but dequantizes each column
+//     twice: measured 10-30 % slower, the VALU being the scarcer unit).
 //   - The LDS reads are inline asm with explicit waits, so the compiler never
 //     drains the ring's later stages before them; a step waits for its own
 //     stage (vmcnt in issue order) and meets the other waves at a bare
 //     s_barrier.
-// Measured limits (rocprofv3 counters): VALU (the dequant, ~2.9 instructions
-// per weight per pass) and MFMA each occupy ~45 % of a SIMD's cycles with
-// little co-issue; the 2 x 4 split keeps LDS traffic at ~70 % of its rate.
+// Measured limits: on gfx950 the matrix cores and the VALU hardly overlap while
+// the accumulators sit in arch VGPRs (a micro-benchmark: MFMA + independent
+// VALU cost the sum of both), so a step costs MFMA + dequant VALU; the dequant
+// is ~3 VALU instructions per weight (byte -> f32, fma, pack).  Accumulators in
+// AGPRs (asm MFMAs) overlap the two in isolation but measured no faster here.
 //
 // Workgroup -> tile: workgroups are dealt round-robin over the 8 XCDs, so
 // workgroup b takes tile (b % 8) * (T / 8) + b / 8 (T tiles, padded to a
@@ -152,10 +155,10 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
                                                               int tiles_pad) {
     static_assert(NW == 8, "the ring's load split assumes 8 waves");
     constexpr int QB = QT == UNILLM_QTYPE_Q4_0 ? 16 : 32;  // payload bytes per block
-    // waves: 2 row groups x 4 column groups; wave (rw, cw) owns rows BM / 2 * rw .. and
-    // columns 64 cw .. 64 cw + 63 of the tile (each column group's weights are
-    // dequantized by both of its waves: half the A traffic of a 1 x 8 split)
-    constexpr int RW = 2, CW = 4;
+    // waves: RW row groups x CW column groups; wave (rw, cw) owns rows BM / RW * rw ..
+    // and columns PBN / CW * cw .. of the tile; its columns' weights are dequantized
+    // by the RW waves of the group.  RW = 1: each weight once, all of A per wave.
+    constexpr int RW = 1, CW = NW / RW;
     constexpr int WR = BM / RW;                            // rows per wave
     constexpr int WC = PBN / CW;                           // output columns per wave (64)
     constexpr int TI = WR / 16;                            // MFMA tiles along m per wave
@@ -263,24 +266,34 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
         // B: raw bytes and scales of this wave's columns -> bf16 fragments
         u32x2 raw[TJ][2];
         uint32_t sc[TJ];
-        static_assert(TJ == 4, "unrolled for four column tiles");
-        raw[0][0] = (u32x2)lds_read64<0 * 16 * 2 * QB>(st + boff0);
-        raw[0][1] = (u32x2)lds_read64<0 * 16 * 2 * QB + QB>(st + boff0);
-        raw[1][0] = (u32x2)lds_read64<1 * 16 * 2 * QB>(st + boff0);
-        raw[1][1] = (u32x2)lds_read64<1 * 16 * 2 * QB + QB>(st + boff0);
-        raw[2][0] = (u32x2)lds_read64<2 * 16 * 2 * QB>(st + boff0);
-        raw[2][1] = (u32x2)lds_read64<2 * 16 * 2 * QB + QB>(st + boff0);
-        raw[3][0] = (u32x2)lds_read64<3 * 16 * 2 * QB>(st + boff0);
-        raw[3][1] = (u32x2)lds_read64<3 * 16 * 2 * QB + QB>(st + boff0);
-        // column tiles j and j + 2 are 32 columns apart: the next 256-byte scale group
-        sc[0] = lds_read32<0>(st + soff0);
-        sc[1] = lds_read32<64>(st + soff0);
-        sc[2] = lds_read32<256>(st + soff0);
-        sc[3] = lds_read32<256 + 64>(st + soff0);
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(raw[0][0]), "+v"(raw[0][1]), "+v"(raw[1][0]), "+v"(raw[1][1]),
-                       "+v"(raw[2][0]), "+v"(raw[2][1]), "+v"(raw[3][0]), "+v"(raw[3][1]),
-                       "+v"(sc[0]), "+v"(sc[1]), "+v"(sc[2]), "+v"(sc[3]));
+        // raw payload of column tile j at j * 16 * 2 QB (block 1 at + QB); scales of
+        // tile j at (16 j / 32) * 256 + (16 j % 32) * 4 relative to tile 0's
+        static_assert(TJ == 2 || TJ == 4, "two or four column tiles");
+        constexpr int T = 16 * 2 * QB;
+        if constexpr (TJ == 4) {
+            asm volatile(
+                "ds_read_b64 %0, %12 offset:%c14\n ds_read_b64 %1, %12 offset:%c15\n"
+                "ds_read_b64 %2, %12 offset:%c16\n ds_read_b64 %3, %12 offset:%c17\n"
+                "ds_read_b64 %4, %12 offset:%c18\n ds_read_b64 %5, %12 offset:%c19\n"
+                "ds_read_b64 %6, %12 offset:%c20\n ds_read_b64 %7, %12 offset:%c21\n"
+                "ds_read_b32 %8, %13\n ds_read_b32 %9, %13 offset:64\n"
+                "ds_read_b32 %10, %13 offset:256\n ds_read_b32 %11, %13 offset:320\n"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(raw[0][0]), "=&v"(raw[0][1]), "=&v"(raw[1][0]), "=&v"(raw[1][1]),
+                  "=&v"(raw[2][0]), "=&v"(raw[2][1]), "=&v"(raw[3][0]), "=&v"(raw[3][1]),
+                  "=&v"(sc[0]), "=&v"(sc[1]), "=&v"(sc[2]), "=&v"(sc[3])
+                : "v"(st + boff0), "v"(st + soff0), "i"(0), "i"(QB), "i"(T), "i"(T + QB),
+                  "i"(2 * T), "i"(2 * T + QB), "i"(3 * T), "i"(3 * T + QB));
+        } else {
+            asm volatile(
+                "ds_read_b64 %0, %6 offset:%c8\n ds_read_b64 %1, %6 offset:%c9\n"
+                "ds_read_b64 %2, %6 offset:%c10\n ds_read_b64 %3, %6 offset:%c11\n"
+                "ds_read_b32 %4, %7\n ds_read_b32 %5, %7 offset:64\n"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(raw[0][0]), "=&v"(raw[0][1]), "=&v"(raw[TJ - 1][0]),
+                  "=&v"(raw[TJ - 1][1]), "=&v"(sc[0]), "=&v"(sc[TJ - 1])
+                : "v"(st + boff0), "v"(st + soff0), "i"(0), "i"(QB), "i"(T), "i"(T + QB));
+        }
         const bool b1ok = 2 * ks + 1 < KB;
         float d0[TJ], d1[TJ];
 #pragma unroll

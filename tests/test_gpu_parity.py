@@ -196,8 +196,9 @@ def test_baseline_prefill_rows_sampled(qtype, m, k, n):
     xd = _dev(x)
     y2 = ql.forward(xd * 2.0)
     torch.cuda.synchronize()
-    # scaling by 2 is exact in bf16 and f32: outputs scale exactly
-    assert np.array_equal(y2.cpu().numpy(), 2.0 * y)
+    # scaling by 2 is exact in bf16 and f32: outputs scale exactly, up to the order
+    # of the atomic adds where the k range is split (k = 14336 at m = 512)
+    assert oracle.normwise_error(y2.cpu().numpy(), 2.0 * y) < 1e-6
 
 
 @pytest.mark.parametrize("qtype,m,k,n", [(Q4_0, 2048, 4096, 14336), (Q8_0, 1100, 4128, 14000),
@@ -212,7 +213,7 @@ def test_prefill_large_tiles(qtype, m, k, n):
     assert oracle.normwise_error(y[rows], ref) < 2e-2
     y2 = ql.forward(_dev(x) * 2.0)
     torch.cuda.synchronize()
-    assert np.array_equal(y2.cpu().numpy(), 2.0 * y)
+    assert np.array_equal(y2.cpu().numpy(), 2.0 * y)  # enough tiles: no k split
 
 
 # ---- edges -----------------------------------------------------------------------------------
@@ -251,11 +252,12 @@ def test_forward_argument_errors():
 
 
 def test_repeat_calls_deterministic():
-    # GEMV (m <= 4) and prefill compute every output in one fixed order: bitwise
-    # repeatable.  Batched decode splits k over workgroups whose partial sums
-    # meet in y by f32 atomic adds, so the order of those few adds (at most 4)
-    # can vary between calls: repeatable to f32 rounding, not bitwise.
-    for m, exact in ((1, True), (130, True), (16, False), (64, False)):
+    # GEMV (m <= 4) and prefill with enough tiles compute every output in one
+    # fixed order: bitwise repeatable.  Batched decode, and prefill with few tiles
+    # (m = 130 here: 32 tiles), split k over workgroups whose partial sums meet in
+    # y by f32 atomic adds, so the order of those few adds (at most 4) can vary
+    # between calls: repeatable to f32 rounding, not bitwise.
+    for m, exact in ((1, True), (2048, True), (130, False), (16, False), (64, False)):
         blocks, x = _case(Q4_0, m, 4096, 4096, seed=9)
         ql = QuantLinear.from_blocks(Q4_0, 4096, 4096, blocks)
         xd = _dev(x)

@@ -104,9 +104,11 @@ __device__ __forceinline__ bf16x8 dequant8(u32x2 raw, int shift, float d) {
     return __builtin_bit_cast(bf16x8, p);
 }
 
-// x (f32) -> bf16, round to nearest even; 8 elements per thread per pass.
+// x (f32) -> bf16, round to nearest even; 8 elements per thread per pass.  y[0, ny)
+// <- 0 (a split k range adds into it).
 __global__ __launch_bounds__(256) void x_to_bf16_kernel(const float* __restrict__ x,
-                                                        uint4* __restrict__ xb, int64_t n8) {
+                                                        uint4* __restrict__ xb, int64_t n8,
+                                                        float* __restrict__ y, int64_t ny) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8;
          i += (int64_t)gridDim.x * blockDim.x) {
         const float4 a = reinterpret_cast<const float4*>(x)[2 * i];
@@ -114,6 +116,15 @@ __global__ __launch_bounds__(256) void x_to_bf16_kernel(const float* __restrict_
         xb[i] = make_uint4(pack_bf16(a.x, a.y), pack_bf16(a.z, a.w), pack_bf16(b.x, b.y),
                            pack_bf16(b.z, b.w));
     }
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t head = std::min<int64_t>(ny, (int64_t)((16 - ((uintptr_t)y & 15)) & 15) / 4);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < head; i += stride) y[i] = 0.0f;
+    float4* y4 = reinterpret_cast<float4*>(y + head);
+    const int64_t n4 = (ny - head) / 4;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride)
+        y4[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int64_t i = head + 4 * n4 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < ny; i += stride)
+        y[i] = 0.0f;
 }
 
 // ---- LDS ring ------------------------------------------------------------------------------
@@ -152,7 +163,7 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
                                                               const __bf16* __restrict__ xb,
                                                               float* __restrict__ y, int M, int N,
                                                               int KB, int tiles_n, int tiles,
-                                                              int tiles_pad) {
+                                                              int units_pad, int S) {
     static_assert(NW == 8, "the ring's load split assumes 8 waves");
     constexpr int QB = QT == UNILLM_QTYPE_Q4_0 ? 16 : 32;  // payload bytes per block
     // waves: RW row groups x CW column groups; wave (rw, cw) owns rows BM / RW * rw ..
@@ -168,16 +179,21 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
     constexpr int CPB = R::CPB;
     extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
 
-    // ---- tile (XCD-aware) ----
-    const int per_xcd = tiles_pad / 8;
-    const int t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-    if (t >= tiles) return;  // padding workgroups (uniform: the whole workgroup leaves)
+    // ---- work unit (XCD-aware): unit u = (k slice sp, tile t), in (sp, m-tile,
+    // n-tile) order ----
+    const int per_xcd = units_pad / 8;
+    const int u = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (u >= tiles * S) return;  // padding workgroups (uniform: the whole workgroup leaves)
+    const int sp = u / tiles, t = u % tiles;
     const int mt = t / tiles_n, nt = t % tiles_n;
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int m0 = mt * BM, n0 = nt * PBN;
     const uint32_t K = (uint32_t)KB * QK;
     const int ksteps = (KB + 1) / 2;
+    // this unit's k steps [ks0, ks0 + nks)
+    const int ks0 = (int)((int64_t)sp * ksteps / S);
+    const int nks = (int)((int64_t)(sp + 1) * ksteps / S) - ks0;
 
     // ---- this lane's direct-load sources (k-independent parts) ----
     // A: load q covers tile rows 8 q .. 8 q + 7; lane -> row 8 q + lane / 8, slot lane % 8,
@@ -252,15 +268,16 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
     // prologue: stages 0 .. kStages - 2 in flight
 #pragma unroll
     for (int d = 0; d < kStages - 1; ++d)
-        if (d < ksteps) issue(d);
+        if (d < nks) issue(ks0 + d);
 
-    for (int ks = 0; ks < ksteps; ++ks) {
+    for (int j = 0; j < nks; ++j) {
+        const int ks = ks0 + j;
         // wait for this wave's loads of step ks: the loads of later steps already
         // issued (at most kStages - 2 of them) may stay in flight
-        if (ks + 1 < ksteps) wait_vmcnt<R::DMA>();
+        if (j + 1 < nks) wait_vmcnt<R::DMA>();
         else wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
-        if (ks + kStages - 1 < ksteps) issue(ks + kStages - 1);
+        if (j + kStages - 1 < nks) issue(ks + kStages - 1);
 
         const uint32_t st = ring0 + (uint32_t)((ks % kStages) * R::STAGE);
         // B: raw bytes and scales of this wave's columns -> bf16 fragments
@@ -335,7 +352,8 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
         }
     }
 
-    // ---- epilogue: lane holds C[4 (l / 16) + e][l % 16] of each 16 x 16 tile ----
+    // ---- epilogue: lane holds C[4 (l / 16) + e][l % 16] of each 16 x 16 tile; the
+    // S k slices of a tile meet in y by f32 atomic adds onto zeros ----
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
         const int col = n0 + WC * cw + 16 * j + fr;
@@ -345,18 +363,23 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int row = m0 + WR * rw + 16 * i + 4 * g + e;
-                if (row < M) y[(int64_t)row * N + col] = acc[i][j][e];
+                if (row >= M) continue;
+                float* dst = y + (int64_t)row * N + col;
+                if (S == 1) *dst = acc[i][j][e];
+                else unsafeAtomicAdd(dst, acc[i][j][e]);
             }
     }
 }
 
 template <int QT, int BM>
-hipError_t launch_bm(const QWeight& w, const __bf16* xb, int64_t m, float* y, hipStream_t s) {
+hipError_t launch_bm(const QWeight& w, const __bf16* xb, int64_t m, float* y, int S,
+                     hipStream_t s) {
     // x is addressed with 32-bit element offsets: launch in row chunks below 2^30 elements
     const int64_t chunk = std::max<int64_t>(BM, ((int64_t)1 << 30) / w.k / BM * BM);
     if (m > chunk) {
         for (int64_t r = 0; r < m; r += chunk) {
-            hipError_t e = launch_bm<QT, BM>(w, xb + r * w.k, std::min(chunk, m - r), y + r * w.n, s);
+            hipError_t e =
+                launch_bm<QT, BM>(w, xb + r * w.k, std::min(chunk, m - r), y + r * w.n, S, s);
             if (e != hipSuccess) return e;
         }
         return hipSuccess;
@@ -370,19 +393,29 @@ hipError_t launch_bm(const QWeight& w, const __bf16* xb, int64_t m, float* y, hi
     const int tiles_m = (int)((m + BM - 1) / BM);
     const int tiles_n = (int)((w.n + PBN - 1) / PBN);
     const int tiles = tiles_m * tiles_n;
-    const int tiles_pad = (tiles + 7) / 8 * 8;
-    prefill_kernel<QT, BM, kWaves><<<tiles_pad, kWaves * 64, Ring<QT, BM>::BYTES, s>>>(
-        w.base, w.row_bytes, xb, y, (int)m, (int)w.n, (int)w.kb, tiles_n, tiles, tiles_pad);
+    const int units_pad = (tiles * S + 7) / 8 * 8;
+    prefill_kernel<QT, BM, kWaves><<<units_pad, kWaves * 64, Ring<QT, BM>::BYTES, s>>>(
+        w.base, w.row_bytes, xb, y, (int)m, (int)w.n, (int)w.kb, tiles_n, tiles, units_pad, S);
     return hipGetLastError();
 }
 
-template <int QT>
-hipError_t launch_qt(const QWeight& w, const __bf16* xb, int64_t m, float* y, hipStream_t s) {
-    // 256-row tiles when they give at least one tile per CU, else 128-row tiles
+// Tile rows and k split.  256-row tiles when they give at least one tile per CU,
+// else 128-row tiles; when even those leave most CUs idle (a short, deep
+// product), the k steps are split over up to 4 workgroups per tile, at least
+// 16 steps each.  Calls beyond the 32-bit x offsets (chunked) never split.
+struct PrefillPlan {
+    int bm, S;
+};
+PrefillPlan prefill_plan(const QWeight& w, int64_t m) {
+    const int64_t cus = device_info().cu_count;
     const int64_t tiles_n = (w.n + PBN - 1) / PBN;
-    const int64_t tiles256 = (m + 255) / 256 * tiles_n;
-    if (tiles256 >= device_info().cu_count) return launch_bm<QT, 256>(w, xb, m, y, s);
-    return launch_bm<QT, 128>(w, xb, m, y, s);
+    if ((m + 255) / 256 * tiles_n >= cus) return {256, 1};
+    const int64_t tiles = (m + 127) / 128 * tiles_n;
+    const int64_t ksteps = (w.kb + 1) / 2;
+    int64_t S = 1;
+    if (2 * tiles < cus && m * w.k < ((int64_t)1 << 30))
+        S = std::max<int64_t>(1, std::min<int64_t>({4, cus / tiles, ksteps / 16}));
+    return {128, (int)S};
 }
 
 }  // namespace
@@ -391,19 +424,25 @@ hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, floa
                                hipStream_t s) {
     // x in bf16 (the operand precision) in the stream's workspace: the GEMM
     // re-reads x once per 256-column tile, so it reads half the bytes, and no
-    // conversion sits in its inner loop.
+    // conversion sits in its inner loop.  The same kernel zeroes y for a split k.
+    const PrefillPlan plan = prefill_plan(w, m);
     const int64_t n = m * w.k;  // k % 32 == 0, so n % 8 == 0
     void* ws = nullptr;
     hipError_t e = stream_workspace(s, (size_t)n * sizeof(__bf16), &ws);
     if (e != hipSuccess) return e;
-    const int64_t n8 = n / 8;
-    const int grid = (int)std::min<int64_t>((n8 + 255) / 256, (int64_t)device_info().cu_count * 16);
-    x_to_bf16_kernel<<<grid, 256, 0, s>>>(x, static_cast<uint4*>(ws), n8);
+    const int64_t n8 = n / 8, ny = plan.S > 1 ? m * w.n : 0;
+    const int grid = (int)std::min<int64_t>((std::max(n8, ny / 4) + 255) / 256,
+                                            (int64_t)device_info().cu_count * 16);
+    x_to_bf16_kernel<<<grid, 256, 0, s>>>(x, static_cast<uint4*>(ws), n8, y, ny);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     const __bf16* xb = static_cast<const __bf16*>(ws);
-    return w.qtype == UNILLM_QTYPE_Q4_0 ? launch_qt<UNILLM_QTYPE_Q4_0>(w, xb, m, y, s)
-                                        : launch_qt<UNILLM_QTYPE_Q8_0>(w, xb, m, y, s);
+    const bool q4 = w.qtype == UNILLM_QTYPE_Q4_0;
+    if (plan.bm == 256)
+        return q4 ? launch_bm<UNILLM_QTYPE_Q4_0, 256>(w, xb, m, y, 1, s)
+                  : launch_bm<UNILLM_QTYPE_Q8_0, 256>(w, xb, m, y, 1, s);
+    return q4 ? launch_bm<UNILLM_QTYPE_Q4_0, 128>(w, xb, m, y, plan.S, s)
+              : launch_bm<UNILLM_QTYPE_Q8_0, 128>(w, xb, m, y, plan.S, s);
 }
 
 }  // namespace unillm

@@ -15,7 +15,7 @@
 // (output columns), k in steps of 64 (two blocks).  Eight waves (two per
 // SIMD) side by side: wave w owns all BM rows x columns 32 w .. 32 w + 31,
 // BM / 16 x 2 MFMA tiles of 16 x 16, fp32 accumulators in registers.
-//   - Operands reach LDS by direct global -> LDS loads through a 3-stage ring
+//   - Operands reach LDS by direct global -> LDS loads through a 3- or 4-stage ring
 //     (two k steps in flight, no VGPR staging): A as bf16 rows with an XOR
 //     swizzle of 16-byte chunks, B as the raw Q4_0 / Q8_0 payload bytes and
 //     scales of the tile's 256 weight rows.
@@ -142,7 +142,6 @@ __global__ __launch_bounds__(256) void x_to_bf16_kernel(const float* __restrict_
 // for exactly the stage it reads (vmcnt counts a wave's loads in issue order)
 // and then meets the other waves at a bare s_barrier (no fence: a fence would
 // also drain the stages still in flight).
-constexpr int kStages = 3;
 
 template <int QT, int BM>
 struct Ring {
@@ -151,7 +150,10 @@ struct Ring {
     static constexpr int BP = PBN * 2 * QB;
     static constexpr int BS = 2 * PBN * 4;
     static constexpr int STAGE = A + BP + BS;
-    static constexpr int BYTES = kStages * STAGE;
+    // stages: 4 for 128-row tiles (four fit in LDS; ~10 % over three measured),
+    // 3 for 256-row tiles
+    static constexpr int STAGES = BM == 128 ? 4 : 3;
+    static constexpr int BYTES = STAGES * STAGE;
     static constexpr int CPB = 2 * QB / 16;            // 16-byte payload chunks per column
     static constexpr int AQ = BM / 8 / 8;              // A loads (8 rows each) per wave
     static constexpr int DMA = AQ + CPB / 2 + 1;       // direct loads per wave per stage
@@ -175,6 +177,7 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
     constexpr int TI = WR / 16;                            // MFMA tiles along m per wave
     constexpr int TJ = WC / 16;                            // MFMA tiles along n per wave (4)
     using R = Ring<QT, BM>;
+    constexpr int kStages = R::STAGES;
     constexpr int AQ = R::AQ;
     constexpr int CPB = R::CPB;
     extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
@@ -274,7 +277,10 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
         const int ks = ks0 + j;
         // wait for this wave's loads of step ks: the loads of later steps already
         // issued (at most kStages - 2 of them) may stay in flight
-        if (j + 1 < nks) wait_vmcnt<R::DMA>();
+        // (min(kStages - 2, nks - 1 - j) younger steps in flight: the full count, one
+        // or none at the end)
+        if (j + kStages - 2 < nks) wait_vmcnt<(kStages - 2) * R::DMA>();
+        else if (j + 1 < nks) wait_vmcnt<R::DMA>();
         else wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
         if (j + kStages - 1 < nks) issue(ks + kStages - 1);

@@ -27,11 +27,17 @@
 //     drains the ring's later stages before them; a step waits for its own
 //     stage (vmcnt in issue order) and meets the other waves at a bare
 //     s_barrier.
-// Measured limits: on gfx950 the matrix cores and the VALU hardly overlap while
-// the accumulators sit in arch VGPRs (a micro-benchmark: MFMA + independent
-// VALU cost the sum of both), so a step costs MFMA + dequant VALU; the dequant
-// is ~3 VALU instructions per weight (byte -> f32, fma, pack).  Accumulators in
-// AGPRs (asm MFMAs) overlap the two in isolation but measured no faster here.
+// Measured limits (m2048 k4096 n14336, with parts of the work switched off in
+// copies of this kernel): the matrix cores, the dequant VALU and the LDS reads
+// hardly overlap.  Without the dequant a call takes 84 % of the time, without
+// the MFMAs 68 %, with neither 59 %, and with no global loads either (barriers
+// and LDS reads only) 40 %: each of the 8 waves reads the whole A tile from LDS,
+// 256 KB per step per CU.  A 2 x 4 grid halves those reads but dequantizes every
+// weight twice: 15-40 % slower.  On gfx950 the matrix cores and the VALU hardly
+// co-issue while the accumulators sit in arch VGPRs (a micro-benchmark: MFMA +
+// independent VALU cost the sum of both); accumulators in AGPRs (asm MFMAs)
+// overlap the two in isolation but measured 8 % slower here, the asm fixing the
+// instruction order.  The ring depth (3, 4 or 6 stages) makes no difference.
 //
 // Workgroup -> tile: workgroups are dealt round-robin over the 8 XCDs, so
 // workgroup b takes tile (b % 8) * (T / 8) + b / 8 (T tiles, padded to a
@@ -331,17 +337,24 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
         bf16x8 bfrag[TJ][2];
 #pragma unroll
         for (int j = 0; j < TJ; ++j) bfrag[j][0] = dequant8<QT>(raw[j][0], bshift, d0[j]);
-        // A fragments, one ahead: fragment f = kk * TI + i at aoff[kk] + 2048 i
+        // A fragments, two ahead (one ahead leaves ~2 MFMAs to cover an LDS read;
+        // deeper measured no better): fragment f = kk * TI + i at aoff[kk] + 2048 i
+        constexpr int PF = 2;
         bf16x8 afr[2 * TI];
-        afr[0] = __builtin_bit_cast(bf16x8, lds_read128<0>(st + aoff[0]));
+        constexpr_for<PF>([&](auto F) {
+            afr[F.value] = __builtin_bit_cast(
+                bf16x8, lds_read128<(F.value % TI) * 2048>(st + aoff[F.value / TI]));
+        });
 #pragma unroll
         for (int f = 0; f < 2 * TI; ++f) {
-            if (f + 1 < 2 * TI) {
+            if (f + PF < 2 * TI) {
                 constexpr_for<2 * TI>([&](auto F) {
-                    if (F.value == f + 1)
+                    if (F.value == f + PF)
                         afr[F.value] = __builtin_bit_cast(
                             bf16x8, lds_read128<(F.value % TI) * 2048>(st + aoff[F.value / TI]));
                 });
+                asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(afr[f]));
+            } else if (f + 1 < 2 * TI) {
                 asm volatile("s_waitcnt lgkmcnt(1)" : "+v"(afr[f]));
             } else {
                 asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(afr[f]));

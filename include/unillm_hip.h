@@ -16,8 +16,9 @@
  *     blocks along k, exactly as GGUF stores a tensor with ne = [k, n]
  *     (candle reverses ne into shape [n, k]).  x is [m, k] f32 row-major and
  *     y = x . dequant(W)^T is [m, n] f32 row-major.
- *   - Preconditions checked on the host before any launch: k % 32 == 0,
- *     n >= 1, k >= 32, m >= 0, non-null pointers, known qtype.
+ *   - Preconditions checked on the host before any launch: k % 32 == 0
+ *     (k % 256 == 0 for Q4_K), n >= 1, k >= 32, m >= 0, non-null pointers,
+ *     known qtype.
  *   - Streams: a `void* stream` is a hipStream_t (NULL = the null stream).
  *     Compute calls are asynchronous on that stream and never synchronise.
  *   - Ownership: a qweight owns its device copy of the weights and is
@@ -34,9 +35,11 @@
 extern "C" {
 #endif
 
-/* GGML type ids as GGUF stores them (candle GgmlDType::Q4_0 / Q8_0). */
+/* GGML type ids as GGUF stores them (candle GgmlDType::Q4_0 / Q8_0 / Q4K; the
+ * reference maps Q4K at crates/runtime/src/weight_loader_core.rs:481). */
 #define UNILLM_QTYPE_Q4_0 2
 #define UNILLM_QTYPE_Q8_0 8
+#define UNILLM_QTYPE_Q4_K 12
 
 #define UNILLM_OK 0
 #define UNILLM_ERR_INVALID_ARG (-1)
@@ -62,7 +65,8 @@ int unillm_hip_init(int device);
 /* Message of the last error on the calling thread ("" if none). */
 const char* unillm_hip_last_error(void);
 
-/* Upload one GGUF Q4_0 / Q8_0 tensor ([n, k], n * k/32 blocks of 18 / 34 B)
+/* Upload one GGUF Q4_0 / Q8_0 / Q4_K tensor ([n, k]: n * k/32 blocks of 18 /
+ * 34 B, or n * k/256 blocks of 144 B)
  * to the device, repacked there into the kernels' layout.  Replaces
  * `QMatMul::from_arc(Arc::new(qtensor))` at
  * crates/runtime/src/weight_loader_core.rs:569-571 (the QTensor read at :545).

@@ -18,8 +18,11 @@ import numpy as np
 
 Q4_0 = 2
 Q8_0 = 8
+Q4_K = 12
+Q6_K = 14
 QK = 32
-BLOCK_BYTES = {Q4_0: 18, Q8_0: 34}
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}
+BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256}
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liboracle.so")
@@ -84,7 +87,7 @@ def quantize(qtype: int, w: np.ndarray) -> np.ndarray:
 
 def dequant(qtype: int, blocks: np.ndarray, n: int, k: int) -> np.ndarray:
     blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
-    assert blocks.size == n * (k // QK) * BLOCK_BYTES[qtype]
+    assert blocks.size == n * (k // BLOCK_ELEMS[qtype]) * BLOCK_BYTES[qtype]
     out = np.empty((n, k), dtype=np.float32)
     if lib().oracle_dequant(qtype, _ptr(blocks), n, k, _ptr(out)) != 0:
         raise ValueError("oracle_dequant rejected its arguments")
@@ -133,3 +136,51 @@ def elementwise_error(y: np.ndarray, ref: np.ndarray, floor: float = 1e-3) -> fl
         return 0.0
     d = np.abs(np.asarray(y, dtype=np.float64)[big] - ref[big]) / np.abs(ref[big])
     return float(d.max())
+
+
+# ---- K-quant test data ---------------------------------------------------------------------
+# GGML has no simple reference quantizer for Q4_K / Q6_K (quantize_row_q4_K_ref
+# searches scales iteratively); the parity tests need valid blocks, not GGML's
+# choice of them, so blocks are drawn directly: random codes and 6- / 8-bit
+# scales under f16 super-block scales sized like N(0, 0.02) weights.
+
+def pack_q4_k_scales(sc, m) -> np.ndarray:
+    """GGML's packing of eight 6-bit scales and mins into scales[12], as
+    quantize_row_q4_K_ref writes it (the inverse of get_scale_min_k4)."""
+    out = np.zeros(12, np.uint8)
+    for j in range(8):
+        ls, lm = int(sc[j]), int(m[j])
+        assert 0 <= ls < 64 and 0 <= lm < 64
+        if j < 4:
+            out[j] = ls
+            out[j + 4] = lm
+        else:
+            out[j + 4] = (ls & 0xF) | ((lm & 0xF) << 4)
+            out[j - 4] |= (ls >> 4) << 6
+            out[j] |= (lm >> 4) << 6
+    return out
+
+
+def random_q4_k(n: int, k: int, seed: int) -> np.ndarray:
+    """[n, k/256 * 144] valid Q4_K blocks, weights of roughly N(0, 0.02) size."""
+    assert k % 256 == 0
+    rng = np.random.default_rng(seed)
+    nb = n * (k // 256)
+    blk = rng.integers(0, 256, size=(nb, 144), dtype=np.uint8)  # scales[12] and qs: any bytes
+    d = (np.abs(rng.normal(0, 1, nb)) * 4e-5 + 1e-5).astype(np.float16)
+    dmin = (np.abs(rng.normal(0, 1, nb)) * 2e-4 + 1e-5).astype(np.float16)
+    blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    blk[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)
+    return blk.reshape(n, -1)
+
+
+def random_q6_k(n: int, k: int, seed: int) -> np.ndarray:
+    """[n, k/256 * 210] valid Q6_K blocks (signed 8-bit sub-block scales)."""
+    assert k % 256 == 0
+    rng = np.random.default_rng(seed)
+    nb = n * (k // 256)
+    blk = rng.integers(0, 256, size=(nb, 210), dtype=np.uint8)  # ql, qh: any bytes
+    blk[:, 192:208] = rng.integers(-64, 128, size=(nb, 16)).astype(np.int8).view(np.uint8)
+    d = (np.abs(rng.normal(0, 1, nb)) * 2e-5 + 5e-6).astype(np.float16)
+    blk[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
+    return blk.reshape(n, -1)

@@ -17,12 +17,24 @@
 #include <omp.h>
 #endif
 
+int oracle_block_elems(int qtype) {
+    if (qtype == ORACLE_Q4_0 || qtype == ORACLE_Q8_0) return 32;
+    if (qtype == ORACLE_Q4_K || qtype == ORACLE_Q6_K) return 256;
+    return 0;
+}
+
 size_t oracle_block_bytes(int qtype) {
     /* Q4_0: {f16 d; u8 qs[16]} = 18 B; Q8_0: {f16 d; i8 qs[32]} = 34 B.
      * (The reference's in-repo Q4_0Block is 32 B because of align(32),
-     * crates/runtime/src/simd/quant/block.rs:27 -- not the GGUF stride.) */
+     * crates/runtime/src/simd/quant/block.rs:27 -- not the GGUF stride.)
+     * Q4_K: 2 + 2 + 12 + 128 = 144 B; Q6_K: 128 + 64 + 16 + 2 = 210 B (GGML
+     * block_q4_K / block_q6_K; the in-repo Q4_KBlock, block.rs:100-110, has
+     * the same size but a simplified scale packing, block.rs:124-139, and is
+     * not what candle's Q4K reads). */
     if (qtype == ORACLE_Q4_0) return 18;
     if (qtype == ORACLE_Q8_0) return 34;
+    if (qtype == ORACLE_Q4_K) return 144;
+    if (qtype == ORACLE_Q6_K) return 210;
     return 0;
 }
 
@@ -118,7 +130,7 @@ static void quantize_block_q8_0(const float* x, uint8_t* out) {
 
 int oracle_quantize(int qtype, const float* w, int64_t n, int64_t k, uint8_t* blocks) {
     const size_t bb = oracle_block_bytes(qtype);
-    if (!bb || k % 32 || n < 0 || k < 0) return -1;
+    if ((qtype != ORACLE_Q4_0 && qtype != ORACLE_Q8_0) || k % 32 || n < 0 || k < 0) return -1;
     const int64_t kb = k / 32;
     for (int64_t r = 0; r < n; ++r)
         for (int64_t b = 0; b < kb; ++b) {
@@ -133,7 +145,77 @@ int oracle_quantize(int qtype, const float* w, int64_t n, int64_t k, uint8_t* bl
 /* BlockQ4_0::to_float / BlockQ8_0::to_float (candle, external), reached from
  * qtensor.dequantize at crates/runtime/src/weight_loader_core.rs:579.  The
  * products are exact in f32 (<= 8-bit integer times an 11-bit significand). */
+/* GGML get_scale_min_k4: sub-block j's 6-bit scale and min.  j < 4: low six
+ * bits of scales[j] and scales[j + 4]; j >= 4: low / high nibble of
+ * scales[j + 4] plus the top two bits of scales[j - 4] / scales[j]. */
+static void q4_k_scale_min(int j, const uint8_t* q, int* sc, int* m) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 0x0F) | ((q[j - 4] >> 6) << 4);
+        *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+/* GGML dequantize_row_q4_K, one 256-weight block (BlockQ4K::to_float in candle,
+ * the type weight_loader_core.rs:481 maps as Q4K).  d * sc and dmin * m are
+ * exact in f32 (11-bit significand times 6 bits); (d sc) q is exact too, so the
+ * one rounding is the subtraction, the same with or without a fused multiply-add. */
+static void dequant_q4_k(const uint8_t* blk, float* y) {
+    const float d = oracle_f16_to_f32(rd16(blk));
+    const float dmin = oracle_f16_to_f32(rd16(blk + 2));
+    const uint8_t* scales = blk + 4;
+    const uint8_t* q = blk + 16;
+    for (int g = 0; g < 4; ++g) {
+        int sc, m;
+        q4_k_scale_min(2 * g, scales, &sc, &m);
+        const float d1 = d * (float)sc, m1 = dmin * (float)m;
+        q4_k_scale_min(2 * g + 1, scales, &sc, &m);
+        const float d2 = d * (float)sc, m2 = dmin * (float)m;
+        for (int l = 0; l < 32; ++l) y[64 * g + l] = d1 * (float)(q[32 * g + l] & 0x0F) - m1;
+        for (int l = 0; l < 32; ++l) y[64 * g + 32 + l] = d2 * (float)(q[32 * g + l] >> 4) - m2;
+    }
+}
+
+/* GGML dequantize_row_q6_K, one 256-weight block: two halves of 128 weights,
+ * each from 64 bytes of ql, 32 of qh and 8 scales; weight l + 32 t of a half
+ * (t = 0..3, l = 0..31) has q = (ql nibble) | (2 bits of qh[l]) << 4, scale
+ * scales[l / 16 + 2 t].  Evaluated as GGML writes it, (d * sc) * (q - 32):
+ * d * sc is exact, the second product rounds once. */
+static void dequant_q6_k(const uint8_t* blk, float* y) {
+    const uint8_t* ql = blk;
+    const uint8_t* qh = blk + 128;
+    const int8_t* sc = (const int8_t*)(blk + 192);
+    const float d = oracle_f16_to_f32(rd16(blk + 208));
+    for (int h = 0; h < 2; ++h) {
+        for (int l = 0; l < 32; ++l) {
+            const int is = l / 16;
+            const int q1 = ((ql[l] & 0x0F) | (((qh[l] >> 0) & 3) << 4)) - 32;
+            const int q2 = ((ql[l + 32] & 0x0F) | (((qh[l] >> 2) & 3) << 4)) - 32;
+            const int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+            const int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+            y[l] = d * (float)sc[is] * (float)q1;
+            y[l + 32] = d * (float)sc[is + 2] * (float)q2;
+            y[l + 64] = d * (float)sc[is + 4] * (float)q3;
+            y[l + 96] = d * (float)sc[is + 6] * (float)q4;
+        }
+        y += 128;
+        ql += 64;
+        qh += 32;
+        sc += 8;
+    }
+}
+
 static void dequant_block(int qtype, const uint8_t* blk, float* y) {
+    if (qtype == ORACLE_Q4_K) {
+        dequant_q4_k(blk, y);
+        return;
+    }
+    if (qtype == ORACLE_Q6_K) {
+        dequant_q6_k(blk, y);
+        return;
+    }
     const float d = oracle_f16_to_f32(rd16(blk));
     const uint8_t* qs = blk + 2;
     if (qtype == ORACLE_Q4_0) {
@@ -148,11 +230,12 @@ static void dequant_block(int qtype, const uint8_t* blk, float* y) {
 
 int oracle_dequant(int qtype, const uint8_t* blocks, int64_t n, int64_t k, float* out) {
     const size_t bb = oracle_block_bytes(qtype);
-    if (!bb || k % 32 || n < 0 || k < 0) return -1;
-    const int64_t kb = k / 32;
+    const int be = oracle_block_elems(qtype);
+    if (!bb || n < 0 || k < 0 || k % be) return -1;
+    const int64_t kb = k / be;
     for (int64_t r = 0; r < n; ++r)
         for (int64_t b = 0; b < kb; ++b)
-            dequant_block(qtype, blocks + (size_t)(r * kb + b) * bb, out + r * k + b * 32);
+            dequant_block(qtype, blocks + (size_t)(r * kb + b) * bb, out + r * k + b * be);
     return 0;
 }
 
@@ -165,8 +248,9 @@ int oracle_dequant(int qtype, const uint8_t* blocks, int64_t n, int64_t k, float
 int oracle_qmatmul_f64(int qtype, const uint8_t* blocks, const float* x,
                        int64_t m, int64_t n, int64_t k, double* y, int nthreads) {
     const size_t bb = oracle_block_bytes(qtype);
-    if (!bb || k % 32 || n < 0 || k < 0 || m < 0) return -1;
-    const int64_t kb = k / 32;
+    const int be = oracle_block_elems(qtype);
+    if (!bb || n < 0 || k < 0 || m < 0 || k % be) return -1;
+    const int64_t kb = k / be;
 #ifdef _OPENMP
     if (nthreads > 0) omp_set_num_threads(nthreads);
 #pragma omp parallel
@@ -178,7 +262,7 @@ int oracle_qmatmul_f64(int qtype, const uint8_t* blocks, const float* x,
 #endif
         for (int64_t c = 0; c < n; ++c) {
             for (int64_t b = 0; b < kb; ++b)
-                dequant_block(qtype, blocks + (size_t)(c * kb + b) * bb, wrow + b * 32);
+                dequant_block(qtype, blocks + (size_t)(c * kb + b) * bb, wrow + b * be);
             for (int64_t r = 0; r < m; ++r) {
                 const float* xr = x + r * k;
                 double acc = 0.0;
@@ -229,7 +313,8 @@ static float vec_dot_q8_0_q8_0(const uint8_t* w, const uint8_t* xq, int64_t kb) 
 int oracle_candle_qmatmul(int qtype, const uint8_t* blocks, const float* x,
                           int64_t m, int64_t n, int64_t k, float* y, int nthreads) {
     const size_t bb = oracle_block_bytes(qtype);
-    if (!bb || k % 32 || n < 0 || k < 0 || m < 0) return -1;
+    if ((qtype != ORACLE_Q4_0 && qtype != ORACLE_Q8_0) || k % 32 || n < 0 || k < 0 || m < 0)
+        return -1;
     const int64_t kb = k / 32;
     uint8_t* xq = (uint8_t*)malloc((size_t)(m * kb * 34) + 1);
     if (!xq) return -2;

@@ -15,6 +15,17 @@
  *        w[j]    = ((qs[j] & 0xF) - 8) * d      j = 0..15
  *        w[j+16] = ((qs[j] >>  4) - 8) * d
  *   Q8_0 block (34 B / 32 weights): { f16 d; i8 qs[32]; }   w[j] = qs[j] * d
+ *   Q4_K block (144 B / 256 weights, GGML block_q4_K, candle GgmlDType::Q4K,
+ *        mapped at weight_loader_core.rs:481):
+ *        { f16 d; f16 dmin; u8 scales[12]; u8 qs[128]; }
+ *        sub-block j (32 weights) has a 6-bit scale sc_j and min m_j packed in
+ *        scales[] (get_scale_min_k4); group g = 0..3 of 64 weights uses
+ *        qs[32 g .. 32 g + 31]: low nibbles -> sub-block 2 g, high -> 2 g + 1;
+ *        w = (d * sc_j) * q - (dmin * m_j)       (dequantize_row_q4_K)
+ *   Q6_K block (210 B / 256 weights, GGML block_q6_K):
+ *        { u8 ql[128]; u8 qh[64]; i8 scales[16]; f16 d; }
+ *        w = (d * scales[s]) * (q - 32), q 6-bit from ql (4) and qh (2)
+ *                                                  (dequantize_row_q6_K)
  *
  * Call sites in the reference that this path serves:
  *   crates/runtime/src/weight_loader_core.rs:543-584  (GGUF read, QMatMul::from_arc)
@@ -26,7 +37,12 @@
  *   f16<->f32          : numpy's float16 conversions, exhaustive over 65536 codes
  *   dequant            : closed form, exhaustive over all scales x all codes;
  *                        the reference's layout-neutral known answers
- *                        (simd/quant/block.rs:398-423, q4_0.rs:131-178)
+ *                        (simd/quant/block.rs:398-423, q4_0.rs:131-178).
+ *                        Q4_K / Q6_K: one-hot blocks that expose every index
+ *                        (which byte, nibble, scale and min each weight uses),
+ *                        the 6-bit scale packing as the inverse of GGML's
+ *                        packer over all 64 x 64 values per sub-block, and an
+ *                        independent numpy decoding (tests/test_oracle.py)
  *   quantizers         : invariants (max-magnitude element -> code 0 for Q4_0,
  *                        round-trip error <= d/2 for Q8_0), hand-computed blocks,
  *                        and an independent numpy restatement (tests/golden)
@@ -50,26 +66,30 @@ extern "C" {
 #define ORACLE_QK 32
 #define ORACLE_Q4_0 2
 #define ORACLE_Q8_0 8
+#define ORACLE_Q4_K 12
+#define ORACLE_Q6_K 14
 
-/* bytes per 32-weight block: 18 (Q4_0) or 34 (Q8_0); 0 for unknown types */
+/* weights per block: 32 (Q4_0, Q8_0) or 256 (Q4_K, Q6_K); 0 for unknown types */
+int oracle_block_elems(int qtype);
+/* bytes per block: 18 (Q4_0), 34 (Q8_0), 144 (Q4_K), 210 (Q6_K); 0 for unknown */
 size_t oracle_block_bytes(int qtype);
 
 /* IEEE binary16 <-> binary32 (round to nearest even, subnormals, inf, nan) */
 float oracle_f16_to_f32(uint16_t h);
 uint16_t oracle_f32_to_f16(float f);
 
-/* GGML reference quantizers, weights [n, k] row-major -> GGUF block bytes */
+/* GGML reference quantizers (Q4_0, Q8_0), weights [n, k] row-major -> GGUF block bytes */
 int oracle_quantize(int qtype, const float* w, int64_t n, int64_t k, uint8_t* blocks);
 
-/* exact dequant, GGUF block bytes -> f32 [n, k] */
+/* exact dequant, GGUF block bytes -> f32 [n, k] (k a multiple of the block size) */
 int oracle_dequant(int qtype, const uint8_t* blocks, int64_t n, int64_t k, float* out);
 
 /* the parity oracle: y[m, n] = sum_k x[m, k] * dequant(W)[n, k], accumulated in f64 */
 int oracle_qmatmul_f64(int qtype, const uint8_t* blocks, const float* x,
                        int64_t m, int64_t n, int64_t k, double* y, int nthreads);
 
-/* candle CPU semantics (timing baseline): x rows -> Q8_0, integer block dots,
- * f32 accumulation of isum * d_w * d_x, parallel over N in column chunks */
+/* candle CPU semantics (timing baseline; Q4_0 and Q8_0): x rows -> Q8_0, integer
+ * block dots, f32 accumulation of isum * d_w * d_x, parallel over N in column chunks */
 int oracle_candle_qmatmul(int qtype, const uint8_t* blocks, const float* x,
                           int64_t m, int64_t n, int64_t k, float* y, int nthreads);
 

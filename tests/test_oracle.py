@@ -232,3 +232,175 @@ def test_fill_normal_is_deterministic_and_normal():
     assert np.array_equal(a, b)
     assert abs(float(a.mean())) < 0.01 and abs(float(a.std()) - 1.0) < 0.01
     assert not np.array_equal(a[:1000], oracle.normal(1000, seed=6))
+
+
+# ---- Q4_K / Q6_K (GGML block_q4_K / block_q6_K) ---------------------------------------------
+
+from oracle import Q4_K, Q6_K  # noqa: E402
+
+
+def _q4k_block(d, dmin, sc, m, qs) -> np.ndarray:
+    b = np.zeros(144, np.uint8)
+    b[0:2] = np.array([d], np.float16).view(np.uint8)
+    b[2:4] = np.array([dmin], np.float16).view(np.uint8)
+    b[4:16] = oracle.pack_q4_k_scales(sc, m)
+    b[16:] = np.asarray(qs, np.uint8)
+    return b
+
+
+def test_q4_k_code_positions_one_hot():
+    # d = 1, every scale 1, every min 0: weight = code.  Byte b of qs, low nibble
+    # -> weight 64 (b // 32) + b % 32; high nibble -> the same + 32.
+    blocks = []
+    want = np.zeros((256, 256), np.float32)
+    for case in range(256):
+        b, hi = case // 2, case % 2
+        qs = np.zeros(128, np.uint8)
+        qs[b] = 0x50 if hi else 0x05
+        blocks.append(_q4k_block(1.0, 0.0, [1] * 8, [0] * 8, qs))
+        want[case, 64 * (b // 32) + b % 32 + 32 * hi] = 5.0
+    got = oracle.dequant(Q4_K, np.stack(blocks), 256, 256)
+    assert np.array_equal(got, want)
+
+
+def test_q4_k_scale_and_min_per_sub_block():
+    # every code 1, scale of sub-block j = j + 1: weights 32 j .. 32 j + 31 = j + 1
+    got = oracle.dequant(Q4_K, _q4k_block(1.0, 0.0, range(1, 9), [0] * 8, [0x11] * 128), 1, 256)
+    assert np.array_equal(got[0], np.repeat(np.arange(1, 9, dtype=np.float32), 32))
+    # every code 0, dmin 1, min of sub-block j = 2 j + 1: weights = -(2 j + 1)
+    got = oracle.dequant(Q4_K, _q4k_block(1.0, 1.0, [1] * 8, range(1, 17, 2), [0] * 128), 1, 256)
+    assert np.array_equal(got[0], -np.repeat(np.arange(1, 17, 2, dtype=np.float32), 32))
+
+
+def test_q4_k_scale_packing_inverse_of_ggml_packer():
+    # all 64 x 64 (scale, min) values in every sub-block position, the other
+    # positions random: the oracle's unpacking must return exactly what GGML's
+    # packer stored (codes 1 and 0 read back the scale and the min separately)
+    rng = np.random.default_rng(3)
+    for j in range(8):
+        blocks1, blocks0, want_sc, want_m = [], [], [], []
+        for v in range(64 * 64):
+            sc = rng.integers(0, 64, 8)
+            m = rng.integers(0, 64, 8)
+            sc[j], m[j] = v // 64, v % 64
+            blocks1.append(_q4k_block(1.0, 0.0, sc, m, [0x11] * 128))
+            blocks0.append(_q4k_block(1.0, 1.0, sc, m, [0x00] * 128))
+            want_sc.append(sc[j])
+            want_m.append(m[j])
+        s = oracle.dequant(Q4_K, np.stack(blocks1), 4096, 256)[:, 32 * j:32 * j + 32]
+        mn = oracle.dequant(Q4_K, np.stack(blocks0), 4096, 256)[:, 32 * j:32 * j + 32]
+        assert np.array_equal(s, np.repeat(np.array(want_sc, np.float32)[:, None], 32, 1))
+        assert np.array_equal(mn, -np.repeat(np.array(want_m, np.float32)[:, None], 32, 1))
+
+
+def _numpy_q4_k(blocks: np.ndarray) -> np.ndarray:
+    """Independent vectorised decoding: 6-bit fields by bit position, codes by
+    reshaping qs to [4 groups][32 bytes] (low nibbles first)."""
+    b = blocks.reshape(-1, 144)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    dmin = b[:, 2:4].copy().view(np.float16).astype(np.float32)[:, 0]
+    bits = np.unpackbits(b[:, 4:16], axis=1, bitorder="little")  # [nb, 96], bit i of byte i // 8
+    def field(byte, lo, width):
+        return sum(bits[:, 8 * byte + lo + t].astype(np.int64) << t for t in range(width))
+    sc = np.stack([field(j, 0, 6) if j < 4 else field(j + 4, 0, 4) | (field(j - 4, 6, 2) << 4)
+                   for j in range(8)], 1)
+    m = np.stack([field(j + 4, 0, 6) if j < 4 else field(j + 4, 4, 4) | (field(j, 6, 2) << 4)
+                  for j in range(8)], 1)
+    q = b[:, 16:].reshape(-1, 4, 32)
+    codes = np.concatenate([q & 15, q >> 4], axis=2).reshape(-1, 8, 32).astype(np.float32)
+    s1 = (d[:, None] * sc.astype(np.float32))[:, :, None]
+    m1 = (dmin[:, None] * m.astype(np.float32))[:, :, None]
+    return (s1 * codes - m1).astype(np.float32).reshape(-1, 256)
+
+
+def test_q4_k_random_blocks_match_numpy_decoder():
+    blocks = oracle.random_q4_k(64, 1024, seed=9)
+    got = oracle.dequant(Q4_K, blocks, 64, 1024)
+    assert np.array_equal(got.reshape(-1, 256), _numpy_q4_k(blocks))
+
+
+def _q6k_block(d, sc, ql, qh) -> np.ndarray:
+    b = np.zeros(210, np.uint8)
+    b[0:128] = np.asarray(ql, np.uint8)
+    b[128:192] = np.asarray(qh, np.uint8)
+    b[192:208] = np.asarray(sc, np.int8).view(np.uint8)
+    b[208:210] = np.array([d], np.float16).view(np.uint8)
+    return b
+
+
+def test_q6_k_code_positions_one_hot():
+    # d = 1, scales 1, all codes 32 (weight 0) except one field.  ql byte
+    # 64 h + c: low nibble -> weight 128 h + c, high -> + 64 (c < 32 covers
+    # weights c, c + 64; c >= 32 covers c, c + 64 as well: l + 32 and l + 96);
+    # qh byte 32 h + l, bit pair t -> weight 128 h + l + 32 t.
+    cases, want = [], []
+    base_ql, base_qh = np.zeros(128, np.uint8), np.full(64, 0xAA, np.uint8)  # q = 0 | 2 << 4 = 32
+    for h in range(2):
+        for c in range(64):
+            for hi in range(2):
+                ql = base_ql.copy()
+                ql[64 * h + c] = 0x70 if hi else 0x07
+                cases.append(_q6k_block(1.0, [1] * 16, ql, base_qh))
+                e = np.zeros(256, np.float32)
+                e[128 * h + c + 64 * hi] = 7.0
+                want.append(e)
+        for l in range(32):
+            for t in range(4):
+                qh = base_qh.copy()
+                qh[32 * h + l] = (0xAA & ~(3 << (2 * t))) | (3 << (2 * t))  # that pair 3: q = 48
+                cases.append(_q6k_block(1.0, [1] * 16, base_ql, qh))
+                e = np.zeros(256, np.float32)
+                e[128 * h + l + 32 * t] = 16.0
+                want.append(e)
+    got = oracle.dequant(Q6_K, np.stack(cases), len(cases), 256)
+    assert np.array_equal(got, np.stack(want))
+
+
+def test_q6_k_scale_per_16_weights():
+    # codes all 33 (weight = scale), scale s -> weights 16 s .. 16 s + 15 in the
+    # order GGML indexes them: weight l + 32 t of half h uses scales[8 h + l // 16 + 2 t]
+    sc = np.arange(1, 17, dtype=np.int8) * np.array([1, -1] * 8, np.int8)
+    got = oracle.dequant(Q6_K, _q6k_block(1.0, sc, [0x11] * 128, [0xAA] * 64), 1, 256)[0]
+    want = np.empty(256, np.float32)
+    for e in range(256):
+        h, r = divmod(e, 128)
+        want[e] = sc[8 * h + (r % 32) // 16 + 2 * (r // 32)]
+    assert np.array_equal(got, want)
+
+
+def _numpy_q6_k(blocks: np.ndarray) -> np.ndarray:
+    b = blocks.reshape(-1, 210)
+    d = b[:, 208:210].copy().view(np.float16).astype(np.float32)[:, 0]
+    sc = b[:, 192:208].view(np.int8).astype(np.float32).reshape(-1, 2, 4, 2)  # [h][t][l // 16]
+    ql = b[:, 0:128].reshape(-1, 2, 2, 32)   # [h][which 32][l]
+    qh = b[:, 128:192].reshape(-1, 2, 32)    # [h][l]
+    lo = np.stack([ql[:, :, 0] & 15, ql[:, :, 1] & 15, ql[:, :, 0] >> 4, ql[:, :, 1] >> 4], 2)
+    hb = np.stack([(qh >> (2 * t)) & 3 for t in range(4)], 2)
+    q = (lo.astype(np.int32) | (hb.astype(np.int32) << 4)) - 32        # [nb][h][t][l]
+    s = np.repeat(sc, 16, axis=3)                                        # [nb][h][t][l]
+    return ((d[:, None, None, None] * s) * q.astype(np.float32)).astype(np.float32).reshape(-1, 256)
+
+
+def test_q6_k_random_blocks_match_numpy_decoder():
+    blocks = oracle.random_q6_k(64, 1024, seed=10)
+    got = oracle.dequant(Q6_K, blocks, 64, 1024)
+    assert np.array_equal(got.reshape(-1, 256), _numpy_q6_k(blocks))
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+def test_qmatmul_f64_k_quants_match_numpy_float64(qtype):
+    n, k, m = 29, 512, 3
+    gen = oracle.random_q4_k if qtype == Q4_K else oracle.random_q6_k
+    blocks = gen(n, k, seed=12)
+    x = oracle.normal(m * k, seed=13).reshape(m, k)
+    want = x.astype(np.float64) @ oracle.dequant(qtype, blocks, n, k).astype(np.float64).T
+    np.testing.assert_allclose(oracle.qmatmul_f64(qtype, blocks, x, n, k), want,
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_k_quants_rejected_by_q8_paths():
+    w = np.zeros((1, 256), np.float32)
+    with pytest.raises(ValueError):
+        oracle.quantize(Q4_K, w)
+    with pytest.raises(ValueError):
+        oracle.candle_qmatmul(Q4_K, oracle.random_q4_k(1, 256, 0), w, 1, 256)

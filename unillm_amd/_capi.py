@@ -14,8 +14,9 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "unillm_hip.h")
 
 Q4_0 = 2
 Q8_0 = 8
+Q4_K = 12
 QK = 32
-BLOCK_BYTES = {Q4_0: 18, Q8_0: 34}
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 18}  # GGUF bytes per 32 weights (Q4_K: 144 / 256)
 
 PATH_AUTO = 0
 PATH_GEMV = 1

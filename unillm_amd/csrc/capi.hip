@@ -74,16 +74,20 @@ int ensure_init() {
     return g_init_status;
 }
 
-bool valid_qtype(int q) { return q == UNILLM_QTYPE_Q4_0 || q == UNILLM_QTYPE_Q8_0; }
+bool valid_qtype(int q) {
+    return q == UNILLM_QTYPE_Q4_0 || q == UNILLM_QTYPE_Q8_0 || q == UNILLM_QTYPE_Q4_K;
+}
 
 int check_shape(int qtype, int64_t n, int64_t k) {
     if (!valid_qtype(qtype))
-        return fail(UNILLM_ERR_UNSUPPORTED,
-                    "unsupported qtype " + std::to_string(qtype) + " (want 2 = Q4_0, 8 = Q8_0)");
-    if (n < 1 || k < QK || k % QK != 0)
+        return fail(UNILLM_ERR_UNSUPPORTED, "unsupported qtype " + std::to_string(qtype) +
+                                                " (want 2 = Q4_0, 8 = Q8_0, 12 = Q4_K)");
+    const int64_t blk = qtype == UNILLM_QTYPE_Q4_K ? 256 : QK;
+    if (n < 1 || k < blk || k % blk != 0)
         return fail(UNILLM_ERR_INVALID_ARG, "bad weight shape [" + std::to_string(n) + ", " +
                                                 std::to_string(k) +
-                                                "]: need n >= 1 and k a positive multiple of 32");
+                                                "]: need n >= 1 and k a positive multiple of " +
+                                                std::to_string(blk));
     if (n > (int64_t)INT32_MAX || k / QK > (int64_t)INT32_MAX / 4)
         return fail(UNILLM_ERR_INVALID_ARG, "weight shape too large");
     return UNILLM_OK;
@@ -126,18 +130,22 @@ int alloc_weight(int qtype, int64_t n, int64_t k, QWeight** out) {
 // Synchronises `s`.
 int finish_weight(QWeight* w, hipStream_t s) {
     uint32_t* slot = reinterpret_cast<uint32_t*>(w->base + w->bytes - 256);
-    uint32_t bits = 0;
+    uint32_t bits[2] = {0, 0};
     hipError_t e;
-    if ((e = hipMemsetAsync(slot, 0, sizeof(uint32_t), s)) != hipSuccess)
+    if ((e = hipMemsetAsync(slot, 0, sizeof(bits), s)) != hipSuccess)
         return fail_hip(e, "hipMemsetAsync");
     if ((e = launch_scale_absmax(*w, slot, s)) != hipSuccess) return fail_hip(e, "scale scan");
-    if ((e = hipMemcpyAsync(&bits, slot, sizeof(bits), hipMemcpyDeviceToHost, s)) != hipSuccess)
+    if ((e = hipMemcpyAsync(bits, slot, sizeof(bits), hipMemcpyDeviceToHost, s)) != hipSuccess)
         return fail_hip(e, "hipMemcpyAsync");
     if ((e = hipStreamSynchronize(s)) != hipSuccess) return fail_hip(e, "weight upload");
-    // |code| <= 8 (Q4_0) or 128 (Q8_0); f16 holds magnitudes up to 65504
-    const float dmax = __half2float(__ushort_as_half((unsigned short)(bits > 0x7BFFu ? 0x7BFFu
-                                                                                    : bits)));
-    const float wmax = dmax * (w->qtype == UNILLM_QTYPE_Q4_0 ? 8.0f : 128.0f);
+    auto f16max = [](uint32_t b) {  // finite f16 magnitude bits -> float (inf/nan clamp to max)
+        return __half2float(__ushort_as_half((unsigned short)(b > 0x7BFFu ? 0x7BFFu : b)));
+    };
+    // |code| <= 8 (Q4_0) or 128 (Q8_0); Q4_K: |(d sc) q - dmin m| <= 63 (15 |d| + |dmin|);
+    // f16 holds magnitudes up to 65504
+    const float wmax = w->qtype == UNILLM_QTYPE_Q4_K
+                           ? 63.0f * (15.0f * f16max(bits[0]) + f16max(bits[1]))
+                           : f16max(bits[0]) * (w->qtype == UNILLM_QTYPE_Q4_0 ? 8.0f : 128.0f);
     // the largest power-of-two scaling that keeps every dequantized weight in
     // f16 range: small scales stay normal in f16 (also divided by 16)
     int E = 0;
@@ -298,6 +306,7 @@ int unillm_hip_qweight_info(const unillm_qweight* w, int* qtype, int64_t* n, int
 int unillm_hip_select_path(const unillm_qweight* w, int64_t m) {
     if (!w || m < 0) return fail(UNILLM_ERR_INVALID_ARG, "bad arguments to select_path");
     if (gemv_supports(*w, m)) return UNILLM_PATH_GEMV;
+    if (w->qtype == UNILLM_QTYPE_Q4_K) return UNILLM_PATH_GEMV;  // the only Q4_K path so far
     if (m <= kDecodeMaxM) return UNILLM_PATH_DECODE_MFMA;
     return UNILLM_PATH_PREFILL_MFMA;
 }
@@ -314,6 +323,9 @@ int unillm_hip_qmatmul_path(const unillm_qweight* w, const float* x_dev, int64_t
     if (m > (int64_t)INT32_MAX / 2)
         return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: m too large");
     if (path == UNILLM_PATH_AUTO) path = unillm_hip_select_path(w, m);
+    if (w->qtype == UNILLM_QTYPE_Q4_K && path != UNILLM_PATH_GEMV)
+        return fail(UNILLM_ERR_UNSUPPORTED,
+                    "QMatMul forward failed: Q4_K weights run on the GEMV path only (m <= 4)");
     if (int rc = ensure_init()) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipError_t e;

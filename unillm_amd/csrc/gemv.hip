@@ -125,10 +125,19 @@ __device__ __forceinline__ float quad_absmax(const float (&v)[8]) {
 // The math runs on every thread and only the stores are conditional, so the
 // compiler keeps the x loads where they are issued.
 
-// Q4_0: v[2i] = x[4t + i], v[2i + 1] = x[16 + 4t + i] (i = 0..3).
+// Q4_0: v[2i] = x[4t + i], v[2i + 1] = x[16 + 4t + i] (i = 0..3).  SUM (Q4_K):
+// dword 17 = the block's sum of x, for the term (8 d sc - dmin m) sum x.
+template <bool SUM = false>
 __device__ __forceinline__ void prep_q4(const float (&v)[8], int t, bool store,
                                         uint32_t* __restrict__ dst) {
     const float amax = quad_absmax(v);
+    float xsum = 0.0f;
+    if constexpr (SUM) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xsum += v[j];
+        xsum += dpp_f32<0xB1>(xsum);
+        xsum += dpp_f32<0x4E>(xsum);
+    }
     // s = 2^e with max|x| / 7 < s: frexp gives max|x| / 7 = f * 2^e, f in [0.5, 1);
     // e >= -100 keeps 2^(12 - e) finite (blocks below 2^-100 round to zero)
     int e = 0;
@@ -163,6 +172,7 @@ __device__ __forceinline__ void prep_q4(const float (&v)[8], int t, bool store,
     dst[8 + t] = d1;
     dst[12 + t] = d0;
     if (t == 0) dst[16] = __float_as_uint(amax > 0.0f ? ldexpf(1.0f, e - 12) : 0.0f);
+    if (SUM && t == 0) dst[17] = __float_as_uint(xsum);
 }
 
 // Q8_0: v[j] = x[8u + j], u = quarter 0..3.
@@ -194,7 +204,7 @@ __device__ __forceinline__ void prep_q8(const float (&v)[8], int u, bool store,
 // The x elements a prep thread handles (q = 4 * block + quarter), as two float4 offsets.
 template <int QT>
 __device__ __forceinline__ void quarter_offsets(int quarter, int& o0, int& o1) {
-    if constexpr (QT == UNILLM_QTYPE_Q4_0) {
+    if constexpr (QT != UNILLM_QTYPE_Q8_0) {
         o0 = 4 * quarter;       // x[4t .. 4t+3]
         o1 = 16 + 4 * quarter;  // x[16+4t .. 16+4t+3]
     } else {
@@ -208,19 +218,22 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 struct XBlock {
     u32x4 dg[4];  // 16 digit dwords, in record order
     float sx;     // 0 for a lane's clamped (duplicate) block
+    float xsum;   // Q4_K: sum of the block's x (0 for a clamped block)
 };
 
+template <int QT>
 __device__ __forceinline__ void load_xblock(const uint32_t* __restrict__ src, bool valid,
                                             XBlock& o) {
     const u32x4* p = reinterpret_cast<const u32x4*>(src);
 #pragma unroll
     for (int i = 0; i < 4; ++i) o.dg[i] = p[i];
     o.sx = valid ? __uint_as_float(src[16]) : 0.0f;
+    o.xsum = QT == UNILLM_QTYPE_Q4_K && valid ? __uint_as_float(src[17]) : 0.0f;
 }
 
 // A wave's x records: read once from LDS into registers (M * NB records,
 // 17 VGPRs each) and reused for every row of the wave.
-template <int M, int NB>
+template <int QT, int M, int NB>
 struct XRegs {
     XBlock xb[M][NB];
     __device__ __forceinline__ XRegs(const uint32_t* xlds, int KB, const int (&bidx)[NB],
@@ -229,20 +242,21 @@ struct XRegs {
         for (int m = 0; m < M; ++m)
 #pragma unroll
             for (int i = 0; i < NB; ++i)
-                load_xblock(xlds + ((size_t)m * KB + bidx[i]) * kXWords, bval[i], xb[m][i]);
+                load_xblock<QT>(xlds + ((size_t)m * KB + bidx[i]) * kXWords, bval[i], xb[m][i]);
     }
 };
 
 // ---- weights --------------------------------------------------------------------------------
 template <int QT>
 struct Payload {
-    static constexpr int V = QT == UNILLM_QTYPE_Q4_0 ? 1 : 2;  // 128-bit loads per block
+    static constexpr int V = QT == UNILLM_QTYPE_Q8_0 ? 2 : 1;  // 128-bit loads per block
 };
 
 template <int QT, int NB, int R>
 struct Chunk {
     u32x4 q[R][NB][Payload<QT>::V];
-    uint16_t d[R][NB];
+    uint16_t d[R][NB];  // f16 d; Q4_K: sc | m << 8
+    uint32_t h[R][NB];  // Q4_K: d | dmin << 16 of the block's 256-weight group
 };
 
 // Weight addresses: base + row * rb + a lane offset, with the row offset
@@ -263,7 +277,8 @@ struct Chunk {
 template <int QT, int NB, int R>
 __device__ __forceinline__ void load_chunk(Chunk<QT, NB, R>& c, const uint8_t* __restrict__ base,
                                            uint32_t rb, int w, int W, int j0, int jlast,
-                                           const uint32_t (&poff)[NB], const uint32_t (&soff)[NB]) {
+                                           const uint32_t (&poff)[NB], const uint32_t (&soff)[NB],
+                                           const uint32_t (&hoff)[NB]) {
     constexpr int V = Payload<QT>::V;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -276,12 +291,14 @@ __device__ __forceinline__ void load_chunk(Chunk<QT, NB, R>& c, const uint8_t* _
                 c.q[r][i][v] = __builtin_nontemporal_load(
                     reinterpret_cast<const u32x4*>(base + ro + poff[i]) + v);
             c.d[r][i] = *reinterpret_cast<const uint16_t*>(base + ro + soff[i]);
+            if constexpr (QT == UNILLM_QTYPE_Q4_K)
+                c.h[r][i] = *reinterpret_cast<const uint32_t*>(base + ro + hoff[i]);
         }
     }
 }
 
 template <int QT, int M, int NB, int R>
-__device__ __forceinline__ void compute_chunk(const Chunk<QT, NB, R>& c, const XRegs<M, NB>& xs,
+__device__ __forceinline__ void compute_chunk(const Chunk<QT, NB, R>& c, const XRegs<QT, M, NB>& xs,
                                               float* __restrict__ y, int w, int W, int j0,
                                               int jcount, int N, int lane, int m_real) {
     float part[M][R];
@@ -297,7 +314,7 @@ __device__ __forceinline__ void compute_chunk(const Chunk<QT, NB, R>& c, const X
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 int acc;
-                if constexpr (QT == UNILLM_QTYPE_Q4_0) {
+                if constexpr (QT != UNILLM_QTYPE_Q8_0) {
                     // digit levels 3..0: A = ((a3 * 16 + a2) * 16 + a1) * 16 + a0
                     const u32x4 w4 = c.q[r][i][0];
                     int lv[4] = {0, 0, 0, 0};
@@ -319,8 +336,17 @@ __device__ __forceinline__ void compute_chunk(const Chunk<QT, NB, R>& c, const X
                     }
                     acc = a0 * 254 + a1;
                 }
-                const float dw = __half2float(__ushort_as_half(c.d[r][i]));
-                part[m][r] = fmaf(dw, (float)acc * xb.sx, part[m][r]);
+                if constexpr (QT == UNILLM_QTYPE_Q4_K) {
+                    // (d sc) (acc sx + 8 sum x) - (dmin m) sum x: acc is sum (q - 8) x
+                    const uint32_t h = c.h[r][i], sm = c.d[r][i];
+                    const float s = __half2float(__ushort_as_half((uint16_t)h)) * (float)(sm & 0xFFu);
+                    const float o = __half2float(__ushort_as_half((uint16_t)(h >> 16))) * (float)(sm >> 8);
+                    const float t = fmaf((float)acc, xb.sx, 8.0f * xb.xsum);
+                    part[m][r] = fmaf(-o, xb.xsum, fmaf(s, t, part[m][r]));
+                } else {
+                    const float dw = __half2float(__ushort_as_half(c.d[r][i]));
+                    part[m][r] = fmaf(dw, (float)acc * xb.sx, part[m][r]);
+                }
             }
         }
 #pragma unroll
@@ -369,7 +395,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
 
     int bidx[NB];
     bool bval[NB];
-    uint32_t poff[NB], soff[NB];  // this lane's byte offsets inside a row
+    uint32_t poff[NB], soff[NB], hoff[NB];  // this lane's byte offsets inside a row
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         const int b = i * 64 + lane;
@@ -377,6 +403,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
         bidx[i] = min(b, KB - 1);
         poff[i] = (uint32_t)bidx[i] * (16 * Payload<QT>::V);
         soff[i] = (uint32_t)KB * (16 * Payload<QT>::V) + 2u * (uint32_t)bidx[i];
+        hoff[i] = (uint32_t)KB * 18u + 4u * (uint32_t)(bidx[i] >> 3);  // Q4_K group header
     }
 
     // 1. x for the digits.  A wave whose quarters of a pass all lie past nq
@@ -396,7 +423,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
         quarter_offsets<QT>(q & 3, o0, o1);
         const float4 f0 = *reinterpret_cast<const float4*>(xb + o0);
         const float4 f1 = *reinterpret_cast<const float4*>(xb + o1);
-        if constexpr (QT == UNILLM_QTYPE_Q4_0) {  // payload nibble order
+        if constexpr (QT != UNILLM_QTYPE_Q8_0) {  // payload nibble order
             v[p][0] = f0.x; v[p][1] = f1.x; v[p][2] = f0.y; v[p][3] = f1.y;
             v[p][4] = f0.z; v[p][5] = f1.z; v[p][6] = f0.w; v[p][7] = f1.w;
         } else {
@@ -411,7 +438,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     //    up, everything behind them (here: the digit work every row needs)
     //    waits until they are accepted.
     Chunk<QT, NB, R> a, b;
-    load_chunk<QT, NB, R>(a, base, (uint32_t)rb, wrow, waves, 0, jlast, poff, soff);
+    load_chunk<QT, NB, R>(a, base, (uint32_t)rb, wrow, waves, 0, jlast, poff, soff, hoff);
 
     // 3. x digit records for all M * KB blocks, four threads per block (threads
     //    past nq compute on a clamped copy and store nothing; nq is a multiple
@@ -421,15 +448,15 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
         if (wave0 + p * THREADS >= nq) continue;
         const int q = threadIdx.x + p * THREADS;
         uint32_t* dst = xlds + (size_t)(min(q, nq - 1) >> 2) * kXWords;
-        if constexpr (QT == UNILLM_QTYPE_Q4_0) prep_q4(v[p], q & 3, q < nq, dst);
-        else prep_q8(v[p], q & 3, q < nq, dst);
+        if constexpr (QT == UNILLM_QTYPE_Q8_0) prep_q8(v[p], q & 3, q < nq, dst);
+        else prep_q4<QT == UNILLM_QTYPE_Q4_K>(v[p], q & 3, q < nq, dst);
         __builtin_amdgcn_sched_barrier(0);  // one pass's temporaries live at a time
     }
     __syncthreads();
 
 
     // 4. this lane's records, read once from LDS into registers for all rows
-    const XRegs<M, NB> xs(xlds, KB, bidx, bval);
+    const XRegs<QT, M, NB> xs(xlds, KB, bidx, bval);
     __builtin_amdgcn_sched_barrier(0);
 
     // 5. with more rows than one chunk: request the second chunk, then compute
@@ -437,12 +464,12 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     //    branch is wave-uniform and each side has its own memory waits (a
     //    shared join would make the wait for chunk a cover chunk b as well).
     if (jcount > R) {
-        load_chunk<QT, NB, R>(b, base, (uint32_t)rb, wrow, waves, R, jlast, poff, soff);
+        load_chunk<QT, NB, R>(b, base, (uint32_t)rb, wrow, waves, R, jlast, poff, soff, hoff);
         compute_chunk<QT, M, NB, R>(a, xs, y, wrow, waves, 0, jcount, N, lane, m_real);
         compute_chunk<QT, M, NB, R>(b, xs, y, wrow, waves, R, jcount, N, lane, m_real);
         for (int j = 2 * R; j < jcount; j += 2 * R) {
-            load_chunk<QT, NB, R>(a, base, (uint32_t)rb, wrow, waves, j, jlast, poff, soff);
-            load_chunk<QT, NB, R>(b, base, (uint32_t)rb, wrow, waves, j + R, jlast, poff, soff);
+            load_chunk<QT, NB, R>(a, base, (uint32_t)rb, wrow, waves, j, jlast, poff, soff, hoff);
+            load_chunk<QT, NB, R>(b, base, (uint32_t)rb, wrow, waves, j + R, jlast, poff, soff, hoff);
             compute_chunk<QT, M, NB, R>(a, xs, y, wrow, waves, j, jcount, N, lane, m_real);
             compute_chunk<QT, M, NB, R>(b, xs, y, wrow, waves, j + R, jcount, N, lane, m_real);
         }
@@ -501,9 +528,9 @@ hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipSt
         case 2: return launch_nb<QT, M, 2>(w, x, m, y, st);
         case 3: if constexpr (M <= 2) return launch_nb<QT, M, 3>(w, x, m, y, st); break;
         case 4: if constexpr (M <= 2) return launch_nb<QT, M, 4>(w, x, m, y, st); break;
-        case 5: if constexpr (M == 1 && QT == UNILLM_QTYPE_Q4_0) return launch_nb<QT, M, 5>(w, x, m, y, st); break;
-        case 6: if constexpr (M == 1 && QT == UNILLM_QTYPE_Q4_0) return launch_nb<QT, M, 6>(w, x, m, y, st); break;
-        case 7: if constexpr (M == 1 && QT == UNILLM_QTYPE_Q4_0) return launch_nb<QT, M, 7>(w, x, m, y, st); break;
+        case 5: if constexpr (M == 1 && QT != UNILLM_QTYPE_Q8_0) return launch_nb<QT, M, 5>(w, x, m, y, st); break;
+        case 6: if constexpr (M == 1 && QT != UNILLM_QTYPE_Q8_0) return launch_nb<QT, M, 6>(w, x, m, y, st); break;
+        case 7: if constexpr (M == 1 && QT != UNILLM_QTYPE_Q8_0) return launch_nb<QT, M, 7>(w, x, m, y, st); break;
         default: break;
     }
     return hipErrorInvalidValue;
@@ -528,6 +555,11 @@ bool gemv_supports(const QWeight& w, int64_t m) {
 }
 
 hipError_t launch_gemv(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t s) {
+    if (w.qtype == UNILLM_QTYPE_Q4_K) {
+        if (m == 1) return launch_m<UNILLM_QTYPE_Q4_K, 1>(w, x, m, y, s);
+        if (m == 2) return launch_m<UNILLM_QTYPE_Q4_K, 2>(w, x, m, y, s);
+        return launch_m<UNILLM_QTYPE_Q4_K, 4>(w, x, m, y, s);
+    }
     if (w.qtype == UNILLM_QTYPE_Q4_0) {
         if (m == 1) return launch_m<UNILLM_QTYPE_Q4_0, 1>(w, x, m, y, s);
         if (m == 2) return launch_m<UNILLM_QTYPE_Q4_0, 2>(w, x, m, y, s);

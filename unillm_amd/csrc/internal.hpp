@@ -12,6 +12,15 @@
 // them (measured: cheaper to stream than a separate scale plane).  The byte
 // count is GGUF's (18 or 34 B per 32 weights) plus at most 15 B of row
 // padding; dequant of this layout is bit-exact with the GGUF bytes.
+//
+// Q4_K (GGML block_q4_K: 256 weights = 8 sub-blocks of 32 under one f16 d and
+// one f16 dmin, 6-bit scale sc_j and min m_j per sub-block) is repacked into the
+// same frame, one 32-weight sub-block per block:
+//   [kb x 16 B payload][kb x u16 (sc | m << 8)][kb / 8 x u32 (d | dmin << 16)][pad]
+// The payload is the sub-block's 32 codes q in Q4_0's order and form (signed
+// q - 8; element j low nibble of byte j, element j + 16 high nibble), so
+// w = (d sc) q - dmin m = (d sc)(q - 8) + (8 d sc - dmin m).  18.5 B per 32
+// weights against GGUF's 18; d sc and dmin m are exact in f32.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -40,9 +49,10 @@ using QWeight = ::unillm_qweight;
 int64_t gemv_max_kb(int64_t m, int qtype);
 bool gemv_supports(const unillm_qweight& w, int64_t m);
 
-inline int qbytes(int qtype) { return qtype == UNILLM_QTYPE_Q4_0 ? 16 : 32; }
+inline int qbytes(int qtype) { return qtype == UNILLM_QTYPE_Q8_0 ? 32 : 16; }
 inline int64_t row_bytes_for(int qtype, int64_t kb) {
-    return (kb * (qbytes(qtype) + 2) + 15) / 16 * 16;
+    const int64_t hdr = qtype == UNILLM_QTYPE_Q4_K ? kb / 8 * 4 : 0;
+    return (kb * (qbytes(qtype) + 2) + hdr + 15) / 16 * 16;
 }
 
 // Addresses inside a row (QB = payload bytes per block).
@@ -56,7 +66,13 @@ __host__ __device__ __forceinline__ const uint16_t* blk_scale(const uint8_t* bas
                                                                int64_t kb, int64_t row, int64_t b) {
     return reinterpret_cast<const uint16_t*>(base + row * rb + kb * QB) + b;
 }
-inline int gguf_block_bytes(int qtype) { return qtype == UNILLM_QTYPE_Q4_0 ? 18 : 34; }
+// Q4_K: the u32 (d | dmin << 16) of the 256-weight group holding block b.
+__host__ __device__ __forceinline__ const uint32_t* q4k_header(const uint8_t* base, int64_t rb,
+                                                               int64_t kb, int64_t row, int64_t b) {
+    return reinterpret_cast<const uint32_t*>(base + row * rb + kb * 18) + (b >> 3);
+}
+// GGUF bytes per 32 weights: 18 (Q4_0, and Q4_K's 144 per 256), 34 (Q8_0)
+inline int gguf_block_bytes(int qtype) { return qtype == UNILLM_QTYPE_Q8_0 ? 34 : 18; }
 
 // Per-device properties cached at init.
 struct DeviceInfo {
@@ -78,7 +94,8 @@ bool debug_launch();
 // All return a hipError_t from the launch; shapes are validated by the caller.
 hipError_t launch_repack(const QWeight& w, const uint8_t* gguf, hipStream_t s);
 hipError_t launch_dequant(const QWeight& w, float* out, hipStream_t s);
-// max over the scale plane of (f16 bits & 0x7FFF), atomically max-ed into *out
+// max over the scale plane of (f16 bits & 0x7FFF), atomically max-ed into out[0]
+// (Q4_K: max |d| into out[0], max |dmin| into out[1])
 hipError_t launch_scale_absmax(const QWeight& w, uint32_t* out, hipStream_t s);
 hipError_t launch_quantize(int qtype, const float* w, int64_t n, int64_t k, uint8_t* out,
                            hipStream_t s);

@@ -41,22 +41,94 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
         dst[v] = make_uint4(words[4 * v], words[4 * v + 1], words[4 * v + 2], words[4 * v + 3]);
 }
 
+// GGML get_scale_min_k4: 6-bit scale and min of sub-block j from scales[12].
+__device__ __forceinline__ void q4k_scale_min(int j, const uint8_t* q, uint32_t& sc, uint32_t& m) {
+    if (j < 4) {
+        sc = q[j] & 63u;
+        m = q[j + 4] & 63u;
+    } else {
+        sc = (q[j + 4] & 0x0Fu) | ((uint32_t)(q[j - 4] >> 6) << 4);
+        m = (uint32_t)(q[j + 4] >> 4) | ((uint32_t)(q[j] >> 6) << 4);
+    }
+}
+
+// One thread per 32-weight sub-block of GGUF Q4_K (144-byte blocks {f16 d;
+// f16 dmin; u8 scales[12]; u8 qs[128]}; 64-weight group g = j / 2 of a block
+// takes qs[32 g .. 32 g + 31], low nibbles for sub-block 2 g, high for 2 g + 1)
+// -> payload in Q4_0 order (signed q - 8), u16 (sc | m << 8), and for j = 0 the
+// group header u32 (d | dmin << 16).
+__global__ __launch_bounds__(256) void repack_q4k_kernel(const uint8_t* __restrict__ src,
+                                                         uint8_t* __restrict__ base, int64_t rb,
+                                                         int64_t kb, int64_t nblocks) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const int64_t row = i / kb, blk = i - row * kb;
+    const int j = (int)(blk & 7);
+    const uint8_t* b = src + (i >> 3) * 144;  // kb % 8 == 0: a row's groups are whole blocks
+    uint32_t sc, m;
+    q4k_scale_min(j, b + 4, sc, m);
+    *const_cast<uint16_t*>(blk_scale<16>(base, rb, kb, row, blk)) = (uint16_t)(sc | (m << 8));
+    if (j == 0)
+        *const_cast<uint32_t*>(q4k_header(base, rb, kb, row, blk)) =
+            (uint32_t)ld_u16(b) | ((uint32_t)ld_u16(b + 2) << 16);
+    const uint8_t* qs = b + 16 + 32 * (j >> 1);
+    const int sh = 4 * (j & 1);
+    uint32_t words[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int e = 4 * w + t;  // byte e: element e (low), element e + 16 (high)
+            const uint32_t lo = ((uint32_t)qs[e] >> sh) & 15u, hi = ((uint32_t)qs[e + 16] >> sh) & 15u;
+            v |= ((lo ^ 8u) | ((hi ^ 8u) << 4)) << (8 * t);
+        }
+        words[w] = v;
+    }
+    *reinterpret_cast<uint4*>(const_cast<uint8_t*>(blk_payload<16>(base, rb, row, blk))) =
+        make_uint4(words[0], words[1], words[2], words[3]);
+}
+
 // Exact dequant (GGML to_float): Q4_0 w[j] = (lo(qs[j]) - 8) * d,
 // w[j + 16] = (hi(qs[j]) - 8) * d (stored here as the signed nibbles q - 8);
 // Q8_0 w[j] = qs[j] * d.  One thread per
 // block.  Every product is exact in f32, so any evaluation order is bit-exact.
+// Q4_K (dequantize_row_q4_K): w = (d sc) q - dmin m with q = nibble + 8; d sc
+// and (d sc) q are exact in f32, so the subtraction is the one rounding, fused
+// into a multiply-add or not.
 template <int QT>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ base,
                                                       int64_t rb, int64_t kb,
                                                       float* __restrict__ out,
                                                       int64_t nblocks) {
-    constexpr int QB = QT == UNILLM_QTYPE_Q4_0 ? 16 : 32;
+    constexpr int QB = QT == UNILLM_QTYPE_Q8_0 ? 32 : 16;
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nblocks) return;
     const int64_t row = i / kb, blk = i - row * kb;
-    const float d = __half2float(__ushort_as_half(*blk_scale<QB>(base, rb, kb, row, blk)));
+    const uint16_t sw = *blk_scale<QB>(base, rb, kb, row, blk);
     const uint8_t* qs = blk_payload<QB>(base, rb, row, blk);
     float4* o = reinterpret_cast<float4*>(out + i * QK);
+    if constexpr (QT == UNILLM_QTYPE_Q4_K) {
+        const uint32_t h = *q4k_header(base, rb, kb, row, blk);
+        const float s = __half2float(__ushort_as_half((uint16_t)h)) * (float)(sw & 0xFFu);
+        const float mn = __half2float(__ushort_as_half((uint16_t)(h >> 16))) * (float)(sw >> 8);
+        const uint4 q = *reinterpret_cast<const uint4*>(qs);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            float lo[4], hi[4];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const uint32_t byte = (w[t] >> (8 * b)) & 0xFFu;
+                lo[b] = s * (float)((byte & 15u) ^ 8u) - mn;  // code q = (q - 8) ^ 8
+                hi[b] = s * (float)((byte >> 4) ^ 8u) - mn;
+            }
+            o[t] = make_float4(lo[0], lo[1], lo[2], lo[3]);
+            o[4 + t] = make_float4(hi[0], hi[1], hi[2], hi[3]);
+        }
+        return;
+    }
+    const float d = __half2float(__ushort_as_half(sw));
     if constexpr (QT == UNILLM_QTYPE_Q4_0) {
         const uint4 q = *reinterpret_cast<const uint4*>(qs);
         const uint32_t w[4] = {q.x, q.y, q.z, q.w};
@@ -169,6 +241,37 @@ __global__ __launch_bounds__(256) void scale_absmax_kernel(const uint8_t* __rest
     if (threadIdx.x == 0) atomicMax(out, part[0]);
 }
 
+// Q4_K: max |d| and max |dmin| over the group headers, as f16 magnitude bits.
+__global__ __launch_bounds__(256) void q4k_header_absmax_kernel(const uint8_t* __restrict__ base,
+                                                                int64_t rb, int64_t kb,
+                                                                int64_t count,
+                                                                uint32_t* __restrict__ out) {
+    __shared__ uint32_t part[2][256];
+    uint32_t md = 0, mm = 0;
+    const int64_t groups = kb / 8;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = i / groups;
+        const uint32_t h = *q4k_header(base, rb, kb, row, 8 * (i - row * groups));
+        md = max(md, h & 0x7FFFu);
+        mm = max(mm, (h >> 16) & 0x7FFFu);
+    }
+    part[0][threadIdx.x] = md;
+    part[1][threadIdx.x] = mm;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) {
+            part[0][threadIdx.x] = max(part[0][threadIdx.x], part[0][threadIdx.x + s]);
+            part[1][threadIdx.x] = max(part[1][threadIdx.x], part[1][threadIdx.x + s]);
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        atomicMax(out, part[0][0]);
+        atomicMax(out + 1, part[1][0]);
+    }
+}
+
 inline unsigned grid_for(int64_t items, int block) {
     return (unsigned)((items + block - 1) / block);
 }
@@ -177,7 +280,9 @@ inline unsigned grid_for(int64_t items, int block) {
 
 hipError_t launch_repack(const QWeight& w, const uint8_t* gguf, hipStream_t s) {
     const int64_t nb = w.n * w.kb;
-    if (w.qtype == UNILLM_QTYPE_Q4_0)
+    if (w.qtype == UNILLM_QTYPE_Q4_K)
+        repack_q4k_kernel<<<grid_for(nb, 256), 256, 0, s>>>(gguf, w.base, w.row_bytes, w.kb, nb);
+    else if (w.qtype == UNILLM_QTYPE_Q4_0)
         repack_kernel<16><<<grid_for(nb, 256), 256, 0, s>>>(gguf, w.base, w.row_bytes, w.kb, nb);
     else
         repack_kernel<32><<<grid_for(nb, 256), 256, 0, s>>>(gguf, w.base, w.row_bytes, w.kb, nb);
@@ -187,7 +292,9 @@ hipError_t launch_repack(const QWeight& w, const uint8_t* gguf, hipStream_t s) {
 hipError_t launch_scale_absmax(const QWeight& w, uint32_t* out, hipStream_t s) {
     const int64_t nb = w.n * w.kb;
     const unsigned grid = (unsigned)std::min<int64_t>(1024, (nb + 255) / 256);
-    if (w.qtype == UNILLM_QTYPE_Q4_0)
+    if (w.qtype == UNILLM_QTYPE_Q4_K)
+        q4k_header_absmax_kernel<<<grid, 256, 0, s>>>(w.base, w.row_bytes, w.kb, nb / 8, out);
+    else if (w.qtype == UNILLM_QTYPE_Q4_0)
         scale_absmax_kernel<16><<<grid, 256, 0, s>>>(w.base, w.row_bytes, w.kb, nb, out);
     else
         scale_absmax_kernel<32><<<grid, 256, 0, s>>>(w.base, w.row_bytes, w.kb, nb, out);
@@ -196,7 +303,10 @@ hipError_t launch_scale_absmax(const QWeight& w, uint32_t* out, hipStream_t s) {
 
 hipError_t launch_dequant(const QWeight& w, float* out, hipStream_t s) {
     const int64_t nb = w.n * w.kb;
-    if (w.qtype == UNILLM_QTYPE_Q4_0)
+    if (w.qtype == UNILLM_QTYPE_Q4_K)
+        dequant_kernel<UNILLM_QTYPE_Q4_K><<<grid_for(nb, 256), 256, 0, s>>>(w.base, w.row_bytes,
+                                                                            w.kb, out, nb);
+    else if (w.qtype == UNILLM_QTYPE_Q4_0)
         dequant_kernel<UNILLM_QTYPE_Q4_0><<<grid_for(nb, 256), 256, 0, s>>>(w.base, w.row_bytes,
                                                                             w.kb, out, nb);
     else
@@ -207,6 +317,7 @@ hipError_t launch_dequant(const QWeight& w, float* out, hipStream_t s) {
 
 hipError_t launch_quantize(int qtype, const float* w, int64_t n, int64_t k, uint8_t* out,
                            hipStream_t s) {
+    if (qtype != UNILLM_QTYPE_Q4_0 && qtype != UNILLM_QTYPE_Q8_0) return hipErrorInvalidValue;
     const int64_t nb = n * (k / QK);
     if (qtype == UNILLM_QTYPE_Q4_0)
         quantize_kernel<UNILLM_QTYPE_Q4_0><<<grid_for(nb, 256), 256, 0, s>>>(w, out, nb);

@@ -1,4 +1,4 @@
-"""QuantLinear: a device-resident GGUF Q4_0 / Q8_0 weight and its forward.
+"""QuantLinear: a device-resident GGUF Q4_0 / Q8_0 / Q4_K weight and its forward.
 
 It takes the slot that `Arc<QMatMul>` holds in unillm's
 `ModelWeights.quantized_tensors` (crates/runtime/src/model_core.rs:134) and
@@ -20,7 +20,7 @@ import numpy as np
 import torch
 
 from . import _capi
-from ._capi import BLOCK_BYTES, QK, Q4_0, Q8_0, HipError
+from ._capi import BLOCK_BYTES, QK, Q4_0, Q4_K, Q8_0, HipError
 
 
 def _stream_ptr(stream: torch.cuda.Stream | None) -> int:
@@ -40,7 +40,8 @@ class QuantLinear:
     # ---- construction (WeightLoaderCore's QMatMul::from_arc, weight_loader_core.rs:569)
     @classmethod
     def from_blocks(cls, qtype: int, n: int, k: int, blocks) -> "QuantLinear":
-        """From GGUF block bytes in host memory (n * k/32 blocks of 18 / 34 B)."""
+        """From GGUF block bytes in host memory (n * k/32 blocks of 18 / 34 B, or
+        n * k/256 blocks of 144 B for Q4_K)."""
         buf = np.ascontiguousarray(np.frombuffer(memoryview(blocks), dtype=np.uint8))
         h = ctypes.c_void_p()
         _capi.check(_capi.lib().unillm_hip_qweight_create(
@@ -134,7 +135,7 @@ class QuantLinear:
             pass
 
     def __repr__(self) -> str:
-        name = {Q4_0: "Q4_0", Q8_0: "Q8_0"}.get(self.qtype, str(self.qtype))
+        name = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K"}.get(self.qtype, str(self.qtype))
         return f"QuantLinear({name}, n={self.n}, k={self.k})"
 
 

@@ -1,8 +1,9 @@
 """GPU parity for Q4_K weights (GGML block_q4_K), through the C ABI, against the oracle.
 
 Bars as for Q4_0: dequant bit-exact with GGML's dequantize_row_q4_K (oracle
-restatement, pinned in tests/test_oracle.py); GEMV within 1e-3 normwise of the
-f64 matmul of the exactly dequantized weights.  Test weights are random valid
+restatement, pinned in tests/test_oracle.py); GEMV within 1e-3 and the bf16
+MFMA prefill within 2e-2 normwise of the f64 matmul of the exactly dequantized
+weights.  Test weights are random valid
 blocks (random codes and 6-bit scales / mins under f16 super-block scales):
 GGML's Q4_K quantizer is not on the path and is not restated.
 """
@@ -109,9 +110,43 @@ def test_q4k_gemv_zero_mins():
     assert oracle.normwise_error(y.cpu().numpy(), ref) < 1e-3
 
 
-@pytest.mark.parametrize("path", [PATH_DECODE_MFMA, PATH_PREFILL_MFMA])
-def test_q4k_unsupported_paths_raise(path):
+def test_q4k_decode_path_unsupported():
     ql = QuantLinear.from_blocks(Q4_K, 16, 256, oracle.random_q4_k(16, 256, seed=5))
     with pytest.raises(HipError) as e:
-        ql.forward(torch.zeros(8, 256, device="cuda"), path=path)
+        ql.forward(torch.zeros(8, 256, device="cuda"), path=PATH_DECODE_MFMA)
     assert e.value.status == ERR_UNSUPPORTED
+
+
+# ---- prefill (bf16 MFMA): the same kernel as Q4_0 with per-block (d sc, dmin m) ----------
+
+@pytest.mark.parametrize("m,n,k", [(5, 300, 1024), (64, 257, 2048), (128, 512, 4096),
+                                   (200, 130, 768), (130, 256, 8192), (512, 1024, 4096)])
+def test_q4k_prefill_parity(m, n, k):
+    # (130, 256, 8192): two tiles -> the k range splits over workgroups;
+    # m <= 64 runs here too (auto path) until Q4_K has a batched-decode kernel
+    blocks, x = _gemv_case(m, n, k, seed=m + 3 * n + k)
+    ql = QuantLinear.from_blocks(Q4_K, n, k, blocks)
+    assert ql.select_path(m) == PATH_PREFILL_MFMA
+    print(f"q4k prefill m={m} n={n} k={k}", flush=True)
+    y = ql.forward(_dev(x))
+    torch.cuda.synchronize()
+    ref = oracle.qmatmul_f64(Q4_K, blocks, x, n, k)
+    assert oracle.normwise_error(y.cpu().numpy(), ref) < 2e-2
+    # the bf16 operands keep it far inside the bar; a wrong scale or min would not
+    assert oracle.normwise_error(y.cpu().numpy(), ref) < 5e-3
+
+
+def test_q4k_prefill_large_tiles_rows_sampled():
+    # 256-row tiles (8 x 32 tiles fill the CUs); the oracle checks sampled rows
+    m, n, k = 2048, 8192, 2048
+    blocks, x = _gemv_case(m, n, k, seed=77)
+    ql = QuantLinear.from_blocks(Q4_K, n, k, blocks)
+    print(f"q4k prefill large m={m} n={n} k={k}", flush=True)
+    y = ql.forward(_dev(x))
+    torch.cuda.synchronize()
+    rows = np.array([0, 1, 255, 256, 1023, m - 77, m - 1])
+    ref = oracle.qmatmul_f64(Q4_K, blocks, x[rows], n, k)
+    assert oracle.normwise_error(y.cpu().numpy()[rows], ref) < 5e-3
+    y2 = ql.forward(_dev(x) * 2.0)
+    torch.cuda.synchronize()
+    assert np.array_equal(y2.cpu().numpy(), 2.0 * y.cpu().numpy())  # no k split here

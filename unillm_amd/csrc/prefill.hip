@@ -81,15 +81,19 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 // One lane's B fragment of one 32-block: 8 codes (4 per dword of `raw`, in
 // element order) -> 8 bf16 of code * d + off (off = -8 d for Q4_0, -128 d for
 // Q8_0, the codes being unsigned here).  Exact in fp32, one rounding to bf16.
+//
+// Q4_K: the same 4-bit codes with d = d_group * sc and off = -dmin_group * m of
+// the block (both exact in fp32), so (d sc) q - dmin m is exact too before the
+// one rounding to bf16.
 template <int QT>
-__device__ __forceinline__ bf16x8 dequant8(u32x2 raw, int shift, float d) {
-    constexpr uint32_t kFlip = QT == UNILLM_QTYPE_Q4_0 ? 0x88888888u : 0x80808080u;
-    const float off = d * (QT == UNILLM_QTYPE_Q4_0 ? -8.0f : -128.0f);
+__device__ __forceinline__ bf16x8 dequant8(u32x2 raw, int shift, float d, float off) {
+    constexpr bool kNib = QT != UNILLM_QTYPE_Q8_0;
+    constexpr uint32_t kFlip = kNib ? 0x88888888u : 0x80808080u;
     uint32_t u[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const uint32_t w = raw[h] ^ kFlip;  // signed codes -> unsigned (q, or q + 128)
-        u[h] = QT == UNILLM_QTYPE_Q4_0 ? (w >> shift) & 0x0F0F0F0Fu : w;
+        u[h] = kNib ? (w >> shift) & 0x0F0F0F0Fu : w;
     }
     float f[8];
 #pragma unroll
@@ -151,18 +155,20 @@ __global__ __launch_bounds__(256) void x_to_bf16_kernel(const float* __restrict_
 
 template <int QT, int BM>
 struct Ring {
-    static constexpr int QB = QT == UNILLM_QTYPE_Q4_0 ? 16 : 32;  // payload bytes per block
+    static constexpr int QB = QT == UNILLM_QTYPE_Q8_0 ? 32 : 16;  // payload bytes per block
+    static constexpr bool K4 = QT == UNILLM_QTYPE_Q4_K;
     static constexpr int A = BM * 128;
     static constexpr int BP = PBN * 2 * QB;
     static constexpr int BS = 2 * PBN * 4;
-    static constexpr int STAGE = A + BP + BS;
+    static constexpr int BH = K4 ? 2 * PBN * 4 : 0;  // Q4_K: the step's group header per column
+    static constexpr int STAGE = A + BP + BS + BH;
     // stages: 4 for 128-row tiles (four fit in LDS; ~10 % over three measured),
     // 3 for 256-row tiles
     static constexpr int STAGES = BM == 128 ? 4 : 3;
     static constexpr int BYTES = STAGES * STAGE;
     static constexpr int CPB = 2 * QB / 16;            // 16-byte payload chunks per column
     static constexpr int AQ = BM / 8 / 8;              // A loads (8 rows each) per wave
-    static constexpr int DMA = AQ + CPB / 2 + 1;       // direct loads per wave per stage
+    static constexpr int DMA = AQ + CPB / 2 + 1 + (K4 ? 1 : 0);  // direct loads per wave per stage
 };
 
 template <int QT, int BM, int NW>
@@ -173,7 +179,7 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
                                                               int KB, int tiles_n, int tiles,
                                                               int units_pad, int S) {
     static_assert(NW == 8, "the ring's load split assumes 8 waves");
-    constexpr int QB = QT == UNILLM_QTYPE_Q4_0 ? 16 : 32;  // payload bytes per block
+    constexpr int QB = QT == UNILLM_QTYPE_Q8_0 ? 32 : 16;  // payload bytes per block
     // waves: RW row groups x CW column groups; wave (rw, cw) owns rows BM / RW * rw ..
     // and columns PBN / CW * cw .. of the tile; its columns' weights are dequantized
     // by the RW waves of the group.  RW = 1: each weight once, all of A per wave.
@@ -242,14 +248,18 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
         // the step's two scales (2 ks is even: one aligned dword; an odd KB's last step
         // reads two bytes past the scales, inside the row padding or the weight's tail slot)
         dma4(base + ssrc + 4u * ks, st + R::A + R::BP + wv * 256);
+        // Q4_K: the 256-weight group header of the step (blocks 2 ks, 2 ks + 1 share it)
+        if constexpr (R::K4)
+            dma4(base + ssrc + 2u * (uint32_t)KB + 4u * (uint32_t)(ks >> 2),
+                 st + R::A + R::BP + R::BS + wv * 256);
     };
 
     // ---- B fragment geometry: lane -> column 16 j + l % 16 of the wave's 32, elements
     // 8 g .. +7 of a block (g = l / 16): Q4_0 payload bytes 8 (g & 1) .. +7, low nibbles
     // for g < 2, high for g >= 2; Q8_0 bytes 8 g .. +7
     const int g = lane / 16, fr = lane % 16;
-    const uint32_t boff = QT == UNILLM_QTYPE_Q4_0 ? 8 * (g & 1) : 8 * g;
-    const int bshift = QT == UNILLM_QTYPE_Q4_0 ? 4 * (g >> 1) : 0;
+    const uint32_t boff = QT != UNILLM_QTYPE_Q8_0 ? 8 * (g & 1) : 8 * g;
+    const int bshift = QT != UNILLM_QTYPE_Q8_0 ? 4 * (g >> 1) : 0;
     const int rw = wv / CW, cw = wv % CW;
     bool bval[TJ];
 #pragma unroll
@@ -324,19 +334,50 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
                 : "v"(st + boff0), "v"(st + soff0), "i"(0), "i"(QB), "i"(T), "i"(T + QB));
         }
         const bool b1ok = 2 * ks + 1 < KB;
-        float d0[TJ], d1[TJ];
+        float d0[TJ], d1[TJ], o0[TJ], o1[TJ];
+        if constexpr (R::K4) {
+            // the group header (d | dmin << 16) of each column tile, laid out as the scales;
+            // sc[j] holds (sc | m << 8) of block 0 in its low half, of block 1 in its high
+            uint32_t hd[TJ];
+            if constexpr (TJ == 4)
+                asm volatile(
+                    "ds_read_b32 %0, %4\n ds_read_b32 %1, %4 offset:64\n"
+                    "ds_read_b32 %2, %4 offset:256\n ds_read_b32 %3, %4 offset:320\n"
+                    "s_waitcnt lgkmcnt(0)"
+                    : "=&v"(hd[0]), "=&v"(hd[1]), "=&v"(hd[2]), "=&v"(hd[3])
+                    : "v"(st + soff0 + R::BS));
+            else
+                asm volatile("ds_read_b32 %0, %2\n ds_read_b32 %1, %2 offset:64\n"
+                             "s_waitcnt lgkmcnt(0)"
+                             : "=&v"(hd[0]), "=&v"(hd[TJ - 1])
+                             : "v"(st + soff0 + R::BS));
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-            d0[j] = bval[j] ? __half2float(__ushort_as_half((uint16_t)sc[j])) : 0.0f;
-            d1[j] = bval[j] && b1ok ? __half2float(__ushort_as_half((uint16_t)(sc[j] >> 16)))
-                                    : 0.0f;
+            for (int j = 0; j < TJ; ++j) {
+                const float dd = bval[j] ? __half2float(__ushort_as_half((uint16_t)hd[j])) : 0.0f;
+                const float dm = bval[j] ? __half2float(__ushort_as_half((uint16_t)(hd[j] >> 16)))
+                                         : 0.0f;
+                d0[j] = dd * (float)(sc[j] & 0xFFu);
+                o0[j] = -(dm * (float)((sc[j] >> 8) & 0xFFu));
+                d1[j] = b1ok ? dd * (float)((sc[j] >> 16) & 0xFFu) : 0.0f;
+                o1[j] = b1ok ? -(dm * (float)(sc[j] >> 24)) : 0.0f;
+            }
+        } else {
+            constexpr float kOff = QT == UNILLM_QTYPE_Q4_0 ? -8.0f : -128.0f;
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                d0[j] = bval[j] ? __half2float(__ushort_as_half((uint16_t)sc[j])) : 0.0f;
+                d1[j] = bval[j] && b1ok ? __half2float(__ushort_as_half((uint16_t)(sc[j] >> 16)))
+                                        : 0.0f;
+                o0[j] = d0[j] * kOff;
+                o1[j] = d1[j] * kOff;
+            }
         }
         // block 0's fragments first; block 1's are dequantized between the MFMAs of
         // the first 32 k (one column tile after every TI / TJ row tiles), so the
         // VALU work overlaps the matrix cores instead of following them
         bf16x8 bfrag[TJ][2];
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) bfrag[j][0] = dequant8<QT>(raw[j][0], bshift, d0[j]);
+        for (int j = 0; j < TJ; ++j) bfrag[j][0] = dequant8<QT>(raw[j][0], bshift, d0[j], o0[j]);
         // A fragments, two ahead (one ahead leaves ~2 MFMAs to cover an LDS read;
         // deeper measured no better): fragment f = kk * TI + i at aoff[kk] + 2048 i
         constexpr int PF = 2;
@@ -366,7 +407,7 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
                                                                     0, 0, 0);
             if (kk == 0 && (i + 1) % (TI / TJ) == 0) {
                 const int j = (i + 1) / (TI / TJ) - 1;
-                bfrag[j][1] = dequant8<QT>(raw[j][1], bshift, d1[j]);
+                bfrag[j][1] = dequant8<QT>(raw[j][1], bshift, d1[j], o1[j]);
             }
         }
     }
@@ -456,6 +497,9 @@ hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, floa
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     const __bf16* xb = static_cast<const __bf16*>(ws);
+    if (w.qtype == UNILLM_QTYPE_Q4_K)
+        return plan.bm == 256 ? launch_bm<UNILLM_QTYPE_Q4_K, 256>(w, xb, m, y, 1, s)
+                              : launch_bm<UNILLM_QTYPE_Q4_K, 128>(w, xb, m, y, plan.S, s);
     const bool q4 = w.qtype == UNILLM_QTYPE_Q4_0;
     if (plan.bm == 256)
         return q4 ? launch_bm<UNILLM_QTYPE_Q4_0, 256>(w, xb, m, y, 1, s)

@@ -13,8 +13,7 @@ import torch
 
 import oracle
 from oracle import Q4_K
-from unillm_amd import (ERR_UNSUPPORTED, PATH_DECODE_MFMA, PATH_GEMV, PATH_PREFILL_MFMA, HipError,
-                        QuantLinear)
+from unillm_amd import PATH_DECODE_MFMA, PATH_GEMV, PATH_PREFILL_MFMA, HipError, QuantLinear
 
 pytestmark = pytest.mark.gpu
 
@@ -110,20 +109,45 @@ def test_q4k_gemv_zero_mins():
     assert oracle.normwise_error(y.cpu().numpy(), ref) < 1e-3
 
 
-def test_q4k_decode_path_unsupported():
-    ql = QuantLinear.from_blocks(Q4_K, 16, 256, oracle.random_q4_k(16, 256, seed=5))
-    with pytest.raises(HipError) as e:
-        ql.forward(torch.zeros(8, 256, device="cuda"), path=PATH_DECODE_MFMA)
-    assert e.value.status == ERR_UNSUPPORTED
+# ---- batched decode (f16 MFMA): per-block f16 (d sc 2^-E, dmin m 2^-E) ---------------------
+
+@pytest.mark.parametrize("m,n,k", [(5, 257, 256), (8, 300, 4096), (16, 4096, 4096),
+                                   (33, 129, 2048), (64, 512, 4096), (16, 257, 11008),
+                                   (12, 1024, 14336)])
+def test_q4k_decode_parity(m, n, k):
+    # k = 11008: 86 chunks in slices that start on odd chunks (a 256-weight group
+    # split between two workgroups); m = 33, 64: two token tiles
+    blocks, x = _gemv_case(m, n, k, seed=5 * m + n + k)
+    ql = QuantLinear.from_blocks(Q4_K, n, k, blocks)
+    assert ql.select_path(m) == PATH_DECODE_MFMA
+    print(f"q4k decode m={m} n={n} k={k}", flush=True)
+    y = ql.forward(_dev(x))
+    torch.cuda.synchronize()
+    ref = oracle.qmatmul_f64(Q4_K, blocks, x, n, k)
+    assert oracle.normwise_error(y.cpu().numpy(), ref) < 1e-3
+
+
+def test_q4k_decode_scale_range():
+    # scales far from 1 (the weight's f16 exponent offset must keep d sc and dmin m
+    # normal in f16): d, dmin around 2^-20 and around 2^6
+    m, n, k = 16, 128, 2048
+    x = oracle.normal(m * k, seed=61).reshape(m, k)
+    for mult in (2.0 ** -14, 2.0 ** 12):
+        blocks = oracle.random_q4_k(n, k, seed=62).reshape(-1, 144)
+        for off in (0, 2):
+            v = blocks[:, off:off + 2].copy().view(np.float16).astype(np.float32) * mult
+            blocks[:, off:off + 2] = v.astype(np.float16).view(np.uint8)
+        y = QuantLinear.from_blocks(Q4_K, n, k, blocks).forward(_dev(x), path=PATH_DECODE_MFMA)
+        ref = oracle.qmatmul_f64(Q4_K, blocks, x, n, k)
+        assert oracle.normwise_error(y.cpu().numpy(), ref) < 1e-3, mult
 
 
 # ---- prefill (bf16 MFMA): the same kernel as Q4_0 with per-block (d sc, dmin m) ----------
 
-@pytest.mark.parametrize("m,n,k", [(5, 300, 1024), (64, 257, 2048), (128, 512, 4096),
-                                   (200, 130, 768), (130, 256, 8192), (512, 1024, 4096)])
+@pytest.mark.parametrize("m,n,k", [(65, 300, 1024), (128, 512, 4096), (200, 130, 768),
+                                   (130, 256, 8192), (512, 1024, 4096)])
 def test_q4k_prefill_parity(m, n, k):
-    # (130, 256, 8192): two tiles -> the k range splits over workgroups;
-    # m <= 64 runs here too (auto path) until Q4_K has a batched-decode kernel
+    # (130, 256, 8192): two tiles -> the k range splits over workgroups
     blocks, x = _gemv_case(m, n, k, seed=m + 3 * n + k)
     ql = QuantLinear.from_blocks(Q4_K, n, k, blocks)
     assert ql.select_path(m) == PATH_PREFILL_MFMA
@@ -133,6 +157,15 @@ def test_q4k_prefill_parity(m, n, k):
     ref = oracle.qmatmul_f64(Q4_K, blocks, x, n, k)
     assert oracle.normwise_error(y.cpu().numpy(), ref) < 2e-2
     # the bf16 operands keep it far inside the bar; a wrong scale or min would not
+    assert oracle.normwise_error(y.cpu().numpy(), ref) < 5e-3
+
+
+def test_q4k_prefill_small_m_explicit_path():
+    # the prefill kernel takes any m when asked for (tiles of 128 rows, rows past m unused)
+    m, n, k = 5, 300, 1024
+    blocks, x = _gemv_case(m, n, k, seed=71)
+    y = QuantLinear.from_blocks(Q4_K, n, k, blocks).forward(_dev(x), path=PATH_PREFILL_MFMA)
+    ref = oracle.qmatmul_f64(Q4_K, blocks, x, n, k)
     assert oracle.normwise_error(y.cpu().numpy(), ref) < 5e-3
 
 

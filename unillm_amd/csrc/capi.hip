@@ -306,8 +306,6 @@ int unillm_hip_qweight_info(const unillm_qweight* w, int* qtype, int64_t* n, int
 int unillm_hip_select_path(const unillm_qweight* w, int64_t m) {
     if (!w || m < 0) return fail(UNILLM_ERR_INVALID_ARG, "bad arguments to select_path");
     if (gemv_supports(*w, m)) return UNILLM_PATH_GEMV;
-    // Q4_K has no batched-decode kernel yet: 5 <= m <= 64 runs the prefill kernel
-    if (w->qtype == UNILLM_QTYPE_Q4_K && m > kGemvMaxM) return UNILLM_PATH_PREFILL_MFMA;
     if (m <= kDecodeMaxM) return UNILLM_PATH_DECODE_MFMA;
     return UNILLM_PATH_PREFILL_MFMA;
 }
@@ -324,9 +322,6 @@ int unillm_hip_qmatmul_path(const unillm_qweight* w, const float* x_dev, int64_t
     if (m > (int64_t)INT32_MAX / 2)
         return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: m too large");
     if (path == UNILLM_PATH_AUTO) path = unillm_hip_select_path(w, m);
-    if (w->qtype == UNILLM_QTYPE_Q4_K && path == UNILLM_PATH_DECODE_MFMA)
-        return fail(UNILLM_ERR_UNSUPPORTED,
-                    "QMatMul forward failed: Q4_K weights run on the GEMV and prefill paths");
     if (int rc = ensure_init()) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipError_t e;

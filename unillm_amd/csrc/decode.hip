@@ -100,6 +100,31 @@ __device__ __forceinline__ void dequant_q4(u32x4 raw, f16x2 dh, f16x2 dh16, f16x
     for (int q = 0; q < 4; ++q) f[q] = __builtin_bit_cast(f16x8, o[q]);
 }
 
+// Q4_K: as dequant_q4 with the block's f16 scale s = d sc 2^-E and min o =
+// dmin m 2^-E: (1024 + q - 1024) s - o (high nibbles: (1024 + 16 q - 1024) s / 16 - o).
+// s and o are rounded to f16 once each, the weight once more.
+__device__ __forceinline__ void dequant_q4k(u32x4 raw, f16x2 sh, f16x2 sh16, f16x2 oh,
+                                            f16x8 (&f)[4]) {
+    const f16x2 b = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const uint32_t magic = 0x64006400u;
+    auto fma2 = [&](uint32_t v, f16x2 sc) {
+        return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, v) - b) * sc - oh);
+    };
+    u32x4 o[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const uint32_t w = raw[d] ^ 0x88888888u;  // signed nibble -> q
+        const uint32_t w8 = w >> 8;
+        const int lo = d / 2, e = 2 * (d % 2);
+        o[lo][e] = fma2(and_or(w, 0x000F000Fu, magic), sh);
+        o[lo][e + 1] = fma2(and_or(w8, 0x000F000Fu, magic), sh);
+        o[2 + lo][e] = fma2(and_or(w, 0x00F000F0u, magic), sh16);
+        o[2 + lo][e + 1] = fma2(and_or(w8, 0x00F000F0u, magic), sh16);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) f[q] = __builtin_bit_cast(f16x8, o[q]);
+}
+
 // Q8_0: 16 payload bytes (elements 16h .. 16h + 15) -> two fragments (elements
 // 16h .. +7 and 16h + 8 .. +7), each in the order 0 2 1 3 4 6 5 7.
 __device__ __forceinline__ void dequant_q8(u32x4 raw, f16x2 dh, f16x8& f0, f16x8& f1) {
@@ -161,7 +186,7 @@ constexpr int kMaxSplit = DECODE_MAX_SPLIT;
 
 template <int QT, int MT2>
 struct Stage {
-    static constexpr int QB = QT == UNILLM_QTYPE_Q4_0 ? 16 : 32;
+    static constexpr int QB = QT == UNILLM_QTYPE_Q8_0 ? 32 : 16;
     static constexpr int TOK = 32 * MT2;
     static constexpr int X = TOK * 256;
     static constexpr int P = DROWS * 4 * QB;
@@ -172,9 +197,12 @@ struct Stage {
     static constexpr int LPR = 4 * QB / 16;          // payload lanes per row (4 / 8)
     static constexpr int RPI = 64 / LPR;             // payload rows per direct load
     static constexpr int SCALES = 4 * 32 * 8 * kMaxSliceChunks;
+    // Q4_K: the slice's group headers, per wave [32 rows][8 x 4 B] (a slice of at
+    // most 8 chunks touches at most 5 groups of 2 chunks)
+    static constexpr int HDR = QT == UNILLM_QTYPE_Q4_K ? 4 * 32 * 32 : 0;
     // depth: as deep as keeps two workgroups per CU, where the stage allows
     static constexpr int D = BYTES <= 16384 ? 4 : 3;
-    static constexpr int LDS = D * BYTES + SCALES;
+    static constexpr int LDS = D * BYTES + SCALES + HDR;
 };
 
 // s_waitcnt vmcnt(rem * LPC) for a wave-uniform rem in [0, R].
@@ -252,10 +280,12 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
                                                      int S, float wscale, float oscale) {
     using ST = Stage<QT, MT2>;
     constexpr int QB = ST::QB, D = ST::D, LPC = ST::LPC;
-    constexpr bool Q4 = QT == UNILLM_QTYPE_Q4_0;
+    constexpr bool Q4 = QT != UNILLM_QTYPE_Q8_0;  // 4-bit codes: Q4_0 and Q4_K
+    constexpr bool K4 = QT == UNILLM_QTYPE_Q4_K;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     uint8_t* const ring = lds;
     uint8_t* const scl = lds + D * ST::BYTES;
+    uint8_t* const hdr = scl + ST::SCALES;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -284,6 +314,20 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
         const uint32_t g = (uint32_t)min(row0 + r, N - 1) * (uint32_t)rb + sbase +
                            8u * (uint32_t)(c0 + jj) + 4u * (uint32_t)(dw & 1);
         dma4(base + g, scl + wv * 2048 + i * 256);
+    }
+    // ---- Q4_K: the slice's group headers (d | dmin << 16), 8 positions of 4 bytes a
+    // row; lane -> flat dword f = 64 i + lane = row f / 8, position f % 8 = group
+    // c0 / 2 + position (clamped to the slice's last group) ----
+    if constexpr (K4) {
+        const int g0 = c0 >> 1, glast = (c1 - 1) >> 1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int f = 64 * i + lane;
+            const int r = f >> 3, grp = min(g0 + (f & 7), glast);
+            const uint32_t g = (uint32_t)min(row0 + r, N - 1) * (uint32_t)rb +
+                               (uint32_t)KB * 18u + 4u * (uint32_t)grp;
+            dma4(base + g, hdr + wv * 1024 + i * 256);
+        }
     }
 
     // ---- per-chunk direct-load sources (32-bit offsets; the host checks sizes) ----
@@ -357,11 +401,22 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
     }
     const uint32_t ring0 = (uint32_t)(uintptr_t)ring;
     const uint32_t srow = (uint32_t)(uintptr_t)scl + (uint32_t)(wv * 2048 + col * 64);
+    const uint32_t hrow = (uint32_t)(uintptr_t)hdr + (uint32_t)(wv * 1024 + col * 32);
 
     auto compute = [&](int j) {
         const uint32_t st = ring0 + (uint32_t)((j % D) * ST::BYTES);
         const int kb0 = 4 * (c0 + j);
         const uint32_t sa = srow + 8 * ((j + col) & 7);
+        // Q4_K: the chunk's group header (the 4 blocks of a chunk share one group)
+        float gd = 0.0f, gm = 0.0f;
+        if constexpr (K4) {
+            uint32_t hd;
+            asm volatile("ds_read_b32 %0, %1\n s_waitcnt lgkmcnt(0)"
+                         : "=&v"(hd)
+                         : "v"(hrow + 4u * (uint32_t)(((c0 + j) >> 1) - (c0 >> 1))));
+            gd = __half2float(__ushort_as_half((uint16_t)hd)) * wscale;
+            gm = __half2float(__ushort_as_half((uint16_t)(hd >> 16))) * wscale;
+        }
 #pragma unroll
         for (int hp = 0; hp < 2; ++hp) {
             lds_u32x4 xa[MT2][4];
@@ -373,12 +428,22 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
             if constexpr (Q4) {
                 // this lane's block 2 hp + h and its scale
                 const uint16_t sb = (uint16_t)(scp[hp] >> (16 * h));
-                const float dv =
-                    kb0 + 2 * hp + h < KB ? __half2float(__ushort_as_half(sb)) * wscale : 0.0f;
-                const _Float16 d = (_Float16)dv, d16 = (_Float16)(dv * 0.0625f);
-                const f16x2 dh = {d, d}, dh16 = {d16, d16};
+                const bool ok = kb0 + 2 * hp + h < KB;
                 f16x8 b[4];
-                dequant_q4(pw[0], dh, dh16, b);
+                if constexpr (K4) {
+                    // sb = sc | m << 8: s = d sc 2^-E and o = dmin m 2^-E, each once to f16
+                    const float sv = ok ? gd * (float)(sb & 0xFFu) : 0.0f;
+                    const float ov = ok ? gm * (float)(sb >> 8) : 0.0f;
+                    const _Float16 s1 = (_Float16)sv, s16 = (_Float16)(sv * 0.0625f),
+                                   o1 = (_Float16)ov;
+                    const f16x2 sh = {s1, s1}, sh16 = {s16, s16}, oh = {o1, o1};
+                    dequant_q4k(pw[0], sh, sh16, oh, b);
+                } else {
+                    const float dv = ok ? __half2float(__ushort_as_half(sb)) * wscale : 0.0f;
+                    const _Float16 d = (_Float16)dv, d16 = (_Float16)(dv * 0.0625f);
+                    const f16x2 dh = {d, d}, dh16 = {d16, d16};
+                    dequant_q4(pw[0], dh, dh16, b);
+                }
 #pragma unroll
                 for (int t = 0; t < MT2; ++t)
 #pragma unroll
@@ -492,9 +557,10 @@ hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float
     if ((uint64_t)m * (uint64_t)w.k >= (1ull << 31) ||
         (uint64_t)w.n * (uint64_t)w.row_bytes >= (1ull << 32))
         return hipErrorInvalidValue;
-    const bool q4 = w.qtype == UNILLM_QTYPE_Q4_0, wide = m > 32;
-    const int lds = q4 ? (wide ? Stage<UNILLM_QTYPE_Q4_0, 2>::LDS : Stage<UNILLM_QTYPE_Q4_0, 1>::LDS)
-                       : (wide ? Stage<UNILLM_QTYPE_Q8_0, 2>::LDS : Stage<UNILLM_QTYPE_Q8_0, 1>::LDS);
+    const bool q4 = w.qtype == UNILLM_QTYPE_Q4_0, k4 = w.qtype == UNILLM_QTYPE_Q4_K, wide = m > 32;
+    const int lds = k4   ? (wide ? Stage<UNILLM_QTYPE_Q4_K, 2>::LDS : Stage<UNILLM_QTYPE_Q4_K, 1>::LDS)
+                    : q4 ? (wide ? Stage<UNILLM_QTYPE_Q4_0, 2>::LDS : Stage<UNILLM_QTYPE_Q4_0, 1>::LDS)
+                         : (wide ? Stage<UNILLM_QTYPE_Q8_0, 2>::LDS : Stage<UNILLM_QTYPE_Q8_0, 1>::LDS);
     const int S = choose_split(w, lds);
     void* ws = nullptr;
     hipError_t e = stream_workspace(s, (size_t)m * (size_t)w.k * 2, &ws);
@@ -507,6 +573,9 @@ hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float
     xprep_kernel<<<grid, 256, 0, s>>>(x, static_cast<uint4*>(ws), n8, y, ny);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const _Float16* xh = static_cast<const _Float16*>(ws);
+    if (k4)
+        return wide ? launch_mt<UNILLM_QTYPE_Q4_K, 2>(w, xh, m, y, S, s)
+                    : launch_mt<UNILLM_QTYPE_Q4_K, 1>(w, xh, m, y, S, s);
     if (!wide)
         return q4 ? launch_mt<UNILLM_QTYPE_Q4_0, 1>(w, xh, m, y, S, s)
                   : launch_mt<UNILLM_QTYPE_Q8_0, 1>(w, xh, m, y, S, s);

@@ -17,7 +17,7 @@
  *     (candle reverses ne into shape [n, k]).  x is [m, k] f32 row-major and
  *     y = x . dequant(W)^T is [m, n] f32 row-major.
  *   - Preconditions checked on the host before any launch: k % 32 == 0
- *     (k % 256 == 0 for Q4_K), n >= 1, k >= 32, m >= 0, non-null pointers,
+ *     (k % 256 == 0 for Q4_K, Q6_K), n >= 1, k >= 32, m >= 0, non-null pointers,
  *     known qtype.
  *   - Streams: a `void* stream` is a hipStream_t (NULL = the null stream).
  *     Compute calls are asynchronous on that stream and never synchronise.
@@ -35,11 +35,13 @@
 extern "C" {
 #endif
 
-/* GGML type ids as GGUF stores them (candle GgmlDType::Q4_0 / Q8_0 / Q4K; the
- * reference maps Q4K at crates/runtime/src/weight_loader_core.rs:481). */
+/* GGML type ids as GGUF stores them (candle GgmlDType::Q4_0 / Q8_0 / Q4K / Q6K;
+ * the reference maps Q4K at crates/runtime/src/weight_loader_core.rs:481; Q6K is
+ * what GGUF Q4_K_M files use for output.weight and some attn_v / ffn_down). */
 #define UNILLM_QTYPE_Q4_0 2
 #define UNILLM_QTYPE_Q8_0 8
 #define UNILLM_QTYPE_Q4_K 12
+#define UNILLM_QTYPE_Q6_K 14
 
 #define UNILLM_OK 0
 #define UNILLM_ERR_INVALID_ARG (-1)
@@ -65,8 +67,8 @@ int unillm_hip_init(int device);
 /* Message of the last error on the calling thread ("" if none). */
 const char* unillm_hip_last_error(void);
 
-/* Upload one GGUF Q4_0 / Q8_0 / Q4_K tensor ([n, k]: n * k/32 blocks of 18 /
- * 34 B, or n * k/256 blocks of 144 B)
+/* Upload one GGUF Q4_0 / Q8_0 / Q4_K / Q6_K tensor ([n, k]: n * k/32 blocks of
+ * 18 / 34 B, or n * k/256 blocks of 144 / 210 B)
  * to the device, repacked there into the kernels' layout.  Replaces
  * `QMatMul::from_arc(Arc::new(qtensor))` at
  * crates/runtime/src/weight_loader_core.rs:569-571 (the QTensor read at :545).
@@ -111,7 +113,9 @@ int unillm_hip_dequant(const unillm_qweight* w, float* out_dev, void* stream);
 
 /* GGML reference quantizer on the device: w[n, k] f32 -> GGUF block bytes
  * (n * k/32 blocks of 18 / 34 B), bit-exact with GGML quantize_row_q4_0/q8_0
- * (candle QTensor::quantize; used by the reference only to make GGUF files). */
+ * (candle QTensor::quantize; used by the reference only to make GGUF files).
+ * Q4_K / Q6_K are refused with UNILLM_ERR_UNSUPPORTED (their GGML quantizers
+ * search scales iteratively and are not on this path). */
 int unillm_hip_quantize(int qtype, const float* w_dev, int64_t n, int64_t k, void* blocks_dev,
                         void* stream);
 

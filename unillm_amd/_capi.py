@@ -15,8 +15,11 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "unillm_hip.h")
 Q4_0 = 2
 Q8_0 = 8
 Q4_K = 12
+Q6_K = 14
 QK = 32
-BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 18}  # GGUF bytes per 32 weights (Q4_K: 144 / 256)
+# GGUF block geometry: weights per block and bytes per block
+BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}
 
 PATH_AUTO = 0
 PATH_GEMV = 1

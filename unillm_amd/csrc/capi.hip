@@ -75,14 +75,15 @@ int ensure_init() {
 }
 
 bool valid_qtype(int q) {
-    return q == UNILLM_QTYPE_Q4_0 || q == UNILLM_QTYPE_Q8_0 || q == UNILLM_QTYPE_Q4_K;
+    return q == UNILLM_QTYPE_Q4_0 || q == UNILLM_QTYPE_Q8_0 || q == UNILLM_QTYPE_Q4_K ||
+           q == UNILLM_QTYPE_Q6_K;
 }
 
 int check_shape(int qtype, int64_t n, int64_t k) {
     if (!valid_qtype(qtype))
         return fail(UNILLM_ERR_UNSUPPORTED, "unsupported qtype " + std::to_string(qtype) +
-                                                " (want 2 = Q4_0, 8 = Q8_0, 12 = Q4_K)");
-    const int64_t blk = qtype == UNILLM_QTYPE_Q4_K ? 256 : QK;
+                                                " (want 2 = Q4_0, 8 = Q8_0, 12 = Q4_K, 14 = Q6_K)");
+    const int64_t blk = gguf_block_elems(qtype);
     if (n < 1 || k < blk || k % blk != 0)
         return fail(UNILLM_ERR_INVALID_ARG, "bad weight shape [" + std::to_string(n) + ", " +
                                                 std::to_string(k) +
@@ -142,10 +143,10 @@ int finish_weight(QWeight* w, hipStream_t s) {
         return __half2float(__ushort_as_half((unsigned short)(b > 0x7BFFu ? 0x7BFFu : b)));
     };
     // |code| <= 8 (Q4_0) or 128 (Q8_0); Q4_K: |(d sc) q - dmin m| <= 63 (15 |d| + |dmin|);
-    // f16 holds magnitudes up to 65504
-    const float wmax = w->qtype == UNILLM_QTYPE_Q4_K
-                           ? 63.0f * (15.0f * f16max(bits[0]) + f16max(bits[1]))
-                           : f16max(bits[0]) * (w->qtype == UNILLM_QTYPE_Q4_0 ? 8.0f : 128.0f);
+    // Q6_K: |(d sc)(q - 32)| <= 128 * 32 |d|; f16 holds magnitudes up to 65504
+    const float wmax = w->qtype == UNILLM_QTYPE_Q4_K   ? 63.0f * (15.0f * f16max(bits[0]) + f16max(bits[1]))
+                       : w->qtype == UNILLM_QTYPE_Q6_K ? 4096.0f * f16max(bits[0])
+                       : f16max(bits[0]) * (w->qtype == UNILLM_QTYPE_Q4_0 ? 8.0f : 128.0f);
     // the largest power-of-two scaling that keeps every dequantized weight in
     // f16 range: small scales stay normal in f16 (also divided by 16)
     int E = 0;
@@ -225,7 +226,7 @@ int unillm_hip_qweight_create(int qtype, int64_t n, int64_t k, const void* host_
     if (int rc = check_shape(qtype, n, k)) return rc;
     if (!host_blocks) return fail(UNILLM_ERR_INVALID_ARG, "host_blocks is NULL");
     if (layout_flags != 0) return fail(UNILLM_ERR_INVALID_ARG, "layout_flags must be 0");
-    const size_t want = (size_t)(n * (k / QK)) * gguf_block_bytes(qtype);
+    const size_t want = (size_t)(n * (k / gguf_block_elems(qtype))) * gguf_block_bytes(qtype);
     if (nbytes != want)
         return fail(UNILLM_ERR_INVALID_ARG, "nbytes " + std::to_string(nbytes) + " != " +
                                                 std::to_string(want) + " for this shape");
@@ -264,7 +265,7 @@ int unillm_hip_qweight_create_device(int qtype, int64_t n, int64_t k, const void
     if (int rc = check_shape(qtype, n, k)) return rc;
     if (!dev_blocks) return fail(UNILLM_ERR_INVALID_ARG, "dev_blocks is NULL");
     if (layout_flags != 0) return fail(UNILLM_ERR_INVALID_ARG, "layout_flags must be 0");
-    const size_t want = (size_t)(n * (k / QK)) * gguf_block_bytes(qtype);
+    const size_t want = (size_t)(n * (k / gguf_block_elems(qtype))) * gguf_block_bytes(qtype);
     if (nbytes != want)
         return fail(UNILLM_ERR_INVALID_ARG, "nbytes " + std::to_string(nbytes) + " != " +
                                                 std::to_string(want) + " for this shape");
@@ -364,6 +365,8 @@ int unillm_hip_dequant(const unillm_qweight* w, float* out_dev, void* stream) {
 int unillm_hip_quantize(int qtype, const float* w_dev, int64_t n, int64_t k, void* blocks_dev,
                         void* stream) {
     if (int rc = check_shape(qtype, n, k)) return rc;
+    if (is_kquant(qtype))
+        return fail(UNILLM_ERR_UNSUPPORTED, "the device quantizer covers Q4_0 and Q8_0 only");
     if (!w_dev || !blocks_dev) return fail(UNILLM_ERR_INVALID_ARG, "w or blocks is NULL");
     if (!aligned16(w_dev)) return fail(UNILLM_ERR_INVALID_ARG, "w must be 16-byte aligned");
     if (int rc = ensure_init()) return rc;

@@ -186,7 +186,7 @@ constexpr int kMaxSplit = DECODE_MAX_SPLIT;
 
 template <int QT, int MT2>
 struct Stage {
-    static constexpr int QB = QT == UNILLM_QTYPE_Q8_0 ? 32 : 16;
+    static constexpr int QB = QT == UNILLM_QTYPE_Q8_0 || QT == UNILLM_QTYPE_Q6_K ? 32 : 16;
     static constexpr int TOK = 32 * MT2;
     static constexpr int X = TOK * 256;
     static constexpr int P = DROWS * 4 * QB;
@@ -197,9 +197,10 @@ struct Stage {
     static constexpr int LPR = 4 * QB / 16;          // payload lanes per row (4 / 8)
     static constexpr int RPI = 64 / LPR;             // payload rows per direct load
     static constexpr int SCALES = 4 * 32 * 8 * kMaxSliceChunks;
-    // Q4_K: the slice's group headers, per wave [32 rows][8 x 4 B] (a slice of at
-    // most 8 chunks touches at most 5 groups of 2 chunks)
-    static constexpr int HDR = QT == UNILLM_QTYPE_Q4_K ? 4 * 32 * 32 : 0;
+    // K-quants: the slice's group headers, per wave [32 rows][8 x 4 B] (a slice of
+    // at most 8 chunks touches at most 5 groups of 2 chunks)
+    static constexpr int HDR =
+        QT == UNILLM_QTYPE_Q4_K || QT == UNILLM_QTYPE_Q6_K ? 4 * 32 * 32 : 0;
     // depth: as deep as keeps two workgroups per CU, where the stage allows
     static constexpr int D = BYTES <= 16384 ? 4 : 3;
     static constexpr int LDS = D * BYTES + SCALES + HDR;
@@ -280,8 +281,9 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
                                                      int S, float wscale, float oscale) {
     using ST = Stage<QT, MT2>;
     constexpr int QB = ST::QB, D = ST::D, LPC = ST::LPC;
-    constexpr bool Q4 = QT != UNILLM_QTYPE_Q8_0;  // 4-bit codes: Q4_0 and Q4_K
-    constexpr bool K4 = QT == UNILLM_QTYPE_Q4_K;
+    // 4-bit codes: Q4_0 and Q4_K; byte codes: Q8_0 and Q6_K (repacked to int8)
+    constexpr bool Q4 = QT == UNILLM_QTYPE_Q4_0 || QT == UNILLM_QTYPE_Q4_K;
+    constexpr bool K4 = QT == UNILLM_QTYPE_Q4_K, K6 = QT == UNILLM_QTYPE_Q6_K;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     uint8_t* const ring = lds;
     uint8_t* const scl = lds + D * ST::BYTES;
@@ -315,17 +317,17 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
                            8u * (uint32_t)(c0 + jj) + 4u * (uint32_t)(dw & 1);
         dma4(base + g, scl + wv * 2048 + i * 256);
     }
-    // ---- Q4_K: the slice's group headers (d | dmin << 16), 8 positions of 4 bytes a
-    // row; lane -> flat dword f = 64 i + lane = row f / 8, position f % 8 = group
-    // c0 / 2 + position (clamped to the slice's last group) ----
-    if constexpr (K4) {
+    // ---- K-quants: the slice's group headers (Q4_K d | dmin << 16, Q6_K d), 8
+    // positions of 4 bytes a row; lane -> flat dword f = 64 i + lane = row f / 8,
+    // position f % 8 = group c0 / 2 + position (clamped to the slice's last group) ----
+    if constexpr (K4 || K6) {
         const int g0 = c0 >> 1, glast = (c1 - 1) >> 1;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int f = 64 * i + lane;
             const int r = f >> 3, grp = min(g0 + (f & 7), glast);
             const uint32_t g = (uint32_t)min(row0 + r, N - 1) * (uint32_t)rb +
-                               (uint32_t)KB * 18u + 4u * (uint32_t)grp;
+                               (uint32_t)KB * (QB + 2u) + 4u * (uint32_t)grp;
             dma4(base + g, hdr + wv * 1024 + i * 256);
         }
     }
@@ -409,7 +411,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
         const uint32_t sa = srow + 8 * ((j + col) & 7);
         // Q4_K: the chunk's group header (the 4 blocks of a chunk share one group)
         float gd = 0.0f, gm = 0.0f;
-        if constexpr (K4) {
+        if constexpr (K4 || K6) {
             uint32_t hd;
             asm volatile("ds_read_b32 %0, %1\n s_waitcnt lgkmcnt(0)"
                          : "=&v"(hd)
@@ -454,9 +456,11 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
 #pragma unroll
                 for (int bi = 0; bi < 2; ++bi) {
                     const uint16_t sb = (uint16_t)(scp[hp] >> (16 * bi));
-                    const float dv = kb0 + 2 * hp + bi < KB
-                                         ? __half2float(__ushort_as_half(sb)) * wscale
-                                         : 0.0f;
+                    const bool ok = kb0 + 2 * hp + bi < KB;
+                    // Q6_K: sb = the two int8 scales; this lane's 16 weights take half h's
+                    const float dv = !ok ? 0.0f
+                                     : K6 ? gd * (float)(int8_t)(sb >> (8 * h))
+                                          : __half2float(__ushort_as_half(sb)) * wscale;
                     const _Float16 d = (_Float16)dv;
                     const f16x2 dh = {d, d};
                     f16x8 b0, b1;
@@ -557,8 +561,10 @@ hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float
     if ((uint64_t)m * (uint64_t)w.k >= (1ull << 31) ||
         (uint64_t)w.n * (uint64_t)w.row_bytes >= (1ull << 32))
         return hipErrorInvalidValue;
-    const bool q4 = w.qtype == UNILLM_QTYPE_Q4_0, k4 = w.qtype == UNILLM_QTYPE_Q4_K, wide = m > 32;
+    const bool q4 = w.qtype == UNILLM_QTYPE_Q4_0, k4 = w.qtype == UNILLM_QTYPE_Q4_K,
+               k6 = w.qtype == UNILLM_QTYPE_Q6_K, wide = m > 32;
     const int lds = k4   ? (wide ? Stage<UNILLM_QTYPE_Q4_K, 2>::LDS : Stage<UNILLM_QTYPE_Q4_K, 1>::LDS)
+                    : k6 ? (wide ? Stage<UNILLM_QTYPE_Q6_K, 2>::LDS : Stage<UNILLM_QTYPE_Q6_K, 1>::LDS)
                     : q4 ? (wide ? Stage<UNILLM_QTYPE_Q4_0, 2>::LDS : Stage<UNILLM_QTYPE_Q4_0, 1>::LDS)
                          : (wide ? Stage<UNILLM_QTYPE_Q8_0, 2>::LDS : Stage<UNILLM_QTYPE_Q8_0, 1>::LDS);
     const int S = choose_split(w, lds);
@@ -576,6 +582,9 @@ hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float
     if (k4)
         return wide ? launch_mt<UNILLM_QTYPE_Q4_K, 2>(w, xh, m, y, S, s)
                     : launch_mt<UNILLM_QTYPE_Q4_K, 1>(w, xh, m, y, S, s);
+    if (k6)
+        return wide ? launch_mt<UNILLM_QTYPE_Q6_K, 2>(w, xh, m, y, S, s)
+                    : launch_mt<UNILLM_QTYPE_Q6_K, 1>(w, xh, m, y, S, s);
     if (!wide)
         return q4 ? launch_mt<UNILLM_QTYPE_Q4_0, 1>(w, xh, m, y, S, s)
                   : launch_mt<UNILLM_QTYPE_Q8_0, 1>(w, xh, m, y, S, s);

@@ -202,9 +202,13 @@ __device__ __forceinline__ void prep_q8(const float (&v)[8], int u, bool store,
 }
 
 // The x elements a prep thread handles (q = 4 * block + quarter), as two float4 offsets.
+// Byte codes (Q8_0, and Q6_K repacked to int8) or nibbles (Q4_0, Q4_K).
+template <int QT>
+constexpr bool kByteCodes = QT == UNILLM_QTYPE_Q8_0 || QT == UNILLM_QTYPE_Q6_K;
+
 template <int QT>
 __device__ __forceinline__ void quarter_offsets(int quarter, int& o0, int& o1) {
-    if constexpr (QT != UNILLM_QTYPE_Q8_0) {
+    if constexpr (!kByteCodes<QT>) {
         o0 = 4 * quarter;       // x[4t .. 4t+3]
         o1 = 16 + 4 * quarter;  // x[16+4t .. 16+4t+3]
     } else {
@@ -249,14 +253,14 @@ struct XRegs {
 // ---- weights --------------------------------------------------------------------------------
 template <int QT>
 struct Payload {
-    static constexpr int V = QT == UNILLM_QTYPE_Q8_0 ? 2 : 1;  // 128-bit loads per block
+    static constexpr int V = kByteCodes<QT> ? 2 : 1;  // 128-bit loads per block
 };
 
 template <int QT, int NB, int R>
 struct Chunk {
     u32x4 q[R][NB][Payload<QT>::V];
-    uint16_t d[R][NB];  // f16 d; Q4_K: sc | m << 8
-    uint32_t h[R][NB];  // Q4_K: d | dmin << 16 of the block's 256-weight group
+    uint16_t d[R][NB];  // f16 d; Q4_K: sc | m << 8; Q6_K: int8 scales of the two halves
+    uint32_t h[R][NB];  // Q4_K: d | dmin << 16 of the block's 256-weight group; Q6_K: d
 };
 
 // Weight addresses: base + row * rb + a lane offset, with the row offset
@@ -291,7 +295,7 @@ __device__ __forceinline__ void load_chunk(Chunk<QT, NB, R>& c, const uint8_t* _
                 c.q[r][i][v] = __builtin_nontemporal_load(
                     reinterpret_cast<const u32x4*>(base + ro + poff[i]) + v);
             c.d[r][i] = *reinterpret_cast<const uint16_t*>(base + ro + soff[i]);
-            if constexpr (QT == UNILLM_QTYPE_Q4_K)
+            if constexpr (QT == UNILLM_QTYPE_Q4_K || QT == UNILLM_QTYPE_Q6_K)
                 c.h[r][i] = *reinterpret_cast<const uint32_t*>(base + ro + hoff[i]);
         }
     }
@@ -314,7 +318,27 @@ __device__ __forceinline__ void compute_chunk(const Chunk<QT, NB, R>& c, const X
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 int acc;
-                if constexpr (QT != UNILLM_QTYPE_Q8_0) {
+                if constexpr (QT == UNILLM_QTYPE_Q6_K) {
+                    // per 16-weight half v: A_v = 254 sum q d0 + sum q d1, scaled by d sc_v
+                    int ah[2];
+#pragma unroll
+                    for (int v = 0; v < 2; ++v) {
+                        const u32x4 w4 = c.q[r][i][v];
+                        int a0 = 0, a1 = 0;
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            a0 = sdot4((int)w4[t], (int)xb.dg[v][t], a0);
+                            a1 = sdot4((int)w4[t], (int)xb.dg[2 + v][t], a1);
+                        }
+                        ah[v] = a0 * 254 + a1;
+                    }
+                    const uint32_t sm = c.d[r][i];
+                    const float dd = __half2float(__ushort_as_half((uint16_t)c.h[r][i]));
+                    const float sv = fmaf((float)(int8_t)(sm & 0xFFu), (float)ah[0],
+                                          (float)(int8_t)(sm >> 8) * (float)ah[1]);
+                    part[m][r] = fmaf(dd, sv * xb.sx, part[m][r]);
+                    continue;
+                } else if constexpr (!kByteCodes<QT>) {
                     // digit levels 3..0: A = ((a3 * 16 + a2) * 16 + a1) * 16 + a0
                     const u32x4 w4 = c.q[r][i][0];
                     int lv[4] = {0, 0, 0, 0};
@@ -403,7 +427,8 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
         bidx[i] = min(b, KB - 1);
         poff[i] = (uint32_t)bidx[i] * (16 * Payload<QT>::V);
         soff[i] = (uint32_t)KB * (16 * Payload<QT>::V) + 2u * (uint32_t)bidx[i];
-        hoff[i] = (uint32_t)KB * 18u + 4u * (uint32_t)(bidx[i] >> 3);  // Q4_K group header
+        // K-quant group header, after the payload and scale planes
+        hoff[i] = (uint32_t)KB * (16u * Payload<QT>::V + 2u) + 4u * (uint32_t)(bidx[i] >> 3);
     }
 
     // 1. x for the digits.  A wave whose quarters of a pass all lie past nq
@@ -423,7 +448,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
         quarter_offsets<QT>(q & 3, o0, o1);
         const float4 f0 = *reinterpret_cast<const float4*>(xb + o0);
         const float4 f1 = *reinterpret_cast<const float4*>(xb + o1);
-        if constexpr (QT != UNILLM_QTYPE_Q8_0) {  // payload nibble order
+        if constexpr (!kByteCodes<QT>) {  // payload nibble order
             v[p][0] = f0.x; v[p][1] = f1.x; v[p][2] = f0.y; v[p][3] = f1.y;
             v[p][4] = f0.z; v[p][5] = f1.z; v[p][6] = f0.w; v[p][7] = f1.w;
         } else {
@@ -448,7 +473,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
         if (wave0 + p * THREADS >= nq) continue;
         const int q = threadIdx.x + p * THREADS;
         uint32_t* dst = xlds + (size_t)(min(q, nq - 1) >> 2) * kXWords;
-        if constexpr (QT == UNILLM_QTYPE_Q8_0) prep_q8(v[p], q & 3, q < nq, dst);
+        if constexpr (kByteCodes<QT>) prep_q8(v[p], q & 3, q < nq, dst);
         else prep_q4<QT == UNILLM_QTYPE_Q4_K>(v[p], q & 3, q < nq, dst);
         __builtin_amdgcn_sched_barrier(0);  // one pass's temporaries live at a time
     }
@@ -528,9 +553,9 @@ hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipSt
         case 2: return launch_nb<QT, M, 2>(w, x, m, y, st);
         case 3: if constexpr (M <= 2) return launch_nb<QT, M, 3>(w, x, m, y, st); break;
         case 4: if constexpr (M <= 2) return launch_nb<QT, M, 4>(w, x, m, y, st); break;
-        case 5: if constexpr (M == 1 && QT != UNILLM_QTYPE_Q8_0) return launch_nb<QT, M, 5>(w, x, m, y, st); break;
-        case 6: if constexpr (M == 1 && QT != UNILLM_QTYPE_Q8_0) return launch_nb<QT, M, 6>(w, x, m, y, st); break;
-        case 7: if constexpr (M == 1 && QT != UNILLM_QTYPE_Q8_0) return launch_nb<QT, M, 7>(w, x, m, y, st); break;
+        case 5: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 5>(w, x, m, y, st); break;
+        case 6: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 6>(w, x, m, y, st); break;
+        case 7: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 7>(w, x, m, y, st); break;
         default: break;
     }
     return hipErrorInvalidValue;
@@ -543,7 +568,7 @@ hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipSt
 // NB = 7 at one row (K = 14336), 4 at two, 2 at four; Q8_0 payloads are twice
 // as wide, so it stops at NB = 4.  M * KB <= 512 also bounds the LDS (40 KiB).
 int64_t gemv_max_kb(int64_t m, int qtype) {
-    if (m <= 1) return qtype == UNILLM_QTYPE_Q8_0 ? 256 : 448;
+    if (m <= 1) return qtype == UNILLM_QTYPE_Q8_0 || qtype == UNILLM_QTYPE_Q6_K ? 256 : 448;
     if (m <= 2) return 256;
     return 128;
 }
@@ -559,6 +584,11 @@ hipError_t launch_gemv(const QWeight& w, const float* x, int64_t m, float* y, hi
         if (m == 1) return launch_m<UNILLM_QTYPE_Q4_K, 1>(w, x, m, y, s);
         if (m == 2) return launch_m<UNILLM_QTYPE_Q4_K, 2>(w, x, m, y, s);
         return launch_m<UNILLM_QTYPE_Q4_K, 4>(w, x, m, y, s);
+    }
+    if (w.qtype == UNILLM_QTYPE_Q6_K) {
+        if (m == 1) return launch_m<UNILLM_QTYPE_Q6_K, 1>(w, x, m, y, s);
+        if (m == 2) return launch_m<UNILLM_QTYPE_Q6_K, 2>(w, x, m, y, s);
+        return launch_m<UNILLM_QTYPE_Q6_K, 4>(w, x, m, y, s);
     }
     if (w.qtype == UNILLM_QTYPE_Q4_0) {
         if (m == 1) return launch_m<UNILLM_QTYPE_Q4_0, 1>(w, x, m, y, s);

@@ -21,6 +21,13 @@
 // q - 8; element j low nibble of byte j, element j + 16 high nibble), so
 // w = (d sc) q - dmin m = (d sc)(q - 8) + (8 d sc - dmin m).  18.5 B per 32
 // weights against GGUF's 18; d sc and dmin m are exact in f32.
+//
+// Q6_K (GGML block_q6_K: 256 weights, 6-bit codes q, int8 scale per 16
+// weights, one f16 d) is repacked into Q8_0's frame:
+//   [kb x 32 B int8 codes q - 32][kb x u16 (sc_lo | sc_hi << 8)][kb / 8 x u32 d][pad]
+// sc_lo scales weights 0 .. 15 of the block, sc_hi 16 .. 31 (GGML's scales[j]
+// covers weights 16 j .. 16 j + 15); w = (d sc) (q - 32), d sc exact in f32.
+// 34.5 B per 32 weights against GGUF's 26.25: the 6-bit codes take a byte each.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -49,9 +56,14 @@ using QWeight = ::unillm_qweight;
 int64_t gemv_max_kb(int64_t m, int qtype);
 bool gemv_supports(const unillm_qweight& w, int64_t m);
 
-inline int qbytes(int qtype) { return qtype == UNILLM_QTYPE_Q8_0 ? 32 : 16; }
+inline bool is_kquant(int qtype) {
+    return qtype == UNILLM_QTYPE_Q4_K || qtype == UNILLM_QTYPE_Q6_K;
+}
+inline int qbytes(int qtype) {
+    return qtype == UNILLM_QTYPE_Q8_0 || qtype == UNILLM_QTYPE_Q6_K ? 32 : 16;
+}
 inline int64_t row_bytes_for(int qtype, int64_t kb) {
-    const int64_t hdr = qtype == UNILLM_QTYPE_Q4_K ? kb / 8 * 4 : 0;
+    const int64_t hdr = is_kquant(qtype) ? kb / 8 * 4 : 0;
     return (kb * (qbytes(qtype) + 2) + hdr + 15) / 16 * 16;
 }
 
@@ -66,13 +78,27 @@ __host__ __device__ __forceinline__ const uint16_t* blk_scale(const uint8_t* bas
                                                                int64_t kb, int64_t row, int64_t b) {
     return reinterpret_cast<const uint16_t*>(base + row * rb + kb * QB) + b;
 }
-// Q4_K: the u32 (d | dmin << 16) of the 256-weight group holding block b.
+// K-quants: the u32 header of the 256-weight group holding block b (Q4_K:
+// d | dmin << 16; Q6_K: d), after the payload (QB bytes a block) and u16 planes.
+template <int QB>
+__host__ __device__ __forceinline__ const uint32_t* kq_header(const uint8_t* base, int64_t rb,
+                                                              int64_t kb, int64_t row, int64_t b) {
+    return reinterpret_cast<const uint32_t*>(base + row * rb + kb * (QB + 2)) + (b >> 3);
+}
 __host__ __device__ __forceinline__ const uint32_t* q4k_header(const uint8_t* base, int64_t rb,
                                                                int64_t kb, int64_t row, int64_t b) {
-    return reinterpret_cast<const uint32_t*>(base + row * rb + kb * 18) + (b >> 3);
+    return kq_header<16>(base, rb, kb, row, b);
 }
-// GGUF bytes per 32 weights: 18 (Q4_0, and Q4_K's 144 per 256), 34 (Q8_0)
-inline int gguf_block_bytes(int qtype) { return qtype == UNILLM_QTYPE_Q8_0 ? 34 : 18; }
+// GGUF bytes per block and weights per block
+inline int gguf_block_elems(int qtype) { return is_kquant(qtype) ? 256 : QK; }
+inline int gguf_block_bytes(int qtype) {
+    switch (qtype) {
+        case UNILLM_QTYPE_Q8_0: return 34;
+        case UNILLM_QTYPE_Q4_K: return 144;
+        case UNILLM_QTYPE_Q6_K: return 210;
+        default: return 18;
+    }
+}
 
 // Per-device properties cached at init.
 struct DeviceInfo {
@@ -95,7 +121,7 @@ bool debug_launch();
 hipError_t launch_repack(const QWeight& w, const uint8_t* gguf, hipStream_t s);
 hipError_t launch_dequant(const QWeight& w, float* out, hipStream_t s);
 // max over the scale plane of (f16 bits & 0x7FFF), atomically max-ed into out[0]
-// (Q4_K: max |d| into out[0], max |dmin| into out[1])
+// (Q4_K: max |d| into out[0], max |dmin| into out[1]; Q6_K: max |d| into out[0])
 hipError_t launch_scale_absmax(const QWeight& w, uint32_t* out, hipStream_t s);
 hipError_t launch_quantize(int qtype, const float* w, int64_t n, int64_t k, uint8_t* out,
                            hipStream_t s);

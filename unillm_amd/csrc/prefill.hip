@@ -87,7 +87,7 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 // one rounding to bf16.
 template <int QT>
 __device__ __forceinline__ bf16x8 dequant8(u32x2 raw, int shift, float d, float off) {
-    constexpr bool kNib = QT != UNILLM_QTYPE_Q8_0;
+    constexpr bool kNib = QT == UNILLM_QTYPE_Q4_0 || QT == UNILLM_QTYPE_Q4_K;
     constexpr uint32_t kFlip = kNib ? 0x88888888u : 0x80808080u;
     uint32_t u[2];
 #pragma unroll
@@ -155,12 +155,14 @@ __global__ __launch_bounds__(256) void x_to_bf16_kernel(const float* __restrict_
 
 template <int QT, int BM>
 struct Ring {
-    static constexpr int QB = QT == UNILLM_QTYPE_Q8_0 ? 32 : 16;  // payload bytes per block
-    static constexpr bool K4 = QT == UNILLM_QTYPE_Q4_K;
+    static constexpr int QB =
+        QT == UNILLM_QTYPE_Q8_0 || QT == UNILLM_QTYPE_Q6_K ? 32 : 16;  // payload bytes per block
+    static constexpr bool K4 = QT == UNILLM_QTYPE_Q4_K, K6 = QT == UNILLM_QTYPE_Q6_K;
+    static constexpr bool KQ = K4 || K6;
     static constexpr int A = BM * 128;
     static constexpr int BP = PBN * 2 * QB;
     static constexpr int BS = 2 * PBN * 4;
-    static constexpr int BH = K4 ? 2 * PBN * 4 : 0;  // Q4_K: the step's group header per column
+    static constexpr int BH = KQ ? 2 * PBN * 4 : 0;  // K-quants: the step's group header per column
     static constexpr int STAGE = A + BP + BS + BH;
     // stages: 4 for 128-row tiles (four fit in LDS; ~10 % over three measured),
     // 3 for 256-row tiles
@@ -168,7 +170,7 @@ struct Ring {
     static constexpr int BYTES = STAGES * STAGE;
     static constexpr int CPB = 2 * QB / 16;            // 16-byte payload chunks per column
     static constexpr int AQ = BM / 8 / 8;              // A loads (8 rows each) per wave
-    static constexpr int DMA = AQ + CPB / 2 + 1 + (K4 ? 1 : 0);  // direct loads per wave per stage
+    static constexpr int DMA = AQ + CPB / 2 + 1 + (KQ ? 1 : 0);  // direct loads per wave per stage
 };
 
 template <int QT, int BM, int NW>
@@ -179,7 +181,7 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
                                                               int KB, int tiles_n, int tiles,
                                                               int units_pad, int S) {
     static_assert(NW == 8, "the ring's load split assumes 8 waves");
-    constexpr int QB = QT == UNILLM_QTYPE_Q8_0 ? 32 : 16;  // payload bytes per block
+    constexpr int QB = Ring<QT, BM>::QB;  // payload bytes per block
     // waves: RW row groups x CW column groups; wave (rw, cw) owns rows BM / RW * rw ..
     // and columns PBN / CW * cw .. of the tile; its columns' weights are dequantized
     // by the RW waves of the group.  RW = 1: each weight once, all of A per wave.
@@ -248,8 +250,8 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
         // the step's two scales (2 ks is even: one aligned dword; an odd KB's last step
         // reads two bytes past the scales, inside the row padding or the weight's tail slot)
         dma4(base + ssrc + 4u * ks, st + R::A + R::BP + wv * 256);
-        // Q4_K: the 256-weight group header of the step (blocks 2 ks, 2 ks + 1 share it)
-        if constexpr (R::K4)
+        // K-quants: the 256-weight group header of the step (blocks 2 ks, 2 ks + 1 share it)
+        if constexpr (R::KQ)
             dma4(base + ssrc + 2u * (uint32_t)KB + 4u * (uint32_t)(ks >> 2),
                  st + R::A + R::BP + R::BS + wv * 256);
     };
@@ -258,8 +260,9 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
     // 8 g .. +7 of a block (g = l / 16): Q4_0 payload bytes 8 (g & 1) .. +7, low nibbles
     // for g < 2, high for g >= 2; Q8_0 bytes 8 g .. +7
     const int g = lane / 16, fr = lane % 16;
-    const uint32_t boff = QT != UNILLM_QTYPE_Q8_0 ? 8 * (g & 1) : 8 * g;
-    const int bshift = QT != UNILLM_QTYPE_Q8_0 ? 4 * (g >> 1) : 0;
+    constexpr bool kNib = QB == 16;
+    const uint32_t boff = kNib ? 8 * (g & 1) : 8 * g;
+    const int bshift = kNib ? 4 * (g >> 1) : 0;
     const int rw = wv / CW, cw = wv % CW;
     bool bval[TJ];
 #pragma unroll
@@ -335,9 +338,10 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
         }
         const bool b1ok = 2 * ks + 1 < KB;
         float d0[TJ], d1[TJ], o0[TJ], o1[TJ];
-        if constexpr (R::K4) {
-            // the group header (d | dmin << 16) of each column tile, laid out as the scales;
-            // sc[j] holds (sc | m << 8) of block 0 in its low half, of block 1 in its high
+        if constexpr (R::KQ) {
+            // the group header (Q4_K d | dmin << 16, Q6_K d) of each column tile, laid out
+            // as the scales; sc[j] holds block 0's u16 in its low half, block 1's in its
+            // high: Q4_K sc | m << 8, Q6_K the int8 scales of the two 16-weight halves
             uint32_t hd[TJ];
             if constexpr (TJ == 4)
                 asm volatile(
@@ -354,12 +358,22 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
 #pragma unroll
             for (int j = 0; j < TJ; ++j) {
                 const float dd = bval[j] ? __half2float(__ushort_as_half((uint16_t)hd[j])) : 0.0f;
-                const float dm = bval[j] ? __half2float(__ushort_as_half((uint16_t)(hd[j] >> 16)))
-                                         : 0.0f;
-                d0[j] = dd * (float)(sc[j] & 0xFFu);
-                o0[j] = -(dm * (float)((sc[j] >> 8) & 0xFFu));
-                d1[j] = b1ok ? dd * (float)((sc[j] >> 16) & 0xFFu) : 0.0f;
-                o1[j] = b1ok ? -(dm * (float)(sc[j] >> 24)) : 0.0f;
+                if constexpr (R::K4) {
+                    const float dm =
+                        bval[j] ? __half2float(__ushort_as_half((uint16_t)(hd[j] >> 16))) : 0.0f;
+                    d0[j] = dd * (float)(sc[j] & 0xFFu);
+                    o0[j] = -(dm * (float)((sc[j] >> 8) & 0xFFu));
+                    d1[j] = b1ok ? dd * (float)((sc[j] >> 16) & 0xFFu) : 0.0f;
+                    o1[j] = b1ok ? -(dm * (float)(sc[j] >> 24)) : 0.0f;
+                } else {
+                    // this lane's elements 8 g .. 8 g + 7 lie in half g / 2 of each block;
+                    // codes are q - 32 + 128 after the flip, so off = -128 d sc
+                    const int hs = 8 * (g >> 1);
+                    d0[j] = dd * (float)(int8_t)(sc[j] >> hs);
+                    d1[j] = b1ok ? dd * (float)(int8_t)(sc[j] >> (16 + hs)) : 0.0f;
+                    o0[j] = -128.0f * d0[j];
+                    o1[j] = -128.0f * d1[j];
+                }
             }
         } else {
             constexpr float kOff = QT == UNILLM_QTYPE_Q4_0 ? -8.0f : -128.0f;
@@ -500,6 +514,9 @@ hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, floa
     if (w.qtype == UNILLM_QTYPE_Q4_K)
         return plan.bm == 256 ? launch_bm<UNILLM_QTYPE_Q4_K, 256>(w, xb, m, y, 1, s)
                               : launch_bm<UNILLM_QTYPE_Q4_K, 128>(w, xb, m, y, plan.S, s);
+    if (w.qtype == UNILLM_QTYPE_Q6_K)
+        return plan.bm == 256 ? launch_bm<UNILLM_QTYPE_Q6_K, 256>(w, xb, m, y, 1, s)
+                              : launch_bm<UNILLM_QTYPE_Q6_K, 128>(w, xb, m, y, plan.S, s);
     const bool q4 = w.qtype == UNILLM_QTYPE_Q4_0;
     if (plan.bm == 256)
         return q4 ? launch_bm<UNILLM_QTYPE_Q4_0, 256>(w, xb, m, y, 1, s)

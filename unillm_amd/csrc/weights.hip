@@ -89,6 +89,44 @@ __global__ __launch_bounds__(256) void repack_q4k_kernel(const uint8_t* __restri
         make_uint4(words[0], words[1], words[2], words[3]);
 }
 
+// One thread per 32-weight block of GGUF Q6_K (210-byte blocks {u8 ql[128];
+// u8 qh[64]; i8 scales[16]; f16 d}).  Weight e of a block (half h = e / 128,
+// r = e % 128, t = r / 32, l = r % 32): q = (nibble t / 2 of ql[64 h + 32 (t % 2)
+// + l]) | (bits 2 t .. 2 t + 1 of qh[32 h + l]) << 4, scale scales[e / 16]
+// (GGML dequantize_row_q6_K) -> int8 codes q - 32, the two scales, and for the
+// first block of a group the header d.
+__global__ __launch_bounds__(256) void repack_q6k_kernel(const uint8_t* __restrict__ src,
+                                                         uint8_t* __restrict__ base, int64_t rb,
+                                                         int64_t kb, int64_t nblocks) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const int64_t row = i / kb, blk = i - row * kb;
+    const int j = (int)(blk & 7);
+    const uint8_t* b = src + (i >> 3) * 210;
+    const uint8_t* ql = b;
+    const uint8_t* qh = b + 128;
+    *const_cast<uint16_t*>(blk_scale<32>(base, rb, kb, row, blk)) =
+        (uint16_t)(b[192 + 2 * j] | (b[192 + 2 * j + 1] << 8));
+    if (j == 0) *const_cast<uint32_t*>(kq_header<32>(base, rb, kb, row, blk)) = ld_u16(b + 208);
+    uint32_t words[8];
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = 32 * j + 4 * w + u;
+            const int h = e >> 7, r = e & 127, t = r >> 5, l = r & 31;
+            const uint32_t lo = ((uint32_t)ql[64 * h + 32 * (t & 1) + l] >> (4 * (t >> 1))) & 15u;
+            const uint32_t hi = ((uint32_t)qh[32 * h + l] >> (2 * t)) & 3u;
+            v |= (((lo | (hi << 4)) - 32u) & 0xFFu) << (8 * u);
+        }
+        words[w] = v;
+    }
+    uint4* dst = reinterpret_cast<uint4*>(const_cast<uint8_t*>(blk_payload<32>(base, rb, row, blk)));
+    dst[0] = make_uint4(words[0], words[1], words[2], words[3]);
+    dst[1] = make_uint4(words[4], words[5], words[6], words[7]);
+}
+
 // Exact dequant (GGML to_float): Q4_0 w[j] = (lo(qs[j]) - 8) * d,
 // w[j + 16] = (hi(qs[j]) - 8) * d (stored here as the signed nibbles q - 8);
 // Q8_0 w[j] = qs[j] * d.  One thread per
@@ -101,11 +139,32 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
                                                       int64_t rb, int64_t kb,
                                                       float* __restrict__ out,
                                                       int64_t nblocks) {
-    constexpr int QB = QT == UNILLM_QTYPE_Q8_0 ? 32 : 16;
+    constexpr int QB = QT == UNILLM_QTYPE_Q8_0 || QT == UNILLM_QTYPE_Q6_K ? 32 : 16;
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nblocks) return;
     const int64_t row = i / kb, blk = i - row * kb;
     const uint16_t sw = *blk_scale<QB>(base, rb, kb, row, blk);
+    if constexpr (QT == UNILLM_QTYPE_Q6_K) {
+        // (d sc) (q - 32), as GGML evaluates it: d sc exact, the second product rounds once
+        const float d = __half2float(__ushort_as_half((uint16_t)*kq_header<32>(base, rb, kb, row, blk)));
+        const float s0 = d * (float)(int8_t)(sw & 0xFFu), s1 = d * (float)(int8_t)(sw >> 8);
+        const uint4* q = reinterpret_cast<const uint4*>(blk_payload<QB>(base, rb, row, blk));
+        float4* o = reinterpret_cast<float4*>(out + i * QK);
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+            const uint4 qq = q[v];
+            const uint32_t w[4] = {qq.x, qq.y, qq.z, qq.w};
+            const float sv = v ? s1 : s0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                float f[4];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) f[b] = __fmul_rn(sv, (float)(int8_t)(w[t] >> (8 * b)));
+                o[4 * v + t] = make_float4(f[0], f[1], f[2], f[3]);
+            }
+        }
+        return;
+    }
     const uint8_t* qs = blk_payload<QB>(base, rb, row, blk);
     float4* o = reinterpret_cast<float4*>(out + i * QK);
     if constexpr (QT == UNILLM_QTYPE_Q4_K) {
@@ -272,6 +331,28 @@ __global__ __launch_bounds__(256) void q4k_header_absmax_kernel(const uint8_t* _
     }
 }
 
+// Q6_K: max |d| over the group headers.
+__global__ __launch_bounds__(256) void q6k_header_absmax_kernel(const uint8_t* __restrict__ base,
+                                                                int64_t rb, int64_t kb,
+                                                                int64_t count,
+                                                                uint32_t* __restrict__ out) {
+    __shared__ uint32_t part[256];
+    uint32_t md = 0;
+    const int64_t groups = kb / 8;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = i / groups;
+        md = max(md, *kq_header<32>(base, rb, kb, row, 8 * (i - row * groups)) & 0x7FFFu);
+    }
+    part[threadIdx.x] = md;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) part[threadIdx.x] = max(part[threadIdx.x], part[threadIdx.x + s]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) atomicMax(out, part[0]);
+}
+
 inline unsigned grid_for(int64_t items, int block) {
     return (unsigned)((items + block - 1) / block);
 }
@@ -282,6 +363,8 @@ hipError_t launch_repack(const QWeight& w, const uint8_t* gguf, hipStream_t s) {
     const int64_t nb = w.n * w.kb;
     if (w.qtype == UNILLM_QTYPE_Q4_K)
         repack_q4k_kernel<<<grid_for(nb, 256), 256, 0, s>>>(gguf, w.base, w.row_bytes, w.kb, nb);
+    else if (w.qtype == UNILLM_QTYPE_Q6_K)
+        repack_q6k_kernel<<<grid_for(nb, 256), 256, 0, s>>>(gguf, w.base, w.row_bytes, w.kb, nb);
     else if (w.qtype == UNILLM_QTYPE_Q4_0)
         repack_kernel<16><<<grid_for(nb, 256), 256, 0, s>>>(gguf, w.base, w.row_bytes, w.kb, nb);
     else
@@ -294,6 +377,8 @@ hipError_t launch_scale_absmax(const QWeight& w, uint32_t* out, hipStream_t s) {
     const unsigned grid = (unsigned)std::min<int64_t>(1024, (nb + 255) / 256);
     if (w.qtype == UNILLM_QTYPE_Q4_K)
         q4k_header_absmax_kernel<<<grid, 256, 0, s>>>(w.base, w.row_bytes, w.kb, nb / 8, out);
+    else if (w.qtype == UNILLM_QTYPE_Q6_K)
+        q6k_header_absmax_kernel<<<grid, 256, 0, s>>>(w.base, w.row_bytes, w.kb, nb / 8, out);
     else if (w.qtype == UNILLM_QTYPE_Q4_0)
         scale_absmax_kernel<16><<<grid, 256, 0, s>>>(w.base, w.row_bytes, w.kb, nb, out);
     else
@@ -305,6 +390,9 @@ hipError_t launch_dequant(const QWeight& w, float* out, hipStream_t s) {
     const int64_t nb = w.n * w.kb;
     if (w.qtype == UNILLM_QTYPE_Q4_K)
         dequant_kernel<UNILLM_QTYPE_Q4_K><<<grid_for(nb, 256), 256, 0, s>>>(w.base, w.row_bytes,
+                                                                            w.kb, out, nb);
+    else if (w.qtype == UNILLM_QTYPE_Q6_K)
+        dequant_kernel<UNILLM_QTYPE_Q6_K><<<grid_for(nb, 256), 256, 0, s>>>(w.base, w.row_bytes,
                                                                             w.kb, out, nb);
     else if (w.qtype == UNILLM_QTYPE_Q4_0)
         dequant_kernel<UNILLM_QTYPE_Q4_0><<<grid_for(nb, 256), 256, 0, s>>>(w.base, w.row_bytes,

@@ -1,4 +1,4 @@
-"""QuantLinear: a device-resident GGUF Q4_0 / Q8_0 / Q4_K weight and its forward.
+"""QuantLinear: a device-resident GGUF Q4_0 / Q8_0 / Q4_K / Q6_K weight and its forward.
 
 It takes the slot that `Arc<QMatMul>` holds in unillm's
 `ModelWeights.quantized_tensors` (crates/runtime/src/model_core.rs:134) and
@@ -20,7 +20,7 @@ import numpy as np
 import torch
 
 from . import _capi
-from ._capi import BLOCK_BYTES, QK, Q4_0, Q4_K, Q8_0, HipError
+from ._capi import BLOCK_BYTES, BLOCK_ELEMS, QK, Q4_0, Q4_K, Q6_K, Q8_0, HipError
 
 
 def _stream_ptr(stream: torch.cuda.Stream | None) -> int:
@@ -41,7 +41,7 @@ class QuantLinear:
     @classmethod
     def from_blocks(cls, qtype: int, n: int, k: int, blocks) -> "QuantLinear":
         """From GGUF block bytes in host memory (n * k/32 blocks of 18 / 34 B, or
-        n * k/256 blocks of 144 B for Q4_K)."""
+        n * k/256 blocks of 144 / 210 B for Q4_K / Q6_K)."""
         buf = np.ascontiguousarray(np.frombuffer(memoryview(blocks), dtype=np.uint8))
         h = ctypes.c_void_p()
         _capi.check(_capi.lib().unillm_hip_qweight_create(
@@ -81,7 +81,7 @@ class QuantLinear:
 
     @property
     def gguf_bytes(self) -> int:
-        return self.n * (self.k // QK) * BLOCK_BYTES[self.qtype]
+        return self.n * (self.k // BLOCK_ELEMS[self.qtype]) * BLOCK_BYTES[self.qtype]
 
     def select_path(self, m: int) -> int:
         return _capi.lib().unillm_hip_select_path(self._h, m)
@@ -135,7 +135,8 @@ class QuantLinear:
             pass
 
     def __repr__(self) -> str:
-        name = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K"}.get(self.qtype, str(self.qtype))
+        name = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}.get(self.qtype,
+                                                                         str(self.qtype))
         return f"QuantLinear({name}, n={self.n}, k={self.k})"
 
 
@@ -144,6 +145,8 @@ def quantize_blocks(qtype: int, w: torch.Tensor,
     """GGML quantizer on the device: f32 [n, k] -> uint8 GGUF block bytes."""
     if w.dtype != torch.float32 or not w.is_cuda or not w.is_contiguous() or w.dim() != 2:
         raise ValueError("w must be a contiguous f32 [n, k] device tensor")
+    if qtype not in (Q4_0, Q8_0):
+        raise ValueError("the device quantizer (GGML's reference quantizer) covers Q4_0 and Q8_0")
     n, k = w.shape
     if k % QK:
         raise ValueError(f"k = {k} is not a multiple of 32")

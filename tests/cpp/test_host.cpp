@@ -1,15 +1,18 @@
 // test_host.cpp -- tests of the C++ host layer (unillm_amd/host), run by
 // tests/test_host_cpp.py.
 //
-//   test_host cpu <file.gguf> <file.expect>   parsing, name map, plan, errors
-//   test_host gpu <file.gguf> <file.expect>   load to the device + forward parity
+//   test_host cpu <file.gguf> <file.expect>      parsing, name map, plan, errors
+//   test_host gpu <file.gguf> <file.expect>      load to the device + forward parity
+//   test_host cpu-kq / gpu-kq <q4_k_m.gguf> <.expect>   the Q4_K / Q6_K file: plan,
+//                                                 parity, QKV and gate+up fusion
 //
-// The .gguf / .expect pair is written by tests/golden/make_gguf.py.
+// The .gguf / .expect pairs are written by tests/golden/make_gguf.py.
 #include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <fstream>
 #include <functional>
+#include <map>
 #include <string>
 #include <vector>
 
@@ -207,6 +210,86 @@ static void test_gpu(const std::string& gguf, const std::vector<Expect>& ex) {
                       "QMatMul forward failed: input is on CPU"));
 }
 
+static void test_cpu_kq(const std::string& gguf, const std::vector<Expect>& ex) {
+    const GgufFile f = GgufFile::open(gguf);
+    const GgufModelConfig c = GgufWeightLoader::config_from(f);
+    CHECK(c.hidden_size == 256 && c.intermediate_size == 512 && c.num_hidden_layers == 2);
+    GgufWeightLoader loader;
+    const auto plan = loader.plan(f);
+    size_t n4 = 0, n6 = 0;
+    for (size_t i = 0; i < plan.size() && i < ex.size(); ++i) {
+        CHECK(plan[i].type == ex[i].type);
+        CHECK(plan[i].quantized == (ex[i].quantized != 0));
+        n4 += plan[i].type == GGML_Q4_K;
+        n6 += plan[i].type == GGML_Q6_K;
+    }
+    CHECK(n4 == 12 + 1 && n6 == 3);  // token_embd Q4_K; attn_v.0, ffn_down.0, output Q6_K
+    const GgufTensorInfo* q = nullptr;
+    for (const auto& t : f.tensors())
+        if (t.name == "output.weight") q = &t;
+    CHECK(q && q->type == GGML_Q6_K && q->nbytes == 256 * 1 * 210);  // 256 rows x 1 block
+}
+
+static void test_gpu_kq(const std::string& gguf, const std::vector<Expect>& ex) {
+    GgufWeightLoader loader;
+    const ModelWeights w = loader.load_weights(gguf);
+    CHECK(w.quantized_tensors.size() == 15 && w.fused_parts.empty());
+    CHECK(w.get_quantized("lm_head.weight")->qtype() == GGML_Q6_K);
+    CHECK(w.get_quantized("model.layers.1.mlp.down_proj.weight")->qtype() == GGML_Q4_K);
+    CHECK(w.tensors.at("model.embed_tokens.weight").shape() == std::vector<int64_t>({256, 256}));
+    std::map<std::string, std::vector<float>> ys;
+    for (const Expect& e : ex) {
+        if (!e.quantized) continue;
+        auto q = w.get_quantized(e.hf_name);
+        CHECK(q != nullptr);
+        if (!q) continue;
+        const Tensor x = Tensor::from_host(e.x, {(int64_t)e.m, (int64_t)e.k}, Device::hip(0));
+        ys[e.hf_name] = q->forward(x).to_host();
+        const double err = normwise(ys[e.hf_name], e.y);
+        if (err >= 1e-3) std::fprintf(stderr, "  %s: normwise %.3g\n", e.hf_name.c_str(), err);
+        CHECK(err < 1e-3);
+    }
+    // fusion: layer 1 (all Q4_K) fuses q/k/v and gate/up; layer 0 keeps q/k/v apart
+    // (its attn_v is Q6_K) but fuses gate/up
+    LoadOptions opt;
+    opt.fuse_qkv = opt.fuse_gate_up = true;
+    const ModelWeights fw = loader.load_weights(gguf, opt);
+    CHECK(fw.get_quantized("model.layers.1.self_attn.qkv_proj.weight") != nullptr);
+    CHECK(fw.get_quantized("model.layers.1.self_attn.q_proj.weight") == nullptr);
+    CHECK(fw.get_quantized("model.layers.0.self_attn.qkv_proj.weight") == nullptr);
+    CHECK(fw.get_quantized("model.layers.0.self_attn.v_proj.weight") != nullptr);
+    CHECK(fw.get_quantized("model.layers.0.mlp.gate_up_proj.weight") != nullptr);
+    CHECK(fw.fused_parts.size() == 3);  // qkv.1, gate_up.0, gate_up.1
+    for (const auto& [fname, parts] : fw.fused_parts) {
+        auto q = fw.get_quantized(fname);
+        CHECK(q != nullptr);
+        if (!q) continue;
+        const Expect* first = nullptr;
+        for (const Expect& e : ex)
+            if (e.hf_name == parts[0].first) first = &e;
+        CHECK(first != nullptr);
+        if (!first) continue;
+        // the parts' own expectations share x (same input, same k) only through
+        // the first part's x: run the fused handle on it and compare each column
+        // slice with the part loaded on its own, run on the same x
+        const Tensor x =
+            Tensor::from_host(first->x, {(int64_t)first->m, (int64_t)first->k}, Device::hip(0));
+        const std::vector<float> y = q->forward(x).to_host();
+        int64_t off = 0;
+        for (const auto& [pname, rows] : parts) {
+            const std::vector<float> yp = w.get_quantized(pname)->forward(x).to_host();
+            bool same = true;
+            for (int64_t r = 0; r < (int64_t)first->m; ++r)
+                for (int64_t c = 0; c < rows; ++c)
+                    same = same && y[r * q->n() + off + c] == yp[r * rows + c];
+            if (!same) std::fprintf(stderr, "  %s: slice of %s differs\n", pname.c_str(), fname.c_str());
+            CHECK(same);
+            off += rows;
+        }
+        CHECK(off == q->n());
+    }
+}
+
 int main(int argc, char** argv) {
     if (argc != 4) {
         std::fprintf(stderr, "usage: %s cpu|gpu file.gguf file.expect\n", argv[0]);
@@ -217,6 +300,8 @@ int main(int argc, char** argv) {
         const std::vector<Expect> ex = read_expect(argv[3]);
         if (mode == "cpu") test_cpu(argv[2], ex);
         else if (mode == "gpu") test_gpu(argv[2], ex);
+        else if (mode == "cpu-kq") test_cpu_kq(argv[2], ex);
+        else if (mode == "gpu-kq") test_gpu_kq(argv[2], ex);
         else return 2;
     } catch (const std::exception& e) {
         std::fprintf(stderr, "FAIL: uncaught exception: %s\n", e.what());

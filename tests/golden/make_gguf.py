@@ -1,4 +1,4 @@
-"""Write tests/golden/tiny_llama_q4_0.gguf and its expected outputs.
+"""Write tests/golden/tiny_llama_q4_0.gguf, tiny_llama_q4_k_m.gguf and their expected outputs.
 
 A minimal GGUF v3 file in the layout llama.cpp writes for a Llama model:
 2 blocks of attn_q/k/v/output + ffn_gate/up/down (Q4_0), token_embd (Q8_0),
@@ -15,11 +15,17 @@ Expected values (tiny_llama_q4_0.npz): for every projection, x and
 y = x . dequant(W)^T in f64 (numpy), the names after the reference's
 gguf_to_hf_name map (crates/runtime/src/weight_loader_core.rs:760-798), and
 which tensors stay quantized (weight_loader_core.rs:554).
+
+tiny_llama_q4_k_m.gguf has the tensor types llama.cpp's Q4_K_M mix uses:
+Q4_K projections and token_embd, Q6_K for output.weight and for layer 0's
+attn_v / ffn_down.  Its blocks are random valid Q4_K / Q6_K blocks (the
+oracle's generators) and its expectations the oracle's f64 matmul.
 """
 from __future__ import annotations
 
 import os
 import struct
+import sys
 
 import numpy as np
 
@@ -27,7 +33,7 @@ from make_golden import dequant, quantize_q4_0, quantize_q8_0
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ALIGN = 32
-T_F32, T_F16, T_Q4_0, T_Q8_0 = 0, 1, 2, 8
+T_F32, T_F16, T_Q4_0, T_Q8_0, T_Q4_K, T_Q6_K = 0, 1, 2, 8, 12, 14
 V_UINT32, V_FLOAT32, V_STRING, V_ARRAY = 4, 6, 8, 9
 
 HIDDEN, INTER, VOCAB, LAYERS = 64, 96, 128, 2
@@ -82,13 +88,55 @@ def main() -> None:
     add_f32("output_norm.weight", HIDDEN)
     add_q("output.weight", T_Q8_0, VOCAB, HIDDEN)
 
+    write(tensors, "tiny_llama_q4_0", HIDDEN, INTER, LAYERS, rng, npz=True)
+    main_kq()
+
+
+def main_kq() -> None:
+    """The Q4_K_M-style file (k a multiple of 256)."""
+    sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+    import oracle  # test infrastructure: random K-quant blocks and their exact dequant
+
+    hidden, inter, layers = 256, 512, 2
+    rng = np.random.default_rng(11)
+    tensors = []
+    seed = [100]
+
+    def add_k(name, qtype, n, k):
+        seed[0] += 1
+        gen = oracle.random_q4_k if qtype == T_Q4_K else oracle.random_q6_k
+        blocks = gen(n, k, seed[0])
+        tensors.append((name, qtype, (n, k), blocks.tobytes(), oracle.dequant(qtype, blocks, n, k)))
+
+    def add_f32(name, n):
+        v = (1.0 + rng.normal(0, 0.1, size=n)).astype(np.float32)
+        tensors.append((name, T_F32, (n,), v.tobytes(), v))
+
+    add_k("token_embd.weight", T_Q4_K, 256, hidden)
+    for i in range(layers):
+        p = f"blk.{i}."
+        add_f32(p + "attn_norm.weight", hidden)
+        add_k(p + "attn_q.weight", T_Q4_K, hidden, hidden)
+        add_k(p + "attn_k.weight", T_Q4_K, hidden // 2, hidden)
+        add_k(p + "attn_v.weight", T_Q6_K if i == 0 else T_Q4_K, hidden // 2, hidden)
+        add_k(p + "attn_output.weight", T_Q4_K, hidden, hidden)
+        add_f32(p + "ffn_norm.weight", hidden)
+        add_k(p + "ffn_gate.weight", T_Q4_K, inter, hidden)
+        add_k(p + "ffn_up.weight", T_Q4_K, inter, hidden)
+        add_k(p + "ffn_down.weight", T_Q6_K if i == 0 else T_Q4_K, hidden, inter)
+    add_f32("output_norm.weight", hidden)
+    add_k("output.weight", T_Q6_K, 256, hidden)
+    write(tensors, "tiny_llama_q4_k_m", hidden, inter, layers, rng, npz=False)
+
+
+def write(tensors, stem, hidden, inter, layers, rng, npz) -> None:
     kvs = [
         kv("general.architecture", V_STRING, "llama"),
         kv("general.name", V_STRING, "tiny-llama-test"),
         kv("general.alignment", V_UINT32, ALIGN),
-        kv("llama.embedding_length", V_UINT32, HIDDEN),
-        kv("llama.feed_forward_length", V_UINT32, INTER),
-        kv("llama.block_count", V_UINT32, LAYERS),
+        kv("llama.embedding_length", V_UINT32, hidden),
+        kv("llama.feed_forward_length", V_UINT32, inter),
+        kv("llama.block_count", V_UINT32, layers),
         kv("llama.attention.head_count", V_UINT32, 4),
         kv("llama.attention.head_count_kv", V_UINT32, 2),
         kv("llama.attention.layer_norm_rms_epsilon", V_FLOAT32, 1e-5),
@@ -107,7 +155,7 @@ def main() -> None:
         data += raw
     meta = header + infos
     meta += b"\0" * ((-len(meta)) % ALIGN)
-    with open(os.path.join(HERE, "tiny_llama_q4_0.gguf"), "wb") as f:
+    with open(os.path.join(HERE, stem + ".gguf"), "wb") as f:
         f.write(meta + data)
 
     # expected outputs for every tensor the loader keeps quantized
@@ -118,7 +166,7 @@ def main() -> None:
         mapped = hf_name(name)
         names.append(name)
         hf.append(mapped)
-        if ttype in (T_Q4_0, T_Q8_0) and ("_proj.weight" in mapped or "lm_head.weight" in mapped):
+        if ttype != T_F32 and ("_proj.weight" in mapped or "lm_head.weight" in mapped):
             n, k = shape
             x = rng.normal(0, 1, size=(3, k)).astype(np.float32)
             key = mapped.replace(".", "_")
@@ -126,7 +174,8 @@ def main() -> None:
             out["y__" + key] = x.astype(np.float64) @ deq.astype(np.float64).T
     out["gguf_names"] = np.array(names)
     out["hf_names"] = np.array(hf)
-    np.savez_compressed(os.path.join(HERE, "tiny_llama_q4_0.npz"), **out)
+    if npz:
+        np.savez_compressed(os.path.join(HERE, stem + ".npz"), **out)
     # the same expectations in a flat binary the C++ host test reads:
     # "UXPT", u32 count; per tensor: u32 len + gguf name, u32 len + hf name,
     # u32 type, u32 quantized, u32 m, u32 n, u32 k, f32 x[m*k], f64 y[m*n]
@@ -143,9 +192,9 @@ def main() -> None:
             blob += x.astype("<f4").tobytes() + y.astype("<f8").tobytes()
         else:
             blob += struct.pack("<5I", ttype, 0, 0, 0, 0)
-    with open(os.path.join(HERE, "tiny_llama_q4_0.expect"), "wb") as f:
+    with open(os.path.join(HERE, stem + ".expect"), "wb") as f:
         f.write(blob)
-    print(f"wrote tiny_llama_q4_0.gguf ({len(meta) + len(data)} B), {len(tensors)} tensors")
+    print(f"wrote {stem}.gguf ({len(meta) + len(data)} B), {len(tensors)} tensors")
 
 
 def hf_name(name: str) -> str:

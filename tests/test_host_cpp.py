@@ -1,7 +1,8 @@
 """Run the C++ host-layer test program (tests/cpp/test_host.cpp): GGUF
 parsing, the reference's name map and quantized/f32 classification, malformed
-files (CPU), then loading the tiny GGUF onto the device and QMatMul::forward
-parity against the committed expectations (GPU)."""
+files (CPU), then loading the tiny GGUFs onto the device and QMatMul::forward
+parity against the committed expectations, and load-time QKV / gate+up fusion
+(GPU)."""
 import os
 import subprocess
 
@@ -9,13 +10,13 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 BIN = os.path.join(ROOT, "tests", "cpp", "test_host")
-GGUF = os.path.join(ROOT, "tests", "golden", "tiny_llama_q4_0.gguf")
-EXPECT = os.path.join(ROOT, "tests", "golden", "tiny_llama_q4_0.expect")
+GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 
-def _run(mode):
+def _run(mode, stem="tiny_llama_q4_0"):
     assert os.path.exists(BIN), "build first: python -m unillm_amd.build"
-    r = subprocess.run([BIN, mode, GGUF, EXPECT], capture_output=True, text=True, timeout=120)
+    gguf, expect = (os.path.join(GOLDEN, stem + ext) for ext in (".gguf", ".expect"))
+    r = subprocess.run([BIN, mode, gguf, expect], capture_output=True, text=True, timeout=120)
     print(r.stdout, r.stderr)
     assert r.returncode == 0, r.stderr
     assert "0 failed" in r.stdout
@@ -28,3 +29,12 @@ def test_host_cpu():
 @pytest.mark.gpu
 def test_host_gpu():
     _run("gpu")
+
+
+def test_host_k_quants_cpu():
+    _run("cpu-kq", "tiny_llama_q4_k_m")
+
+
+@pytest.mark.gpu
+def test_host_k_quants_gpu():
+    _run("gpu-kq", "tiny_llama_q4_k_m")

@@ -284,19 +284,82 @@ std::vector<GgufWeightLoader::Plan> GgufWeightLoader::plan(const GgufFile& f) co
     return out;
 }
 
-ModelWeights GgufWeightLoader::load_weights(const std::string& path) const {
+namespace {
+
+bool device_qtype(uint32_t t) {
+    return t == GGML_Q4_0 || t == GGML_Q8_0 || t == GGML_Q4_K || t == GGML_Q6_K;
+}
+
+// The fusable groups of one layer: {fused hf name, part hf names}.
+std::vector<std::pair<std::string, std::vector<std::string>>> fusion_groups(
+    const std::string& layer, const LoadOptions& opt) {
+    std::vector<std::pair<std::string, std::vector<std::string>>> g;
+    if (opt.fuse_qkv)
+        g.push_back({layer + "self_attn.qkv_proj.weight",
+                     {layer + "self_attn.q_proj.weight", layer + "self_attn.k_proj.weight",
+                      layer + "self_attn.v_proj.weight"}});
+    if (opt.fuse_gate_up)
+        g.push_back({layer + "mlp.gate_up_proj.weight",
+                     {layer + "mlp.gate_proj.weight", layer + "mlp.up_proj.weight"}});
+    return g;
+}
+
+}  // namespace
+
+ModelWeights GgufWeightLoader::load_weights(const std::string& path,
+                                            const LoadOptions& opt) const {
     const GgufFile f = GgufFile::open(path);
     ModelWeights w;
     w.config = config_from(f);
+    std::map<std::string, const GgufTensorInfo*> by_hf;
+    for (const GgufTensorInfo& t : f.tensors()) by_hf[gguf_to_hf_name(t.name)] = &t;
+
+    // Fused projections: parts that share a type and k are concatenated row-wise
+    // (GGUF rows are whole blocks, so the block bytes simply follow each other)
+    // into one handle; the parts are then not loaded on their own.
+    std::map<std::string, bool> fused_part;
+    for (uint64_t L = 0; L < w.config.num_hidden_layers; ++L) {
+        const std::string layer = "model.layers." + std::to_string(L) + ".";
+        for (const auto& [fname, parts] : fusion_groups(layer, opt)) {
+            std::vector<const GgufTensorInfo*> ts;
+            for (const std::string& pn : parts) {
+                auto it = by_hf.find(pn);
+                if (it == by_hf.end()) break;
+                ts.push_back(it->second);
+            }
+            if (ts.size() != parts.size()) continue;
+            bool same = true;
+            for (const GgufTensorInfo* t : ts)
+                same = same && t->ne.size() == 2 && t->type == ts[0]->type &&
+                       t->ne[0] == ts[0]->ne[0] && device_qtype(t->type);
+            if (!same) continue;  // mixed types (a Q4_K_M layer): keep the parts apart
+            std::vector<uint8_t> bytes;
+            int64_t rows = 0;
+            std::vector<std::pair<std::string, int64_t>> split;
+            for (size_t i = 0; i < ts.size(); ++i) {
+                const std::vector<uint8_t> b = f.read(*ts[i]);
+                bytes.insert(bytes.end(), b.begin(), b.end());
+                split.push_back({parts[i], (int64_t)ts[i]->ne[1]});
+                rows += (int64_t)ts[i]->ne[1];
+                fused_part[parts[i]] = true;
+            }
+            w.quantized_tensors[fname] = QuantLinear::from_blocks(
+                (int)ts[0]->type, rows, (int64_t)ts[0]->ne[0], bytes.data(), bytes.size());
+            w.fused_parts[fname] = std::move(split);
+        }
+    }
+
     for (const GgufTensorInfo& t : f.tensors()) {
         const std::string hf = gguf_to_hf_name(t.name);
+        if (fused_part.count(hf)) continue;
         const std::vector<uint8_t> bytes = f.read(t);
         const std::vector<uint64_t> shp = t.shape();
         if (is_quantized_weight_name(hf)) {
-            if (t.ne.size() != 2 || (t.type != GGML_Q4_0 && t.type != GGML_Q8_0))
+            if (t.ne.size() != 2 || !device_qtype(t.type))
                 throw Error("Failed to create QMatMul for '" + t.name + "': " +
                             ggml_type_name(t.type) + " " + std::to_string(t.ne.size()) +
-                            "-D weights are not supported on the HIP device (Q4_0 / Q8_0 only)");
+                            "-D weights are not supported on the HIP device "
+                            "(Q4_0 / Q8_0 / Q4_K / Q6_K only)");
             w.quantized_tensors[hf] = QuantLinear::from_blocks(
                 (int)t.type, (int64_t)t.ne[1], (int64_t)t.ne[0], bytes.data(), bytes.size());
             continue;
@@ -314,7 +377,7 @@ ModelWeights GgufWeightLoader::load_weights(const std::string& path) const {
                 std::memcpy(&h, bytes.data() + 2 * i, 2);
                 v[i] = t.type == GGML_F16 ? half_to_float(h) : bf16_to_float(h);
             }
-        } else if (t.type == GGML_Q4_0 || t.type == GGML_Q8_0) {
+        } else if (device_qtype(t.type)) {
             const int64_t k = (int64_t)t.ne[0];
             const int64_t n = elems / k;
             auto q = QuantLinear::from_blocks((int)t.type, n, k, bytes.data(), bytes.size());

@@ -149,7 +149,21 @@ struct ModelWeights {
     std::map<std::string, Tensor> tensors;                                  // f32, host
     std::map<std::string, std::shared_ptr<QuantLinear>> quantized_tensors;  // HIP
     GgufModelConfig config;
+    // fused handle -> its parts in row order: {part hf name, rows}; a part's
+    // outputs are columns [sum of the earlier rows, + rows) of the fused output
+    std::map<std::string, std::vector<std::pair<std::string, int64_t>>> fused_parts;
     std::shared_ptr<QuantLinear> get_quantized(const std::string& name) const;
+};
+
+// Load-time fusion of projections that read the same input.  With fuse_qkv,
+// model.layers.N.self_attn.{q,k,v}_proj become one self_attn.qkv_proj handle,
+// with fuse_gate_up mlp.{gate,up}_proj one mlp.gate_up_proj handle -- one launch
+// instead of three / two per token -- when the parts share a GGUF type and k
+// (a Q4_K_M layer whose attn_v is Q6_K keeps its parts apart).  Off by default:
+// the reference model calls the parts by name.
+struct LoadOptions {
+    bool fuse_qkv = false;
+    bool fuse_gate_up = false;
 };
 
 // weight_loader_core.rs:760-798: ordered substring replacements.
@@ -161,8 +175,8 @@ class GgufWeightLoader {
 public:
     bool supports(const std::string& path) const;
     // Parses the file, uploads every *_proj / lm_head tensor to the device as
-    // a QuantLinear and dequantizes the rest to host f32.
-    ModelWeights load_weights(const std::string& path) const;
+    // a QuantLinear (Q4_0, Q8_0, Q4_K, Q6_K) and dequantizes the rest to host f32.
+    ModelWeights load_weights(const std::string& path, const LoadOptions& opt = {}) const;
     // What load_weights would do, without any device work: hf name, shape,
     // type and whether it would be quantized, per tensor.
     struct Plan {

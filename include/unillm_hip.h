@@ -104,6 +104,28 @@ int unillm_hip_qmatmul(const unillm_qweight* w, const float* x_dev, int64_t m, f
 int unillm_hip_qmatmul_path(const unillm_qweight* w, const float* x_dev, int64_t m,
                             float* y_dev, int path, void* stream);
 
+/* y[m, n] += x[m, k] . dequant(W)^T: the projection with the decoder layer's
+ * residual add in its epilogue.  Replaces qmatmul.forward followed by
+ * ops_fn::add(hidden_states, out) for o_proj and down_proj
+ * (crates/runtime/src/models_v2/llama.rs:668, 677).  y holds the residual on
+ * entry.  Equal bit for bit to qmatmul then the add, except where k is split
+ * over workgroups (partials then add onto y in any order: f32 rounding). */
+int unillm_hip_qmatmul_add(const unillm_qweight* w, const float* x_dev, int64_t m, float* y_dev,
+                           void* stream);
+
+/* act[m, I] = silu(x . G^T) * (x . U^T) for a weight whose n = 2 I rows are
+ * gate_proj (rows 0 .. I - 1) then up_proj (I .. 2 I - 1), e.g. a gate_up
+ * handle fused at load.  Replaces the two quantized_matmul calls and
+ * ops_fn::fused_swiglu of LlamaMLP::forward (llama.rs:1275-1283;
+ * tensor_core.rs:1385-1396: candle silu(v) = v / (1 + e^-v)).  On the GEMV path
+ * (m = 1: k <= 8192 for Q4_0 / Q4_K, 4096 for Q8_0 / Q6_K; half that at m = 2,
+ * a quarter at m = 3, 4) the gate and up rows meet in one wave and the
+ * activation is its epilogue; otherwise the
+ * [m, 2 I] product goes to a per-stream workspace and one elementwise pass
+ * follows.  n odd is an error. */
+int unillm_hip_qmatmul_swiglu(const unillm_qweight* w, const float* x_dev, int64_t m,
+                              float* act_dev, void* stream);
+
 /* Kernel path that unillm_hip_qmatmul selects for m rows (UNILLM_PATH_*). */
 int unillm_hip_select_path(const unillm_qweight* w, int64_t m);
 

@@ -287,6 +287,40 @@ static void test_gpu_kq(const std::string& gguf, const std::vector<Expect>& ex) 
             off += rows;
         }
         CHECK(off == q->n());
+        // the fused gate_up handle's SwiGLU: silu(gate) * up of the parts' own outputs
+        if (fname.find("gate_up_proj") != std::string::npos) {
+            const Tensor act = q->forward_swiglu(x);
+            CHECK(act.shape() == std::vector<int64_t>({(int64_t)first->m, q->n() / 2}));
+            const std::vector<float> a = act.to_host();
+            const int64_t I = q->n() / 2;
+            double worst = 0.0;
+            for (int64_t r = 0; r < (int64_t)first->m; ++r)
+                for (int64_t c = 0; c < I; ++c) {
+                    const double g = y[r * q->n() + c], u = y[r * q->n() + I + c];
+                    const double want = g / (1.0 + std::exp(-g)) * u;
+                    worst = std::max(worst, std::fabs(a[r * I + c] - want) / (1e-6 + std::fabs(want)));
+                }
+            CHECK(worst < 1e-5);
+        }
+    }
+    // the residual add: r + forward(x) in the projection's epilogue
+    {
+        auto q = w.get_quantized("model.layers.1.self_attn.o_proj.weight");
+        const Expect* e = nullptr;
+        for (const Expect& ee : ex)
+            if (ee.hf_name == "model.layers.1.self_attn.o_proj.weight") e = &ee;
+        CHECK(q && e);
+        if (q && e) {
+            const Tensor x = Tensor::from_host(e->x, {(int64_t)e->m, (int64_t)e->k}, Device::hip(0));
+            std::vector<float> r0((size_t)e->m * e->n);
+            for (size_t i = 0; i < r0.size(); ++i) r0[i] = 0.25f * (float)(i % 13) - 1.0f;
+            Tensor r = Tensor::from_host(r0, {(int64_t)e->m, (int64_t)e->n}, Device::hip(0));
+            q->forward_add(x, r);
+            const std::vector<float> got = r.to_host(), plain = q->forward(x).to_host();
+            bool same = true;
+            for (size_t i = 0; i < got.size(); ++i) same = same && got[i] == r0[i] + plain[i];
+            CHECK(same);  // GEMV: one rounding of r + the same row sum
+        }
     }
 }
 

@@ -1,0 +1,113 @@
+"""GPU parity of the fused epilogues (the scope table's row f3), through the C ABI.
+
+- unillm_hip_qmatmul_add: y += x W^T, the decoder layer's residual add
+  (llama.rs:668, 677) in the projection's epilogue;
+- unillm_hip_qmatmul_swiglu: silu(x G^T) * (x U^T) for a [gate; up] weight
+  (LlamaMLP, llama.rs:1275-1283; fused_swiglu, tensor_core.rs:1385-1396).
+
+References: the oracle's f64 matmul, plus the residual / activation in f64;
+where the kernel's own plain output is available, the fused result must equal
+"plain output, then the op" (bitwise for the add where k is not split).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import Q4_0, Q4_K, Q6_K, Q8_0
+from unillm_amd import (PATH_DECODE_MFMA, PATH_GEMV, PATH_PREFILL_MFMA, HipError, QuantLinear)
+
+pytestmark = pytest.mark.gpu
+
+TOL = {PATH_GEMV: 1e-3, PATH_DECODE_MFMA: 1e-3, PATH_PREFILL_MFMA: 2e-2}
+
+
+def _blocks(qtype, n, k, seed):
+    if qtype == Q4_K:
+        return oracle.random_q4_k(n, k, seed)
+    if qtype == Q6_K:
+        return oracle.random_q6_k(n, k, seed)
+    return oracle.quantize(qtype, oracle.normal(n * k, seed=seed, std=0.02).reshape(n, k))
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.parametrize("qtype,m,n,k,path", [
+    (Q4_0, 1, 300, 4096, PATH_GEMV), (Q4_0, 3, 129, 2048, PATH_GEMV),
+    (Q8_0, 2, 257, 2048, PATH_GEMV), (Q4_K, 1, 512, 4096, PATH_GEMV),
+    (Q4_0, 16, 4096, 4096, PATH_DECODE_MFMA), (Q4_0, 64, 300, 4096, PATH_DECODE_MFMA),
+    (Q6_K, 16, 257, 2048, PATH_DECODE_MFMA), (Q4_0, 256, 1024, 4096, PATH_PREFILL_MFMA),
+    (Q8_0, 130, 256, 8192, PATH_PREFILL_MFMA)])
+def test_residual_add(qtype, m, n, k, path):
+    # (Q4_0, 64, 300, 4096) and (Q8_0, 130, 256, 8192) split k: the partials add onto y
+    blocks = _blocks(qtype, n, k, seed=3 * n + k)
+    x = oracle.normal(m * k, seed=n + 1).reshape(m, k)
+    ql = QuantLinear.from_blocks(qtype, n, k, blocks)
+    assert ql.select_path(m) == path
+    ref = oracle.qmatmul_f64(qtype, blocks, x, n, k)
+    y0 = (oracle.normal(m * n, seed=n + 2).reshape(m, n) * float(np.abs(ref).max()))
+    y0 = y0.astype(np.float32)
+    print(f"add qtype={qtype} m={m} n={n} k={k}", flush=True)
+    xd = _dev(x)
+    y = _dev(y0)
+    ql.forward_add(xd, y)
+    plain = ql.forward(xd)
+    torch.cuda.synchronize()
+    y, plain = y.cpu().numpy(), plain.cpu().numpy()
+    assert oracle.normwise_error(y, y0.astype(np.float64) + ref) < TOL[path]
+    if path == PATH_GEMV:  # one rounding of y0 + the same row sum
+        assert np.array_equal(y, y0 + plain)
+    else:
+        assert oracle.normwise_error(y, y0 + plain) < 1e-6
+
+
+def _silu_mul(g, u):
+    return g / (1.0 + np.exp(-g)) * u
+
+
+@pytest.mark.parametrize("qtype,m,i_rows,k,path,fused", [
+    (Q4_0, 1, 1376, 4096, PATH_GEMV, True), (Q4_0, 4, 300, 1024, PATH_GEMV, True),
+    (Q4_K, 2, 512, 4096, PATH_GEMV, True), (Q8_0, 1, 700, 2048, PATH_GEMV, True),
+    (Q6_K, 1, 257, 4096, PATH_GEMV, True), (Q4_0, 4, 300, 4096, PATH_GEMV, False),
+    (Q6_K, 3, 257, 2048, PATH_GEMV, False), (Q8_0, 1, 256, 8192, PATH_GEMV, False),
+    (Q4_0, 16, 1024, 4096, PATH_DECODE_MFMA, False), (Q4_K, 64, 300, 2048, PATH_DECODE_MFMA, False),
+    (Q4_0, 256, 512, 4096, PATH_PREFILL_MFMA, False)])
+def test_swiglu(qtype, m, i_rows, k, path, fused):
+    # [gate; up] stacked as a load-time gate_up fusion would; fused = the GEMV pair
+    # epilogue (tokens x 128-bit loads per row <= 4); past its reach the GEMV
+    # stores into the workspace and an elementwise pass follows
+    gate = _blocks(qtype, i_rows, k, seed=11 + i_rows)
+    up = _blocks(qtype, i_rows, k, seed=12 + i_rows)
+    gu = np.concatenate([gate.reshape(i_rows, -1), up.reshape(i_rows, -1)], axis=0)
+    x = oracle.normal(m * k, seed=13).reshape(m, k)
+    ql = QuantLinear.from_blocks(qtype, 2 * i_rows, k, gu)
+    assert ql.select_path(m) == path
+    print(f"swiglu qtype={qtype} m={m} I={i_rows} k={k}", flush=True)
+    xd = _dev(x)
+    act = ql.forward_swiglu(xd)
+    plain = ql.forward(xd)
+    torch.cuda.synchronize()
+    act, plain = act.cpu().numpy(), plain.cpu().numpy()
+    assert act.shape == (m, i_rows)
+    g = oracle.qmatmul_f64(qtype, gate, x, i_rows, k)
+    u = oracle.qmatmul_f64(qtype, up, x, i_rows, k)
+    tol = {PATH_GEMV: 2e-3, PATH_DECODE_MFMA: 2e-3, PATH_PREFILL_MFMA: 3e-2}[path]
+    assert oracle.normwise_error(act, _silu_mul(g, u)) < tol
+    # the same as the activation applied to the kernel's own gate / up outputs
+    mine = _silu_mul(plain[:, :i_rows].astype(np.float64), plain[:, i_rows:].astype(np.float64))
+    assert oracle.normwise_error(act, mine) < (1e-6 if fused or path == PATH_GEMV else 1e-5)
+
+
+def test_swiglu_odd_rows_rejected():
+    ql = QuantLinear.from_blocks(Q4_0, 3, 64, _blocks(Q4_0, 3, 64, seed=1))
+    with pytest.raises(HipError):
+        ql.forward_swiglu(torch.zeros(1, 64, device="cuda"))
+
+
+def test_add_and_swiglu_m0_noop():
+    ql = QuantLinear.from_blocks(Q4_0, 4, 64, _blocks(Q4_0, 4, 64, seed=2))
+    y = torch.ones(0, 4, device="cuda")
+    ql.forward_add(torch.zeros(0, 64, device="cuda"), y)
+    assert ql.forward_swiglu(torch.zeros(0, 64, device="cuda")).shape == (0, 2)

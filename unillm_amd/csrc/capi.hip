@@ -5,6 +5,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <map>
 #include <mutex>
 #include <new>
 #include <string>
@@ -162,15 +163,15 @@ struct StreamWs {
     size_t bytes = 0;
 };
 std::mutex g_ws_mutex;
-std::unordered_map<hipStream_t, StreamWs> g_ws;
+std::map<std::pair<hipStream_t, int>, StreamWs> g_ws;
 
 }  // namespace
 
 const DeviceInfo& device_info() { return g_info; }
 
-hipError_t stream_workspace(hipStream_t s, size_t bytes, void** out) {
+hipError_t stream_workspace(hipStream_t s, size_t bytes, void** out, int slot) {
     std::lock_guard<std::mutex> lock(g_ws_mutex);
-    StreamWs& w = g_ws[s];
+    StreamWs& w = g_ws[{s, slot}];
     if (w.bytes < bytes) {
         // grow in stream order: earlier work on s that uses the old buffer runs
         // before the free, later work uses the new one
@@ -311,10 +312,17 @@ int unillm_hip_select_path(const unillm_qweight* w, int64_t m) {
     return UNILLM_PATH_PREFILL_MFMA;
 }
 
-int unillm_hip_qmatmul_path(const unillm_qweight* w, const float* x_dev, int64_t m,
-                            float* y_dev, int path, void* stream) {
+namespace {
+
+// The matmul on `path` with epilogue `epi` (kEpiStore / kEpiAdd; kEpiSwiglu runs
+// fused on the GEMV, else as store into the stream's second workspace + swiglu).
+int qmatmul_impl(const unillm_qweight* w, const float* x_dev, int64_t m, float* y_dev, int path,
+                 void* stream, int epi) {
     if (!w) return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: weight is NULL");
     if (m < 0) return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: m < 0");
+    if (epi == kEpiSwiglu && w->n % 2 != 0)
+        return fail(UNILLM_ERR_INVALID_ARG,
+                    "QMatMul forward failed: a SwiGLU weight stacks gate and up rows (even n)");
     if (m == 0) return UNILLM_OK;
     if (!x_dev || !y_dev)
         return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: x or y is NULL");
@@ -325,6 +333,15 @@ int unillm_hip_qmatmul_path(const unillm_qweight* w, const float* x_dev, int64_t
     if (path == UNILLM_PATH_AUTO) path = unillm_hip_select_path(w, m);
     if (int rc = ensure_init()) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    float* out = y_dev;
+    int run_epi = epi;
+    if (epi == kEpiSwiglu && !(path == UNILLM_PATH_GEMV && gemv_supports_swiglu(*w, m))) {
+        void* ws = nullptr;
+        hipError_t e = stream_workspace(s, (size_t)m * (size_t)w->n * sizeof(float), &ws, 1);
+        if (e != hipSuccess) return fail_hip(e, "QMatMul forward failed: workspace");
+        out = static_cast<float*>(ws);
+        run_epi = kEpiStore;
+    }
     hipError_t e;
     switch (path) {
         case UNILLM_PATH_GEMV:
@@ -333,20 +350,38 @@ int unillm_hip_qmatmul_path(const unillm_qweight* w, const float* x_dev, int64_t
                             "GEMV path takes m <= 4, k <= " +
                                 std::to_string(gemv_max_kb(m, w->qtype) * QK) +
                                 " at this m and weights under 4 GiB");
-            e = launch_gemv(*w, x_dev, m, y_dev, s);
+            e = launch_gemv(*w, x_dev, m, out, s, run_epi);
             break;
         case UNILLM_PATH_DECODE_MFMA:
             if (m > kDecodeMaxM)
                 return fail(UNILLM_ERR_UNSUPPORTED, "decode MFMA path takes m <= 64");
-            e = launch_decode_mfma(*w, x_dev, m, y_dev, s);
+            e = launch_decode_mfma(*w, x_dev, m, out, s, run_epi);
             break;
         case UNILLM_PATH_PREFILL_MFMA:
-            e = launch_prefill_mfma(*w, x_dev, m, y_dev, s);
+            e = launch_prefill_mfma(*w, x_dev, m, out, s, run_epi);
             break;
         default:
             return fail(UNILLM_ERR_INVALID_ARG, "unknown path " + std::to_string(path));
     }
+    if (e == hipSuccess && out != y_dev) e = launch_swiglu(out, m, w->n / 2, y_dev, s);
     return e == hipSuccess ? UNILLM_OK : fail_hip(e, "QMatMul forward failed: kernel launch");
+}
+
+}  // namespace
+
+int unillm_hip_qmatmul_path(const unillm_qweight* w, const float* x_dev, int64_t m,
+                            float* y_dev, int path, void* stream) {
+    return qmatmul_impl(w, x_dev, m, y_dev, path, stream, kEpiStore);
+}
+
+int unillm_hip_qmatmul_add(const unillm_qweight* w, const float* x_dev, int64_t m, float* y_dev,
+                           void* stream) {
+    return qmatmul_impl(w, x_dev, m, y_dev, UNILLM_PATH_AUTO, stream, kEpiAdd);
+}
+
+int unillm_hip_qmatmul_swiglu(const unillm_qweight* w, const float* x_dev, int64_t m,
+                              float* act_dev, void* stream) {
+    return qmatmul_impl(w, x_dev, m, act_dev, UNILLM_PATH_AUTO, stream, kEpiSwiglu);
 }
 
 int unillm_hip_qmatmul(const unillm_qweight* w, const float* x_dev, int64_t m, float* y_dev,

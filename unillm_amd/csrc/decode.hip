@@ -278,7 +278,7 @@ template <int QT, int MT2>
 __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__ base, int64_t rb,
                                                      const _Float16* __restrict__ xh,
                                                      float* __restrict__ y, int M, int N, int KB,
-                                                     int S, float wscale, float oscale) {
+                                                     int S, float wscale, float oscale, int add) {
     using ST = Stage<QT, MT2>;
     constexpr int QB = ST::QB, D = ST::D, LPC = ST::LPC;
     // 4-bit codes: Q4_0 and Q4_K; byte codes: Q8_0 and Q6_K (repacked to int8)
@@ -497,8 +497,10 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
     const int n = row0 + col;
     if (n < N) {
         float* yb = y + (int64_t)(4 * h) * N + n;
+        // y += (the residual add) or y =; a split k range always adds (onto zeros
+        // written by xprep_kernel, or onto y itself with add)
         auto put = [&](float* dst, float v) {
-            if (S == 1) *dst = v * oscale;
+            if (S == 1) *dst = add ? *dst + v * oscale : v * oscale;
             else unsafeAtomicAdd(dst, v * oscale);
         };
         if (M % 8 == 0) {
@@ -525,7 +527,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
 
 template <int QT, int MT2>
 hipError_t launch_mt(const QWeight& w, const _Float16* xh, int64_t m, float* y, int S,
-                     hipStream_t s) {
+                     hipStream_t s, int add) {
     using ST = Stage<QT, MT2>;
     static const bool attr = hipFuncSetAttribute((const void*)decode_kernel<QT, MT2>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -534,7 +536,7 @@ hipError_t launch_mt(const QWeight& w, const _Float16* xh, int64_t m, float* y, 
     const float wscale = ldexpf(1.0f, -w.f16_exp), oscale = ldexpf(1.0f, w.f16_exp);
     const int groups = (int)((w.n + DROWS - 1) / DROWS);
     decode_kernel<QT, MT2><<<groups * S, 256, ST::LDS, s>>>(
-        w.base, w.row_bytes, xh, y, (int)m, (int)w.n, (int)w.kb, S, wscale, oscale);
+        w.base, w.row_bytes, xh, y, (int)m, (int)w.n, (int)w.kb, S, wscale, oscale, add);
     return hipGetLastError();
 }
 
@@ -553,10 +555,30 @@ int choose_split(const QWeight& w, int lds_bytes) {
     return (int)S;
 }
 
+// act[m, I] = silu(g) * u from gu[m, 2 I] (g = columns 0 .. I - 1, u = I .. 2 I - 1);
+// candle's silu, v / (1 + e^-v).
+__global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ gu, int64_t m,
+                                                     int64_t I, float* __restrict__ act) {
+    const int64_t total = m * I;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / I, c = i - r * I;
+        const float g = gu[r * 2 * I + c], u = gu[r * 2 * I + I + c];
+        act[i] = g / (1.0f + expf(-g)) * u;
+    }
+}
+
 }  // namespace
 
+hipError_t launch_swiglu(const float* gu, int64_t m, int64_t I, float* act, hipStream_t s) {
+    const int64_t total = m * I;
+    const int grid = (int)std::min<int64_t>((total + 255) / 256, (int64_t)device_info().cu_count * 8);
+    swiglu_kernel<<<std::max(grid, 1), 256, 0, s>>>(gu, m, I, act);
+    return hipGetLastError();
+}
+
 hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float* y,
-                              hipStream_t s) {
+                              hipStream_t s, int epi) {
     // 32-bit offsets: x in f16 elements, weight bytes
     if ((uint64_t)m * (uint64_t)w.k >= (1ull << 31) ||
         (uint64_t)w.n * (uint64_t)w.row_bytes >= (1ull << 32))
@@ -572,7 +594,8 @@ hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float
     hipError_t e = stream_workspace(s, (size_t)m * (size_t)w.k * 2, &ws);
     if (e != hipSuccess) return e;
     const int64_t n8 = m * w.k / 8;  // k % 32 == 0
-    const int64_t ny = S > 1 ? m * w.n : 0;
+    const int add = epi == kEpiAdd;
+    const int64_t ny = S > 1 && !add ? m * w.n : 0;
     const int64_t work = std::max(n8, ny / 4);
     const int grid =
         (int)std::min<int64_t>((work + 255) / 256, (int64_t)device_info().cu_count * 8);
@@ -580,16 +603,16 @@ hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const _Float16* xh = static_cast<const _Float16*>(ws);
     if (k4)
-        return wide ? launch_mt<UNILLM_QTYPE_Q4_K, 2>(w, xh, m, y, S, s)
-                    : launch_mt<UNILLM_QTYPE_Q4_K, 1>(w, xh, m, y, S, s);
+        return wide ? launch_mt<UNILLM_QTYPE_Q4_K, 2>(w, xh, m, y, S, s, add)
+                    : launch_mt<UNILLM_QTYPE_Q4_K, 1>(w, xh, m, y, S, s, add);
     if (k6)
-        return wide ? launch_mt<UNILLM_QTYPE_Q6_K, 2>(w, xh, m, y, S, s)
-                    : launch_mt<UNILLM_QTYPE_Q6_K, 1>(w, xh, m, y, S, s);
+        return wide ? launch_mt<UNILLM_QTYPE_Q6_K, 2>(w, xh, m, y, S, s, add)
+                    : launch_mt<UNILLM_QTYPE_Q6_K, 1>(w, xh, m, y, S, s, add);
     if (!wide)
-        return q4 ? launch_mt<UNILLM_QTYPE_Q4_0, 1>(w, xh, m, y, S, s)
-                  : launch_mt<UNILLM_QTYPE_Q8_0, 1>(w, xh, m, y, S, s);
-    return q4 ? launch_mt<UNILLM_QTYPE_Q4_0, 2>(w, xh, m, y, S, s)
-              : launch_mt<UNILLM_QTYPE_Q8_0, 2>(w, xh, m, y, S, s);
+        return q4 ? launch_mt<UNILLM_QTYPE_Q4_0, 1>(w, xh, m, y, S, s, add)
+                  : launch_mt<UNILLM_QTYPE_Q8_0, 1>(w, xh, m, y, S, s, add);
+    return q4 ? launch_mt<UNILLM_QTYPE_Q4_0, 2>(w, xh, m, y, S, s, add)
+              : launch_mt<UNILLM_QTYPE_Q8_0, 2>(w, xh, m, y, S, s, add);
 }
 
 }  // namespace unillm

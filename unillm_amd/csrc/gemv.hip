@@ -278,16 +278,18 @@ struct Chunk {
 // the whole grid requests at one moment form one contiguous stretch of the
 // matrix.  Chunk j0 holds the wave's rows j0 .. j0 + R - 1; rows past the
 // wave's last are clamped to that last row (an address the wave reads anyway).
-template <int QT, int NB, int R>
+// PAIR (the SwiGLU epilogue, R = 2): chunk j0 is the wave's logical row
+// L = w + j0 W of a [gate; up] weight with I rows each: physical rows L and I + L.
+template <int QT, int NB, int R, bool PAIR = false>
 __device__ __forceinline__ void load_chunk(Chunk<QT, NB, R>& c, const uint8_t* __restrict__ base,
                                            uint32_t rb, int w, int W, int j0, int jlast,
                                            const uint32_t (&poff)[NB], const uint32_t (&soff)[NB],
-                                           const uint32_t (&hoff)[NB]) {
+                                           const uint32_t (&hoff)[NB], int I = 0) {
     constexpr int V = Payload<QT>::V;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const uint32_t ro =
-            __builtin_amdgcn_readfirstlane((uint32_t)(w + min(j0 + r, jlast) * W) * rb);
+        const int row = PAIR ? w + min(j0, jlast) * W + r * I : w + min(j0 + r, jlast) * W;
+        const uint32_t ro = __builtin_amdgcn_readfirstlane((uint32_t)row * rb);
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
 #pragma unroll
@@ -301,10 +303,12 @@ __device__ __forceinline__ void load_chunk(Chunk<QT, NB, R>& c, const uint8_t* _
     }
 }
 
-template <int QT, int M, int NB, int R>
+// Epilogue: y = sum (store), y += sum (the residual add, `add`), or with PAIR
+// y[m, L] = silu(gate) * up over the I logical rows (candle silu: v / (1 + e^-v)).
+template <int QT, int M, int NB, int R, bool PAIR = false>
 __device__ __forceinline__ void compute_chunk(const Chunk<QT, NB, R>& c, const XRegs<QT, M, NB>& xs,
                                               float* __restrict__ y, int w, int W, int j0,
-                                              int jcount, int N, int lane, int m_real) {
+                                              int jcount, int N, int lane, int m_real, int add) {
     float part[M][R];
 #pragma unroll
     for (int m = 0; m < M; ++m)
@@ -378,12 +382,25 @@ __device__ __forceinline__ void compute_chunk(const Chunk<QT, NB, R>& c, const X
 #pragma unroll
         for (int r = 0; r < R; ++r) part[m][r] = wave_sum(part[m][r]);
     if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (j0 + r < jcount)
+        if constexpr (PAIR) {
+            if (j0 < jcount)
 #pragma unroll
                 for (int m = 0; m < M; ++m)
-                    if (m < m_real) y[(int64_t)m * N + w + (j0 + r) * W] = part[m][r];
+                    if (m < m_real) {
+                        const float g = part[m][0], u = part[m][1];
+                        y[(int64_t)m * N + w + j0 * W] = g / (1.0f + expf(-g)) * u;
+                    }
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (j0 + r < jcount)
+#pragma unroll
+                    for (int m = 0; m < M; ++m)
+                        if (m < m_real) {
+                            float* dst = y + (int64_t)m * N + w + (j0 + r) * W;
+                            *dst = add ? *dst + part[m][r] : part[m][r];
+                        }
+        }
     }
 }
 
@@ -398,12 +415,18 @@ constexpr int gemv_threads() {
 // m_real <= M rows of x are used; rows m >= m_real repeat row m_real - 1 and
 // are not written.  Dynamic LDS: M * KB * kXWords dwords of x digits.
 // KB <= NB * 64, so a thread builds at most PASSES = ceil(M * NB * 256 / THREADS) quarter-blocks.
-template <int QT, int M, int NB, int R, int THREADS>
+// PAIR: the weight is [gate; up] (2 I rows); the waves cover the I logical rows
+// and y is [m, I] = silu(gate) * up.  Otherwise `add` selects y += x W^T.
+template <int QT, int M, int NB, int R, int THREADS, bool PAIR = false>
 __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict__ base,
                                                        int64_t rb,
                                                        const float* __restrict__ x,
-                                                       float* __restrict__ y, int N, int KB,
-                                                       int m_real) {
+                                                       float* __restrict__ y, int N_rows, int KB,
+                                                       int m_real, int add) {
+    static_assert(!PAIR || R == 2, "the SwiGLU pair is one gate and one up row per chunk");
+    constexpr int LR = PAIR ? 1 : R;  // logical rows per chunk
+    const int I = PAIR ? N_rows / 2 : 0;
+    const int N = PAIR ? I : N_rows;  // logical rows (output columns)
     constexpr int WAVES = THREADS / 64;
     constexpr int PASSES = (M * NB * 256 + THREADS - 1) / THREADS;  // quarter-blocks per thread
     extern __shared__ uint32_t xlds[];
@@ -463,7 +486,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     //    up, everything behind them (here: the digit work every row needs)
     //    waits until they are accepted.
     Chunk<QT, NB, R> a, b;
-    load_chunk<QT, NB, R>(a, base, (uint32_t)rb, wrow, waves, 0, jlast, poff, soff, hoff);
+    load_chunk<QT, NB, R, PAIR>(a, base, (uint32_t)rb, wrow, waves, 0, jlast, poff, soff, hoff, I);
 
     // 3. x digit records for all M * KB blocks, four threads per block (threads
     //    past nq compute on a clamped copy and store nothing; nq is a multiple
@@ -488,30 +511,34 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     //    both, then two chunks per step; with one chunk, just compute it.  The
     //    branch is wave-uniform and each side has its own memory waits (a
     //    shared join would make the wait for chunk a cover chunk b as well).
-    if (jcount > R) {
-        load_chunk<QT, NB, R>(b, base, (uint32_t)rb, wrow, waves, R, jlast, poff, soff, hoff);
-        compute_chunk<QT, M, NB, R>(a, xs, y, wrow, waves, 0, jcount, N, lane, m_real);
-        compute_chunk<QT, M, NB, R>(b, xs, y, wrow, waves, R, jcount, N, lane, m_real);
-        for (int j = 2 * R; j < jcount; j += 2 * R) {
-            load_chunk<QT, NB, R>(a, base, (uint32_t)rb, wrow, waves, j, jlast, poff, soff, hoff);
-            load_chunk<QT, NB, R>(b, base, (uint32_t)rb, wrow, waves, j + R, jlast, poff, soff, hoff);
-            compute_chunk<QT, M, NB, R>(a, xs, y, wrow, waves, j, jcount, N, lane, m_real);
-            compute_chunk<QT, M, NB, R>(b, xs, y, wrow, waves, j + R, jcount, N, lane, m_real);
+    if (jcount > LR) {
+        load_chunk<QT, NB, R, PAIR>(b, base, (uint32_t)rb, wrow, waves, LR, jlast, poff, soff, hoff, I);
+        compute_chunk<QT, M, NB, R, PAIR>(a, xs, y, wrow, waves, 0, jcount, N, lane, m_real, add);
+        compute_chunk<QT, M, NB, R, PAIR>(b, xs, y, wrow, waves, LR, jcount, N, lane, m_real, add);
+        for (int j = 2 * LR; j < jcount; j += 2 * LR) {
+            load_chunk<QT, NB, R, PAIR>(a, base, (uint32_t)rb, wrow, waves, j, jlast, poff, soff,
+                                        hoff, I);
+            load_chunk<QT, NB, R, PAIR>(b, base, (uint32_t)rb, wrow, waves, j + LR, jlast, poff,
+                                        soff, hoff, I);
+            compute_chunk<QT, M, NB, R, PAIR>(a, xs, y, wrow, waves, j, jcount, N, lane, m_real,
+                                              add);
+            compute_chunk<QT, M, NB, R, PAIR>(b, xs, y, wrow, waves, j + LR, jcount, N, lane,
+                                              m_real, add);
         }
     } else {
-        compute_chunk<QT, M, NB, R>(a, xs, y, wrow, waves, 0, jcount, N, lane, m_real);
+        compute_chunk<QT, M, NB, R, PAIR>(a, xs, y, wrow, waves, 0, jcount, N, lane, m_real, add);
     }
 }
 
-template <int QT, int M, int NB, int R>
+template <int QT, int M, int NB, int R, bool PAIR = false>
 hipError_t launch_r(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st,
-                    int waves) {
+                    int waves, int add) {
     constexpr int THREADS = gemv_threads<QT, M, NB>();
     constexpr int WAVES = THREADS / 64;
     const size_t lds = (size_t)M * w.kb * kXWords * sizeof(uint32_t);
     const int grid = (waves + WAVES - 1) / WAVES;
-    gemv_kernel<QT, M, NB, R, THREADS><<<grid, THREADS, lds, st>>>(w.base, w.row_bytes, x, y,
-                                                                  (int)w.n, (int)w.kb, (int)m);
+    gemv_kernel<QT, M, NB, R, THREADS, PAIR><<<grid, THREADS, lds, st>>>(
+        w.base, w.row_bytes, x, y, (int)w.n, (int)w.kb, (int)m, add);
     return hipGetLastError();
 }
 
@@ -521,17 +548,31 @@ hipError_t launch_r(const QWeight& w, const float* x, int64_t m, float* y, hipSt
 // built).  The chunk size R (rows per request) is capped by the registers a
 // chunk may take (at most 4 payload loads per lane).
 template <int QT, int M, int NB>
-hipError_t launch_nb(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st) {
+hipError_t launch_nb(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st,
+                     int epi) {
     constexpr int V = Payload<QT>::V;
     constexpr int RMAX = NB * V >= 4 ? 1 : 4 / (NB * V);
     constexpr int THREADS = gemv_threads<QT, M, NB>();
     constexpr int WAVES = THREADS / 64;
     int per_cu = 0;
     const size_t lds = (size_t)M * w.kb * kXWords * sizeof(uint32_t);
+    const int64_t cus = device_info().cu_count;
+    if (epi == kEpiSwiglu) {  // one gate and one up row per chunk, over the I = n / 2 outputs
+        if constexpr (M * NB * V <= 4) {
+            hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &per_cu, gemv_kernel<QT, M, NB, 2, THREADS, true>, THREADS, lds);
+            if (e != hipSuccess) return e;
+            const int64_t I = w.n / 2;
+            const int64_t resident = cus * std::max(per_cu, 1) * WAVES;
+            const int64_t waves = std::max<int64_t>(
+                1, std::min({resident, std::max<int64_t>(I / 2, cus * WAVES), I}));
+            return launch_r<QT, M, NB, 2, true>(w, x, m, y, st, (int)waves, 0);
+        }
+        return hipErrorInvalidValue;
+    }
     hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
         &per_cu, gemv_kernel<QT, M, NB, RMAX, THREADS>, THREADS, lds);
     if (e != hipSuccess) return e;
-    const int64_t cus = device_info().cu_count;
     const int64_t resident = cus * std::max(per_cu, 1) * WAVES;
     const int64_t want = std::max<int64_t>(w.n / 2, cus * WAVES);
     const int64_t waves = std::max<int64_t>(1, std::min({resident, want, w.n}));
@@ -540,22 +581,24 @@ hipError_t launch_nb(const QWeight& w, const float* x, int64_t m, float* y, hipS
         fprintf(stderr, "unillm gemv: n=%lld kb=%lld m=%lld threads=%d waves=%lld rows=%lld\n",
                 (long long)w.n, (long long)w.kb, (long long)m, THREADS, (long long)waves,
                 (long long)rows);
-    if (RMAX >= 4 && rows > 4) return launch_r<QT, M, NB, RMAX>(w, x, m, y, st, (int)waves);
+    const int add = epi == kEpiAdd;
+    if (RMAX >= 4 && rows > 4) return launch_r<QT, M, NB, RMAX>(w, x, m, y, st, (int)waves, add);
     if (RMAX >= 2 && rows > 2)
-        return launch_r<QT, M, NB, (RMAX >= 2 ? 2 : 1)>(w, x, m, y, st, (int)waves);
-    return launch_r<QT, M, NB, 1>(w, x, m, y, st, (int)waves);
+        return launch_r<QT, M, NB, (RMAX >= 2 ? 2 : 1)>(w, x, m, y, st, (int)waves, add);
+    return launch_r<QT, M, NB, 1>(w, x, m, y, st, (int)waves, add);
 }
 
 template <int QT, int M>
-hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st) {
+hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st,
+                    int epi) {
     switch ((int)((w.kb + 63) / 64)) {
-        case 1: return launch_nb<QT, M, 1>(w, x, m, y, st);
-        case 2: return launch_nb<QT, M, 2>(w, x, m, y, st);
-        case 3: if constexpr (M <= 2) return launch_nb<QT, M, 3>(w, x, m, y, st); break;
-        case 4: if constexpr (M <= 2) return launch_nb<QT, M, 4>(w, x, m, y, st); break;
-        case 5: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 5>(w, x, m, y, st); break;
-        case 6: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 6>(w, x, m, y, st); break;
-        case 7: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 7>(w, x, m, y, st); break;
+        case 1: return launch_nb<QT, M, 1>(w, x, m, y, st, epi);
+        case 2: return launch_nb<QT, M, 2>(w, x, m, y, st, epi);
+        case 3: if constexpr (M <= 2) return launch_nb<QT, M, 3>(w, x, m, y, st, epi); break;
+        case 4: if constexpr (M <= 2) return launch_nb<QT, M, 4>(w, x, m, y, st, epi); break;
+        case 5: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 5>(w, x, m, y, st, epi); break;
+        case 6: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 6>(w, x, m, y, st, epi); break;
+        case 7: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 7>(w, x, m, y, st, epi); break;
         default: break;
     }
     return hipErrorInvalidValue;
@@ -573,31 +616,41 @@ int64_t gemv_max_kb(int64_t m, int qtype) {
     return 128;
 }
 
+// The SwiGLU pair epilogue holds two chunks of one gate and one up row: the
+// tokens times the 128-bit payload loads of a row at most 4, past which it spills
+// (m = 1: Q4_0 / Q4_K k <= 8192, Q8_0 / Q6_K k <= 4096; halved per doubling of m).
+bool gemv_supports_swiglu(const QWeight& w, int64_t m) {
+    const int64_t nbv = (w.kb + 63) / 64 * (qbytes(w.qtype) / 16);
+    const int64_t mb = m <= 1 ? 1 : m <= 2 ? 2 : 4;  // the kernel's token count M
+    return gemv_supports(w, m) && w.n % 2 == 0 && mb * nbv <= 4;
+}
+
 // The GEMV addresses a weight with 32-bit row offsets.
 bool gemv_supports(const QWeight& w, int64_t m) {
     return m >= 1 && m <= kGemvMaxM && w.kb <= gemv_max_kb(m, w.qtype) &&
            (uint64_t)w.n * (uint64_t)w.row_bytes <= 0xFFFFFFFFull;
 }
 
-hipError_t launch_gemv(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t s) {
+hipError_t launch_gemv(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t s,
+                       int epi) {
     if (w.qtype == UNILLM_QTYPE_Q4_K) {
-        if (m == 1) return launch_m<UNILLM_QTYPE_Q4_K, 1>(w, x, m, y, s);
-        if (m == 2) return launch_m<UNILLM_QTYPE_Q4_K, 2>(w, x, m, y, s);
-        return launch_m<UNILLM_QTYPE_Q4_K, 4>(w, x, m, y, s);
+        if (m == 1) return launch_m<UNILLM_QTYPE_Q4_K, 1>(w, x, m, y, s, epi);
+        if (m == 2) return launch_m<UNILLM_QTYPE_Q4_K, 2>(w, x, m, y, s, epi);
+        return launch_m<UNILLM_QTYPE_Q4_K, 4>(w, x, m, y, s, epi);
     }
     if (w.qtype == UNILLM_QTYPE_Q6_K) {
-        if (m == 1) return launch_m<UNILLM_QTYPE_Q6_K, 1>(w, x, m, y, s);
-        if (m == 2) return launch_m<UNILLM_QTYPE_Q6_K, 2>(w, x, m, y, s);
-        return launch_m<UNILLM_QTYPE_Q6_K, 4>(w, x, m, y, s);
+        if (m == 1) return launch_m<UNILLM_QTYPE_Q6_K, 1>(w, x, m, y, s, epi);
+        if (m == 2) return launch_m<UNILLM_QTYPE_Q6_K, 2>(w, x, m, y, s, epi);
+        return launch_m<UNILLM_QTYPE_Q6_K, 4>(w, x, m, y, s, epi);
     }
     if (w.qtype == UNILLM_QTYPE_Q4_0) {
-        if (m == 1) return launch_m<UNILLM_QTYPE_Q4_0, 1>(w, x, m, y, s);
-        if (m == 2) return launch_m<UNILLM_QTYPE_Q4_0, 2>(w, x, m, y, s);
-        return launch_m<UNILLM_QTYPE_Q4_0, 4>(w, x, m, y, s);
+        if (m == 1) return launch_m<UNILLM_QTYPE_Q4_0, 1>(w, x, m, y, s, epi);
+        if (m == 2) return launch_m<UNILLM_QTYPE_Q4_0, 2>(w, x, m, y, s, epi);
+        return launch_m<UNILLM_QTYPE_Q4_0, 4>(w, x, m, y, s, epi);
     }
-    if (m == 1) return launch_m<UNILLM_QTYPE_Q8_0, 1>(w, x, m, y, s);
-    if (m == 2) return launch_m<UNILLM_QTYPE_Q8_0, 2>(w, x, m, y, s);
-    return launch_m<UNILLM_QTYPE_Q8_0, 4>(w, x, m, y, s);
+    if (m == 1) return launch_m<UNILLM_QTYPE_Q8_0, 1>(w, x, m, y, s, epi);
+    if (m == 2) return launch_m<UNILLM_QTYPE_Q8_0, 2>(w, x, m, y, s, epi);
+    return launch_m<UNILLM_QTYPE_Q8_0, 4>(w, x, m, y, s, epi);
 }
 
 }  // namespace unillm

@@ -55,6 +55,12 @@ using QWeight = ::unillm_qweight;
 
 int64_t gemv_max_kb(int64_t m, int qtype);
 bool gemv_supports(const unillm_qweight& w, int64_t m);
+bool gemv_supports_swiglu(const unillm_qweight& w, int64_t m);
+
+// Epilogues of the matmul launches: y = x W^T (store), y += x W^T (the decoder
+// layer's residual add, llama.rs:668, 677), or for a [gate; up] weight of 2 I
+// rows y[m, I] = silu(x G^T) * (x U^T) (fused_swiglu, tensor_core.rs:1385-1396).
+constexpr int kEpiStore = 0, kEpiAdd = 1, kEpiSwiglu = 2;
 
 inline bool is_kquant(int qtype) {
     return qtype == UNILLM_QTYPE_Q4_K || qtype == UNILLM_QTYPE_Q6_K;
@@ -112,7 +118,9 @@ const DeviceInfo& device_info();
 // kernels finish before the next call's start).  Grows stream-ordered; the
 // memory is held until the process ends.  Calls on one stream from several
 // host threads are ordered by the stream, the map by a mutex.
-hipError_t stream_workspace(hipStream_t s, size_t bytes, void** out);
+// Slot 0 holds x in the MFMA paths' operand type; slot 1 the [gate | up] outputs
+// of a SwiGLU call off the GEMV path (both live during that call).
+hipError_t stream_workspace(hipStream_t s, size_t bytes, void** out, int slot = 0);
 // UNILLM_DEBUG_LAUNCH=1 prints each kernel's launch shape to stderr.
 bool debug_launch();
 
@@ -125,11 +133,17 @@ hipError_t launch_dequant(const QWeight& w, float* out, hipStream_t s);
 hipError_t launch_scale_absmax(const QWeight& w, uint32_t* out, hipStream_t s);
 hipError_t launch_quantize(int qtype, const float* w, int64_t n, int64_t k, uint8_t* out,
                            hipStream_t s);
-hipError_t launch_gemv(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t s);
+// epi: kEpiStore or kEpiAdd on every path; kEpiSwiglu on the GEMV only
+// (gemv_supports_swiglu), the other paths run it as store + swiglu_kernel.
+hipError_t launch_gemv(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t s,
+                       int epi = kEpiStore);
 hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float* y,
-                              hipStream_t s);
+                              hipStream_t s, int epi = kEpiStore);
 hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, float* y,
-                               hipStream_t s);
+                               hipStream_t s, int epi = kEpiStore);
+// act[m, I] = silu(g[m, i]) * u[m, i] with g, u the two halves of each row of
+// gu[m, 2 I] (the SwiGLU of the MFMA paths, after their store)
+hipError_t launch_swiglu(const float* gu, int64_t m, int64_t I, float* act, hipStream_t s);
 
 constexpr int64_t kGemvMaxM = 4;
 constexpr int64_t kDecodeMaxM = 64;

@@ -179,7 +179,7 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
                                                               const __bf16* __restrict__ xb,
                                                               float* __restrict__ y, int M, int N,
                                                               int KB, int tiles_n, int tiles,
-                                                              int units_pad, int S) {
+                                                              int units_pad, int S, int add) {
     static_assert(NW == 8, "the ring's load split assumes 8 waves");
     constexpr int QB = Ring<QT, BM>::QB;  // payload bytes per block
     // waves: RW row groups x CW column groups; wave (rw, cw) owns rows BM / RW * rw ..
@@ -439,21 +439,21 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
                 const int row = m0 + WR * rw + 16 * i + 4 * g + e;
                 if (row >= M) continue;
                 float* dst = y + (int64_t)row * N + col;
-                if (S == 1) *dst = acc[i][j][e];
-                else unsafeAtomicAdd(dst, acc[i][j][e]);
+                if (S == 1) *dst = add ? *dst + acc[i][j][e] : acc[i][j][e];
+                else unsafeAtomicAdd(dst, acc[i][j][e]);  // onto zeros, or onto y with add
             }
     }
 }
 
 template <int QT, int BM>
 hipError_t launch_bm(const QWeight& w, const __bf16* xb, int64_t m, float* y, int S,
-                     hipStream_t s) {
+                     hipStream_t s, int add) {
     // x is addressed with 32-bit element offsets: launch in row chunks below 2^30 elements
     const int64_t chunk = std::max<int64_t>(BM, ((int64_t)1 << 30) / w.k / BM * BM);
     if (m > chunk) {
         for (int64_t r = 0; r < m; r += chunk) {
             hipError_t e =
-                launch_bm<QT, BM>(w, xb + r * w.k, std::min(chunk, m - r), y + r * w.n, S, s);
+                launch_bm<QT, BM>(w, xb + r * w.k, std::min(chunk, m - r), y + r * w.n, S, s, add);
             if (e != hipSuccess) return e;
         }
         return hipSuccess;
@@ -469,7 +469,8 @@ hipError_t launch_bm(const QWeight& w, const __bf16* xb, int64_t m, float* y, in
     const int tiles = tiles_m * tiles_n;
     const int units_pad = (tiles * S + 7) / 8 * 8;
     prefill_kernel<QT, BM, kWaves><<<units_pad, kWaves * 64, Ring<QT, BM>::BYTES, s>>>(
-        w.base, w.row_bytes, xb, y, (int)m, (int)w.n, (int)w.kb, tiles_n, tiles, units_pad, S);
+        w.base, w.row_bytes, xb, y, (int)m, (int)w.n, (int)w.kb, tiles_n, tiles, units_pad, S,
+        add);
     return hipGetLastError();
 }
 
@@ -495,7 +496,7 @@ PrefillPlan prefill_plan(const QWeight& w, int64_t m) {
 }  // namespace
 
 hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, float* y,
-                               hipStream_t s) {
+                               hipStream_t s, int epi) {
     // x in bf16 (the operand precision) in the stream's workspace: the GEMM
     // re-reads x once per 256-column tile, so it reads half the bytes, and no
     // conversion sits in its inner loop.  The same kernel zeroes y for a split k.
@@ -504,7 +505,8 @@ hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, floa
     void* ws = nullptr;
     hipError_t e = stream_workspace(s, (size_t)n * sizeof(__bf16), &ws);
     if (e != hipSuccess) return e;
-    const int64_t n8 = n / 8, ny = plan.S > 1 ? m * w.n : 0;
+    const int add = epi == kEpiAdd;
+    const int64_t n8 = n / 8, ny = plan.S > 1 && !add ? m * w.n : 0;
     const int grid = (int)std::min<int64_t>((std::max(n8, ny / 4) + 255) / 256,
                                             (int64_t)device_info().cu_count * 16);
     x_to_bf16_kernel<<<grid, 256, 0, s>>>(x, static_cast<uint4*>(ws), n8, y, ny);
@@ -512,17 +514,17 @@ hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, floa
     if (e != hipSuccess) return e;
     const __bf16* xb = static_cast<const __bf16*>(ws);
     if (w.qtype == UNILLM_QTYPE_Q4_K)
-        return plan.bm == 256 ? launch_bm<UNILLM_QTYPE_Q4_K, 256>(w, xb, m, y, 1, s)
-                              : launch_bm<UNILLM_QTYPE_Q4_K, 128>(w, xb, m, y, plan.S, s);
+        return plan.bm == 256 ? launch_bm<UNILLM_QTYPE_Q4_K, 256>(w, xb, m, y, 1, s, add)
+                              : launch_bm<UNILLM_QTYPE_Q4_K, 128>(w, xb, m, y, plan.S, s, add);
     if (w.qtype == UNILLM_QTYPE_Q6_K)
-        return plan.bm == 256 ? launch_bm<UNILLM_QTYPE_Q6_K, 256>(w, xb, m, y, 1, s)
-                              : launch_bm<UNILLM_QTYPE_Q6_K, 128>(w, xb, m, y, plan.S, s);
+        return plan.bm == 256 ? launch_bm<UNILLM_QTYPE_Q6_K, 256>(w, xb, m, y, 1, s, add)
+                              : launch_bm<UNILLM_QTYPE_Q6_K, 128>(w, xb, m, y, plan.S, s, add);
     const bool q4 = w.qtype == UNILLM_QTYPE_Q4_0;
     if (plan.bm == 256)
-        return q4 ? launch_bm<UNILLM_QTYPE_Q4_0, 256>(w, xb, m, y, 1, s)
-                  : launch_bm<UNILLM_QTYPE_Q8_0, 256>(w, xb, m, y, 1, s);
-    return q4 ? launch_bm<UNILLM_QTYPE_Q4_0, 128>(w, xb, m, y, plan.S, s)
-              : launch_bm<UNILLM_QTYPE_Q8_0, 128>(w, xb, m, y, plan.S, s);
+        return q4 ? launch_bm<UNILLM_QTYPE_Q4_0, 256>(w, xb, m, y, 1, s, add)
+                  : launch_bm<UNILLM_QTYPE_Q8_0, 256>(w, xb, m, y, 1, s, add);
+    return q4 ? launch_bm<UNILLM_QTYPE_Q4_0, 128>(w, xb, m, y, plan.S, s, add)
+              : launch_bm<UNILLM_QTYPE_Q8_0, 128>(w, xb, m, y, plan.S, s, add);
 }
 
 }  // namespace unillm

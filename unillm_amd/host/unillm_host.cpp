@@ -159,9 +159,9 @@ std::shared_ptr<QuantLinear> QuantLinear::from_blocks(int qtype, int64_t n, int6
 
 QuantLinear::~QuantLinear() { unillm_hip_qweight_destroy(w_); }
 
-Tensor QuantLinear::forward(const Tensor& x, void* stream) const {
+void QuantLinear::check_input(const Tensor& x) const {
     // candle QMatMul::forward rules (called at llama.rs:1188): f32, rank >= 2,
-    // last dim == k; output [.., n], freshly allocated.
+    // last dim == k
     if (x.shape().size() < 2)
         throw Error("QMatMul forward failed: rank " + std::to_string(x.shape().size()) +
                     " input, need rank >= 2");
@@ -171,12 +171,36 @@ Tensor QuantLinear::forward(const Tensor& x, void* stream) const {
     if (!x.device().is_hip())
         throw Error("QMatMul forward failed: input is on " + x.device().to_string() +
                     ", weight is on HIP");
+}
+
+Tensor QuantLinear::forward(const Tensor& x, void* stream) const {
+    check_input(x);  // output [.., n], freshly allocated
     std::vector<int64_t> oshape = x.shape();
     oshape.back() = n_;
     Tensor y = Tensor::empty(oshape, x.device());
     const int64_t m = x.numel() / k_;
     check(unillm_hip_qmatmul(w_, x.data(), m, y.data_mut(), stream), "QMatMul forward failed");
     return y;
+}
+
+void QuantLinear::forward_add(const Tensor& x, Tensor& residual, void* stream) const {
+    check_input(x);
+    std::vector<int64_t> oshape = x.shape();
+    oshape.back() = n_;
+    if (residual.shape() != oshape || !residual.device().is_hip())
+        throw Error("QMatMul forward failed: residual must be a HIP tensor of the output shape");
+    check(unillm_hip_qmatmul_add(w_, x.data(), x.numel() / k_, residual.data_mut(), stream),
+          "QMatMul forward failed");
+}
+
+Tensor QuantLinear::forward_swiglu(const Tensor& x, void* stream) const {
+    check_input(x);
+    std::vector<int64_t> oshape = x.shape();
+    oshape.back() = n_ / 2;
+    Tensor act = Tensor::empty(oshape, x.device());
+    check(unillm_hip_qmatmul_swiglu(w_, x.data(), x.numel() / k_, act.data_mut(), stream),
+          "QMatMul forward failed");
+    return act;
 }
 
 Tensor QuantLinear::dequantize(void* stream) const {

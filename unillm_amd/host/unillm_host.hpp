@@ -105,6 +105,12 @@ public:
 
     // QMatMul::forward: [.., k] f32 -> [.., n] f32 (rank >= 2, last dim k).
     Tensor forward(const Tensor& x, void* stream = nullptr) const;
+    // residual += forward(x) in the projection's epilogue: the decoder layer's
+    // residual add after o_proj / down_proj (llama.rs:668, 677).
+    void forward_add(const Tensor& x, Tensor& residual, void* stream = nullptr) const;
+    // For a [gate; up] handle (LoadOptions::fuse_gate_up): silu(gate) * up, [.., n / 2]
+    // (LlamaMLP::forward's two projections and fused_swiglu, llama.rs:1275-1283).
+    Tensor forward_swiglu(const Tensor& x, void* stream = nullptr) const;
     // qtensor.dequantize: f32 [n, k] on the device, bit-exact with GGML.
     Tensor dequantize(void* stream = nullptr) const;
 
@@ -115,6 +121,7 @@ public:
 
 private:
     QuantLinear() = default;
+    void check_input(const Tensor& x) const;
     unillm_qweight* w_ = nullptr;
     int qtype_ = 0;
     int64_t n_ = 0, k_ = 0;

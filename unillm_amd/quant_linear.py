@@ -87,10 +87,7 @@ class QuantLinear:
         return _capi.lib().unillm_hip_select_path(self._h, m)
 
     # ---- compute -------------------------------------------------------------------------
-    def forward(self, x: torch.Tensor, path: int = _capi.PATH_AUTO,
-                out: torch.Tensor | None = None,
-                stream: torch.cuda.Stream | None = None) -> torch.Tensor:
-        """y[..., n] = x[..., k] . dequant(W)^T (QMatMul::forward)."""
+    def _check_input(self, x: torch.Tensor) -> int:
         if x.dtype != torch.float32:
             raise RuntimeError(f"QMatMul forward failed: expected f32 input, got {x.dtype}")
         if x.dim() < 2:
@@ -102,14 +99,47 @@ class QuantLinear:
             raise RuntimeError("QMatMul forward failed: input is not on the HIP device")
         if not x.is_contiguous():
             raise RuntimeError("QMatMul forward failed: input is not contiguous")
-        m = x.numel() // self.k
+        return x.numel() // self.k
+
+    def _out(self, x: torch.Tensor, m: int, n: int, out: torch.Tensor | None) -> torch.Tensor:
         if out is None:
-            out = torch.empty(*x.shape[:-1], self.n, dtype=torch.float32, device=x.device)
-        elif (out.dtype != torch.float32 or not out.is_contiguous()
-              or out.numel() != m * self.n):
+            return torch.empty(*x.shape[:-1], n, dtype=torch.float32, device=x.device)
+        if out.dtype != torch.float32 or not out.is_contiguous() or out.numel() != m * n:
             raise RuntimeError("QMatMul forward failed: bad output tensor")
+        return out
+
+    def forward(self, x: torch.Tensor, path: int = _capi.PATH_AUTO,
+                out: torch.Tensor | None = None,
+                stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        """y[..., n] = x[..., k] . dequant(W)^T (QMatMul::forward)."""
+        m = self._check_input(x)
+        out = self._out(x, m, self.n, out)
         rc = _capi.lib().unillm_hip_qmatmul_path(self._h, x.data_ptr(), m, out.data_ptr(), path,
                                                  _stream_ptr(stream))
+        if rc != _capi.OK:
+            raise HipError(rc, _capi.last_error())
+        return out
+
+    def forward_add(self, x: torch.Tensor, residual: torch.Tensor,
+                    stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        """residual[..., n] += x[..., k] . dequant(W)^T in place (the decoder layer's
+        residual add fused into the projection, llama.rs:668, 677); returns residual."""
+        m = self._check_input(x)
+        self._out(x, m, self.n, residual)
+        rc = _capi.lib().unillm_hip_qmatmul_add(self._h, x.data_ptr(), m, residual.data_ptr(),
+                                                _stream_ptr(stream))
+        if rc != _capi.OK:
+            raise HipError(rc, _capi.last_error())
+        return residual
+
+    def forward_swiglu(self, x: torch.Tensor, out: torch.Tensor | None = None,
+                       stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        """silu(x G^T) * (x U^T) for a [gate; up] weight (n = 2 I): [..., I]
+        (LlamaMLP's gate, up and fused_swiglu, llama.rs:1275-1283)."""
+        m = self._check_input(x)
+        out = self._out(x, m, self.n // 2, out)
+        rc = _capi.lib().unillm_hip_qmatmul_swiglu(self._h, x.data_ptr(), m, out.data_ptr(),
+                                                   _stream_ptr(stream))
         if rc != _capi.OK:
             raise HipError(rc, _capi.last_error())
         return out

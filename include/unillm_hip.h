@@ -126,6 +126,24 @@ int unillm_hip_qmatmul_add(const unillm_qweight* w, const float* x_dev, int64_t 
 int unillm_hip_qmatmul_swiglu(const unillm_qweight* w, const float* x_dev, int64_t m,
                               float* act_dev, void* stream);
 
+/* y[m, n] = LN(x)[m, k] . dequant(W)^T with LN(x) = (x - mean) / sqrt(var + eps)
+ * * gamma (+ beta) along k, var = mean((x - mean)^2): the layer norm the
+ * reference applies before the attention and MLP projections
+ * (ops_fn::layer_norm, crates/runtime/src/tensor_core.rs:973-1008, called with
+ * eps = 1e-6 at crates/runtime/src/models_v2/llama.rs:662, 671) fused into the
+ * matmul: on the GEMV path every workgroup normalizes x while its first
+ * weights stream in; the MFMA paths normalize in their x conversion.
+ * gamma[k] (and beta[k], which may be NULL) are device f32, 16-byte aligned. */
+int unillm_hip_qmatmul_norm(const unillm_qweight* w, const float* x_dev, const float* gamma_dev,
+                            const float* beta_dev, float eps, int64_t m, float* y_dev,
+                            void* stream);
+
+/* unillm_hip_qmatmul_swiglu on LN(x): post_attention_layernorm, gate, up and
+ * SwiGLU of LlamaMLP in one call (llama.rs:671-674, 1275-1283). */
+int unillm_hip_qmatmul_norm_swiglu(const unillm_qweight* w, const float* x_dev,
+                                   const float* gamma_dev, const float* beta_dev, float eps,
+                                   int64_t m, float* act_dev, void* stream);
+
 /* Kernel path that unillm_hip_qmatmul selects for m rows (UNILLM_PATH_*). */
 int unillm_hip_select_path(const unillm_qweight* w, int64_t m);
 

@@ -111,3 +111,65 @@ def test_add_and_swiglu_m0_noop():
     y = torch.ones(0, 4, device="cuda")
     ql.forward_add(torch.zeros(0, 64, device="cuda"), y)
     assert ql.forward_swiglu(torch.zeros(0, 64, device="cuda")).shape == (0, 2)
+
+
+# ---- the layer norm fused in front of the matmul (tensor_core.rs:973-1008) ------------------
+
+def _layer_norm(x, gamma, beta, eps):
+    # the reference's formula in f64: mean, mean of squared deviations, divide, scale
+    x = x.astype(np.float64)
+    mu = x.mean(axis=-1, keepdims=True)
+    var = ((x - mu) ** 2).mean(axis=-1, keepdims=True)
+    out = (x - mu) / np.sqrt(var + eps) * gamma.astype(np.float64)
+    return out + beta.astype(np.float64) if beta is not None else out
+
+
+@pytest.mark.parametrize("qtype,m,n,k,path,bias,offset", [
+    (Q4_0, 1, 300, 4096, PATH_GEMV, False, 0.0), (Q4_K, 3, 257, 2048, PATH_GEMV, True, 0.0),
+    (Q8_0, 2, 129, 4096, PATH_GEMV, False, 100.0), (Q4_0, 16, 1024, 4096, PATH_DECODE_MFMA, True, 0.0),
+    (Q4_0, 1, 256, 11008, PATH_DECODE_MFMA, False, 0.0), (Q6_K, 64, 300, 2048, PATH_DECODE_MFMA, False, 50.0),
+    (Q8_0, 256, 512, 4096, PATH_PREFILL_MFMA, True, 0.0), (Q4_0, 130, 256, 8192, PATH_PREFILL_MFMA, False, 10.0)])
+def test_layer_norm_matmul(qtype, m, n, k, path, bias, offset):
+    # offset: x = offset + N(0, 1) per row, so the mean dwarfs the deviations (a
+    # one-pass variance would lose them); (Q4_0, 1, 256, 11008): past the GEMV's
+    # norm reach, routed to batched decode
+    blocks = _blocks(qtype, n, k, seed=5 * n + k)
+    rng = np.random.default_rng(n + m)
+    x = (oracle.normal(m * k, seed=k + m).reshape(m, k) + offset).astype(np.float32)
+    gamma = (1.0 + 0.1 * rng.normal(size=k)).astype(np.float32)
+    beta = (0.1 * rng.normal(size=k)).astype(np.float32) if bias else None
+    ql = QuantLinear.from_blocks(qtype, n, k, blocks)
+    print(f"norm qtype={qtype} m={m} n={n} k={k}", flush=True)
+    y = ql.forward_norm(_dev(x), _dev(gamma), _dev(beta) if bias else None, eps=1e-6)
+    torch.cuda.synchronize()
+    xn = _layer_norm(x, gamma, beta, 1e-6)
+    ref = oracle.qmatmul_f64(qtype, blocks, xn.astype(np.float32), n, k)
+    tol = {PATH_GEMV: 1e-3, PATH_DECODE_MFMA: 1e-3, PATH_PREFILL_MFMA: 2e-2}[path]
+    assert oracle.normwise_error(y.cpu().numpy(), ref) < tol
+
+
+@pytest.mark.parametrize("qtype,m,i_rows,k", [(Q4_0, 1, 1376, 4096), (Q4_K, 16, 300, 2048)])
+def test_layer_norm_swiglu(qtype, m, i_rows, k):
+    # post_attention_layernorm + gate + up + SwiGLU in one call (m = 1: the GEMV
+    # pair epilogue on the normalized x; m = 16: batched decode + elementwise)
+    gate = _blocks(qtype, i_rows, k, seed=21 + i_rows)
+    up = _blocks(qtype, i_rows, k, seed=22 + i_rows)
+    gu = np.concatenate([gate.reshape(i_rows, -1), up.reshape(i_rows, -1)], axis=0)
+    rng = np.random.default_rng(3)
+    x = (oracle.normal(m * k, seed=23).reshape(m, k) + 3.0).astype(np.float32)
+    gamma = (1.0 + 0.1 * rng.normal(size=k)).astype(np.float32)
+    ql = QuantLinear.from_blocks(qtype, 2 * i_rows, k, gu)
+    act = ql.forward_swiglu(_dev(x), norm=(_dev(gamma), None, 1e-6)).cpu().numpy()
+    xn = _layer_norm(x, gamma, None, 1e-6).astype(np.float32)
+    g = oracle.qmatmul_f64(qtype, gate, xn, i_rows, k)
+    u = oracle.qmatmul_f64(qtype, up, xn, i_rows, k)
+    assert oracle.normwise_error(act, _silu_mul(g, u)) < 2e-3
+
+
+def test_layer_norm_argument_checks():
+    ql = QuantLinear.from_blocks(Q4_0, 4, 64, _blocks(Q4_0, 4, 64, seed=2))
+    x = torch.zeros(1, 64, device="cuda")
+    with pytest.raises(RuntimeError):  # gamma of the wrong length
+        ql.forward_norm(x, torch.ones(32, device="cuda"))
+    with pytest.raises(HipError):  # negative eps
+        ql.forward_norm(x, torch.ones(64, device="cuda"), eps=-1.0)

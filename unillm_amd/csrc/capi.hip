@@ -317,7 +317,7 @@ namespace {
 // The matmul on `path` with epilogue `epi` (kEpiStore / kEpiAdd; kEpiSwiglu runs
 // fused on the GEMV, else as store into the stream's second workspace + swiglu).
 int qmatmul_impl(const unillm_qweight* w, const float* x_dev, int64_t m, float* y_dev, int path,
-                 void* stream, int epi) {
+                 void* stream, int epi, const NormArgs& norm = NormArgs{nullptr, nullptr, 0.f}) {
     if (!w) return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: weight is NULL");
     if (m < 0) return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: m < 0");
     if (epi == kEpiSwiglu && w->n % 2 != 0)
@@ -330,7 +330,19 @@ int qmatmul_impl(const unillm_qweight* w, const float* x_dev, int64_t m, float* 
         return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: x must be 16-byte aligned");
     if (m > (int64_t)INT32_MAX / 2)
         return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: m too large");
-    if (path == UNILLM_PATH_AUTO) path = unillm_hip_select_path(w, m);
+    if (norm.gamma && (!aligned16(norm.gamma) || (norm.beta && !aligned16(norm.beta)) ||
+                       !(norm.eps >= 0.0f)))
+        return fail(UNILLM_ERR_INVALID_ARG,
+                    "QMatMul forward failed: norm weight / bias must be 16-byte aligned, eps >= 0");
+    if (path == UNILLM_PATH_AUTO) {
+        path = unillm_hip_select_path(w, m);
+        // a fused layer norm on the GEMV takes k <= 8192; past it, batched decode
+        if (norm.gamma && path == UNILLM_PATH_GEMV && !gemv_supports_norm(*w, m))
+            path = UNILLM_PATH_DECODE_MFMA;
+    }
+    if (norm.gamma && path == UNILLM_PATH_GEMV && !gemv_supports_norm(*w, m))
+        return fail(UNILLM_ERR_UNSUPPORTED,
+                    "QMatMul forward failed: a fused layer norm on the GEMV path takes k <= 8192");
     if (int rc = ensure_init()) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     float* out = y_dev;
@@ -350,15 +362,15 @@ int qmatmul_impl(const unillm_qweight* w, const float* x_dev, int64_t m, float* 
                             "GEMV path takes m <= 4, k <= " +
                                 std::to_string(gemv_max_kb(m, w->qtype) * QK) +
                                 " at this m and weights under 4 GiB");
-            e = launch_gemv(*w, x_dev, m, out, s, run_epi);
+            e = launch_gemv(*w, x_dev, m, out, s, run_epi, norm);
             break;
         case UNILLM_PATH_DECODE_MFMA:
             if (m > kDecodeMaxM)
                 return fail(UNILLM_ERR_UNSUPPORTED, "decode MFMA path takes m <= 64");
-            e = launch_decode_mfma(*w, x_dev, m, out, s, run_epi);
+            e = launch_decode_mfma(*w, x_dev, m, out, s, run_epi, norm);
             break;
         case UNILLM_PATH_PREFILL_MFMA:
-            e = launch_prefill_mfma(*w, x_dev, m, out, s, run_epi);
+            e = launch_prefill_mfma(*w, x_dev, m, out, s, run_epi, norm);
             break;
         default:
             return fail(UNILLM_ERR_INVALID_ARG, "unknown path " + std::to_string(path));
@@ -382,6 +394,22 @@ int unillm_hip_qmatmul_add(const unillm_qweight* w, const float* x_dev, int64_t 
 int unillm_hip_qmatmul_swiglu(const unillm_qweight* w, const float* x_dev, int64_t m,
                               float* act_dev, void* stream) {
     return qmatmul_impl(w, x_dev, m, act_dev, UNILLM_PATH_AUTO, stream, kEpiSwiglu);
+}
+
+int unillm_hip_qmatmul_norm(const unillm_qweight* w, const float* x_dev, const float* gamma_dev,
+                            const float* beta_dev, float eps, int64_t m, float* y_dev,
+                            void* stream) {
+    if (!gamma_dev) return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: gamma is NULL");
+    return qmatmul_impl(w, x_dev, m, y_dev, UNILLM_PATH_AUTO, stream, kEpiStore,
+                        NormArgs{gamma_dev, beta_dev, eps});
+}
+
+int unillm_hip_qmatmul_norm_swiglu(const unillm_qweight* w, const float* x_dev,
+                                   const float* gamma_dev, const float* beta_dev, float eps,
+                                   int64_t m, float* act_dev, void* stream) {
+    if (!gamma_dev) return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: gamma is NULL");
+    return qmatmul_impl(w, x_dev, m, act_dev, UNILLM_PATH_AUTO, stream, kEpiSwiglu,
+                        NormArgs{gamma_dev, beta_dev, eps});
 }
 
 int unillm_hip_qmatmul(const unillm_qweight* w, const float* x_dev, int64_t m, float* y_dev,

@@ -570,6 +570,68 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
 
 }  // namespace
 
+// One workgroup per row r of x: the row's layer norm (two passes for the mean and
+// the mean squared deviation, as ops_fn::layer_norm computes them), then each
+// group of 8 normalized values converted to the MFMA operand type -- f16 in the
+// decode kernel's order 0 2 1 3 4 6 5 7, or bf16 in order -- and y's row r
+// zeroed over ny columns.
+template <bool F16PERM>
+__global__ __launch_bounds__(256) void norm_convert_kernel(const float* __restrict__ x, int64_t k,
+                                                           NormArgs norm, uint4* __restrict__ out,
+                                                           float* __restrict__ y, int64_t ny) {
+    __shared__ float red[4];
+    const int64_t r = blockIdx.x;
+    const float4* xr = reinterpret_cast<const float4*>(x + r * k);
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    auto block_sum = [&](float t) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
+        if (lane == 0) red[wv] = t;
+        __syncthreads();
+        const float sum = red[0] + red[1] + red[2] + red[3];
+        __syncthreads();
+        return sum;
+    };
+    float t = 0.0f;
+    for (int64_t i = threadIdx.x; i < k / 4; i += 256) {
+        const float4 a = xr[i];
+        t += (a.x + a.y) + (a.z + a.w);
+    }
+    const float mean = block_sum(t) / (float)k;
+    t = 0.0f;
+    for (int64_t i = threadIdx.x; i < k / 4; i += 256) {
+        const float4 a = xr[i];
+        t += (a.x - mean) * (a.x - mean) + (a.y - mean) * (a.y - mean) +
+             (a.z - mean) * (a.z - mean) + (a.w - mean) * (a.w - mean);
+    }
+    const float sd = sqrtf(block_sum(t) / (float)k + norm.eps);
+    const float4* g4 = reinterpret_cast<const float4*>(norm.gamma);
+    const float4* b4 = reinterpret_cast<const float4*>(norm.beta);
+    for (int64_t i = threadIdx.x; i < k / 8; i += 256) {
+        float v[8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float4 a = xr[2 * i + h], g = g4[2 * i + h];
+            const float4 b = norm.beta ? b4[2 * i + h] : make_float4(0.f, 0.f, 0.f, 0.f);
+            v[4 * h + 0] = (a.x - mean) / sd * g.x + b.x;
+            v[4 * h + 1] = (a.y - mean) / sd * g.y + b.y;
+            v[4 * h + 2] = (a.z - mean) / sd * g.z + b.z;
+            v[4 * h + 3] = (a.w - mean) / sd * g.w + b.w;
+        }
+        uint32_t o[4];
+        if constexpr (F16PERM) {
+            o[0] = pk_f16(v[0], v[2]); o[1] = pk_f16(v[1], v[3]);
+            o[2] = pk_f16(v[4], v[6]); o[3] = pk_f16(v[5], v[7]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(o[j]) : "v"(v[2 * j]), "v"(v[2 * j + 1]));
+        }
+        out[r * (k / 8) + i] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    for (int64_t i = threadIdx.x; i < ny; i += 256) y[r * ny + i] = 0.0f;
+}
+
 hipError_t launch_swiglu(const float* gu, int64_t m, int64_t I, float* act, hipStream_t s) {
     const int64_t total = m * I;
     const int grid = (int)std::min<int64_t>((total + 255) / 256, (int64_t)device_info().cu_count * 8);
@@ -577,8 +639,18 @@ hipError_t launch_swiglu(const float* gu, int64_t m, int64_t I, float* act, hipS
     return hipGetLastError();
 }
 
+hipError_t launch_norm_convert(const float* x, int64_t m, int64_t k, const NormArgs& norm,
+                               bool f16_perm, void* out, float* y, int64_t ny, hipStream_t s) {
+    if (m <= 0) return hipSuccess;
+    if (f16_perm)
+        norm_convert_kernel<true><<<(unsigned)m, 256, 0, s>>>(x, k, norm, static_cast<uint4*>(out), y, ny);
+    else
+        norm_convert_kernel<false><<<(unsigned)m, 256, 0, s>>>(x, k, norm, static_cast<uint4*>(out), y, ny);
+    return hipGetLastError();
+}
+
 hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float* y,
-                              hipStream_t s, int epi) {
+                              hipStream_t s, int epi, const NormArgs& norm) {
     // 32-bit offsets: x in f16 elements, weight bytes
     if ((uint64_t)m * (uint64_t)w.k >= (1ull << 31) ||
         (uint64_t)w.n * (uint64_t)w.row_bytes >= (1ull << 32))
@@ -599,8 +671,14 @@ hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float
     const int64_t work = std::max(n8, ny / 4);
     const int grid =
         (int)std::min<int64_t>((work + 255) / 256, (int64_t)device_info().cu_count * 8);
-    xprep_kernel<<<grid, 256, 0, s>>>(x, static_cast<uint4*>(ws), n8, y, ny);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (norm.gamma) {
+        if ((e = launch_norm_convert(x, m, w.k, norm, true, ws, y, ny > 0 ? w.n : 0, s)) !=
+            hipSuccess)
+            return e;
+    } else {
+        xprep_kernel<<<grid, 256, 0, s>>>(x, static_cast<uint4*>(ws), n8, y, ny);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
     const _Float16* xh = static_cast<const _Float16*>(ws);
     if (k4)
         return wide ? launch_mt<UNILLM_QTYPE_Q4_K, 2>(w, xh, m, y, S, s, add)

@@ -417,12 +417,18 @@ constexpr int gemv_threads() {
 // KB <= NB * 64, so a thread builds at most PASSES = ceil(M * NB * 256 / THREADS) quarter-blocks.
 // PAIR: the weight is [gate; up] (2 I rows); the waves cover the I logical rows
 // and y is [m, I] = silu(gate) * up.  Otherwise `add` selects y += x W^T.
-template <int QT, int M, int NB, int R, int THREADS, bool PAIR = false>
+//
+// norm.gamma != nullptr: x is first replaced by its layer norm along k,
+// (x - mean) / sqrt(var + eps) * gamma (+ beta), var the mean of the squared
+// deviations (the reference's ops_fn::layer_norm before the projections,
+// tensor_core.rs:973-1008).  Every workgroup reads all of x anyway, so each
+// computes the row statistics itself: two block reductions, no extra launch.
+template <int QT, int M, int NB, int R, int THREADS, bool PAIR = false, bool NORM = false>
 __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict__ base,
                                                        int64_t rb,
                                                        const float* __restrict__ x,
                                                        float* __restrict__ y, int N_rows, int KB,
-                                                       int m_real, int add) {
+                                                       int m_real, int add, NormArgs norm) {
     static_assert(!PAIR || R == 2, "the SwiGLU pair is one gate and one up row per chunk");
     constexpr int LR = PAIR ? 1 : R;  // logical rows per chunk
     const int I = PAIR ? N_rows / 2 : 0;
@@ -488,6 +494,103 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     Chunk<QT, NB, R> a, b;
     load_chunk<QT, NB, R, PAIR>(a, base, (uint32_t)rb, wrow, waves, 0, jlast, poff, soff, hoff, I);
 
+    // 2b. the layer norm of x: row means, then the mean squared deviations, each
+    //     summed over the workgroup; only real quarters count
+    if constexpr (NORM) {
+        __shared__ float red[M * WAVES];
+        const int wv = threadIdx.x >> 6;
+        float mean[M], sd[M];
+        auto block_sum = [&](float (&acc)[M], float (&out)[M]) {
+#pragma unroll
+            for (int mm = 0; mm < M; ++mm) {
+                const float t = wave_sum(acc[mm]);
+                if (lane == 0) red[mm * WAVES + wv] = t;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int mm = 0; mm < M; ++mm) {
+                float t = 0.0f;
+                for (int w2 = 0; w2 < WAVES; ++w2) t += red[mm * WAVES + w2];
+                out[mm] = t;
+            }
+            __syncthreads();
+        };
+        float acc[M];
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) acc[mm] = 0.0f;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            if (wave0 + p * THREADS >= nq) continue;
+            const int q = (int)threadIdx.x + p * THREADS;
+            const int m = min(q, nq - 1) / (4 * KB);
+            float t = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) t += v[p][j];
+#pragma unroll
+            for (int mm = 0; mm < M; ++mm) acc[mm] += q < nq && m == mm ? t : 0.0f;
+        }
+        block_sum(acc, mean);
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) {
+            mean[mm] = mean[mm] / (float)K;
+            acc[mm] = 0.0f;
+        }
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            if (wave0 + p * THREADS >= nq) continue;
+            const int q = (int)threadIdx.x + p * THREADS;
+            const int m = min(q, nq - 1) / (4 * KB);
+            float mu = mean[0];
+#pragma unroll
+            for (int mm = 1; mm < M; ++mm) mu = m == mm ? mean[mm] : mu;
+            float t = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) t += (v[p][j] - mu) * (v[p][j] - mu);
+#pragma unroll
+            for (int mm = 0; mm < M; ++mm) acc[mm] += q < nq && m == mm ? t : 0.0f;
+        }
+        block_sum(acc, sd);
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) sd[mm] = sqrtf(sd[mm] / (float)K + norm.eps);
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            if (wave0 + p * THREADS >= nq) continue;
+            const int q = min((int)threadIdx.x + p * THREADS, nq - 1);
+            const int blk = q >> 2;
+            const int m = blk / KB;
+            float mu = mean[0], sg = sd[0];
+#pragma unroll
+            for (int mm = 1; mm < M; ++mm) {
+                mu = m == mm ? mean[mm] : mu;
+                sg = m == mm ? sd[mm] : sg;
+            }
+            int o0, o1;
+            quarter_offsets<QT>(q & 3, o0, o1);
+            const int64_t e = (int64_t)(blk - m * KB) * QK;
+            const float4 g0 = *reinterpret_cast<const float4*>(norm.gamma + e + o0);
+            const float4 g1 = *reinterpret_cast<const float4*>(norm.gamma + e + o1);
+            float4 b0 = make_float4(0.f, 0.f, 0.f, 0.f), b1 = b0;
+            if (norm.beta) {
+                b0 = *reinterpret_cast<const float4*>(norm.beta + e + o0);
+                b1 = *reinterpret_cast<const float4*>(norm.beta + e + o1);
+            }
+            float g[8], bb[8];
+            if constexpr (!kByteCodes<QT>) {  // the nibble order of v
+                g[0] = g0.x; g[1] = g1.x; g[2] = g0.y; g[3] = g1.y;
+                g[4] = g0.z; g[5] = g1.z; g[6] = g0.w; g[7] = g1.w;
+                bb[0] = b0.x; bb[1] = b1.x; bb[2] = b0.y; bb[3] = b1.y;
+                bb[4] = b0.z; bb[5] = b1.z; bb[6] = b0.w; bb[7] = b1.w;
+            } else {
+                g[0] = g0.x; g[1] = g0.y; g[2] = g0.z; g[3] = g0.w;
+                g[4] = g1.x; g[5] = g1.y; g[6] = g1.z; g[7] = g1.w;
+                bb[0] = b0.x; bb[1] = b0.y; bb[2] = b0.z; bb[3] = b0.w;
+                bb[4] = b1.x; bb[5] = b1.y; bb[6] = b1.z; bb[7] = b1.w;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[p][j] = (v[p][j] - mu) / sg * g[j] + bb[j];
+        }
+    }
+
     // 3. x digit records for all M * KB blocks, four threads per block (threads
     //    past nq compute on a clamped copy and store nothing; nq is a multiple
     //    of 4, so a DPP quad is either all real or all clamped).
@@ -530,15 +633,26 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     }
 }
 
+// The norm variants exist for k <= 8192 (NB <= 4): the layer-normed inputs
+// feed QKV and gate/up, whose k is the hidden size; larger k with a norm runs
+// on the batched-decode path (gemv_supports_norm).
 template <int QT, int M, int NB, int R, bool PAIR = false>
 hipError_t launch_r(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st,
-                    int waves, int add) {
+                    int waves, int add, const NormArgs& norm) {
     constexpr int THREADS = gemv_threads<QT, M, NB>();
     constexpr int WAVES = THREADS / 64;
     const size_t lds = (size_t)M * w.kb * kXWords * sizeof(uint32_t);
     const int grid = (waves + WAVES - 1) / WAVES;
-    gemv_kernel<QT, M, NB, R, THREADS, PAIR><<<grid, THREADS, lds, st>>>(
-        w.base, w.row_bytes, x, y, (int)w.n, (int)w.kb, (int)m, add);
+    if (norm.gamma) {
+        if constexpr (NB <= 4)
+            gemv_kernel<QT, M, NB, R, THREADS, PAIR, true><<<grid, THREADS, lds, st>>>(
+                w.base, w.row_bytes, x, y, (int)w.n, (int)w.kb, (int)m, add, norm);
+        else
+            return hipErrorInvalidValue;
+    } else {
+        gemv_kernel<QT, M, NB, R, THREADS, PAIR><<<grid, THREADS, lds, st>>>(
+            w.base, w.row_bytes, x, y, (int)w.n, (int)w.kb, (int)m, add, norm);
+    }
     return hipGetLastError();
 }
 
@@ -549,7 +663,7 @@ hipError_t launch_r(const QWeight& w, const float* x, int64_t m, float* y, hipSt
 // chunk may take (at most 4 payload loads per lane).
 template <int QT, int M, int NB>
 hipError_t launch_nb(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st,
-                     int epi) {
+                     int epi, const NormArgs& norm) {
     constexpr int V = Payload<QT>::V;
     constexpr int RMAX = NB * V >= 4 ? 1 : 4 / (NB * V);
     constexpr int THREADS = gemv_threads<QT, M, NB>();
@@ -566,7 +680,7 @@ hipError_t launch_nb(const QWeight& w, const float* x, int64_t m, float* y, hipS
             const int64_t resident = cus * std::max(per_cu, 1) * WAVES;
             const int64_t waves = std::max<int64_t>(
                 1, std::min({resident, std::max<int64_t>(I / 2, cus * WAVES), I}));
-            return launch_r<QT, M, NB, 2, true>(w, x, m, y, st, (int)waves, 0);
+            return launch_r<QT, M, NB, 2, true>(w, x, m, y, st, (int)waves, 0, norm);
         }
         return hipErrorInvalidValue;
     }
@@ -582,23 +696,24 @@ hipError_t launch_nb(const QWeight& w, const float* x, int64_t m, float* y, hipS
                 (long long)w.n, (long long)w.kb, (long long)m, THREADS, (long long)waves,
                 (long long)rows);
     const int add = epi == kEpiAdd;
-    if (RMAX >= 4 && rows > 4) return launch_r<QT, M, NB, RMAX>(w, x, m, y, st, (int)waves, add);
+    if (RMAX >= 4 && rows > 4)
+        return launch_r<QT, M, NB, RMAX>(w, x, m, y, st, (int)waves, add, norm);
     if (RMAX >= 2 && rows > 2)
-        return launch_r<QT, M, NB, (RMAX >= 2 ? 2 : 1)>(w, x, m, y, st, (int)waves, add);
-    return launch_r<QT, M, NB, 1>(w, x, m, y, st, (int)waves, add);
+        return launch_r<QT, M, NB, (RMAX >= 2 ? 2 : 1)>(w, x, m, y, st, (int)waves, add, norm);
+    return launch_r<QT, M, NB, 1>(w, x, m, y, st, (int)waves, add, norm);
 }
 
 template <int QT, int M>
 hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st,
-                    int epi) {
+                    int epi, const NormArgs& norm) {
     switch ((int)((w.kb + 63) / 64)) {
-        case 1: return launch_nb<QT, M, 1>(w, x, m, y, st, epi);
-        case 2: return launch_nb<QT, M, 2>(w, x, m, y, st, epi);
-        case 3: if constexpr (M <= 2) return launch_nb<QT, M, 3>(w, x, m, y, st, epi); break;
-        case 4: if constexpr (M <= 2) return launch_nb<QT, M, 4>(w, x, m, y, st, epi); break;
-        case 5: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 5>(w, x, m, y, st, epi); break;
-        case 6: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 6>(w, x, m, y, st, epi); break;
-        case 7: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 7>(w, x, m, y, st, epi); break;
+        case 1: return launch_nb<QT, M, 1>(w, x, m, y, st, epi, norm);
+        case 2: return launch_nb<QT, M, 2>(w, x, m, y, st, epi, norm);
+        case 3: if constexpr (M <= 2) return launch_nb<QT, M, 3>(w, x, m, y, st, epi, norm); break;
+        case 4: if constexpr (M <= 2) return launch_nb<QT, M, 4>(w, x, m, y, st, epi, norm); break;
+        case 5: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 5>(w, x, m, y, st, epi, norm); break;
+        case 6: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 6>(w, x, m, y, st, epi, norm); break;
+        case 7: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 7>(w, x, m, y, st, epi, norm); break;
         default: break;
     }
     return hipErrorInvalidValue;
@@ -625,6 +740,10 @@ bool gemv_supports_swiglu(const QWeight& w, int64_t m) {
     return gemv_supports(w, m) && w.n % 2 == 0 && mb * nbv <= 4;
 }
 
+bool gemv_supports_norm(const QWeight& w, int64_t m) {
+    return gemv_supports(w, m) && (w.kb + 63) / 64 <= 4;
+}
+
 // The GEMV addresses a weight with 32-bit row offsets.
 bool gemv_supports(const QWeight& w, int64_t m) {
     return m >= 1 && m <= kGemvMaxM && w.kb <= gemv_max_kb(m, w.qtype) &&
@@ -632,25 +751,25 @@ bool gemv_supports(const QWeight& w, int64_t m) {
 }
 
 hipError_t launch_gemv(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t s,
-                       int epi) {
+                       int epi, const NormArgs& norm) {
     if (w.qtype == UNILLM_QTYPE_Q4_K) {
-        if (m == 1) return launch_m<UNILLM_QTYPE_Q4_K, 1>(w, x, m, y, s, epi);
-        if (m == 2) return launch_m<UNILLM_QTYPE_Q4_K, 2>(w, x, m, y, s, epi);
-        return launch_m<UNILLM_QTYPE_Q4_K, 4>(w, x, m, y, s, epi);
+        if (m == 1) return launch_m<UNILLM_QTYPE_Q4_K, 1>(w, x, m, y, s, epi, norm);
+        if (m == 2) return launch_m<UNILLM_QTYPE_Q4_K, 2>(w, x, m, y, s, epi, norm);
+        return launch_m<UNILLM_QTYPE_Q4_K, 4>(w, x, m, y, s, epi, norm);
     }
     if (w.qtype == UNILLM_QTYPE_Q6_K) {
-        if (m == 1) return launch_m<UNILLM_QTYPE_Q6_K, 1>(w, x, m, y, s, epi);
-        if (m == 2) return launch_m<UNILLM_QTYPE_Q6_K, 2>(w, x, m, y, s, epi);
-        return launch_m<UNILLM_QTYPE_Q6_K, 4>(w, x, m, y, s, epi);
+        if (m == 1) return launch_m<UNILLM_QTYPE_Q6_K, 1>(w, x, m, y, s, epi, norm);
+        if (m == 2) return launch_m<UNILLM_QTYPE_Q6_K, 2>(w, x, m, y, s, epi, norm);
+        return launch_m<UNILLM_QTYPE_Q6_K, 4>(w, x, m, y, s, epi, norm);
     }
     if (w.qtype == UNILLM_QTYPE_Q4_0) {
-        if (m == 1) return launch_m<UNILLM_QTYPE_Q4_0, 1>(w, x, m, y, s, epi);
-        if (m == 2) return launch_m<UNILLM_QTYPE_Q4_0, 2>(w, x, m, y, s, epi);
-        return launch_m<UNILLM_QTYPE_Q4_0, 4>(w, x, m, y, s, epi);
+        if (m == 1) return launch_m<UNILLM_QTYPE_Q4_0, 1>(w, x, m, y, s, epi, norm);
+        if (m == 2) return launch_m<UNILLM_QTYPE_Q4_0, 2>(w, x, m, y, s, epi, norm);
+        return launch_m<UNILLM_QTYPE_Q4_0, 4>(w, x, m, y, s, epi, norm);
     }
-    if (m == 1) return launch_m<UNILLM_QTYPE_Q8_0, 1>(w, x, m, y, s, epi);
-    if (m == 2) return launch_m<UNILLM_QTYPE_Q8_0, 2>(w, x, m, y, s, epi);
-    return launch_m<UNILLM_QTYPE_Q8_0, 4>(w, x, m, y, s, epi);
+    if (m == 1) return launch_m<UNILLM_QTYPE_Q8_0, 1>(w, x, m, y, s, epi, norm);
+    if (m == 2) return launch_m<UNILLM_QTYPE_Q8_0, 2>(w, x, m, y, s, epi, norm);
+    return launch_m<UNILLM_QTYPE_Q8_0, 4>(w, x, m, y, s, epi, norm);
 }
 
 }  // namespace unillm

@@ -56,11 +56,21 @@ using QWeight = ::unillm_qweight;
 int64_t gemv_max_kb(int64_t m, int qtype);
 bool gemv_supports(const unillm_qweight& w, int64_t m);
 bool gemv_supports_swiglu(const unillm_qweight& w, int64_t m);
+bool gemv_supports_norm(const unillm_qweight& w, int64_t m);
 
 // Epilogues of the matmul launches: y = x W^T (store), y += x W^T (the decoder
 // layer's residual add, llama.rs:668, 677), or for a [gate; up] weight of 2 I
 // rows y[m, I] = silu(x G^T) * (x U^T) (fused_swiglu, tensor_core.rs:1385-1396).
 constexpr int kEpiStore = 0, kEpiAdd = 1, kEpiSwiglu = 2;
+
+// The layer norm applied to x before the matmul (gamma == nullptr: none):
+// (x - mean) / sqrt(var + eps) * gamma (+ beta) along k, var = mean((x - mean)^2)
+// (ops_fn::layer_norm, tensor_core.rs:973-1008; eps 1e-6 at llama.rs:662, 671).
+struct NormArgs {
+    const float* gamma;
+    const float* beta;  // may be nullptr
+    float eps;
+};
 
 inline bool is_kquant(int qtype) {
     return qtype == UNILLM_QTYPE_Q4_K || qtype == UNILLM_QTYPE_Q6_K;
@@ -136,11 +146,18 @@ hipError_t launch_quantize(int qtype, const float* w, int64_t n, int64_t k, uint
 // epi: kEpiStore or kEpiAdd on every path; kEpiSwiglu on the GEMV only
 // (gemv_supports_swiglu), the other paths run it as store + swiglu_kernel.
 hipError_t launch_gemv(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t s,
-                       int epi = kEpiStore);
+                       int epi = kEpiStore, const NormArgs& norm = NormArgs{nullptr, nullptr, 0.f});
 hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float* y,
-                              hipStream_t s, int epi = kEpiStore);
+                              hipStream_t s, int epi = kEpiStore,
+                              const NormArgs& norm = NormArgs{nullptr, nullptr, 0.f});
 hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, float* y,
-                               hipStream_t s, int epi = kEpiStore);
+                               hipStream_t s, int epi = kEpiStore,
+                               const NormArgs& norm = NormArgs{nullptr, nullptr, 0.f});
+// x[m, k] -> its layer norm in the MFMA paths' operand form (f16 in the decode
+// kernel's element order, or bf16), one workgroup per row; zeroes y rows
+// [0, m) of width ny when ny > 0 (a split k adds into it).
+hipError_t launch_norm_convert(const float* x, int64_t m, int64_t k, const NormArgs& norm,
+                               bool f16_perm, void* out, float* y, int64_t ny, hipStream_t s);
 // act[m, I] = silu(g[m, i]) * u[m, i] with g, u the two halves of each row of
 // gu[m, 2 I] (the SwiGLU of the MFMA paths, after their store)
 hipError_t launch_swiglu(const float* gu, int64_t m, int64_t I, float* act, hipStream_t s);

@@ -496,7 +496,7 @@ PrefillPlan prefill_plan(const QWeight& w, int64_t m) {
 }  // namespace
 
 hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, float* y,
-                               hipStream_t s, int epi) {
+                               hipStream_t s, int epi, const NormArgs& norm) {
     // x in bf16 (the operand precision) in the stream's workspace: the GEMM
     // re-reads x once per 256-column tile, so it reads half the bytes, and no
     // conversion sits in its inner loop.  The same kernel zeroes y for a split k.
@@ -509,8 +509,12 @@ hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, floa
     const int64_t n8 = n / 8, ny = plan.S > 1 && !add ? m * w.n : 0;
     const int grid = (int)std::min<int64_t>((std::max(n8, ny / 4) + 255) / 256,
                                             (int64_t)device_info().cu_count * 16);
-    x_to_bf16_kernel<<<grid, 256, 0, s>>>(x, static_cast<uint4*>(ws), n8, y, ny);
-    e = hipGetLastError();
+    if (norm.gamma)
+        e = launch_norm_convert(x, m, w.k, norm, false, ws, y, ny > 0 ? w.n : 0, s);
+    else {
+        x_to_bf16_kernel<<<grid, 256, 0, s>>>(x, static_cast<uint4*>(ws), n8, y, ny);
+        e = hipGetLastError();
+    }
     if (e != hipSuccess) return e;
     const __bf16* xb = static_cast<const __bf16*>(ws);
     if (w.qtype == UNILLM_QTYPE_Q4_K)

@@ -133,13 +133,43 @@ class QuantLinear:
         return residual
 
     def forward_swiglu(self, x: torch.Tensor, out: torch.Tensor | None = None,
-                       stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+                       stream: torch.cuda.Stream | None = None,
+                       norm: tuple | None = None) -> torch.Tensor:
         """silu(x G^T) * (x U^T) for a [gate; up] weight (n = 2 I): [..., I]
-        (LlamaMLP's gate, up and fused_swiglu, llama.rs:1275-1283)."""
+        (LlamaMLP's gate, up and fused_swiglu, llama.rs:1275-1283); with norm =
+        (gamma, beta or None, eps), on the layer norm of x."""
         m = self._check_input(x)
         out = self._out(x, m, self.n // 2, out)
-        rc = _capi.lib().unillm_hip_qmatmul_swiglu(self._h, x.data_ptr(), m, out.data_ptr(),
-                                                   _stream_ptr(stream))
+        if norm is None:
+            rc = _capi.lib().unillm_hip_qmatmul_swiglu(self._h, x.data_ptr(), m, out.data_ptr(),
+                                                       _stream_ptr(stream))
+        else:
+            g, b, eps = self._norm_args(norm)
+            rc = _capi.lib().unillm_hip_qmatmul_norm_swiglu(
+                self._h, x.data_ptr(), g, b, eps, m, out.data_ptr(), _stream_ptr(stream))
+        if rc != _capi.OK:
+            raise HipError(rc, _capi.last_error())
+        return out
+
+    def _norm_args(self, norm):
+        gamma, beta, eps = norm
+        for t in (gamma, beta):
+            if t is not None and (t.dtype != torch.float32 or not t.is_cuda
+                                  or not t.is_contiguous() or t.numel() != self.k):
+                raise RuntimeError("QMatMul forward failed: norm weight / bias must be "
+                                   "contiguous f32 [k] device tensors")
+        return gamma.data_ptr(), (beta.data_ptr() if beta is not None else None), float(eps)
+
+    def forward_norm(self, x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor | None = None,
+                     eps: float = 1e-6, out: torch.Tensor | None = None,
+                     stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        """LN(x) . dequant(W)^T with the reference's layer norm (tensor_core.rs:973-1008)
+        fused into the matmul's x preparation."""
+        m = self._check_input(x)
+        out = self._out(x, m, self.n, out)
+        g, b, e = self._norm_args((gamma, beta, eps))
+        rc = _capi.lib().unillm_hip_qmatmul_norm(self._h, x.data_ptr(), g, b, e, m,
+                                                 out.data_ptr(), _stream_ptr(stream))
         if rc != _capi.OK:
             raise HipError(rc, _capi.last_error())
         return out

@@ -320,6 +320,30 @@ static void test_gpu_kq(const std::string& gguf, const std::vector<Expect>& ex) 
             bool same = true;
             for (size_t i = 0; i < got.size(); ++i) same = same && got[i] == r0[i] + plain[i];
             CHECK(same);  // GEMV: one rounding of r + the same row sum
+            // the layer norm in front: gamma = 1, no bias -> the same as normalizing on
+            // the host (two-pass mean and variance, eps 1e-6) and a plain forward
+            std::vector<float> xn(e->x.size());
+            for (uint32_t row = 0; row < e->m; ++row) {
+                const float* xr = e->x.data() + (size_t)row * e->k;
+                double mu = 0, var = 0;
+                for (uint32_t c = 0; c < e->k; ++c) mu += xr[c];
+                mu /= e->k;
+                for (uint32_t c = 0; c < e->k; ++c) var += (xr[c] - mu) * (xr[c] - mu);
+                const double sd = std::sqrt(var / e->k + 1e-6);
+                for (uint32_t c = 0; c < e->k; ++c) xn[(size_t)row * e->k + c] = (float)((xr[c] - mu) / sd);
+            }
+            const Tensor gamma = Tensor::from_host(std::vector<float>(e->k, 1.0f), {(int64_t)e->k},
+                                                   Device::hip(0));
+            const std::vector<float> yn = q->forward_norm(x, gamma, nullptr, 1e-6f).to_host();
+            const std::vector<float> yh =
+                q->forward(Tensor::from_host(xn, {(int64_t)e->m, (int64_t)e->k}, Device::hip(0)))
+                    .to_host();
+            double num = 0, den = 0;
+            for (size_t i = 0; i < yn.size(); ++i) {
+                num = std::max(num, (double)std::fabs(yn[i] - yh[i]));
+                den = std::max(den, (double)std::fabs(yh[i]));
+            }
+            CHECK(num <= 1e-3 * den);
         }
     }
 }

@@ -203,6 +203,23 @@ Tensor QuantLinear::forward_swiglu(const Tensor& x, void* stream) const {
     return act;
 }
 
+Tensor QuantLinear::forward_norm(const Tensor& x, const Tensor& gamma, const Tensor* beta,
+                                 float eps, void* stream) const {
+    check_input(x);
+    auto vec_k = [&](const Tensor& t) {
+        return t.device().is_hip() && t.numel() == k_;
+    };
+    if (!vec_k(gamma) || (beta && !vec_k(*beta)))
+        throw Error("QMatMul forward failed: norm weight / bias must be HIP tensors of k elements");
+    std::vector<int64_t> oshape = x.shape();
+    oshape.back() = n_;
+    Tensor y = Tensor::empty(oshape, x.device());
+    check(unillm_hip_qmatmul_norm(w_, x.data(), gamma.data(), beta ? beta->data() : nullptr, eps,
+                                  x.numel() / k_, y.data_mut(), stream),
+          "QMatMul forward failed");
+    return y;
+}
+
 Tensor QuantLinear::dequantize(void* stream) const {
     Tensor out = Tensor::empty({n_, k_}, Device::hip(0));
     check(unillm_hip_dequant(w_, out.data_mut(), stream), "Failed to dequantize");

@@ -111,6 +111,11 @@ public:
     // For a [gate; up] handle (LoadOptions::fuse_gate_up): silu(gate) * up, [.., n / 2]
     // (LlamaMLP::forward's two projections and fused_swiglu, llama.rs:1275-1283).
     Tensor forward_swiglu(const Tensor& x, void* stream = nullptr) const;
+    // forward on the layer norm of x along k, (x - mean) / sqrt(var + eps) *
+    // gamma (+ beta) (ops_fn::layer_norm, tensor_core.rs:973-1008), fused into the
+    // matmul; gamma / beta are HIP tensors of k elements (beta may be empty).
+    Tensor forward_norm(const Tensor& x, const Tensor& gamma, const Tensor* beta, float eps,
+                        void* stream = nullptr) const;
     // qtensor.dequantize: f32 [n, k] on the device, bit-exact with GGML.
     Tensor dequantize(void* stream = nullptr) const;
 

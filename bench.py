@@ -316,6 +316,31 @@ def extra_configs(torch, QuantLinear, gen, stream, only):
                 "GB/s": round(b / ms / 1e6, 1), "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 3),
                 "ms_per_step": round(ms, 4), "tokens/s": round(m * 1e3 / ms, 1),
                 "weight_bytes": total_w}
+
+            # the same four launches per layer with the layer's elementwise work in
+            # them: input_layernorm + QKV, o_proj + residual add, post_attention_layernorm
+            # + gate_up + SwiGLU, down + residual add (the lm_head as before)
+            gam = torch.ones(4096, device="cuda")
+            h = torch.empty(m, 4096, device="cuda").normal_(generator=gen)
+            act = torch.empty(m, 11008, device="cuda")
+
+            def fused_step():
+                for qkv, o, gu, down in layers:
+                    qkv.forward_norm(h, gam, eps=1e-6, out=ys[12288], stream=stream)
+                    o.forward_add(xs[4096], h, stream=stream)
+                    gu.forward_swiglu(h, out=act, stream=stream, norm=(gam, None, 1e-6))
+                    down.forward_add(act, h, stream=stream)
+                head.forward(xs[4096], out=ys[32000], stream=stream)
+
+            with torch.cuda.stream(stream):
+                h.normal_(generator=gen)
+                fused_step()
+                h.normal_(generator=gen)  # the residual grows by design; restart it
+                msf = float(np.median([timer.run(fused_step, 3) for _ in range(3)]))
+            res[f"llama2_7b_stack_q4_0_fused_m{m}"] = {
+                "GB/s": round(b / msf / 1e6, 1), "ms_per_step": round(msf, 4),
+                "tokens/s": round(m * 1e3 / msf, 1),
+                "note": "norms, residual adds and SwiGLU fused into the same 4 launches a layer"}
         del layers, head
     torch.cuda.synchronize()
     return res

@@ -576,10 +576,10 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
 // decode kernel's order 0 2 1 3 4 6 5 7, or bf16 in order -- and y's row r
 // zeroed over ny columns.
 template <bool F16PERM>
-__global__ __launch_bounds__(256) void norm_convert_kernel(const float* __restrict__ x, int64_t k,
+__global__ __launch_bounds__(1024) void norm_convert_kernel(const float* __restrict__ x, int64_t k,
                                                            NormArgs norm, uint4* __restrict__ out,
                                                            float* __restrict__ y, int64_t ny) {
-    __shared__ float red[4];
+    __shared__ float red[16];
     const int64_t r = blockIdx.x;
     const float4* xr = reinterpret_cast<const float4*>(x + r * k);
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -588,18 +588,20 @@ __global__ __launch_bounds__(256) void norm_convert_kernel(const float* __restri
         for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
         if (lane == 0) red[wv] = t;
         __syncthreads();
-        const float sum = red[0] + red[1] + red[2] + red[3];
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) sum += red[w];
         __syncthreads();
         return sum;
     };
     float t = 0.0f;
-    for (int64_t i = threadIdx.x; i < k / 4; i += 256) {
+    for (int64_t i = threadIdx.x; i < k / 4; i += 1024) {
         const float4 a = xr[i];
         t += (a.x + a.y) + (a.z + a.w);
     }
     const float mean = block_sum(t) / (float)k;
     t = 0.0f;
-    for (int64_t i = threadIdx.x; i < k / 4; i += 256) {
+    for (int64_t i = threadIdx.x; i < k / 4; i += 1024) {
         const float4 a = xr[i];
         t += (a.x - mean) * (a.x - mean) + (a.y - mean) * (a.y - mean) +
              (a.z - mean) * (a.z - mean) + (a.w - mean) * (a.w - mean);
@@ -607,7 +609,7 @@ __global__ __launch_bounds__(256) void norm_convert_kernel(const float* __restri
     const float sd = sqrtf(block_sum(t) / (float)k + norm.eps);
     const float4* g4 = reinterpret_cast<const float4*>(norm.gamma);
     const float4* b4 = reinterpret_cast<const float4*>(norm.beta);
-    for (int64_t i = threadIdx.x; i < k / 8; i += 256) {
+    for (int64_t i = threadIdx.x; i < k / 8; i += 1024) {
         float v[8];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -629,7 +631,7 @@ __global__ __launch_bounds__(256) void norm_convert_kernel(const float* __restri
         }
         out[r * (k / 8) + i] = make_uint4(o[0], o[1], o[2], o[3]);
     }
-    for (int64_t i = threadIdx.x; i < ny; i += 256) y[r * ny + i] = 0.0f;
+    for (int64_t i = threadIdx.x; i < ny; i += 1024) y[r * ny + i] = 0.0f;
 }
 
 hipError_t launch_swiglu(const float* gu, int64_t m, int64_t I, float* act, hipStream_t s) {
@@ -643,9 +645,9 @@ hipError_t launch_norm_convert(const float* x, int64_t m, int64_t k, const NormA
                                bool f16_perm, void* out, float* y, int64_t ny, hipStream_t s) {
     if (m <= 0) return hipSuccess;
     if (f16_perm)
-        norm_convert_kernel<true><<<(unsigned)m, 256, 0, s>>>(x, k, norm, static_cast<uint4*>(out), y, ny);
+        norm_convert_kernel<true><<<(unsigned)m, 1024, 0, s>>>(x, k, norm, static_cast<uint4*>(out), y, ny);
     else
-        norm_convert_kernel<false><<<(unsigned)m, 256, 0, s>>>(x, k, norm, static_cast<uint4*>(out), y, ny);
+        norm_convert_kernel<false><<<(unsigned)m, 1024, 0, s>>>(x, k, norm, static_cast<uint4*>(out), y, ny);
     return hipGetLastError();
 }
 

@@ -466,24 +466,27 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     const int nq = M * KB * 4;
     const int wave0 = __builtin_amdgcn_readfirstlane((int)threadIdx.x & ~63);
     float v[PASSES][8];
+    auto order = [](float (&d)[8], float4 f0, float4 f1) {
+        if constexpr (!kByteCodes<QT>) {  // payload nibble order
+            d[0] = f0.x; d[1] = f1.x; d[2] = f0.y; d[3] = f1.y;
+            d[4] = f0.z; d[5] = f1.z; d[6] = f0.w; d[7] = f1.w;
+        } else {
+            d[0] = f0.x; d[1] = f0.y; d[2] = f0.z; d[3] = f0.w;
+            d[4] = f1.x; d[5] = f1.y; d[6] = f1.z; d[7] = f1.w;
+        }
+    };
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
         if (wave0 + p * THREADS >= nq) continue;
         const int q = min((int)threadIdx.x + p * THREADS, nq - 1);
         const int blk = q >> 2;
         const int m = blk / KB;
-        const float* xb = x + (int64_t)min(m, m_real - 1) * K + (int64_t)(blk - m * KB) * QK;
+        const int64_t e = (int64_t)(blk - m * KB) * QK;
+        const float* xb = x + (int64_t)min(m, m_real - 1) * K + e;
         int o0, o1;
         quarter_offsets<QT>(q & 3, o0, o1);
-        const float4 f0 = *reinterpret_cast<const float4*>(xb + o0);
-        const float4 f1 = *reinterpret_cast<const float4*>(xb + o1);
-        if constexpr (!kByteCodes<QT>) {  // payload nibble order
-            v[p][0] = f0.x; v[p][1] = f1.x; v[p][2] = f0.y; v[p][3] = f1.y;
-            v[p][4] = f0.z; v[p][5] = f1.z; v[p][6] = f0.w; v[p][7] = f1.w;
-        } else {
-            v[p][0] = f0.x; v[p][1] = f0.y; v[p][2] = f0.z; v[p][3] = f0.w;
-            v[p][4] = f1.x; v[p][5] = f1.y; v[p][6] = f1.z; v[p][7] = f1.w;
-        }
+        order(v[p], *reinterpret_cast<const float4*>(xb + o0),
+              *reinterpret_cast<const float4*>(xb + o1));
     }
 
     // 2. the first chunk of weights: one chunk per wave keeps the memory
@@ -494,28 +497,29 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     Chunk<QT, NB, R> a, b;
     load_chunk<QT, NB, R, PAIR>(a, base, (uint32_t)rb, wrow, waves, 0, jlast, poff, soff, hoff, I);
 
-    // 2b. the layer norm of x: row means, then the mean squared deviations, each
-    //     summed over the workgroup; only real quarters count
+    // 2b. the layer norm of x: row means, then the mean squared deviations (the
+    //     reference's two passes), each summed by DPP within a wave and over the
+    //     waves in LDS (separate arrays: one barrier each); only real quarters
+    //     count.  gamma and beta are read after the sums, so the loads issued
+    //     before the first weights stay x alone.
     if constexpr (NORM) {
-        __shared__ float red[M * WAVES];
+        __shared__ float red[2][M * WAVES];
         const int wv = threadIdx.x >> 6;
-        float mean[M], sd[M];
-        auto block_sum = [&](float (&acc)[M], float (&out)[M]) {
+        auto block_sum = [&](float (&acc)[M], float (&out)[M], float* r) {
 #pragma unroll
             for (int mm = 0; mm < M; ++mm) {
                 const float t = wave_sum(acc[mm]);
-                if (lane == 0) red[mm * WAVES + wv] = t;
+                if (lane == 0) r[mm * WAVES + wv] = t;
             }
             __syncthreads();
 #pragma unroll
             for (int mm = 0; mm < M; ++mm) {
                 float t = 0.0f;
-                for (int w2 = 0; w2 < WAVES; ++w2) t += red[mm * WAVES + w2];
+                for (int w2 = 0; w2 < WAVES; ++w2) t += r[mm * WAVES + w2];
                 out[mm] = t;
             }
-            __syncthreads();
         };
-        float acc[M];
+        float acc[M], mean[M], sd[M];
 #pragma unroll
         for (int mm = 0; mm < M; ++mm) acc[mm] = 0.0f;
 #pragma unroll
@@ -529,7 +533,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
 #pragma unroll
             for (int mm = 0; mm < M; ++mm) acc[mm] += q < nq && m == mm ? t : 0.0f;
         }
-        block_sum(acc, mean);
+        block_sum(acc, mean, red[0]);
 #pragma unroll
         for (int mm = 0; mm < M; ++mm) {
             mean[mm] = mean[mm] / (float)K;
@@ -549,7 +553,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
 #pragma unroll
             for (int mm = 0; mm < M; ++mm) acc[mm] += q < nq && m == mm ? t : 0.0f;
         }
-        block_sum(acc, sd);
+        block_sum(acc, sd, red[1]);
 #pragma unroll
         for (int mm = 0; mm < M; ++mm) sd[mm] = sqrtf(sd[mm] / (float)K + norm.eps);
 #pragma unroll
@@ -567,25 +571,12 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
             int o0, o1;
             quarter_offsets<QT>(q & 3, o0, o1);
             const int64_t e = (int64_t)(blk - m * KB) * QK;
-            const float4 g0 = *reinterpret_cast<const float4*>(norm.gamma + e + o0);
-            const float4 g1 = *reinterpret_cast<const float4*>(norm.gamma + e + o1);
-            float4 b0 = make_float4(0.f, 0.f, 0.f, 0.f), b1 = b0;
-            if (norm.beta) {
-                b0 = *reinterpret_cast<const float4*>(norm.beta + e + o0);
-                b1 = *reinterpret_cast<const float4*>(norm.beta + e + o1);
-            }
             float g[8], bb[8];
-            if constexpr (!kByteCodes<QT>) {  // the nibble order of v
-                g[0] = g0.x; g[1] = g1.x; g[2] = g0.y; g[3] = g1.y;
-                g[4] = g0.z; g[5] = g1.z; g[6] = g0.w; g[7] = g1.w;
-                bb[0] = b0.x; bb[1] = b1.x; bb[2] = b0.y; bb[3] = b1.y;
-                bb[4] = b0.z; bb[5] = b1.z; bb[6] = b0.w; bb[7] = b1.w;
-            } else {
-                g[0] = g0.x; g[1] = g0.y; g[2] = g0.z; g[3] = g0.w;
-                g[4] = g1.x; g[5] = g1.y; g[6] = g1.z; g[7] = g1.w;
-                bb[0] = b0.x; bb[1] = b0.y; bb[2] = b0.z; bb[3] = b0.w;
-                bb[4] = b1.x; bb[5] = b1.y; bb[6] = b1.z; bb[7] = b1.w;
-            }
+            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+            order(g, *reinterpret_cast<const float4*>(norm.gamma + e + o0),
+                  *reinterpret_cast<const float4*>(norm.gamma + e + o1));
+            order(bb, norm.beta ? *reinterpret_cast<const float4*>(norm.beta + e + o0) : z,
+                  norm.beta ? *reinterpret_cast<const float4*>(norm.beta + e + o1) : z);
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[p][j] = (v[p][j] - mu) / sg * g[j] + bb[j];
         }

@@ -51,7 +51,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default="", help="comma list of extra configs to run "
-                    "(q8_gemv,batched,prefill,stack,q4_k) -- for profiling")
+                    "(q8_gemv,batched,prefill,stack,q4_k,attention) -- for profiling")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 64 MiB once (device to device) and exit: the known-size "
                     "kernel that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
@@ -207,7 +207,8 @@ def extra_configs(torch, QuantLinear, gen, stream, only):
             ts = [timer.run(call_all, reps_per_copy) / len(ws) for _ in range(3)]
         return float(np.median(ts))
 
-    want = set(only.split(",")) if only else {"q8_gemv", "batched", "prefill", "stack", "q4_k"}
+    want = set(only.split(",")) if only else {"q8_gemv", "batched", "prefill", "stack", "q4_k",
+                                              "attention"}
     if "q8_gemv" in want:
         n, k = 5632, 2048
         ws = rotate(Q8_0, n, k)
@@ -289,6 +290,36 @@ def extra_configs(torch, QuantLinear, gen, stream, only):
             "TFLOP/s": round(tf, 1), "frac_bf16": round(tf / BF16_PEAK_TFLOPS, 3),
             "us": round(ms * 1e3, 1)}
         del ws
+    if "attention" in want:
+        # decode attention over a KV cache of L positions (row f4): one new token a
+        # call, the cache truncated back to L - 1 before each; HBM-bound on the cached
+        # K and V (2 KVH L hd 4 bytes), timed per call
+        from unillm_amd import KvCache
+        for (H, KVH, D, label) in ((32, 32, 128, "llama2_7b"), (32, 8, 128, "gqa_32_8")):
+            for L in (1024, 4096):
+                kv = KvCache(KVH, D, L)
+                w = (H + 2 * KVH) * D
+                mf = max(1, 16 // (H // KVH))  # tokens a fill call: m H / KVH <= 16
+                fill = torch.empty(mf, w, device="cuda").normal_(generator=gen)
+                while kv.seq_len + mf <= L - 1:
+                    kv.attention(fill, H, stream=stream)
+                while kv.seq_len < L - 1:
+                    kv.attention(fill[:1].contiguous(), H, stream=stream)
+                q1 = torch.empty(1, w, device="cuda").normal_(generator=gen)
+                out = torch.empty(1, H * D, device="cuda")
+
+                def one():
+                    kv.truncate(L - 1)
+                    kv.attention(q1, H, out=out, stream=stream)
+
+                with torch.cuda.stream(stream):
+                    one()
+                    ms = float(np.median([timer.run(one, 20) for _ in range(3)]))
+                b = 2 * KVH * L * D * 4
+                res[f"attention_decode_{label}_L{L}"] = {
+                    "GB/s": round(b / ms / 1e6, 1), "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 3),
+                    "us": round(ms * 1e3, 2), "kv_bytes": b}
+                del kv
     if "stack" in want:
         # config 5: 32 layers (QKV, o, gate+up fused 22016, down) + Q8_0 lm_head
         shapes = [(Q4_0, 4096, 12288), (Q4_0, 4096, 4096), (Q4_0, 4096, 22016),

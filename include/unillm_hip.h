@@ -57,6 +57,7 @@ extern "C" {
 #define UNILLM_PATH_PREFILL_MFMA 3 /* prefill, LDS-staged bf16 MFMA, fp32 accumulate */
 
 typedef struct unillm_qweight unillm_qweight;
+typedef struct unillm_kv_cache unillm_kv_cache;
 
 /* Select and check the device (must be gfx950).  Replaces the device choice the
  * reference makes with `Device` (crates/runtime/src/tensor_core.rs:39-44), to
@@ -146,6 +147,37 @@ int unillm_hip_qmatmul_norm_swiglu(const unillm_qweight* w, const float* x_dev,
 
 /* Kernel path that unillm_hip_qmatmul selects for m rows (UNILLM_PATH_*). */
 int unillm_hip_select_path(const unillm_qweight* w, int64_t m);
+
+/* One decoder layer's KV cache on the device for one sequence: K and V of
+ * n_kv_heads heads, max_seq positions of head_dim f32 each (zeroed), and the
+ * RoPE frequencies of rope_theta.  Replaces LayerKVCache::with_capacity
+ * (crates/runtime/src/kv_cache.rs:46-53; its buffers are allocated on the first
+ * append there).  head_dim is 64, 128 or 256. */
+int unillm_hip_kv_cache_create(int64_t n_kv_heads, int64_t head_dim, int64_t max_seq,
+                               float rope_theta, unillm_kv_cache** out);
+int unillm_hip_kv_cache_destroy(unillm_kv_cache* c);
+/* Filled positions (LayerKVCache::seq_len, kv_cache.rs:74-76). */
+int unillm_hip_kv_cache_length(const unillm_kv_cache* c, int64_t* len);
+/* Forget the filled positions, keep the buffers (LayerKVCache::clear, kv_cache.rs:61-63). */
+int unillm_hip_kv_cache_clear(unillm_kv_cache* c);
+/* Keep the first len positions (0 <= len <= the filled length): a rolled-back
+ * step, e.g. rejected speculative tokens.  No counterpart in LayerKVCache,
+ * whose only shrink is clear(); the positions past len are rewritten by the
+ * next appends. */
+int unillm_hip_kv_cache_truncate(unillm_kv_cache* c, int64_t len);
+
+/* The attention of LlamaAttention::forward_with_cache after its projections
+ * (crates/runtime/src/models_v2/llama.rs:1044-1150) for m new tokens of one
+ * sequence: qkv_dev[m, (n_heads + 2 n_kv_heads) head_dim] holds the q, k and v
+ * projections (a fused qkv handle's output); RoPE (apply_rope_with_offset,
+ * llama.rs:827-883) at positions len .. len + m - 1, k and v appended to the
+ * cache, then softmax(q k^T / sqrt(head_dim) + causal mask) v into
+ * out_dev[m, n_heads head_dim], head h reading kv head h / (n_heads /
+ * n_kv_heads).  The cache's length grows by m.  Decode steps only:
+ * m * n_heads / n_kv_heads <= 16.  Overflow of max_seq is an error with the
+ * reference's message (kv_cache.rs:114-121). */
+int unillm_hip_attention_decode(unillm_kv_cache* c, const float* qkv_dev, int64_t m,
+                                int64_t n_heads, float* out_dev, void* stream);
 
 /* out[n, k] = dequant(W) in f32, bit-exact with GGML's to_float.  Replaces
  * `qtensor.dequantize(&device)` at crates/runtime/src/weight_loader_core.rs:579. */

@@ -50,6 +50,8 @@ def lib() -> ctypes.CDLL:
         l.oracle_dequant.argtypes = [ctypes.c_int, P, I64, I64, P]
         l.oracle_qmatmul_f64.argtypes = [ctypes.c_int, P, P, I64, I64, I64, P, ctypes.c_int]
         l.oracle_candle_qmatmul.argtypes = [ctypes.c_int, P, P, I64, I64, I64, P, ctypes.c_int]
+        l.oracle_attention_decode.argtypes = [P, I64, I64, I64, I64, ctypes.c_float, P, P, I64,
+                                              I64, P]
         l.oracle_fill_normal.argtypes = [P, I64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double]
         l.oracle_fill_normal.restype = None
         _lib = l
@@ -184,3 +186,22 @@ def random_q6_k(n: int, k: int, seed: int) -> np.ndarray:
     d = (np.abs(rng.normal(0, 1, nb)) * 2e-5 + 5e-6).astype(np.float16)
     blk[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
     return blk.reshape(n, -1)
+
+
+def attention_decode(qkv: np.ndarray, n_heads: int, n_kv_heads: int, head_dim: int,
+                     rope_theta: float, k_cache: np.ndarray, v_cache: np.ndarray,
+                     length: int) -> np.ndarray:
+    """Decode attention with a KV cache (oracle.h): RoPE, append (k_cache / v_cache
+    [KVH, max_seq, hd] f32, updated in place), causal softmax attention in f64.
+    Returns out [m, H * hd] (f64)."""
+    qkv = np.ascontiguousarray(qkv, dtype=np.float32)
+    m = qkv.shape[0]
+    assert k_cache.flags["C_CONTIGUOUS"] and v_cache.flags["C_CONTIGUOUS"]
+    assert k_cache.dtype == np.float32 and v_cache.dtype == np.float32
+    out = np.empty((m, n_heads * head_dim), dtype=np.float64)
+    rc = lib().oracle_attention_decode(_ptr(qkv), m, n_heads, n_kv_heads, head_dim,
+                                       float(rope_theta), _ptr(k_cache), _ptr(v_cache),
+                                       k_cache.shape[1], length, _ptr(out))
+    if rc != 0:
+        raise ValueError("oracle_attention_decode rejected its arguments")
+    return out

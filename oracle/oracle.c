@@ -357,3 +357,70 @@ void oracle_fill_normal(float* out, int64_t count, uint64_t seed, double mean, d
         if (i + 1 < count) out[i + 1] = (float)(mean + std * r * sin(two_pi * u2));
     }
 }
+
+/* ---- decode attention (see oracle.h) --------------------------------------------------- */
+int oracle_attention_decode(const float* qkv, int64_t m, int64_t n_heads, int64_t n_kv_heads,
+                            int64_t head_dim, float rope_theta, float* k_cache, float* v_cache,
+                            int64_t max_seq, int64_t len, double* out) {
+    if (m < 0 || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads || head_dim <= 0 ||
+        head_dim % 2 || len < 0 || len + m > max_seq)
+        return -1;
+    const int64_t H = n_heads, KVH = n_kv_heads, D = head_dim, half = D / 2;
+    const int64_t row = (H + 2 * KVH) * D, groups = H / KVH;
+    /* inv_freq and the angles in f32, as apply_rope_with_offset builds them */
+    float* inv = (float*)malloc(sizeof(float) * (size_t)half);
+    for (int64_t i = 0; i < half; ++i) inv[i] = 1.0f / powf(rope_theta, (float)(2 * i) / (float)D);
+    double* q = (double*)malloc(sizeof(double) * (size_t)(m * H * D));
+    for (int64_t t = 0; t < m; ++t) {
+        const float pos = (float)(len + t);
+        const float* r = qkv + t * row;
+        for (int64_t h = 0; h < H + KVH; ++h) {  /* q heads, then k heads */
+            const float* x = r + h * D;
+            for (int64_t i = 0; i < half; ++i) {
+                const float ang = pos * inv[i];
+                const double c = cos((double)ang), sn = sin((double)ang);
+                const double a = x[i], b = x[i + half];
+                const double r1 = a * c - b * sn, r2 = a * sn + b * c;
+                if (h < H) {
+                    q[(t * H + h) * D + i] = r1;
+                    q[(t * H + h) * D + i + half] = r2;
+                } else {
+                    float* kc = k_cache + ((h - H) * max_seq + len + t) * D;
+                    kc[i] = (float)r1;
+                    kc[i + half] = (float)r2;
+                }
+            }
+        }
+        for (int64_t g = 0; g < KVH; ++g)  /* v: no rotation */
+            memcpy(v_cache + (g * max_seq + len + t) * D, r + (H + KVH + g) * D,
+                   sizeof(float) * (size_t)D);
+    }
+    const double scale = 1.0 / sqrt((double)D);
+    double* sc = (double*)malloc(sizeof(double) * (size_t)(len + m));
+    for (int64_t t = 0; t < m; ++t)
+        for (int64_t h = 0; h < H; ++h) {
+            const int64_t g = h / groups, n = len + t + 1;  /* causal: positions 0 .. len + t */
+            const double* qh = q + (t * H + h) * D;
+            double mx = -INFINITY;
+            for (int64_t j = 0; j < n; ++j) {
+                const float* kj = k_cache + (g * max_seq + j) * D;
+                double s = 0.0;
+                for (int64_t i = 0; i < D; ++i) s += qh[i] * (double)kj[i];
+                sc[j] = s * scale;
+                if (sc[j] > mx) mx = sc[j];
+            }
+            double z = 0.0;
+            for (int64_t j = 0; j < n; ++j) z += (sc[j] = exp(sc[j] - mx));
+            double* o = out + (t * H + h) * D;
+            for (int64_t i = 0; i < D; ++i) o[i] = 0.0;
+            for (int64_t j = 0; j < n; ++j) {
+                const float* vj = v_cache + (g * max_seq + j) * D;
+                const double p = sc[j] / z;
+                for (int64_t i = 0; i < D; ++i) o[i] += p * (double)vj[i];
+            }
+        }
+    free(sc);
+    free(q);
+    free(inv);
+    return 0;
+}

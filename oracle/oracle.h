@@ -93,6 +93,19 @@ int oracle_qmatmul_f64(int qtype, const uint8_t* blocks, const float* x,
 int oracle_candle_qmatmul(int qtype, const uint8_t* blocks, const float* x,
                           int64_t m, int64_t n, int64_t k, float* y, int nthreads);
 
+/* Decode attention with a KV cache (LlamaAttention::forward_with_cache,
+ * crates/runtime/src/models_v2/llama.rs:1044-1150; LayerKVCache::append,
+ * crates/runtime/src/kv_cache.rs:91-130):
+ *   qkv[m, (H + 2 KVH) hd]: the fused q / k / v projections of m new tokens;
+ *   RoPE (apply_rope_with_offset, llama.rs:827-883: half-split rotation,
+ *   inv_freq = 1 / theta^(2i / hd) and angle = pos * inv_freq in f32) at
+ *   positions len .. len + m - 1; k, v appended to k_cache / v_cache
+ *   ([KVH][max_seq][hd], updated in place); head h reads kv head h / (H / KVH);
+ *   out[m, H hd] = softmax(q k^T / sqrt(hd) + causal mask) v, in f64. */
+int oracle_attention_decode(const float* qkv, int64_t m, int64_t n_heads, int64_t n_kv_heads,
+                            int64_t head_dim, float rope_theta, float* k_cache, float* v_cache,
+                            int64_t max_seq, int64_t len, double* out);
+
 /* deterministic N(mean, std) generator: SplitMix64 -> Box-Muller (f64) -> f32 */
 void oracle_fill_normal(float* out, int64_t count, uint64_t seed, double mean, double std);
 

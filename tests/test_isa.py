@@ -23,7 +23,7 @@ import pytest
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "..", "unillm_amd", "csrc")
-SOURCES = ["decode.hip", "prefill.hip", "gemv.hip", "weights.hip"]
+SOURCES = ["decode.hip", "prefill.hip", "gemv.hip", "weights.hip", "attention.hip"]
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Xclang", "-target-feature",
          "-Xclang", "-packed-fp32-ops", "-S", "--cuda-device-only"]
 

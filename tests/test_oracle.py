@@ -404,3 +404,88 @@ def test_k_quants_rejected_by_q8_paths():
         oracle.quantize(Q4_K, w)
     with pytest.raises(ValueError):
         oracle.candle_qmatmul(Q4_K, oracle.random_q4_k(1, 256, 0), w, 1, 256)
+
+
+# ---- decode attention with a KV cache (llama.rs:827-883, 1044-1150) --------------------------
+
+def _attn(qkv, H, KVH, D, theta=10000.0, max_seq=64, length=0, k=None, v=None):
+    k = np.zeros((KVH, max_seq, D), np.float32) if k is None else k
+    v = np.zeros((KVH, max_seq, D), np.float32) if v is None else v
+    out = oracle.attention_decode(qkv, H, KVH, D, theta, k, v, length)
+    return out, k, v
+
+
+def test_attention_single_position_returns_v():
+    H, KVH, D = 4, 2, 8
+    qkv = oracle.normal((H + 2 * KVH) * D, seed=1).reshape(1, -1)
+    out, _, _ = _attn(qkv, H, KVH, D)
+    vv = qkv[0, (H + KVH) * D:].reshape(KVH, D)
+    for h in range(H):  # softmax over one position is 1; head h reads kv head h // 2
+        assert np.array_equal(out[0, h * D:(h + 1) * D], vv[h // 2].astype(np.float64))
+
+
+def test_attention_equal_keys_average_values():
+    # every cached key the same: uniform weights, out = mean of the values seen
+    H, KVH, D, L = 2, 1, 8, 5
+    k = np.zeros((KVH, 16, D), np.float32)
+    v = np.zeros((KVH, 16, D), np.float32)
+    v[0, :L] = oracle.normal(L * D, seed=2).reshape(L, D)
+    qkv = oracle.normal((H + 2 * KVH) * D, seed=3).reshape(1, -1)
+    qkv[0, H * D:(H + KVH) * D] = 0.0  # the new key: 0, like the cached ones
+    out, k, v = _attn(qkv, H, KVH, D, max_seq=16, length=L, k=k, v=v)
+    want = v[0, :L + 1].astype(np.float64).mean(axis=0)
+    for h in range(H):
+        np.testing.assert_allclose(out[0, h * D:(h + 1) * D], want, rtol=1e-12, atol=1e-12)
+
+
+def test_rope_known_answers_and_pairing():
+    # pos 0: identity.  A unit vector at dim i of a key at position p lands on dims i
+    # (cos) and i + D/2 (sin) at angle p * inv_freq[i], inv_freq in f32 as the reference
+    H, KVH, D, theta = 1, 1, 8, 10000.0
+    m = 6
+    qkv = np.zeros((m, (H + 2 * KVH) * D), np.float32)
+    kk = oracle.normal(D, seed=4)
+    qkv[0, H * D:(H + 1) * D] = kk
+    for t in range(1, m):
+        qkv[t, H * D + (t - 1) % (D // 2)] = 1.0
+    _, k, _ = _attn(qkv, H, KVH, D, theta=theta)
+    assert np.array_equal(k[0, 0], kk)
+    for t in range(1, m):
+        i = (t - 1) % (D // 2)
+        ang = np.float32(t) * np.float32(1.0 / np.power(np.float32(theta), np.float32(2 * i) / np.float32(D)))
+        want = np.zeros(D, np.float32)
+        want[i], want[i + D // 2] = np.cos(np.float64(ang)), np.sin(np.float64(ang))
+        np.testing.assert_allclose(k[0, t], want, atol=1e-7)
+
+
+def test_rope_relative_position_invariant():
+    # the same key content at positions 0 .. N-1: <K_j, K_j+s> depends on s only
+    H, KVH, D, N = 1, 1, 16, 12
+    qkv = np.zeros((N, (H + 2 * KVH) * D), np.float32)
+    qkv[:, H * D:(H + 1) * D] = oracle.normal(D, seed=5)
+    _, k, _ = _attn(qkv, H, KVH, D, theta=100.0)
+    K = k[0, :N].astype(np.float64)
+    for s in range(1, 4):
+        d = [K[j] @ K[j + s] for j in range(N - s)]
+        np.testing.assert_allclose(d, d[0], rtol=1e-5)
+    np.testing.assert_allclose(np.linalg.norm(K, axis=1), np.linalg.norm(K[0]), rtol=1e-6)
+
+
+def test_attention_causal_and_gqa_heads():
+    # two new tokens: token 0 must not see token 1's key / value
+    H, KVH, D = 4, 2, 8
+    qkv = oracle.normal(2 * (H + 2 * KVH) * D, seed=6).reshape(2, -1)
+    out_a, _, _ = _attn(qkv, H, KVH, D, length=3,
+                        k=oracle.normal(2 * 64 * D, seed=7).reshape(2, 64, D).copy(),
+                        v=oracle.normal(2 * 64 * D, seed=8).reshape(2, 64, D).copy())
+    qkv2 = qkv.copy()
+    qkv2[1, H * D:] = 1e3  # token 1's k and v only
+    out_b, _, _ = _attn(qkv2, H, KVH, D, length=3,
+                        k=oracle.normal(2 * 64 * D, seed=7).reshape(2, 64, D).copy(),
+                        v=oracle.normal(2 * 64 * D, seed=8).reshape(2, 64, D).copy())
+    assert np.array_equal(out_a[0], out_b[0]) and not np.allclose(out_a[1], out_b[1])
+
+
+def test_attention_overflow_rejected():
+    with pytest.raises(ValueError):
+        _attn(np.zeros((3, 4 * 8), np.float32), 2, 1, 8, max_seq=4, length=2)

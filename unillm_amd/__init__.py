@@ -14,7 +14,7 @@ __all__ = [
     "BLOCK_BYTES", "BLOCK_ELEMS", "ERR_HIP", "ERR_INVALID_ARG", "ERR_UNSUPPORTED", "OK", "PATH_AUTO",
     "PATH_DECODE_MFMA", "PATH_GEMV", "PATH_PREFILL_MFMA", "QK", "Q4_0", "Q4_K", "Q6_K", "Q8_0",
     "HipError",
-    "QuantLinear", "quantize_blocks",
+    "QuantLinear", "quantize_blocks", "KvCache",
 ]
 
 
@@ -23,4 +23,7 @@ def __getattr__(name):
     if name in ("QuantLinear", "quantize_blocks"):
         from . import quant_linear
         return getattr(quant_linear, name)
+    if name == "KvCache":
+        from . import attention
+        return attention.KvCache
     raise AttributeError(name)

@@ -63,6 +63,12 @@ SIGNATURES = {
     "unillm_hip_qmatmul_add": ([P, P, I64, P, P], ctypes.c_int),
     "unillm_hip_qmatmul_swiglu": ([P, P, I64, P, P], ctypes.c_int),
     "unillm_hip_qmatmul_norm": ([P, P, P, P, ctypes.c_float, I64, P, P], ctypes.c_int),
+    "unillm_hip_kv_cache_create": ([I64, I64, I64, ctypes.c_float, P], ctypes.c_int),
+    "unillm_hip_kv_cache_destroy": ([P], ctypes.c_int),
+    "unillm_hip_kv_cache_length": ([P, P], ctypes.c_int),
+    "unillm_hip_kv_cache_clear": ([P], ctypes.c_int),
+    "unillm_hip_kv_cache_truncate": ([P, I64], ctypes.c_int),
+    "unillm_hip_attention_decode": ([P, P, I64, I64, P, P], ctypes.c_int),
     "unillm_hip_qmatmul_norm_swiglu": ([P, P, P, P, ctypes.c_float, I64, P, P], ctypes.c_int),
     "unillm_hip_select_path": ([P, I64], ctypes.c_int),
     "unillm_hip_dequant": ([P, P, P], ctypes.c_int),

@@ -23,7 +23,7 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libunillm_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["capi.hip", "weights.hip", "gemv.hip", "decode.hip", "prefill.hip"]
+SOURCES = ["capi.hip", "weights.hip", "gemv.hip", "decode.hip", "prefill.hip", "attention.hip"]
 HOST_SOURCES = ["gguf.cpp", "unillm_host.cpp"]
 HOST_LIB = os.path.join(HERE, "libunillm_host.so")
 HOST_TEST = os.path.join(os.path.dirname(HERE), "tests", "cpp", "test_host")

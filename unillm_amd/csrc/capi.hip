@@ -10,6 +10,7 @@
 #include <new>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include <hip/hip_fp16.h>
 #include <math.h>
@@ -436,6 +437,104 @@ int unillm_hip_quantize(int qtype, const float* w_dev, int64_t n, int64_t k, voi
     hipError_t e = launch_quantize(qtype, w_dev, n, k, static_cast<uint8_t*>(blocks_dev),
                                    static_cast<hipStream_t>(stream));
     return e == hipSuccess ? UNILLM_OK : fail_hip(e, "quantize launch");
+}
+
+int unillm_hip_kv_cache_create(int64_t n_kv_heads, int64_t head_dim, int64_t max_seq,
+                               float rope_theta, unillm_kv_cache** out) {
+    if (!out) return fail(UNILLM_ERR_INVALID_ARG, "out is NULL");
+    *out = nullptr;
+    if (n_kv_heads < 1 || max_seq < 1 || !(head_dim == 64 || head_dim == 128 || head_dim == 256) ||
+        !(rope_theta > 0.0f) || n_kv_heads * max_seq * head_dim > ((int64_t)1 << 31))
+        return fail(UNILLM_ERR_INVALID_ARG,
+                    "KV cache: need n_kv_heads >= 1, head_dim 64 / 128 / 256, max_seq >= 1, "
+                    "rope_theta > 0 and under 2^31 elements per buffer");
+    if (int rc = ensure_init()) return rc;
+    unillm_kv_cache* c = new (std::nothrow) unillm_kv_cache{};
+    if (!c) return fail(UNILLM_ERR_OUT_OF_MEMORY, "host allocation failed");
+    c->device = g_device;
+    c->n_kv_heads = n_kv_heads;
+    c->head_dim = head_dim;
+    c->max_seq = max_seq;
+    c->rope_theta = rope_theta;
+    const size_t buf = (size_t)(n_kv_heads * max_seq * head_dim) * sizeof(float);
+    // inv_freq[i] = 1 / theta^(2 i / hd) in f32, as apply_rope_with_offset computes it
+    // (crates/runtime/src/models_v2/llama.rs:839-841)
+    std::vector<float> inv((size_t)head_dim / 2);
+    for (size_t i = 0; i < inv.size(); ++i)
+        inv[i] = 1.0f / powf(rope_theta, (float)(2 * i) / (float)head_dim);
+    hipError_t e;
+    void *k = nullptr, *v = nullptr, *f = nullptr;
+    if ((e = hipMalloc(&k, buf)) != hipSuccess || (e = hipMalloc(&v, buf)) != hipSuccess ||
+        (e = hipMalloc(&f, inv.size() * sizeof(float))) != hipSuccess ||
+        (e = hipMemset(k, 0, buf)) != hipSuccess || (e = hipMemset(v, 0, buf)) != hipSuccess ||
+        (e = hipMemcpy(f, inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice)) !=
+            hipSuccess) {
+        (void)hipFree(k);
+        (void)hipFree(v);
+        (void)hipFree(f);
+        delete c;
+        return e == hipErrorOutOfMemory ? fail(UNILLM_ERR_OUT_OF_MEMORY, "KV cache allocation")
+                                        : fail_hip(e, "KV cache allocation");
+    }
+    c->k = static_cast<float*>(k);
+    c->v = static_cast<float*>(v);
+    c->inv_freq = static_cast<float*>(f);
+    *out = c;
+    return UNILLM_OK;
+}
+
+int unillm_hip_kv_cache_destroy(unillm_kv_cache* c) {
+    if (!c) return UNILLM_OK;
+    hipError_t e = hipFree(c->k), e2 = hipFree(c->v), e3 = hipFree(c->inv_freq);
+    delete c;
+    if (e == hipSuccess) e = e2;
+    if (e == hipSuccess) e = e3;
+    return e == hipSuccess ? UNILLM_OK : fail_hip(e, "hipFree (KV cache)");
+}
+
+int unillm_hip_kv_cache_length(const unillm_kv_cache* c, int64_t* len) {
+    if (!c || !len) return fail(UNILLM_ERR_INVALID_ARG, "cache or len is NULL");
+    *len = c->len;
+    return UNILLM_OK;
+}
+
+int unillm_hip_kv_cache_clear(unillm_kv_cache* c) {
+    if (!c) return fail(UNILLM_ERR_INVALID_ARG, "cache is NULL");
+    c->len = 0;
+    return UNILLM_OK;
+}
+
+int unillm_hip_kv_cache_truncate(unillm_kv_cache* c, int64_t len) {
+    if (!c) return fail(UNILLM_ERR_INVALID_ARG, "cache is NULL");
+    if (len < 0 || len > c->len)
+        return fail(UNILLM_ERR_INVALID_ARG, "KV cache truncate: length " + std::to_string(len) +
+                                                " outside [0, " + std::to_string(c->len) + "]");
+    c->len = len;
+    return UNILLM_OK;
+}
+
+int unillm_hip_attention_decode(unillm_kv_cache* c, const float* qkv_dev, int64_t m,
+                                int64_t n_heads, float* out_dev, void* stream) {
+    if (!c || !qkv_dev || !out_dev)
+        return fail(UNILLM_ERR_INVALID_ARG, "attention: cache, qkv or out is NULL");
+    if (m < 1 || n_heads < c->n_kv_heads || n_heads % c->n_kv_heads != 0)
+        return fail(UNILLM_ERR_INVALID_ARG,
+                    "attention: need m >= 1 and n_heads a multiple of n_kv_heads");
+    if (m * (n_heads / c->n_kv_heads) > attention_max_queries())
+        return fail(UNILLM_ERR_UNSUPPORTED,
+                    "attention: m * n_heads / n_kv_heads must be <= " +
+                        std::to_string(attention_max_queries()) + " (decode steps)");
+    if (c->len + m > c->max_seq)  // LayerKVCache::append's check (kv_cache.rs:114-121)
+        return fail(UNILLM_ERR_INVALID_ARG,
+                    "KV cache append failed: KV cache overflow: current_len=" +
+                        std::to_string(c->len) + ", new_len=" + std::to_string(m) +
+                        ", max_seq_len=" + std::to_string(c->max_seq));
+    if (int rc = ensure_init()) return rc;
+    hipError_t e = launch_attention_decode(*c, qkv_dev, m, n_heads, out_dev,
+                                           static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail_hip(e, "attention launch");
+    c->len += m;  // the kernels run in stream order: later calls see the appended rows
+    return UNILLM_OK;
 }
 
 int unillm_hip_malloc(void** ptr, size_t bytes) {

@@ -48,6 +48,18 @@ struct unillm_qweight {
     int f16_exp;           // smallest E with max|q d| 2^-E <= 65504 (f16 range)
 };
 
+// The opaque KV-cache handle (one decoder layer, one sequence): K and V of
+// n_kv_heads heads, [n_kv_heads][max_seq][head_dim] f32 each, the first len
+// positions filled; inv_freq[head_dim / 2] the RoPE frequencies in f32.
+struct unillm_kv_cache {
+    int device;
+    int64_t n_kv_heads, head_dim, max_seq, len;
+    float rope_theta;
+    float* k;
+    float* v;
+    float* inv_freq;
+};
+
 namespace unillm {
 
 constexpr int QK = 32;  // weights per block
@@ -129,7 +141,8 @@ const DeviceInfo& device_info();
 // memory is held until the process ends.  Calls on one stream from several
 // host threads are ordered by the stream, the map by a mutex.
 // Slot 0 holds x in the MFMA paths' operand type; slot 1 the [gate | up] outputs
-// of a SwiGLU call off the GEMV path (both live during that call).
+// of a SwiGLU call off the GEMV path (both live during that call); slot 2 the
+// rotated queries and the per-chunk partials of decode attention.
 hipError_t stream_workspace(hipStream_t s, size_t bytes, void** out, int slot = 0);
 // UNILLM_DEBUG_LAUNCH=1 prints each kernel's launch shape to stderr.
 bool debug_launch();
@@ -161,6 +174,14 @@ hipError_t launch_norm_convert(const float* x, int64_t m, int64_t k, const NormA
 // act[m, I] = silu(g[m, i]) * u[m, i] with g, u the two halves of each row of
 // gu[m, 2 I] (the SwiGLU of the MFMA paths, after their store)
 hipError_t launch_swiglu(const float* gu, int64_t m, int64_t I, float* act, hipStream_t s);
+
+// Decode attention (attention.hip): RoPE at positions len .. len + m - 1 on the
+// fused QKV rows qkv[m, (H + 2 KVH) hd], k / v appended to the cache, causal
+// softmax attention into out[m, H hd]; the caller advances len.
+using KvCache = ::unillm_kv_cache;
+hipError_t launch_attention_decode(const KvCache& kv, const float* qkv, int64_t m, int64_t H,
+                                   float* out, hipStream_t s);
+int attention_max_queries();  // m * H / KVH per call
 
 constexpr int64_t kGemvMaxM = 4;
 constexpr int64_t kDecodeMaxM = 64;

@@ -314,11 +314,22 @@ def extra_configs(torch, QuantLinear, gen, stream, only):
 
                 with torch.cuda.stream(stream):
                     one()
-                    ms = float(np.median([timer.run(one, 20) for _ in range(3)]))
+                    eager = float(np.median([timer.run(one, 20) for _ in range(3)]))
+                    # the same 20 calls captured once and replayed (as a decode step
+                    # would run them): each captured call has the length truncate()
+                    # set on the host, L - 1, so a replay repeats exactly those calls
+                    g = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
+                        for _ in range(20):
+                            one()
+                    kv.truncate(L - 1)
+                    g.replay()
+                    ms = float(np.median([timer.run(g.replay, 1) for _ in range(5)])) / 20
+                    del g
                 b = 2 * KVH * L * D * 4
                 res[f"attention_decode_{label}_L{L}"] = {
                     "GB/s": round(b / ms / 1e6, 1), "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 3),
-                    "us": round(ms * 1e3, 2), "kv_bytes": b}
+                    "us": round(ms * 1e3, 2), "eager_us": round(eager * 1e3, 2), "kv_bytes": b}
                 del kv
     if "stack" in want:
         # config 5: 32 layers (QKV, o, gate+up fused 22016, down) + Q8_0 lm_head

@@ -1,4 +1,4 @@
-// attention.hip -- decode attention with a KV cache in HBM (m new tokens, m <= 16).
+// attention.hip -- decode attention with a KV cache in HBM (m new tokens, m H / KVH <= 16).
 //
 // What it computes: LlamaAttention::forward_with_cache after the projections
 // (crates/runtime/src/models_v2/llama.rs:1044-1150): RoPE on q and k at the
@@ -11,19 +11,26 @@
 // Bound: HBM -- the cached K and V are read once per step (2 KVH len hd 4 bytes,
 // f32 like the reference's cache).
 //
-// Three kernels on the caller's stream:
-//   1. rope_append_kernel: one wave per (token, head) of the fused QKV row:
-//      q heads rotated into the workspace, k heads rotated into the cache, v
-//      heads copied into it.
-//   2. attn_chunk_kernel: a workgroup per (kv head, chunk of C positions); its
-//      four waves split the chunk, each lane holding hd / 64 dimensions of a
-//      position's k and v, and run an online softmax for every query that
-//      reads this kv head (the m tokens times the H / KVH heads of the group),
-//      so each cached k and v is read from HBM once per step.  The waves'
-//      (max, sum, weighted v) meet in LDS; the chunk's triple goes to the
-//      workspace.
-//   3. attn_merge_kernel: per (token, head), the chunks' triples merged by
-//      log-sum-exp into the output row [m, H hd].
+// One kernel on the caller's stream, a workgroup per (kv head g, chunk c of C
+// positions), 256 threads:
+//   1. the Q = m G queries of kv head g (the m tokens times the G = H / KVH heads
+//      of the group): RoPE at position len + t, times 1 / sqrt(hd), into LDS;
+//   2. the new positions len .. len + m - 1 inside this chunk: k rotated and v
+//      into LDS, and appended to the cache (each position lies in exactly one
+//      chunk, so exactly one workgroup writes it; the scores read these
+//      positions from LDS, never back from the cache);
+//   3. scores: LP = hd / 8 lanes per position, each with 8 dimensions of k and of
+//      every query in registers (256 / LP positions at a time), the dot reduced
+//      over the LP lanes by DPP; causal mask; into LDS;
+//   4. per query (a wave each), the chunk's max and the exponentials and their sum;
+//   5. p v: a float4 of dimensions per thread, positions split over 256 / (hd / 4)
+//      thread groups, the groups' sums meeting by LDS atomic adds;
+//   6. the chunk's (max, sum, o[hd]) per query to the workspace.  The last
+//      workgroup of kv head g to finish (an arrival counter per kv head, which
+//      that workgroup resets to zero for the next call) merges the chunks of
+//      its queries by log-sum-exp into the output rows [m, H hd].
+// Everything a step reads from HBM beyond the cache is the m qkv rows and the
+// per-chunk triples (chunks (hd + 2) floats per query).
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -37,34 +44,9 @@ namespace unillm {
 namespace {
 
 constexpr int kAttnMaxQ = 16;  // queries per kv head in one call: m * H / KVH
-
-// rotation of the pair (x[i], x[i + hd / 2]) by pos * inv_freq[i]; lanes past hd / 2 idle
-__global__ __launch_bounds__(128) void rope_append_kernel(const float* __restrict__ qkv, int H,
-                                                          int KVH, int D,
-                                                          const float* __restrict__ inv_freq,
-                                                          int len, float* __restrict__ q_out,
-                                                          float* __restrict__ kc,
-                                                          float* __restrict__ vc, int max_seq) {
-    const int t = blockIdx.x, h = blockIdx.y;  // token, head of the row (q, then k, then v)
-    const int half = D / 2;
-    const float* x = qkv + (int64_t)t * (H + 2 * KVH) * D + (int64_t)h * D;
-    const int pos = len + t;
-    if (h >= H + KVH) {  // v: copied
-        float* dst = vc + ((int64_t)(h - H - KVH) * max_seq + pos) * D;
-        for (int i = threadIdx.x; i < D; i += blockDim.x) dst[i] = x[i];
-        return;
-    }
-    float* dst = h < H ? q_out + ((int64_t)t * H + h) * D
-                       : kc + ((int64_t)(h - H) * max_seq + pos) * D;
-    for (int i = threadIdx.x; i < half; i += blockDim.x) {
-        const float ang = (float)pos * inv_freq[i];
-        float sn, cs;
-        sincosf(ang, &sn, &cs);
-        const float a = x[i], b = x[i + half];
-        dst[i] = a * cs - b * sn;
-        dst[i + half] = a * sn + b * cs;
-    }
-}
+constexpr int kThreads = 256;
+constexpr int kMaxChunk = 256;   // positions per workgroup
+constexpr int kMaxChunks = 512;  // workgroups per kv head (L <= 131072)
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
@@ -72,220 +54,367 @@ __device__ __forceinline__ float dpp(float v) {
         float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_rows(float v) {  // rows outside ROW_MASK read 0
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                         0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, false));
-}
-
-// Sum over the 64 lanes, all in DPP (no LDS): each 16-lane row sums itself, then
-// row_bcast:15 adds row 0 into row 1 and row 2 into row 3, row_bcast:31 rows 0-1
-// into rows 2-3; lane 63 holds the total, read into a scalar for every lane.
-__device__ __forceinline__ float wave_sum64(float v) {
+// Sum over aligned groups of LP lanes (8, 16 or 32); every lane of a group gets it.
+template <int LP>
+__device__ __forceinline__ float group_sum(float v) {
     v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
-    v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
-    v += dpp<0x124>(v);  // row_ror:4
-    v += dpp<0x128>(v);  // row_ror:8 -> every lane holds its row's sum
-    v += dpp_rows<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
-    v += dpp_rows<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+    v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]: quad sums
+    v += dpp<0x141>(v);  // row_half_mirror: lane i + lane 7 - i of each 8 -> 8-lane sums
+    if constexpr (LP >= 16) v += dpp<0x140>(v);  // row_mirror: lane i + lane 15 - i
+    if constexpr (LP >= 32) v += __shfl_xor(v, 16, 64);
+    return v;
 }
 
-// Workgroup (g, c): kv head g, positions [c C, min((c + 1) C, L)).  Queries of
-// kv head g: token t, head h = g G + e (e < G) -> query qi = t G + e (Q = m G <=
-// QB), whose causal limit is position len + t.  DPL = hd / 64 dimensions per
-// lane; each wave takes U consecutive positions at a time (all their k and v
-// requested before any is used), the four waves interleaved by U.
-template <int DPL, int QB>
-__global__ __launch_bounds__(256) void attn_chunk_kernel(const float* __restrict__ q, int m, int H,
-                                                         int KVH, int len, int C, int chunks,
-                                                         float scale, const float* __restrict__ kc,
-                                                         const float* __restrict__ vc, int max_seq,
-                                                         float* __restrict__ part) {
-    constexpr int D = 64 * DPL, U = 8;
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_add(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Dynamic LDS (floats): qs[QB][D] | nk[m][D] | nv[m][D] | sp[QB][max(C, chunks)] (the scores,
+// then the merge's weights) | red[4][QB][D] | stat[QB][2]
+template <int D, int QB>
+__global__ __launch_bounds__(kThreads) void attn_decode_kernel(
+    const float* __restrict__ qkv, int m, int H, int KVH, int len, int C, int chunks, float scale,
+    const float* __restrict__ inv_freq, float* __restrict__ kc, float* __restrict__ vc,
+    int max_seq, float* __restrict__ part, uint32_t* __restrict__ arrivals,
+    float* __restrict__ out) {
+    constexpr int LP = D / 8;             // lanes per position in the score pass
+    constexpr int SG = kThreads / LP;     // positions at a time (32, 16, 8)
+    constexpr int D4 = D / 4;             // float4 columns in the p v pass
+    constexpr int NG = kThreads / D4;     // position groups in the p v pass (16, 8, 4)
+    constexpr int HALF = D / 2;
     const int g = blockIdx.x, c = blockIdx.y;
     const int G = H / KVH, Q = m * G;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int L = len + m;
-    const int j0 = c * C, j1 = min(j0 + C, L);
-    __shared__ float wred[4][QB][2];
-    __shared__ float wo[4][QB * D];
-    float qv[QB][DPL];  // this lane's dims of every query, pre-scaled by 1 / sqrt(hd)
-#pragma unroll
-    for (int qi = 0; qi < QB; ++qi)
-#pragma unroll
-        for (int d = 0; d < DPL; ++d) {
-            const int t = min(qi, Q - 1) / G, e = min(qi, Q - 1) % G;
-            qv[qi][d] = q[((int64_t)t * H + g * G + e) * D + d * 64 + lane] * scale;
-        }
-    float mx[QB], sm[QB], o[QB][DPL];
-#pragma unroll
-    for (int qi = 0; qi < QB; ++qi) {
-        mx[qi] = -INFINITY;
-        sm[qi] = 0.0f;
-#pragma unroll
-        for (int d = 0; d < DPL; ++d) o[qi][d] = 0.0f;
-    }
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int j0 = c * C, j1 = min(j0 + C, len + m);
+    const int n = j1 - j0;
+    const int64_t W = (int64_t)(H + 2 * KVH) * D;  // floats per qkv row
+    extern __shared__ __attribute__((aligned(16))) float sm[];
+    float* qs = sm;
+    float* nk = qs + QB * D;
+    float* nv = nk + m * D;
+    float* sp = nv + m * D;
+    float* red = sp + QB * max(C, chunks);
+    float* stat = red + 4 * QB * D;
+    __shared__ uint32_t is_last;
     const float* kg = kc + (int64_t)g * max_seq * D;
     const float* vg = vc + (int64_t)g * max_seq * D;
-    for (int jb = j0 + U * wv; jb < j1; jb += 4 * U) {
-        float kj[U][DPL], vj[U][DPL];
+
+    // score pass: group sg = tid / LP takes positions j0 + sg + SG u (+ UK SG per
+    // iteration), lane l8 = tid % LP dimensions 8 l8 .. 8 l8 + 7; p v pass: group
+    // pg = tid / D4 takes positions j0 + pg + NG u (+ UV NG per iteration), column
+    // c4 = tid % D4.  Cached positions (< len) come from HBM, requested one iteration
+    // ahead; the first iteration's k and v are requested before anything else, with
+    // the queries.  Positions >= len (new in this call) are read from LDS at use.
+    constexpr int UK = QB >= 8 ? 2 : 4, UV = QB >= 8 ? 4 : 8;
+    const int sg = tid / LP, l8 = tid % LP;
+    const int pg = tid / D4, c4 = tid % D4;
+    const int nit_k = (n + UK * SG - 1) / (UK * SG), nit_v = (n + UV * NG - 1) / (UV * NG);
+    auto load_k = [&](float (&kr)[UK][8], int it) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t j = min(jb + u, j1 - 1);  // past the chunk: a repeat, skipped below
-#pragma unroll
-            for (int d = 0; d < DPL; ++d) {
-                kj[u][d] = kg[j * D + d * 64 + lane];
-                vj[u][d] = vg[j * D + d * 64 + lane];
-            }
+        for (int u = 0; u < UK; ++u) {
+            const int j = j0 + min(it * UK * SG + sg + u * SG, n - 1);
+            const float* src = kg + (int64_t)(j < len ? j : 0) * D + 8 * l8;  // branch-free
+            const float4 a = *reinterpret_cast<const float4*>(src);
+            const float4 b = *reinterpret_cast<const float4*>(src + 4);
+            kr[u][0] = a.x; kr[u][1] = a.y; kr[u][2] = a.z; kr[u][3] = a.w;
+            kr[u][4] = b.x; kr[u][5] = b.y; kr[u][6] = b.z; kr[u][7] = b.w;
         }
+    };
+    auto load_v = [&](float4 (&vr)[UV], int it) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int j = jb + u;
-            if (j >= j1) break;  // wave-uniform
+        for (int u = 0; u < UV; ++u) {
+            const int j = j0 + min(it * UV * NG + pg + u * NG, n - 1);
+            vr[u] = *reinterpret_cast<const float4*>(vg + (int64_t)(j < len ? j : 0) * D + 4 * c4);
+        }
+    };
+    float kA[UK][8], kB[UK][8];
+    float4 vA[UV], vB[UV];
+    load_k(kA, 0);
+    load_v(vA, 0);
+
+    // 1. rotated, scaled queries
+    for (int i = tid; i < Q * HALF; i += kThreads) {
+        const int qi = i / HALF, p = i - qi * HALF;
+        const int t = qi / G, e = qi - t * G;
+        const float* x = qkv + t * W + (int64_t)(g * G + e) * D;
+        float sn, cs;
+        sincosf((float)(len + t) * inv_freq[p], &sn, &cs);
+        const float a = x[p], b = x[p + HALF];
+        qs[qi * D + p] = (a * cs - b * sn) * scale;
+        qs[qi * D + p + HALF] = (a * sn + b * cs) * scale;
+    }
+    // 2. new positions [nb, j1) of this chunk: k rotated, v copied; into LDS and the cache
+    const int nb = max(j0, len);
+    for (int i = tid; i < (j1 - nb) * D; i += kThreads) {
+        const int j = nb + i / D, d = i % D, t = j - len;
+        const float* xk = qkv + t * W + (int64_t)(H + g) * D;
+        const float* xv = qkv + t * W + (int64_t)(H + KVH + g) * D;
+        const int p = d < HALF ? d : d - HALF;
+        float sn, cs;
+        sincosf((float)j * inv_freq[p], &sn, &cs);
+        const float a = xk[p], b = xk[p + HALF];
+        const float kv = d < HALF ? a * cs - b * sn : a * sn + b * cs;
+        const float vv = xv[d];
+        nk[t * D + d] = kv;
+        nv[t * D + d] = vv;
+        kc[((int64_t)g * max_seq + j) * D + d] = kv;
+        vc[((int64_t)g * max_seq + j) * D + d] = vv;
+    }
+    __syncthreads();
+
+    // 3. scores (causal mask applied), into sp
+    {
+        float qr[QB][8];
 #pragma unroll
-            for (int qi = 0; qi < QB; ++qi) {
-                if (qi >= Q || j > len + qi / G) continue;  // causal (wave-uniform)
-                float sv = 0.0f;
+        for (int qi = 0; qi < QB; ++qi) {
+            const float4 a = *reinterpret_cast<const float4*>(qs + min(qi, Q - 1) * D + 8 * l8);
+            const float4 b = *reinterpret_cast<const float4*>(qs + min(qi, Q - 1) * D + 8 * l8 + 4);
+            qr[qi][0] = a.x; qr[qi][1] = a.y; qr[qi][2] = a.z; qr[qi][3] = a.w;
+            qr[qi][4] = b.x; qr[qi][5] = b.y; qr[qi][6] = b.z; qr[qi][7] = b.w;
+        }
+        auto score = [&](float (&kr)[UK][8], int it) {
 #pragma unroll
-                for (int d = 0; d < DPL; ++d) sv = fmaf(qv[qi][d], kj[u][d], sv);
-                sv = wave_sum64(sv);
-                const float mn = fmaxf(mx[qi], sv);
-                const float a = expf(mx[qi] - mn), pw = expf(sv - mn);
-                sm[qi] = fmaf(sm[qi], a, pw);
+            for (int u = 0; u < UK; ++u) {
+                const int jl = it * UK * SG + sg + u * SG;
+                const int j = j0 + min(jl, n - 1);
+                if (j >= len) {  // a new position: its rotated k is in LDS
+                    const float4 a = *reinterpret_cast<const float4*>(nk + (j - len) * D + 8 * l8);
+                    const float4 b = *reinterpret_cast<const float4*>(nk + (j - len) * D + 8 * l8 + 4);
+                    kr[u][0] = a.x; kr[u][1] = a.y; kr[u][2] = a.z; kr[u][3] = a.w;
+                    kr[u][4] = b.x; kr[u][5] = b.y; kr[u][6] = b.z; kr[u][7] = b.w;
+                }
 #pragma unroll
-                for (int d = 0; d < DPL; ++d) o[qi][d] = fmaf(o[qi][d], a, pw * vj[u][d]);
-                mx[qi] = mn;
+                for (int qi = 0; qi < QB; ++qi) {
+                    float s = 0.0f;
+#pragma unroll
+                    for (int d = 0; d < 8; ++d) s = fmaf(qr[qi][d], kr[u][d], s);
+                    s = group_sum<LP>(s);
+                    // lane qi % LP of the group stores query qi's score
+                    if (jl < n && qi < Q && qi % LP == l8) {
+                        const bool visible = j <= len + qi / G;  // causal
+                        sp[qi * C + jl] = visible ? s : -INFINITY;
+                    }
+                }
+            }
+        };
+        for (int it = 0; it < nit_k; it += 2) {  // wave-uniform trip count
+            if (it + 1 < nit_k) load_k(kB, it + 1);
+            score(kA, it);
+            if (it + 1 < nit_k) {
+                if (it + 2 < nit_k) load_k(kA, it + 2);
+                score(kB, it + 1);
             }
         }
     }
-    // the four waves' triples -> one per query
-#pragma unroll
-    for (int qi = 0; qi < QB; ++qi) {
+    __syncthreads();
+
+    // 4. per query: the chunk's max, exponentials and their sum (a wave per query)
+    for (int qi = wv; qi < Q; qi += kThreads / 64) {
+        float mx = -INFINITY;
+        for (int jl = lane; jl < n; jl += 64) mx = fmaxf(mx, sp[qi * C + jl]);
+        mx = wave_max(mx);
+        float sum = 0.0f;
+        for (int jl = lane; jl < n; jl += 64) {
+            const float pv = mx == -INFINITY ? 0.0f : expf(sp[qi * C + jl] - mx);
+            sp[qi * C + jl] = pv;
+            sum += pv;
+        }
+        sum = wave_add(sum);
         if (lane == 0) {
-            wred[wv][qi][0] = mx[qi];
-            wred[wv][qi][1] = sm[qi];
+            stat[2 * qi] = mx;
+            stat[2 * qi + 1] = sum;
         }
-#pragma unroll
-        for (int d = 0; d < DPL; ++d) wo[wv][qi * D + d * 64 + lane] = o[qi][d];
     }
     __syncthreads();
-    const int P = 2 + D;  // floats per (query, chunk) triple: max, sum, o[D]
-    for (int i = threadIdx.x; i < Q * D; i += blockDim.x) {
-        const int qi = i / D, d = i % D;
-        float M = -INFINITY;
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, wred[w][qi][0]);
-        float S = 0.0f, O = 0.0f;
-        if (M != -INFINITY)
-            for (int w = 0; w < 4; ++w) {
-                const float f = wred[w][qi][0] == -INFINITY ? 0.0f : expf(wred[w][qi][0] - M);
-                S += wred[w][qi][1] * f;
-                O += wo[w][qi * D + d] * f;
+
+    // 5. o = p v
+    {
+        float4 o[QB];
+#pragma unroll
+        for (int qi = 0; qi < QB; ++qi) o[qi] = make_float4(0.f, 0.f, 0.f, 0.f);
+        auto accumulate = [&](float4 (&vr)[UV], int it) {
+#pragma unroll
+            for (int u = 0; u < UV; ++u) {
+                const int jl = it * UV * NG + pg + u * NG;
+                if (jl >= n) break;
+                const int j = j0 + jl;
+                if (j >= len) vr[u] = *reinterpret_cast<const float4*>(nv + (j - len) * D + 4 * c4);
+#pragma unroll
+                for (int qi = 0; qi < QB; ++qi) {
+                    if (qi >= Q) break;
+                    const float p = sp[qi * C + jl];
+                    o[qi].x = fmaf(p, vr[u].x, o[qi].x);
+                    o[qi].y = fmaf(p, vr[u].y, o[qi].y);
+                    o[qi].z = fmaf(p, vr[u].z, o[qi].z);
+                    o[qi].w = fmaf(p, vr[u].w, o[qi].w);
+                }
             }
-        const int t = qi / G, e = qi % G;
-        float* dst = part + (((int64_t)t * H + g * G + e) * chunks + c) * P;
-        if (d == 0) {
-            dst[0] = M;
-            dst[1] = S;
+        };
+        for (int it = 0; it < nit_v; it += 2) {
+            if (it + 1 < nit_v) load_v(vB, it + 1);
+            accumulate(vA, it);
+            if (it + 1 < nit_v) {
+                if (it + 2 < nit_v) load_v(vA, it + 2);
+                accumulate(vB, it + 1);
+            }
         }
-        dst[2 + d] = O;
-    }
-}
-
-// out[t, h D + d] = sum_c o_c e^(M_c - M) / sum_c S_c e^(M_c - M), one workgroup per
-// (token, head): the chunks' maxima and sums reduced once by the workgroup, then
-// 256 / D thread groups take every (256 / D)-th chunk of each dimension's sum
-// (independent loads, unrolled) and meet in LDS.
-__device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
+        // the NG groups' sums: the groups of one wave by lane shuffles, then the
+        // four waves through red[w][qi][D], added up when the triples are written
+        constexpr int GPW = 64 / D4;  // groups per wave (4, 2, 1)
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float w = __shfl_xor(v, o, 64);
-        v = is_max ? fmaxf(v, w) : v + w;
+        for (int qi = 0; qi < QB; ++qi) {
+            if (qi >= Q) continue;  // wave-uniform
+            float4 v = o[qi];
+            if constexpr (GPW >= 4) {
+                v.x += __shfl_xor(v.x, 16, 64); v.y += __shfl_xor(v.y, 16, 64);
+                v.z += __shfl_xor(v.z, 16, 64); v.w += __shfl_xor(v.w, 16, 64);
+            }
+            if constexpr (GPW >= 2) {
+                v.x += __shfl_xor(v.x, 32, 64); v.y += __shfl_xor(v.y, 32, 64);
+                v.z += __shfl_xor(v.z, 32, 64); v.w += __shfl_xor(v.w, 32, 64);
+            }
+            if (lane < D4) *reinterpret_cast<float4*>(red + (wv * QB + qi) * D + 4 * c4) = v;
+        }
     }
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    if (lane == 0) red[wv] = v;
     __syncthreads();
-    float r = red[0];
-    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = is_max ? fmaxf(r, red[w]) : r + red[w];
+
+    // 6. the chunk's (max, sum) pair and o of every query (ms [q][chunk][2], po
+    //    [q][chunk][D], q = t H + h), then the arrival count; the last workgroup merges
+    float* ms = part;
+    float* po = part + (int64_t)m * H * chunks * 2;
+    for (int i = tid; i < Q * D; i += kThreads) {
+        const int qi = i / D, d = i - qi * D;
+        const int t = qi / G, e = qi - t * G;
+        const int64_t qc = ((int64_t)t * H + g * G + e) * chunks + c;
+        if (d == 0) *reinterpret_cast<float2*>(ms + 2 * qc) = make_float2(stat[2 * qi], stat[2 * qi + 1]);
+        po[qc * D + d] = (red[qi * D + d] + red[(QB + qi) * D + d]) +
+                         (red[(2 * QB + qi) * D + d] + red[(3 * QB + qi) * D + d]);
+    }
+    // Every wave's stores complete, then ONE agent-scope release (thread 0): it
+    // writes the L2 back, so the pairs and o are visible to workgroups on other XCDs
+    // before this workgroup counts.  (A fence per thread costs a write-back each.)
+    // The last workgroup's thread 0 acquires (invalidating this CU's caches)
+    // before any of its threads reads the other chunks' results.
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    return r;
+    if (tid == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        const uint32_t prev =
+            __hip_atomic_fetch_add(&arrivals[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        is_last = prev == (uint32_t)chunks - 1;
+        if (is_last) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            arrivals[g] = 0;  // ready for the next call (ordered by the kernel's end)
+        }
+    }
+    __syncthreads();
+    if (!is_last) return;
+    // the merge: per query (a wave each) all chunks' pairs in one pass of loads, the
+    // overall max M and sum S, and each chunk's weight e^(M_c - M) / S into wts (LDS,
+    // reusing sp); then thread (query, dimension) sums o_c[d] times the weights, 32
+    // chunks' loads in flight.  A chunk whose queries were all masked has M_c = -inf
+    // and weight 0.
+    float* wts = sp;  // [QB][chunks]; the launcher sizes sp for it
+    for (int qi = wv; qi < Q; qi += kThreads / 64) {
+        const int t = qi / G, e = qi - t * G;
+        const float2* pq = reinterpret_cast<const float2*>(ms) + ((int64_t)t * H + g * G + e) * chunks;
+        float M = -INFINITY;
+        for (int cc = lane; cc < chunks; cc += 64) {
+            const float2 v = pq[cc];
+            wts[qi * chunks + cc] = v.x;
+            M = fmaxf(M, v.x);
+        }
+        M = wave_max(M);
+        float S = 0.0f;
+        for (int cc = lane; cc < chunks; cc += 64) {
+            const float mc = wts[qi * chunks + cc];
+            const float f = M == -INFINITY || mc == -INFINITY ? 0.0f : expf(mc - M);
+            wts[qi * chunks + cc] = f;
+            S = fmaf(pq[cc].y, f, S);
+        }
+        S = wave_add(S);
+        for (int cc = lane; cc < chunks; cc += 64) wts[qi * chunks + cc] /= S;
+    }
+    __syncthreads();
+    for (int i = tid; i < Q * D; i += kThreads) {
+        const int qi = i / D, d = i - qi * D;
+        const int t = qi / G, e = qi - t * G;
+        const int h = g * G + e;
+        const float* pq = po + ((int64_t)t * H + h) * chunks * D + d;
+        const float* wq = wts + qi * chunks;
+        float O = 0.0f;
+        for (int cc = 0; cc < chunks; cc += 32) {  // the last batch clamps its loads
+            float ov[32];
+#pragma unroll
+            for (int u = 0; u < 32; ++u) ov[u] = pq[(int64_t)min(cc + u, chunks - 1) * D];
+#pragma unroll
+            for (int u = 0; u < 32; ++u)
+                if (cc + u < chunks) O = fmaf(ov[u], wq[cc + u], O);
+        }
+        out[((int64_t)t * H + h) * D + d] = O;
+    }
 }
 
-__global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict__ part, int m,
-                                                         int H, int D, int chunks,
-                                                         float* __restrict__ out) {
-    __shared__ float red[4];
-    __shared__ float acc[256];
-    const int th = blockIdx.x;  // token t * H + head h
-    const int P = 2 + D;
-    const float* pr = part + (int64_t)th * chunks * P;
-    float M = -INFINITY;
-    for (int c = threadIdx.x; c < chunks; c += blockDim.x) M = fmaxf(M, pr[c * P]);
-    M = block_reduce(M, true, red);
-    float S = 0.0f;
-    for (int c = threadIdx.x; c < chunks; c += blockDim.x)
-        if (pr[c * P] != -INFINITY) S += pr[c * P + 1] * expf(pr[c * P] - M);
-    S = block_reduce(S, false, red);
-    const int groups = (int)blockDim.x / D;  // 4 (hd 64), 2 (128) or 1 (256)
-    const int d = threadIdx.x % D, grp = threadIdx.x / D;
-    float O = 0.0f;
-#pragma unroll 8
-    for (int c = grp; c < chunks; c += groups) {
-        const float mc = pr[c * P];
-        O += mc == -INFINITY ? 0.0f : pr[c * P + 2 + d] * expf(mc - M);
-    }
-    acc[threadIdx.x] = O;
-    __syncthreads();
-    if (grp == 0) {
-        for (int gi = 1; gi < groups; ++gi) O += acc[gi * D + d];
-        out[(int64_t)th * D + d] = O / S;
-    }
+template <int D, int QB>
+hipError_t launch_d_q(const KvCache& kv, const float* qkv, int m, int H, int C, int chunks,
+                      float* part, float* out, hipStream_t s) {
+    const size_t lds = sizeof(float) * ((size_t)QB * D * 5 + (size_t)m * D * 2 +
+                                        (size_t)QB * std::max(C, chunks) + 2 * QB);
+    if (lds > 159 * 1024) return hipErrorInvalidValue;
+    static const bool attr = hipFuncSetAttribute((const void*)attn_decode_kernel<D, QB>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 160 * 1024 - 1024) == hipSuccess;
+    if (!attr) return hipErrorInvalidValue;
+    attn_decode_kernel<D, QB><<<dim3((unsigned)kv.n_kv_heads, (unsigned)chunks), kThreads, lds, s>>>(
+        qkv, m, H, (int)kv.n_kv_heads, (int)kv.len, C, chunks, 1.0f / sqrtf((float)D), kv.inv_freq,
+        kv.k, kv.v, (int)kv.max_seq, part, kv.arrivals, out);
+    return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_d(const KvCache& kv, const float* qkv, int m, int H, int C, int chunks,
+                    float* part, float* out, hipStream_t s) {
+    const int Q = m * (H / (int)kv.n_kv_heads);
+    if (Q <= 1) return launch_d_q<D, 1>(kv, qkv, m, H, C, chunks, part, out, s);
+    if (Q <= 2) return launch_d_q<D, 2>(kv, qkv, m, H, C, chunks, part, out, s);
+    if (Q <= 4) return launch_d_q<D, 4>(kv, qkv, m, H, C, chunks, part, out, s);
+    if (Q <= 8) return launch_d_q<D, 8>(kv, qkv, m, H, C, chunks, part, out, s);
+    return launch_d_q<D, 16>(kv, qkv, m, H, C, chunks, part, out, s);
 }
 
 }  // namespace
 
 hipError_t launch_attention_decode(const KvCache& kv, const float* qkv, int64_t m, int64_t H,
                                    float* out, hipStream_t s) {
-    const int D = (int)kv.head_dim, KVH = (int)kv.n_kv_heads, len = (int)kv.len;
-    const int L = len + (int)m;
-    // chunk length: enough (kv head, chunk) workgroups to cover the CUs twice
+    const int D = (int)kv.head_dim, KVH = (int)kv.n_kv_heads;
+    const int64_t L = kv.len + m;
+    // chunk length: enough (kv head, chunk) workgroups to cover the CUs twice, 32 ..
+    // kMaxChunk positions, a multiple of 32
+    // (kv head, chunk) workgroups to cover the CUs twice; chunks of 32 .. kMaxChunk
+    // positions (a multiple of 32), at most kMaxChunks of them
     const int64_t want = 2 * (int64_t)device_info().cu_count;
-    int C = (int)std::max<int64_t>(32, ((int64_t)L * KVH + want - 1) / want);
-    C = (C + 31) / 32 * 32;
-    const int chunks = (L + C - 1) / C;
-    const size_t qbytes = (size_t)m * H * D * sizeof(float);
+    int64_t C = std::max((L * KVH + want - 1) / want, (L + kMaxChunks - 1) / kMaxChunks);
+    C = std::max<int64_t>(32, (C + 31) / 32 * 32);
+    if (C > kMaxChunk) return hipErrorInvalidValue;  // longer than kMaxChunk * kMaxChunks
+    const int chunks = (int)((L + C - 1) / C);
     const size_t pbytes = (size_t)m * H * chunks * (2 + D) * sizeof(float);
     void* ws = nullptr;
-    hipError_t e = stream_workspace(s, qbytes + pbytes, &ws, 2);
+    hipError_t e = stream_workspace(s, pbytes, &ws, 2);
     if (e != hipSuccess) return e;
-    float* qrot = static_cast<float*>(ws);
-    float* part = qrot + (size_t)m * H * D;
-    rope_append_kernel<<<dim3((unsigned)m, (unsigned)(H + 2 * KVH)), 128, 0, s>>>(
-        qkv, (int)H, KVH, D, kv.inv_freq, len, qrot, kv.k, kv.v, (int)kv.max_seq);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    const float scale = 1.0f / sqrtf((float)D);
-    const dim3 grid((unsigned)KVH, (unsigned)chunks);
-    const int Q = (int)(m * (H / KVH));
-    auto go = [&](auto dpl, auto qb) {
-        attn_chunk_kernel<decltype(dpl)::value, decltype(qb)::value><<<grid, 256, 0, s>>>(
-            qrot, (int)m, (int)H, KVH, len, C, chunks, scale, kv.k, kv.v, (int)kv.max_seq, part);
-    };
-    auto by_q = [&](auto dpl) {
-        using I = std::integral_constant<int, 1>;
-        if (Q <= 1) go(dpl, I{});
-        else if (Q <= 2) go(dpl, std::integral_constant<int, 2>{});
-        else if (Q <= 4) go(dpl, std::integral_constant<int, 4>{});
-        else if (Q <= 8) go(dpl, std::integral_constant<int, 8>{});
-        else go(dpl, std::integral_constant<int, 16>{});
-    };
-    if (D == 64) by_q(std::integral_constant<int, 1>{});
-    else if (D == 128) by_q(std::integral_constant<int, 2>{});
-    else by_q(std::integral_constant<int, 4>{});
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    attn_merge_kernel<<<(unsigned)(m * H), 256, 0, s>>>(part, (int)m, (int)H, D, chunks, out);
-    return hipGetLastError();
+    float* part = static_cast<float*>(ws);
+    if (D == 64) return launch_d<64>(kv, qkv, (int)m, (int)H, (int)C, chunks, part, out, s);
+    if (D == 128) return launch_d<128>(kv, qkv, (int)m, (int)H, (int)C, chunks, part, out, s);
+    return launch_d<256>(kv, qkv, (int)m, (int)H, (int)C, chunks, part, out, s);
 }
 
 int attention_max_queries() { return kAttnMaxQ; }
+int64_t attention_max_positions() { return (int64_t)kMaxChunk * kMaxChunks; }
 
 }  // namespace unillm

@@ -465,8 +465,10 @@ int unillm_hip_kv_cache_create(int64_t n_kv_heads, int64_t head_dim, int64_t max
     hipError_t e;
     void *k = nullptr, *v = nullptr, *f = nullptr;
     if ((e = hipMalloc(&k, buf)) != hipSuccess || (e = hipMalloc(&v, buf)) != hipSuccess ||
-        (e = hipMalloc(&f, inv.size() * sizeof(float))) != hipSuccess ||
+        (e = hipMalloc(&f, inv.size() * sizeof(float) + (size_t)n_kv_heads * 4)) != hipSuccess ||
         (e = hipMemset(k, 0, buf)) != hipSuccess || (e = hipMemset(v, 0, buf)) != hipSuccess ||
+        (e = hipMemset(static_cast<float*>(f) + inv.size(), 0, (size_t)n_kv_heads * 4)) !=
+            hipSuccess ||
         (e = hipMemcpy(f, inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice)) !=
             hipSuccess) {
         (void)hipFree(k);
@@ -479,6 +481,7 @@ int unillm_hip_kv_cache_create(int64_t n_kv_heads, int64_t head_dim, int64_t max
     c->k = static_cast<float*>(k);
     c->v = static_cast<float*>(v);
     c->inv_freq = static_cast<float*>(f);
+    c->arrivals = reinterpret_cast<uint32_t*>(c->inv_freq + inv.size());
     *out = c;
     return UNILLM_OK;
 }
@@ -529,6 +532,9 @@ int unillm_hip_attention_decode(unillm_kv_cache* c, const float* qkv_dev, int64_
                     "KV cache append failed: KV cache overflow: current_len=" +
                         std::to_string(c->len) + ", new_len=" + std::to_string(m) +
                         ", max_seq_len=" + std::to_string(c->max_seq));
+    if (c->len + m > attention_max_positions())
+        return fail(UNILLM_ERR_UNSUPPORTED, "attention: len + m must be <= " +
+                                                std::to_string(attention_max_positions()));
     if (int rc = ensure_init()) return rc;
     hipError_t e = launch_attention_decode(*c, qkv_dev, m, n_heads, out_dev,
                                            static_cast<hipStream_t>(stream));

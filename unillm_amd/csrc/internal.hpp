@@ -50,7 +50,10 @@ struct unillm_qweight {
 
 // The opaque KV-cache handle (one decoder layer, one sequence): K and V of
 // n_kv_heads heads, [n_kv_heads][max_seq][head_dim] f32 each, the first len
-// positions filled; inv_freq[head_dim / 2] the RoPE frequencies in f32.
+// positions filled; inv_freq[head_dim / 2] the RoPE frequencies in f32, followed
+// in the same allocation by arrivals[n_kv_heads]: the attention kernel's
+// per-kv-head arrival counters, zero between calls (the last workgroup of a
+// head resets its counter).
 struct unillm_kv_cache {
     int device;
     int64_t n_kv_heads, head_dim, max_seq, len;
@@ -58,6 +61,7 @@ struct unillm_kv_cache {
     float* k;
     float* v;
     float* inv_freq;
+    uint32_t* arrivals;
 };
 
 namespace unillm {
@@ -182,6 +186,7 @@ using KvCache = ::unillm_kv_cache;
 hipError_t launch_attention_decode(const KvCache& kv, const float* qkv, int64_t m, int64_t H,
                                    float* out, hipStream_t s);
 int attention_max_queries();  // m * H / KVH per call
+int64_t attention_max_positions();  // len + m per call
 
 constexpr int64_t kGemvMaxM = 4;
 constexpr int64_t kDecodeMaxM = 64;

@@ -37,7 +37,11 @@ def _run_steps(H, KVH, D, steps, theta=10000.0, max_seq=None, seed=0):
 
 @pytest.mark.parametrize("H,KVH,D,steps", [
     (4, 4, 64, [1, 1, 1]), (8, 2, 128, [4, 1, 1, 3]), (32, 8, 128, [1, 2, 1]),
-    (8, 8, 256, [2, 1]), (4, 1, 128, [4, 4])])
+    (8, 8, 256, [2, 1]), (4, 1, 128, [4, 4]),
+    # hd 64 with 12 and 16 queries a kv head (more queries than the 8 lanes of a position)
+    (8, 2, 64, [4, 3]),
+    # 16 queries a kv head at hd 256 (the largest LDS footprint), and 16 new tokens at G = 1
+    (16, 1, 256, [1, 1]), (2, 2, 64, [16, 16])])
 def test_attention_steps(H, KVH, D, steps):
     print(f"attention H={H} KVH={KVH} D={D} steps={steps}", flush=True)
     assert _run_steps(H, KVH, D, steps) < 1e-4
@@ -101,3 +105,37 @@ def test_attention_overflow_and_limits():
         KvCache(1, 64, 64).attention(torch.zeros(17, 3 * 64, device="cuda"), 1)
     with pytest.raises(HipError):  # head_dim 96 unsupported
         KvCache(1, 96, 8)
+
+
+def test_attention_graph_replays_match_eager():
+    # the chunks of a kv head are merged by the last workgroup to arrive, through a
+    # per-kv-head counter in the cache handle that the merging workgroup resets: a
+    # captured call replayed several times (eager work and synchronisations between
+    # the replays) must give the eager result every time, bit for bit
+    H, KVH, D, L = 32, 8, 128, 700
+    w = (H + 2 * KVH) * D
+    kv = KvCache(KVH, D, L + 1)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        fill = torch.from_numpy(oracle.normal(4 * w, seed=51).reshape(4, w)).cuda()
+        while kv.seq_len + 4 <= L - 1:
+            kv.attention(fill, H, stream=stream)
+        while kv.seq_len < L - 1:
+            kv.attention(fill[:1].contiguous(), H, stream=stream)
+        q1 = torch.from_numpy(oracle.normal(w, seed=52).reshape(1, w)).cuda()
+        out = torch.empty(1, H * D, device="cuda")
+        kv.attention(q1, H, out=out, stream=stream)
+        eager = out.clone()
+        kv.truncate(L - 1)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
+            kv.attention(q1, H, out=out, stream=stream)
+        kv.truncate(L - 1)
+        for i in range(4):
+            out.zero_()
+            g.replay()
+            stream.synchronize()
+            assert torch.equal(out, eager), f"replay {i} differs from the eager call"
+            kv.attention(q1, H, stream=stream)  # eager work between replays
+            kv.truncate(L - 1)
+            stream.synchronize()

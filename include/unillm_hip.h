@@ -176,8 +176,8 @@ int unillm_hip_kv_cache_truncate(unillm_kv_cache* c, int64_t len);
  * n_kv_heads).  The cache's length grows by m.  Decode steps only:
  * m * n_heads / n_kv_heads <= 16, and len + m <= 131072 (UNILLM_ERR_UNSUPPORTED
  * beyond).  Overflow of max_seq is an error with the reference's message
- * (kv_cache.rs:114-121).  One launch; calls on one cache must be ordered (one
- * stream), as each appends to it and uses its per-kv-head arrival counters. */
+ * (kv_cache.rs:114-121).  Calls on one cache must be ordered (one stream), as
+ * each appends to it. */
 int unillm_hip_attention_decode(unillm_kv_cache* c, const float* qkv_dev, int64_t m,
                                 int64_t n_heads, float* out_dev, void* stream);
 

@@ -11,8 +11,8 @@
 // Bound: HBM -- the cached K and V are read once per step (2 KVH len hd 4 bytes,
 // f32 like the reference's cache).
 //
-// One kernel on the caller's stream, a workgroup per (kv head g, chunk c of C
-// positions), 256 threads:
+// Two kernels on the caller's stream.  attn_decode_kernel: a workgroup per (kv
+// head g, chunk c of C positions), 256 threads:
 //   1. the Q = m G queries of kv head g (the m tokens times the G = H / KVH heads
 //      of the group): RoPE at position len + t, times 1 / sqrt(hd), into LDS;
 //   2. the new positions len .. len + m - 1 inside this chunk: k rotated and v
@@ -25,10 +25,13 @@
 //   4. per query (a wave each), the chunk's max and the exponentials and their sum;
 //   5. p v: a float4 of dimensions per thread, positions split over 256 / (hd / 4)
 //      thread groups, the groups' sums meeting by LDS atomic adds;
-//   6. the chunk's (max, sum, o[hd]) per query to the workspace.  The last
-//      workgroup of kv head g to finish (an arrival counter per kv head, which
-//      that workgroup resets to zero for the next call) merges the chunks of
-//      its queries by log-sum-exp into the output rows [m, H hd].
+//   6. the chunk's (max, sum) pair and o[hd] per query to the workspace.
+// attn_merge_kernel: a workgroup per (token, head) merges the chunks by
+// log-sum-exp into the output rows [m, H hd].  The kernel boundary makes the
+// chunk results of every XCD visible to it.  (Merging in the last workgroup of
+// each kv head instead needs an agent-scope release -- an L2 write-back -- in
+// every workgroup and serialises the merge on one CU a head: measured 3-9 us
+// slower.)
 // Everything a step reads from HBM beyond the cache is the m qkv rows and the
 // per-chunk triples (chunks (hd + 2) floats per query).
 #include <hip/hip_runtime.h>
@@ -82,8 +85,7 @@ template <int D, int QB>
 __global__ __launch_bounds__(kThreads) void attn_decode_kernel(
     const float* __restrict__ qkv, int m, int H, int KVH, int len, int C, int chunks, float scale,
     const float* __restrict__ inv_freq, float* __restrict__ kc, float* __restrict__ vc,
-    int max_seq, float* __restrict__ part, uint32_t* __restrict__ arrivals,
-    float* __restrict__ out) {
+    int max_seq, float* __restrict__ part) {
     constexpr int LP = D / 8;             // lanes per position in the score pass
     constexpr int SG = kThreads / LP;     // positions at a time (32, 16, 8)
     constexpr int D4 = D / 4;             // float4 columns in the p v pass
@@ -102,7 +104,6 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(
     float* sp = nv + m * D;
     float* red = sp + QB * max(C, chunks);
     float* stat = red + 4 * QB * D;
-    __shared__ uint32_t is_last;
     const float* kg = kc + (int64_t)g * max_seq * D;
     const float* vg = vc + (int64_t)g * max_seq * D;
 
@@ -286,7 +287,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(
     __syncthreads();
 
     // 6. the chunk's (max, sum) pair and o of every query (ms [q][chunk][2], po
-    //    [q][chunk][D], q = t H + h), then the arrival count; the last workgroup merges
+    //    [q][chunk][D], q = t H + h)
     float* ms = part;
     float* po = part + (int64_t)m * H * chunks * 2;
     for (int i = tid; i < Q * D; i += kThreads) {
@@ -297,69 +298,54 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(
         po[qc * D + d] = (red[qi * D + d] + red[(QB + qi) * D + d]) +
                          (red[(2 * QB + qi) * D + d] + red[(3 * QB + qi) * D + d]);
     }
-    // Every wave's stores complete, then ONE agent-scope release (thread 0): it
-    // writes the L2 back, so the pairs and o are visible to workgroups on other XCDs
-    // before this workgroup counts.  (A fence per thread costs a write-back each.)
-    // The last workgroup's thread 0 acquires (invalidating this CU's caches)
-    // before any of its threads reads the other chunks' results.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        const uint32_t prev =
-            __hip_atomic_fetch_add(&arrivals[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        is_last = prev == (uint32_t)chunks - 1;
-        if (is_last) {
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            arrivals[g] = 0;  // ready for the next call (ordered by the kernel's end)
-        }
-    }
-    __syncthreads();
-    if (!is_last) return;
-    // the merge: per query (a wave each) all chunks' pairs in one pass of loads, the
-    // overall max M and sum S, and each chunk's weight e^(M_c - M) / S into wts (LDS,
-    // reusing sp); then thread (query, dimension) sums o_c[d] times the weights, 32
-    // chunks' loads in flight.  A chunk whose queries were all masked has M_c = -inf
-    // and weight 0.
-    float* wts = sp;  // [QB][chunks]; the launcher sizes sp for it
-    for (int qi = wv; qi < Q; qi += kThreads / 64) {
-        const int t = qi / G, e = qi - t * G;
-        const float2* pq = reinterpret_cast<const float2*>(ms) + ((int64_t)t * H + g * G + e) * chunks;
+}
+
+// The merge, per (token t, head h) = blockIdx.x: wave 0 reads every chunk's (max, sum)
+// pair (one pass of loads), forms the overall max M and sum S and each chunk's weight
+// e^(M_c - M) / S in LDS; thread d sums o_c[d] times the weights, 32 chunks' loads in
+// flight (the first 32 requested at entry).  A chunk whose queries were all masked has M_c = -inf and weight 0.
+template <int D>
+__global__ __launch_bounds__(D) void attn_merge_kernel(const float* __restrict__ part, int m,
+                                                       int H, int chunks, float* __restrict__ out) {
+    extern __shared__ float wts[];  // [chunks]
+    const int th = blockIdx.x;      // t H + h
+    const int tid = threadIdx.x, lane = tid & 63;
+    const float2* pq = reinterpret_cast<const float2*>(part) + (int64_t)th * chunks;
+    const float* po = part + (int64_t)m * H * chunks * 2 + (int64_t)th * chunks * D + tid;
+    // the first 32 chunks' o[d] are requested before the weights exist (they do not
+    // depend on them), so their loads overlap the (max, sum) pass
+    float ov[32];
+#pragma unroll
+    for (int u = 0; u < 32; ++u) ov[u] = po[(int64_t)min(u, chunks - 1) * D];
+    if (tid < 64) {
         float M = -INFINITY;
         for (int cc = lane; cc < chunks; cc += 64) {
             const float2 v = pq[cc];
-            wts[qi * chunks + cc] = v.x;
+            wts[cc] = v.x;
             M = fmaxf(M, v.x);
         }
         M = wave_max(M);
         float S = 0.0f;
         for (int cc = lane; cc < chunks; cc += 64) {
-            const float mc = wts[qi * chunks + cc];
+            const float mc = wts[cc];
             const float f = M == -INFINITY || mc == -INFINITY ? 0.0f : expf(mc - M);
-            wts[qi * chunks + cc] = f;
+            wts[cc] = f;
             S = fmaf(pq[cc].y, f, S);
         }
         S = wave_add(S);
-        for (int cc = lane; cc < chunks; cc += 64) wts[qi * chunks + cc] /= S;
+        for (int cc = lane; cc < chunks; cc += 64) wts[cc] /= S;
     }
     __syncthreads();
-    for (int i = tid; i < Q * D; i += kThreads) {
-        const int qi = i / D, d = i - qi * D;
-        const int t = qi / G, e = qi - t * G;
-        const int h = g * G + e;
-        const float* pq = po + ((int64_t)t * H + h) * chunks * D + d;
-        const float* wq = wts + qi * chunks;
-        float O = 0.0f;
-        for (int cc = 0; cc < chunks; cc += 32) {  // the last batch clamps its loads
-            float ov[32];
+    float O = 0.0f;
+    for (int cc = 0; cc < chunks; cc += 32) {  // the last batch clamps its loads
+        if (cc > 0)
 #pragma unroll
-            for (int u = 0; u < 32; ++u) ov[u] = pq[(int64_t)min(cc + u, chunks - 1) * D];
+            for (int u = 0; u < 32; ++u) ov[u] = po[(int64_t)min(cc + u, chunks - 1) * D];
 #pragma unroll
-            for (int u = 0; u < 32; ++u)
-                if (cc + u < chunks) O = fmaf(ov[u], wq[cc + u], O);
-        }
-        out[((int64_t)t * H + h) * D + d] = O;
+        for (int u = 0; u < 32; ++u)
+            if (cc + u < chunks) O = fmaf(ov[u], wts[cc + u], O);
     }
+    out[(int64_t)th * D + tid] = O;
 }
 
 template <int D, int QB>
@@ -374,7 +360,11 @@ hipError_t launch_d_q(const KvCache& kv, const float* qkv, int m, int H, int C, 
     if (!attr) return hipErrorInvalidValue;
     attn_decode_kernel<D, QB><<<dim3((unsigned)kv.n_kv_heads, (unsigned)chunks), kThreads, lds, s>>>(
         qkv, m, H, (int)kv.n_kv_heads, (int)kv.len, C, chunks, 1.0f / sqrtf((float)D), kv.inv_freq,
-        kv.k, kv.v, (int)kv.max_seq, part, kv.arrivals, out);
+        kv.k, kv.v, (int)kv.max_seq, part);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    attn_merge_kernel<D><<<(unsigned)(m * H), D, sizeof(float) * (size_t)chunks, s>>>(
+        part, m, H, chunks, out);
     return hipGetLastError();
 }
 

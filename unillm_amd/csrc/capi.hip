@@ -465,10 +465,8 @@ int unillm_hip_kv_cache_create(int64_t n_kv_heads, int64_t head_dim, int64_t max
     hipError_t e;
     void *k = nullptr, *v = nullptr, *f = nullptr;
     if ((e = hipMalloc(&k, buf)) != hipSuccess || (e = hipMalloc(&v, buf)) != hipSuccess ||
-        (e = hipMalloc(&f, inv.size() * sizeof(float) + (size_t)n_kv_heads * 4)) != hipSuccess ||
+        (e = hipMalloc(&f, inv.size() * sizeof(float))) != hipSuccess ||
         (e = hipMemset(k, 0, buf)) != hipSuccess || (e = hipMemset(v, 0, buf)) != hipSuccess ||
-        (e = hipMemset(static_cast<float*>(f) + inv.size(), 0, (size_t)n_kv_heads * 4)) !=
-            hipSuccess ||
         (e = hipMemcpy(f, inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice)) !=
             hipSuccess) {
         (void)hipFree(k);
@@ -481,7 +479,6 @@ int unillm_hip_kv_cache_create(int64_t n_kv_heads, int64_t head_dim, int64_t max
     c->k = static_cast<float*>(k);
     c->v = static_cast<float*>(v);
     c->inv_freq = static_cast<float*>(f);
-    c->arrivals = reinterpret_cast<uint32_t*>(c->inv_freq + inv.size());
     *out = c;
     return UNILLM_OK;
 }

@@ -50,10 +50,7 @@ struct unillm_qweight {
 
 // The opaque KV-cache handle (one decoder layer, one sequence): K and V of
 // n_kv_heads heads, [n_kv_heads][max_seq][head_dim] f32 each, the first len
-// positions filled; inv_freq[head_dim / 2] the RoPE frequencies in f32, followed
-// in the same allocation by arrivals[n_kv_heads]: the attention kernel's
-// per-kv-head arrival counters, zero between calls (the last workgroup of a
-// head resets its counter).
+// positions filled; inv_freq[head_dim / 2] the RoPE frequencies in f32.
 struct unillm_kv_cache {
     int device;
     int64_t n_kv_heads, head_dim, max_seq, len;
@@ -61,7 +58,6 @@ struct unillm_kv_cache {
     float* k;
     float* v;
     float* inv_freq;
-    uint32_t* arrivals;
 };
 
 namespace unillm {

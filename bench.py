@@ -15,8 +15,9 @@ roofline.achieved uses the same bytes over the GEMV kernel's average duration,
 measured with HIP events on the stream the kernels run on.
 
 The other BASELINE configs are reported under "extra" (Q8_0 TinyLlama GEMV,
-batched decode, prefill TFLOP/s, full stack with lm_head); they are not the
-headline.  Synthetic data: weights N(0, 0.02) from torch's generator,
+batched decode, prefill TFLOP/s, full stack with lm_head), with decode
+attention and a whole decode step (linear layers + attention over a KV cache);
+they are not the headline.  Synthetic data: weights N(0, 0.02) from torch's generator,
 quantized on the device with the GGML quantizer; activations N(0, 1).
 """
 from __future__ import annotations
@@ -51,7 +52,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default="", help="comma list of extra configs to run "
-                    "(q8_gemv,batched,prefill,stack,q4_k,attention) -- for profiling")
+                    "(q8_gemv,batched,prefill,stack,q4_k,attention,e2e) -- for profiling")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 64 MiB once (device to device) and exit: the known-size "
                     "kernel that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
@@ -208,7 +209,7 @@ def extra_configs(torch, QuantLinear, gen, stream, only):
         return float(np.median(ts))
 
     want = set(only.split(",")) if only else {"q8_gemv", "batched", "prefill", "stack", "q4_k",
-                                              "attention"}
+                                              "attention", "e2e"}
     if "q8_gemv" in want:
         n, k = 5632, 2048
         ws = rotate(Q8_0, n, k)
@@ -331,6 +332,8 @@ def extra_configs(torch, QuantLinear, gen, stream, only):
                     "GB/s": round(b / ms / 1e6, 1), "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 3),
                     "us": round(ms * 1e3, 2), "eager_us": round(eager * 1e3, 2), "kv_bytes": b}
                 del kv
+    if "e2e" in want and "stack" not in want:
+        want.add("stack")  # the end-to-end step reuses the stack's weights
     if "stack" in want:
         # config 5: 32 layers (QKV, o, gate+up fused 22016, down) + Q8_0 lm_head
         shapes = [(Q4_0, 4096, 12288), (Q4_0, 4096, 4096), (Q4_0, 4096, 22016),
@@ -383,8 +386,74 @@ def extra_configs(torch, QuantLinear, gen, stream, only):
                 "GB/s": round(b / msf / 1e6, 1), "ms_per_step": round(msf, 4),
                 "tokens/s": round(m * 1e3 / msf, 1),
                 "note": "norms, residual adds and SwiGLU fused into the same 4 launches a layer"}
+        if "e2e" in want:
+            res.update(decode_step_e2e(torch, layers, head, gen, stream, timer))
         del layers, head
     torch.cuda.synchronize()
+    return res
+
+
+def decode_step_e2e(torch, layers, head, gen, stream, timer):
+    """A whole Llama-2-7B decode step (m = 1) over a KV cache of L positions:
+    per layer input_layernorm + QKV, attention (RoPE, append, causal softmax over
+    the cache: 32 heads, hd 128, f32), o_proj + residual, post_attention_layernorm +
+    gate_up + SwiGLU, down + residual; then the final norm + lm_head.  Captured once
+    as a HIP graph (6 launches a layer) and replayed: every replay recomputes
+    position L - 1, the caches' length being host state set before capture."""
+    from unillm_amd import KvCache
+    H, D = 32, 128
+    res = {}
+    gam = torch.ones(4096, device="cuda")
+    h = torch.empty(1, 4096, device="cuda")
+    qkv_out = torch.empty(1, 3 * 4096, device="cuda")
+    att = torch.empty(1, 4096, device="cuda")
+    act = torch.empty(1, 11008, device="cuda")
+    logits = torch.empty(1, 32000, device="cuda")
+    for L in (1024, 4096):
+        caches = [KvCache(H, D, L) for _ in layers]
+        fill = torch.empty(16, 3 * 4096, device="cuda").normal_(generator=gen)
+        with torch.cuda.stream(stream):
+            for kv in caches:  # fill to L - 1 positions (16 tokens a call, then single)
+                while kv.seq_len + 16 <= L - 1:
+                    kv.attention(fill, H, stream=stream)
+                while kv.seq_len < L - 1:
+                    kv.attention(fill[:1].contiguous(), H, stream=stream)
+
+            def step():
+                for (qkv, o, gu, down), kv in zip(layers, caches):
+                    qkv.forward_norm(h, gam, eps=1e-6, out=qkv_out, stream=stream)
+                    kv.attention(qkv_out, H, out=att, stream=stream)
+                    o.forward_add(att, h, stream=stream)
+                    gu.forward_swiglu(h, out=act, stream=stream, norm=(gam, None, 1e-6))
+                    down.forward_add(act, h, stream=stream)
+                head.forward_norm(h, gam, eps=1e-6, out=logits, stream=stream)
+
+            def rewind():
+                for kv in caches:
+                    kv.truncate(L - 1)
+
+            h.normal_(generator=gen)
+            step()
+            rewind()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
+                step()
+            rewind()
+            h.normal_(generator=gen)
+            g.replay()
+            ms = float(np.median([timer.run(g.replay, 5) for _ in range(3)]))
+            del g
+        kv_bytes = 32 * 2 * H * L * D * 4
+        w_bytes = 32 * (wbytes(Q4_0, 12288, 4096) + wbytes(Q4_0, 4096, 4096) +
+                        wbytes(Q4_0, 22016, 4096) + wbytes(Q4_0, 4096, 11008)) + \
+            wbytes(Q8_0, 32000, 4096)
+        res[f"llama2_7b_decode_step_e2e_m1_L{L}"] = {
+            "ms_per_step": round(ms, 4), "tokens/s": round(1e3 / ms, 1),
+            "GB/s": round((w_bytes + kv_bytes) / ms / 1e6, 1), "kv_bytes": kv_bytes,
+            "launches_per_step": 6 * 32 + 1,
+            "note": "norm+QKV, attention, o+residual, norm+gate_up+SwiGLU, down+residual a layer; "
+                    "final norm + Q8_0 lm_head; HIP-graph replay"}
+        del caches
     return res
 
 

@@ -24,7 +24,8 @@
 //      over the LP lanes by DPP; causal mask; into LDS;
 //   4. per query (a wave each), the chunk's max and the exponentials and their sum;
 //   5. p v: a float4 of dimensions per thread, positions split over 256 / (hd / 4)
-//      thread groups, the groups' sums meeting by LDS atomic adds;
+//      thread groups, whose sums meet by lane shuffles within a wave and one LDS
+//      pass across the four waves;
 //   6. the chunk's (max, sum) pair and o[hd] per query to the workspace.
 // attn_merge_kernel: a workgroup per (token, head) merges the chunks by
 // log-sum-exp into the output rows [m, H hd].  The kernel boundary makes the
@@ -33,7 +34,7 @@
 // every workgroup and serialises the merge on one CU a head: measured 3-9 us
 // slower.)
 // Everything a step reads from HBM beyond the cache is the m qkv rows and the
-// per-chunk triples (chunks (hd + 2) floats per query).
+// per-chunk results (chunks (hd + 2) floats per query, written and read once).
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -79,8 +80,8 @@ __device__ __forceinline__ float wave_add(float v) {
     return v;
 }
 
-// Dynamic LDS (floats): qs[QB][D] | nk[m][D] | nv[m][D] | sp[QB][max(C, chunks)] (the scores,
-// then the merge's weights) | red[4][QB][D] | stat[QB][2]
+// Dynamic LDS (floats): qs[QB][D] | nk[m][D] | nv[m][D] | sp[QB][C] (scores, then
+// exponentials) | red[4][QB][D] | stat[QB][2]
 template <int D, int QB>
 __global__ __launch_bounds__(kThreads) void attn_decode_kernel(
     const float* __restrict__ qkv, int m, int H, int KVH, int len, int C, int chunks, float scale,
@@ -102,7 +103,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(
     float* nk = qs + QB * D;
     float* nv = nk + m * D;
     float* sp = nv + m * D;
-    float* red = sp + QB * max(C, chunks);
+    float* red = sp + QB * C;
     float* stat = red + 4 * QB * D;
     const float* kg = kc + (int64_t)g * max_seq * D;
     const float* vg = vc + (int64_t)g * max_seq * D;
@@ -352,7 +353,7 @@ template <int D, int QB>
 hipError_t launch_d_q(const KvCache& kv, const float* qkv, int m, int H, int C, int chunks,
                       float* part, float* out, hipStream_t s) {
     const size_t lds = sizeof(float) * ((size_t)QB * D * 5 + (size_t)m * D * 2 +
-                                        (size_t)QB * std::max(C, chunks) + 2 * QB);
+                                        (size_t)QB * C + 2 * QB);
     if (lds > 159 * 1024) return hipErrorInvalidValue;
     static const bool attr = hipFuncSetAttribute((const void*)attn_decode_kernel<D, QB>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,

@@ -174,6 +174,8 @@ static double normwise(const std::vector<float>& y, const std::vector<double>& r
     return den > 0 ? num / den : num;
 }
 
+static void test_gpu_kv();
+
 static void test_gpu(const std::string& gguf, const std::vector<Expect>& ex) {
     GgufWeightLoader loader;
     const ModelWeights w = loader.load_weights(gguf);
@@ -208,6 +210,81 @@ static void test_gpu(const std::string& gguf, const std::vector<Expect>& ex) {
                       "QMatMul forward failed: rank 1"));
     CHECK(throws_with([&] { q->forward(Tensor::empty({2, 64}, Device::cpu())); },
                       "QMatMul forward failed: input is on CPU"));
+    test_gpu_kv();
+}
+
+// LayerKVCache / KVCache (kv_cache.rs) and LayerKVCache::attend (forward_with_cache
+// after the projections) through the C ABI: closed forms (one position returns its
+// v exactly; zero keys average the visible values), the length bookkeeping, and the
+// reference's overflow message.  The kernel's parity with the oracle over random
+// inputs is tested from Python (tests/test_gpu_attention.py).
+static void test_gpu_kv() {
+    const int64_t H = 4, KVH = 2, D = 64, W = (H + 2 * KVH) * D;
+    auto row = [&](std::vector<float>& q, int64_t t, int64_t part, int64_t head, int64_t d) -> float& {
+        // part 0 = q heads, 1 = k heads, 2 = v heads
+        const int64_t off = part == 0 ? head * D : part == 1 ? (H + head) * D : (H + KVH + head) * D;
+        return q[(size_t)(t * W + off + d)];
+    };
+    {
+        LayerKVCache c = LayerKVCache::with_capacity(KVH, D, 8);
+        CHECK(c.is_empty() && c.seq_len() == 0 && c.max_seq_len() == 8);
+        std::vector<float> qkv((size_t)W);
+        for (size_t i = 0; i < qkv.size(); ++i) qkv[i] = (float)((i * 37 % 101) - 50) / 16.0f;
+        const std::vector<float> out =
+            c.attend(Tensor::from_host(qkv, {1, W}, Device::hip(0)), H).to_host();
+        CHECK(c.seq_len() == 1);
+        bool exact = out.size() == (size_t)(H * D);
+        for (int64_t h = 0; h < H && exact; ++h)  // head h reads kv head h / (H / KVH)
+            for (int64_t d = 0; d < D; ++d)
+                exact = exact && out[(size_t)(h * D + d)] == row(qkv, 0, 2, h / (H / KVH), d);
+        CHECK(exact);
+        c.truncate(0);
+        CHECK(c.is_empty());
+    }
+    {
+        // three tokens with zero keys: token t sees positions 0 .. t, all scores 0
+        LayerKVCache c = LayerKVCache::with_capacity(KVH, D, 3);
+        std::vector<float> qkv((size_t)(3 * W), 0.0f);
+        for (int64_t t = 0; t < 3; ++t)
+            for (int64_t g = 0; g < KVH; ++g)
+                for (int64_t d = 0; d < D; ++d) {
+                    row(qkv, t, 0, 2 * g, d) = 1.0f + (float)d;  // queries: anything
+                    row(qkv, t, 2, g, d) = (float)(t * 100 + g * 10) + (float)d / 8.0f;
+                }
+        const std::vector<float> out =
+            c.attend(Tensor::from_host(qkv, {3, W}, Device::hip(0)), H).to_host();
+        double worst = 0;
+        for (int64_t t = 0; t < 3; ++t)
+            for (int64_t h = 0; h < H; ++h)
+                for (int64_t d = 0; d < D; ++d) {
+                    double mean = 0;
+                    for (int64_t j = 0; j <= t; ++j) mean += row(qkv, j, 2, h / 2, d);
+                    mean /= (double)(t + 1);
+                    worst = std::max(worst, std::fabs(out[(size_t)((t * H + h) * D + d)] - mean) /
+                                                std::max(1.0, std::fabs(mean)));
+                }
+        CHECK(worst < 1e-6);
+        CHECK(c.seq_len() == 3);
+        // full: one more position is the reference's overflow error, and nothing changes
+        CHECK(throws_with([&] { c.attend(Tensor::from_host(qkv, {3, W}, Device::hip(0)).reshape({3, W}), H); },
+                          "KV cache append failed: KV cache overflow"));
+        CHECK(c.seq_len() == 3);
+        CHECK(throws_with([&] { c.attend(Tensor::empty({1, W - D}, Device::hip(0)), H); },
+                          "attention: qkv width"));
+        c.clear();
+        CHECK(c.is_empty() && c.max_seq_len() == 3);
+    }
+    {
+        KVCache kv = KVCache::with_capacity(3, KVH, D, 16);
+        CHECK(kv.num_layers() == 3 && kv.max_seq_len() == 16 && kv.is_empty());
+        std::vector<float> qkv((size_t)(2 * W), 0.5f);
+        kv.layer_mut(0).attend(Tensor::from_host(qkv, {2, W}, Device::hip(0)), H);
+        kv.layer_mut(2).attend(Tensor::from_host(qkv, {2, W}, Device::hip(0)), H);
+        CHECK(kv.seq_len() == 2 && kv.layer(1).seq_len() == 0 && kv.layer(2).seq_len() == 2);
+        kv.clear();
+        CHECK(kv.is_empty() && kv.layer(2).seq_len() == 0);
+        CHECK(throws_with([&] { kv.layer_mut(3); }, "layer index out of range"));
+    }
 }
 
 static void test_cpu_kq(const std::string& gguf, const std::vector<Expect>& ex) {

@@ -1,8 +1,9 @@
 """Run the C++ host-layer test program (tests/cpp/test_host.cpp): GGUF
 parsing, the reference's name map and quantized/f32 classification, malformed
 files (CPU), then loading the tiny GGUFs onto the device and QMatMul::forward
-parity against the committed expectations, and load-time QKV / gate+up fusion
-(GPU)."""
+parity against the committed expectations, load-time QKV / gate+up fusion, and
+the KV-cache mirror (LayerKVCache / KVCache with closed-form attention checks and
+the reference's overflow message) (GPU)."""
 import os
 import subprocess
 

@@ -432,4 +432,94 @@ ModelWeights GgufWeightLoader::load_weights(const std::string& path,
     return w;
 }
 
+// ---- KV cache and decode attention --------------------------------------------------------------
+
+namespace {
+// the C ABI's message as is: it carries the reference's text ("KV cache append failed: ...")
+void check_msg(int rc) {
+    if (rc != UNILLM_OK) throw Error(unillm_hip_last_error());
+}
+}  // namespace
+
+LayerKVCache LayerKVCache::with_capacity(int64_t n_kv_heads, int64_t head_dim,
+                                         int64_t max_seq_len, float rope_theta) {
+    LayerKVCache c;
+    check_msg(unillm_hip_kv_cache_create(n_kv_heads, head_dim, max_seq_len, rope_theta, &c.c_));
+    c.n_kv_heads_ = n_kv_heads;
+    c.head_dim_ = head_dim;
+    c.max_seq_ = max_seq_len;
+    return c;
+}
+
+LayerKVCache::~LayerKVCache() {
+    if (c_) unillm_hip_kv_cache_destroy(c_);
+}
+
+LayerKVCache::LayerKVCache(LayerKVCache&& o) noexcept
+    : c_(o.c_), n_kv_heads_(o.n_kv_heads_), head_dim_(o.head_dim_), max_seq_(o.max_seq_) {
+    o.c_ = nullptr;
+}
+
+LayerKVCache& LayerKVCache::operator=(LayerKVCache&& o) noexcept {
+    if (this != &o) {
+        if (c_) unillm_hip_kv_cache_destroy(c_);
+        c_ = o.c_;
+        n_kv_heads_ = o.n_kv_heads_;
+        head_dim_ = o.head_dim_;
+        max_seq_ = o.max_seq_;
+        o.c_ = nullptr;
+    }
+    return *this;
+}
+
+int64_t LayerKVCache::seq_len() const {
+    int64_t n = 0;
+    check_msg(unillm_hip_kv_cache_length(c_, &n));
+    return n;
+}
+
+void LayerKVCache::clear() { check_msg(unillm_hip_kv_cache_clear(c_)); }
+
+void LayerKVCache::truncate(int64_t len) { check_msg(unillm_hip_kv_cache_truncate(c_, len)); }
+
+Tensor LayerKVCache::attend(const Tensor& qkv, int64_t n_heads, void* stream) {
+    if (!qkv.device().is_hip() || qkv.shape().size() != 2)
+        throw Error("attention: qkv must be a [m, (n_heads + 2 n_kv_heads) head_dim] HIP tensor");
+    if (n_heads < 1 || qkv.dim(-1) != (n_heads + 2 * n_kv_heads_) * head_dim_)
+        throw Error("attention: qkv width " + std::to_string(qkv.dim(-1)) + " is not (" +
+                    std::to_string(n_heads) + " + 2 x " + std::to_string(n_kv_heads_) + ") x " +
+                    std::to_string(head_dim_));
+    const int64_t m = qkv.dim(0);
+    Tensor out = Tensor::empty({m, n_heads * head_dim_}, qkv.device());
+    check_msg(unillm_hip_attention_decode(c_, qkv.data(), m, n_heads, out.data_mut(), stream));
+    return out;
+}
+
+KVCache KVCache::with_capacity(size_t num_layers, int64_t n_kv_heads, int64_t head_dim,
+                               int64_t max_seq_len, float rope_theta) {
+    KVCache c;
+    c.layers_.reserve(num_layers);
+    for (size_t i = 0; i < num_layers; ++i)
+        c.layers_.push_back(LayerKVCache::with_capacity(n_kv_heads, head_dim, max_seq_len, rope_theta));
+    return c;
+}
+
+LayerKVCache& KVCache::layer_mut(size_t i) {
+    if (i >= layers_.size()) throw Error("layer index out of range");
+    return layers_[i];
+}
+
+const LayerKVCache& KVCache::layer(size_t i) const {
+    if (i >= layers_.size()) throw Error("layer index out of range");
+    return layers_[i];
+}
+
+int64_t KVCache::seq_len() const { return layers_.empty() ? 0 : layers_[0].seq_len(); }
+
+int64_t KVCache::max_seq_len() const { return layers_.empty() ? 0 : layers_[0].max_seq_len(); }
+
+void KVCache::clear() {
+    for (auto& l : layers_) l.clear();
+}
+
 }  // namespace unillm

@@ -14,6 +14,9 @@
 //   candle QMatMul (Arc)   used at llama.rs:1184-1195       QuantLinear
 //   weight_loader_core.rs:504-608  GGUFWeightLoader       GgufWeightLoader
 //   weight_loader_core.rs:760-798  gguf_to_hf_name        gguf_to_hf_name
+//   kv_cache.rs:28-183     LayerKVCache                    LayerKVCache (HIP, f32)
+//   kv_cache.rs:193-270    KVCache                         KVCache
+//   llama.rs:1044-1150     forward_with_cache after the projections   LayerKVCache::attend
 //
 // Errors are exceptions carrying the reference's anyhow text ("QMatMul
 // forward failed: ...").  All device work goes through include/unillm_hip.h.
@@ -130,6 +133,62 @@ private:
     unillm_qweight* w_ = nullptr;
     int qtype_ = 0;
     int64_t n_ = 0, k_ = 0;
+};
+
+// ---- KV cache and decode attention ------------------------------------------------------------
+// One decoder layer's cache for one sequence on the HIP device: K and V of n_kv_heads
+// heads, max_seq_len positions of head_dim f32 (kv_cache.rs:28-183; the reference's
+// buffers are [1, heads, seq, hd] candle tensors on the CPU).  Non-copyable, movable.
+class LayerKVCache {
+public:
+    // LayerKVCache::with_capacity(max_seq_len) (kv_cache.rs:46-53), with the shapes and
+    // the RoPE base that the reference takes from the model config at append time.
+    static LayerKVCache with_capacity(int64_t n_kv_heads, int64_t head_dim, int64_t max_seq_len,
+                                      float rope_theta = 10000.0f);
+    ~LayerKVCache();
+    LayerKVCache(LayerKVCache&& o) noexcept;
+    LayerKVCache& operator=(LayerKVCache&& o) noexcept;
+    LayerKVCache(const LayerKVCache&) = delete;
+    LayerKVCache& operator=(const LayerKVCache&) = delete;
+
+    bool is_empty() const { return seq_len() == 0; }  // kv_cache.rs:56-58
+    int64_t seq_len() const;                           // kv_cache.rs:74-76
+    int64_t max_seq_len() const { return max_seq_; }   // kv_cache.rs:79-81
+    void clear();                                      // kv_cache.rs:61-64
+    // Keep the first len positions (a rolled-back step); no reference counterpart.
+    void truncate(int64_t len);
+    // The part of LlamaAttention::forward_with_cache after the q / k / v projections
+    // (llama.rs:1044-1150): qkv [m, (n_heads + 2 n_kv_heads) head_dim] on the HIP device
+    // (a fused qkv handle's output) -> RoPE at positions seq_len() .., k and v appended
+    // (LayerKVCache::append, kv_cache.rs:91-130, including its overflow error), causal
+    // softmax attention -> [m, n_heads head_dim], freshly allocated.
+    Tensor attend(const Tensor& qkv, int64_t n_heads, void* stream = nullptr);
+
+    int64_t n_kv_heads() const { return n_kv_heads_; }
+    int64_t head_dim() const { return head_dim_; }
+    unillm_kv_cache* handle() const { return c_; }
+
+private:
+    LayerKVCache() = default;
+    unillm_kv_cache* c_ = nullptr;
+    int64_t n_kv_heads_ = 0, head_dim_ = 0, max_seq_ = 0;
+};
+
+// The model's caches, one LayerKVCache per decoder layer (kv_cache.rs:193-270).
+class KVCache {
+public:
+    static KVCache with_capacity(size_t num_layers, int64_t n_kv_heads, int64_t head_dim,
+                                 int64_t max_seq_len, float rope_theta = 10000.0f);
+    size_t num_layers() const { return layers_.size(); }
+    LayerKVCache& layer_mut(size_t i);
+    const LayerKVCache& layer(size_t i) const;
+    int64_t seq_len() const;  // layer 0's, as the reference reports it
+    int64_t max_seq_len() const;
+    bool is_empty() const { return seq_len() == 0; }
+    void clear();
+
+private:
+    std::vector<LayerKVCache> layers_;
 };
 
 // ---- ops dispatch ----------------------------------------------------------------------------

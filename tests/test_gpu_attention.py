@@ -108,8 +108,8 @@ def test_attention_overflow_and_limits():
 
 
 def test_attention_graph_replays_match_eager():
-    # the chunks of a kv head are merged by the last workgroup to arrive, through a
-    # per-kv-head counter in the cache handle that the merging workgroup resets: a
+    # a call is two launches (per-chunk partial results in the stream workspace, then
+    # the merge) and the cache length is host state baked into the captured launch: a
     # captured call replayed several times (eager work and synchronisations between
     # the replays) must give the eager result every time, bit for bit
     H, KVH, D, L = 32, 8, 128, 700

@@ -19,7 +19,7 @@ from unillm_amd import (PATH_DECODE_MFMA, PATH_GEMV, PATH_PREFILL_MFMA, HipError
 
 pytestmark = pytest.mark.gpu
 
-TOL = {PATH_GEMV: 1e-3, PATH_DECODE_MFMA: 1e-3, PATH_PREFILL_MFMA: 2e-2}
+TOL = {PATH_GEMV: 1e-3, PATH_DECODE_MFMA: 1e-3, PATH_PREFILL_MFMA: 1e-3}  # Q4_0 / Q8_0: f16 operands
 
 
 def _blocks(qtype, n, k, seed):
@@ -93,7 +93,7 @@ def test_swiglu(qtype, m, i_rows, k, path, fused):
     assert act.shape == (m, i_rows)
     g = oracle.qmatmul_f64(qtype, gate, x, i_rows, k)
     u = oracle.qmatmul_f64(qtype, up, x, i_rows, k)
-    tol = {PATH_GEMV: 2e-3, PATH_DECODE_MFMA: 2e-3, PATH_PREFILL_MFMA: 3e-2}[path]
+    tol = 2e-3
     assert oracle.normwise_error(act, _silu_mul(g, u)) < tol
     # the same as the activation applied to the kernel's own gate / up outputs
     mine = _silu_mul(plain[:, :i_rows].astype(np.float64), plain[:, i_rows:].astype(np.float64))
@@ -144,7 +144,7 @@ def test_layer_norm_matmul(qtype, m, n, k, path, bias, offset):
     torch.cuda.synchronize()
     xn = _layer_norm(x, gamma, beta, 1e-6)
     ref = oracle.qmatmul_f64(qtype, blocks, xn.astype(np.float32), n, k)
-    tol = {PATH_GEMV: 1e-3, PATH_DECODE_MFMA: 1e-3, PATH_PREFILL_MFMA: 2e-2}[path]
+    tol = TOL[path]
     assert oracle.normwise_error(y.cpu().numpy(), ref) < tol
 
 

@@ -575,10 +575,56 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
 // group of 8 normalized values converted to the MFMA operand type -- f16 in the
 // decode kernel's order 0 2 1 3 4 6 5 7, or bf16 in order -- and y's row r
 // zeroed over ny columns.
+// The power-of-two row scale of an f16 operand row whose largest magnitude is mx:
+// the row is multiplied by 2^(15 - e) (mx < 2^e), so its largest value lands in
+// [2^14, 2^15) whatever the row's range; thread 0 stores the inverse, the output
+// factor 2^(e - 15), at *rs.  Zero or non-finite rows keep the factor 1.  Both
+// scalings are exact, so a row and the same row times a power of two give the
+// same f16 operand.
+__device__ __forceinline__ float f16_row_scale(float mx, float* rs) {
+    int e = 0;
+    const bool ok = mx > 0.0f && mx <= 3.402823466e38f;
+    if (ok) (void)frexpf(mx, &e);
+    e = e < -111 ? -111 : e;  // keep 2^(15 - e) and 2^(e - 15) in range
+    if (threadIdx.x == 0) *rs = ok ? ldexpf(1.0f, e - 15) : 1.0f;
+    return ok ? ldexpf(1.0f, 15 - e) : 1.0f;
+}
+
+// x[m, k] -> f16 rows in the fragment order (each aligned 8 as 0 2 1 3 4 6 5 7),
+// each row scaled by its power of two (f16_row_scale; the factor to undo it in
+// rs[row]); y row zeroed over [0, yn) when yn > 0 (a split k adds into it).  One
+// workgroup per row: the max pass reads the row from HBM, the conversion re-reads
+// it from cache.
+__global__ __launch_bounds__(256) void xrows_kernel(const float* __restrict__ x, int64_t k,
+                                                    uint4* __restrict__ xh, float* __restrict__ rs,
+                                                    float* __restrict__ y, int64_t yn) {
+    __shared__ float red[4];
+    const int64_t r = blockIdx.x;
+    const float4* xr = reinterpret_cast<const float4*>(x + r * k);
+    float mx = 0.0f;
+    for (int64_t i = threadIdx.x; i < k / 4; i += 256) {
+        const float4 a = xr[i];
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    const float sc = f16_row_scale(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), rs + r);
+    for (int64_t i = threadIdx.x; i < k / 8; i += 256) {
+        const float4 a = xr[2 * i], b = xr[2 * i + 1];
+        xh[r * (k / 8) + i] = make_uint4(pk_f16(a.x * sc, a.z * sc), pk_f16(a.y * sc, a.w * sc),
+                                         pk_f16(b.x * sc, b.z * sc), pk_f16(b.y * sc, b.w * sc));
+    }
+    for (int64_t i = threadIdx.x; i < yn; i += 256) y[r * yn + i] = 0.0f;
+}
+
+// rs != nullptr (f16 only): each row scaled by its power of two as in xrows_kernel.
 template <bool F16PERM>
 __global__ __launch_bounds__(1024) void norm_convert_kernel(const float* __restrict__ x, int64_t k,
                                                            NormArgs norm, uint4* __restrict__ out,
-                                                           float* __restrict__ y, int64_t ny) {
+                                                           float* __restrict__ y, int64_t ny,
+                                                           float* __restrict__ rs) {
     __shared__ float red[16];
     const int64_t r = blockIdx.x;
     const float4* xr = reinterpret_cast<const float4*>(x + r * k);
@@ -609,8 +655,7 @@ __global__ __launch_bounds__(1024) void norm_convert_kernel(const float* __restr
     const float sd = sqrtf(block_sum(t) / (float)k + norm.eps);
     const float4* g4 = reinterpret_cast<const float4*>(norm.gamma);
     const float4* b4 = reinterpret_cast<const float4*>(norm.beta);
-    for (int64_t i = threadIdx.x; i < k / 8; i += 1024) {
-        float v[8];
+    auto values = [&](int64_t i, float (&v)[8]) {  // the normalized elements 8 i .. 8 i + 7
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const float4 a = xr[2 * i + h], g = g4[2 * i + h];
@@ -619,6 +664,32 @@ __global__ __launch_bounds__(1024) void norm_convert_kernel(const float* __restr
             v[4 * h + 1] = (a.y - mean) / sd * g.y + b.y;
             v[4 * h + 2] = (a.z - mean) / sd * g.z + b.z;
             v[4 * h + 3] = (a.w - mean) / sd * g.w + b.w;
+        }
+    };
+    float sc = 1.0f;
+    if (F16PERM && rs) {
+        float mx = 0.0f;
+        for (int64_t i = threadIdx.x; i < k / 8; i += 1024) {
+            float v[8];
+            values(i, v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[e]));
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        if (lane == 0) red[wv] = mx;
+        __syncthreads();
+        mx = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) mx = fmaxf(mx, red[w]);
+        sc = f16_row_scale(mx, rs + r);
+    }
+    for (int64_t i = threadIdx.x; i < k / 8; i += 1024) {
+        float v[8];
+        values(i, v);
+        if constexpr (F16PERM) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] *= sc;
         }
         uint32_t o[4];
         if constexpr (F16PERM) {
@@ -642,12 +713,22 @@ hipError_t launch_swiglu(const float* gu, int64_t m, int64_t I, float* act, hipS
 }
 
 hipError_t launch_norm_convert(const float* x, int64_t m, int64_t k, const NormArgs& norm,
-                               bool f16_perm, void* out, float* y, int64_t ny, hipStream_t s) {
+                               bool f16_perm, void* out, float* y, int64_t ny, hipStream_t s,
+                               float* rs) {
     if (m <= 0) return hipSuccess;
     if (f16_perm)
-        norm_convert_kernel<true><<<(unsigned)m, 1024, 0, s>>>(x, k, norm, static_cast<uint4*>(out), y, ny);
+        norm_convert_kernel<true>
+            <<<(unsigned)m, 1024, 0, s>>>(x, k, norm, static_cast<uint4*>(out), y, ny, rs);
     else
-        norm_convert_kernel<false><<<(unsigned)m, 1024, 0, s>>>(x, k, norm, static_cast<uint4*>(out), y, ny);
+        norm_convert_kernel<false>
+            <<<(unsigned)m, 1024, 0, s>>>(x, k, norm, static_cast<uint4*>(out), y, ny, nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_x_to_f16_rows(const float* x, int64_t m, int64_t k, void* out, float* rs,
+                                float* y, int64_t yn, hipStream_t s) {
+    if (m <= 0) return hipSuccess;
+    xrows_kernel<<<(unsigned)m, 256, 0, s>>>(x, k, static_cast<uint4*>(out), rs, y, yn);
     return hipGetLastError();
 }
 

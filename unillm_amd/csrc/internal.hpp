@@ -170,7 +170,15 @@ hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, floa
 // kernel's element order, or bf16), one workgroup per row; zeroes y rows
 // [0, m) of width ny when ny > 0 (a split k adds into it).
 hipError_t launch_norm_convert(const float* x, int64_t m, int64_t k, const NormArgs& norm,
-                               bool f16_perm, void* out, float* y, int64_t ny, hipStream_t s);
+                               bool f16_perm, void* out, float* y, int64_t ny, hipStream_t s,
+                               float* rs = nullptr);
+// x[m, k] (k % 32 == 0) -> f16 rows (round to nearest even) in the decode kernel's
+// element order (each aligned 8 as 0 2 1 3 4 6 5 7), each row scaled by a power
+// of two that puts its largest magnitude in [2^14, 2^15); rs[row] <- the factor
+// that undoes it.  y row r zeroed over [0, yn) when yn > 0.  launch_norm_convert
+// with rs != nullptr (f16) scales its rows the same way.
+hipError_t launch_x_to_f16_rows(const float* x, int64_t m, int64_t k, void* out, float* rs,
+                                float* y, int64_t yn, hipStream_t s);
 // act[m, I] = silu(g[m, i]) * u[m, i] with g, u the two halves of each row of
 // gu[m, 2 I] (the SwiGLU of the MFMA paths, after their store)
 hipError_t launch_swiglu(const float* gu, int64_t m, int64_t I, float* act, hipStream_t s);

@@ -1,15 +1,24 @@
-// prefill.hip -- fused dequant + bf16 MFMA GEMM for prefill (m >= 65).
+// prefill.hip -- fused dequant + f16 / bf16 MFMA GEMM for prefill (m >= 65).
 //
 // y[m, n] = x[m, k] . dequant(W)[n, k]^T, the prefill call of QMatMul::forward
-// (crates/runtime/src/models_v2/llama.rs:1188, 1329) with x f32 rounded to
-// bf16 on the device, weights dequantized exactly ((q - 8) * d, or q * d for
-// Q8_0, in fp32) and rounded once to bf16, fp32 accumulation on the gfx950
-// matrix cores (v_mfma_f32_16x16x32_bf16).  Bound: MFMA (2 m n k flops over
-// ~n k / 32 * 18 + 4 m k + 4 m n bytes).
+// (crates/runtime/src/models_v2/llama.rs:1188, 1329), fp32 accumulation on the
+// gfx950 matrix cores.  Bound: MFMA (2 m n k flops over ~n k / 32 * 18 + 4 m k +
+// 4 m n bytes).
+//   - Q4_0 / Q8_0: f16 operands (v_mfma_f32_16x16x32_f16).  Each row of x is
+//     scaled by a power of two that puts its largest magnitude in [2^14, 2^15)
+//     and rounded to f16 (xrows_kernel, or the fused layer norm); each weight
+//     (q - 8) d 2^-E is built from its code with the f16 magic number and
+//     rounded once (E: the weight's exponent offset).  Both scalings are exact
+//     and are undone on the output, so any finite x works, x and 2 x give the
+//     same operands, and the operands keep 11 significant bits.  ~1.75 VALU a
+//     weight, against ~3.25 for the fp32 dequant and bf16 rounding the K-quants
+//     keep: 2-8 % faster per call, measured on one box.
+//   - Q4_K / Q6_K: x rounded to bf16 (x_to_bf16_kernel), weights dequantized
+//     exactly in fp32 and rounded once to bf16 (v_mfma_f32_16x16x32_bf16).
 //
-// x is first rounded to bf16 once (x_to_bf16_kernel, into the stream's
-// workspace): the GEMM re-reads x once per 256-column tile, so half the bytes,
-// and no conversion sits in its inner loop.
+// x is converted once, into the stream's workspace: the GEMM re-reads x once
+// per 256-column tile, so half the bytes, and no conversion sits in its inner
+// loop.
 //
 // Tile per workgroup: BM rows of x (BM = 256 or 128) x 256 weight rows
 // (output columns), k in steps of 64 (two blocks).  Eight waves (two per
@@ -22,7 +31,9 @@
 //   - Each lane reads the 8 payload bytes behind its MFMA B fragment and
 //     dequantizes them in registers; every weight is dequantized once (a 2 x 4
 //     grid of waves halves the A reads from LDS but dequantizes each column
-//     twice: measured 10-30 % slower, the VALU being the scarcer unit).
+//     twice: measured 10-30 % slower with the bf16 dequant, and still 5-10 %
+//     slower with the f16 one, whose doubled cost matches the bf16 dequant done
+//     once).
 //   - The LDS reads are inline asm with explicit waits, so the compiler never
 //     drains the ring's later stages before them; a step waits for its own
 //     stage (vmcnt in issue order) and meets the other waves at a bare
@@ -60,6 +71,9 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int PBN = 256;         // output columns per workgroup
 constexpr int PBK = 64;          // k per step (two blocks)
@@ -108,10 +122,61 @@ __device__ __forceinline__ bf16x8 dequant8(u32x2 raw, int shift, float d, float 
 #pragma unroll
         for (int e = 0; e < 4; ++e) f[4 * h + e] = fmaf(c[e], d, off);
     }
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     const u32x4 p = {pack_bf16(f[0], f[1]), pack_bf16(f[2], f[3]), pack_bf16(f[4], f[5]),
                      pack_bf16(f[6], f[7])};
     return __builtin_bit_cast(bf16x8, p);
+}
+
+__device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
+    uint32_t r;  // round to nearest even, lo in the low half
+    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(r) : "v"(lo), "v"(hi));
+    return r;
+}
+
+// (a & mask) | bits in one instruction (the compiler splits it in two)
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(mask), "v"(bits));
+    return r;
+}
+
+// f16 pair (v - bias) * sc, v holding two f16 1024 + code: exact but the last step
+__device__ __forceinline__ uint32_t scale2(uint32_t v, f16x2 bias, f16x2 sc) {
+    return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, v) - bias) * sc);
+}
+
+// Q4_0 / Q8_0 on f16 operands: one lane's B fragment of one 32-block, its 8
+// codes (one per byte of `raw`: a nibble of each for Q4_0, selected by `mask`)
+// -> 8 f16 in the order 0 2 1 3 4 6 5 7 (x is stored in that order).  (code |
+// 0x6400) is the f16 1024 + code exactly; minus `bias` it is the signed code
+// exactly, and times sc = d 2^-E it rounds once, as (q - 8) d 2^-E computed in
+// f32 and rounded to f16 would.  A low nibble lands as 1024 + q (bias 1032, sc =
+// d 2^-E), a high nibble in place as 1024 + 16 q (bias 1152, sc = d 2^-E / 16), a
+// Q8_0 byte as 1024 + q + 128 (bias 1152).  About 1.75 VALU per weight, against
+// ~3.25 for the fp32 dequant and bf16 rounding of dequant8.
+template <int QT>
+__device__ __forceinline__ f16x8 dequant8_f16(u32x2 raw, uint32_t mask, f16x2 bias, f16x2 sc) {
+    u32x4 o;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        if constexpr (QT == UNILLM_QTYPE_Q4_0) {
+            const uint32_t w = raw[h] ^ 0x88888888u;  // signed nibbles -> q
+            o[2 * h] = scale2(and_or(w, mask, 0x64006400u), bias, sc);           // bytes 0, 2
+            o[2 * h + 1] = scale2(and_or(w >> 8, mask, 0x64006400u), bias, sc);  // bytes 1, 3
+        } else {
+            const uint32_t w = raw[h] ^ 0x80808080u;  // int8 -> q + 128
+            o[2 * h] = scale2(__builtin_amdgcn_perm(0x64646464u, w, 0x04020400u), bias, sc);
+            o[2 * h + 1] = scale2(__builtin_amdgcn_perm(0x64646464u, w, 0x04030401u), bias, sc);
+        }
+    }
+    return __builtin_bit_cast(f16x8, o);
+}
+
+__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
 // x (f32) -> bf16, round to nearest even; 8 elements per thread per pass.  y[0, ny)
@@ -167,7 +232,9 @@ struct Ring {
     // stages: 4 for 128-row tiles (four fit in LDS; ~10 % over three measured),
     // 3 for 256-row tiles
     static constexpr int STAGES = BM == 128 ? 4 : 3;
-    static constexpr int BYTES = STAGES * STAGE;
+    // + the tile's row scales of x (f16 operands): BM floats after the ring
+    static constexpr int BYTES = STAGES * STAGE + (QT == UNILLM_QTYPE_Q4_0 || QT == UNILLM_QTYPE_Q8_0 ? BM * 4 : 0);
+    static constexpr int RS = STAGES * STAGE;
     static constexpr int CPB = 2 * QB / 16;            // 16-byte payload chunks per column
     static constexpr int AQ = BM / 8 / 8;              // A loads (8 rows each) per wave
     static constexpr int DMA = AQ + CPB / 2 + 1 + (KQ ? 1 : 0);  // direct loads per wave per stage
@@ -176,10 +243,12 @@ struct Ring {
 template <int QT, int BM, int NW>
 __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __restrict__ base,
                                                               int64_t rb,
-                                                              const __bf16* __restrict__ xb,
+                                                              const uint16_t* __restrict__ xb,
                                                               float* __restrict__ y, int M, int N,
                                                               int KB, int tiles_n, int tiles,
-                                                              int units_pad, int S, int add) {
+                                                              int units_pad, int S, int add,
+                                                              float wscale, float oscale,
+                                                              const float* __restrict__ rs) {
     static_assert(NW == 8, "the ring's load split assumes 8 waves");
     constexpr int QB = Ring<QT, BM>::QB;  // payload bytes per block
     // waves: RW row groups x CW column groups; wave (rw, cw) owns rows BM / RW * rw ..
@@ -191,6 +260,11 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
     constexpr int TI = WR / 16;                            // MFMA tiles along m per wave
     constexpr int TJ = WC / 16;                            // MFMA tiles along n per wave (4)
     using R = Ring<QT, BM>;
+    // Q4_0 / Q8_0: f16 operands (x rows in the order 0 2 1 3 4 6 5 7, each scaled by
+    // a power of two undone by rs[row]; weights scaled by wscale = 2^-E, undone by
+    // oscale = 2^E); K-quants: bf16
+    constexpr bool F16 = QT == UNILLM_QTYPE_Q4_0 || QT == UNILLM_QTYPE_Q8_0;
+    using VT = std::conditional_t<F16, f16x8, bf16x8>;
     constexpr int kStages = R::STAGES;
     constexpr int AQ = R::AQ;
     constexpr int CPB = R::CPB;
@@ -267,6 +341,14 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
     bool bval[TJ];
 #pragma unroll
     for (int j = 0; j < TJ; ++j) bval[j] = n0 + WC * cw + 16 * j + fr < N;
+    // f16 dequant constants of this lane (high nibbles: 1024 + 16 q, scale / 16)
+    const bool hnib = kNib && g >= 2;
+    const uint32_t nmask = hnib ? 0x00F000F0u : 0x000F000Fu;
+    const _Float16 bias1 = (_Float16)(QT == UNILLM_QTYPE_Q4_0 && !hnib ? 1032.0f : 1152.0f);
+    const f16x2 fbias = {bias1, bias1};
+    float wl[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) wl[j] = bval[j] ? (hnib ? wscale * 0.0625f : wscale) : 0.0f;
     // LDS byte offsets (within a stage) of this lane's reads; the row tile i and the
     // column tile j enter as immediate offsets.  A: row WR rw + 16 i + fr, chunk
     // 4 kk + g in slot (4 kk + g) ^ (row % 8), and row % 8 == fr % 8.
@@ -287,7 +369,15 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
 #pragma unroll
         for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // prologue: stages 0 .. kStages - 2 in flight
+    // prologue: the tile's row scales (f16 operands; wave 0, ahead of its ring loads, so
+    // the ring's waits cover them), then stages 0 .. kStages - 2 in flight
+    if constexpr (F16) {
+        if (wv == 0) {
+#pragma unroll
+            for (int q = 0; q < BM / 64; ++q)
+                dma4(rs + min(m0 + 64 * q + lane, M - 1), ring + R::RS + q * 256);
+        }
+    }
 #pragma unroll
     for (int d = 0; d < kStages - 1; ++d)
         if (d < nks) issue(ks0 + d);
@@ -338,7 +428,14 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
         }
         const bool b1ok = 2 * ks + 1 < KB;
         float d0[TJ], d1[TJ], o0[TJ], o1[TJ];
-        if constexpr (R::KQ) {
+        uint32_t sp[TJ];  // F16: the f16 scales d 2^-E of blocks 0 (low) and 1 (high)
+        if constexpr (F16) {
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+                sp[j] = pack_f16(__half2float(__ushort_as_half((uint16_t)sc[j])) * wl[j],
+                                 b1ok ? __half2float(__ushort_as_half((uint16_t)(sc[j] >> 16))) * wl[j]
+                                      : 0.0f);
+        } else if constexpr (R::KQ) {
             // the group header (Q4_K d | dmin << 16, Q6_K d) of each column tile, laid out
             // as the scales; sc[j] holds block 0's u16 in its low half, block 1's in its
             // high: Q4_K sc | m << 8, Q6_K the int8 scales of the two 16-weight halves
@@ -375,30 +472,30 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
                     o1[j] = -128.0f * d1[j];
                 }
             }
-        } else {
-            constexpr float kOff = QT == UNILLM_QTYPE_Q4_0 ? -8.0f : -128.0f;
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) {
-                d0[j] = bval[j] ? __half2float(__ushort_as_half((uint16_t)sc[j])) : 0.0f;
-                d1[j] = bval[j] && b1ok ? __half2float(__ushort_as_half((uint16_t)(sc[j] >> 16)))
-                                        : 0.0f;
-                o0[j] = d0[j] * kOff;
-                o1[j] = d1[j] * kOff;
-            }
         }
+        auto deq = [&](int j, int b) -> VT {
+            if constexpr (F16) {
+                const f16x2 s2 = __builtin_bit_cast(f16x2, sp[j]);
+                const f16x2 sb = b == 0 ? f16x2{s2[0], s2[0]} : f16x2{s2[1], s2[1]};
+                return dequant8_f16<QT>(raw[j][b], nmask, fbias, sb);
+            } else {
+                return dequant8<QT>(raw[j][b], bshift, b == 0 ? d0[j] : d1[j],
+                                    b == 0 ? o0[j] : o1[j]);
+            }
+        };
         // block 0's fragments first; block 1's are dequantized between the MFMAs of
         // the first 32 k (one column tile after every TI / TJ row tiles), so the
         // VALU work overlaps the matrix cores instead of following them
-        bf16x8 bfrag[TJ][2];
+        VT bfrag[TJ][2];
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) bfrag[j][0] = dequant8<QT>(raw[j][0], bshift, d0[j], o0[j]);
+        for (int j = 0; j < TJ; ++j) bfrag[j][0] = deq(j, 0);
         // A fragments, two ahead (one ahead leaves ~2 MFMAs to cover an LDS read;
         // deeper measured no better): fragment f = kk * TI + i at aoff[kk] + 2048 i
         constexpr int PF = 2;
-        bf16x8 afr[2 * TI];
+        VT afr[2 * TI];
         constexpr_for<PF>([&](auto F) {
             afr[F.value] = __builtin_bit_cast(
-                bf16x8, lds_read128<(F.value % TI) * 2048>(st + aoff[F.value / TI]));
+                VT, lds_read128<(F.value % TI) * 2048>(st + aoff[F.value / TI]));
         });
 #pragma unroll
         for (int f = 0; f < 2 * TI; ++f) {
@@ -406,7 +503,7 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
                 constexpr_for<2 * TI>([&](auto F) {
                     if (F.value == f + PF)
                         afr[F.value] = __builtin_bit_cast(
-                            bf16x8, lds_read128<(F.value % TI) * 2048>(st + aoff[F.value / TI]));
+                            VT, lds_read128<(F.value % TI) * 2048>(st + aoff[F.value / TI]));
                 });
                 asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(afr[f]));
             } else if (f + 1 < 2 * TI) {
@@ -417,17 +514,27 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
             const int kk = f / TI, i = f % TI;
 #pragma unroll
             for (int j = 0; j < TJ; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr[f], bfrag[j][kk], acc[i][j],
-                                                                    0, 0, 0);
+                acc[i][j] = mfma16(afr[f], bfrag[j][kk], acc[i][j]);
             if (kk == 0 && (i + 1) % (TI / TJ) == 0) {
                 const int j = (i + 1) / (TI / TJ) - 1;
-                bfrag[j][1] = dequant8<QT>(raw[j][1], bshift, d1[j], o1[j]);
+                bfrag[j][1] = deq(j, 1);
             }
         }
     }
 
     // ---- epilogue: lane holds C[4 (l / 16) + e][l % 16] of each 16 x 16 tile; the
-    // S k slices of a tile meet in y by f32 atomic adds onto zeros ----
+    // S k slices of a tile meet in y by f32 atomic adds onto zeros.  f16 operands: the
+    // output factor of row 16 i + 4 g + e is oscale times its row scale (from LDS:
+    // global loads here would wait for the stores before them) ----
+    float4 rsc[F16 ? TI : 1];
+    if constexpr (F16) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            const float4 r4 =
+                *reinterpret_cast<const float4*>(ring + R::RS + (WR * rw + 16 * i + 4 * g) * 4);
+            rsc[i] = make_float4(r4.x * oscale, r4.y * oscale, r4.z * oscale, r4.w * oscale);
+        }
+    }
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
         const int col = n0 + WC * cw + 16 * j + fr;
@@ -439,21 +546,24 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
                 const int row = m0 + WR * rw + 16 * i + 4 * g + e;
                 if (row >= M) continue;
                 float* dst = y + (int64_t)row * N + col;
-                if (S == 1) *dst = add ? *dst + acc[i][j][e] : acc[i][j][e];
-                else unsafeAtomicAdd(dst, acc[i][j][e]);  // onto zeros, or onto y with add
+                float v = acc[i][j][e];
+                if constexpr (F16) v *= e == 0 ? rsc[i].x : e == 1 ? rsc[i].y : e == 2 ? rsc[i].z : rsc[i].w;
+                if (S == 1) *dst = add ? *dst + v : v;
+                else unsafeAtomicAdd(dst, v);  // onto zeros, or onto y with add
             }
     }
 }
 
 template <int QT, int BM>
-hipError_t launch_bm(const QWeight& w, const __bf16* xb, int64_t m, float* y, int S,
-                     hipStream_t s, int add) {
+hipError_t launch_bm(const QWeight& w, const uint16_t* xb, const float* rs, int64_t m, float* y,
+                     int S, hipStream_t s, int add) {
     // x is addressed with 32-bit element offsets: launch in row chunks below 2^30 elements
     const int64_t chunk = std::max<int64_t>(BM, ((int64_t)1 << 30) / w.k / BM * BM);
     if (m > chunk) {
         for (int64_t r = 0; r < m; r += chunk) {
             hipError_t e =
-                launch_bm<QT, BM>(w, xb + r * w.k, std::min(chunk, m - r), y + r * w.n, S, s, add);
+                launch_bm<QT, BM>(w, xb + r * w.k, rs ? rs + r : nullptr, std::min(chunk, m - r),
+                                  y + r * w.n, S, s, add);
             if (e != hipSuccess) return e;
         }
         return hipSuccess;
@@ -468,9 +578,12 @@ hipError_t launch_bm(const QWeight& w, const __bf16* xb, int64_t m, float* y, in
     const int tiles_n = (int)((w.n + PBN - 1) / PBN);
     const int tiles = tiles_m * tiles_n;
     const int units_pad = (tiles * S + 7) / 8 * 8;
+    const bool f16 = QT == UNILLM_QTYPE_Q4_0 || QT == UNILLM_QTYPE_Q8_0;
+    const float wscale = f16 ? ldexpf(1.0f, -w.f16_exp) : 1.0f;
+    const float oscale = f16 ? ldexpf(1.0f, w.f16_exp) : 1.0f;
     prefill_kernel<QT, BM, kWaves><<<units_pad, kWaves * 64, Ring<QT, BM>::BYTES, s>>>(
         w.base, w.row_bytes, xb, y, (int)m, (int)w.n, (int)w.kb, tiles_n, tiles, units_pad, S,
-        add);
+        add, wscale, oscale, rs);
     return hipGetLastError();
 }
 
@@ -497,38 +610,44 @@ PrefillPlan prefill_plan(const QWeight& w, int64_t m) {
 
 hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, float* y,
                                hipStream_t s, int epi, const NormArgs& norm) {
-    // x in bf16 (the operand precision) in the stream's workspace: the GEMM
-    // re-reads x once per 256-column tile, so it reads half the bytes, and no
-    // conversion sits in its inner loop.  The same kernel zeroes y for a split k.
+    // x in the operand type (f16 rows with their power-of-two scales for Q4_0 /
+    // Q8_0, bf16 for the K-quants) in the stream's workspace: the GEMM re-reads x
+    // once per 256-column tile, so it reads half the bytes, and no conversion sits
+    // in its inner loop.  The same kernel zeroes y for a split k.
     const PrefillPlan plan = prefill_plan(w, m);
     const int64_t n = m * w.k;  // k % 32 == 0, so n % 8 == 0
+    const bool f16 = w.qtype == UNILLM_QTYPE_Q4_0 || w.qtype == UNILLM_QTYPE_Q8_0;
+    const size_t xbytes = ((size_t)n * 2 + 255) / 256 * 256;
     void* ws = nullptr;
-    hipError_t e = stream_workspace(s, (size_t)n * sizeof(__bf16), &ws);
+    hipError_t e = stream_workspace(s, xbytes + (f16 ? (size_t)m * sizeof(float) : 0), &ws);
     if (e != hipSuccess) return e;
+    float* rs = f16 ? reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + xbytes) : nullptr;
     const int add = epi == kEpiAdd;
     const int64_t n8 = n / 8, ny = plan.S > 1 && !add ? m * w.n : 0;
-    const int grid = (int)std::min<int64_t>((std::max(n8, ny / 4) + 255) / 256,
-                                            (int64_t)device_info().cu_count * 16);
     if (norm.gamma)
-        e = launch_norm_convert(x, m, w.k, norm, false, ws, y, ny > 0 ? w.n : 0, s);
+        e = launch_norm_convert(x, m, w.k, norm, f16, ws, y, ny > 0 ? w.n : 0, s, rs);
+    else if (f16)
+        e = launch_x_to_f16_rows(x, m, w.k, ws, rs, y, ny > 0 ? w.n : 0, s);
     else {
+        const int grid = (int)std::min<int64_t>((std::max(n8, ny / 4) + 255) / 256,
+                                                (int64_t)device_info().cu_count * 16);
         x_to_bf16_kernel<<<grid, 256, 0, s>>>(x, static_cast<uint4*>(ws), n8, y, ny);
         e = hipGetLastError();
     }
     if (e != hipSuccess) return e;
-    const __bf16* xb = static_cast<const __bf16*>(ws);
+    const uint16_t* xb = static_cast<const uint16_t*>(ws);
     if (w.qtype == UNILLM_QTYPE_Q4_K)
-        return plan.bm == 256 ? launch_bm<UNILLM_QTYPE_Q4_K, 256>(w, xb, m, y, 1, s, add)
-                              : launch_bm<UNILLM_QTYPE_Q4_K, 128>(w, xb, m, y, plan.S, s, add);
+        return plan.bm == 256 ? launch_bm<UNILLM_QTYPE_Q4_K, 256>(w, xb, rs, m, y, 1, s, add)
+                              : launch_bm<UNILLM_QTYPE_Q4_K, 128>(w, xb, rs, m, y, plan.S, s, add);
     if (w.qtype == UNILLM_QTYPE_Q6_K)
-        return plan.bm == 256 ? launch_bm<UNILLM_QTYPE_Q6_K, 256>(w, xb, m, y, 1, s, add)
-                              : launch_bm<UNILLM_QTYPE_Q6_K, 128>(w, xb, m, y, plan.S, s, add);
+        return plan.bm == 256 ? launch_bm<UNILLM_QTYPE_Q6_K, 256>(w, xb, rs, m, y, 1, s, add)
+                              : launch_bm<UNILLM_QTYPE_Q6_K, 128>(w, xb, rs, m, y, plan.S, s, add);
     const bool q4 = w.qtype == UNILLM_QTYPE_Q4_0;
     if (plan.bm == 256)
-        return q4 ? launch_bm<UNILLM_QTYPE_Q4_0, 256>(w, xb, m, y, 1, s, add)
-                  : launch_bm<UNILLM_QTYPE_Q8_0, 256>(w, xb, m, y, 1, s, add);
-    return q4 ? launch_bm<UNILLM_QTYPE_Q4_0, 128>(w, xb, m, y, plan.S, s, add)
-              : launch_bm<UNILLM_QTYPE_Q8_0, 128>(w, xb, m, y, plan.S, s, add);
+        return q4 ? launch_bm<UNILLM_QTYPE_Q4_0, 256>(w, xb, rs, m, y, 1, s, add)
+                  : launch_bm<UNILLM_QTYPE_Q8_0, 256>(w, xb, rs, m, y, 1, s, add);
+    return q4 ? launch_bm<UNILLM_QTYPE_Q4_0, 128>(w, xb, rs, m, y, plan.S, s, add)
+              : launch_bm<UNILLM_QTYPE_Q8_0, 128>(w, xb, rs, m, y, plan.S, s, add);
 }
 
 }  // namespace unillm

@@ -54,7 +54,7 @@ extern "C" {
 #define UNILLM_PATH_AUTO 0
 #define UNILLM_PATH_GEMV 1         /* fused dequant + GEMV (VALU int8 dot), m <= 4 */
 #define UNILLM_PATH_DECODE_MFMA 2  /* batched decode, f16 MFMA, fp32 accumulate */
-#define UNILLM_PATH_PREFILL_MFMA 3 /* prefill, LDS-staged f16 (Q4_0 / Q8_0) or bf16 (K-quants) MFMA, fp32 accumulate */
+#define UNILLM_PATH_PREFILL_MFMA 3 /* prefill, LDS-staged f16 MFMA (x rows scaled by powers of two), fp32 accumulate */
 
 typedef struct unillm_qweight unillm_qweight;
 typedef struct unillm_kv_cache unillm_kv_cache;

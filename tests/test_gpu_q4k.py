@@ -155,9 +155,9 @@ def test_q4k_prefill_parity(m, n, k):
     y = ql.forward(_dev(x))
     torch.cuda.synchronize()
     ref = oracle.qmatmul_f64(Q4_K, blocks, x, n, k)
-    assert oracle.normwise_error(y.cpu().numpy(), ref) < 2e-2
-    # the bf16 operands keep it far inside the bar; a wrong scale or min would not
-    assert oracle.normwise_error(y.cpu().numpy(), ref) < 5e-3
+    # f16 operands (x rows scaled by powers of two; sc and the minimum rounded to
+    # f16 once each, the weight once more), the decode bar
+    assert oracle.normwise_error(y.cpu().numpy(), ref) < 1e-3
 
 
 def test_q4k_prefill_small_m_explicit_path():
@@ -166,7 +166,7 @@ def test_q4k_prefill_small_m_explicit_path():
     blocks, x = _gemv_case(m, n, k, seed=71)
     y = QuantLinear.from_blocks(Q4_K, n, k, blocks).forward(_dev(x), path=PATH_PREFILL_MFMA)
     ref = oracle.qmatmul_f64(Q4_K, blocks, x, n, k)
-    assert oracle.normwise_error(y.cpu().numpy(), ref) < 5e-3
+    assert oracle.normwise_error(y.cpu().numpy(), ref) < 1e-3
 
 
 def test_q4k_prefill_large_tiles_rows_sampled():
@@ -179,7 +179,7 @@ def test_q4k_prefill_large_tiles_rows_sampled():
     torch.cuda.synchronize()
     rows = np.array([0, 1, 255, 256, 1023, m - 77, m - 1])
     ref = oracle.qmatmul_f64(Q4_K, blocks, x[rows], n, k)
-    assert oracle.normwise_error(y.cpu().numpy()[rows], ref) < 5e-3
+    assert oracle.normwise_error(y.cpu().numpy()[rows], ref) < 1e-3
     y2 = ql.forward(_dev(x) * 2.0)
     torch.cuda.synchronize()
     assert np.array_equal(y2.cpu().numpy(), 2.0 * y.cpu().numpy())  # no k split here

@@ -79,7 +79,7 @@ def test_q6k_decode_parity(m, n, k):
 @pytest.mark.parametrize("m,n,k", [(65, 300, 1024), (128, 512, 4096), (130, 256, 8192),
                                    (512, 1024, 4096)])
 def test_q6k_prefill_parity(m, n, k):
-    _check(m, n, k, PATH_PREFILL_MFMA, 5e-3, seed=m + 3 * n + k)
+    _check(m, n, k, PATH_PREFILL_MFMA, 1e-3, seed=m + 3 * n + k)  # f16 operands
 
 
 def test_q6k_prefill_large_tiles_rows_sampled():
@@ -88,7 +88,7 @@ def test_q6k_prefill_large_tiles_rows_sampled():
     ql = QuantLinear.from_blocks(Q6_K, n, k, blocks)
     y = ql.forward(_dev(x)).cpu().numpy()
     rows = np.array([0, 1, 255, 256, 1023, m - 77, m - 1])
-    assert oracle.normwise_error(y[rows], oracle.qmatmul_f64(Q6_K, blocks, x[rows], n, k)) < 5e-3
+    assert oracle.normwise_error(y[rows], oracle.qmatmul_f64(Q6_K, blocks, x[rows], n, k)) < 1e-3
 
 
 def test_q6k_layout_limits():

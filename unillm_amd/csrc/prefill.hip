@@ -1,20 +1,18 @@
-// prefill.hip -- fused dequant + f16 / bf16 MFMA GEMM for prefill (m >= 65).
+// prefill.hip -- fused dequant + f16 MFMA GEMM for prefill (m >= 65).
 //
 // y[m, n] = x[m, k] . dequant(W)[n, k]^T, the prefill call of QMatMul::forward
 // (crates/runtime/src/models_v2/llama.rs:1188, 1329), fp32 accumulation on the
 // gfx950 matrix cores.  Bound: MFMA (2 m n k flops over ~n k / 32 * 18 + 4 m k +
 // 4 m n bytes).
-//   - Q4_0 / Q8_0: f16 operands (v_mfma_f32_16x16x32_f16).  Each row of x is
-//     scaled by a power of two that puts its largest magnitude in [2^14, 2^15)
-//     and rounded to f16 (xrows_kernel, or the fused layer norm); each weight
-//     (q - 8) d 2^-E is built from its code with the f16 magic number and
-//     rounded once (E: the weight's exponent offset).  Both scalings are exact
-//     and are undone on the output, so any finite x works, x and 2 x give the
-//     same operands, and the operands keep 11 significant bits.  ~1.75 VALU a
-//     weight, against ~3.25 for the fp32 dequant and bf16 rounding the K-quants
-//     keep: 2-8 % faster per call, measured on one box.
-//   - Q4_K / Q6_K: x rounded to bf16 (x_to_bf16_kernel), weights dequantized
-//     exactly in fp32 and rounded once to bf16 (v_mfma_f32_16x16x32_bf16).
+// Operands are f16 (v_mfma_f32_16x16x32_f16).  Each row of x is scaled by a
+// power of two that puts its largest magnitude in [2^14, 2^15) and rounded to
+// f16 (xrows_kernel, or the fused layer norm); each weight is built from its
+// code with the f16 magic number and rounded once, scaled by 2^-E (E: the
+// weight's exponent offset).  Both scalings are exact and are undone on the
+// output, so any finite x works, x and 2 x give the same operands, and the
+// operands keep 11 significant bits.  ~1.75 VALU a weight (dequant8_f16),
+// against ~3.25 for an fp32 dequant rounded to bf16 (this kernel's earlier
+// form): 2-8 % faster per call, measured on one box.
 //
 // x is converted once, into the stream's workspace: the GEMM re-reads x once
 // per 256-column tile, so half the bytes, and no conversion sits in its inner
@@ -25,7 +23,7 @@
 // SIMD) side by side: wave w owns all BM rows x columns 32 w .. 32 w + 31,
 // BM / 16 x 2 MFMA tiles of 16 x 16, fp32 accumulators in registers.
 //   - Operands reach LDS by direct global -> LDS loads through a 3- or 4-stage ring
-//     (two k steps in flight, no VGPR staging): A as bf16 rows with an XOR
+//     (two k steps in flight, no VGPR staging): A as f16 rows with an XOR
 //     swizzle of 16-byte chunks, B as the raw Q4_0 / Q8_0 payload bytes and
 //     scales of the tile's 256 weight rows.
 //   - Each lane reads the 8 payload bytes behind its MFMA B fragment and
@@ -55,7 +53,6 @@
 // multiple of 8): each XCD gets a contiguous run of tiles in row-major
 // (m-tile, n-tile) order, i.e. mostly one m-tile, whose A rows then stay in
 // that XCD's L2 while its CUs sweep the n-tiles.
-#include <hip/hip_bf16.h>
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
@@ -68,7 +65,6 @@
 namespace unillm {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -77,55 +73,10 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int PBN = 256;         // output columns per workgroup
 constexpr int PBK = 64;          // k per step (two blocks)
-constexpr int PLD = PBK + 8;     // LDS row stride in bf16 (144 B): spreads rows over banks
 #ifndef PREFILL_WAVES
 #define PREFILL_WAVES 8
 #endif
 constexpr int kWaves = PREFILL_WAVES;  // waves per workgroup (8: two per SIMD)
-
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-    // round to nearest even; the pair in one dword, lo in the low half
-    // (v_cvt_pk_bf16_f32 directly: two scalar conversions compile to two of them
-    // plus a shift and an or)
-    uint32_t r;
-    asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(lo), "v"(hi));
-    return r;
-}
-
-// One lane's B fragment of one 32-block: 8 codes (4 per dword of `raw`, in
-// element order) -> 8 bf16 of code * d + off (off = -8 d for Q4_0, -128 d for
-// Q8_0, the codes being unsigned here).  Exact in fp32, one rounding to bf16.
-//
-// Q4_K: the same 4-bit codes with d = d_group * sc and off = -dmin_group * m of
-// the block (both exact in fp32), so (d sc) q - dmin m is exact too before the
-// one rounding to bf16.
-template <int QT>
-__device__ __forceinline__ bf16x8 dequant8(u32x2 raw, int shift, float d, float off) {
-    constexpr bool kNib = QT == UNILLM_QTYPE_Q4_0 || QT == UNILLM_QTYPE_Q4_K;
-    constexpr uint32_t kFlip = kNib ? 0x88888888u : 0x80808080u;
-    uint32_t u[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const uint32_t w = raw[h] ^ kFlip;  // signed codes -> unsigned (q, or q + 128)
-        u[h] = kNib ? (w >> shift) & 0x0F0F0F0Fu : w;
-    }
-    float f[8];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        // v_cvt_f32_ubyte{0..3} directly: the compiler otherwise rewrites the byte
-        // masks (the codes are known to be < 16) into bit-field extracts plus ubyte0
-        float c[4];
-        asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(c[0]) : "v"(u[h]));
-        asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(c[1]) : "v"(u[h]));
-        asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(c[2]) : "v"(u[h]));
-        asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(c[3]) : "v"(u[h]));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) f[4 * h + e] = fmaf(c[e], d, off);
-    }
-    const u32x4 p = {pack_bf16(f[0], f[1]), pack_bf16(f[2], f[3]), pack_bf16(f[4], f[5]),
-                     pack_bf16(f[6], f[7])};
-    return __builtin_bit_cast(bf16x8, p);
-}
 
 __device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
     uint32_t r;  // round to nearest even, lo in the low half
@@ -145,28 +96,48 @@ __device__ __forceinline__ uint32_t scale2(uint32_t v, f16x2 bias, f16x2 sc) {
     return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, v) - bias) * sc);
 }
 
-// Q4_0 / Q8_0 on f16 operands: one lane's B fragment of one 32-block, its 8
-// codes (one per byte of `raw`: a nibble of each for Q4_0, selected by `mask`)
-// -> 8 f16 in the order 0 2 1 3 4 6 5 7 (x is stored in that order).  (code |
-// 0x6400) is the f16 1024 + code exactly; minus `bias` it is the signed code
-// exactly, and times sc = d 2^-E it rounds once, as (q - 8) d 2^-E computed in
-// f32 and rounded to f16 would.  A low nibble lands as 1024 + q (bias 1032, sc =
-// d 2^-E), a high nibble in place as 1024 + 16 q (bias 1152, sc = d 2^-E / 16), a
-// Q8_0 byte as 1024 + q + 128 (bias 1152).  About 1.75 VALU per weight, against
-// ~3.25 for the fp32 dequant and bf16 rounding of dequant8.
+// f16 pair (v - bias) * sc - off (Q4_K's block minimum)
+__device__ __forceinline__ uint32_t scale2o(uint32_t v, f16x2 bias, f16x2 sc, f16x2 off) {
+    return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, v) - bias) * sc - off);
+}
+
+// One lane's B fragment of one 32-block: its 8 codes (one per byte of `raw`: a
+// nibble of each for Q4_0 / Q4_K, selected by `mask`) -> 8 f16 in the order
+// 0 2 1 3 4 6 5 7 (x is stored in that order).  (code | 0x6400) is the f16
+// 1024 + code exactly; minus `bias` it is the signed code exactly, and times sc =
+// d 2^-E it rounds once, as (q - 8) d 2^-E computed in f32 and rounded to f16
+// would (E: the weight's exponent offset).
+//   Q4_0: a low nibble lands as 1024 + q (bias 1032, sc = d 2^-E), a high nibble
+//         in place as 1024 + 16 q (bias 1152, sc = d 2^-E / 16);
+//   Q4_K: the same with bias 1024, sc = d sc_b 2^-E (/ 16), minus off = dmin m_b
+//         2^-E (sc and off rounded to f16 once each, the weight once more);
+//   Q8_0 / Q6_K: a byte (int8 code, flipped to q + 128) as 1024 + q + 128, bias
+//         1152 (Q6_K: the code is q - 32, sc = d sc_half 2^-E).
+// About 1.75 VALU per weight (Q4_K 2.25), against ~3.25 for an fp32 dequant
+// rounded to bf16 (this kernel's earlier form).
 template <int QT>
-__device__ __forceinline__ f16x8 dequant8_f16(u32x2 raw, uint32_t mask, f16x2 bias, f16x2 sc) {
+__device__ __forceinline__ f16x8 dequant8_f16(u32x2 raw, uint32_t mask, f16x2 bias, f16x2 sc,
+                                              f16x2 off) {
+    constexpr bool kNib = QT == UNILLM_QTYPE_Q4_0 || QT == UNILLM_QTYPE_Q4_K;
     u32x4 o;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        if constexpr (QT == UNILLM_QTYPE_Q4_0) {
+        uint32_t p0, p1;
+        if constexpr (kNib) {
             const uint32_t w = raw[h] ^ 0x88888888u;  // signed nibbles -> q
-            o[2 * h] = scale2(and_or(w, mask, 0x64006400u), bias, sc);           // bytes 0, 2
-            o[2 * h + 1] = scale2(and_or(w >> 8, mask, 0x64006400u), bias, sc);  // bytes 1, 3
+            p0 = and_or(w, mask, 0x64006400u);         // bytes 0, 2
+            p1 = and_or(w >> 8, mask, 0x64006400u);    // bytes 1, 3
         } else {
             const uint32_t w = raw[h] ^ 0x80808080u;  // int8 -> q + 128
-            o[2 * h] = scale2(__builtin_amdgcn_perm(0x64646464u, w, 0x04020400u), bias, sc);
-            o[2 * h + 1] = scale2(__builtin_amdgcn_perm(0x64646464u, w, 0x04030401u), bias, sc);
+            p0 = __builtin_amdgcn_perm(0x64646464u, w, 0x04020400u);
+            p1 = __builtin_amdgcn_perm(0x64646464u, w, 0x04030401u);
+        }
+        if constexpr (QT == UNILLM_QTYPE_Q4_K) {
+            o[2 * h] = scale2o(p0, bias, sc, off);
+            o[2 * h + 1] = scale2o(p1, bias, sc, off);
+        } else {
+            o[2 * h] = scale2(p0, bias, sc);
+            o[2 * h + 1] = scale2(p1, bias, sc);
         }
     }
     return __builtin_bit_cast(f16x8, o);
@@ -175,38 +146,12 @@ __device__ __forceinline__ f16x8 dequant8_f16(u32x2 raw, uint32_t mask, f16x2 bi
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-// x (f32) -> bf16, round to nearest even; 8 elements per thread per pass.  y[0, ny)
-// <- 0 (a split k range adds into it).
-__global__ __launch_bounds__(256) void x_to_bf16_kernel(const float* __restrict__ x,
-                                                        uint4* __restrict__ xb, int64_t n8,
-                                                        float* __restrict__ y, int64_t ny) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        const float4 a = reinterpret_cast<const float4*>(x)[2 * i];
-        const float4 b = reinterpret_cast<const float4*>(x)[2 * i + 1];
-        xb[i] = make_uint4(pack_bf16(a.x, a.y), pack_bf16(a.z, a.w), pack_bf16(b.x, b.y),
-                           pack_bf16(b.z, b.w));
-    }
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    const int64_t head = std::min<int64_t>(ny, (int64_t)((16 - ((uintptr_t)y & 15)) & 15) / 4);
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < head; i += stride) y[i] = 0.0f;
-    float4* y4 = reinterpret_cast<float4*>(y + head);
-    const int64_t n4 = (ny - head) / 4;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride)
-        y4[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int64_t i = head + 4 * n4 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < ny; i += stride)
-        y[i] = 0.0f;
-}
 
 // ---- LDS ring ------------------------------------------------------------------------------
 // S stages, each one k step (64 k) of both operands, filled by direct
 // global -> LDS loads (global_load_lds_dwordx4: each lane's 16 bytes land at
 // lane * 16 of the instruction's 1 KiB destination; no VGPRs involved):
-//   A  [BM rows][128 B]  bf16 x, swizzled: the 16-byte chunk c of row r sits in
+//   A  [BM rows][128 B]  f16 x, swizzled: the 16-byte chunk c of row r sits in
 //                        slot c ^ (r % 8), so the 16 rows an MFMA fragment read
 //                        touches spread over the banks;
 //   Bp [256 cols][32 B]  the step's two payloads of each weight row;
@@ -233,7 +178,7 @@ struct Ring {
     // 3 for 256-row tiles
     static constexpr int STAGES = BM == 128 ? 4 : 3;
     // + the tile's row scales of x (f16 operands): BM floats after the ring
-    static constexpr int BYTES = STAGES * STAGE + (QT == UNILLM_QTYPE_Q4_0 || QT == UNILLM_QTYPE_Q8_0 ? BM * 4 : 0);
+    static constexpr int BYTES = STAGES * STAGE + BM * 4;
     static constexpr int RS = STAGES * STAGE;
     static constexpr int CPB = 2 * QB / 16;            // 16-byte payload chunks per column
     static constexpr int AQ = BM / 8 / 8;              // A loads (8 rows each) per wave
@@ -260,11 +205,9 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
     constexpr int TI = WR / 16;                            // MFMA tiles along m per wave
     constexpr int TJ = WC / 16;                            // MFMA tiles along n per wave (4)
     using R = Ring<QT, BM>;
-    // Q4_0 / Q8_0: f16 operands (x rows in the order 0 2 1 3 4 6 5 7, each scaled by
-    // a power of two undone by rs[row]; weights scaled by wscale = 2^-E, undone by
-    // oscale = 2^E); K-quants: bf16
-    constexpr bool F16 = QT == UNILLM_QTYPE_Q4_0 || QT == UNILLM_QTYPE_Q8_0;
-    using VT = std::conditional_t<F16, f16x8, bf16x8>;
+    // f16 operands: x rows in the order 0 2 1 3 4 6 5 7, each scaled by a power of
+    // two undone by rs[row]; weights scaled by wscale = 2^-E, undone by oscale = 2^E
+    using VT = f16x8;
     constexpr int kStages = R::STAGES;
     constexpr int AQ = R::AQ;
     constexpr int CPB = R::CPB;
@@ -336,7 +279,6 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
     const int g = lane / 16, fr = lane % 16;
     constexpr bool kNib = QB == 16;
     const uint32_t boff = kNib ? 8 * (g & 1) : 8 * g;
-    const int bshift = kNib ? 4 * (g >> 1) : 0;
     const int rw = wv / CW, cw = wv % CW;
     bool bval[TJ];
 #pragma unroll
@@ -344,7 +286,10 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
     // f16 dequant constants of this lane (high nibbles: 1024 + 16 q, scale / 16)
     const bool hnib = kNib && g >= 2;
     const uint32_t nmask = hnib ? 0x00F000F0u : 0x000F000Fu;
-    const _Float16 bias1 = (_Float16)(QT == UNILLM_QTYPE_Q4_0 && !hnib ? 1032.0f : 1152.0f);
+    const _Float16 bias1 = (_Float16)(QT == UNILLM_QTYPE_Q4_K                 ? 1024.0f
+                                      : QT == UNILLM_QTYPE_Q4_0 && !hnib ? 1032.0f
+                                                                         : 1152.0f);
+    const float lsc = hnib ? 0.0625f : 1.0f;
     const f16x2 fbias = {bias1, bias1};
     float wl[TJ];
 #pragma unroll
@@ -371,12 +316,10 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
 
     // prologue: the tile's row scales (f16 operands; wave 0, ahead of its ring loads, so
     // the ring's waits cover them), then stages 0 .. kStages - 2 in flight
-    if constexpr (F16) {
-        if (wv == 0) {
+    if (wv == 0) {
 #pragma unroll
-            for (int q = 0; q < BM / 64; ++q)
-                dma4(rs + min(m0 + 64 * q + lane, M - 1), ring + R::RS + q * 256);
-        }
+        for (int q = 0; q < BM / 64; ++q)
+            dma4(rs + min(m0 + 64 * q + lane, M - 1), ring + R::RS + q * 256);
     }
 #pragma unroll
     for (int d = 0; d < kStages - 1; ++d)
@@ -395,7 +338,7 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
         if (j + kStages - 1 < nks) issue(ks + kStages - 1);
 
         const uint32_t st = ring0 + (uint32_t)((ks % kStages) * R::STAGE);
-        // B: raw bytes and scales of this wave's columns -> bf16 fragments
+        // B: raw bytes and scales of this wave's columns -> f16 fragments
         u32x2 raw[TJ][2];
         uint32_t sc[TJ];
         // raw payload of column tile j at j * 16 * 2 QB (block 1 at + QB); scales of
@@ -427,15 +370,18 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
                 : "v"(st + boff0), "v"(st + soff0), "i"(0), "i"(QB), "i"(T), "i"(T + QB));
         }
         const bool b1ok = 2 * ks + 1 < KB;
-        float d0[TJ], d1[TJ], o0[TJ], o1[TJ];
-        uint32_t sp[TJ];  // F16: the f16 scales d 2^-E of blocks 0 (low) and 1 (high)
-        if constexpr (F16) {
+        // the f16 scales of blocks 0 (low half) and 1 (high half) of each column tile,
+        // and Q4_K's offsets
+        uint32_t sp[TJ], op[TJ];
+        if constexpr (!R::KQ) {
 #pragma unroll
-            for (int j = 0; j < TJ; ++j)
+            for (int j = 0; j < TJ; ++j) {
                 sp[j] = pack_f16(__half2float(__ushort_as_half((uint16_t)sc[j])) * wl[j],
                                  b1ok ? __half2float(__ushort_as_half((uint16_t)(sc[j] >> 16))) * wl[j]
                                       : 0.0f);
-        } else if constexpr (R::KQ) {
+                op[j] = 0;
+            }
+        } else {
             // the group header (Q4_K d | dmin << 16, Q6_K d) of each column tile, laid out
             // as the scales; sc[j] holds block 0's u16 in its low half, block 1's in its
             // high: Q4_K sc | m << 8, Q6_K the int8 scales of the two 16-weight halves
@@ -454,34 +400,30 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
                              : "v"(st + soff0 + R::BS));
 #pragma unroll
             for (int j = 0; j < TJ; ++j) {
-                const float dd = bval[j] ? __half2float(__ushort_as_half((uint16_t)hd[j])) : 0.0f;
+                const float dd =
+                    bval[j] ? __half2float(__ushort_as_half((uint16_t)hd[j])) * wscale : 0.0f;
                 if constexpr (R::K4) {
                     const float dm =
-                        bval[j] ? __half2float(__ushort_as_half((uint16_t)(hd[j] >> 16))) : 0.0f;
-                    d0[j] = dd * (float)(sc[j] & 0xFFu);
-                    o0[j] = -(dm * (float)((sc[j] >> 8) & 0xFFu));
-                    d1[j] = b1ok ? dd * (float)((sc[j] >> 16) & 0xFFu) : 0.0f;
-                    o1[j] = b1ok ? -(dm * (float)(sc[j] >> 24)) : 0.0f;
+                        bval[j] ? __half2float(__ushort_as_half((uint16_t)(hd[j] >> 16))) * wscale
+                                : 0.0f;
+                    sp[j] = pack_f16(dd * (float)(sc[j] & 0xFFu) * lsc,
+                                     b1ok ? dd * (float)((sc[j] >> 16) & 0xFFu) * lsc : 0.0f);
+                    op[j] = pack_f16(dm * (float)((sc[j] >> 8) & 0xFFu),
+                                     b1ok ? dm * (float)(sc[j] >> 24) : 0.0f);
                 } else {
-                    // this lane's elements 8 g .. 8 g + 7 lie in half g / 2 of each block;
-                    // codes are q - 32 + 128 after the flip, so off = -128 d sc
+                    // this lane's elements 8 g .. 8 g + 7 lie in half g / 2 of each block
                     const int hs = 8 * (g >> 1);
-                    d0[j] = dd * (float)(int8_t)(sc[j] >> hs);
-                    d1[j] = b1ok ? dd * (float)(int8_t)(sc[j] >> (16 + hs)) : 0.0f;
-                    o0[j] = -128.0f * d0[j];
-                    o1[j] = -128.0f * d1[j];
+                    sp[j] = pack_f16(dd * (float)(int8_t)(sc[j] >> hs),
+                                     b1ok ? dd * (float)(int8_t)(sc[j] >> (16 + hs)) : 0.0f);
+                    op[j] = 0;
                 }
             }
         }
         auto deq = [&](int j, int b) -> VT {
-            if constexpr (F16) {
-                const f16x2 s2 = __builtin_bit_cast(f16x2, sp[j]);
-                const f16x2 sb = b == 0 ? f16x2{s2[0], s2[0]} : f16x2{s2[1], s2[1]};
-                return dequant8_f16<QT>(raw[j][b], nmask, fbias, sb);
-            } else {
-                return dequant8<QT>(raw[j][b], bshift, b == 0 ? d0[j] : d1[j],
-                                    b == 0 ? o0[j] : o1[j]);
-            }
+            const f16x2 s2 = __builtin_bit_cast(f16x2, sp[j]), o2 = __builtin_bit_cast(f16x2, op[j]);
+            const f16x2 sb = b == 0 ? f16x2{s2[0], s2[0]} : f16x2{s2[1], s2[1]};
+            const f16x2 ob = b == 0 ? f16x2{o2[0], o2[0]} : f16x2{o2[1], o2[1]};
+            return dequant8_f16<QT>(raw[j][b], nmask, fbias, sb, ob);
         };
         // block 0's fragments first; block 1's are dequantized between the MFMAs of
         // the first 32 k (one column tile after every TI / TJ row tiles), so the
@@ -526,14 +468,12 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
     // S k slices of a tile meet in y by f32 atomic adds onto zeros.  f16 operands: the
     // output factor of row 16 i + 4 g + e is oscale times its row scale (from LDS:
     // global loads here would wait for the stores before them) ----
-    float4 rsc[F16 ? TI : 1];
-    if constexpr (F16) {
+    float4 rsc[TI];
 #pragma unroll
-        for (int i = 0; i < TI; ++i) {
-            const float4 r4 =
-                *reinterpret_cast<const float4*>(ring + R::RS + (WR * rw + 16 * i + 4 * g) * 4);
-            rsc[i] = make_float4(r4.x * oscale, r4.y * oscale, r4.z * oscale, r4.w * oscale);
-        }
+    for (int i = 0; i < TI; ++i) {
+        const float4 r4 =
+            *reinterpret_cast<const float4*>(ring + R::RS + (WR * rw + 16 * i + 4 * g) * 4);
+        rsc[i] = make_float4(r4.x * oscale, r4.y * oscale, r4.z * oscale, r4.w * oscale);
     }
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
@@ -546,8 +486,8 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
                 const int row = m0 + WR * rw + 16 * i + 4 * g + e;
                 if (row >= M) continue;
                 float* dst = y + (int64_t)row * N + col;
-                float v = acc[i][j][e];
-                if constexpr (F16) v *= e == 0 ? rsc[i].x : e == 1 ? rsc[i].y : e == 2 ? rsc[i].z : rsc[i].w;
+                const float v =
+                    acc[i][j][e] * (e == 0 ? rsc[i].x : e == 1 ? rsc[i].y : e == 2 ? rsc[i].z : rsc[i].w);
                 if (S == 1) *dst = add ? *dst + v : v;
                 else unsafeAtomicAdd(dst, v);  // onto zeros, or onto y with add
             }
@@ -578,9 +518,7 @@ hipError_t launch_bm(const QWeight& w, const uint16_t* xb, const float* rs, int6
     const int tiles_n = (int)((w.n + PBN - 1) / PBN);
     const int tiles = tiles_m * tiles_n;
     const int units_pad = (tiles * S + 7) / 8 * 8;
-    const bool f16 = QT == UNILLM_QTYPE_Q4_0 || QT == UNILLM_QTYPE_Q8_0;
-    const float wscale = f16 ? ldexpf(1.0f, -w.f16_exp) : 1.0f;
-    const float oscale = f16 ? ldexpf(1.0f, w.f16_exp) : 1.0f;
+    const float wscale = ldexpf(1.0f, -w.f16_exp), oscale = ldexpf(1.0f, w.f16_exp);
     prefill_kernel<QT, BM, kWaves><<<units_pad, kWaves * 64, Ring<QT, BM>::BYTES, s>>>(
         w.base, w.row_bytes, xb, y, (int)m, (int)w.n, (int)w.kb, tiles_n, tiles, units_pad, S,
         add, wscale, oscale, rs);
@@ -610,30 +548,19 @@ PrefillPlan prefill_plan(const QWeight& w, int64_t m) {
 
 hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, float* y,
                                hipStream_t s, int epi, const NormArgs& norm) {
-    // x in the operand type (f16 rows with their power-of-two scales for Q4_0 /
-    // Q8_0, bf16 for the K-quants) in the stream's workspace: the GEMM re-reads x
-    // once per 256-column tile, so it reads half the bytes, and no conversion sits
-    // in its inner loop.  The same kernel zeroes y for a split k.
+    // x as f16 rows with their power-of-two scales in the stream's workspace: the
+    // GEMM re-reads x once per 256-column tile, so it reads half the bytes, and no
+    // conversion sits in its inner loop.  The conversion zeroes y for a split k.
     const PrefillPlan plan = prefill_plan(w, m);
-    const int64_t n = m * w.k;  // k % 32 == 0, so n % 8 == 0
-    const bool f16 = w.qtype == UNILLM_QTYPE_Q4_0 || w.qtype == UNILLM_QTYPE_Q8_0;
-    const size_t xbytes = ((size_t)n * 2 + 255) / 256 * 256;
+    const size_t xbytes = ((size_t)m * (size_t)w.k * 2 + 255) / 256 * 256;
     void* ws = nullptr;
-    hipError_t e = stream_workspace(s, xbytes + (f16 ? (size_t)m * sizeof(float) : 0), &ws);
+    hipError_t e = stream_workspace(s, xbytes + (size_t)m * sizeof(float), &ws);
     if (e != hipSuccess) return e;
-    float* rs = f16 ? reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + xbytes) : nullptr;
+    float* rs = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + xbytes);
     const int add = epi == kEpiAdd;
-    const int64_t n8 = n / 8, ny = plan.S > 1 && !add ? m * w.n : 0;
-    if (norm.gamma)
-        e = launch_norm_convert(x, m, w.k, norm, f16, ws, y, ny > 0 ? w.n : 0, s, rs);
-    else if (f16)
-        e = launch_x_to_f16_rows(x, m, w.k, ws, rs, y, ny > 0 ? w.n : 0, s);
-    else {
-        const int grid = (int)std::min<int64_t>((std::max(n8, ny / 4) + 255) / 256,
-                                                (int64_t)device_info().cu_count * 16);
-        x_to_bf16_kernel<<<grid, 256, 0, s>>>(x, static_cast<uint4*>(ws), n8, y, ny);
-        e = hipGetLastError();
-    }
+    const int64_t yn = plan.S > 1 && !add ? w.n : 0;
+    e = norm.gamma ? launch_norm_convert(x, m, w.k, norm, true, ws, y, yn, s, rs)
+                   : launch_x_to_f16_rows(x, m, w.k, ws, rs, y, yn, s);
     if (e != hipSuccess) return e;
     const uint16_t* xb = static_cast<const uint16_t*>(ws);
     if (w.qtype == UNILLM_QTYPE_Q4_K)

@@ -96,7 +96,11 @@ int unillm_hip_qweight_info(const unillm_qweight* w, int* qtype, int64_t* n, int
  * QMatMul::forward as called from LlamaAttention/LlamaMLP::quantized_matmul
  * (crates/runtime/src/models_v2/llama.rs:1184-1195, 1325-1336) and
  * LlamaModelV2::lm_head_forward (llama.rs:396-405); the m rows are the
- * flattened leading dims of the [.., k] input.  m == 0 is a no-op. */
+ * flattened leading dims of the [.., k] input.  m == 0 is a no-op.
+ * Operand range: the GEMV (exact integer digits of x) and prefill (f16 rows,
+ * each scaled by its own power of two) take any finite x; batched decode
+ * (UNILLM_PATH_DECODE_MFMA) rounds x to f16 unscaled, so its x must satisfy
+ * |x| <= 65504 (values below 2^-14 keep f16's fixed absolute precision). */
 int unillm_hip_qmatmul(const unillm_qweight* w, const float* x_dev, int64_t m, float* y_dev,
                        void* stream);
 

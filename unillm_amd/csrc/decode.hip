@@ -593,30 +593,51 @@ __device__ __forceinline__ float f16_row_scale(float mx, float* rs) {
 // x[m, k] -> f16 rows in the fragment order (each aligned 8 as 0 2 1 3 4 6 5 7),
 // each row scaled by its power of two (f16_row_scale; the factor to undo it in
 // rs[row]); y row zeroed over [0, yn) when yn > 0 (a split k adds into it).  One
-// workgroup per row: the max pass reads the row from HBM, the conversion re-reads
-// it from cache.
-__global__ __launch_bounds__(256) void xrows_kernel(const float* __restrict__ x, int64_t k,
-                                                    uint4* __restrict__ xh, float* __restrict__ rs,
-                                                    float* __restrict__ y, int64_t yn) {
-    __shared__ float red[4];
-    const int64_t r = blockIdx.x;
+// workgroup per row (64 .. 1024 threads, two groups of 8 a thread where the row
+// allows), one HBM read: a thread keeps its first two groups in registers (rows up
+// to 16384 elements); a longer row's further groups are read again for the
+// conversion.
+__global__ __launch_bounds__(1024) void xrows_kernel(const float* __restrict__ x, int64_t k,
+                                                     uint4* __restrict__ xh, float* __restrict__ rs,
+                                                     float* __restrict__ y, int64_t yn) {
+    __shared__ float red[16];
+    const int64_t r = blockIdx.x, g8 = k / 8;
+    const int t = threadIdx.x, nt = blockDim.x;
     const float4* xr = reinterpret_cast<const float4*>(x + r * k);
+    auto amax = [](float4 v) {
+        return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    };
+    float4 a[2], b[2];
     float mx = 0.0f;
-    for (int64_t i = threadIdx.x; i < k / 4; i += 256) {
-        const float4 a = xr[i];
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int64_t i = t + nt * j;
+        a[j] = b[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (i < g8) {
+            a[j] = xr[2 * i];
+            b[j] = xr[2 * i + 1];
+        }
+        mx = fmaxf(mx, fmaxf(amax(a[j]), amax(b[j])));
     }
+    for (int64_t i = t + 2 * nt; i < g8; i += nt)
+        mx = fmaxf(mx, fmaxf(amax(xr[2 * i]), amax(xr[2 * i + 1])));
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    if ((t & 63) == 0) red[t >> 6] = mx;
     __syncthreads();
-    const float sc = f16_row_scale(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), rs + r);
-    for (int64_t i = threadIdx.x; i < k / 8; i += 256) {
-        const float4 a = xr[2 * i], b = xr[2 * i + 1];
-        xh[r * (k / 8) + i] = make_uint4(pk_f16(a.x * sc, a.z * sc), pk_f16(a.y * sc, a.w * sc),
-                                         pk_f16(b.x * sc, b.z * sc), pk_f16(b.y * sc, b.w * sc));
-    }
-    for (int64_t i = threadIdx.x; i < yn; i += 256) y[r * yn + i] = 0.0f;
+    mx = 0.0f;
+    for (int w = 0; w < nt / 64; ++w) mx = fmaxf(mx, red[w]);
+    const float sc = f16_row_scale(mx, rs + r);
+    uint4* xo = xh + r * g8;
+    auto put = [&](int64_t i, float4 p, float4 q) {
+        xo[i] = make_uint4(pk_f16(p.x * sc, p.z * sc), pk_f16(p.y * sc, p.w * sc),
+                           pk_f16(q.x * sc, q.z * sc), pk_f16(q.y * sc, q.w * sc));
+    };
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        if (t + nt * j < g8) put(t + nt * j, a[j], b[j]);
+    for (int64_t i = t + 2 * nt; i < g8; i += nt) put(i, xr[2 * i], xr[2 * i + 1]);
+    for (int64_t i = t; i < yn; i += nt) y[r * yn + i] = 0.0f;
 }
 
 // rs != nullptr (f16 only): each row scaled by its power of two as in xrows_kernel.
@@ -728,7 +749,9 @@ hipError_t launch_norm_convert(const float* x, int64_t m, int64_t k, const NormA
 hipError_t launch_x_to_f16_rows(const float* x, int64_t m, int64_t k, void* out, float* rs,
                                 float* y, int64_t yn, hipStream_t s) {
     if (m <= 0) return hipSuccess;
-    xrows_kernel<<<(unsigned)m, 256, 0, s>>>(x, k, static_cast<uint4*>(out), rs, y, yn);
+    // two groups of 8 a thread, whole waves, 64 .. 1024 threads
+    const int nt = (int)std::min<int64_t>(1024, std::max<int64_t>(64, (k / 16 + 63) / 64 * 64));
+    xrows_kernel<<<(unsigned)m, nt, 0, s>>>(x, k, static_cast<uint4*>(out), rs, y, yn);
     return hipGetLastError();
 }
 

@@ -31,6 +31,8 @@ import time
 import numpy as np
 
 HBM_PEAK_GBS = 8000.0
+# MI355X dense MFMA peak for bf16 and f16 alike (the prefill kernel's f16
+# operands are priced against it; the "frac_bf16" fields use it)
 BF16_PEAK_TFLOPS = 2516.6
 Q4_0, Q8_0, Q4_K = 2, 8, 12
 BPB = {Q4_0: 18, Q8_0: 34, Q4_K: 18}  # GGUF bytes per 32 weights (Q4_K: 144 per 256)

@@ -31,9 +31,9 @@ import time
 import numpy as np
 
 HBM_PEAK_GBS = 8000.0
-# MI355X dense MFMA peak for bf16 and f16 alike (the prefill kernel's f16
-# operands are priced against it; the "frac_bf16" fields use it)
-BF16_PEAK_TFLOPS = 2516.6
+# MI355X dense MFMA peak, the same for bf16 and f16 operands (the prefill kernel
+# runs f16; the "frac_dense" fields price it against this)
+DENSE_PEAK_TFLOPS = 2516.6
 Q4_0, Q8_0, Q4_K = 2, 8, 12
 BPB = {Q4_0: 18, Q8_0: 34, Q4_K: 18}  # GGUF bytes per 32 weights (Q4_K: 144 per 256)
 
@@ -246,7 +246,7 @@ def extra_configs(torch, QuantLinear, gen, stream, only):
                     ms = timed(ws, x, y, reps_per_copy=2, path=PATH_PREFILL_MFMA)
                     tf = 2 * m * n * k / ms / 1e9
                     res[f"{'q4_0' if qtype == Q4_0 else 'q8_0'}_prefill_m{m}_k{k}_n{n}"] = {
-                        "TFLOP/s": round(tf, 1), "frac_bf16": round(tf / BF16_PEAK_TFLOPS, 3),
+                        "TFLOP/s": round(tf, 1), "frac_dense": round(tf / DENSE_PEAK_TFLOPS, 3),
                         "us": round(ms * 1e3, 1)}
                 del ws
     if "q4_k" in want:
@@ -290,7 +290,7 @@ def extra_configs(torch, QuantLinear, gen, stream, only):
         ms = timed(ws, x, y, path=PATH_PREFILL_MFMA)
         tf = 2 * 2048 * 14336 * 4096 / ms / 1e9
         res["q4_k_prefill_m2048_k4096_n14336"] = {
-            "TFLOP/s": round(tf, 1), "frac_bf16": round(tf / BF16_PEAK_TFLOPS, 3),
+            "TFLOP/s": round(tf, 1), "frac_dense": round(tf / DENSE_PEAK_TFLOPS, 3),
             "us": round(ms * 1e3, 1)}
         del ws
     if "attention" in want:
@@ -526,7 +526,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 weights, f32 activations, fp32 accumulate",
+        "dtype": "q4_0 weights x f32 activations held per 32-block as exact 16-bit "
+                 "fixed-point integers (4 base-16 digits; the reference holds them as int8 "
+                 "Q8_0), int32 block dots, fp32 accumulate",
         "data": "synthetic: weights N(0,0.02) quantized on device with the GGML Q4_0 "
                 "quantizer, x N(0,1); random-init Llama-2-7B projection shapes",
         "config": {"workload": "Q4_0 decode GEMV, m=1, Llama-2-7B shapes (QKV 4096x12288, "

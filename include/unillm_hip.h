@@ -104,6 +104,20 @@ int unillm_hip_qweight_info(const unillm_qweight* w, int* qtype, int64_t* n, int
 int unillm_hip_qmatmul(const unillm_qweight* w, const float* x_dev, int64_t m, float* y_dev,
                        void* stream);
 
+/* x and y need only f32 (4-byte) alignment, as candle's contiguous f32 tensors
+ * have; x not on a 16-byte boundary is first copied (stream-ordered) into an
+ * aligned per-stream buffer, since the kernels load it 16 bytes at a time.
+ *
+ * Workspace.  The MFMA paths (and SwiGLU off the GEMV path) use per-stream
+ * device buffers that grow on first use and are then kept for later calls on
+ * that stream.  Growing allocates, which cannot be recorded into a HIP graph: a
+ * call that would grow a buffer while its stream is being captured fails with
+ * UNILLM_ERR_UNSUPPORTED and a message naming the size.  Reserve the buffers
+ * before capturing (unillm_hip_qmatmul_reserve / unillm_hip_attention_reserve),
+ * or make the same calls once eagerly first.  Outgrown buffers are never freed
+ * (a captured graph may still use them).  A graph uses the buffers of the stream
+ * it was captured on: replay it on that stream. */
+
 /* As unillm_hip_qmatmul with an explicit kernel path (UNILLM_PATH_*), for
  * tests and benchmarks; AUTO picks what unillm_hip_qmatmul picks. */
 int unillm_hip_qmatmul_path(const unillm_qweight* w, const float* x_dev, int64_t m,
@@ -152,6 +166,13 @@ int unillm_hip_qmatmul_norm_swiglu(const unillm_qweight* w, const float* x_dev,
 /* Kernel path that unillm_hip_qmatmul selects for m rows (UNILLM_PATH_*). */
 int unillm_hip_select_path(const unillm_qweight* w, int64_t m);
 
+/* Grow `stream`'s workspace to what any qmatmul / _add / _norm call on w with up
+ * to m rows needs (and, with swiglu != 0, the _swiglu / _norm_swiglu calls), so
+ * such calls can then be captured into a HIP graph.  No counterpart in the
+ * reference (candle allocates per call and has no graphs): it serves callers
+ * that capture.  Allocates stream-ordered on `stream`; not while capturing. */
+int unillm_hip_qmatmul_reserve(const unillm_qweight* w, int64_t m, int swiglu, void* stream);
+
 /* One decoder layer's KV cache on the device for one sequence: K and V of
  * n_kv_heads heads, max_seq positions of head_dim f32 each (zeroed), and the
  * RoPE frequencies of rope_theta.  Replaces LayerKVCache::with_capacity
@@ -184,6 +205,13 @@ int unillm_hip_kv_cache_truncate(unillm_kv_cache* c, int64_t len);
  * each appends to it. */
 int unillm_hip_attention_decode(unillm_kv_cache* c, const float* qkv_dev, int64_t m,
                                 int64_t n_heads, float* out_dev, void* stream);
+
+/* Grow `stream`'s attention workspace to what unillm_hip_attention_decode of up to
+ * m tokens and n_heads heads needs at any cache length, so such calls can be
+ * captured into a HIP graph (no counterpart in the reference; as
+ * unillm_hip_qmatmul_reserve). */
+int unillm_hip_attention_reserve(const unillm_kv_cache* c, int64_t m, int64_t n_heads,
+                                 void* stream);
 
 /* out[n, k] = dequant(W) in f32, bit-exact with GGML's to_float.  Replaces
  * `qtensor.dequantize(&device)` at crates/runtime/src/weight_loader_core.rs:579. */

@@ -159,6 +159,38 @@ static void test_cpu(const std::string& gguf, const std::vector<Expect>& ex) {
     std::vector<char> hdr(bytes.begin(), bytes.begin() + 40);
     CHECK(throws_with([&] { GgufFile::open(write_tmp("hdr.gguf", hdr)); }, "end of file"));
     CHECK(throws_with([&] { GgufFile::open("/nonexistent/x.gguf"); }, "cannot open"));
+    // a header declaring one metadata array of 2^31 one-byte items over a few MB of
+    // file: each parsed item costs far more memory than its byte, so the reader
+    // must run out of file (GgufError), not out of memory (bad_alloc)
+    {
+        std::vector<char> h;
+        auto put = [&](const void* p, size_t n) {
+            const char* c = static_cast<const char*>(p);
+            h.insert(h.end(), c, c + n);
+        };
+        const uint32_t ver = 3, t_arr = 9, t_u8 = 0;
+        const uint64_t n_tensors = 0, n_kv = 1, klen = 3, count = 1ull << 31;
+        put("GGUF", 4);
+        put(&ver, 4);
+        put(&n_tensors, 8);
+        put(&n_kv, 8);
+        put(&klen, 8);
+        put("arr", 3);
+        put(&t_arr, 4);
+        put(&t_u8, 4);
+        put(&count, 8);
+        h.resize(h.size() + (4u << 20), 1);  // 4 MiB of items, far short of the count
+        CHECK(throws_with([&] { GgufFile::open(write_tmp("huge_array.gguf", h)); },
+                          "array length"));
+        // 2^22 two-byte items: a count the remaining bytes pass, twice the bytes they
+        // hold: parsed item by item (the reserve stays bounded) until the file ends
+        const uint32_t t_u16 = 2;
+        const uint64_t fits = 4u << 20;
+        std::memcpy(h.data() + 4 + 4 + 8 + 8 + 8 + 3 + 4, &t_u16, 4);
+        std::memcpy(h.data() + 4 + 4 + 8 + 8 + 8 + 3 + 4 + 4, &fits, 8);
+        CHECK(throws_with([&] { GgufFile::open(write_tmp("short_array.gguf", h)); },
+                          "end of file"));
+    }
 
     // shape rules of QMatMul::forward are checked before any device work
     Device d = Device::hip(0);
@@ -210,6 +242,14 @@ static void test_gpu(const std::string& gguf, const std::vector<Expect>& ex) {
                       "QMatMul forward failed: rank 1"));
     CHECK(throws_with([&] { q->forward(Tensor::empty({2, 64}, Device::cpu())); },
                       "QMatMul forward failed: input is on CPU"));
+    // lm_head_forward (llama.rs:396-405): the same result, the reference's lm_head context
+    {
+        const Tensor h = Tensor::from_host(std::vector<float>(2 * 64, 0.25f), {2, 64},
+                                           Device::hip(0));
+        CHECK(lm_head_forward(*q, h).to_host() == q->forward(h).to_host());
+        CHECK(throws_with([&] { lm_head_forward(*q, Tensor::empty({3, 32}, Device::hip(0))); },
+                          "QMatMul lm_head forward failed: input last dim 32"));
+    }
     test_gpu_kv();
 }
 

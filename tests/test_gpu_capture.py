@@ -1,0 +1,105 @@
+"""HIP-graph capture of the matmul and attention calls, and their per-stream workspace.
+
+The MFMA paths keep x in a per-stream device buffer that grows on first use.
+Growing allocates, which a capture cannot record: such a call must fail with a
+clear error and leave the capture usable, and a reserved stream must capture and
+replay correctly, also after later eager calls have grown the buffer again.
+Replays are checked against eager calls, with eager work and synchronisations
+between them.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import Q4_0
+from unillm_amd import PATH_DECODE_MFMA, PATH_PREFILL_MFMA, HipError, KvCache, QuantLinear
+
+pytestmark = pytest.mark.gpu
+
+
+def _weight(n, k, seed):
+    w = oracle.normal(n * k, seed=seed, std=0.02).reshape(n, k)
+    b = oracle.quantize(Q4_0, w)
+    return b, QuantLinear.from_blocks(Q4_0, n, k, b)
+
+
+def _x(m, k, seed):
+    return torch.from_numpy(oracle.normal(m * k, seed=seed).reshape(m, k)).cuda()
+
+
+def test_capture_with_cold_workspace_fails_cleanly():
+    _, ql = _weight(512, 1024, seed=11)
+    s = torch.cuda.Stream()  # a fresh stream: no workspace yet
+    x = _x(16, 1024, seed=12)
+    y = torch.empty(16, 512, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(HipError, match="while the stream is being captured"):
+        with torch.cuda.graph(g, stream=s, capture_error_mode="thread_local"):
+            ql.forward(x, out=y, path=PATH_DECODE_MFMA, stream=s)
+    del g
+    torch.cuda.synchronize()
+    # the stream still works eagerly afterwards
+    with torch.cuda.stream(s):
+        ql.forward(x, out=y, path=PATH_DECODE_MFMA, stream=s)
+    s.synchronize()
+    assert torch.isfinite(y).all()
+
+
+@pytest.mark.parametrize("m,path", [(16, PATH_DECODE_MFMA), (300, PATH_PREFILL_MFMA)])
+def test_reserved_stream_captures_and_replays(m, path):
+    n, k = 1024, 2048
+    blocks, ql = _weight(n, k, seed=21 + m)
+    s = torch.cuda.Stream()
+    ql.reserve(m, stream=s)
+    x = _x(m, k, seed=22 + m)
+    y = torch.empty(m, n, device="cuda")
+    with torch.cuda.stream(s):
+        eager = ql.forward(x, path=path, stream=s).clone()
+    s.synchronize()
+    ref = oracle.qmatmul_f64(Q4_0, blocks, x.cpu().numpy(), n, k)
+    assert oracle.normwise_error(eager.cpu().numpy(), ref) < 1e-3
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s, capture_error_mode="thread_local"):
+        ql.forward(x, out=y, path=path, stream=s)
+    big = _x(2048, k, seed=23)
+    for i in range(4):
+        y.zero_()
+        with torch.cuda.stream(s):
+            g.replay()
+        s.synchronize()
+        # split k ranges meet by f32 atomics: equal up to their order
+        assert oracle.normwise_error(y.cpu().numpy(), eager.cpu().numpy()) < 1e-6, i
+        # eager work between replays; the second one grows the stream's workspace
+        # (the captured buffer is retired, not freed, so the graph stays valid)
+        with torch.cuda.stream(s):
+            ql.forward(big if i == 1 else x, path=PATH_PREFILL_MFMA, stream=s)
+        s.synchronize()
+    del g
+
+
+def test_reserved_attention_captures_and_replays():
+    H, KVH, D, L = 8, 2, 128, 256
+    s = torch.cuda.Stream()
+    kv = KvCache(KVH, D, L)
+    kv.reserve(1, H, stream=s)
+    w = (H + 2 * KVH) * D
+    pre = _x(40, w, seed=31)
+    q1 = _x(1, w, seed=32)
+    out = torch.empty(1, H * D, device="cuda")
+    with torch.cuda.stream(s):
+        for t in range(40):
+            kv.attention(pre[t:t + 1].contiguous(), H, stream=s)
+        eager = kv.attention(q1, H, stream=s).clone()
+    s.synchronize()
+    kv.truncate(40)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s, capture_error_mode="thread_local"):
+        kv.attention(q1, H, out=out, stream=s)
+    for i in range(3):
+        kv.truncate(40)
+        out.zero_()
+        with torch.cuda.stream(s):
+            g.replay()
+        s.synchronize()
+        assert torch.equal(out, eager), i

@@ -1,8 +1,8 @@
 """GPU parity for Q4_K weights (GGML block_q4_K), through the C ABI, against the oracle.
 
 Bars as for Q4_0: dequant bit-exact with GGML's dequantize_row_q4_K (oracle
-restatement, pinned in tests/test_oracle.py); GEMV within 1e-3 and the bf16
-MFMA prefill within 2e-2 normwise of the f64 matmul of the exactly dequantized
+restatement, pinned in tests/test_oracle.py); GEMV, batched decode and the f16
+MFMA prefill within 1e-3 normwise of the f64 matmul of the exactly dequantized
 weights.  Test weights are random valid
 blocks (random codes and 6-bit scales / mins under f16 super-block scales):
 GGML's Q4_K quantizer is not on the path and is not restated.
@@ -142,7 +142,7 @@ def test_q4k_decode_scale_range():
         assert oracle.normwise_error(y.cpu().numpy(), ref) < 1e-3, mult
 
 
-# ---- prefill (bf16 MFMA): the same kernel as Q4_0 with per-block (d sc, dmin m) ----------
+# ---- prefill (f16 MFMA): the same kernel as Q4_0 with per-block (d sc, dmin m) -----------
 
 @pytest.mark.parametrize("m,n,k", [(65, 300, 1024), (128, 512, 4096), (200, 130, 768),
                                    (130, 256, 8192), (512, 1024, 4096)])

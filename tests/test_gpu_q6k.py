@@ -3,7 +3,7 @@
 Q6_K is what GGUF Q4_K_M files use for output.weight (lm_head) and for some
 attn_v / ffn_down tensors.  Bars: dequant bit-exact with GGML's
 dequantize_row_q6_K (oracle restatement, pinned in tests/test_oracle.py);
-GEMV and batched decode within 1e-3, the bf16 prefill within 2e-2, normwise
+GEMV, batched decode and the f16 prefill within 1e-3, normwise
 against the f64 matmul of the exactly dequantized weights.  Test weights are
 random valid blocks (random 6-bit codes, int8 scales, f16 d).
 """

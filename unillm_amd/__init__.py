@@ -14,13 +14,13 @@ __all__ = [
     "BLOCK_BYTES", "BLOCK_ELEMS", "ERR_HIP", "ERR_INVALID_ARG", "ERR_UNSUPPORTED", "OK", "PATH_AUTO",
     "PATH_DECODE_MFMA", "PATH_GEMV", "PATH_PREFILL_MFMA", "QK", "Q4_0", "Q4_K", "Q6_K", "Q8_0",
     "HipError",
-    "QuantLinear", "quantize_blocks", "KvCache",
+    "QuantLinear", "quantize_blocks", "lm_head_forward", "KvCache",
 ]
 
 
 def __getattr__(name):
     # QuantLinear needs torch; import it lazily so the ABI binding loads without it.
-    if name in ("QuantLinear", "quantize_blocks"):
+    if name in ("QuantLinear", "quantize_blocks", "lm_head_forward"):
         from . import quant_linear
         return getattr(quant_linear, name)
     if name == "KvCache":

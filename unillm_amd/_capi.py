@@ -71,6 +71,8 @@ SIGNATURES = {
     "unillm_hip_attention_decode": ([P, P, I64, I64, P, P], ctypes.c_int),
     "unillm_hip_qmatmul_norm_swiglu": ([P, P, P, P, ctypes.c_float, I64, P, P], ctypes.c_int),
     "unillm_hip_select_path": ([P, I64], ctypes.c_int),
+    "unillm_hip_qmatmul_reserve": ([P, I64, ctypes.c_int, P], ctypes.c_int),
+    "unillm_hip_attention_reserve": ([P, I64, I64, P], ctypes.c_int),
     "unillm_hip_dequant": ([P, P, P], ctypes.c_int),
     "unillm_hip_quantize": ([ctypes.c_int, P, I64, I64, P, P], ctypes.c_int),
     "unillm_hip_malloc": ([ctypes.POINTER(P), ctypes.c_size_t], ctypes.c_int),

@@ -40,6 +40,12 @@ class KvCache:
     def clear(self) -> None:
         _capi.check(_capi.lib().unillm_hip_kv_cache_clear(self._h))
 
+    def reserve(self, m: int, n_heads: int, stream: torch.cuda.Stream | None = None) -> None:
+        """Grow the stream's attention workspace for calls of up to m tokens, so they
+        can be captured into a HIP graph."""
+        _capi.check(_capi.lib().unillm_hip_attention_reserve(self._h, m, n_heads,
+                                                             _stream_ptr(stream)))
+
     def truncate(self, length: int) -> None:
         """Keep the first `length` positions (<= seq_len): a rolled-back step."""
         _capi.check(_capi.lib().unillm_hip_kv_cache_truncate(self._h, length))

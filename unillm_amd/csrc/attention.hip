@@ -382,18 +382,30 @@ hipError_t launch_d(const KvCache& kv, const float* qkv, int m, int H, int C, in
 
 }  // namespace
 
-hipError_t launch_attention_decode(const KvCache& kv, const float* qkv, int64_t m, int64_t H,
-                                   float* out, hipStream_t s) {
-    const int D = (int)kv.head_dim, KVH = (int)kv.n_kv_heads;
-    const int64_t L = kv.len + m;
-    // chunk length: enough (kv head, chunk) workgroups to cover the CUs twice, 32 ..
-    // kMaxChunk positions, a multiple of 32
-    // (kv head, chunk) workgroups to cover the CUs twice; chunks of 32 .. kMaxChunk
-    // positions (a multiple of 32), at most kMaxChunks of them
+namespace {
+// Chunk length for L positions: (kv head, chunk) workgroups to cover the CUs
+// twice; chunks of 32 .. kMaxChunk positions (a multiple of 32), at most
+// kMaxChunks of them.  0 when L is beyond kMaxChunk * kMaxChunks.
+int64_t chunk_len(int64_t L, int64_t KVH) {
     const int64_t want = 2 * (int64_t)device_info().cu_count;
     int64_t C = std::max((L * KVH + want - 1) / want, (L + kMaxChunks - 1) / kMaxChunks);
     C = std::max<int64_t>(32, (C + 31) / 32 * 32);
-    if (C > kMaxChunk) return hipErrorInvalidValue;  // longer than kMaxChunk * kMaxChunks
+    return C > kMaxChunk ? 0 : C;
+}
+}  // namespace
+
+// The per-chunk partials of a call of m tokens at any length: at most kMaxChunks
+// chunks of (max, sum) and o[hd] per query.
+size_t attention_workspace_bytes(const KvCache& kv, int64_t m, int64_t H) {
+    return (size_t)m * H * kMaxChunks * (2 + kv.head_dim) * sizeof(float);
+}
+
+hipError_t launch_attention_decode(const KvCache& kv, const float* qkv, int64_t m, int64_t H,
+                                   float* out, hipStream_t s) {
+    const int D = (int)kv.head_dim;
+    const int64_t L = kv.len + m;
+    const int64_t C = chunk_len(L, kv.n_kv_heads);
+    if (C == 0) return hipErrorInvalidValue;  // longer than kMaxChunk * kMaxChunks
     const int chunks = (int)((L + C - 1) / C);
     const size_t pbytes = (size_t)m * H * chunks * (2 + D) * sizeof(float);
     void* ws = nullptr;

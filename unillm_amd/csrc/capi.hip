@@ -165,6 +165,11 @@ struct StreamWs {
 };
 std::mutex g_ws_mutex;
 std::map<std::pair<hipStream_t, int>, StreamWs> g_ws;
+// Buffers a workspace has outgrown.  A graph captured while one of them was
+// current still reads and writes it at every replay, so none is ever freed;
+// growth at least doubles a slot, so they add up to less than the slot itself.
+std::vector<void*> g_ws_retired;
+thread_local size_t g_ws_capture_need = 0;  // size a capture-time growth asked for
 
 }  // namespace
 
@@ -174,20 +179,22 @@ hipError_t stream_workspace(hipStream_t s, size_t bytes, void** out, int slot) {
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     StreamWs& w = g_ws[{s, slot}];
     if (w.bytes < bytes) {
-        // grow in stream order: earlier work on s that uses the old buffer runs
-        // before the free, later work uses the new one
-        if (w.buf) {
-            hipError_t e = hipFreeAsync(w.buf, s);
-            w.buf = nullptr;
-            w.bytes = 0;
-            if (e != hipSuccess) return e;
+        // Growing allocates: refused while s is being captured (the allocation and
+        // the buffer it replaces would belong to the graph, not to later eager calls)
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        hipError_t e = hipStreamIsCapturing(s, &cs);
+        if (e != hipSuccess) return e;
+        if (cs != hipStreamCaptureStatusNone) {
+            g_ws_capture_need = bytes;
+            return hipErrorStreamCaptureUnsupported;
         }
-        const size_t want = std::max(bytes, (size_t)1 << 20);
-        hipError_t e = hipMallocAsync(&w.buf, want, s);
-        if (e != hipSuccess) {
-            w.buf = nullptr;
-            return e;
-        }
+        // Grow in stream order: work on s already issued keeps the old buffer, later
+        // work uses the new one.  The old buffer is retired, never freed.
+        const size_t want = std::max({bytes, (size_t)1 << 20, 2 * w.bytes});
+        void* nb = nullptr;
+        if ((e = hipMallocAsync(&nb, want, s)) != hipSuccess) return e;
+        if (w.buf) g_ws_retired.push_back(w.buf);
+        w.buf = nb;
         w.bytes = want;
     }
     *out = w.buf;
@@ -315,26 +322,39 @@ int unillm_hip_select_path(const unillm_qweight* w, int64_t m) {
 
 namespace {
 
+// A failed launch or workspace request as a status: a workspace that would have
+// to grow while its stream is being captured gets its own message.
+int fail_launch(hipError_t e, const std::string& what) {
+    if (e == hipErrorStreamCaptureUnsupported)
+        return fail(UNILLM_ERR_UNSUPPORTED,
+                    what + ": the stream's workspace must grow to " +
+                        std::to_string(g_ws_capture_need) +
+                        " bytes, which cannot happen while the stream is being captured; "
+                        "reserve it before capture (unillm_hip_qmatmul_reserve / "
+                        "unillm_hip_attention_reserve) or make the same call once eagerly");
+    return fail_hip(e, what.c_str());
+}
+
 // The matmul on `path` with epilogue `epi` (kEpiStore / kEpiAdd; kEpiSwiglu runs
 // fused on the GEMV, else as store into the stream's second workspace + swiglu).
+// `what` prefixes every error message (the caller's anyhow context).
 int qmatmul_impl(const unillm_qweight* w, const float* x_dev, int64_t m, float* y_dev, int path,
-                 void* stream, int epi, const NormArgs& norm = NormArgs{nullptr, nullptr, 0.f}) {
-    if (!w) return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: weight is NULL");
-    if (m < 0) return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: m < 0");
+                 void* stream, int epi, const NormArgs& norm = NormArgs{nullptr, nullptr, 0.f},
+                 const std::string& what = "QMatMul forward failed") {
+    if (!w) return fail(UNILLM_ERR_INVALID_ARG, what + ": weight is NULL");
+    if (m < 0) return fail(UNILLM_ERR_INVALID_ARG, what + ": m < 0");
     if (epi == kEpiSwiglu && w->n % 2 != 0)
         return fail(UNILLM_ERR_INVALID_ARG,
-                    "QMatMul forward failed: a SwiGLU weight stacks gate and up rows (even n)");
+                    what + ": a SwiGLU weight stacks gate and up rows (even n)");
     if (m == 0) return UNILLM_OK;
-    if (!x_dev || !y_dev)
-        return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: x or y is NULL");
-    if (!aligned16(x_dev))
-        return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: x must be 16-byte aligned");
-    if (m > (int64_t)INT32_MAX / 2)
-        return fail(UNILLM_ERR_INVALID_ARG, "QMatMul forward failed: m too large");
+    if (!x_dev || !y_dev) return fail(UNILLM_ERR_INVALID_ARG, what + ": x or y is NULL");
+    if (((uintptr_t)x_dev & 3u) != 0 || ((uintptr_t)y_dev & 3u) != 0)
+        return fail(UNILLM_ERR_INVALID_ARG, what + ": x and y must be 4-byte aligned (f32)");
+    if (m > (int64_t)INT32_MAX / 2) return fail(UNILLM_ERR_INVALID_ARG, what + ": m too large");
     if (norm.gamma && (!aligned16(norm.gamma) || (norm.beta && !aligned16(norm.beta)) ||
                        !(norm.eps >= 0.0f)))
         return fail(UNILLM_ERR_INVALID_ARG,
-                    "QMatMul forward failed: norm weight / bias must be 16-byte aligned, eps >= 0");
+                    what + ": norm weight / bias must be 16-byte aligned, eps >= 0");
     if (path == UNILLM_PATH_AUTO) {
         path = unillm_hip_select_path(w, m);
         // a fused layer norm on the GEMV takes k <= 8192; past it, batched decode
@@ -343,41 +363,57 @@ int qmatmul_impl(const unillm_qweight* w, const float* x_dev, int64_t m, float* 
     }
     if (norm.gamma && path == UNILLM_PATH_GEMV && !gemv_supports_norm(*w, m))
         return fail(UNILLM_ERR_UNSUPPORTED,
-                    "QMatMul forward failed: a fused layer norm on the GEMV path takes k <= 8192");
+                    what + ": a fused layer norm on the GEMV path takes k <= 8192");
+    if ((path == UNILLM_PATH_DECODE_MFMA || path == UNILLM_PATH_PREFILL_MFMA) &&
+        !mfma_supports(*w))
+        return fail(UNILLM_ERR_UNSUPPORTED,
+                    what + ": the MFMA paths take weights under 4 GiB (32-bit byte offsets)");
     if (int rc = ensure_init()) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e;
+    // x not on a 16-byte boundary (candle takes any contiguous f32): the kernels
+    // load x 16 bytes at a time, so it is first copied, stream-ordered, into an
+    // aligned workspace (slot 3)
+    if (!aligned16(x_dev)) {
+        void* xa = nullptr;
+        const size_t xb = (size_t)m * (size_t)w->k * sizeof(float);
+        if ((e = stream_workspace(s, xb, &xa, 3)) != hipSuccess)
+            return fail_launch(e, what + ": workspace");
+        if ((e = hipMemcpyAsync(xa, x_dev, xb, hipMemcpyDeviceToDevice, s)) != hipSuccess)
+            return fail_hip(e, (what + ": staging x").c_str());
+        x_dev = static_cast<const float*>(xa);
+    }
     float* out = y_dev;
     int run_epi = epi;
     if (epi == kEpiSwiglu && !(path == UNILLM_PATH_GEMV && gemv_supports_swiglu(*w, m))) {
         void* ws = nullptr;
-        hipError_t e = stream_workspace(s, (size_t)m * (size_t)w->n * sizeof(float), &ws, 1);
-        if (e != hipSuccess) return fail_hip(e, "QMatMul forward failed: workspace");
+        e = stream_workspace(s, (size_t)m * (size_t)w->n * sizeof(float), &ws, 1);
+        if (e != hipSuccess) return fail_launch(e, what + ": workspace");
         out = static_cast<float*>(ws);
         run_epi = kEpiStore;
     }
-    hipError_t e;
     switch (path) {
         case UNILLM_PATH_GEMV:
             if (!gemv_supports(*w, m))
                 return fail(UNILLM_ERR_UNSUPPORTED,
-                            "GEMV path takes m <= 4, k <= " +
+                            what + ": GEMV path takes m <= 4, k <= " +
                                 std::to_string(gemv_max_kb(m, w->qtype) * QK) +
                                 " at this m and weights under 4 GiB");
             e = launch_gemv(*w, x_dev, m, out, s, run_epi, norm);
             break;
         case UNILLM_PATH_DECODE_MFMA:
             if (m > kDecodeMaxM)
-                return fail(UNILLM_ERR_UNSUPPORTED, "decode MFMA path takes m <= 64");
+                return fail(UNILLM_ERR_UNSUPPORTED, what + ": decode MFMA path takes m <= 64");
             e = launch_decode_mfma(*w, x_dev, m, out, s, run_epi, norm);
             break;
         case UNILLM_PATH_PREFILL_MFMA:
             e = launch_prefill_mfma(*w, x_dev, m, out, s, run_epi, norm);
             break;
         default:
-            return fail(UNILLM_ERR_INVALID_ARG, "unknown path " + std::to_string(path));
+            return fail(UNILLM_ERR_INVALID_ARG, what + ": unknown path " + std::to_string(path));
     }
     if (e == hipSuccess && out != y_dev) e = launch_swiglu(out, m, w->n / 2, y_dev, s);
-    return e == hipSuccess ? UNILLM_OK : fail_hip(e, "QMatMul forward failed: kernel launch");
+    return e == hipSuccess ? UNILLM_OK : fail_launch(e, what + ": kernel launch");
 }
 
 }  // namespace
@@ -416,6 +452,35 @@ int unillm_hip_qmatmul_norm_swiglu(const unillm_qweight* w, const float* x_dev,
 int unillm_hip_qmatmul(const unillm_qweight* w, const float* x_dev, int64_t m, float* y_dev,
                        void* stream) {
     return unillm_hip_qmatmul_path(w, x_dev, m, y_dev, UNILLM_PATH_AUTO, stream);
+}
+
+int unillm_hip_qmatmul_reserve(const unillm_qweight* w, int64_t m, int swiglu, void* stream) {
+    if (!w || m < 0) return fail(UNILLM_ERR_INVALID_ARG, "reserve: weight is NULL or m < 0");
+    if (m == 0) return UNILLM_OK;
+    if (m > (int64_t)INT32_MAX / 2) return fail(UNILLM_ERR_INVALID_ARG, "reserve: m too large");
+    if (int rc = ensure_init()) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // slot 0: the x operand of either MFMA path at any m' <= m (both sizes grow with m)
+    const size_t x0 = std::max(decode_workspace_bytes(*w, std::min<int64_t>(m, kDecodeMaxM)),
+                               prefill_workspace_bytes(*w, m));
+    void* p = nullptr;
+    hipError_t e = stream_workspace(s, x0, &p, 0);
+    // slot 1: the [gate | up] product of a SwiGLU call off the GEMV path
+    if (e == hipSuccess && swiglu)
+        e = stream_workspace(s, (size_t)m * (size_t)w->n * sizeof(float), &p, 1);
+    return e == hipSuccess ? UNILLM_OK : fail_launch(e, "reserve");
+}
+
+int unillm_hip_attention_reserve(const unillm_kv_cache* c, int64_t m, int64_t n_heads,
+                                 void* stream) {
+    if (!c || m < 1 || n_heads < c->n_kv_heads || n_heads % c->n_kv_heads != 0)
+        return fail(UNILLM_ERR_INVALID_ARG,
+                    "attention reserve: need a cache, m >= 1 and n_heads a multiple of n_kv_heads");
+    if (int rc = ensure_init()) return rc;
+    void* p = nullptr;
+    hipError_t e = stream_workspace(static_cast<hipStream_t>(stream),
+                                    attention_workspace_bytes(*c, m, n_heads), &p, 2);
+    return e == hipSuccess ? UNILLM_OK : fail_launch(e, "attention reserve");
 }
 
 int unillm_hip_dequant(const unillm_qweight* w, float* out_dev, void* stream) {
@@ -535,7 +600,7 @@ int unillm_hip_attention_decode(unillm_kv_cache* c, const float* qkv_dev, int64_
     if (int rc = ensure_init()) return rc;
     hipError_t e = launch_attention_decode(*c, qkv_dev, m, n_heads, out_dev,
                                            static_cast<hipStream_t>(stream));
-    if (e != hipSuccess) return fail_hip(e, "attention launch");
+    if (e != hipSuccess) return fail_launch(e, "attention launch");
     c->len += m;  // the kernels run in stream order: later calls see the appended rows
     return UNILLM_OK;
 }

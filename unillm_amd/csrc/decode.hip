@@ -755,11 +755,12 @@ hipError_t launch_x_to_f16_rows(const float* x, int64_t m, int64_t k, void* out,
     return hipGetLastError();
 }
 
+size_t decode_workspace_bytes(const QWeight& w, int64_t m) { return (size_t)m * (size_t)w.k * 2; }
+
 hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float* y,
-                              hipStream_t s, int epi, const NormArgs& norm) {
+                              hipStream_t s, int epi, const NormArgs& norm, void* ws) {
     // 32-bit offsets: x in f16 elements, weight bytes
-    if ((uint64_t)m * (uint64_t)w.k >= (1ull << 31) ||
-        (uint64_t)w.n * (uint64_t)w.row_bytes >= (1ull << 32))
+    if ((uint64_t)m * (uint64_t)w.k >= (1ull << 31) || !mfma_supports(w))
         return hipErrorInvalidValue;
     const bool q4 = w.qtype == UNILLM_QTYPE_Q4_0, k4 = w.qtype == UNILLM_QTYPE_Q4_K,
                k6 = w.qtype == UNILLM_QTYPE_Q6_K, wide = m > 32;
@@ -768,9 +769,9 @@ hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float
                     : q4 ? (wide ? Stage<UNILLM_QTYPE_Q4_0, 2>::LDS : Stage<UNILLM_QTYPE_Q4_0, 1>::LDS)
                          : (wide ? Stage<UNILLM_QTYPE_Q8_0, 2>::LDS : Stage<UNILLM_QTYPE_Q8_0, 1>::LDS);
     const int S = choose_split(w, lds);
-    void* ws = nullptr;
-    hipError_t e = stream_workspace(s, (size_t)m * (size_t)w.k * 2, &ws);
-    if (e != hipSuccess) return e;
+    hipError_t e = hipSuccess;
+    if (!ws && (e = stream_workspace(s, decode_workspace_bytes(w, m), &ws)) != hipSuccess)
+        return e;
     const int64_t n8 = m * w.k / 8;  // k % 32 == 0
     const int add = epi == kEpiAdd;
     const int64_t ny = S > 1 && !add ? m * w.n : 0;

@@ -160,12 +160,23 @@ hipError_t launch_quantize(int qtype, const float* w, int64_t n, int64_t k, uint
 // (gemv_supports_swiglu), the other paths run it as store + swiglu_kernel.
 hipError_t launch_gemv(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t s,
                        int epi = kEpiStore, const NormArgs& norm = NormArgs{nullptr, nullptr, 0.f});
+// The MFMA paths take their x operand buffer from `ws` when it is given (at least
+// decode_workspace_bytes / prefill_workspace_bytes for this w and m), else from
+// the stream's workspace (slot 0).
 hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float* y,
                               hipStream_t s, int epi = kEpiStore,
-                              const NormArgs& norm = NormArgs{nullptr, nullptr, 0.f});
+                              const NormArgs& norm = NormArgs{nullptr, nullptr, 0.f},
+                              void* ws = nullptr);
 hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, float* y,
                                hipStream_t s, int epi = kEpiStore,
-                               const NormArgs& norm = NormArgs{nullptr, nullptr, 0.f});
+                               const NormArgs& norm = NormArgs{nullptr, nullptr, 0.f},
+                               void* ws = nullptr);
+size_t decode_workspace_bytes(const QWeight& w, int64_t m);
+size_t prefill_workspace_bytes(const QWeight& w, int64_t m);
+// Both MFMA paths address weight bytes with 32-bit offsets: weights under 4 GiB.
+inline bool mfma_supports(const QWeight& w) {
+    return (uint64_t)w.n * (uint64_t)w.row_bytes < (1ull << 32);
+}
 // x[m, k] -> its layer norm in the MFMA paths' operand form (f16 in the decode
 // kernel's element order, or bf16), one workgroup per row; zeroes y rows
 // [0, m) of width ny when ny > 0 (a split k adds into it).
@@ -189,6 +200,8 @@ hipError_t launch_swiglu(const float* gu, int64_t m, int64_t I, float* act, hipS
 using KvCache = ::unillm_kv_cache;
 hipError_t launch_attention_decode(const KvCache& kv, const float* qkv, int64_t m, int64_t H,
                                    float* out, hipStream_t s);
+// Workspace (slot 2) a call of m tokens and H heads needs at any cache length.
+size_t attention_workspace_bytes(const KvCache& kv, int64_t m, int64_t H);
 int attention_max_queries();  // m * H / KVH per call
 int64_t attention_max_positions();  // len + m per call
 

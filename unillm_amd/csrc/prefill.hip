@@ -546,16 +546,22 @@ PrefillPlan prefill_plan(const QWeight& w, int64_t m) {
 
 }  // namespace
 
+size_t prefill_workspace_bytes(const QWeight& w, int64_t m) {
+    return ((size_t)m * (size_t)w.k * 2 + 255) / 256 * 256 + (size_t)m * sizeof(float);
+}
+
 hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, float* y,
-                               hipStream_t s, int epi, const NormArgs& norm) {
-    // x as f16 rows with their power-of-two scales in the stream's workspace: the
-    // GEMM re-reads x once per 256-column tile, so it reads half the bytes, and no
+                               hipStream_t s, int epi, const NormArgs& norm, void* ws) {
+    // weight bytes are addressed with 32-bit offsets (pcol_off, ssrc)
+    if (!mfma_supports(w)) return hipErrorInvalidValue;
+    // x as f16 rows with their power-of-two scales in the workspace: the GEMM
+    // re-reads x once per 256-column tile, so it reads half the bytes, and no
     // conversion sits in its inner loop.  The conversion zeroes y for a split k.
     const PrefillPlan plan = prefill_plan(w, m);
     const size_t xbytes = ((size_t)m * (size_t)w.k * 2 + 255) / 256 * 256;
-    void* ws = nullptr;
-    hipError_t e = stream_workspace(s, xbytes + (size_t)m * sizeof(float), &ws);
-    if (e != hipSuccess) return e;
+    hipError_t e = hipSuccess;
+    if (!ws && (e = stream_workspace(s, prefill_workspace_bytes(w, m), &ws)) != hipSuccess)
+        return e;
     float* rs = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + xbytes);
     const int add = epi == kEpiAdd;
     const int64_t yn = plan.S > 1 && !add ? w.n : 0;

@@ -2,6 +2,7 @@
 // against the file size, so truncated or hostile files raise GgufError.
 #include "gguf.hpp"
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <memory>
@@ -70,7 +71,9 @@ public:
                 const uint64_t n = pod<uint64_t>();
                 if (n > kMaxCount || n > size_ - pos_)
                     throw GgufError("gguf: array length " + std::to_string(n));
-                v.items.reserve(n);
+                // a parsed item is ~100 bytes against >= 1 byte of file: reserve a
+                // bounded count and let the vector grow with the items actually read
+                v.items.reserve((size_t)std::min<uint64_t>(n, 4096));
                 for (uint64_t i = 0; i < n; ++i) v.items.push_back(value(v.array_type, depth + 1));
                 break;
             }
@@ -163,7 +166,7 @@ GgufFile GgufFile::open(const std::string& path) {
             throw GgufError("gguf: general.alignment must be a power of two");
         g.alignment_ = a->u;
     }
-    g.tensors_.reserve(n_tensors);
+    g.tensors_.reserve((size_t)std::min<uint64_t>(n_tensors, 4096));  // grows as read
     for (uint64_t i = 0; i < n_tensors; ++i) {
         GgufTensorInfo t;
         t.name = r.str();

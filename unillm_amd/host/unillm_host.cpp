@@ -12,6 +12,16 @@ void check(int rc, const char* what) {
         throw Error(std::string(what) + ": " + unillm_hip_last_error());
 }
 
+// A failed matmul call: `ctx` (the caller's anyhow context, llama.rs:399, 1189) and
+// the C ABI's detail, without the ABI's own "QMatMul forward failed: " prefix.
+void check_qmatmul(int rc, const char* ctx) {
+    if (rc == UNILLM_OK) return;
+    std::string m = unillm_hip_last_error();
+    const std::string p = "QMatMul forward failed: ";
+    if (m.compare(0, p.size(), p) == 0) m = m.substr(p.size());
+    throw Error(std::string(ctx) + ": " + m);
+}
+
 int64_t product(const std::vector<int64_t>& shape) {
     int64_t p = 1;
     for (int64_t d : shape) {
@@ -179,7 +189,7 @@ Tensor QuantLinear::forward(const Tensor& x, void* stream) const {
     oshape.back() = n_;
     Tensor y = Tensor::empty(oshape, x.device());
     const int64_t m = x.numel() / k_;
-    check(unillm_hip_qmatmul(w_, x.data(), m, y.data_mut(), stream), "QMatMul forward failed");
+    check_qmatmul(unillm_hip_qmatmul(w_, x.data(), m, y.data_mut(), stream), "QMatMul forward failed");
     return y;
 }
 
@@ -189,8 +199,9 @@ void QuantLinear::forward_add(const Tensor& x, Tensor& residual, void* stream) c
     oshape.back() = n_;
     if (residual.shape() != oshape || !residual.device().is_hip())
         throw Error("QMatMul forward failed: residual must be a HIP tensor of the output shape");
-    check(unillm_hip_qmatmul_add(w_, x.data(), x.numel() / k_, residual.data_mut(), stream),
-          "QMatMul forward failed");
+    check_qmatmul(
+        unillm_hip_qmatmul_add(w_, x.data(), x.numel() / k_, residual.data_mut(), stream),
+        "QMatMul forward failed");
 }
 
 Tensor QuantLinear::forward_swiglu(const Tensor& x, void* stream) const {
@@ -198,8 +209,9 @@ Tensor QuantLinear::forward_swiglu(const Tensor& x, void* stream) const {
     std::vector<int64_t> oshape = x.shape();
     oshape.back() = n_ / 2;
     Tensor act = Tensor::empty(oshape, x.device());
-    check(unillm_hip_qmatmul_swiglu(w_, x.data(), x.numel() / k_, act.data_mut(), stream),
-          "QMatMul forward failed");
+    check_qmatmul(
+        unillm_hip_qmatmul_swiglu(w_, x.data(), x.numel() / k_, act.data_mut(), stream),
+        "QMatMul forward failed");
     return act;
 }
 
@@ -214,10 +226,24 @@ Tensor QuantLinear::forward_norm(const Tensor& x, const Tensor& gamma, const Ten
     std::vector<int64_t> oshape = x.shape();
     oshape.back() = n_;
     Tensor y = Tensor::empty(oshape, x.device());
-    check(unillm_hip_qmatmul_norm(w_, x.data(), gamma.data(), beta ? beta->data() : nullptr, eps,
-                                  x.numel() / k_, y.data_mut(), stream),
-          "QMatMul forward failed");
+    check_qmatmul(unillm_hip_qmatmul_norm(w_, x.data(), gamma.data(),
+                                          beta ? beta->data() : nullptr, eps, x.numel() / k_,
+                                          y.data_mut(), stream),
+                  "QMatMul forward failed");
     return y;
+}
+
+Tensor lm_head_forward(const QuantLinear& lm_head, const Tensor& hidden_states, void* stream) {
+    // LlamaModelV2::lm_head_forward (llama.rs:396-405) maps the QMatMul error to
+    // "QMatMul lm_head forward failed: {e}"
+    try {
+        return lm_head.forward(hidden_states, stream);
+    } catch (const Error& e) {
+        std::string m = e.what();
+        const std::string p = "QMatMul forward failed: ";
+        if (m.compare(0, p.size(), p) == 0) m = m.substr(p.size());
+        throw Error("QMatMul lm_head forward failed: " + m);
+    }
 }
 
 Tensor QuantLinear::dequantize(void* stream) const {

@@ -135,6 +135,12 @@ private:
     int64_t n_ = 0, k_ = 0;
 };
 
+// LlamaModelV2::lm_head_forward (llama.rs:396-405) with a quantized lm_head: the
+// projection of the final hidden states to logits, errors reported as the reference
+// reports them ("QMatMul lm_head forward failed: ...").
+Tensor lm_head_forward(const QuantLinear& lm_head, const Tensor& hidden_states,
+                       void* stream = nullptr);
+
 // ---- KV cache and decode attention ------------------------------------------------------------
 // One decoder layer's cache for one sequence on the HIP device: K and V of n_kv_heads
 // heads, max_seq_len positions of head_dim f32 (kv_cache.rs:28-183; the reference's

@@ -86,6 +86,13 @@ class QuantLinear:
     def select_path(self, m: int) -> int:
         return _capi.lib().unillm_hip_select_path(self._h, m)
 
+    def reserve(self, m: int, swiglu: bool = False,
+                stream: torch.cuda.Stream | None = None) -> None:
+        """Grow the stream's workspace for calls of up to m rows, so they can be
+        captured into a HIP graph (a capture cannot allocate)."""
+        _capi.check(_capi.lib().unillm_hip_qmatmul_reserve(self._h, m, int(swiglu),
+                                                           _stream_ptr(stream)))
+
     # ---- compute -------------------------------------------------------------------------
     def _check_input(self, x: torch.Tensor) -> int:
         if x.dtype != torch.float32:
@@ -198,6 +205,25 @@ class QuantLinear:
         name = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}.get(self.qtype,
                                                                          str(self.qtype))
         return f"QuantLinear({name}, n={self.n}, k={self.k})"
+
+
+def lm_head_forward(lm_head: QuantLinear, hidden_states: torch.Tensor,
+                    out: torch.Tensor | None = None,
+                    stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """LlamaModelV2::lm_head_forward (crates/runtime/src/models_v2/llama.rs:396-405)
+    with a quantized lm_head: logits = hidden . dequant(W)^T, errors worded as the
+    reference words them ("QMatMul lm_head forward failed: ...")."""
+    prefix = "QMatMul forward failed: "
+    try:
+        return lm_head.forward(hidden_states, out=out, stream=stream)
+    except HipError as e:
+        msg = str(e)
+        raise HipError(e.status, "QMatMul lm_head forward failed: " +
+                       (msg[len(prefix):] if msg.startswith(prefix) else msg)) from None
+    except RuntimeError as e:
+        msg = str(e)
+        raise RuntimeError("QMatMul lm_head forward failed: " +
+                           (msg[len(prefix):] if msg.startswith(prefix) else msg)) from None
 
 
 def quantize_blocks(qtype: int, w: torch.Tensor,

@@ -118,6 +118,19 @@ int unillm_hip_qmatmul(const unillm_qweight* w, const float* x_dev, int64_t m, f
  * (a captured graph may still use them).  A graph uses the buffers of the stream
  * it was captured on: replay it on that stream. */
 
+/* unillm_hip_qmatmul without any allocation.  No counterpart in the reference
+ * (candle allocates per call): it is for callers that cannot allocate device
+ * memory -- code under HIP graph capture, tight serving loops.  Same result as
+ * unillm_hip_qmatmul (same kernels); the MFMA paths keep their f16 copy of x in
+ * a 64 MiB scratch array that the library holds on each GPU from load to process
+ * end, instead of the stream's workspace.  Limits: x 16-byte aligned; the scratch
+ * takes m * k * 2 bytes (+ 4 m for prefill): calls beyond 64 MiB fail with
+ * UNILLM_ERR_UNSUPPORTED before any launch.  All calls on one GPU share its
+ * scratch: calls that overlap in time on one GPU (concurrent streams, or threads
+ * without ordering) race and must not be issued. */
+int unillm_hip_qmatmul_noalloc(const unillm_qweight* w, const float* x_dev, int64_t m,
+                               float* y_dev, void* stream);
+
 /* As unillm_hip_qmatmul with an explicit kernel path (UNILLM_PATH_*), for
  * tests and benchmarks; AUTO picks what unillm_hip_qmatmul picks. */
 int unillm_hip_qmatmul_path(const unillm_qweight* w, const float* x_dev, int64_t m,

@@ -60,6 +60,7 @@ SIGNATURES = {
          ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
     "unillm_hip_qmatmul": ([P, P, I64, P, P], ctypes.c_int),
     "unillm_hip_qmatmul_path": ([P, P, I64, P, ctypes.c_int, P], ctypes.c_int),
+    "unillm_hip_qmatmul_noalloc": ([P, P, I64, P, P], ctypes.c_int),
     "unillm_hip_qmatmul_add": ([P, P, I64, P, P], ctypes.c_int),
     "unillm_hip_qmatmul_swiglu": ([P, P, I64, P, P], ctypes.c_int),
     "unillm_hip_qmatmul_norm": ([P, P, P, P, ctypes.c_float, I64, P, P], ctypes.c_int),

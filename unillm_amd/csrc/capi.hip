@@ -20,6 +20,15 @@
 namespace unillm {
 namespace {
 
+// The scratch of the no-allocation entry point (unillm_hip_qmatmul_noalloc): the x
+// operand of the MFMA paths, in device memory that exists from module load to
+// process end, one copy per GPU.  In host code the array's name denotes a host-side
+// stand-in, not device memory: host code uses only the device address that
+// hipGetSymbolAddress returns at init, kept per device in g_scratch_ptr.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+std::vector<void*> g_scratch_ptr;  // by device index; nullptr before that device's init
+
 thread_local std::string g_last_error;
 std::once_flag g_init_once;
 int g_init_status = UNILLM_ERR_NOT_INITIALIZED;
@@ -63,6 +72,13 @@ int do_init(int device) {
         uint64_t keep = UINT64_MAX;
         (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
     }
+    // this GPU's copy of the no-allocation scratch: its device address, once
+    void* sp = nullptr;
+    if ((e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch))) != hipSuccess)
+        return fail_hip(e, "hipGetSymbolAddress (no-allocation scratch)");
+    if (!sp) return fail(UNILLM_ERR_HIP, "hipGetSymbolAddress returned no address for scratch");
+    g_scratch_ptr.assign((size_t)count, nullptr);
+    g_scratch_ptr[(size_t)device] = sp;
     g_device = device;
     return UNILLM_OK;
 }
@@ -338,9 +354,12 @@ int fail_launch(hipError_t e, const std::string& what) {
 // The matmul on `path` with epilogue `epi` (kEpiStore / kEpiAdd; kEpiSwiglu runs
 // fused on the GEMV, else as store into the stream's second workspace + swiglu).
 // `what` prefixes every error message (the caller's anyhow context).
+// fixed_ws != nullptr (the no-allocation entry point, store epilogue only): the MFMA
+// paths take their x operand from fixed_ws (fixed_bytes long), and nothing allocates.
 int qmatmul_impl(const unillm_qweight* w, const float* x_dev, int64_t m, float* y_dev, int path,
                  void* stream, int epi, const NormArgs& norm = NormArgs{nullptr, nullptr, 0.f},
-                 const std::string& what = "QMatMul forward failed") {
+                 const std::string& what = "QMatMul forward failed", void* fixed_ws = nullptr,
+                 size_t fixed_bytes = 0) {
     if (!w) return fail(UNILLM_ERR_INVALID_ARG, what + ": weight is NULL");
     if (m < 0) return fail(UNILLM_ERR_INVALID_ARG, what + ": m < 0");
     if (epi == kEpiSwiglu && w->n % 2 != 0)
@@ -374,6 +393,19 @@ int qmatmul_impl(const unillm_qweight* w, const float* x_dev, int64_t m, float* 
     // x not on a 16-byte boundary (candle takes any contiguous f32): the kernels
     // load x 16 bytes at a time, so it is first copied, stream-ordered, into an
     // aligned workspace (slot 3)
+    if (fixed_ws) {
+        if (!aligned16(x_dev))
+            return fail(UNILLM_ERR_INVALID_ARG,
+                        what + ": the no-allocation entry point takes x 16-byte aligned");
+        const size_t need = path == UNILLM_PATH_DECODE_MFMA    ? decode_workspace_bytes(*w, m)
+                            : path == UNILLM_PATH_PREFILL_MFMA ? prefill_workspace_bytes(*w, m)
+                                                               : 0;
+        if (need > fixed_bytes)
+            return fail(UNILLM_ERR_UNSUPPORTED,
+                        what + ": this call needs " + std::to_string(need) +
+                            " bytes of scratch; the no-allocation entry point holds " +
+                            std::to_string(fixed_bytes) + " (m * k too large)");
+    }
     if (!aligned16(x_dev)) {
         void* xa = nullptr;
         const size_t xb = (size_t)m * (size_t)w->k * sizeof(float);
@@ -404,10 +436,10 @@ int qmatmul_impl(const unillm_qweight* w, const float* x_dev, int64_t m, float* 
         case UNILLM_PATH_DECODE_MFMA:
             if (m > kDecodeMaxM)
                 return fail(UNILLM_ERR_UNSUPPORTED, what + ": decode MFMA path takes m <= 64");
-            e = launch_decode_mfma(*w, x_dev, m, out, s, run_epi, norm);
+            e = launch_decode_mfma(*w, x_dev, m, out, s, run_epi, norm, fixed_ws);
             break;
         case UNILLM_PATH_PREFILL_MFMA:
-            e = launch_prefill_mfma(*w, x_dev, m, out, s, run_epi, norm);
+            e = launch_prefill_mfma(*w, x_dev, m, out, s, run_epi, norm, fixed_ws);
             break;
         default:
             return fail(UNILLM_ERR_INVALID_ARG, what + ": unknown path " + std::to_string(path));
@@ -452,6 +484,16 @@ int unillm_hip_qmatmul_norm_swiglu(const unillm_qweight* w, const float* x_dev,
 int unillm_hip_qmatmul(const unillm_qweight* w, const float* x_dev, int64_t m, float* y_dev,
                        void* stream) {
     return unillm_hip_qmatmul_path(w, x_dev, m, y_dev, UNILLM_PATH_AUTO, stream);
+}
+
+int unillm_hip_qmatmul_noalloc(const unillm_qweight* w, const float* x_dev, int64_t m,
+                               float* y_dev, void* stream) {
+    if (int rc = ensure_init()) return rc;
+    void* sp = (size_t)g_device < g_scratch_ptr.size() ? g_scratch_ptr[(size_t)g_device] : nullptr;
+    if (!sp) return fail(UNILLM_ERR_NOT_INITIALIZED, "no-allocation scratch has no device address");
+    return qmatmul_impl(w, x_dev, m, y_dev, UNILLM_PATH_AUTO, stream, kEpiStore,
+                        NormArgs{nullptr, nullptr, 0.f}, "QMatMul forward failed", sp,
+                        kNoAllocScratchBytes);
 }
 
 int unillm_hip_qmatmul_reserve(const unillm_qweight* w, int64_t m, int swiglu, void* stream) {

@@ -97,10 +97,10 @@ int unillm_hip_qweight_info(const unillm_qweight* w, int* qtype, int64_t* n, int
  * (crates/runtime/src/models_v2/llama.rs:1184-1195, 1325-1336) and
  * LlamaModelV2::lm_head_forward (llama.rs:396-405); the m rows are the
  * flattened leading dims of the [.., k] input.  m == 0 is a no-op.
- * Operand range: the GEMV (exact integer digits of x) and prefill (f16 rows,
- * each scaled by its own power of two) take any finite x; batched decode
- * (UNILLM_PATH_DECODE_MFMA) rounds x to f16 unscaled, so its x must satisfy
- * |x| <= 65504 (values below 2^-14 keep f16's fixed absolute precision). */
+ * Operand range: every path takes any finite x, as candle's per-block Q8_0
+ * activations do: the GEMV holds x as exact integer digits per 32-block, prefill
+ * rounds each row of x to f16 after scaling it by its own power of two, and
+ * batched decode does the same per row and k slice of its split. */
 int unillm_hip_qmatmul(const unillm_qweight* w, const float* x_dev, int64_t m, float* y_dev,
                        void* stream);
 

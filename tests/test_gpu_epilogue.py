@@ -166,6 +166,28 @@ def test_layer_norm_swiglu(qtype, m, i_rows, k):
     assert oracle.normwise_error(act, _silu_mul(g, u)) < 2e-3
 
 
+@pytest.mark.parametrize("qtype,m,k,path", [(Q4_0, 16, 4096, PATH_DECODE_MFMA),
+                                             (Q8_0, 5, 11008, PATH_DECODE_MFMA),
+                                             (Q4_0, 64, 4096, PATH_DECODE_MFMA),
+                                             (Q4_0, 96, 4096, PATH_PREFILL_MFMA)])
+def test_layer_norm_any_gamma_magnitude(qtype, m, k, path):
+    # the normalized rows times gamma ~ 1e6 (far past f16's 65504) or ~ 1e-7 (deep in
+    # its subnormals): the MFMA paths scale their f16 operand by powers of two, so
+    # every row stays as accurate as a unit one
+    n = 256
+    blocks = _blocks(qtype, n, k, seed=31 + k)
+    x = oracle.normal(m * k, seed=17 + m).reshape(m, k)
+    ql = QuantLinear.from_blocks(qtype, n, k, blocks)
+    assert ql.select_path(m) == path
+    for g in (1e6, 1e-7):
+        gamma = np.full(k, g, np.float32)
+        y = ql.forward_norm(_dev(x), _dev(gamma), None, eps=1e-6).cpu().numpy()
+        ref = oracle.qmatmul_f64(qtype, blocks, _layer_norm(x, gamma, None, 1e-6).astype(np.float32),
+                                 n, k)
+        for r in range(m):
+            assert oracle.normwise_error(y[r:r + 1], ref[r:r + 1]) < 1e-3, (g, r)
+
+
 def test_layer_norm_argument_checks():
     ql = QuantLinear.from_blocks(Q4_0, 4, 64, _blocks(Q4_0, 4, 64, seed=2))
     x = torch.zeros(1, 64, device="cuda")

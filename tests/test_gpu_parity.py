@@ -268,22 +268,54 @@ def test_prefill_large_tiles(qtype, m, k, n):
     assert np.array_equal(y2.cpu().numpy(), 2.0 * y)  # enough tiles: no k split
 
 
-@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
-def test_prefill_rows_of_any_magnitude(qtype):
-    # f16 operands with a power-of-two scale per row of x: rows far beyond the f16
-    # range (|x| ~ 1e6 > 65504), rows deep in its subnormals (~1e-7), an all-zero
-    # row and unit rows side by side, each as accurate as a unit row alone
-    m, n, k = 96, 256, 1024
-    blocks, x = _case(qtype, m, n, k, seed=91)
+@pytest.mark.parametrize("qtype,m,k,path", [(Q4_0, 96, 1024, PATH_PREFILL_MFMA),
+                                             (Q8_0, 96, 1024, PATH_PREFILL_MFMA),
+                                             (Q4_0, 5, 4096, PATH_DECODE_MFMA),
+                                             (Q4_0, 16, 4096, PATH_DECODE_MFMA),
+                                             (Q8_0, 16, 11008, PATH_DECODE_MFMA),
+                                             (Q4_0, 64, 4096, PATH_DECODE_MFMA),
+                                             (Q4_0, 2, 11008, PATH_DECODE_MFMA)])
+def test_rows_of_any_magnitude(qtype, m, k, path):
+    # f16 operands with a power-of-two scale per row of x (prefill) or per row and k
+    # slice (batched decode): rows far beyond the f16 range (|x| ~ 1e6 > 65504), rows
+    # deep in its subnormals (~1e-7), an all-zero row and unit rows side by side, each
+    # as accurate as a unit row alone.  (Q4_0, 2, 11008): the down projection at m = 2,
+    # which auto-routes here (past the GEMV's k at that m)
+    n = 256
+    blocks, x = _case(qtype, m, n, k, seed=91 + m)
     scale = np.ones(m, np.float32)
-    scale[0::4], scale[1::4], scale[6] = 1e6, 1e-7, 0.0
+    scale[0::4], scale[1::4] = 1e6, 1e-7
+    zero = 2 if m > 2 else None
+    if zero is not None:
+        scale[zero] = 0.0
     xs = (x * scale[:, None]).astype(np.float32)
-    y = _run(QuantLinear.from_blocks(qtype, n, k, blocks), xs, PATH_PREFILL_MFMA)
+    ql = QuantLinear.from_blocks(qtype, n, k, blocks)
+    if path == PATH_DECODE_MFMA and m <= 4:
+        assert ql.select_path(m) == PATH_DECODE_MFMA
+    y = _run(ql, xs, path)
     ref = oracle.qmatmul_f64(qtype, blocks, xs, n, k)
-    assert np.all(y[6] == 0.0)
+    if zero is not None:
+        assert np.all(y[zero] == 0.0)
     for r in range(m):
-        if r != 6:
+        if r != zero:
             assert oracle.normwise_error(y[r:r + 1], ref[r:r + 1]) < 1e-3, (r, scale[r])
+    # within a row: a slice of huge values next to slices of small ones (each k slice
+    # of the batched-decode split has its own scale)
+    xm = x.copy()
+    xm[:, : k // 4] *= 1e5
+    y = _run(ql, xm, path)
+    assert oracle.normwise_error(y, oracle.qmatmul_f64(qtype, blocks, xm, n, k)) < 1e-3
+
+
+@pytest.mark.parametrize("m", [5, 16, 64])
+def test_batched_decode_power_of_two_scaling_exact(m):
+    # x and x times a power of two give the same f16 operands (per-slice scales):
+    # outputs scale exactly, up to the order of the split k's atomic adds
+    blocks, x = _case(Q4_0, m, 4096, 4096, seed=3 * m)
+    ql = QuantLinear.from_blocks(Q4_0, 4096, 4096, blocks)
+    y = _run(ql, x, PATH_DECODE_MFMA)
+    y2 = _run(ql, x * np.float32(2.0 ** 40), PATH_DECODE_MFMA)
+    assert oracle.normwise_error(y2, y * 2.0 ** 40) < 1e-6
 
 
 # ---- edges -----------------------------------------------------------------------------------

@@ -10,6 +10,11 @@
 //   1. xprep_kernel rounds x to f16 (round to nearest even) into a stream-ordered
 //      workspace, each aligned group of 8 k stored in the order 0 2 1 3 4 6 5 7
 //      (the order the dequant below produces), and zeroes y when k is split.
+//      Each (token, k slice of the split below) is first scaled by the power of two
+//      that puts its largest magnitude in [2^14, 2^15); the decode kernel multiplies
+//      each token's partial sum by the factor that undoes it.  So any finite x works
+//      (no f16 overflow, no loss to f16 subnormals), and x and x times a power of
+//      two give the same operands.
 //   2. decode_kernel: v_mfma_f32_32x32x16_f16 with the tokens as the A operand
 //      (32 tokens x 16 k) and the weights as B (16 k x 32 weight rows), so a
 //      lane's accumulator column is one weight row and the output stores and
@@ -37,7 +42,7 @@
 //   E is the weight's f16 exponent offset (8 max|d| 2^-E <= 65504), undone on
 //   the output: both scalings are exact.
 // Normwise error vs the f64 oracle ~3e-4 (f16 operands, f32 accumulation;
-// bound 1e-3).  x must lie in the f16 range (|x| <= 65504).
+// bound 1e-3).
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
@@ -145,26 +150,74 @@ __device__ __forceinline__ void dequant_q8(u32x4 raw, f16x2 dh, f16x8& f0, f16x8
     f1 = __builtin_bit_cast(f16x8, b);
 }
 
-// x (f32 [m, k]) -> f16 in the fragment order; y[0, ny) <- 0 (a split k range
-// adds into it).
-__global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x,
-                                                    uint4* __restrict__ xh, int64_t n8,
+}  // namespace
+
+// The power-of-two scale of an f16 operand row (or slice) whose largest magnitude is
+// mx: the values are multiplied by 2^(15 - e) (mx < 2^e), so the largest lands in
+// [2^14, 2^15) whatever the range; thread 0 stores the inverse, the output factor
+// 2^(e - 15), at *rs.  Zero or non-finite inputs keep the factor 1.  Both scalings are
+// exact, so x and x times a power of two give the same f16 operand.
+__device__ __forceinline__ float f16_row_scale(float mx, float* rs) {
+    int e = 0;
+    const bool ok = mx > 0.0f && mx <= 3.402823466e38f;
+    if (ok) (void)frexpf(mx, &e);
+    e = e < -111 ? -111 : e;  // keep 2^(15 - e) and 2^(e - 15) in range
+    if (threadIdx.x == 0) *rs = ok ? ldexpf(1.0f, e - 15) : 1.0f;
+    return ok ? ldexpf(1.0f, 15 - e) : 1.0f;
+}
+
+namespace {
+
+// Slice s of S of a row of k elements: the decode kernel's k split, 128-k chunks
+// [s C / S, (s + 1) C / S) with C = ceil(k / 128) (elements [e0, e1)).
+__device__ __forceinline__ void slice_range(int64_t k, int S, int s, int64_t& e0, int64_t& e1) {
+    const int64_t C = (k + 127) / 128;
+    e0 = (int64_t)s * C / S * 128;
+    e1 = min((int64_t)(s + 1) * C / S * 128, k);
+}
+
+// One workgroup (128 threads, one aligned group of 8 elements each) per (row r, k slice
+// s) of x[m, k]: the slice's largest magnitude, then the slice scaled by the power of two
+// that puts it in [2^14, 2^15) and rounded to f16 (round to nearest even) in the fragment
+// order 0 2 1 3 4 6 5 7 of each 8; rf[s * 64 + r] <- the factor that undoes the scaling
+// (f16_row_scale).  Each slice is at most kMaxSliceChunks * 128 = 1024 elements.  Any
+// finite x works: no overflow past 65504, no loss to f16 subnormals, and x and x times
+// a power of two give the same operand.  y row r is zeroed over columns
+// [s ny / S, (s + 1) ny / S) when ny > 0 (a split k range adds into it).
+__global__ __launch_bounds__(128) void xprep_kernel(const float* __restrict__ x, int64_t k,
+                                                    int S, uint4* __restrict__ xh,
+                                                    float* __restrict__ rf,
                                                     float* __restrict__ y, int64_t ny) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += stride) {
-        const float4 a = reinterpret_cast<const float4*>(x)[2 * i];
-        const float4 b = reinterpret_cast<const float4*>(x)[2 * i + 1];
-        xh[i] = make_uint4(pk_f16(a.x, a.z), pk_f16(a.y, a.w), pk_f16(b.x, b.z), pk_f16(b.y, b.w));
+    __shared__ float red[2];
+    const int r = blockIdx.x / S, s = blockIdx.x % S;
+    const int t = threadIdx.x;
+    int64_t e0, e1;
+    slice_range(k, S, s, e0, e1);
+    const int64_t g = e0 / 8 + t;
+    const bool live = 8 * (int64_t)t < e1 - e0;
+    const float4* xr = reinterpret_cast<const float4*>(x + (int64_t)r * k);
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+    if (live) {
+        a = xr[2 * g];
+        b = xr[2 * g + 1];
     }
-    // y: scalar stores up to a 16-byte boundary, then float4, then the tail
-    const int64_t head = std::min<int64_t>(ny, (int64_t)((16 - ((uintptr_t)y & 15)) & 15) / 4);
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < head; i += stride) y[i] = 0.0f;
-    float4* y4 = reinterpret_cast<float4*>(y + head);
-    const int64_t n4 = (ny - head) / 4;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride)
-        y4[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int64_t i = head + 4 * n4 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < ny; i += stride)
-        y[i] = 0.0f;
+    auto amax4 = [](float4 v) {
+        return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    };
+    float mx = fmaxf(amax4(a), amax4(b));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if ((t & 63) == 0) red[t >> 6] = mx;
+    __syncthreads();
+    const float sc = f16_row_scale(fmaxf(red[0], red[1]), rf + (int64_t)s * 64 + r);
+    if (live)
+        xh[(int64_t)r * (k / 8) + g] =
+            make_uint4(pk_f16(a.x * sc, a.z * sc), pk_f16(a.y * sc, a.w * sc),
+                       pk_f16(b.x * sc, b.z * sc), pk_f16(b.y * sc, b.w * sc));
+    if (ny > 0) {
+        const int64_t c0 = (int64_t)s * ny / S, c1 = (int64_t)(s + 1) * ny / S;
+        for (int64_t c = c0 + t; c < c1; c += 128) y[(int64_t)r * ny + c] = 0.0f;
+    }
 }
 
 // LDS: a D-stage ring, each stage one 128-k chunk of
@@ -177,12 +230,13 @@ __global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x,
 // rotation put the rows (tokens) that one LDS read pass serves -- 8 or 16
 // consecutive lanes -- on distinct banks.
 constexpr int kMaxSliceChunks = 8;
-#ifndef DECODE_MAX_SPLIT
-#define DECODE_MAX_SPLIT 4
-#endif
-// at most this many k slices add into one output (more slices contend on the
-// same y lines with their atomics)
-constexpr int kMaxSplit = DECODE_MAX_SPLIT;
+// most k slices of one row (a row of up to 256 * 8 * 128 = 262144 elements)
+constexpr int kMaxSplitSlices = 256;
+// At most this many k slices add into one output when the row groups alone leave
+// CUs idle: 8 for one 32-token tile (m16 n4096: 9.9 us a call against 11.1 with 4),
+// 4 for two (more slices contend on the same y lines with their atomics; m64 n4096:
+// 16.0 us with 4 against 16.4 with 8).
+constexpr int kMaxSplit1 = 8, kMaxSplit2 = 4;
 
 template <int QT, int MT2>
 struct Stage {
@@ -277,6 +331,7 @@ __device__ __forceinline__ void read_half(lds_u32x4 (&xa)[MT2][4], u32x4 (&pw)[2
 template <int QT, int MT2>
 __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__ base, int64_t rb,
                                                      const _Float16* __restrict__ xh,
+                                                     const float* __restrict__ rf,
                                                      float* __restrict__ y, int M, int N, int KB,
                                                      int S, float wscale, float oscale, int add) {
     using ST = Stage<QT, MT2>;
@@ -302,6 +357,16 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
     const int nch = c1 - c0;
     const int row0 = rg * DROWS + 32 * wv;  // this wave's 32 weight rows
     const uint32_t sbase = (uint32_t)KB * QB;  // the scales follow the payloads in a row
+
+    // ---- the output factors of this k slice's token rows (the power-of-two scale x's
+    // slice took in xprep_kernel): token 32 t + 8 q + 4 h + e in fac[t][q] component e.
+    // Loaded first, so every later wait covers them; tokens past m read unused values.
+    float4 fac[MT2][4];
+#pragma unroll
+    for (int t = 0; t < MT2; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            fac[t][q] = *reinterpret_cast<const float4*>(rf + sp * 64 + 32 * t + 8 * q + 4 * h);
 
     // ---- the slice's scales: 8 positions of 8 bytes a row (kMaxSliceChunks), 8
     // dword loads per wave; lane -> flat dword f = 64 i + lane = row f / 16,
@@ -492,16 +557,22 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
     }
 
     // ---- epilogue: acc[t][r] = C[token 32 t + 8 (r / 4) + 4 h + r % 4][row row0 + col] ----
-    // A split k range (S > 1) meets in y by f32 atomic adds onto zeros.  With
-    // m % 8 == 0 a token block (t, r / 4) is valid for all lanes or none.
+    // Each token's sum is scaled back by its slice factor and the weight's 2^E.  A
+    // split k range (S > 1) meets in y by f32 atomic adds onto zeros.  With m % 8 == 0
+    // a token block (t, r / 4) is valid for all lanes or none.
     const int n = row0 + col;
     if (n < N) {
         float* yb = y + (int64_t)(4 * h) * N + n;
         // y += (the residual add) or y =; a split k range always adds (onto zeros
         // written by xprep_kernel, or onto y itself with add)
-        auto put = [&](float* dst, float v) {
-            if (S == 1) *dst = add ? *dst + v * oscale : v * oscale;
-            else unsafeAtomicAdd(dst, v * oscale);
+        auto put = [&](float* dst, float v, float f) {
+            const float o = v * (f * oscale);
+            if (S == 1) *dst = add ? *dst + o : o;
+            else unsafeAtomicAdd(dst, o);
+        };
+        auto fct = [&](int t, int r) {
+            const float4 f = fac[t][r / 4];
+            return r % 4 == 0 ? f.x : r % 4 == 1 ? f.y : r % 4 == 2 ? f.z : f.w;
         };
         if (M % 8 == 0) {
 #pragma unroll
@@ -511,7 +582,8 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
                     if (32 * t + 8 * rb4 >= M) break;
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        put(yb + (int64_t)(32 * t + 8 * rb4 + e) * N, acc[t][4 * rb4 + e]);
+                        put(yb + (int64_t)(32 * t + 8 * rb4 + e) * N, acc[t][4 * rb4 + e],
+                            fct(t, 4 * rb4 + e));
                 }
         } else {
 #pragma unroll
@@ -519,15 +591,15 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int m0 = 32 * t + 8 * (r / 4) + (r % 4);
-                    if (m0 + 4 * h < M) put(yb + (int64_t)m0 * N, acc[t][r]);
+                    if (m0 + 4 * h < M) put(yb + (int64_t)m0 * N, acc[t][r], fct(t, r));
                 }
         }
     }
 }
 
 template <int QT, int MT2>
-hipError_t launch_mt(const QWeight& w, const _Float16* xh, int64_t m, float* y, int S,
-                     hipStream_t s, int add) {
+hipError_t launch_mt(const QWeight& w, const _Float16* xh, const float* rf, int64_t m, float* y,
+                     int S, hipStream_t s, int add) {
     using ST = Stage<QT, MT2>;
     static const bool attr = hipFuncSetAttribute((const void*)decode_kernel<QT, MT2>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -536,22 +608,20 @@ hipError_t launch_mt(const QWeight& w, const _Float16* xh, int64_t m, float* y, 
     const float wscale = ldexpf(1.0f, -w.f16_exp), oscale = ldexpf(1.0f, w.f16_exp);
     const int groups = (int)((w.n + DROWS - 1) / DROWS);
     decode_kernel<QT, MT2><<<groups * S, 256, ST::LDS, s>>>(
-        w.base, w.row_bytes, xh, y, (int)m, (int)w.n, (int)w.kb, S, wscale, oscale, add);
+        w.base, w.row_bytes, xh, rf, y, (int)m, (int)w.n, (int)w.kb, S, wscale, oscale, add);
     return hipGetLastError();
 }
 
 // k split S: the fewest slices of at most kMaxSliceChunks chunks, then more
 // while the workgroups still fit the CUs at once (lds_bytes each).
-int choose_split(const QWeight& w, int lds_bytes) {
+int choose_split(const QWeight& w, int lds_bytes, bool wide) {
     const int64_t groups = (w.n + DROWS - 1) / DROWS;
     const int64_t chunks = (w.kb + 3) / 4;
     const int64_t per_cu = std::max(1, device_info().max_lds_cu / lds_bytes);
     const int64_t slots = (int64_t)device_info().cu_count * per_cu;
     int64_t S = (chunks + kMaxSliceChunks - 1) / kMaxSliceChunks;
-    while (S < std::min<int64_t>(chunks, kMaxSplit) && groups * (S + 1) <= slots) ++S;
-#ifdef FORCE_S
-    S = std::min<int64_t>(std::max<int64_t>(FORCE_S, (chunks + kMaxSliceChunks - 1) / kMaxSliceChunks), chunks);
-#endif
+    const int64_t cap = std::min<int64_t>(chunks, wide ? kMaxSplit2 : kMaxSplit1);
+    while (S < cap && groups * (S + 1) <= slots) ++S;
     return (int)S;
 }
 
@@ -569,26 +639,6 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
 }
 
 }  // namespace
-
-// One workgroup per row r of x: the row's layer norm (two passes for the mean and
-// the mean squared deviation, as ops_fn::layer_norm computes them), then each
-// group of 8 normalized values converted to the MFMA operand type -- f16 in the
-// decode kernel's order 0 2 1 3 4 6 5 7, or bf16 in order -- and y's row r
-// zeroed over ny columns.
-// The power-of-two row scale of an f16 operand row whose largest magnitude is mx:
-// the row is multiplied by 2^(15 - e) (mx < 2^e), so its largest value lands in
-// [2^14, 2^15) whatever the row's range; thread 0 stores the inverse, the output
-// factor 2^(e - 15), at *rs.  Zero or non-finite rows keep the factor 1.  Both
-// scalings are exact, so a row and the same row times a power of two give the
-// same f16 operand.
-__device__ __forceinline__ float f16_row_scale(float mx, float* rs) {
-    int e = 0;
-    const bool ok = mx > 0.0f && mx <= 3.402823466e38f;
-    if (ok) (void)frexpf(mx, &e);
-    e = e < -111 ? -111 : e;  // keep 2^(15 - e) and 2^(e - 15) in range
-    if (threadIdx.x == 0) *rs = ok ? ldexpf(1.0f, e - 15) : 1.0f;
-    return ok ? ldexpf(1.0f, 15 - e) : 1.0f;
-}
 
 // x[m, k] -> f16 rows in the fragment order (each aligned 8 as 0 2 1 3 4 6 5 7),
 // each row scaled by its power of two (f16_row_scale; the factor to undo it in
@@ -640,13 +690,20 @@ __global__ __launch_bounds__(1024) void xrows_kernel(const float* __restrict__ x
     for (int64_t i = t; i < yn; i += nt) y[r * yn + i] = 0.0f;
 }
 
-// rs != nullptr (f16 only): each row scaled by its power of two as in xrows_kernel.
-template <bool F16PERM>
+// One workgroup per row r of x: the row's layer norm (two passes for the mean and
+// the mean squared deviation, as ops_fn::layer_norm computes them), then each group
+// of 8 normalized values rounded to f16 in the fragment order 0 2 1 3 4 6 5 7, and
+// y's row r zeroed over ny columns.  The f16 values are scaled by powers of two as x
+// is on the path without the norm: per row (rs != nullptr: the prefill operand, as
+// xrows_kernel) or per k slice of the row (rf != nullptr: the S slices of the
+// batched-decode split, factors at rf[s * 64 + r], as xprep_kernel).
 __global__ __launch_bounds__(1024) void norm_convert_kernel(const float* __restrict__ x, int64_t k,
                                                            NormArgs norm, uint4* __restrict__ out,
                                                            float* __restrict__ y, int64_t ny,
-                                                           float* __restrict__ rs) {
+                                                           float* __restrict__ rs, int S,
+                                                           float* __restrict__ rf) {
     __shared__ float red[16];
+    __shared__ unsigned smax[kMaxSplitSlices];  // per-slice max |v| as f32 bits (>= 0)
     const int64_t r = blockIdx.x;
     const float4* xr = reinterpret_cast<const float4*>(x + r * k);
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -687,41 +744,65 @@ __global__ __launch_bounds__(1024) void norm_convert_kernel(const float* __restr
             v[4 * h + 3] = (a.w - mean) / sd * g.w + b.w;
         }
     };
+    // the scale of group i: per row (sc) or per slice (ssc[slice of i])
     float sc = 1.0f;
-    if (F16PERM && rs) {
+    __shared__ float ssc[kMaxSplitSlices];
+    const int64_t C = (k + 127) / 128;  // 128-k chunks; slice s = chunks [s C / S, (s + 1) C / S)
+    auto slice_of = [&](int64_t i) {  // the slice holding group i (chunk i / 16)
+        const int64_t c = i / 16;
+        int s = (int)(c * S / C);  // floor(s C / S) <= c; then the largest such s
+        while (s + 1 < S && (int64_t)(s + 1) * C / S <= c) ++s;
+        while (s > 0 && (int64_t)s * C / S > c) --s;
+        return s;
+    };
+    if (rs || rf) {  // kernel arguments: every branch on them is uniform, barriers included
+        if (rf) {
+            for (int s = threadIdx.x; s < S; s += 1024) smax[s] = 0u;
+            __syncthreads();
+        }
         float mx = 0.0f;
         for (int64_t i = threadIdx.x; i < k / 8; i += 1024) {
             float v[8];
             values(i, v);
+            float gm = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[e]));
+            for (int e = 0; e < 8; ++e) gm = fmaxf(gm, fabsf(v[e]));
+            if (rf) atomicMax(&smax[slice_of(i)], __float_as_uint(gm));
+            else mx = fmaxf(mx, gm);
         }
+        if (rf) {
+            __syncthreads();
+            for (int s = threadIdx.x; s < S; s += 1024) {
+                // the scale of f16_row_scale, one thread per slice (f16_row_scale
+                // stores from thread 0 only)
+                const float m = __uint_as_float(smax[s]);
+                int e = 0;
+                const bool ok = m > 0.0f && m <= 3.402823466e38f;
+                if (ok) (void)frexpf(m, &e);
+                e = e < -111 ? -111 : e;
+                rf[(int64_t)s * 64 + r] = ok ? ldexpf(1.0f, e - 15) : 1.0f;
+                ssc[s] = ok ? ldexpf(1.0f, 15 - e) : 1.0f;
+            }
+            __syncthreads();
+        } else {
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-        if (lane == 0) red[wv] = mx;
-        __syncthreads();
-        mx = 0.0f;
+            for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            if (lane == 0) red[wv] = mx;
+            __syncthreads();
+            mx = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 16; ++w) mx = fmaxf(mx, red[w]);
-        sc = f16_row_scale(mx, rs + r);
+            for (int w = 0; w < 16; ++w) mx = fmaxf(mx, red[w]);
+            sc = f16_row_scale(mx, rs + r);
+        }
     }
     for (int64_t i = threadIdx.x; i < k / 8; i += 1024) {
         float v[8];
         values(i, v);
-        if constexpr (F16PERM) {
+        const float f = rf ? ssc[slice_of(i)] : sc;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] *= sc;
-        }
-        uint32_t o[4];
-        if constexpr (F16PERM) {
-            o[0] = pk_f16(v[0], v[2]); o[1] = pk_f16(v[1], v[3]);
-            o[2] = pk_f16(v[4], v[6]); o[3] = pk_f16(v[5], v[7]);
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(o[j]) : "v"(v[2 * j]), "v"(v[2 * j + 1]));
-        }
-        out[r * (k / 8) + i] = make_uint4(o[0], o[1], o[2], o[3]);
+        for (int e = 0; e < 8; ++e) v[e] *= f;
+        out[r * (k / 8) + i] = make_uint4(pk_f16(v[0], v[2]), pk_f16(v[1], v[3]),
+                                          pk_f16(v[4], v[6]), pk_f16(v[5], v[7]));
     }
     for (int64_t i = threadIdx.x; i < ny; i += 1024) y[r * ny + i] = 0.0f;
 }
@@ -734,15 +815,12 @@ hipError_t launch_swiglu(const float* gu, int64_t m, int64_t I, float* act, hipS
 }
 
 hipError_t launch_norm_convert(const float* x, int64_t m, int64_t k, const NormArgs& norm,
-                               bool f16_perm, void* out, float* y, int64_t ny, hipStream_t s,
-                               float* rs) {
+                               void* out, float* y, int64_t ny, hipStream_t s, float* rs, int S,
+                               float* rf) {
     if (m <= 0) return hipSuccess;
-    if (f16_perm)
-        norm_convert_kernel<true>
-            <<<(unsigned)m, 1024, 0, s>>>(x, k, norm, static_cast<uint4*>(out), y, ny, rs);
-    else
-        norm_convert_kernel<false>
-            <<<(unsigned)m, 1024, 0, s>>>(x, k, norm, static_cast<uint4*>(out), y, ny, nullptr);
+    if (rf && (S < 1 || S > kMaxSplitSlices)) return hipErrorInvalidValue;
+    norm_convert_kernel<<<(unsigned)m, 1024, 0, s>>>(x, k, norm, static_cast<uint4*>(out), y, ny,
+                                                     rs, S, rf);
     return hipGetLastError();
 }
 
@@ -755,49 +833,62 @@ hipError_t launch_x_to_f16_rows(const float* x, int64_t m, int64_t k, void* out,
     return hipGetLastError();
 }
 
-size_t decode_workspace_bytes(const QWeight& w, int64_t m) { return (size_t)m * (size_t)w.k * 2; }
-
-hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float* y,
-                              hipStream_t s, int epi, const NormArgs& norm, void* ws) {
-    // 32-bit offsets: x in f16 elements, weight bytes
-    if ((uint64_t)m * (uint64_t)w.k >= (1ull << 31) || !mfma_supports(w))
-        return hipErrorInvalidValue;
+namespace {
+// The k split of a batched-decode call of m rows on w (as the launch picks it).
+int decode_split(const QWeight& w, int64_t m) {
     const bool q4 = w.qtype == UNILLM_QTYPE_Q4_0, k4 = w.qtype == UNILLM_QTYPE_Q4_K,
                k6 = w.qtype == UNILLM_QTYPE_Q6_K, wide = m > 32;
     const int lds = k4   ? (wide ? Stage<UNILLM_QTYPE_Q4_K, 2>::LDS : Stage<UNILLM_QTYPE_Q4_K, 1>::LDS)
                     : k6 ? (wide ? Stage<UNILLM_QTYPE_Q6_K, 2>::LDS : Stage<UNILLM_QTYPE_Q6_K, 1>::LDS)
                     : q4 ? (wide ? Stage<UNILLM_QTYPE_Q4_0, 2>::LDS : Stage<UNILLM_QTYPE_Q4_0, 1>::LDS)
                          : (wide ? Stage<UNILLM_QTYPE_Q8_0, 2>::LDS : Stage<UNILLM_QTYPE_Q8_0, 1>::LDS);
-    const int S = choose_split(w, lds);
+    return choose_split(w, lds, wide);
+}
+// x as f16 (m k 2 bytes, padded to 256), then the slice factors rf[S][64]
+size_t decode_x_bytes(const QWeight& w, int64_t m) {
+    return ((size_t)m * (size_t)w.k * 2 + 255) / 256 * 256;
+}
+}  // namespace
+
+size_t decode_workspace_bytes(const QWeight& w, int64_t m) {
+    return decode_x_bytes(w, m) + (size_t)decode_split(w, m) * 64 * sizeof(float);
+}
+
+hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float* y,
+                              hipStream_t s, int epi, const NormArgs& norm, void* ws) {
+    // 32-bit offsets: x in f16 elements, weight bytes
+    if ((uint64_t)m * (uint64_t)w.k >= (1ull << 31) || !mfma_supports(w) || m > 64)
+        return hipErrorInvalidValue;
+    const bool q4 = w.qtype == UNILLM_QTYPE_Q4_0, k4 = w.qtype == UNILLM_QTYPE_Q4_K,
+               k6 = w.qtype == UNILLM_QTYPE_Q6_K, wide = m > 32;
+    const int S = decode_split(w, m);
     hipError_t e = hipSuccess;
     if (!ws && (e = stream_workspace(s, decode_workspace_bytes(w, m), &ws)) != hipSuccess)
         return e;
-    const int64_t n8 = m * w.k / 8;  // k % 32 == 0
+    float* rf = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + decode_x_bytes(w, m));
     const int add = epi == kEpiAdd;
-    const int64_t ny = S > 1 && !add ? m * w.n : 0;
-    const int64_t work = std::max(n8, ny / 4);
-    const int grid =
-        (int)std::min<int64_t>((work + 255) / 256, (int64_t)device_info().cu_count * 8);
+    const int64_t ny = S > 1 && !add ? w.n : 0;  // y columns to zero per row
     if (norm.gamma) {
-        if ((e = launch_norm_convert(x, m, w.k, norm, true, ws, y, ny > 0 ? w.n : 0, s)) !=
+        if ((e = launch_norm_convert(x, m, w.k, norm, ws, y, ny, s, nullptr, S, rf)) !=
             hipSuccess)
             return e;
     } else {
-        xprep_kernel<<<grid, 256, 0, s>>>(x, static_cast<uint4*>(ws), n8, y, ny);
+        xprep_kernel<<<(unsigned)(m * S), 128, 0, s>>>(x, w.k, S, static_cast<uint4*>(ws), rf, y,
+                                                        ny);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     const _Float16* xh = static_cast<const _Float16*>(ws);
     if (k4)
-        return wide ? launch_mt<UNILLM_QTYPE_Q4_K, 2>(w, xh, m, y, S, s, add)
-                    : launch_mt<UNILLM_QTYPE_Q4_K, 1>(w, xh, m, y, S, s, add);
+        return wide ? launch_mt<UNILLM_QTYPE_Q4_K, 2>(w, xh, rf, m, y, S, s, add)
+                    : launch_mt<UNILLM_QTYPE_Q4_K, 1>(w, xh, rf, m, y, S, s, add);
     if (k6)
-        return wide ? launch_mt<UNILLM_QTYPE_Q6_K, 2>(w, xh, m, y, S, s, add)
-                    : launch_mt<UNILLM_QTYPE_Q6_K, 1>(w, xh, m, y, S, s, add);
+        return wide ? launch_mt<UNILLM_QTYPE_Q6_K, 2>(w, xh, rf, m, y, S, s, add)
+                    : launch_mt<UNILLM_QTYPE_Q6_K, 1>(w, xh, rf, m, y, S, s, add);
     if (!wide)
-        return q4 ? launch_mt<UNILLM_QTYPE_Q4_0, 1>(w, xh, m, y, S, s, add)
-                  : launch_mt<UNILLM_QTYPE_Q8_0, 1>(w, xh, m, y, S, s, add);
-    return q4 ? launch_mt<UNILLM_QTYPE_Q4_0, 2>(w, xh, m, y, S, s, add)
-              : launch_mt<UNILLM_QTYPE_Q8_0, 2>(w, xh, m, y, S, s, add);
+        return q4 ? launch_mt<UNILLM_QTYPE_Q4_0, 1>(w, xh, rf, m, y, S, s, add)
+                  : launch_mt<UNILLM_QTYPE_Q8_0, 1>(w, xh, rf, m, y, S, s, add);
+    return q4 ? launch_mt<UNILLM_QTYPE_Q4_0, 2>(w, xh, rf, m, y, S, s, add)
+              : launch_mt<UNILLM_QTYPE_Q8_0, 2>(w, xh, rf, m, y, S, s, add);
 }
 
 }  // namespace unillm

@@ -177,12 +177,13 @@ size_t prefill_workspace_bytes(const QWeight& w, int64_t m);
 inline bool mfma_supports(const QWeight& w) {
     return (uint64_t)w.n * (uint64_t)w.row_bytes < (1ull << 32);
 }
-// x[m, k] -> its layer norm in the MFMA paths' operand form (f16 in the decode
-// kernel's element order, or bf16), one workgroup per row; zeroes y rows
-// [0, m) of width ny when ny > 0 (a split k adds into it).
+// x[m, k] -> its layer norm as f16 in the MFMA paths' element order, one workgroup
+// per row, scaled by powers of two: per row (rs[row] <- the undoing factor) for the
+// prefill path, or per k slice of the batched-decode split (S slices, rf[s * 64 +
+// row]); zeroes y rows [0, m) of width ny when ny > 0 (a split k adds into it).
 hipError_t launch_norm_convert(const float* x, int64_t m, int64_t k, const NormArgs& norm,
-                               bool f16_perm, void* out, float* y, int64_t ny, hipStream_t s,
-                               float* rs = nullptr);
+                               void* out, float* y, int64_t ny, hipStream_t s,
+                               float* rs = nullptr, int S = 0, float* rf = nullptr);
 // x[m, k] (k % 32 == 0) -> f16 rows (round to nearest even) in the decode kernel's
 // element order (each aligned 8 as 0 2 1 3 4 6 5 7), each row scaled by a power
 // of two that puts its largest magnitude in [2^14, 2^15); rs[row] <- the factor

@@ -565,7 +565,7 @@ hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, floa
     float* rs = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + xbytes);
     const int add = epi == kEpiAdd;
     const int64_t yn = plan.S > 1 && !add ? w.n : 0;
-    e = norm.gamma ? launch_norm_convert(x, m, w.k, norm, true, ws, y, yn, s, rs)
+    e = norm.gamma ? launch_norm_convert(x, m, w.k, norm, ws, y, yn, s, rs)
                    : launch_x_to_f16_rows(x, m, w.k, ws, rs, y, yn, s);
     if (e != hipSuccess) return e;
     const uint16_t* xb = static_cast<const uint16_t*>(ws);

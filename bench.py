@@ -34,6 +34,8 @@ HBM_PEAK_GBS = 8000.0
 # MI355X dense MFMA peak, the same for bf16 and f16 operands (the prefill kernel
 # runs f16; the "frac_dense" fields price it against this)
 DENSE_PEAK_TFLOPS = 2516.6
+# MI355X f32 peak (the prompt attention kernel's f32 FMA work is priced against it)
+F32_PEAK_TFLOPS = 157.3
 Q4_0, Q8_0, Q4_K = 2, 8, 12
 BPB = {Q4_0: 18, Q8_0: 34, Q4_K: 18}  # GGUF bytes per 32 weights (Q4_K: 144 per 256)
 
@@ -294,46 +296,70 @@ def extra_configs(torch, QuantLinear, gen, stream, only):
             "us": round(ms * 1e3, 1)}
         del ws
     if "attention" in want:
-        # decode attention over a KV cache of L positions (row f4): one new token a
-        # call, the cache truncated back to L - 1 before each; HBM-bound on the cached
+        # decode attention over a KV cache of about L positions (row f4): 20 calls of
+        # one new token each, starting from L - 10 cached positions (the cache is
+        # rewound between samples, outside the timed region); HBM-bound on the cached
         # K and V (2 KVH L hd 4 bytes), timed per call
         from unillm_amd import KvCache
+        R = 20
         for (H, KVH, D, label) in ((32, 32, 128, "llama2_7b"), (32, 8, 128, "gqa_32_8")):
             for L in (1024, 4096):
-                kv = KvCache(KVH, D, L)
+                kv = KvCache(KVH, D, L + 64)
                 w = (H + 2 * KVH) * D
-                mf = max(1, 16 // (H // KVH))  # tokens a fill call: m H / KVH <= 16
-                fill = torch.empty(mf, w, device="cuda").normal_(generator=gen)
-                while kv.seq_len + mf <= L - 1:
-                    kv.attention(fill, H, stream=stream)
-                while kv.seq_len < L - 1:
-                    kv.attention(fill[:1].contiguous(), H, stream=stream)
+                start = L - R // 2
+                fill = torch.empty(start, w, device="cuda").normal_(generator=gen)
                 q1 = torch.empty(1, w, device="cuda").normal_(generator=gen)
                 out = torch.empty(1, H * D, device="cuda")
 
                 def one():
-                    kv.truncate(L - 1)
                     kv.attention(q1, H, out=out, stream=stream)
 
+                def sample(fn):
+                    kv.truncate(start)
+                    return timer.run(fn, 1)
+
                 with torch.cuda.stream(stream):
+                    kv.attention(fill, H, stream=stream)  # the prompt, one call
+                    del fill
                     one()
-                    eager = float(np.median([timer.run(one, 20) for _ in range(3)]))
-                    # the same 20 calls captured once and replayed (as a decode step
-                    # would run them): each captured call has the length truncate()
-                    # set on the host, L - 1, so a replay repeats exactly those calls
+                    eager = float(np.median([sample(lambda: [one() for _ in range(R)])
+                                             for _ in range(3)])) / R
+                    # the same R calls captured once and replayed, as a decode step
+                    # would run them: the cache length lives on the device, so each
+                    # replayed call appends at the position the previous one left
                     g = torch.cuda.CUDAGraph()
                     with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
-                        for _ in range(20):
+                        for _ in range(R):
                             one()
-                    kv.truncate(L - 1)
-                    g.replay()
-                    ms = float(np.median([timer.run(g.replay, 1) for _ in range(5)])) / 20
+                    sample(g.replay)
+                    ms = float(np.median([sample(g.replay) for _ in range(5)])) / R
                     del g
                 b = 2 * KVH * L * D * 4
                 res[f"attention_decode_{label}_L{L}"] = {
                     "GB/s": round(b / ms / 1e6, 1), "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 3),
                     "us": round(ms * 1e3, 2), "eager_us": round(eager * 1e3, 2), "kv_bytes": b}
                 del kv
+        # prompt attention (m tokens into an empty cache, causal): 4 H hd m (m + 1) / 2
+        # flops of f32 FMA work (scores and the weighted sum), priced against the
+        # f32 vector peak
+        for (H, KVH, D, label) in ((32, 32, 128, "llama2_7b"), (32, 8, 128, "gqa_32_8")):
+            for m in (512, 2048):
+                kv = KvCache(KVH, D, m)
+                x = torch.empty(m, (H + 2 * KVH) * D, device="cuda").normal_(generator=gen)
+                out = torch.empty(m, H * D, device="cuda")
+
+                def sample():
+                    kv.truncate(0)
+                    return timer.run(lambda: kv.attention(x, H, out=out, stream=stream), 1)
+
+                with torch.cuda.stream(stream):
+                    sample()
+                    ms = float(np.median([sample() for _ in range(5)]))
+                tf = 4 * H * D * m * (m + 1) / 2 / ms / 1e9
+                res[f"attention_prompt_{label}_m{m}"] = {
+                    "TFLOP/s": round(tf, 1), "frac_f32": round(tf / F32_PEAK_TFLOPS, 3),
+                    "us": round(ms * 1e3, 1)}
+                del kv, x, out
     if "e2e" in want and "stack" not in want:
         want.add("stack")  # the end-to-end step reuses the stack's weights
     if "stack" in want:
@@ -400,8 +426,9 @@ def decode_step_e2e(torch, layers, head, gen, stream, timer):
     per layer input_layernorm + QKV, attention (RoPE, append, causal softmax over
     the cache: 32 heads, hd 128, f32), o_proj + residual, post_attention_layernorm +
     gate_up + SwiGLU, down + residual; then the final norm + lm_head.  Captured once
-    as a HIP graph (6 launches a layer) and replayed: every replay recomputes
-    position L - 1, the caches' length being host state set before capture."""
+    as a HIP graph (6 launches a layer) and replayed: each replay appends one
+    position to every cache (the length lives on the device), starting from L - 5
+    cached positions after a rewind outside the timed region."""
     from unillm_amd import KvCache
     H, D = 32, 128
     res = {}
@@ -411,15 +438,15 @@ def decode_step_e2e(torch, layers, head, gen, stream, timer):
     att = torch.empty(1, 4096, device="cuda")
     act = torch.empty(1, 11008, device="cuda")
     logits = torch.empty(1, 32000, device="cuda")
+    R = 5
     for L in (1024, 4096):
-        caches = [KvCache(H, D, L) for _ in layers]
-        fill = torch.empty(16, 3 * 4096, device="cuda").normal_(generator=gen)
+        caches = [KvCache(H, D, L + 64) for _ in layers]
+        start = L - R
+        fill = torch.empty(start, 3 * 4096, device="cuda").normal_(generator=gen)
         with torch.cuda.stream(stream):
-            for kv in caches:  # fill to L - 1 positions (16 tokens a call, then single)
-                while kv.seq_len + 16 <= L - 1:
-                    kv.attention(fill, H, stream=stream)
-                while kv.seq_len < L - 1:
-                    kv.attention(fill[:1].contiguous(), H, stream=stream)
+            for kv in caches:  # the prompt: one call a layer
+                kv.attention(fill, H, stream=stream)
+            del fill
 
             def step():
                 for (qkv, o, gu, down), kv in zip(layers, caches):
@@ -430,20 +457,19 @@ def decode_step_e2e(torch, layers, head, gen, stream, timer):
                     down.forward_add(act, h, stream=stream)
                 head.forward_norm(h, gam, eps=1e-6, out=logits, stream=stream)
 
-            def rewind():
+            def sample():
                 for kv in caches:
-                    kv.truncate(L - 1)
+                    kv.truncate(start)
+                h.normal_(generator=gen)  # the residual grows by design; restart it
+                return timer.run(g.replay, R)
 
             h.normal_(generator=gen)
             step()
-            rewind()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
                 step()
-            rewind()
-            h.normal_(generator=gen)
-            g.replay()
-            ms = float(np.median([timer.run(g.replay, 5) for _ in range(3)]))
+            sample()
+            ms = float(np.median([sample() for _ in range(3)]))
             del g
         kv_bytes = 32 * 2 * H * L * D * 4
         w_bytes = 32 * (wbytes(Q4_0, 12288, 4096) + wbytes(Q4_0, 4096, 4096) +

@@ -194,14 +194,18 @@ int unillm_hip_qmatmul_reserve(const unillm_qweight* w, int64_t m, int swiglu, v
 int unillm_hip_kv_cache_create(int64_t n_kv_heads, int64_t head_dim, int64_t max_seq,
                                float rope_theta, unillm_kv_cache** out);
 int unillm_hip_kv_cache_destroy(unillm_kv_cache* c);
-/* Filled positions (LayerKVCache::seq_len, kv_cache.rs:74-76). */
+/* Filled positions (LayerKVCache::seq_len, kv_cache.rs:74-76).  The length lives
+ * in device memory (see unillm_hip_attention_decode); after a call on the cache
+ * has been captured into a HIP graph this synchronises the device to read it. */
 int unillm_hip_kv_cache_length(const unillm_kv_cache* c, int64_t* len);
-/* Forget the filled positions, keep the buffers (LayerKVCache::clear, kv_cache.rs:61-63). */
+/* Forget the filled positions, keep the buffers (LayerKVCache::clear,
+ * kv_cache.rs:61-63).  Synchronises the device (the new length is written to
+ * device memory once all issued work is done); not during graph capture. */
 int unillm_hip_kv_cache_clear(unillm_kv_cache* c);
 /* Keep the first len positions (0 <= len <= the filled length): a rolled-back
  * step, e.g. rejected speculative tokens.  No counterpart in LayerKVCache,
  * whose only shrink is clear(); the positions past len are rewritten by the
- * next appends. */
+ * next appends.  Synchronises the device, as unillm_hip_kv_cache_clear. */
 int unillm_hip_kv_cache_truncate(unillm_kv_cache* c, int64_t len);
 
 /* The attention of LlamaAttention::forward_with_cache after its projections
@@ -211,11 +215,17 @@ int unillm_hip_kv_cache_truncate(unillm_kv_cache* c, int64_t len);
  * llama.rs:827-883) at positions len .. len + m - 1, k and v appended to the
  * cache, then softmax(q k^T / sqrt(head_dim) + causal mask) v into
  * out_dev[m, n_heads head_dim], head h reading kv head h / (n_heads /
- * n_kv_heads).  The cache's length grows by m.  Decode steps only:
- * m * n_heads / n_kv_heads <= 16, and len + m <= 131072 (UNILLM_ERR_UNSUPPORTED
- * beyond).  Overflow of max_seq is an error with the reference's message
+ * n_kv_heads).  The cache's length grows by m.  Any m: decode steps
+ * (m * n_heads / n_kv_heads <= 16, len + m <= 131072) split the cache into
+ * chunks; longer calls (the prompt, llama.rs:488-497) run a tiled causal kernel.
+ * Overflow of max_seq is an error with the reference's message
  * (kv_cache.rs:114-121).  Calls on one cache must be ordered (one stream), as
- * each appends to it. */
+ * each appends to it.
+ * Graph capture: the kernels read the cache length from device memory and
+ * advance it there, so a captured call appends at the next position on every
+ * replay (a decode step captured once serves successive tokens).  A replayed
+ * call past max_seq appends nothing, writes NaN and makes the next length query
+ * or eager call fail with the overflow message; clear / truncate reset it. */
 int unillm_hip_attention_decode(unillm_kv_cache* c, const float* qkv_dev, int64_t m,
                                 int64_t n_heads, float* out_dev, void* stream);
 

@@ -69,6 +69,24 @@ def test_attention_long_context_many_chunks():
     assert oracle.normwise_error(out, ref) < 1e-4
 
 
+def test_attention_decode_past_4096_with_32_kv_heads():
+    # with 32 kv heads the CUs fill with chunks of L / 16 positions, beyond the
+    # 256-position maximum once L > 4096: the chunk length must cap, not fail.  The
+    # decode step's output for token 4100 is checked against the prompt path's
+    # output for the same token (the prompt path's own parity is pinned above; the
+    # oracle's f64 loop over a 4101-token prompt would take minutes)
+    H, KVH, D, L = 32, 32, 128, 4100
+    w = (H + 2 * KVH) * D
+    qkv = torch.from_numpy(oracle.normal((L + 2) * w, seed=41).reshape(L + 2, w)).cuda()
+    a, b = KvCache(KVH, D, L + 8), KvCache(KVH, D, L + 8)
+    whole = a.attention(qkv, H).cpu().numpy()
+    b.attention(qkv[:L].contiguous(), H)
+    for t in (L, L + 1):
+        step = b.attention(qkv[t:t + 1].contiguous(), H).cpu().numpy()
+        assert oracle.normwise_error(step, whole[t:t + 1].astype(np.float64)) < 1e-5
+    assert b.seq_len == L + 2
+
+
 def test_attention_truncate_then_append_matches_fresh_sequence():
     # a rolled-back step (speculative decoding) must leave no trace: run two steps,
     # truncate the second away, run a different second step -- equal to a cache
@@ -101,10 +119,120 @@ def test_attention_overflow_and_limits():
         kv.truncate(2)  # only shortens
     kv.clear()
     assert kv.seq_len == 0
-    with pytest.raises(HipError):  # 17 queries a kv head: past decode's limit
-        KvCache(1, 64, 64).attention(torch.zeros(17, 3 * 64, device="cuda"), 1)
     with pytest.raises(HipError):  # head_dim 96 unsupported
         KvCache(1, 96, 8)
+    # a prompt-length call past max_seq: the same message, nothing appended
+    kv = KvCache(2, 64, 40)
+    with pytest.raises(HipError, match="KV cache overflow"):
+        kv.attention(torch.zeros(41, 8 * 64, device="cuda"), 4)
+    assert kv.seq_len == 0
+
+
+# ---- prompt-length calls (the prefill of generate_with_cache, llama.rs:488-497) ---------------
+
+@pytest.mark.parametrize("H,KVH,D,steps", [
+    (4, 4, 64, [17]),            # 17 queries a kv head: just past a decode step
+    (32, 8, 128, [64]),          # Llama-2-7B-like GQA, one full query block
+    (32, 32, 128, [300, 1, 1]),  # MHA prompt (ragged blocks), then decode steps
+    (8, 2, 64, [130, 70]),       # a second prompt-length call on a filled cache
+    (16, 2, 256, [100, 2]),      # hd 256 (32-query blocks)
+    (4, 1, 128, [513]),          # MQA, blocks of 64 plus one query
+])
+def test_attention_prompt_parity(H, KVH, D, steps):
+    print(f"prompt attention H={H} KVH={KVH} D={D} steps={steps}", flush=True)
+    assert _run_steps(H, KVH, D, steps, seed=7 * D + H) < 1e-4
+
+
+def test_attention_prompt_long_context():
+    # a 512-token prompt onto 700 cached positions, Llama-2-7B heads
+    H, KVH, D = 32, 32, 128
+    assert _run_steps(H, KVH, D, [350, 350, 512], max_seq=1300, seed=3) < 1e-4
+
+
+def test_attention_prompt_causality():
+    # changing token 9's q, k and v leaves the outputs of tokens 0 .. 8 bit for bit
+    H, KVH, D, m = 8, 2, 64, 40
+    w = (H + 2 * KVH) * D
+    a = oracle.normal(m * w, seed=61).reshape(m, w)
+    b = a.copy()
+    b[9] = oracle.normal(w, seed=62)
+    oa = KvCache(KVH, D, 64).attention(torch.from_numpy(a).cuda(), H).cpu().numpy()
+    ob = KvCache(KVH, D, 64).attention(torch.from_numpy(b).cuda(), H).cpu().numpy()
+    assert np.array_equal(oa[:9], ob[:9])
+    assert not np.array_equal(oa[9], ob[9])
+
+
+# ---- the cache length in device memory: a captured step replays at successive positions -----
+
+def test_captured_decode_step_advances_each_replay():
+    # generate_with_cache's loop (llama.rs:488-560) as a graph: prompt once, then one
+    # captured decode step replayed for every new token -- each replay appends at the
+    # next position and attends over everything before it
+    H, KVH, D = 8, 2, 128
+    w = (H + 2 * KVH) * D
+    P, N, max_seq = 37, 6, 64
+    kv = KvCache(KVH, D, max_seq)
+    kc = np.zeros((KVH, max_seq, D), np.float32)
+    vc = np.zeros((KVH, max_seq, D), np.float32)
+    stream = torch.cuda.Stream()
+    kv.reserve(1, H, stream=stream)
+    prompt = oracle.normal(P * w, seed=71).reshape(P, w)
+    tokens = [oracle.normal(w, seed=80 + i).reshape(1, w) for i in range(N)]
+    qkv = torch.empty(1, w, device="cuda")
+    out = torch.empty(1, H * D, device="cuda")
+    with torch.cuda.stream(stream):
+        kv.attention(torch.from_numpy(prompt).cuda(), H, stream=stream)
+    stream.synchronize()
+    oracle.attention_decode(prompt, H, KVH, D, 10000.0, kc, vc, 0)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
+        kv.attention(qkv, H, out=out, stream=stream)
+    assert kv.seq_len == P  # capture runs nothing
+    for i in range(N):
+        qkv.copy_(torch.from_numpy(tokens[i]))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            g.replay()
+        stream.synchronize()
+        ref = oracle.attention_decode(tokens[i], H, KVH, D, 10000.0, kc, vc, P + i)
+        assert oracle.normwise_error(out.cpu().numpy(), ref) < 1e-4, i
+    assert kv.seq_len == P + N
+    # an eager call after the replays continues from the device length
+    t = oracle.normal(w, seed=99).reshape(1, w)
+    o = kv.attention(torch.from_numpy(t).cuda(), H).cpu().numpy()
+    assert oracle.normwise_error(o, oracle.attention_decode(t, H, KVH, D, 10000.0, kc, vc,
+                                                           P + N)) < 1e-4
+    assert kv.seq_len == P + N + 1
+    del g
+
+
+def test_replay_past_max_seq_reports_overflow():
+    H, KVH, D = 4, 2, 64
+    w = (H + 2 * KVH) * D
+    kv = KvCache(KVH, D, 3)
+    stream = torch.cuda.Stream()
+    kv.reserve(1, H, stream=stream)
+    qkv = torch.from_numpy(oracle.normal(w, seed=5).reshape(1, w)).cuda()
+    out = torch.empty(1, H * D, device="cuda")
+    with torch.cuda.stream(stream):
+        kv.attention(qkv, H, stream=stream)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
+        kv.attention(qkv, H, out=out, stream=stream)
+    for _ in range(2):  # positions 1 and 2: fine
+        with torch.cuda.stream(stream):
+            g.replay()
+    stream.synchronize()
+    assert bool(torch.isfinite(out).all())
+    with torch.cuda.stream(stream):
+        g.replay()  # position 3 = max_seq: overflow
+    stream.synchronize()
+    assert bool(torch.isnan(out).all())
+    with pytest.raises(HipError, match="KV cache overflow"):
+        kv.seq_len
+    kv.clear()
+    assert kv.seq_len == 0
+    del g
 
 
 def test_attention_graph_replays_match_eager():

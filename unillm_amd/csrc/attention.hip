@@ -1,4 +1,10 @@
-// attention.hip -- decode attention with a KV cache in HBM (m new tokens, m H / KVH <= 16).
+// attention.hip -- attention with a KV cache in HBM: decode steps (m H / KVH <= 16 new
+// query rows a kv head) and prompt-length calls (any m; the tiled kernel further down).
+//
+// The cache's filled length is device state (the handle's `state`): the first kernel
+// of a call reads it and publishes it for the second, which advances it by m.  So the
+// kernels never take the length from the host, and a call captured into a HIP graph
+// appends at a new position every replay.
 //
 // What it computes: LlamaAttention::forward_with_cache after the projections
 // (crates/runtime/src/models_v2/llama.rs:1044-1150): RoPE on q and k at the
@@ -82,11 +88,13 @@ __device__ __forceinline__ float wave_add(float v) {
 
 // Dynamic LDS (floats): qs[QB][D] | nk[m][D] | nv[m][D] | sp[QB][C] (scores, then
 // exponentials) | red[4][QB][D] | stat[QB][2]
+// state: the cache's device state ([0] filled length, [1] overflow flag, [2] this
+// call's length, published by workgroup (0, 0) for the merge kernel).
 template <int D, int QB>
 __global__ __launch_bounds__(kThreads) void attn_decode_kernel(
-    const float* __restrict__ qkv, int m, int H, int KVH, int len, int C, int chunks, float scale,
-    const float* __restrict__ inv_freq, float* __restrict__ kc, float* __restrict__ vc,
-    int max_seq, float* __restrict__ part) {
+    const float* __restrict__ qkv, int m, int H, int KVH, int* __restrict__ state, int C,
+    int chunks, float scale, const float* __restrict__ inv_freq, float* __restrict__ kc,
+    float* __restrict__ vc, int max_seq, float* __restrict__ part) {
     constexpr int LP = D / 8;             // lanes per position in the score pass
     constexpr int SG = kThreads / LP;     // positions at a time (32, 16, 8)
     constexpr int D4 = D / 4;             // float4 columns in the p v pass
@@ -95,8 +103,23 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(
     const int g = blockIdx.x, c = blockIdx.y;
     const int G = H / KVH, Q = m * G;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int len = state[0];
+    if (g == 0 && c == 0 && tid == 0) state[2] = len;
+    if (len + m > max_seq) return;  // overflow: nothing appended; the merge reports it
     const int j0 = c * C, j1 = min(j0 + C, len + m);
     const int n = j1 - j0;
+    if (n <= 0) {  // a chunk past the filled positions (a grid sized for max_seq): empty
+        float* ms = part;
+        float* po = part + (int64_t)m * H * chunks * 2;
+        for (int i = tid; i < Q * D; i += kThreads) {
+            const int qi = i / D, d = i - qi * D;
+            const int t = qi / G, e = qi - t * G;
+            const int64_t qc = ((int64_t)t * H + g * G + e) * chunks + c;
+            if (d == 0) *reinterpret_cast<float2*>(ms + 2 * qc) = make_float2(-INFINITY, 0.0f);
+            po[qc * D + d] = 0.0f;
+        }
+        return;
+    }
     const int64_t W = (int64_t)(H + 2 * KVH) * D;  // floats per qkv row
     extern __shared__ __attribute__((aligned(16))) float sm[];
     float* qs = sm;
@@ -305,12 +328,22 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(
 // pair (one pass of loads), forms the overall max M and sum S and each chunk's weight
 // e^(M_c - M) / S in LDS; thread d sums o_c[d] times the weights, 32 chunks' loads in
 // flight (the first 32 requested at entry).  A chunk whose queries were all masked has M_c = -inf and weight 0.
+// The cache length advances here (workgroup 0, after every chunk has read it), or,
+// when the call found len + m > max_seq, the output is NaN and the overflow flag set.
 template <int D>
 __global__ __launch_bounds__(D) void attn_merge_kernel(const float* __restrict__ part, int m,
-                                                       int H, int chunks, float* __restrict__ out) {
+                                                       int H, int chunks, float* __restrict__ out,
+                                                       int* __restrict__ state, int max_seq) {
     extern __shared__ float wts[];  // [chunks]
     const int th = blockIdx.x;      // t H + h
     const int tid = threadIdx.x, lane = tid & 63;
+    const int len = state[2];
+    if (len + m > max_seq) {
+        out[(int64_t)th * D + tid] = __builtin_nanf("");
+        if (th == 0 && tid == 0) state[1] = 1;
+        return;
+    }
+    if (th == 0 && tid == 0) state[0] = len + m;
     const float2* pq = reinterpret_cast<const float2*>(part) + (int64_t)th * chunks;
     const float* po = part + (int64_t)m * H * chunks * 2 + (int64_t)th * chunks * D + tid;
     // the first 32 chunks' o[d] are requested before the weights exist (they do not
@@ -360,12 +393,12 @@ hipError_t launch_d_q(const KvCache& kv, const float* qkv, int m, int H, int C, 
                                                  160 * 1024 - 1024) == hipSuccess;
     if (!attr) return hipErrorInvalidValue;
     attn_decode_kernel<D, QB><<<dim3((unsigned)kv.n_kv_heads, (unsigned)chunks), kThreads, lds, s>>>(
-        qkv, m, H, (int)kv.n_kv_heads, (int)kv.len, C, chunks, 1.0f / sqrtf((float)D), kv.inv_freq,
+        qkv, m, H, (int)kv.n_kv_heads, kv.state, C, chunks, 1.0f / sqrtf((float)D), kv.inv_freq,
         kv.k, kv.v, (int)kv.max_seq, part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     attn_merge_kernel<D><<<(unsigned)(m * H), D, sizeof(float) * (size_t)chunks, s>>>(
-        part, m, H, chunks, out);
+        part, m, H, chunks, out, kv.state, (int)kv.max_seq);
     return hipGetLastError();
 }
 
@@ -380,37 +413,256 @@ hipError_t launch_d(const KvCache& kv, const float* qkv, int m, int H, int C, in
     return launch_d_q<D, 16>(kv, qkv, m, H, C, chunks, part, out, s);
 }
 
-}  // namespace
-
-namespace {
 // Chunk length for L positions: (kv head, chunk) workgroups to cover the CUs
 // twice; chunks of 32 .. kMaxChunk positions (a multiple of 32), at most
 // kMaxChunks of them.  0 when L is beyond kMaxChunk * kMaxChunks.
 int64_t chunk_len(int64_t L, int64_t KVH) {
     const int64_t want = 2 * (int64_t)device_info().cu_count;
-    int64_t C = std::max((L * KVH + want - 1) / want, (L + kMaxChunks - 1) / kMaxChunks);
+    // enough chunks for the CUs, but none longer than kMaxChunk: with many kv heads
+    // the CUs fill with fewer, longer chunks, and the cap takes over from there
+    int64_t C = std::min<int64_t>((L * KVH + want - 1) / want, kMaxChunk);
+    C = std::max(C, (L + kMaxChunks - 1) / kMaxChunks);
     C = std::max<int64_t>(32, (C + 31) / 32 * 32);
     return C > kMaxChunk ? 0 : C;
 }
-}  // namespace
 
-// The per-chunk partials of a call of m tokens at any length: at most kMaxChunks
-// chunks of (max, sum) and o[hd] per query.
-size_t attention_workspace_bytes(const KvCache& kv, int64_t m, int64_t H) {
-    return (size_t)m * H * kMaxChunks * (2 + kv.head_dim) * sizeof(float);
+// ---- prompt-length calls (m H / KVH beyond a decode step) ---------------------------------
+//
+// Two kernels.  rope_append_kernel, a workgroup per (token t, head): q heads rotated at
+// position len + t and scaled by 1 / sqrt(hd) into the workspace qw[H][m][hd]; k heads
+// rotated and, with v, appended to the cache (the decode kernel's formulas, so either
+// path writes the same cache).  attn_prefill_kernel, a workgroup per (block of BQ
+// queries, head h): flash-style causal attention over the cache in f32 --
+//   - the block's queries Q^T [hd][BQ] stay in LDS; the key positions run in tiles of BK
+//     (K^T [hd][BK] and V [BK][hd] in LDS), only up to the block's last query position;
+//   - thread (tr, tc) of 16 x 16 computes scores for rows tr RT .. and columns tc CT ..
+//     (RT = BQ / 16, CT = BK / 16), masks positions past each query (and past the
+//     filled length), and keeps each row's running max and sum (online softmax: the
+//     earlier partial output rescaled by e^(m_old - m_new)); the row reductions run over
+//     the 16 lanes of one tc group by lane shuffles;
+//   - the exponentials go to LDS as P^T [BK][BQ]; the same thread then accumulates
+//     rows tr RT .. of O for output dimensions tc hd / 16 .., read P and V from LDS.
+// f32 throughout, like the reference's cache and matmuls (llama.rs:1108-1146).  LDS
+// rows are padded by 4 floats so the transposing stores spread over the banks.
+
+template <int D>
+__global__ __launch_bounds__(D / 2) void rope_append_kernel(
+    const float* __restrict__ qkv, int m, int H, int KVH, int* __restrict__ state, float scale,
+    const float* __restrict__ inv_freq, float* __restrict__ kc, float* __restrict__ vc,
+    int max_seq, float* __restrict__ qw) {
+    constexpr int HALF = D / 2;
+    const int len = state[0];
+    const int t = blockIdx.x, hh = blockIdx.y, p = threadIdx.x;
+    if (t == 0 && hh == 0 && p == 0) state[2] = len;  // this call's length, for the next kernel
+    if (len + m > max_seq) return;  // overflow: nothing appended; the attention kernel reports it
+    const float* row = qkv + (int64_t)t * (H + 2 * KVH) * D;
+    float sn, cs;
+    sincosf((float)(len + t) * inv_freq[p], &sn, &cs);
+    if (hh < H) {
+        const float* x = row + (int64_t)hh * D;
+        const float a = x[p], b = x[p + HALF];
+        float* q = qw + ((int64_t)hh * m + t) * D;
+        q[p] = (a * cs - b * sn) * scale;
+        q[p + HALF] = (a * sn + b * cs) * scale;
+    } else {
+        const int g = hh - H;
+        const float* xk = row + (int64_t)(H + g) * D;
+        const float* xv = row + (int64_t)(H + KVH + g) * D;
+        const float a = xk[p], b = xk[p + HALF];
+        const int64_t dst = ((int64_t)g * max_seq + len + t) * D;
+        kc[dst + p] = a * cs - b * sn;
+        kc[dst + p + HALF] = a * sn + b * cs;
+        vc[dst + p] = xv[p];
+        vc[dst + p + HALF] = xv[p + HALF];
+    }
 }
 
-hipError_t launch_attention_decode(const KvCache& kv, const float* qkv, int64_t m, int64_t H,
-                                   float* out, hipStream_t s) {
+template <int D, int BQ, int BK>
+struct PrefillLds {
+    static constexpr int QP = BQ + 4, KP = BK + 4, VP = D + 4, PP = BQ + 4;  // padded rows
+    static constexpr int FLOATS = D * QP + D * KP + BK * VP + BK * PP;
+    static constexpr size_t BYTES = (size_t)FLOATS * sizeof(float);
+};
+
+template <int D, int BQ, int BK>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restrict__ qw, int m,
+                                                           int H, int KVH,
+                                                           int* __restrict__ state,
+                                                           const float* __restrict__ kc,
+                                                           const float* __restrict__ vc,
+                                                           int max_seq, float* __restrict__ out) {
+    using L = PrefillLds<D, BQ, BK>;
+    constexpr int RT = BQ / 16, CT = BK / 16, DC = D / 16;
+    extern __shared__ __attribute__((aligned(16))) float sm[];
+    float* qT = sm;                 // [D][QP]
+    float* kT = qT + D * L::QP;     // [D][KP]
+    float* vs = kT + D * L::KP;     // [BK][VP]
+    float* pT = vs + BK * L::VP;    // [BK][PP]
+    const int h = blockIdx.y, g = h / (H / KVH);
+    const int q0 = blockIdx.x * BQ;
+    const int tid = threadIdx.x, tr = tid / 16, tc = tid % 16;
+    const int len = state[2];
+    const int nq = min(BQ, m - q0);  // real queries of the block
+    if (len + m > max_seq) {
+        for (int i = tid; i < nq * D; i += 256)
+            out[(int64_t)(q0 + i / D) * H * D + (int64_t)h * D + i % D] = __builtin_nanf("");
+        if (blockIdx.x == 0 && h == 0 && tid == 0) state[1] = 1;
+        return;
+    }
+    // the length advances here: no workgroup of this kernel reads state[0], and the next
+    // call's kernels run after this one
+    if (blockIdx.x == 0 && h == 0 && tid == 0) state[0] = len + m;
+    const int total = len + m;  // filled positions once this call's keys are in
+    // the block's queries, transposed (rows past m repeat the last query)
+    for (int i = tid; i < BQ * D; i += 256) {
+        const int r = i / D, d = i - r * D;
+        qT[d * L::QP + r] = qw[((int64_t)h * m + min(q0 + r, m - 1)) * D + d];
+    }
+    float mrow[RT], lrow[RT], o[RT][DC];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        mrow[r] = -INFINITY;
+        lrow[r] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < DC; ++c) o[r][c] = 0.0f;
+    }
+    const int last_pos = len + q0 + nq - 1;  // the block's last query position
+    const int nkb = last_pos / BK + 1;
+    const float* kg = kc + (int64_t)g * max_seq * D;
+    const float* vg = vc + (int64_t)g * max_seq * D;
+    for (int kb = 0; kb < nkb; ++kb) {
+        __syncthreads();  // the previous tile's readers are done (and Q is staged)
+        for (int i = tid; i < BK * D; i += 256) {
+            const int j = i / D, d = i - j * D;
+            const int64_t src = (int64_t)min(kb * BK + j, total - 1) * D + d;
+            kT[d * L::KP + j] = kg[src];
+            vs[j * L::VP + d] = vg[src];
+        }
+        __syncthreads();
+        float s[RT][CT];
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+            for (int c = 0; c < CT; ++c) s[r][c] = 0.0f;
+        for (int d = 0; d < D; ++d) {
+            float qv[RT], kv[CT];
+#pragma unroll
+            for (int r = 0; r < RT; ++r) qv[r] = qT[d * L::QP + tr * RT + r];
+#pragma unroll
+            for (int c = 0; c < CT; ++c) kv[c] = kT[d * L::KP + tc * CT + c];
+#pragma unroll
+            for (int r = 0; r < RT; ++r)
+#pragma unroll
+                for (int c = 0; c < CT; ++c) s[r][c] = fmaf(qv[r], kv[c], s[r][c]);
+        }
+        // causal mask (position j visible to query i when j <= len + i), running max
+        // and sum per row over the 16 lanes of the row group
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            const int qpos = len + q0 + tr * RT + r;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int c = 0; c < CT; ++c) {
+                const int kpos = kb * BK + tc * CT + c;
+                if (kpos > qpos || kpos >= total) s[r][c] = -INFINITY;
+                mx = fmaxf(mx, s[r][c]);
+            }
+#pragma unroll
+            for (int o2 = 8; o2 > 0; o2 >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o2, 16));
+            const float mnew = fmaxf(mrow[r], mx);
+            const float alpha = mnew == -INFINITY ? 1.0f : expf(mrow[r] - mnew);
+            float sum = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CT; ++c) {
+                const float p = s[r][c] == -INFINITY ? 0.0f : expf(s[r][c] - mnew);
+                s[r][c] = p;
+                sum += p;
+            }
+#pragma unroll
+            for (int o2 = 8; o2 > 0; o2 >>= 1) sum += __shfl_xor(sum, o2, 16);
+            lrow[r] = lrow[r] * alpha + sum;
+            mrow[r] = mnew;
+#pragma unroll
+            for (int c = 0; c < DC; ++c) o[r][c] *= alpha;
+#pragma unroll
+            for (int c = 0; c < CT; ++c) pT[(tc * CT + c) * L::PP + tr * RT + r] = s[r][c];
+        }
+        __syncthreads();
+        for (int j = 0; j < BK; ++j) {
+            float pv[RT], vv[DC];
+#pragma unroll
+            for (int r = 0; r < RT; ++r) pv[r] = pT[j * L::PP + tr * RT + r];
+#pragma unroll
+            for (int c = 0; c < DC; ++c) vv[c] = vs[j * L::VP + tc * DC + c];
+#pragma unroll
+            for (int r = 0; r < RT; ++r)
+#pragma unroll
+                for (int c = 0; c < DC; ++c) o[r][c] = fmaf(pv[r], vv[c], o[r][c]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        const int qi = q0 + tr * RT + r;
+        if (qi >= m) continue;
+        const float inv = 1.0f / lrow[r];
+#pragma unroll
+        for (int c = 0; c < DC; ++c)
+            out[(int64_t)qi * H * D + (int64_t)h * D + tc * DC + c] = o[r][c] * inv;
+    }
+}
+
+template <int D, int BQ, int BK>
+hipError_t launch_prefill_attn(const KvCache& kv, const float* qkv, int m, int H, float* qw,
+                               float* out, hipStream_t s) {
+    using L = PrefillLds<D, BQ, BK>;
+    static const bool attr = hipFuncSetAttribute((const void*)attn_prefill_kernel<D, BQ, BK>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)L::BYTES) == hipSuccess;
+    if (!attr) return hipErrorInvalidValue;
+    const int KVH = (int)kv.n_kv_heads;
+    rope_append_kernel<D><<<dim3((unsigned)m, (unsigned)(H + KVH)), D / 2, 0, s>>>(
+        qkv, m, H, KVH, kv.state, 1.0f / sqrtf((float)D), kv.inv_freq, kv.k, kv.v,
+        (int)kv.max_seq, qw);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    attn_prefill_kernel<D, BQ, BK><<<dim3((unsigned)((m + BQ - 1) / BQ), (unsigned)H), 256,
+                                     L::BYTES, s>>>(qw, m, H, KVH, kv.state, kv.k, kv.v,
+                                                    (int)kv.max_seq, out);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+// Workspace (slot 2): the decode path's per-chunk partials at any length (at most
+// kMaxChunks chunks of (max, sum) and o[hd] per query), or the prompt path's rotated
+// queries [H][m][hd].
+size_t attention_workspace_bytes(const KvCache& kv, int64_t m, int64_t H) {
+    const int64_t G = H / std::max<int64_t>(kv.n_kv_heads, 1);
+    if (m * G <= kAttnMaxQ) return (size_t)m * H * kMaxChunks * (2 + kv.head_dim) * sizeof(float);
+    return (size_t)m * H * kv.head_dim * sizeof(float);
+}
+
+hipError_t launch_attention(const KvCache& kv, const float* qkv, int64_t m, int64_t H,
+                            float* out, int64_t len_hint, hipStream_t s) {
     const int D = (int)kv.head_dim;
-    const int64_t L = kv.len + m;
+    void* ws = nullptr;
+    hipError_t e;
+    if (m * (H / kv.n_kv_heads) > kAttnMaxQ) {
+        if ((e = stream_workspace(s, attention_workspace_bytes(kv, m, H), &ws, 2)) != hipSuccess)
+            return e;
+        float* qw = static_cast<float*>(ws);
+        if (D == 64) return launch_prefill_attn<64, 64, 64>(kv, qkv, (int)m, (int)H, qw, out, s);
+        if (D == 128) return launch_prefill_attn<128, 64, 64>(kv, qkv, (int)m, (int)H, qw, out, s);
+        return launch_prefill_attn<256, 32, 32>(kv, qkv, (int)m, (int)H, qw, out, s);
+    }
+    // decode: chunks sized for the known length, or for the longest the cache holds
+    const int64_t L = len_hint >= 0 ? len_hint + m
+                                    : std::min<int64_t>(kv.max_seq, attention_max_positions());
     const int64_t C = chunk_len(L, kv.n_kv_heads);
     if (C == 0) return hipErrorInvalidValue;  // longer than kMaxChunk * kMaxChunks
     const int chunks = (int)((L + C - 1) / C);
     const size_t pbytes = (size_t)m * H * chunks * (2 + D) * sizeof(float);
-    void* ws = nullptr;
-    hipError_t e = stream_workspace(s, pbytes, &ws, 2);
-    if (e != hipSuccess) return e;
+    if ((e = stream_workspace(s, pbytes, &ws, 2)) != hipSuccess) return e;
     float* part = static_cast<float*>(ws);
     if (D == 64) return launch_d<64>(kv, qkv, (int)m, (int)H, (int)C, chunks, part, out, s);
     if (D == 128) return launch_d<128>(kv, qkv, (int)m, (int)H, (int)C, chunks, part, out, s);

@@ -570,15 +570,18 @@ int unillm_hip_kv_cache_create(int64_t n_kv_heads, int64_t head_dim, int64_t max
     for (size_t i = 0; i < inv.size(); ++i)
         inv[i] = 1.0f / powf(rope_theta, (float)(2 * i) / (float)head_dim);
     hipError_t e;
-    void *k = nullptr, *v = nullptr, *f = nullptr;
+    void *k = nullptr, *v = nullptr, *f = nullptr, *st = nullptr;
     if ((e = hipMalloc(&k, buf)) != hipSuccess || (e = hipMalloc(&v, buf)) != hipSuccess ||
         (e = hipMalloc(&f, inv.size() * sizeof(float))) != hipSuccess ||
+        (e = hipMalloc(&st, 4 * sizeof(int))) != hipSuccess ||
         (e = hipMemset(k, 0, buf)) != hipSuccess || (e = hipMemset(v, 0, buf)) != hipSuccess ||
+        (e = hipMemset(st, 0, 4 * sizeof(int))) != hipSuccess ||
         (e = hipMemcpy(f, inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice)) !=
             hipSuccess) {
         (void)hipFree(k);
         (void)hipFree(v);
         (void)hipFree(f);
+        (void)hipFree(st);
         delete c;
         return e == hipErrorOutOfMemory ? fail(UNILLM_ERR_OUT_OF_MEMORY, "KV cache allocation")
                                         : fail_hip(e, "KV cache allocation");
@@ -586,38 +589,78 @@ int unillm_hip_kv_cache_create(int64_t n_kv_heads, int64_t head_dim, int64_t max
     c->k = static_cast<float*>(k);
     c->v = static_cast<float*>(v);
     c->inv_freq = static_cast<float*>(f);
+    c->state = static_cast<int*>(st);
     *out = c;
     return UNILLM_OK;
 }
 
 int unillm_hip_kv_cache_destroy(unillm_kv_cache* c) {
     if (!c) return UNILLM_OK;
-    hipError_t e = hipFree(c->k), e2 = hipFree(c->v), e3 = hipFree(c->inv_freq);
+    hipError_t e = hipFree(c->k), e2 = hipFree(c->v), e3 = hipFree(c->inv_freq),
+               e4 = hipFree(c->state);
     delete c;
     if (e == hipSuccess) e = e2;
     if (e == hipSuccess) e = e3;
+    if (e == hipSuccess) e = e4;
     return e == hipSuccess ? UNILLM_OK : fail_hip(e, "hipFree (KV cache)");
 }
 
+namespace {
+// The cache's device state after all work issued so far on `s` (s == nullptr and
+// device_wide: after all work on the device): refreshes the host's copy of the length.
+// A replayed call that overflowed is reported with the reference's message.
+int refresh_length(unillm_kv_cache* c, hipStream_t s, bool device_wide) {
+    int st[2] = {0, 0};
+    hipError_t e = device_wide ? hipDeviceSynchronize() : hipSuccess;
+    if (e == hipSuccess) e = hipMemcpyAsync(st, c->state, sizeof(st), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return fail_hip(e, "KV cache: reading the device length");
+    c->len = st[0];
+    // once a call on this cache has been captured, replays may run at any time
+    // between calls: the host copy is read back before every later use
+    c->len_stale = c->captured;
+    if (st[1])
+        return fail(UNILLM_ERR_INVALID_ARG,
+                    "KV cache append failed: KV cache overflow in a replayed call: current_len=" +
+                        std::to_string(st[0]) + ", max_seq_len=" + std::to_string(c->max_seq));
+    return UNILLM_OK;
+}
+
+// Sets the device length (and clears the overflow flag) once all device work is done.
+int set_length(unillm_kv_cache* c, int64_t len) {
+    const int st[3] = {(int)len, 0, (int)len};
+    hipError_t e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMemcpy(c->state, st, sizeof(st), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return fail_hip(e, "KV cache: setting the device length");
+    c->len = len;
+    c->len_stale = c->captured;
+    return UNILLM_OK;
+}
+}  // namespace
+
 int unillm_hip_kv_cache_length(const unillm_kv_cache* c, int64_t* len) {
     if (!c || !len) return fail(UNILLM_ERR_INVALID_ARG, "cache or len is NULL");
+    if (c->len_stale) {
+        if (int rc = refresh_length(const_cast<unillm_kv_cache*>(c), nullptr, true)) return rc;
+    }
     *len = c->len;
     return UNILLM_OK;
 }
 
 int unillm_hip_kv_cache_clear(unillm_kv_cache* c) {
     if (!c) return fail(UNILLM_ERR_INVALID_ARG, "cache is NULL");
-    c->len = 0;
-    return UNILLM_OK;
+    return set_length(c, 0);
 }
 
 int unillm_hip_kv_cache_truncate(unillm_kv_cache* c, int64_t len) {
     if (!c) return fail(UNILLM_ERR_INVALID_ARG, "cache is NULL");
+    if (c->len_stale) {
+        if (int rc = refresh_length(c, nullptr, true)) return rc;
+    }
     if (len < 0 || len > c->len)
         return fail(UNILLM_ERR_INVALID_ARG, "KV cache truncate: length " + std::to_string(len) +
                                                 " outside [0, " + std::to_string(c->len) + "]");
-    c->len = len;
-    return UNILLM_OK;
+    return set_length(c, len);
 }
 
 int unillm_hip_attention_decode(unillm_kv_cache* c, const float* qkv_dev, int64_t m,
@@ -627,23 +670,43 @@ int unillm_hip_attention_decode(unillm_kv_cache* c, const float* qkv_dev, int64_
     if (m < 1 || n_heads < c->n_kv_heads || n_heads % c->n_kv_heads != 0)
         return fail(UNILLM_ERR_INVALID_ARG,
                     "attention: need m >= 1 and n_heads a multiple of n_kv_heads");
-    if (m * (n_heads / c->n_kv_heads) > attention_max_queries())
-        return fail(UNILLM_ERR_UNSUPPORTED,
-                    "attention: m * n_heads / n_kv_heads must be <= " +
-                        std::to_string(attention_max_queries()) + " (decode steps)");
+    if (((uintptr_t)qkv_dev & 15u) != 0 || ((uintptr_t)out_dev & 3u) != 0)
+        return fail(UNILLM_ERR_INVALID_ARG, "attention: qkv must be 16-byte aligned, out 4-byte");
+    if (int rc = ensure_init()) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(s, &cs);
+    if (e != hipSuccess) return fail_hip(e, "attention: hipStreamIsCapturing");
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    const bool decode = m * (n_heads / c->n_kv_heads) <= attention_max_queries();
+    if (capturing) {
+        // the kernels read the length from the device at each replay: the grid covers
+        // the longest the cache holds, and the host's copy is unknown afterwards
+        if (decode && c->max_seq > attention_max_positions())
+            return fail(UNILLM_ERR_UNSUPPORTED,
+                        "attention: a captured decode step covers at most " +
+                            std::to_string(attention_max_positions()) + " cache positions");
+        e = launch_attention(*c, qkv_dev, m, n_heads, out_dev, -1, s);
+        if (e != hipSuccess) return fail_launch(e, "attention launch");
+        c->captured = true;
+        c->len_stale = true;
+        return UNILLM_OK;
+    }
+    if (c->len_stale) {
+        if (int rc = refresh_length(c, s, false)) return rc;
+    }
     if (c->len + m > c->max_seq)  // LayerKVCache::append's check (kv_cache.rs:114-121)
         return fail(UNILLM_ERR_INVALID_ARG,
                     "KV cache append failed: KV cache overflow: current_len=" +
                         std::to_string(c->len) + ", new_len=" + std::to_string(m) +
                         ", max_seq_len=" + std::to_string(c->max_seq));
-    if (c->len + m > attention_max_positions())
+    if (decode && c->len + m > attention_max_positions())
         return fail(UNILLM_ERR_UNSUPPORTED, "attention: len + m must be <= " +
-                                                std::to_string(attention_max_positions()));
-    if (int rc = ensure_init()) return rc;
-    hipError_t e = launch_attention_decode(*c, qkv_dev, m, n_heads, out_dev,
-                                           static_cast<hipStream_t>(stream));
+                                                std::to_string(attention_max_positions()) +
+                                                " on a decode step");
+    e = launch_attention(*c, qkv_dev, m, n_heads, out_dev, c->len, s);
     if (e != hipSuccess) return fail_launch(e, "attention launch");
-    c->len += m;  // the kernels run in stream order: later calls see the appended rows
+    c->len += m;  // the kernels advance the device copy in stream order
     return UNILLM_OK;
 }
 

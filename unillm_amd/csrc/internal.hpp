@@ -51,6 +51,13 @@ struct unillm_qweight {
 // The opaque KV-cache handle (one decoder layer, one sequence): K and V of
 // n_kv_heads heads, [n_kv_heads][max_seq][head_dim] f32 each, the first len
 // positions filled; inv_freq[head_dim / 2] the RoPE frequencies in f32.
+// The filled length lives in device memory, state[0], read and advanced by the
+// attention kernels themselves (so a captured call replays at successive
+// positions); state[1] is set to 1 by a kernel that found len + m > max_seq (the
+// call then appends nothing and writes NaN); state[2] is scratch between a call's
+// kernels.  `len` is the host's copy, exact while only eager calls ran; once a call
+// on the cache has been captured (captured), replays can move the device length at
+// any time, so the host reads state[0] back before each later use (len_stale).
 struct unillm_kv_cache {
     int device;
     int64_t n_kv_heads, head_dim, max_seq, len;
@@ -58,6 +65,9 @@ struct unillm_kv_cache {
     float* k;
     float* v;
     float* inv_freq;
+    int* state;
+    bool len_stale;
+    bool captured;
 };
 
 namespace unillm {
@@ -195,15 +205,19 @@ hipError_t launch_x_to_f16_rows(const float* x, int64_t m, int64_t k, void* out,
 // gu[m, 2 I] (the SwiGLU of the MFMA paths, after their store)
 hipError_t launch_swiglu(const float* gu, int64_t m, int64_t I, float* act, hipStream_t s);
 
-// Decode attention (attention.hip): RoPE at positions len .. len + m - 1 on the
-// fused QKV rows qkv[m, (H + 2 KVH) hd], k / v appended to the cache, causal
-// softmax attention into out[m, H hd]; the caller advances len.
+// Attention (attention.hip): RoPE at positions len .. len + m - 1 on the fused QKV
+// rows qkv[m, (H + 2 KVH) hd], k / v appended to the cache, causal softmax
+// attention into out[m, H hd]; the kernels read len from kv.state[0] and advance
+// it by m.  Decode steps (m H / KVH <= attention_max_queries()) split the cache
+// into chunks merged by log-sum-exp; longer calls (a prompt) run a tiled kernel
+// per (query block, head).  `len_hint` is the host's length, used only to size the
+// decode grid; a negative hint sizes it for max_seq (graph capture).
 using KvCache = ::unillm_kv_cache;
-hipError_t launch_attention_decode(const KvCache& kv, const float* qkv, int64_t m, int64_t H,
-                                   float* out, hipStream_t s);
+hipError_t launch_attention(const KvCache& kv, const float* qkv, int64_t m, int64_t H,
+                            float* out, int64_t len_hint, hipStream_t s);
 // Workspace (slot 2) a call of m tokens and H heads needs at any cache length.
 size_t attention_workspace_bytes(const KvCache& kv, int64_t m, int64_t H);
-int attention_max_queries();  // m * H / KVH per call
+int attention_max_queries();  // m * H / KVH per decode call
 int64_t attention_max_positions();  // len + m per call
 
 constexpr int64_t kGemvMaxM = 4;

@@ -5,6 +5,7 @@
 //   test_host gpu <file.gguf> <file.expect>      load to the device + forward parity
 //   test_host cpu-kq / gpu-kq <q4_k_m.gguf> <.expect>   the Q4_K / Q6_K file: plan,
 //                                                 parity, QKV and gate+up fusion
+//   test_host gpu-step <file.gguf> <file.step>   LlamaModel::forward_with_cache logits
 //
 // The .gguf / .expect pairs are written by tests/golden/make_gguf.py.
 #include <cmath>
@@ -118,9 +119,12 @@ static void test_cpu(const std::string& gguf, const std::vector<Expect>& ex) {
     CHECK(f.tensors().size() == ex.size());
     const GgufModelConfig c = GgufWeightLoader::config_from(f);
     CHECK(c.architecture == "llama");
-    CHECK(c.hidden_size == 64 && c.intermediate_size == 96 && c.num_hidden_layers == 2);
-    CHECK(c.num_attention_heads == 4 && c.num_key_value_heads == 2);
+    CHECK(c.hidden_size == 128 && c.intermediate_size == 96 && c.num_hidden_layers == 2);
+    CHECK(c.num_attention_heads == 2 && c.num_key_value_heads == 1 && c.head_dim == 64);
     CHECK(c.vocab_size == 8);  // from tokenizer.ggml.tokens
+    // GGUFModelConfig::from_gguf_metadata's float keys (weight_loader_core.rs:72-82)
+    CHECK(c.rms_norm_eps == 1e-5f && c.rope_theta == 20000.0f);
+    CHECK(c.max_position_embeddings == 2048);  // no context_length key: the default
 
     GgufWeightLoader loader;
     CHECK(loader.supports("model.gguf") && !loader.supports("model.safetensors"));
@@ -143,7 +147,7 @@ static void test_cpu(const std::string& gguf, const std::vector<Expect>& ex) {
     const GgufTensorInfo* q = nullptr;
     for (const auto& t : f.tensors())
         if (t.name == "blk.0.attn_q.weight") q = &t;
-    CHECK(q && q->type == GGML_Q4_0 && q->nbytes == 64 * 2 * 18);
+    CHECK(q && q->type == GGML_Q4_0 && q->nbytes == 128 * 4 * 18);
     if (q) CHECK(f.read(*q).size() == q->nbytes);
 
     // malformed files
@@ -215,7 +219,7 @@ static void test_gpu(const std::string& gguf, const std::vector<Expect>& ex) {
     CHECK(w.get_quantized("model.layers.1.mlp.down_proj.weight") != nullptr);
     CHECK(w.get_quantized("model.embed_tokens.weight") == nullptr);
     CHECK(w.tensors.count("model.embed_tokens.weight") == 1);
-    CHECK(w.tensors.at("model.embed_tokens.weight").shape() == std::vector<int64_t>({128, 64}));
+    CHECK(w.tensors.at("model.embed_tokens.weight").shape() == std::vector<int64_t>({128, 128}));
     HipTensorOps ops;
     for (const Expect& e : ex) {
         if (!e.quantized) continue;
@@ -240,17 +244,73 @@ static void test_gpu(const std::string& gguf, const std::vector<Expect>& ex) {
                       "QMatMul forward failed: input last dim 32"));
     CHECK(throws_with([&] { q->forward(Tensor::empty({64}, Device::hip(0))); },
                       "QMatMul forward failed: rank 1"));
-    CHECK(throws_with([&] { q->forward(Tensor::empty({2, 64}, Device::cpu())); },
+    CHECK(throws_with([&] { q->forward(Tensor::empty({2, 128}, Device::cpu())); },
                       "QMatMul forward failed: input is on CPU"));
     // lm_head_forward (llama.rs:396-405): the same result, the reference's lm_head context
     {
-        const Tensor h = Tensor::from_host(std::vector<float>(2 * 64, 0.25f), {2, 64},
+        const Tensor h = Tensor::from_host(std::vector<float>(2 * 128, 0.25f), {2, 128},
                                            Device::hip(0));
         CHECK(lm_head_forward(*q, h).to_host() == q->forward(h).to_host());
         CHECK(throws_with([&] { lm_head_forward(*q, Tensor::empty({3, 32}, Device::hip(0))); },
                           "QMatMul lm_head forward failed: input last dim 32"));
     }
     test_gpu_kv();
+}
+
+// LlamaModel::forward_with_cache (llama.rs:421-462) on the tiny Q4_0 model: three calls
+// on one cache (a 12-token prompt -- the prompt-length attention kernels -- then two
+// single tokens -- the decode kernels), logits against the f64 chain of the .step
+// file at 1e-3 normwise per call.  Both the fused-qkv load and the unfused one (q, k, v
+// a token at a time) are run; they must agree with each other as well.
+static void test_gpu_step(const std::string& gguf, const std::string& step_path) {
+    std::ifstream f(step_path, std::ios::binary);
+    char magic[4];
+    f.read(magic, 4);
+    CHECK(f && std::memcmp(magic, "USTP", 4) == 0);
+    uint32_t vocab = 0, nsteps = 0;
+    f.read(reinterpret_cast<char*>(&vocab), 4);
+    f.read(reinterpret_cast<char*>(&nsteps), 4);
+    std::vector<std::vector<int32_t>> ids(nsteps);
+    std::vector<std::vector<double>> ref(nsteps);
+    for (uint32_t s = 0; s < nsteps; ++s) {
+        uint32_t m = 0;
+        f.read(reinterpret_cast<char*>(&m), 4);
+        ids[s].resize(m);
+        ref[s].resize((size_t)m * vocab);
+        f.read(reinterpret_cast<char*>(ids[s].data()), (std::streamsize)(m * 4));
+        f.read(reinterpret_cast<char*>(ref[s].data()), (std::streamsize)(ref[s].size() * 8));
+    }
+    CHECK((bool)f);
+    if (!f) return;
+
+    const LlamaModel fused = LlamaModel::load(gguf);
+    LoadOptions only_gate_up;
+    only_gate_up.fuse_gate_up = true;
+    const LlamaModel split(GgufWeightLoader().load_weights(gguf, only_gate_up));
+    CHECK(fused.vocab_size() == (int64_t)vocab && fused.config().rope_theta == 20000.0f);
+    KVCache c1 = fused.new_cache(64), c2 = split.new_cache(64);
+    int64_t len = 0;
+    for (uint32_t s = 0; s < nsteps; ++s) {
+        const std::vector<float> a = fused.forward_with_cache(ids[s], c1).to_host();
+        const std::vector<float> b = split.forward_with_cache(ids[s], c2).to_host();
+        len += (int64_t)ids[s].size();
+        const double ea = normwise(a, ref[s]), eb = normwise(b, ref[s]);
+        std::printf("  step %u (m = %zu): normwise %.3g fused, %.3g unfused\n", s, ids[s].size(),
+                    ea, eb);
+        CHECK(ea < 1e-3 && eb < 1e-3);
+        CHECK(c1.seq_len() == len && c2.seq_len() == len);
+    }
+    // argument errors
+    CHECK(throws_with([&] { fused.forward_with_cache({}, c1); }, "no input tokens"));
+    CHECK(throws_with([&] { fused.forward_with_cache({128}, c1); }, "token id 128 outside"));
+    KVCache one = KVCache::with_capacity(1, 1, 64, 8);
+    CHECK(throws_with([&] { fused.forward_with_cache({1}, one); }, "the cache has 1 layers"));
+    KVCache small = fused.new_cache(4);
+    CHECK(throws_with([&] { fused.forward_with_cache({1, 2, 3, 4, 5}, small); },
+                      "KV cache overflow"));
+    LoadOptions none;
+    CHECK(throws_with([&] { LlamaModel(GgufWeightLoader().load_weights(gguf, none)); },
+                      "no fused gate_up handle"));
 }
 
 // LayerKVCache / KVCache (kv_cache.rs) and LayerKVCache::attend (forward_with_cache
@@ -472,11 +532,13 @@ int main(int argc, char** argv) {
     }
     const std::string mode = argv[1];
     try {
-        const std::vector<Expect> ex = read_expect(argv[3]);
+        const std::vector<Expect> ex = mode == "gpu-step" ? std::vector<Expect>{}
+                                                           : read_expect(argv[3]);
         if (mode == "cpu") test_cpu(argv[2], ex);
         else if (mode == "gpu") test_gpu(argv[2], ex);
         else if (mode == "cpu-kq") test_cpu_kq(argv[2], ex);
         else if (mode == "gpu-kq") test_gpu_kq(argv[2], ex);
+        else if (mode == "gpu-step") test_gpu_step(argv[2], argv[3]);
         else return 2;
     } catch (const std::exception& e) {
         std::fprintf(stderr, "FAIL: uncaught exception: %s\n", e.what());

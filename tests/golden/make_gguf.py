@@ -16,6 +16,13 @@ y = x . dequant(W)^T in f64 (numpy), the names after the reference's
 gguf_to_hf_name map (crates/runtime/src/weight_loader_core.rs:760-798), and
 which tensors stay quantized (weight_loader_core.rs:554).
 
+tiny_llama_q4_0.step: the logits of LlamaModelV2::forward_with_cache
+(llama.rs:421-462) over three calls on one cache (a 12-token prompt, then two
+single tokens), computed in f64 from the oracle's pieces: its exact dequant, its
+attention with a KV cache, and numpy for the layer norms, SwiGLU and residuals.
+Layout: "USTP", u32 vocab, u32 n_steps; per step u32 m, i32 ids[m],
+f64 logits[m * vocab].
+
 tiny_llama_q4_k_m.gguf has the tensor types llama.cpp's Q4_K_M mix uses:
 Q4_K projections and token_embd, Q6_K for output.weight and for layer 0's
 attn_v / ffn_down.  Its blocks are random valid Q4_K / Q6_K blocks (the
@@ -36,7 +43,11 @@ ALIGN = 32
 T_F32, T_F16, T_Q4_0, T_Q8_0, T_Q4_K, T_Q6_K = 0, 1, 2, 8, 12, 14
 V_UINT32, V_FLOAT32, V_STRING, V_ARRAY = 4, 6, 8, 9
 
-HIDDEN, INTER, VOCAB, LAYERS = 64, 96, 128, 2
+HIDDEN, INTER, VOCAB, LAYERS = 128, 96, 128, 2
+HEADS, KV_HEADS = 2, 1  # head_dim 64, two query heads a kv head
+ROPE_BASE = 20000.0
+NORM_EPS = 1e-5
+STEPS = [[3, 17, 42, 99, 5, 64, 127, 0, 31, 77, 12, 88], [7], [100]]
 
 
 def gstr(s: str) -> bytes:
@@ -88,8 +99,59 @@ def main() -> None:
     add_f32("output_norm.weight", HIDDEN)
     add_q("output.weight", T_Q8_0, VOCAB, HIDDEN)
 
-    write(tensors, "tiny_llama_q4_0", HIDDEN, INTER, LAYERS, rng, npz=True)
+    write(tensors, "tiny_llama_q4_0", HIDDEN, INTER, LAYERS, rng, npz=True,
+          heads=(HEADS, KV_HEADS), rope_base=ROPE_BASE)
+    write_steps(tensors, "tiny_llama_q4_0")
     main_kq()
+
+
+def layer_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """ops_fn::layer_norm with no bias (tensor_core.rs:973-1008): mean-subtracting,
+    biased variance, in f64."""
+    c = x - x.mean(axis=-1, keepdims=True)
+    return c / np.sqrt((c * c).mean(axis=-1, keepdims=True) + eps) * w
+
+
+def write_steps(tensors, stem) -> None:
+    """The f64 logits of forward_with_cache (llama.rs:421-462; the decoder layer
+    llama.rs:654-680) for the calls in STEPS, one cache across them."""
+    sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+    import oracle  # test infrastructure: exact dequant, attention with a KV cache
+
+    W = {}
+    for name, ttype, shape, raw, deq in tensors:
+        if ttype == T_F32:
+            W[hf_name(name)] = deq.astype(np.float64)
+        else:
+            n, k = shape
+            blocks = np.frombuffer(raw, dtype=np.uint8)
+            W[hf_name(name)] = oracle.dequant(ttype, blocks, n, k).astype(np.float64)
+    hd = HIDDEN // HEADS
+    max_seq = sum(len(s) for s in STEPS)
+    caches = [(np.zeros((KV_HEADS, max_seq, hd), np.float32),
+               np.zeros((KV_HEADS, max_seq, hd), np.float32)) for _ in range(LAYERS)]
+    length = 0
+    blob = b"USTP" + struct.pack("<II", VOCAB, len(STEPS))
+    for ids in STEPS:
+        h = W["model.embed_tokens.weight"][ids]
+        for i, (kc, vc) in enumerate(caches):
+            p = f"model.layers.{i}."
+            xn = layer_norm(h, W[p + "input_layernorm.weight"], 1e-6)
+            qkv = np.concatenate([xn @ W[p + f"self_attn.{t}_proj.weight"].T for t in "qkv"],
+                                 axis=1)
+            att = oracle.attention_decode(qkv.astype(np.float32), HEADS, KV_HEADS, hd,
+                                          ROPE_BASE, kc, vc, length)
+            h = h + att @ W[p + "self_attn.o_proj.weight"].T
+            xn = layer_norm(h, W[p + "post_attention_layernorm.weight"], 1e-6)
+            g = xn @ W[p + "mlp.gate_proj.weight"].T
+            u = xn @ W[p + "mlp.up_proj.weight"].T
+            h = h + (g / (1.0 + np.exp(-g)) * u) @ W[p + "mlp.down_proj.weight"].T
+        length += len(ids)
+        logits = layer_norm(h, W["model.norm.weight"], NORM_EPS) @ W["lm_head.weight"].T
+        blob += struct.pack("<I", len(ids)) + struct.pack(f"<{len(ids)}i", *ids)
+        blob += logits.astype("<f8").tobytes()
+    with open(os.path.join(HERE, stem + ".step"), "wb") as f:
+        f.write(blob)
 
 
 def main_kq() -> None:
@@ -129,7 +191,7 @@ def main_kq() -> None:
     write(tensors, "tiny_llama_q4_k_m", hidden, inter, layers, rng, npz=False)
 
 
-def write(tensors, stem, hidden, inter, layers, rng, npz) -> None:
+def write(tensors, stem, hidden, inter, layers, rng, npz, heads=(4, 2), rope_base=None) -> None:
     kvs = [
         kv("general.architecture", V_STRING, "llama"),
         kv("general.name", V_STRING, "tiny-llama-test"),
@@ -137,11 +199,13 @@ def write(tensors, stem, hidden, inter, layers, rng, npz) -> None:
         kv("llama.embedding_length", V_UINT32, hidden),
         kv("llama.feed_forward_length", V_UINT32, inter),
         kv("llama.block_count", V_UINT32, layers),
-        kv("llama.attention.head_count", V_UINT32, 4),
-        kv("llama.attention.head_count_kv", V_UINT32, 2),
-        kv("llama.attention.layer_norm_rms_epsilon", V_FLOAT32, 1e-5),
+        kv("llama.attention.head_count", V_UINT32, heads[0]),
+        kv("llama.attention.head_count_kv", V_UINT32, heads[1]),
+        kv("llama.attention.layer_norm_rms_epsilon", V_FLOAT32, NORM_EPS),
         kv("tokenizer.ggml.tokens", V_ARRAY, (V_STRING, [f"t{i}" for i in range(8)])),
     ]
+    if rope_base is not None:
+        kvs.append(kv("llama.rope.freq_base", V_FLOAT32, rope_base))
     header = b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(kvs)) + b"".join(kvs)
 
     infos = b""

@@ -3,7 +3,8 @@ parsing, the reference's name map and quantized/f32 classification, malformed
 files (CPU), then loading the tiny GGUFs onto the device and QMatMul::forward
 parity against the committed expectations, load-time QKV / gate+up fusion, and
 the KV-cache mirror (LayerKVCache / KVCache with closed-form attention checks and
-the reference's overflow message) (GPU)."""
+the reference's overflow message), and LlamaModel::forward_with_cache over the
+tiny Q4_0 model against the f64 logits of tests/golden/tiny_llama_q4_0.step (GPU)."""
 import os
 import subprocess
 
@@ -14,9 +15,9 @@ BIN = os.path.join(ROOT, "tests", "cpp", "test_host")
 GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 
-def _run(mode, stem="tiny_llama_q4_0"):
+def _run(mode, stem="tiny_llama_q4_0", data=".expect"):
     assert os.path.exists(BIN), "build first: python -m unillm_amd.build"
-    gguf, expect = (os.path.join(GOLDEN, stem + ext) for ext in (".gguf", ".expect"))
+    gguf, expect = (os.path.join(GOLDEN, stem + ext) for ext in (".gguf", data))
     r = subprocess.run([BIN, mode, gguf, expect], capture_output=True, text=True, timeout=120)
     print(r.stdout, r.stderr)
     assert r.returncode == 0, r.stderr
@@ -39,3 +40,8 @@ def test_host_k_quants_cpu():
 @pytest.mark.gpu
 def test_host_k_quants_gpu():
     _run("gpu-kq", "tiny_llama_q4_k_m")
+
+
+@pytest.mark.gpu
+def test_host_model_step_gpu():
+    _run("gpu-step", data=".step")

@@ -216,6 +216,15 @@ uint64_t GgufFile::get_uint(const std::string& key, uint64_t dflt) const {
     return dflt;
 }
 
+double GgufFile::get_float(const std::string& key, double dflt) const {
+    const GgufValue* v = find(key);
+    if (!v) return dflt;
+    if (v->kind == GgufValue::FLOAT) return v->f;
+    if (v->kind == GgufValue::UINT) return (double)v->u;
+    if (v->kind == GgufValue::INT) return (double)v->i;
+    return dflt;
+}
+
 std::string GgufFile::get_string(const std::string& key, const std::string& dflt) const {
     const GgufValue* v = find(key);
     return v && v->kind == GgufValue::STRING ? v->s : dflt;

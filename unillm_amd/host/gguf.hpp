@@ -71,6 +71,7 @@ public:
     const std::map<std::string, GgufValue>& metadata() const { return metadata_; }
     const GgufValue* find(const std::string& key) const;
     uint64_t get_uint(const std::string& key, uint64_t dflt) const;
+    double get_float(const std::string& key, double dflt) const;  // FLOAT (or integer) values
     std::string get_string(const std::string& key, const std::string& dflt) const;
 
     // Raw bytes of one tensor (block bytes for quantized types).

@@ -1,6 +1,7 @@
 // unillm_host.cpp -- implementation of the C++ host layer (see unillm_host.hpp).
 #include "unillm_host.hpp"
 
+#include <algorithm>
 #include <cstring>
 
 namespace unillm {
@@ -233,6 +234,24 @@ Tensor QuantLinear::forward_norm(const Tensor& x, const Tensor& gamma, const Ten
     return y;
 }
 
+Tensor QuantLinear::forward_norm_swiglu(const Tensor& x, const Tensor& gamma, const Tensor* beta,
+                                        float eps, void* stream) const {
+    check_input(x);
+    auto vec_k = [&](const Tensor& t) {
+        return t.device().is_hip() && t.numel() == k_;
+    };
+    if (!vec_k(gamma) || (beta && !vec_k(*beta)))
+        throw Error("QMatMul forward failed: norm weight / bias must be HIP tensors of k elements");
+    std::vector<int64_t> oshape = x.shape();
+    oshape.back() = n_ / 2;
+    Tensor act = Tensor::empty(oshape, x.device());
+    check_qmatmul(unillm_hip_qmatmul_norm_swiglu(w_, x.data(), gamma.data(),
+                                                 beta ? beta->data() : nullptr, eps,
+                                                 x.numel() / k_, act.data_mut(), stream),
+                  "QMatMul forward failed");
+    return act;
+}
+
 Tensor lm_head_forward(const QuantLinear& lm_head, const Tensor& hidden_states, void* stream) {
     // LlamaModelV2::lm_head_forward (llama.rs:396-405) maps the QMatMul error to
     // "QMatMul lm_head forward failed: {e}"
@@ -334,6 +353,14 @@ GgufModelConfig GgufWeightLoader::config_from(const GgufFile& f) {
     if (c.vocab_size == 0)
         if (const GgufValue* t = f.find("tokenizer.ggml.tokens"))
             if (t->kind == GgufValue::ARRAY) c.vocab_size = t->items.size();
+    c.head_dim = c.num_attention_heads ? c.hidden_size / c.num_attention_heads : 128;
+    auto getf = [&](const std::string& key, double dflt) {
+        return (float)f.get_float(c.architecture + "." + key, f.get_float("llama." + key, dflt));
+    };
+    c.rms_norm_eps = getf("attention.layer_norm_rms_epsilon", 1e-5);
+    c.rope_theta = getf("rope.freq_base", 10000.0);
+    c.max_position_embeddings = f.get_uint(c.architecture + ".context_length",
+                                           f.get_uint("llama.context_length", 2048));
     return c;
 }
 
@@ -546,6 +573,134 @@ int64_t KVCache::max_seq_len() const { return layers_.empty() ? 0 : layers_[0].m
 
 void KVCache::clear() {
     for (auto& l : layers_) l.clear();
+}
+
+// ---- LlamaModel ----------------------------------------------------------------------------
+LlamaModel::LlamaModel(ModelWeights weights) : w_(std::move(weights)) {
+    const GgufModelConfig& c = w_.config;
+    if (c.num_attention_heads == 0 || c.num_key_value_heads == 0 ||
+        c.hidden_size % c.num_attention_heads != 0 ||
+        c.num_attention_heads % c.num_key_value_heads != 0)
+        throw Error("LlamaModel: hidden_size, head_count and head_count_kv do not make heads");
+    hidden_ = (int64_t)c.hidden_size;
+    heads_ = (int64_t)c.num_attention_heads;
+    kv_heads_ = (int64_t)c.num_key_value_heads;
+    head_dim_ = hidden_ / heads_;
+    auto host = [&](const std::string& name) -> const Tensor& {
+        auto it = w_.tensors.find(name);
+        if (it == w_.tensors.end()) throw Error("LlamaModel: missing weight " + name);
+        return it->second;
+    };
+    auto vec = [&](const std::string& name) {
+        const Tensor& t = host(name);
+        if (t.numel() != hidden_)
+            throw Error("LlamaModel: " + name + " has " + std::to_string(t.numel()) +
+                        " elements, not hidden_size " + std::to_string(hidden_));
+        return t.to_device(Device::hip(0));
+    };
+    auto proj = [&](const std::string& name, int64_t n, int64_t k) {
+        std::shared_ptr<QuantLinear> q = w_.get_quantized(name);
+        if (!q) throw Error("LlamaModel: missing quantized weight " + name);
+        if (q->n() != n || q->k() != k)
+            throw Error("LlamaModel: " + name + " is [" + std::to_string(q->n()) + ", " +
+                        std::to_string(q->k()) + "], not [" + std::to_string(n) + ", " +
+                        std::to_string(k) + "]");
+        return q;
+    };
+    embed_ = host("model.embed_tokens.weight");
+    if (embed_.shape().size() != 2 || embed_.dim(1) != hidden_)
+        throw Error("LlamaModel: model.embed_tokens.weight is not [vocab, hidden_size]");
+    const int64_t kvw = kv_heads_ * head_dim_, inter = (int64_t)c.intermediate_size;
+    for (uint64_t L = 0; L < c.num_hidden_layers; ++L) {
+        const std::string p = "model.layers." + std::to_string(L) + ".";
+        Layer l;
+        l.in_norm = vec(p + "input_layernorm.weight");
+        l.post_norm = vec(p + "post_attention_layernorm.weight");
+        if (w_.get_quantized(p + "self_attn.qkv_proj.weight")) {
+            l.qkv = proj(p + "self_attn.qkv_proj.weight", hidden_ + 2 * kvw, hidden_);
+        } else {
+            l.q = proj(p + "self_attn.q_proj.weight", hidden_, hidden_);
+            l.k = proj(p + "self_attn.k_proj.weight", kvw, hidden_);
+            l.v = proj(p + "self_attn.v_proj.weight", kvw, hidden_);
+        }
+        l.o = proj(p + "self_attn.o_proj.weight", hidden_, hidden_);
+        if (!w_.get_quantized(p + "mlp.gate_up_proj.weight"))
+            throw Error("LlamaModel: layer " + std::to_string(L) +
+                        " has no fused gate_up handle (load with LoadOptions::fuse_gate_up)");
+        l.gate_up = proj(p + "mlp.gate_up_proj.weight", 2 * inter, hidden_);
+        l.down = proj(p + "mlp.down_proj.weight", hidden_, inter);
+        layers_.push_back(std::move(l));
+    }
+    norm_ = vec("model.norm.weight");
+    lm_head_ = w_.get_quantized("lm_head.weight");
+    if (!lm_head_ || lm_head_->k() != hidden_)
+        throw Error("LlamaModel: missing quantized lm_head.weight [vocab, hidden_size]");
+}
+
+LlamaModel LlamaModel::load(const std::string& gguf_path) {
+    LoadOptions opt;
+    opt.fuse_qkv = opt.fuse_gate_up = true;
+    return LlamaModel(GgufWeightLoader().load_weights(gguf_path, opt));
+}
+
+KVCache LlamaModel::new_cache(int64_t max_seq_len) const {
+    return KVCache::with_capacity(layers_.size(), kv_heads_, head_dim_, max_seq_len,
+                                  w_.config.rope_theta);
+}
+
+Tensor LlamaModel::forward_with_cache(const std::vector<int32_t>& input_ids, KVCache& cache,
+                                      void* stream) const {
+    const int64_t m = (int64_t)input_ids.size();
+    if (m == 0) throw Error("forward_with_cache: no input tokens");
+    if (cache.num_layers() != layers_.size())
+        throw Error("forward_with_cache: the cache has " + std::to_string(cache.num_layers()) +
+                    " layers, the model " + std::to_string(layers_.size()));
+    // 1. token embedding (ops_fn::embedding: rows of the table)
+    const int64_t vocab = embed_.dim(0);
+    std::vector<float> rows((size_t)(m * hidden_));
+    const float* table = embed_.data();
+    for (int64_t t = 0; t < m; ++t) {
+        const int32_t id = input_ids[(size_t)t];
+        if (id < 0 || id >= vocab)
+            throw Error("forward_with_cache: token id " + std::to_string(id) + " outside [0, " +
+                        std::to_string(vocab) + ")");
+        std::copy(table + (int64_t)id * hidden_, table + ((int64_t)id + 1) * hidden_,
+                  rows.begin() + t * hidden_);
+    }
+    Tensor h = Tensor::from_host(rows, {m, hidden_}, Device::hip(0));
+    // 2. the decoder layers
+    const int64_t kvw = kv_heads_ * head_dim_, width = hidden_ + 2 * kvw;
+    for (size_t L = 0; L < layers_.size(); ++L) {
+        const Layer& l = layers_[L];
+        Tensor qkv;
+        if (l.qkv) {
+            qkv = l.qkv->forward_norm(h, l.in_norm, nullptr, 1e-6f, stream);
+        } else {  // parts of different GGUF types: each part into its columns, a row at a time
+            qkv = Tensor::empty({m, width}, Device::hip(0));
+            const std::pair<const QuantLinear*, int64_t> parts[3] = {
+                {l.q.get(), 0}, {l.k.get(), hidden_}, {l.v.get(), hidden_ + kvw}};
+            for (int64_t t = 0; t < m; ++t)
+                for (const auto& [q, off] : parts)
+                    check_qmatmul(unillm_hip_qmatmul_norm(q->handle(), h.data() + t * hidden_,
+                                                          l.in_norm.data(), nullptr, 1e-6f, 1,
+                                                          qkv.data_mut() + t * width + off,
+                                                          stream),
+                                  "QMatMul forward failed");
+        }
+        const Tensor att = cache.layer_mut(L).attend(qkv, heads_, stream);
+        l.o->forward_add(att, h, stream);
+        const Tensor act = l.gate_up->forward_norm_swiglu(h, l.post_norm, nullptr, 1e-6f, stream);
+        l.down->forward_add(act, h, stream);
+    }
+    // 3. final norm fused into the head (lm_head_forward's error context)
+    try {
+        return lm_head_->forward_norm(h, norm_, nullptr, w_.config.rms_norm_eps, stream);
+    } catch (const Error& e) {
+        std::string msg = e.what();
+        const std::string p = "QMatMul forward failed: ";
+        if (msg.compare(0, p.size(), p) == 0) msg = msg.substr(p.size());
+        throw Error("QMatMul lm_head forward failed: " + msg);
+    }
 }
 
 }  // namespace unillm

@@ -119,6 +119,10 @@ public:
     // matmul; gamma / beta are HIP tensors of k elements (beta may be empty).
     Tensor forward_norm(const Tensor& x, const Tensor& gamma, const Tensor* beta, float eps,
                         void* stream = nullptr) const;
+    // forward_swiglu on the layer norm of x: post_attention_layernorm, gate, up and
+    // SwiGLU in one call (llama.rs:671-674, 1275-1283).
+    Tensor forward_norm_swiglu(const Tensor& x, const Tensor& gamma, const Tensor* beta,
+                               float eps, void* stream = nullptr) const;
     // qtensor.dequantize: f32 [n, k] on the device, bit-exact with GGML.
     Tensor dequantize(void* stream = nullptr) const;
 
@@ -220,6 +224,10 @@ struct GgufModelConfig {
     std::string architecture;
     uint64_t hidden_size = 0, intermediate_size = 0, num_hidden_layers = 0;
     uint64_t num_attention_heads = 0, num_key_value_heads = 0, vocab_size = 0;
+    uint64_t head_dim = 0;                  // hidden_size / num_attention_heads
+    float rms_norm_eps = 1e-5f;             // {arch}.attention.layer_norm_rms_epsilon
+    float rope_theta = 10000.0f;            // {arch}.rope.freq_base
+    uint64_t max_position_embeddings = 2048;  // {arch}.context_length
 };
 
 struct ModelWeights {
@@ -264,6 +272,50 @@ public:
     };
     std::vector<Plan> plan(const GgufFile& file) const;
     static GgufModelConfig config_from(const GgufFile& file);
+};
+
+// ---- the model ---------------------------------------------------------------------------
+// LlamaModelV2::forward_with_cache (llama.rs:421-462) over device-resident GGUF weights.
+// Per call of m new tokens:
+//   1. embedding: rows of model.embed_tokens.weight (f32 on the host, as the loader
+//      keeps it) gathered and copied to the device;
+//   2. per decoder layer (llama.rs:654-680): input_layernorm (eps 1e-6) fused into the
+//      q/k/v projection, attention with the layer's cache (LayerKVCache::attend),
+//      o_proj with the residual add in its epilogue, post_attention_layernorm
+//      (eps 1e-6) fused into gate_up with SwiGLU, down_proj with the residual add;
+//   3. model.norm (eps = rms_norm_eps of the GGUF) fused into lm_head.
+// "layer_norm" is the reference's ops_fn::layer_norm: mean-subtracting, no bias
+// (tensor_core.rs:973-1008).  Six launches a layer and one for the head.
+// The weights must hold the fused gate_up handle of every layer (load with
+// LoadOptions::fuse_gate_up); q/k/v use the fused qkv handle where the loader made
+// one, else the three projections run a token at a time into the qkv rows.
+class LlamaModel {
+public:
+    explicit LlamaModel(ModelWeights weights);  // throws if a tensor is missing
+    // GgufWeightLoader::load_weights with q/k/v and gate/up fused, then the model.
+    static LlamaModel load(const std::string& gguf_path);
+
+    const GgufModelConfig& config() const { return w_.config; }
+    int64_t vocab_size() const { return lm_head_->n(); }
+    // A cache for this model: one LayerKVCache per layer, the model's kv heads, head
+    // dim and rope_theta.
+    KVCache new_cache(int64_t max_seq_len) const;
+    // input_ids: the m new tokens -> logits [m, vocab] (HIP), freshly allocated; the
+    // cache grows by m (forward_with_cache's position offset is the cache's length).
+    Tensor forward_with_cache(const std::vector<int32_t>& input_ids, KVCache& cache,
+                              void* stream = nullptr) const;
+
+private:
+    struct Layer {
+        Tensor in_norm, post_norm;  // HIP, hidden_size each
+        std::shared_ptr<QuantLinear> qkv, q, k, v, o, gate_up, down;
+    };
+    ModelWeights w_;
+    int64_t hidden_ = 0, heads_ = 0, kv_heads_ = 0, head_dim_ = 0;
+    Tensor embed_;  // host [vocab, hidden] (shares w_'s storage)
+    std::vector<Layer> layers_;
+    Tensor norm_;  // HIP
+    std::shared_ptr<QuantLinear> lm_head_;
 };
 
 }  // namespace unillm

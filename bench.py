@@ -191,6 +191,84 @@ def cpu_baseline():
             "ms_per_pass": round(med * 1e3, 3)}
 
 
+_CPU_WEIGHTS = {}
+
+
+def cpu_rows(qtype, n, k, rows, budget_s=1.5, seed=0):
+    """Median seconds of oracle.candle_qmatmul (the reference's CPU QMatMul: Q8_0
+    activations, integer block dots, a loop over rows with OpenMP over columns) on
+    `rows` rows of one [n, k] weight drawn like the device's, and the threads used."""
+    import oracle
+
+    threads = len(os.sched_getaffinity(0))
+    rng = np.random.default_rng(seed)
+    if (qtype, n, k) not in _CPU_WEIGHTS:  # one weight per shape (the batched widths share it)
+        _CPU_WEIGHTS.clear()
+        _CPU_WEIGHTS[(qtype, n, k)] = oracle.quantize(
+            qtype, rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+    w = _CPU_WEIGHTS[(qtype, n, k)]
+    x = rng.standard_normal((rows, k), dtype=np.float32)
+    oracle.candle_qmatmul(qtype, w, x, n, k, nthreads=threads)  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        oracle.candle_qmatmul(qtype, w, x, n, k, nthreads=threads)
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), threads
+
+
+def extra_cpu_baselines(extra):
+    """A cpu_baseline for every extra entry of BASELINE configs 0, 2, 3 and 4, on the
+    same algorithmic bytes / flops as the device figure.  Bounded samples: prefill
+    times 8 rows (the reference's row loop costs the same per row, so m rows take m
+    times as long); the stack times one layer's four projections and the lm_head
+    (32 identical layers)."""
+    def entry(value, unit, cores, sample):
+        return {"value": round(value, 3), "unit": unit, "cores": cores, "kind": "port",
+                "sample": sample + "; candle QMatMul semantics restated in C (oracle/oracle.c), "
+                                   "OpenMP over columns, median of timed calls"}
+
+    key = "q8_0_gemv_m1_k2048_n5632"
+    if key in extra:
+        t, c = cpu_rows(Q8_0, 5632, 2048, 1)
+        b = wbytes(Q8_0, 5632, 2048) + 4 * 2048 + 4 * 5632
+        extra[key]["cpu_baseline"] = entry(b / t / 1e9, "GB/s", c, "the full call (m = 1)")
+    for n in (4096, 14336):
+        for m in (4, 16, 64):
+            key = f"q4_0_batched_m{m}_k4096_n{n}"
+            if key in extra:
+                t, c = cpu_rows(Q4_0, n, 4096, m)
+                b = wbytes(Q4_0, n, 4096) + 4 * m * 4096 + 4 * m * n
+                extra[key]["cpu_baseline"] = entry(b / t / 1e9, "GB/s", c, f"the full call (m = {m})")
+    for qtype, qn in ((Q4_0, "q4_0"), (Q8_0, "q8_0")):
+        for k, n in ((4096, 14336), (14336, 4096)):
+            keys = [f"{qn}_prefill_m{m}_k{k}_n{n}" for m in (512, 2048)]
+            if any(kk in extra for kk in keys):
+                t, c = cpu_rows(qtype, n, k, 8)
+                tf = 2 * 8 * n * k / t / 1e12
+                for kk in keys:
+                    if kk in extra:
+                        extra[kk]["cpu_baseline"] = entry(
+                            tf, "TFLOP/s", c, "8 of the m rows timed, the rate scaled to m rows")
+    for m in (1, 16):
+        key = f"llama2_7b_stack_q4_0_m{m}"
+        if key in extra:
+            layer = 0.0
+            for q, k, n in ((Q4_0, 4096, 12288), (Q4_0, 4096, 4096), (Q4_0, 4096, 22016),
+                            (Q4_0, 11008, 4096)):
+                t, c = cpu_rows(q, n, k, m, budget_s=1.0)
+                layer += t
+            head, c = cpu_rows(Q8_0, 32000, 4096, m, budget_s=1.0)
+            step = 32 * layer + head
+            extra[key]["cpu_baseline"] = entry(
+                m / step, "tokens/s", c,
+                f"one layer's 4 projections and the Q8_0 lm_head at m = {m} timed, "
+                f"the step = 32 layers + head ({step * 1e3:.1f} ms)")
+            extra[key]["cpu_baseline"]["GB/s"] = round(
+                extra[key]["GB/s"] * extra[key]["ms_per_step"] / (step * 1e3), 2)
+
+
 def extra_configs(torch, QuantLinear, gen, stream, only):
     """The other BASELINE configs, each timed with HIP events (median of 3
     rounds), weights rotated over >= 1 GB where the op is HBM-bound."""
@@ -533,6 +611,7 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline()
+        extra_cpu_baselines(extra)
 
     traffic, tinfo = measured_traffic()
     traffic_src = None

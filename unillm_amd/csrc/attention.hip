@@ -611,6 +611,237 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
     }
 }
 
+// ---- prompt-length attention on the f32 matrix cores (hd 64 and 128) ------------------------
+//
+// attn_prefill_mfma<D, NW>: a workgroup per (block of 32 NW queries, head h), NW waves,
+// wave w owning queries q0 + 32 w .. + 31.  Everything is f32: v_mfma_f32_32x32x2f32
+// multiplies f32 operands exactly and accumulates in f32, like the FMA loop above, so
+// the numbers match it to summation order.  The products are formed transposed so that
+// no row reduction crosses more than two lanes and P never leaves the registers:
+//   S^T [32 keys][32 queries] = K . Q^T -- the MFMA's A operand is a key row (lane l:
+//     key l % 32), B is the wave's queries (lane l: query l % 32), and MFMA s contracts
+//     dimensions s and D / 2 + s (lane half l / 32 takes one of each pair), so a lane
+//     reads its key's and its query's dimensions as float4s from LDS (the wave's
+//     queries are staged there once; rows padded to D + 4 floats);
+//   a lane's 16 accumulators are 16 keys of ONE query (rows 8 (r / 4) + 4 (l / 32) +
+//     r % 4, column l % 32): the query's max and sum over the tile are a 16-value
+//     register reduction and one exchange with lane l ^ 32;
+//   O^T [D][32 queries] += V^T . P^T -- MFMA s contracts keys 8 (s / 4) + s % 4 and the
+//     same + 4, exactly the two keys whose exponentials lanes l and l ^ 32 hold in
+//     accumulator s: B is the lane's own p[s], A is V[that key][32 t + l % 32] (D / 32
+//     output tiles).
+// Key tiles of 32 positions (K and V rows padded to D + 4 floats in LDS) are double
+// buffered: tile k + 1 is read into registers while tile k is computed and stored to
+// LDS after it.  A wave skips the tiles wholly past its last query (causal) but keeps
+// loading and meeting the others.  Same length and overflow handling as
+// attn_prefill_kernel.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int D, int NW>
+struct MfmaPrefillLds {
+    static constexpr int ROW = D + 4;                     // padded row (floats)
+    static constexpr int TILE = 32 * ROW;                 // one of K or V, or a wave's queries
+    // 2 stages x (K, V), then each wave's 32 queries
+    static constexpr size_t BYTES = (size_t)(2 * 2 + NW) * TILE * sizeof(float);
+    static constexpr int LPT = 2 * 32 * D / 4 / (64 * NW);  // float4 loads a thread per tile
+};
+
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_prefill_mfma(const float* __restrict__ qw, int m,
+                                                             int H, int KVH,
+                                                             int* __restrict__ state,
+                                                             const float* __restrict__ kc,
+                                                             const float* __restrict__ vc,
+                                                             int max_seq, float* __restrict__ out) {
+    using L = MfmaPrefillLds<D, NW>;
+    constexpr int HALF = D / 2, OT = D / 32, ROW = L::ROW;
+    extern __shared__ __attribute__((aligned(16))) float sm[];
+    const int h = blockIdx.y, g = h / (H / KVH);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int col = lane & 31, hf = lane >> 5;
+    const int q0 = blockIdx.x * 32 * NW;
+    const int len = state[2];
+    const int nq = min(32 * NW, m - q0);  // real queries of the block
+    if (len + m > max_seq) {
+        for (int i = tid; i < nq * D; i += 64 * NW)
+            out[(int64_t)(q0 + i / D) * H * D + (int64_t)h * D + i % D] = __builtin_nanf("");
+        if (blockIdx.x == 0 && h == 0 && tid == 0) state[1] = 1;
+        return;
+    }
+    if (blockIdx.x == 0 && h == 0 && tid == 0) state[0] = len + m;
+    const int total = len + m;
+    const float* kg = kc + (int64_t)g * max_seq * D;
+    const float* vg = vc + (int64_t)g * max_seq * D;
+
+    // the wave's 32 queries into LDS (rows past m repeat the last one): lane l copies
+    // float4 columns l, l + 64, ... of each row
+    const int qi = q0 + 32 * wv + col;
+    float* Qs = sm + 4 * L::TILE + wv * L::TILE;
+    for (int r = 0; r < 32; ++r) {
+        const float* src = qw + ((int64_t)h * m + min(q0 + 32 * wv + r, m - 1)) * D;
+        for (int c = lane; c < D / 4; c += 64)
+            *reinterpret_cast<float4*>(Qs + r * ROW + 4 * c) =
+                *reinterpret_cast<const float4*>(src + 4 * c);
+    }
+    const int qpos = len + qi;  // this lane's query position
+    const int wave_last = len + min(q0 + 32 * wv + 31, m - 1);
+    const int last_pos = len + q0 + nq - 1;
+    const int ntiles = last_pos / 32 + 1;
+
+    // tile loads: float4 f = i (64 NW) + tid, i < LPT, over [K rows 0..31 | V rows 0..31];
+    // the staged floats sit in one vector (a vector stays in registers)
+    typedef float stage_t __attribute__((ext_vector_type(4 * L::LPT)));
+    stage_t st;
+    auto src_of = [&](int i, int kt) {
+        const int f = i * 64 * NW + tid;
+        const int which = f / (32 * D / 4), r = (f / (D / 4)) % 32, c = f % (D / 4);
+        return (which ? vg : kg) + (int64_t)min(kt * 32 + r, total - 1) * D + 4 * c;
+    };
+    auto dst_of = [&](int i) {
+        const int f = i * 64 * NW + tid;
+        const int which = f / (32 * D / 4), r = (f / (D / 4)) % 32, c = f % (D / 4);
+        return which * L::TILE + r * ROW + 4 * c;
+    };
+
+    float mrun = -INFINITY, lrun = 0.0f;
+    f32x16 o[OT];
+#pragma unroll
+    for (int t = 0; t < OT; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[t][e] = 0.0f;
+
+#pragma unroll
+    for (int i = 0; i < L::LPT; ++i) {
+        const float4 v = *reinterpret_cast<const float4*>(src_of(i, 0));
+        *reinterpret_cast<float4*>(sm + dst_of(i)) = v;
+    }
+    __syncthreads();
+    for (int kt = 0; kt < ntiles; ++kt) {
+        const float* Ks = sm + (kt & 1) * 2 * L::TILE;
+        const float* Vs = Ks + L::TILE;
+        const bool more = kt + 1 < ntiles;
+        const bool live = kt * 32 <= wave_last;  // wave-uniform: tiles past the wave's last query skipped
+        f32x16 s;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[e] = 0.0f;
+        if (live) {
+            // S^T = K . Q^T, the next float4 of the key row read ahead of the MFMAs
+            const float* krow = Ks + col * ROW + hf * HALF;
+            const float* qrow = Qs + col * ROW + hf * HALF;
+            float4 kv = *reinterpret_cast<const float4*>(krow);
+            float4 qv = *reinterpret_cast<const float4*>(qrow);
+#pragma unroll
+            for (int u = 0; u < HALF / 4; ++u) {
+                const bool nx = u + 1 < HALF / 4;
+                const float4 kn = nx ? *reinterpret_cast<const float4*>(krow + 4 * (u + 1)) : kv;
+                const float4 qn = nx ? *reinterpret_cast<const float4*>(qrow + 4 * (u + 1)) : qv;
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qv.x, s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qv.y, s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qv.z, s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qv.w, s, 0, 0, 0);
+                kv = kn;
+                qv = qn;
+            }
+        }
+        // the next tile's rows requested while this one's softmax and p v run
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < L::LPT; ++i) {
+                const float4 v = *reinterpret_cast<const float4*>(src_of(i, kt + 1));
+                st[4 * i] = v.x;
+                st[4 * i + 1] = v.y;
+                st[4 * i + 2] = v.z;
+                st[4 * i + 3] = v.w;
+            }
+        }
+        if (live) {
+            // causal mask and the query's running max / sum
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int kpos = kt * 32 + 8 * (r / 4) + 4 * hf + r % 4;
+                if (kpos > qpos || kpos >= total) s[r] = -INFINITY;
+                tmax = fmaxf(tmax, s[r]);
+            }
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+            const float mnew = fmaxf(mrun, tmax);
+            const float alpha = mnew == -INFINITY ? 1.0f : expf(mrun - mnew);
+            float tsum = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = s[r] == -INFINITY ? 0.0f : expf(s[r] - mnew);
+                s[r] = p;
+                tsum += p;
+            }
+            tsum += __shfl_xor(tsum, 32, 64);
+            lrun = lrun * alpha + tsum;
+            mrun = mnew;
+            // O^T = alpha O^T + V^T . P^T
+#pragma unroll
+            for (int t = 0; t < OT; ++t) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) o[t][e] *= alpha;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = 8 * (r / 4) + 4 * hf + r % 4;
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[key * ROW + 32 * t + col], s[r],
+                                                                o[t], 0, 0, 0);
+                }
+            }
+        }
+        if (more) {
+            float* base = sm + ((kt + 1) & 1) * 2 * L::TILE;
+#pragma unroll
+            for (int i = 0; i < L::LPT; ++i)
+                *reinterpret_cast<float4*>(base + dst_of(i)) =
+                    make_float4(st[4 * i], st[4 * i + 1], st[4 * i + 2], st[4 * i + 3]);
+        }
+        __syncthreads();
+    }
+    // O[q][32 t + 8 u + 4 hf + 0..3] = o[t][4 u + 0..3] / l, a float4 each
+    if (qi < m) {
+        const float inv = 1.0f / lrun;
+        float* orow = out + (int64_t)qi * H * D + (int64_t)h * D + 4 * hf;
+#pragma unroll
+        for (int t = 0; t < OT; ++t)
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                *reinterpret_cast<float4*>(orow + 32 * t + 8 * u) =
+                    make_float4(o[t][4 * u] * inv, o[t][4 * u + 1] * inv, o[t][4 * u + 2] * inv,
+                                o[t][4 * u + 3] * inv);
+    }
+}
+
+template <int D, int NW>
+hipError_t launch_prefill_mfma(const KvCache& kv, const float* qkv, int m, int H, float* qw,
+                               float* out, hipStream_t s) {
+    using L = MfmaPrefillLds<D, NW>;
+    static const bool attr = hipFuncSetAttribute((const void*)attn_prefill_mfma<D, NW>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)L::BYTES) == hipSuccess;
+    if (!attr) return hipErrorInvalidValue;
+    const int KVH = (int)kv.n_kv_heads;
+    rope_append_kernel<D><<<dim3((unsigned)m, (unsigned)(H + KVH)), D / 2, 0, s>>>(
+        qkv, m, H, KVH, kv.state, 1.0f / sqrtf((float)D), kv.inv_freq, kv.k, kv.v,
+        (int)kv.max_seq, qw);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    attn_prefill_mfma<D, NW><<<dim3((unsigned)((m + 32 * NW - 1) / (32 * NW)), (unsigned)H),
+                               64 * NW, L::BYTES, s>>>(qw, m, H, KVH, kv.state, kv.k, kv.v,
+                                                       (int)kv.max_seq, out);
+    return hipGetLastError();
+}
+
+// 128 queries a workgroup when that still gives two workgroups a CU, else 64.
+template <int D>
+hipError_t launch_prefill_mfma_auto(const KvCache& kv, const float* qkv, int m, int H, float* qw,
+                                    float* out, hipStream_t s) {
+    const int64_t blocks128 = (int64_t)((m + 127) / 128) * H;
+    if (blocks128 >= 2 * (int64_t)device_info().cu_count)
+        return launch_prefill_mfma<D, 4>(kv, qkv, m, H, qw, out, s);
+    return launch_prefill_mfma<D, 2>(kv, qkv, m, H, qw, out, s);
+}
+
 template <int D, int BQ, int BK>
 hipError_t launch_prefill_attn(const KvCache& kv, const float* qkv, int m, int H, float* qw,
                                float* out, hipStream_t s) {
@@ -651,8 +882,8 @@ hipError_t launch_attention(const KvCache& kv, const float* qkv, int64_t m, int6
         if ((e = stream_workspace(s, attention_workspace_bytes(kv, m, H), &ws, 2)) != hipSuccess)
             return e;
         float* qw = static_cast<float*>(ws);
-        if (D == 64) return launch_prefill_attn<64, 64, 64>(kv, qkv, (int)m, (int)H, qw, out, s);
-        if (D == 128) return launch_prefill_attn<128, 64, 64>(kv, qkv, (int)m, (int)H, qw, out, s);
+        if (D == 64) return launch_prefill_mfma_auto<64>(kv, qkv, (int)m, (int)H, qw, out, s);
+        if (D == 128) return launch_prefill_mfma_auto<128>(kv, qkv, (int)m, (int)H, qw, out, s);
         return launch_prefill_attn<256, 32, 32>(kv, qkv, (int)m, (int)H, qw, out, s);
     }
     // decode: chunks sized for the known length, or for the longest the cache holds

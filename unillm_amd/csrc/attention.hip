@@ -621,8 +621,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
 //   S^T [32 keys][32 queries] = K . Q^T -- the MFMA's A operand is a key row (lane l:
 //     key l % 32), B is the wave's queries (lane l: query l % 32), and MFMA s contracts
 //     dimensions s and D / 2 + s (lane half l / 32 takes one of each pair), so a lane
-//     reads its key's and its query's dimensions as float4s from LDS (the wave's
-//     queries are staged there once; rows padded to D + 4 floats);
+//     reads its key's dimensions as float4s from LDS and keeps its query's half in
+//     registers for the whole kernel;
 //   a lane's 16 accumulators are 16 keys of ONE query (rows 8 (r / 4) + 4 (l / 32) +
 //     r % 4, column l % 32): the query's max and sum over the tile are a 16-value
 //     register reduction and one exchange with lane l ^ 32;
@@ -641,8 +641,7 @@ template <int D, int NW>
 struct MfmaPrefillLds {
     static constexpr int ROW = D + 4;                     // padded row (floats)
     static constexpr int TILE = 32 * ROW;                 // one of K or V, or a wave's queries
-    // 2 stages x (K, V), then each wave's 32 queries
-    static constexpr size_t BYTES = (size_t)(2 * 2 + NW) * TILE * sizeof(float);
+    static constexpr size_t BYTES = (size_t)2 * 2 * TILE * sizeof(float);  // 2 stages x (K, V)
     static constexpr int LPT = 2 * 32 * D / 4 / (64 * NW);  // float4 loads a thread per tile
 };
 
@@ -673,15 +672,21 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_mfma(const float* __rest
     const float* kg = kc + (int64_t)g * max_seq * D;
     const float* vg = vc + (int64_t)g * max_seq * D;
 
-    // the wave's 32 queries into LDS (rows past m repeat the last one): lane l copies
-    // float4 columns l, l + 64, ... of each row
+    // this lane's query (rows past m repeat the last one), its half of the dimensions
+    // in one vector (a vector stays in registers)
     const int qi = q0 + 32 * wv + col;
-    float* Qs = sm + 4 * L::TILE + wv * L::TILE;
-    for (int r = 0; r < 32; ++r) {
-        const float* src = qw + ((int64_t)h * m + min(q0 + 32 * wv + r, m - 1)) * D;
-        for (int c = lane; c < D / 4; c += 64)
-            *reinterpret_cast<float4*>(Qs + r * ROW + 4 * c) =
-                *reinterpret_cast<const float4*>(src + 4 * c);
+    typedef float qhalf_t __attribute__((ext_vector_type(HALF)));
+    qhalf_t qr;
+    {
+        const float* qrow = qw + ((int64_t)h * m + min(qi, m - 1)) * D + hf * HALF;
+#pragma unroll
+        for (int u = 0; u < HALF / 4; ++u) {
+            const float4 v = *reinterpret_cast<const float4*>(qrow + 4 * u);
+            qr[4 * u] = v.x;
+            qr[4 * u + 1] = v.y;
+            qr[4 * u + 2] = v.z;
+            qr[4 * u + 3] = v.w;
+        }
     }
     const int qpos = len + qi;  // this lane's query position
     const int wave_last = len + min(q0 + 32 * wv + 31, m - 1);
@@ -727,21 +732,23 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_mfma(const float* __rest
         if (live) {
             // S^T = K . Q^T, the next float4 of the key row read ahead of the MFMAs
             const float* krow = Ks + col * ROW + hf * HALF;
-            const float* qrow = Qs + col * ROW + hf * HALF;
+            // two accumulators (dimension pairs alternate), so consecutive MFMAs do not
+            // wait on each other's results
+            f32x16 s2;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s2[e] = 0.0f;
             float4 kv = *reinterpret_cast<const float4*>(krow);
-            float4 qv = *reinterpret_cast<const float4*>(qrow);
 #pragma unroll
             for (int u = 0; u < HALF / 4; ++u) {
-                const bool nx = u + 1 < HALF / 4;
-                const float4 kn = nx ? *reinterpret_cast<const float4*>(krow + 4 * (u + 1)) : kv;
-                const float4 qn = nx ? *reinterpret_cast<const float4*>(qrow + 4 * (u + 1)) : qv;
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qv.x, s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qv.y, s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qv.z, s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qv.w, s, 0, 0, 0);
+                const float4 kn =
+                    u + 1 < HALF / 4 ? *reinterpret_cast<const float4*>(krow + 4 * (u + 1)) : kv;
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qr[4 * u], s, 0, 0, 0);
+                s2 = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qr[4 * u + 1], s2, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qr[4 * u + 2], s, 0, 0, 0);
+                s2 = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qr[4 * u + 3], s2, 0, 0, 0);
                 kv = kn;
-                qv = qn;
             }
+            s += s2;
         }
         // the next tile's rows requested while this one's softmax and p v run
         if (more) {
@@ -776,16 +783,30 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_mfma(const float* __rest
             tsum += __shfl_xor(tsum, 32, 64);
             lrun = lrun * alpha + tsum;
             mrun = mnew;
-            // O^T = alpha O^T + V^T . P^T
+            // O^T = alpha O^T + V^T . P^T.  The rescale moves the accumulators through
+            // the VALU, so it runs only when some query's running max changed (alpha
+            // is then < 1 somewhere in the wave; after the first tiles it rarely is).
+            if (__any(alpha != 1.0f)) {
 #pragma unroll
-            for (int t = 0; t < OT; ++t) {
+                for (int t = 0; t < OT; ++t)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) o[t][e] *= alpha;
+                    for (int e = 0; e < 16; ++e) o[t][e] *= alpha;
+            }
+            // two output tiles at a time, their MFMAs interleaved (independent chains),
+            // the tiles' 32 V values read ahead
+#pragma unroll
+            for (int t = 0; t < OT; t += 2) {
+                float vv[2][16];
+#pragma unroll
+                for (int a = 0; a < 2; ++a)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        vv[a][r] = Vs[(8 * (r / 4) + 4 * hf + r % 4) * ROW + 32 * (t + a) + col];
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int key = 8 * (r / 4) + 4 * hf + r % 4;
-                    o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[key * ROW + 32 * t + col], s[r],
-                                                                o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[0][r], s[r], o[t], 0, 0, 0);
+                    o[t + 1] =
+                        __builtin_amdgcn_mfma_f32_32x32x2f32(vv[1][r], s[r], o[t + 1], 0, 0, 0);
                 }
             }
         }
@@ -832,12 +853,15 @@ hipError_t launch_prefill_mfma(const KvCache& kv, const float* qkv, int m, int H
     return hipGetLastError();
 }
 
-// 128 queries a workgroup when that still gives two workgroups a CU, else 64.
+// The largest workgroup (8, 4 or 2 waves of 32 queries) that still gives every CU a
+// workgroup: eight waves are two a SIMD.
 template <int D>
 hipError_t launch_prefill_mfma_auto(const KvCache& kv, const float* qkv, int m, int H, float* qw,
                                     float* out, hipStream_t s) {
-    const int64_t blocks128 = (int64_t)((m + 127) / 128) * H;
-    if (blocks128 >= 2 * (int64_t)device_info().cu_count)
+    const int64_t cus = device_info().cu_count;
+    if ((int64_t)((m + 255) / 256) * H >= cus)
+        return launch_prefill_mfma<D, 8>(kv, qkv, m, H, qw, out, s);
+    if ((int64_t)((m + 127) / 128) * H >= cus)
         return launch_prefill_mfma<D, 4>(kv, qkv, m, H, qw, out, s);
     return launch_prefill_mfma<D, 2>(kv, qkv, m, H, qw, out, s);
 }

@@ -128,11 +128,13 @@ def _layer_norm(x, gamma, beta, eps):
     (Q4_0, 1, 300, 4096, PATH_GEMV, False, 0.0), (Q4_K, 3, 257, 2048, PATH_GEMV, True, 0.0),
     (Q8_0, 2, 129, 4096, PATH_GEMV, False, 100.0), (Q4_0, 16, 1024, 4096, PATH_DECODE_MFMA, True, 0.0),
     (Q4_0, 1, 256, 11008, PATH_DECODE_MFMA, False, 0.0), (Q6_K, 64, 300, 2048, PATH_DECODE_MFMA, False, 50.0),
-    (Q8_0, 256, 512, 4096, PATH_PREFILL_MFMA, True, 0.0), (Q4_0, 130, 256, 8192, PATH_PREFILL_MFMA, False, 10.0)])
+    (Q8_0, 256, 512, 4096, PATH_PREFILL_MFMA, True, 0.0), (Q4_0, 130, 256, 8192, PATH_PREFILL_MFMA, False, 10.0),
+    (Q4_0, 3, 128, 20480, PATH_DECODE_MFMA, True, 5.0), (Q8_0, 70, 128, 20480, PATH_PREFILL_MFMA, True, 5.0)])
 def test_layer_norm_matmul(qtype, m, n, k, path, bias, offset):
     # offset: x = offset + N(0, 1) per row, so the mean dwarfs the deviations (a
     # one-pass variance would lose them); (Q4_0, 1, 256, 11008): past the GEMV's
-    # norm reach, routed to batched decode
+    # norm reach, routed to batched decode; k = 20480: rows longer than the norm
+    # kernel holds in registers (16 x 1024 elements), the rest read again
     blocks = _blocks(qtype, n, k, seed=5 * n + k)
     rng = np.random.default_rng(n + m)
     x = (oracle.normal(m * k, seed=k + m).reshape(m, k) + offset).astype(np.float32)

@@ -55,6 +55,7 @@ namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -66,6 +67,34 @@ __device__ __forceinline__ uint32_t pk_f16(float a, float b) {
     uint32_t r;  // round to nearest even, a in the low half
     asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
     return r;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// v combined by op over the 64 lanes of a (whole, converged) wave, the same value in
+// every lane: four DPP steps give each lane its 16-lane row's result (quad_perm
+// [1,0,3,2], [2,3,0,1], row_ror 4, row_ror 8), and the four rows are read with
+// v_readlane -- no LDS round trips, as a shuffle across rows would take.
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+    v = op(v, dpp_mov<0xB1>(v));
+    v = op(v, dpp_mov<0x4E>(v));
+    v = op(v, dpp_mov<0x124>(v));
+    v = op(v, dpp_mov<0x128>(v));
+    auto lane = [&](int l) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+    };
+    return op(op(lane(0), lane(16)), op(lane(32), lane(48)));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    return wave_reduce(v, [](float a, float b) { return a + b; });
 }
 
 // (a & mask) | bits in one instruction (the compiler splits it in two).
@@ -205,8 +234,7 @@ __global__ __launch_bounds__(128) void xprep_kernel(const float* __restrict__ x,
         return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     };
     float mx = fmaxf(amax4(a), amax4(b));
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    mx = wave_max(mx);
     if ((t & 63) == 0) red[t >> 6] = mx;
     __syncthreads();
     const float sc = f16_row_scale(fmaxf(red[0], red[1]), rf + (int64_t)s * 64 + r);
@@ -671,8 +699,7 @@ __global__ __launch_bounds__(1024) void xrows_kernel(const float* __restrict__ x
     }
     for (int64_t i = t + 2 * nt; i < g8; i += nt)
         mx = fmaxf(mx, fmaxf(amax(xr[2 * i]), amax(xr[2 * i + 1])));
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    mx = wave_max(mx);
     if ((t & 63) == 0) red[t >> 6] = mx;
     __syncthreads();
     mx = 0.0f;
@@ -697,6 +724,10 @@ __global__ __launch_bounds__(1024) void xrows_kernel(const float* __restrict__ x
 // is on the path without the norm: per row (rs != nullptr: the prefill operand, as
 // xrows_kernel) or per k slice of the row (rf != nullptr: the S slices of the
 // batched-decode split, factors at rf[s * 64 + r], as xprep_kernel).
+// One HBM read: a thread holds groups t and t + nt of x, gamma and beta in registers
+// across the passes (rows up to 16 nt elements); a longer row's further groups are
+// read again in each pass.  Grid (m, 1 + Z): blockIdx.y == 0 normalizes row r, the
+// Z others zero parts of y's row r.
 __global__ __launch_bounds__(1024) void norm_convert_kernel(const float* __restrict__ x, int64_t k,
                                                            NormArgs norm, uint4* __restrict__ out,
                                                            float* __restrict__ y, int64_t ny,
@@ -704,75 +735,97 @@ __global__ __launch_bounds__(1024) void norm_convert_kernel(const float* __restr
                                                            float* __restrict__ rf) {
     __shared__ float red[16];
     __shared__ unsigned smax[kMaxSplitSlices];  // per-slice max |v| as f32 bits (>= 0)
-    const int64_t r = blockIdx.x;
+    __shared__ float ssc[kMaxSplitSlices];
+    const int64_t r = blockIdx.x, g8 = k / 8;
+    const int t = threadIdx.x, nt = blockDim.x, lane = t & 63, wv = t >> 6;
+    if (blockIdx.y > 0) {  // (uniform) zero y's row r over column range blockIdx.y - 1 of Z
+        const int64_t Z = gridDim.y - 1, z = blockIdx.y - 1;
+        float* yr = y + r * ny;
+        for (int64_t i = ny * z / Z + t; i < ny * (z + 1) / Z; i += nt) yr[i] = 0.0f;
+        return;
+    }
     const float4* xr = reinterpret_cast<const float4*>(x + r * k);
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    auto block_sum = [&](float t) {
+    const float4* g4 = reinterpret_cast<const float4*>(norm.gamma);
+    const float4* b4 = reinterpret_cast<const float4*>(norm.beta);
+    auto ld8 = [](const float4* p, int64_t i) {
+        const float4 a = p[2 * i], b = p[2 * i + 1];
+        return f32x8{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    };
+    auto hsum = [](f32x8 v) {
+        return ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+    };
+    auto amax = [](f32x8 v) {
+        float m = 0.0f;
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
-        if (lane == 0) red[wv] = t;
+        for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
+        return m;
+    };
+    auto block_sum = [&](float v) {
+        v = wave_sum(v);
+        if (lane == 0) red[wv] = v;
         __syncthreads();
         float sum = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 16; ++w) sum += red[w];
+        for (int w = 0; w < nt / 64; ++w) sum += red[w];
         __syncthreads();
         return sum;
     };
-    float t = 0.0f;
-    for (int64_t i = threadIdx.x; i < k / 4; i += 1024) {
-        const float4 a = xr[i];
-        t += (a.x + a.y) + (a.z + a.w);
+    const bool l0 = t < g8, l1 = t + nt < g8;
+    const f32x8 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    f32x8 x0 = zero, x1 = zero, ga0 = zero, ga1 = zero, be0 = zero, be1 = zero;
+    if (l0) {
+        x0 = ld8(xr, t);
+        ga0 = ld8(g4, t);
+        if (b4) be0 = ld8(b4, t);
     }
-    const float mean = block_sum(t) / (float)k;
-    t = 0.0f;
-    for (int64_t i = threadIdx.x; i < k / 4; i += 1024) {
-        const float4 a = xr[i];
-        t += (a.x - mean) * (a.x - mean) + (a.y - mean) * (a.y - mean) +
-             (a.z - mean) * (a.z - mean) + (a.w - mean) * (a.w - mean);
+    if (l1) {
+        x1 = ld8(xr, t + nt);
+        ga1 = ld8(g4, t + nt);
+        if (b4) be1 = ld8(b4, t + nt);
     }
-    const float sd = sqrtf(block_sum(t) / (float)k + norm.eps);
-    const float4* g4 = reinterpret_cast<const float4*>(norm.gamma);
-    const float4* b4 = reinterpret_cast<const float4*>(norm.beta);
-    auto values = [&](int64_t i, float (&v)[8]) {  // the normalized elements 8 i .. 8 i + 7
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const float4 a = xr[2 * i + h], g = g4[2 * i + h];
-            const float4 b = norm.beta ? b4[2 * i + h] : make_float4(0.f, 0.f, 0.f, 0.f);
-            v[4 * h + 0] = (a.x - mean) / sd * g.x + b.x;
-            v[4 * h + 1] = (a.y - mean) / sd * g.y + b.y;
-            v[4 * h + 2] = (a.z - mean) / sd * g.z + b.z;
-            v[4 * h + 3] = (a.w - mean) / sd * g.w + b.w;
-        }
+    float acc = hsum(x0) + hsum(x1);
+    for (int64_t i = t + 2 * nt; i < g8; i += nt) acc += hsum(ld8(xr, i));
+    const float mean = block_sum(acc) / (float)k;
+    auto dev2 = [&](f32x8 v) {
+        const f32x8 d = v - mean;
+        return hsum(d * d);
     };
+    acc = (l0 ? dev2(x0) : 0.0f) + (l1 ? dev2(x1) : 0.0f);
+    for (int64_t i = t + 2 * nt; i < g8; i += nt) acc += dev2(ld8(xr, i));
+    const float sd = sqrtf(block_sum(acc) / (float)k + norm.eps);
+    // the normalized elements of a group from its x, gamma and beta
+    auto normed = [&](f32x8 v, f32x8 g, f32x8 b) { return (v - mean) / sd * g + b; };
+    auto values = [&](int64_t i) {  // a group past the registers, read again
+        return normed(ld8(xr, i), ld8(g4, i), b4 ? ld8(b4, i) : zero);
+    };
+    const f32x8 v0 = normed(x0, ga0, be0), v1 = normed(x1, ga1, be1);
     // the scale of group i: per row (sc) or per slice (ssc[slice of i])
     float sc = 1.0f;
-    __shared__ float ssc[kMaxSplitSlices];
-    const int64_t C = (k + 127) / 128;  // 128-k chunks; slice s = chunks [s C / S, (s + 1) C / S)
-    auto slice_of = [&](int64_t i) {  // the slice holding group i (chunk i / 16)
-        const int64_t c = i / 16;
-        int s = (int)(c * S / C);  // floor(s C / S) <= c; then the largest such s
-        while (s + 1 < S && (int64_t)(s + 1) * C / S <= c) ++s;
-        while (s > 0 && (int64_t)s * C / S > c) --s;
+    // 128-k chunks; slice s = chunks [s C / S, (s + 1) C / S), its first group sb[s]
+    // (16 groups a chunk; sb[S] = 16 C).  The slice of group i: a float estimate of
+    // floor(c S / C), then the largest s with sb[s] <= i (no 64-bit division per group)
+    __shared__ int sb[kMaxSplitSlices + 1];
+    const int64_t C = (k + 127) / 128;
+    const float sfac = (float)S / (float)C;
+    auto slice_of = [&](int64_t i) {
+        int s = min(S - 1, (int)((float)(i >> 4) * sfac));
+        while (s + 1 < S && sb[s + 1] <= i) ++s;
+        while (s > 0 && sb[s] > i) --s;
         return s;
     };
+    int s0 = 0, s1 = 0;  // the slices of groups t and t + nt
     if (rs || rf) {  // kernel arguments: every branch on them is uniform, barriers included
         if (rf) {
-            for (int s = threadIdx.x; s < S; s += 1024) smax[s] = 0u;
+            for (int s = t; s < S; s += nt) smax[s] = 0u;
+            for (int s = t; s <= S; s += nt) sb[s] = (int)((int64_t)s * C / S) * 16;
             __syncthreads();
-        }
-        float mx = 0.0f;
-        for (int64_t i = threadIdx.x; i < k / 8; i += 1024) {
-            float v[8];
-            values(i, v);
-            float gm = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) gm = fmaxf(gm, fabsf(v[e]));
-            if (rf) atomicMax(&smax[slice_of(i)], __float_as_uint(gm));
-            else mx = fmaxf(mx, gm);
-        }
-        if (rf) {
+            s0 = l0 ? slice_of(t) : 0;
+            s1 = l1 ? slice_of(t + nt) : 0;
+            if (l0) atomicMax(&smax[s0], __float_as_uint(amax(v0)));
+            if (l1) atomicMax(&smax[s1], __float_as_uint(amax(v1)));
+            for (int64_t i = t + 2 * nt; i < g8; i += nt)
+                atomicMax(&smax[slice_of(i)], __float_as_uint(amax(values(i))));
             __syncthreads();
-            for (int s = threadIdx.x; s < S; s += 1024) {
+            for (int s = t; s < S; s += nt) {
                 // the scale of f16_row_scale, one thread per slice (f16_row_scale
                 // stores from thread 0 only)
                 const float m = __uint_as_float(smax[s]);
@@ -785,26 +838,25 @@ __global__ __launch_bounds__(1024) void norm_convert_kernel(const float* __restr
             }
             __syncthreads();
         } else {
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            float mx = fmaxf(l0 ? amax(v0) : 0.0f, l1 ? amax(v1) : 0.0f);
+            for (int64_t i = t + 2 * nt; i < g8; i += nt) mx = fmaxf(mx, amax(values(i)));
+            mx = wave_max(mx);
             if (lane == 0) red[wv] = mx;
             __syncthreads();
             mx = 0.0f;
-#pragma unroll
-            for (int w = 0; w < 16; ++w) mx = fmaxf(mx, red[w]);
+            for (int w = 0; w < nt / 64; ++w) mx = fmaxf(mx, red[w]);
             sc = f16_row_scale(mx, rs + r);
         }
     }
-    for (int64_t i = threadIdx.x; i < k / 8; i += 1024) {
-        float v[8];
-        values(i, v);
-        const float f = rf ? ssc[slice_of(i)] : sc;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] *= f;
-        out[r * (k / 8) + i] = make_uint4(pk_f16(v[0], v[2]), pk_f16(v[1], v[3]),
-                                          pk_f16(v[4], v[6]), pk_f16(v[5], v[7]));
-    }
-    for (int64_t i = threadIdx.x; i < ny; i += 1024) y[r * ny + i] = 0.0f;
+    uint4* xo = out + r * g8;
+    auto put = [&](int64_t i, f32x8 v, float f) {
+        v *= f;
+        xo[i] = make_uint4(pk_f16(v[0], v[2]), pk_f16(v[1], v[3]), pk_f16(v[4], v[6]),
+                           pk_f16(v[5], v[7]));
+    };
+    if (l0) put(t, v0, rf ? ssc[s0] : sc);
+    if (l1) put(t + nt, v1, rf ? ssc[s1] : sc);
+    for (int64_t i = t + 2 * nt; i < g8; i += nt) put(i, values(i), rf ? ssc[slice_of(i)] : sc);
 }
 
 hipError_t launch_swiglu(const float* gu, int64_t m, int64_t I, float* act, hipStream_t s) {
@@ -819,8 +871,12 @@ hipError_t launch_norm_convert(const float* x, int64_t m, int64_t k, const NormA
                                float* rf) {
     if (m <= 0) return hipSuccess;
     if (rf && (S < 1 || S > kMaxSplitSlices)) return hipErrorInvalidValue;
-    norm_convert_kernel<<<(unsigned)m, 1024, 0, s>>>(x, k, norm, static_cast<uint4*>(out), y, ny,
-                                                     rs, S, rf);
+    // two groups of 8 a thread, whole waves, 64 .. 1024 threads; y zeroed by further
+    // workgroups, 2048 columns (8 KiB) each, at most 16 a row
+    const int nt = (int)std::min<int64_t>(1024, std::max<int64_t>(64, (k / 16 + 63) / 64 * 64));
+    const unsigned Z = ny > 0 ? (unsigned)std::min<int64_t>(16, (ny + 2047) / 2048) : 0;
+    norm_convert_kernel<<<dim3((unsigned)m, 1 + Z), nt, 0, s>>>(
+        x, k, norm, static_cast<uint4*>(out), y, ny, rs, S, rf);
     return hipGetLastError();
 }
 

@@ -613,8 +613,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
 
 // ---- prompt-length attention on the f32 matrix cores (hd 64 and 128) ------------------------
 //
-// attn_prefill_mfma<D, NW>: a workgroup per (block of 32 NW queries, head h), NW waves,
-// wave w owning queries q0 + 32 w .. + 31.  Everything is f32: v_mfma_f32_32x32x2f32
+// attn_prefill_mfma<D, NW>: a workgroup per (NW / 2 pairs of 32-query tiles, head h), NW
+// waves, each owning one tile (the pairing below balances the causal work).  Everything is f32: v_mfma_f32_32x32x2f32
 // multiplies f32 operands exactly and accumulates in f32, like the FMA loop above, so
 // the numbers match it to summation order.  The products are formed transposed so that
 // no row reduction crosses more than two lanes and P never leaves the registers:
@@ -658,12 +658,29 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_mfma(const float* __rest
     const int h = blockIdx.y, g = h / (H / KVH);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int col = lane & 31, hf = lane >> 5;
-    const int q0 = blockIdx.x * 32 * NW;
+    // The head's T tiles of 32 queries are paired (i, T - 1 - i), so that under the
+    // causal mask every pair holds the same work (the middle tile of an odd T has no
+    // partner); workgroup b takes pairs b NW / 2 .. + NW / 2 - 1, waves w < NW / 2
+    // their low tiles and the others their high ones (one of each a SIMD).  -1: no
+    // tile for this wave.
+    const int T = (m + 31) / 32, P = (T + 1) / 2;
+    auto tile_of = [&](int w) {
+        const int i = (int)blockIdx.x * (NW / 2) + w % (NW / 2);
+        if (i >= P) return -1;
+        if (w < NW / 2) return i;
+        return T - 1 - i > i ? T - 1 - i : -1;
+    };
+    const int mytile = tile_of(wv);  // wave-uniform
+    int top = 0;                     // the workgroup's last tile
+#pragma unroll
+    for (int w = 0; w < NW; ++w) top = max(top, tile_of(w));
     const int len = state[2];
-    const int nq = min(32 * NW, m - q0);  // real queries of the block
     if (len + m > max_seq) {
-        for (int i = tid; i < nq * D; i += 64 * NW)
-            out[(int64_t)(q0 + i / D) * H * D + (int64_t)h * D + i % D] = __builtin_nanf("");
+        if (mytile >= 0)
+            for (int i = lane; i < 32 * D; i += 64) {
+                const int q = 32 * mytile + i / D;
+                if (q < m) out[(int64_t)q * H * D + (int64_t)h * D + i % D] = __builtin_nanf("");
+            }
         if (blockIdx.x == 0 && h == 0 && tid == 0) state[1] = 1;
         return;
     }
@@ -672,9 +689,9 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_mfma(const float* __rest
     const float* kg = kc + (int64_t)g * max_seq * D;
     const float* vg = vc + (int64_t)g * max_seq * D;
 
-    // this lane's query (rows past m repeat the last one), its half of the dimensions
-    // in one vector (a vector stays in registers)
-    const int qi = q0 + 32 * wv + col;
+    // this lane's query (rows past m, and a wave without a tile, repeat the last one),
+    // its half of the dimensions in one vector (a vector stays in registers)
+    const int qi = mytile >= 0 ? 32 * mytile + col : m;
     typedef float qhalf_t __attribute__((ext_vector_type(HALF)));
     qhalf_t qr;
     {
@@ -689,8 +706,9 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_mfma(const float* __rest
         }
     }
     const int qpos = len + qi;  // this lane's query position
-    const int wave_last = len + min(q0 + 32 * wv + 31, m - 1);
-    const int last_pos = len + q0 + nq - 1;
+    // the wave's last query position (-1: no tile, every key tile skipped)
+    const int wave_last = mytile >= 0 ? len + min(32 * mytile + 31, m - 1) : -1;
+    const int last_pos = len + min(32 * top + 31, m - 1);
     const int ntiles = last_pos / 32 + 1;
 
     // tile loads: float4 f = i (64 NW) + tid, i < LPT, over [K rows 0..31 | V rows 0..31];
@@ -847,7 +865,9 @@ hipError_t launch_prefill_mfma(const KvCache& kv, const float* qkv, int m, int H
         (int)kv.max_seq, qw);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    attn_prefill_mfma<D, NW><<<dim3((unsigned)((m + 32 * NW - 1) / (32 * NW)), (unsigned)H),
+    // pairs of 32-query tiles, NW / 2 pairs a workgroup
+    const int pairs = ((m + 31) / 32 + 1) / 2;
+    attn_prefill_mfma<D, NW><<<dim3((unsigned)((pairs + NW / 2 - 1) / (NW / 2)), (unsigned)H),
                                64 * NW, L::BYTES, s>>>(qw, m, H, KVH, kv.state, kv.k, kv.v,
                                                        (int)kv.max_seq, out);
     return hipGetLastError();

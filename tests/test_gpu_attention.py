@@ -149,6 +149,25 @@ def test_attention_prompt_long_context():
     assert _run_steps(H, KVH, D, [350, 350, 512], max_seq=1300, seed=3) < 1e-4
 
 
+@pytest.mark.parametrize("KVH", [8, 32])
+def test_attention_prompt_unsplit_matches_split(KVH):
+    # A 2048-token prompt at 32 heads has query waves enough for the chip and runs in
+    # one kernel.  The same prompt as two 1024-token calls splits each workgroup's key
+    # tiles in two and merges the partials, the path the oracle tests above pin (their
+    # sizes all split).  The two outputs agree to f32 rounding.
+    H, D, m = 32, 128, 2048
+    w = (H + 2 * KVH) * D
+    qkv = torch.from_numpy(oracle.normal(m * w, seed=91 + KVH).reshape(m, w)).cuda()
+    print(f"prompt split vs unsplit H={H} KVH={KVH} m={m}", flush=True)
+    whole = KvCache(KVH, D, m).attention(qkv, H).cpu().numpy()
+    kv = KvCache(KVH, D, m)
+    first = kv.attention(qkv[:m // 2].contiguous(), H).cpu().numpy()
+    second = kv.attention(qkv[m // 2:].contiguous(), H).cpu().numpy()
+    halves = np.concatenate([first, second])
+    assert kv.seq_len == m
+    assert oracle.normwise_error(whole, halves) < 1e-5
+
+
 def test_attention_prompt_causality():
     # changing token 9's q, k and v leaves the outputs of tokens 0 .. 8 bit for bit
     H, KVH, D, m = 8, 2, 64, 40

@@ -651,7 +651,8 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_mfma(const float* __rest
                                                              int* __restrict__ state,
                                                              const float* __restrict__ kc,
                                                              const float* __restrict__ vc,
-                                                             int max_seq, float* __restrict__ out) {
+                                                             int max_seq, float* __restrict__ out,
+                                                             float* __restrict__ part) {
     using L = MfmaPrefillLds<D, NW>;
     constexpr int HALF = D / 2, OT = D / 32, ROW = L::ROW;
     extern __shared__ __attribute__((aligned(16))) float sm[];
@@ -674,17 +675,23 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_mfma(const float* __rest
     int top = 0;                     // the workgroup's last tile
 #pragma unroll
     for (int w = 0; w < NW; ++w) top = max(top, tile_of(w));
+    // gridDim.z > 1: this workgroup takes split blockIdx.z of the key tiles and writes
+    // partials (max, sum, unnormalized o) for attn_merge_kernel, which then also
+    // advances the length or reports the overflow
+    const int S = gridDim.z, z = blockIdx.z;
     const int len = state[2];
     if (len + m > max_seq) {
-        if (mytile >= 0)
-            for (int i = lane; i < 32 * D; i += 64) {
-                const int q = 32 * mytile + i / D;
-                if (q < m) out[(int64_t)q * H * D + (int64_t)h * D + i % D] = __builtin_nanf("");
-            }
-        if (blockIdx.x == 0 && h == 0 && tid == 0) state[1] = 1;
+        if (S == 1) {
+            if (mytile >= 0)
+                for (int i = lane; i < 32 * D; i += 64) {
+                    const int q = 32 * mytile + i / D;
+                    if (q < m) out[(int64_t)q * H * D + (int64_t)h * D + i % D] = __builtin_nanf("");
+                }
+            if (blockIdx.x == 0 && h == 0 && tid == 0) state[1] = 1;
+        }
         return;
     }
-    if (blockIdx.x == 0 && h == 0 && tid == 0) state[0] = len + m;
+    if (S == 1 && blockIdx.x == 0 && h == 0 && tid == 0) state[0] = len + m;
     const int total = len + m;
     const float* kg = kc + (int64_t)g * max_seq * D;
     const float* vg = vc + (int64_t)g * max_seq * D;
@@ -710,6 +717,7 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_mfma(const float* __rest
     const int wave_last = mytile >= 0 ? len + min(32 * mytile + 31, m - 1) : -1;
     const int last_pos = len + min(32 * top + 31, m - 1);
     const int ntiles = last_pos / 32 + 1;
+    const int kt0 = z * ntiles / S, kt1 = (z + 1) * ntiles / S;  // this workgroup's key tiles
 
     // tile loads: float4 f = i (64 NW) + tid, i < LPT, over [K rows 0..31 | V rows 0..31];
     // the staged floats sit in one vector (a vector stays in registers)
@@ -735,14 +743,14 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_mfma(const float* __rest
 
 #pragma unroll
     for (int i = 0; i < L::LPT; ++i) {
-        const float4 v = *reinterpret_cast<const float4*>(src_of(i, 0));
-        *reinterpret_cast<float4*>(sm + dst_of(i)) = v;
+        const float4 v = *reinterpret_cast<const float4*>(src_of(i, kt0));
+        *reinterpret_cast<float4*>(sm + (kt0 & 1) * 2 * L::TILE + dst_of(i)) = v;
     }
     __syncthreads();
-    for (int kt = 0; kt < ntiles; ++kt) {
+    for (int kt = kt0; kt < kt1; ++kt) {
         const float* Ks = sm + (kt & 1) * 2 * L::TILE;
         const float* Vs = Ks + L::TILE;
-        const bool more = kt + 1 < ntiles;
+        const bool more = kt + 1 < kt1;
         const bool live = kt * 32 <= wave_last;  // wave-uniform: tiles past the wave's last query skipped
         f32x16 s;
 #pragma unroll
@@ -837,6 +845,23 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_mfma(const float* __rest
         }
         __syncthreads();
     }
+    if (S > 1) {
+        // partials as attn_merge_kernel reads them: (max, sum) at [q H + h][S], o at
+        // [q H + h][S][hd] after all the pairs (a query with no live tile in this split
+        // leaves (-inf, 0) and zeros, weight 0 in the merge)
+        if (qi < m) {
+            const int64_t qc = ((int64_t)qi * H + h) * S + z;
+            if (hf == 0) *reinterpret_cast<float2*>(part + 2 * qc) = make_float2(mrun, lrun);
+            float* prow = part + (int64_t)m * H * S * 2 + qc * D + 4 * hf;
+#pragma unroll
+            for (int t = 0; t < OT; ++t)
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    *reinterpret_cast<float4*>(prow + 32 * t + 8 * u) =
+                        make_float4(o[t][4 * u], o[t][4 * u + 1], o[t][4 * u + 2], o[t][4 * u + 3]);
+        }
+        return;
+    }
     // O[q][32 t + 8 u + 4 hf + 0..3] = o[t][4 u + 0..3] / l, a float4 each
     if (qi < m) {
         const float inv = 1.0f / lrun;
@@ -851,9 +876,51 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_mfma(const float* __rest
     }
 }
 
+// The merge of a split prompt call (S splits of each workgroup's key tiles, a handful):
+// a thread per (query q, head h, 4 dimensions); out = sum_z e^(M_z - M) o_z /
+// sum_z e^(M_z - M) l_z over the splits' (M_z, l_z, o_z) partials (a split in which the
+// query had no live key leaves M_z = -inf: weight 0).  The length advance and the
+// overflow report are attn_merge_kernel's.
+template <int D>
+__global__ __launch_bounds__(256) void attn_merge_split_kernel(const float* __restrict__ part,
+                                                               int m, int H, int S,
+                                                               float* __restrict__ out,
+                                                               int* __restrict__ state,
+                                                               int max_seq) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (q H + h) (D / 4) + d4
+    const int64_t total = (int64_t)m * H * (D / 4);
+    const int len = state[2];
+    if (len + m > max_seq) {
+        if (i < total)
+            reinterpret_cast<float4*>(out)[i] =
+                make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""),
+                            __builtin_nanf(""));
+        if (i == 0) state[1] = 1;
+        return;
+    }
+    if (i == 0) state[0] = len + m;
+    if (i >= total) return;
+    const int64_t qh = i / (D / 4), d4 = i % (D / 4);
+    const float2* ms = reinterpret_cast<const float2*>(part) + qh * S;
+    const float4* po = reinterpret_cast<const float4*>(part + (int64_t)m * H * S * 2) + qh * S * (D / 4) + d4;
+    float M = -INFINITY;
+    for (int z = 0; z < S; ++z) M = fmaxf(M, ms[z].x);
+    float l = 0.0f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int z = 0; z < S; ++z) {
+        const float2 p = ms[z];
+        const float f = p.x == -INFINITY ? 0.0f : expf(p.x - M);
+        const float4 v = po[(int64_t)z * (D / 4)];
+        l = fmaf(p.y, f, l);
+        o = make_float4(fmaf(v.x, f, o.x), fmaf(v.y, f, o.y), fmaf(v.z, f, o.z), fmaf(v.w, f, o.w));
+    }
+    const float inv = 1.0f / l;
+    reinterpret_cast<float4*>(out)[i] = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+}
+
 template <int D, int NW>
 hipError_t launch_prefill_mfma(const KvCache& kv, const float* qkv, int m, int H, float* qw,
-                               float* out, hipStream_t s) {
+                               float* part, int S, float* out, hipStream_t s) {
     using L = MfmaPrefillLds<D, NW>;
     static const bool attr = hipFuncSetAttribute((const void*)attn_prefill_mfma<D, NW>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -865,25 +932,31 @@ hipError_t launch_prefill_mfma(const KvCache& kv, const float* qkv, int m, int H
         (int)kv.max_seq, qw);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    // pairs of 32-query tiles, NW / 2 pairs a workgroup
+    // pairs of 32-query tiles, NW / 2 pairs a workgroup; S splits of the key tiles
     const int pairs = ((m + 31) / 32 + 1) / 2;
-    attn_prefill_mfma<D, NW><<<dim3((unsigned)((pairs + NW / 2 - 1) / (NW / 2)), (unsigned)H),
+    attn_prefill_mfma<D, NW><<<dim3((unsigned)((pairs + NW / 2 - 1) / (NW / 2)), (unsigned)H,
+                                    (unsigned)S),
                                64 * NW, L::BYTES, s>>>(qw, m, H, KVH, kv.state, kv.k, kv.v,
-                                                       (int)kv.max_seq, out);
+                                                       (int)kv.max_seq, out, part);
+    e = hipGetLastError();
+    if (S == 1 || e != hipSuccess) return e;
+    const int64_t merge_threads = (int64_t)m * H * (D / 4);
+    attn_merge_split_kernel<D><<<(unsigned)((merge_threads + 255) / 256), 256, 0, s>>>(
+        part, m, H, S, out, kv.state, (int)kv.max_seq);
     return hipGetLastError();
 }
 
-// The largest workgroup (8, 4 or 2 waves of 32 queries) that still gives every CU a
-// workgroup: eight waves are two a SIMD.
+// The largest workgroup (8, 4 or 2 waves of 32 queries) whose grid, with the call's S
+// key splits, still gives every CU a workgroup: eight waves are two a SIMD (the K and V
+// tiles in LDS allow only two workgroups a CU).
 template <int D>
 hipError_t launch_prefill_mfma_auto(const KvCache& kv, const float* qkv, int m, int H, float* qw,
-                                    float* out, hipStream_t s) {
-    const int64_t cus = device_info().cu_count;
-    if ((int64_t)((m + 255) / 256) * H >= cus)
-        return launch_prefill_mfma<D, 8>(kv, qkv, m, H, qw, out, s);
-    if ((int64_t)((m + 127) / 128) * H >= cus)
-        return launch_prefill_mfma<D, 4>(kv, qkv, m, H, qw, out, s);
-    return launch_prefill_mfma<D, 2>(kv, qkv, m, H, qw, out, s);
+                                    float* part, int S, float* out, hipStream_t s) {
+    const int64_t cus = device_info().cu_count, pairs = ((m + 31) / 32 + 1) / 2;
+    auto wgs = [&](int nw) { return (pairs + nw / 2 - 1) / (nw / 2) * H * S; };
+    if (wgs(8) >= cus) return launch_prefill_mfma<D, 8>(kv, qkv, m, H, qw, part, S, out, s);
+    if (wgs(4) >= cus) return launch_prefill_mfma<D, 4>(kv, qkv, m, H, qw, part, S, out, s);
+    return launch_prefill_mfma<D, 2>(kv, qkv, m, H, qw, part, S, out, s);
 }
 
 template <int D, int BQ, int BK>
@@ -908,13 +981,30 @@ hipError_t launch_prefill_attn(const KvCache& kv, const float* qkv, int m, int H
 
 }  // namespace
 
+namespace {
+// Key-range splits of a prompt call on the matrix-core kernel: the largest of 1, 2, 4
+// that keeps the call's 32-query waves at most two a SIMD (m512 at 32 heads: 512
+// waves on 1024 SIMDs, 4 splits); 1 needs no partials and no merge.
+int prompt_split(int64_t m, int64_t H, int64_t D) {
+    if (D != 64 && D != 128) return 1;
+    const int64_t waves = (m + 31) / 32 * H, target = 8 * (int64_t)device_info().cu_count;
+    int S = 1;
+    while (S < 4 && waves * 2 * S <= target) S *= 2;
+    return S;
+}
+size_t prompt_q_bytes(int64_t m, int64_t H, int64_t D) {
+    return ((size_t)m * H * D * sizeof(float) + 255) / 256 * 256;
+}
+}  // namespace
+
 // Workspace (slot 2): the decode path's per-chunk partials at any length (at most
 // kMaxChunks chunks of (max, sum) and o[hd] per query), or the prompt path's rotated
-// queries [H][m][hd].
+// queries [H][m][hd] followed, for a split call, by its S partials per query.
 size_t attention_workspace_bytes(const KvCache& kv, int64_t m, int64_t H) {
-    const int64_t G = H / std::max<int64_t>(kv.n_kv_heads, 1);
-    if (m * G <= kAttnMaxQ) return (size_t)m * H * kMaxChunks * (2 + kv.head_dim) * sizeof(float);
-    return (size_t)m * H * kv.head_dim * sizeof(float);
+    const int64_t G = H / std::max<int64_t>(kv.n_kv_heads, 1), D = kv.head_dim;
+    if (m * G <= kAttnMaxQ) return (size_t)m * H * kMaxChunks * (2 + D) * sizeof(float);
+    const int S = prompt_split(m, H, D);
+    return prompt_q_bytes(m, H, D) + (S > 1 ? (size_t)m * H * S * (2 + D) * sizeof(float) : 0);
 }
 
 hipError_t launch_attention(const KvCache& kv, const float* qkv, int64_t m, int64_t H,
@@ -926,8 +1016,12 @@ hipError_t launch_attention(const KvCache& kv, const float* qkv, int64_t m, int6
         if ((e = stream_workspace(s, attention_workspace_bytes(kv, m, H), &ws, 2)) != hipSuccess)
             return e;
         float* qw = static_cast<float*>(ws);
-        if (D == 64) return launch_prefill_mfma_auto<64>(kv, qkv, (int)m, (int)H, qw, out, s);
-        if (D == 128) return launch_prefill_mfma_auto<128>(kv, qkv, (int)m, (int)H, qw, out, s);
+        float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + prompt_q_bytes(m, H, D));
+        const int S = prompt_split(m, H, D);
+        if (D == 64)
+            return launch_prefill_mfma_auto<64>(kv, qkv, (int)m, (int)H, qw, part, S, out, s);
+        if (D == 128)
+            return launch_prefill_mfma_auto<128>(kv, qkv, (int)m, (int)H, qw, part, S, out, s);
         return launch_prefill_attn<256, 32, 32>(kv, qkv, (int)m, (int)H, qw, out, s);
     }
     // decode: chunks sized for the known length, or for the longest the cache holds

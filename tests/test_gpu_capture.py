@@ -103,3 +103,32 @@ def test_reserved_attention_captures_and_replays():
             g.replay()
         s.synchronize()
         assert torch.equal(out, eager), i
+
+
+def test_attention_reserve_covers_every_shorter_call():
+    # Reserving for 2048 tokens covers every shorter call, though the need is not
+    # monotone in m: a 512-token prompt at 32 heads splits its key range and keeps
+    # partials (more workspace than the unsplit 2048-token call), and a 4-token decode
+    # step keeps per-chunk partials.  Both capture without growing the workspace.
+    H, KVH, D = 32, 8, 128
+    s = torch.cuda.Stream()
+    kv = KvCache(KVH, D, 2048)
+    kv.reserve(2048, H, stream=s)
+    w = (H + 2 * KVH) * D
+    for m in (512, 4):
+        x = _x(m, w, seed=40 + m)
+        out = torch.empty(m, H * D, device="cuda")
+        kv.truncate(0)
+        with torch.cuda.stream(s):
+            eager = kv.attention(x, H, stream=s).clone()
+        s.synchronize()
+        kv.truncate(0)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s, capture_error_mode="thread_local"):
+            kv.attention(x, H, out=out, stream=s)
+        kv.truncate(0)
+        with torch.cuda.stream(s):
+            g.replay()
+        s.synchronize()
+        assert torch.equal(out, eager), m
+        del g

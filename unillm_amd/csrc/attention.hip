@@ -997,14 +997,34 @@ size_t prompt_q_bytes(int64_t m, int64_t H, int64_t D) {
 }
 }  // namespace
 
-// Workspace (slot 2): the decode path's per-chunk partials at any length (at most
-// kMaxChunks chunks of (max, sum) and o[hd] per query), or the prompt path's rotated
-// queries [H][m][hd] followed, for a split call, by its S partials per query.
-size_t attention_workspace_bytes(const KvCache& kv, int64_t m, int64_t H) {
+namespace {
+// Workspace (slot 2) of one call of m tokens: the decode path's per-chunk partials at
+// any length (at most kMaxChunks chunks of (max, sum) and o[hd] per query), or the
+// prompt path's rotated queries [H][m][hd] followed, for a split call, by its S
+// partials per query.
+size_t attention_call_bytes(const KvCache& kv, int64_t m, int64_t H) {
     const int64_t G = H / std::max<int64_t>(kv.n_kv_heads, 1), D = kv.head_dim;
     if (m * G <= kAttnMaxQ) return (size_t)m * H * kMaxChunks * (2 + D) * sizeof(float);
     const int S = prompt_split(m, H, D);
     return prompt_q_bytes(m, H, D) + (S > 1 ? (size_t)m * H * S * (2 + D) * sizeof(float) : 0);
+}
+}  // namespace
+
+// Enough for every call of up to m tokens (what unillm_hip_attention_reserve grows to).
+// A call's need grows with m inside each regime -- decode, then prompts with 4, 2 and
+// 1 key splits -- but not across them (a split 512-token prompt takes more than an
+// unsplit 2048-token one), so the largest lies at the right end of a regime, clipped
+// to m.
+size_t attention_workspace_bytes(const KvCache& kv, int64_t m, int64_t H) {
+    const int64_t G = H / std::max<int64_t>(kv.n_kv_heads, 1);
+    const int64_t target = 8 * (int64_t)device_info().cu_count;  // prompt_split's two a SIMD
+    const int64_t ends[4] = {m, kAttnMaxQ / G, 32 * (target / (4 * H)), 32 * (target / (2 * H))};
+    size_t need = 0;
+    for (int64_t c : ends) {
+        c = std::min(c, m);
+        if (c >= 1) need = std::max(need, attention_call_bytes(kv, c, H));
+    }
+    return need;
 }
 
 hipError_t launch_attention(const KvCache& kv, const float* qkv, int64_t m, int64_t H,
@@ -1013,7 +1033,7 @@ hipError_t launch_attention(const KvCache& kv, const float* qkv, int64_t m, int6
     void* ws = nullptr;
     hipError_t e;
     if (m * (H / kv.n_kv_heads) > kAttnMaxQ) {
-        if ((e = stream_workspace(s, attention_workspace_bytes(kv, m, H), &ws, 2)) != hipSuccess)
+        if ((e = stream_workspace(s, attention_call_bytes(kv, m, H), &ws, 2)) != hipSuccess)
             return e;
         float* qw = static_cast<float*>(ws);
         float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + prompt_q_bytes(m, H, D));

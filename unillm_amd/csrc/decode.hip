@@ -740,8 +740,9 @@ __global__ __launch_bounds__(1024) void norm_convert_kernel(const float* __restr
     const int t = threadIdx.x, nt = blockDim.x, lane = t & 63, wv = t >> 6;
     if (blockIdx.y > 0) {  // (uniform) zero y's row r over column range blockIdx.y - 1 of Z
         const int64_t Z = gridDim.y - 1, z = blockIdx.y - 1;
+        const int64_t c0 = ny * z / Z, c1 = ny * (z + 1) / Z;
         float* yr = y + r * ny;
-        for (int64_t i = ny * z / Z + t; i < ny * (z + 1) / Z; i += nt) yr[i] = 0.0f;
+        for (int64_t i = c0 + t; i < c1; i += nt) yr[i] = 0.0f;
         return;
     }
     const float4* xr = reinterpret_cast<const float4*>(x + r * k);

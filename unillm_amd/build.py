@@ -30,7 +30,8 @@ HOST_SOURCES = ["gguf.cpp", "unillm_host.cpp"]
 HOST_LIB = os.path.join(HERE, "libunillm_host.so")
 HOST_TEST = os.path.join(os.path.dirname(HERE), "tests", "cpp", "test_host")
 # measurement infrastructure (not part of the library): the HBM streaming-ceiling probe
-PROBES = [os.path.join(HERE, "probe", p) for p in ("stream_probe", "decode_probe", "step_probe")]
+PROBES = [os.path.join(HERE, "probe", p)
+          for p in ("stream_probe", "decode_probe", "step_probe", "prefill_probe")]
 CXX = os.environ.get("CXX", "g++")
 CXXFLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
 FLAGS = [
@@ -92,8 +93,8 @@ def build_host(verbose: bool = False) -> str:
 
 def build_probe(verbose: bool = False) -> None:
     """unillm_amd/probe: the decode GEMV's streaming-ceiling probe, the batched
-    decode's weight-stream probe and the headline step's chain probe (measurement
-    only)."""
+    decode's weight-stream probe, the headline step's chain probe and the prefill
+    loop's skeleton probe (measurement only)."""
     for probe in PROBES:
         _run([HIPCC, *FLAGS, "-o", probe, probe + ".hip", "-L" + HERE, "-lunillm_hip",
               "-Wl,-rpath,$ORIGIN/.."])

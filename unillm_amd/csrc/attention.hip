@@ -1,5 +1,5 @@
 // attention.hip -- attention with a KV cache in HBM: decode steps (m H / KVH <= 16 new
-// query rows a kv head) and prompt-length calls (any m; the tiled kernel further down).
+// query rows a kv head) and prompt-length calls (any m; the tiled kernels further down).
 //
 // The cache's filled length is device state (the handle's `state`): the first kernel
 // of a call reads it and publishes it for the second, which advances it by m.  So the
@@ -428,11 +428,13 @@ int64_t chunk_len(int64_t L, int64_t KVH) {
 
 // ---- prompt-length calls (m H / KVH beyond a decode step) ---------------------------------
 //
-// Two kernels.  rope_append_kernel, a workgroup per (token t, head): q heads rotated at
-// position len + t and scaled by 1 / sqrt(hd) into the workspace qw[H][m][hd]; k heads
-// rotated and, with v, appended to the cache (the decode kernel's formulas, so either
-// path writes the same cache).  attn_prefill_kernel, a workgroup per (block of BQ
-// queries, head h): flash-style causal attention over the cache in f32 --
+// rope_append_kernel, a workgroup per (token t, head): q heads rotated at position
+// len + t and scaled by 1 / sqrt(hd) into the workspace qw[H][m][hd]; k heads rotated
+// and, with v, appended to the cache (the decode kernel's formulas, so either path
+// writes the same cache).  Then, for hd 64 and 128, attn_prefill_mfma on the f32 matrix
+// cores (further down; with its key range split, attn_merge_split_kernel after it);
+// for hd 256, attn_prefill_kernel, a workgroup per (block of BQ queries, head h):
+// flash-style causal attention over the cache in f32 --
 //   - the block's queries Q^T [hd][BQ] stay in LDS; the key positions run in tiles of BK
 //     (K^T [hd][BK] and V [BK][hd] in LDS), only up to the block's last query position;
 //   - thread (tr, tc) of 16 x 16 computes scores for rows tr RT .. and columns tc CT ..

@@ -36,17 +36,17 @@
 //     drains the ring's later stages before them; a step waits for its own
 //     stage (vmcnt in issue order) and meets the other waves at a bare
 //     s_barrier.
-// Measured limits (m2048 k4096 n14336, with parts of the work switched off in
-// copies of this kernel): the matrix cores, the dequant VALU and the LDS reads
-// hardly overlap.  Without the dequant a call takes 84 % of the time, without
-// the MFMAs 68 %, with neither 59 %, and with no global loads either (barriers
-// and LDS reads only) 40 %: each of the 8 waves reads the whole A tile from LDS,
-// 256 KB per step per CU.  A 2 x 4 grid halves those reads but dequantizes every
-// weight twice: 15-40 % slower.  On gfx950 the matrix cores and the VALU hardly
-// co-issue while the accumulators sit in arch VGPRs (a micro-benchmark: MFMA +
-// independent VALU cost the sum of both); accumulators in AGPRs (asm MFMAs)
-// overlap the two in isolation but measured 8 % slower here, the asm fixing the
-// instruction order.  The ring depth (3, 4 or 6 stages) makes no difference.
+// Measured limits (m2048 k4096 n14336).  The loop alone -- these LDS reads, the MFMAs
+// and a barrier a step, on operands already in LDS (unillm_amd/probe/prefill_probe.hip)
+// -- keeps the matrix cores 87-92 % busy.  Bringing each step's 42 KiB of operands
+// from L2 into LDS costs about a quarter of the cycles however it is done (direct
+// loads or through VGPRs, waited on or not): 68 %.  The dequant VALU does not overlap
+// the same wave's MFMAs (copies of this kernel: without the dequant a call takes
+// 86 % of the time, without the global loads 80 %, without both 75 %), and 448 tiles
+// leave the last of two rounds a quarter idle.  A 2 x 4 wave grid halves the LDS
+// reads but dequantizes every weight twice: 5-40 % slower.  MFMA accumulators in
+// AGPRs, 7-wave tiles, s_setprio around the MFMAs, reads 3 or 4 ahead and the
+// ring depth (3, 4 or 6 stages) made no difference.
 //
 // Workgroup -> tile: workgroups are dealt round-robin over the 8 XCDs, so
 // workgroup b takes tile (b % 8) * (T / 8) + b / 8 (T tiles, padded to a

@@ -252,25 +252,32 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
     const uint32_t ssrc = (uint32_t)min(n0 + 32 * wv + lane % 32, N - 1) * (uint32_t)rb +
                           (uint32_t)KB * QB;
 
-    auto issue = [&](int ks) {  // this wave's R::DMA direct loads of step ks
+    // direct load q (0 .. R::DMA - 1, in this order) of this wave's loads of step ks
+    auto issue_one = [&](int ks, int q) {
         uint8_t* st = ring + (ks % kStages) * R::STAGE;
-        // k chunks past the end (an odd KB's last step) re-read the row's last chunk: x
-        // is finite and those k have zero weights
-#pragma unroll
-        for (int q = 0; q < AQ; ++q)
+        if (q < AQ) {
+            // k chunks past the end (an odd KB's last step) re-read the row's last
+            // chunk: x is finite and those k have zero weights
             dma16(xb + arow_off[q] + min((uint32_t)ks * PBK + achunk[q], K - 8),
                   st + (wv * AQ + q) * 1024);
-        const uint32_t kb = (uint32_t)min(2 * ks + pblk, KB - 1);
-#pragma unroll
-        for (int u = 0; u < CPB / 2; ++u)
+        } else if (q < AQ + CPB / 2) {
+            const int u = q - AQ;
+            const uint32_t kb = (uint32_t)min(2 * ks + pblk, KB - 1);
             dma16(base + pcol_off[u] + kb * QB + phalf, st + R::A + wv * (CPB / 2) * 1024 + u * 1024);
-        // the step's two scales (2 ks is even: one aligned dword; an odd KB's last step
-        // reads two bytes past the scales, inside the row padding or the weight's tail slot)
-        dma4(base + ssrc + 4u * ks, st + R::A + R::BP + wv * 256);
-        // K-quants: the 256-weight group header of the step (blocks 2 ks, 2 ks + 1 share it)
-        if constexpr (R::KQ)
+        } else if (q == AQ + CPB / 2) {
+            // the step's two scales (2 ks is even: one aligned dword; an odd KB's last
+            // step reads two bytes past the scales, inside the row padding or the
+            // weight's tail slot)
+            dma4(base + ssrc + 4u * ks, st + R::A + R::BP + wv * 256);
+        } else if constexpr (R::KQ) {
+            // K-quants: the 256-weight group header of the step (blocks 2 ks, 2 ks + 1)
             dma4(base + ssrc + 2u * (uint32_t)KB + 4u * (uint32_t)(ks >> 2),
                  st + R::A + R::BP + R::BS + wv * 256);
+        }
+    };
+    auto issue = [&](int ks) {  // all of this wave's R::DMA direct loads of step ks
+#pragma unroll
+        for (int q = 0; q < R::DMA; ++q) issue_one(ks, q);
     };
 
     // ---- B fragment geometry: lane -> column 16 j + l % 16 of the wave's 32, elements
@@ -335,7 +342,10 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
         else if (j + 1 < nks) wait_vmcnt<R::DMA>();
         else wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
-        if (j + kStages - 1 < nks) issue(ks + kStages - 1);
+        // the loads of step ks + kStages - 1 are issued spread over this step's MFMAs
+        // (after fragments 0, SPC, 2 SPC, ..), not all at once: their data then reaches
+        // LDS spread over the step rather than in one burst among the fragment reads
+        const bool issue_next = j + kStages - 1 < nks;
 
         const uint32_t st = ring0 + (uint32_t)((ks % kStages) * R::STAGE);
         // B: raw bytes and scales of this wave's columns -> f16 fragments
@@ -461,6 +471,9 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
                 const int j = (i + 1) / (TI / TJ) - 1;
                 bfrag[j][1] = deq(j, 1);
             }
+            constexpr int SPC = 2 * TI / R::DMA;  // fragments between two loads
+            static_assert(SPC >= 1, "a load slot for every direct load");
+            if (issue_next && f % SPC == 0 && f / SPC < R::DMA) issue_one(ks + kStages - 1, f / SPC);
         }
     }
 

@@ -201,9 +201,9 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
     // by the RW waves of the group.  RW = 1: each weight once, all of A per wave.
     constexpr int RW = 1, CW = NW / RW;
     constexpr int WR = BM / RW;                            // rows per wave
-    constexpr int WC = PBN / CW;                           // output columns per wave (64)
+    constexpr int WC = PBN / CW;                           // output columns per wave (32)
     constexpr int TI = WR / 16;                            // MFMA tiles along m per wave
-    constexpr int TJ = WC / 16;                            // MFMA tiles along n per wave (4)
+    constexpr int TJ = WC / 16;                            // MFMA tiles along n per wave (2)
     using R = Ring<QT, BM>;
     // f16 operands: x rows in the order 0 2 1 3 4 6 5 7, each scaled by a power of
     // two undone by rs[row]; weights scaled by wscale = 2^-E, undone by oscale = 2^E

@@ -13,6 +13,9 @@
 //                 i + 1 with G workgroups while GEMV i runs (prefetch i + 1 waits
 //                 for GEMV i - 1; the GEMV chain does not wait for the prefetches
 //                 until the end of the step).
+//   empty G x B   160 launches of an empty kernel, G workgroups of B threads (the
+//                 GEMV's 256 x 1024, and two others): the graph's own cost per
+//                 dependent launch, with no work.
 // Each figure is the best of 8 rounds of 5 graph replays, per replay.
 #include <hip/hip_runtime.h>
 #include <stdio.h>
@@ -58,6 +61,11 @@ __global__ __launch_bounds__(256) void prefetch(const uint4* __restrict__ p, siz
         for (int j = 0; j < 8; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
     }
     if (acc == 0x9E3779B9u && sink) *sink = (int)acc;
+}
+
+// Does nothing; the pointer test keeps the launch from being optimized out.
+__global__ __launch_bounds__(1024) void empty(int* sink) {
+    if (sink && threadIdx.x == 1023 && blockIdx.x == 0) sink[0] = 0;
 }
 
 int main() {
@@ -172,6 +180,20 @@ int main() {
     run("prefetch 64", distinct, 64);
     run("prefetch 128", distinct, 128);
     run("distinct", distinct, 0);
+    const int grids[3][2] = {{256, 1024}, {256, 64}, {2048, 256}};
+    for (const auto& gb : grids) {
+        hipGraph_t g;
+        hipGraphExec_t ge;
+        CK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+        for (int i = 0; i < NW; ++i) empty<<<gb[0], gb[1], 0, s>>>(nullptr);
+        CK(hipStreamEndCapture(s, &g));
+        CK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+        CK(hipGraphDestroy(g));
+        const float ms = timeit(ge);
+        printf("empty %4dx%-4d %.4f ms/step  %.3f us/launch\n", gb[0], gb[1], ms, ms * 1e3 / NW);
+        fflush(stdout);
+        CK(hipGraphExecDestroy(ge));
+    }
     for (auto* q : w) CU(unillm_hip_qweight_destroy(q));
     return 0;
 }

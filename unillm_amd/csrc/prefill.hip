@@ -341,44 +341,41 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
         if (j + kStages - 2 < nks) wait_vmcnt<(kStages - 2) * R::DMA>();
         else if (j + 1 < nks) wait_vmcnt<R::DMA>();
         else wait_vmcnt<0>();
+        const uint32_t st = ring0 + (uint32_t)((ks % kStages) * R::STAGE);
+        // B: raw bytes and scales (K-quants: and group headers) of this wave's columns.
+        // They are this wave's own loads, complete after the wait above, so they are
+        // read before the barrier: the reads' latency passes while the waves meet.
+        // Raw payload of column tile j at j * 16 * 2 QB (block 1 at + QB); scales of
+        // tile j at (16 j / 32) * 256 + (16 j % 32) * 4 relative to tile 0's
+        static_assert(TJ == 2, "two column tiles");
+        constexpr int T = 16 * 2 * QB;
+        u32x2 raw[TJ][2];
+        uint32_t sc[TJ], hd[TJ];
+        asm volatile(
+            "ds_read_b64 %0, %6 offset:%c8\n ds_read_b64 %1, %6 offset:%c9\n"
+            "ds_read_b64 %2, %6 offset:%c10\n ds_read_b64 %3, %6 offset:%c11\n"
+            "ds_read_b32 %4, %7\n ds_read_b32 %5, %7 offset:64"
+            : "=&v"(raw[0][0]), "=&v"(raw[0][1]), "=&v"(raw[1][0]), "=&v"(raw[1][1]), "=&v"(sc[0]),
+              "=&v"(sc[1])
+            : "v"(st + boff0), "v"(st + soff0), "i"(0), "i"(QB), "i"(T), "i"(T + QB));
+        if constexpr (R::KQ)
+            asm volatile("ds_read_b32 %0, %2\n ds_read_b32 %1, %2 offset:64"
+                         : "=&v"(hd[0]), "=&v"(hd[1])
+                         : "v"(st + soff0 + R::BS));
         __builtin_amdgcn_s_barrier();
+        if constexpr (R::KQ)
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(raw[0][0]), "+v"(raw[0][1]), "+v"(raw[1][0]), "+v"(raw[1][1]),
+                           "+v"(sc[0]), "+v"(sc[1]), "+v"(hd[0]), "+v"(hd[1]));
+        else
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(raw[0][0]), "+v"(raw[0][1]), "+v"(raw[1][0]), "+v"(raw[1][1]),
+                           "+v"(sc[0]), "+v"(sc[1]));
         // the loads of step ks + kStages - 1 are issued spread over this step's MFMAs
         // (after fragments 0, SPC, 2 SPC, ..), not all at once: their data then reaches
         // LDS spread over the step rather than in one burst among the fragment reads
         const bool issue_next = j + kStages - 1 < nks;
 
-        const uint32_t st = ring0 + (uint32_t)((ks % kStages) * R::STAGE);
-        // B: raw bytes and scales of this wave's columns -> f16 fragments
-        u32x2 raw[TJ][2];
-        uint32_t sc[TJ];
-        // raw payload of column tile j at j * 16 * 2 QB (block 1 at + QB); scales of
-        // tile j at (16 j / 32) * 256 + (16 j % 32) * 4 relative to tile 0's
-        static_assert(TJ == 2 || TJ == 4, "two or four column tiles");
-        constexpr int T = 16 * 2 * QB;
-        if constexpr (TJ == 4) {
-            asm volatile(
-                "ds_read_b64 %0, %12 offset:%c14\n ds_read_b64 %1, %12 offset:%c15\n"
-                "ds_read_b64 %2, %12 offset:%c16\n ds_read_b64 %3, %12 offset:%c17\n"
-                "ds_read_b64 %4, %12 offset:%c18\n ds_read_b64 %5, %12 offset:%c19\n"
-                "ds_read_b64 %6, %12 offset:%c20\n ds_read_b64 %7, %12 offset:%c21\n"
-                "ds_read_b32 %8, %13\n ds_read_b32 %9, %13 offset:64\n"
-                "ds_read_b32 %10, %13 offset:256\n ds_read_b32 %11, %13 offset:320\n"
-                "s_waitcnt lgkmcnt(0)"
-                : "=&v"(raw[0][0]), "=&v"(raw[0][1]), "=&v"(raw[1][0]), "=&v"(raw[1][1]),
-                  "=&v"(raw[2][0]), "=&v"(raw[2][1]), "=&v"(raw[3][0]), "=&v"(raw[3][1]),
-                  "=&v"(sc[0]), "=&v"(sc[1]), "=&v"(sc[2]), "=&v"(sc[3])
-                : "v"(st + boff0), "v"(st + soff0), "i"(0), "i"(QB), "i"(T), "i"(T + QB),
-                  "i"(2 * T), "i"(2 * T + QB), "i"(3 * T), "i"(3 * T + QB));
-        } else {
-            asm volatile(
-                "ds_read_b64 %0, %6 offset:%c8\n ds_read_b64 %1, %6 offset:%c9\n"
-                "ds_read_b64 %2, %6 offset:%c10\n ds_read_b64 %3, %6 offset:%c11\n"
-                "ds_read_b32 %4, %7\n ds_read_b32 %5, %7 offset:64\n"
-                "s_waitcnt lgkmcnt(0)"
-                : "=&v"(raw[0][0]), "=&v"(raw[0][1]), "=&v"(raw[TJ - 1][0]),
-                  "=&v"(raw[TJ - 1][1]), "=&v"(sc[0]), "=&v"(sc[TJ - 1])
-                : "v"(st + boff0), "v"(st + soff0), "i"(0), "i"(QB), "i"(T), "i"(T + QB));
-        }
         const bool b1ok = 2 * ks + 1 < KB;
         // the f16 scales of blocks 0 (low half) and 1 (high half) of each column tile,
         // and Q4_K's offsets
@@ -395,19 +392,6 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
             // the group header (Q4_K d | dmin << 16, Q6_K d) of each column tile, laid out
             // as the scales; sc[j] holds block 0's u16 in its low half, block 1's in its
             // high: Q4_K sc | m << 8, Q6_K the int8 scales of the two 16-weight halves
-            uint32_t hd[TJ];
-            if constexpr (TJ == 4)
-                asm volatile(
-                    "ds_read_b32 %0, %4\n ds_read_b32 %1, %4 offset:64\n"
-                    "ds_read_b32 %2, %4 offset:256\n ds_read_b32 %3, %4 offset:320\n"
-                    "s_waitcnt lgkmcnt(0)"
-                    : "=&v"(hd[0]), "=&v"(hd[1]), "=&v"(hd[2]), "=&v"(hd[3])
-                    : "v"(st + soff0 + R::BS));
-            else
-                asm volatile("ds_read_b32 %0, %2\n ds_read_b32 %1, %2 offset:64\n"
-                             "s_waitcnt lgkmcnt(0)"
-                             : "=&v"(hd[0]), "=&v"(hd[TJ - 1])
-                             : "v"(st + soff0 + R::BS));
 #pragma unroll
             for (int j = 0; j < TJ; ++j) {
                 const float dd =

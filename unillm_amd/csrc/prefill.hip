@@ -46,7 +46,9 @@
 // leave the last of two rounds a quarter idle.  A 2 x 4 wave grid halves the LDS
 // reads but dequantizes every weight twice: 5-40 % slower.  MFMA accumulators in
 // AGPRs, 7-wave tiles, s_setprio around the MFMAs, reads 3 or 4 ahead and the
-// ring depth (3, 4 or 6 stages) made no difference.
+// ring depth (3, 4 or 6 stages) made no difference.  Reading and dequantizing the
+// next step's B during this step's MFMAs, so that a step starts straight into them,
+// was 4-13 % slower (with the reads' wait deferred as well).
 //
 // Workgroup -> tile: workgroups are dealt round-robin over the 8 XCDs, so
 // workgroup b takes tile (b % 8) * (T / 8) + b / 8 (T tiles, padded to a

@@ -48,7 +48,10 @@
 // AGPRs, 7-wave tiles, s_setprio around the MFMAs, reads 3 or 4 ahead and the
 // ring depth (3, 4 or 6 stages) made no difference.  Reading and dequantizing the
 // next step's B during this step's MFMAs, so that a step starts straight into them,
-// was 4-13 % slower (with the reads' wait deferred as well).
+// was 4-13 % slower (with the reads' wait deferred as well).  Dealing the tiles' k
+// steps evenly over the CUs (1.75 tiles each at 448 tiles, split tiles summed from
+// partial slots) gained nothing even with the cheapest slot exchange: with every
+// CU busy each tile runs slower by about what the idle quarter round cost.
 //
 // Workgroup -> tile: workgroups are dealt round-robin over the 8 XCDs, so
 // workgroup b takes tile (b % 8) * (T / 8) + b / 8 (T tiles, padded to a

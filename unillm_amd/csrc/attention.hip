@@ -334,28 +334,38 @@ template <int D>
 __global__ __launch_bounds__(D) void attn_merge_kernel(const float* __restrict__ part, int m,
                                                        int H, int chunks, float* __restrict__ out,
                                                        int* __restrict__ state, int max_seq) {
-    extern __shared__ float wts[];  // [chunks]
+    extern __shared__ float wts[];  // [chunks] weights, then [chunks] the chunks' sums
     const int th = blockIdx.x;      // t H + h
     const int tid = threadIdx.x, lane = tid & 63;
+    const float2* pq = reinterpret_cast<const float2*>(part) + (int64_t)th * chunks;
+    const float* po = part + (int64_t)m * H * chunks * 2 + (int64_t)th * chunks * D + tid;
+    // every load that needs no other is requested at once, before the length is
+    // checked: the length, the first 64 chunks' (max, sum) and the first 32 chunks'
+    // o[d] (the o loads do not depend on the weights, so they overlap the (max, sum)
+    // pass)
     const int len = state[2];
+    float2 v0 = make_float2(-INFINITY, 0.0f);
+    if (tid < 64 && lane < chunks) v0 = pq[lane];
+    float ov[32];
+#pragma unroll
+    for (int u = 0; u < 32; ++u) ov[u] = po[(int64_t)min(u, chunks - 1) * D];
     if (len + m > max_seq) {
         out[(int64_t)th * D + tid] = __builtin_nanf("");
         if (th == 0 && tid == 0) state[1] = 1;
         return;
     }
     if (th == 0 && tid == 0) state[0] = len + m;
-    const float2* pq = reinterpret_cast<const float2*>(part) + (int64_t)th * chunks;
-    const float* po = part + (int64_t)m * H * chunks * 2 + (int64_t)th * chunks * D + tid;
-    // the first 32 chunks' o[d] are requested before the weights exist (they do not
-    // depend on them), so their loads overlap the (max, sum) pass
-    float ov[32];
-#pragma unroll
-    for (int u = 0; u < 32; ++u) ov[u] = po[(int64_t)min(u, chunks - 1) * D];
     if (tid < 64) {
-        float M = -INFINITY;
-        for (int cc = lane; cc < chunks; cc += 64) {
+        float* sy = wts + chunks;
+        float M = v0.x;
+        if (lane < chunks) {
+            wts[lane] = v0.x;
+            sy[lane] = v0.y;
+        }
+        for (int cc = lane + 64; cc < chunks; cc += 64) {
             const float2 v = pq[cc];
             wts[cc] = v.x;
+            sy[cc] = v.y;
             M = fmaxf(M, v.x);
         }
         M = wave_max(M);
@@ -364,7 +374,7 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(const float* __restrict__
             const float mc = wts[cc];
             const float f = M == -INFINITY || mc == -INFINITY ? 0.0f : expf(mc - M);
             wts[cc] = f;
-            S = fmaf(pq[cc].y, f, S);
+            S = fmaf(sy[cc], f, S);
         }
         S = wave_add(S);
         for (int cc = lane; cc < chunks; cc += 64) wts[cc] /= S;
@@ -397,7 +407,7 @@ hipError_t launch_d_q(const KvCache& kv, const float* qkv, int m, int H, int C, 
         kv.k, kv.v, (int)kv.max_seq, part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    attn_merge_kernel<D><<<(unsigned)(m * H), D, sizeof(float) * (size_t)chunks, s>>>(
+    attn_merge_kernel<D><<<(unsigned)(m * H), D, sizeof(float) * 2 * (size_t)chunks, s>>>(
         part, m, H, chunks, out, kv.state, (int)kv.max_seq);
     return hipGetLastError();
 }

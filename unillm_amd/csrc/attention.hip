@@ -103,10 +103,39 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(
     const int g = blockIdx.x, c = blockIdx.y;
     const int G = H / KVH, Q = m * G;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const float* kg = kc + (int64_t)g * max_seq * D;
+    const float* vg = vc + (int64_t)g * max_seq * D;
+
+    // score pass: group sg = tid / LP takes positions j0 + sg + SG u (+ UK SG per
+    // iteration), lane l8 = tid % LP dimensions 8 l8 .. 8 l8 + 7; p v pass: group
+    // pg = tid / D4 takes positions j0 + pg + NG u (+ UV NG per iteration), column
+    // c4 = tid % D4.  Cached positions (< len) come from HBM, requested one iteration
+    // ahead.  The first iteration's k and v are requested before anything else, the
+    // length included: rows clamped into the cache, and a row at or past the filled
+    // length is never used (new positions are read from LDS, positions past the
+    // chunk's end are masked), so the length's latency and theirs overlap.
+    constexpr int UK = QB >= 8 ? 2 : 4, UV = QB >= 8 ? 4 : 8;
+    const int sg = tid / LP, l8 = tid % LP;
+    const int pg = tid / D4, c4 = tid % D4;
+    const int j0 = c * C;
+    float kA[UK][8], kB[UK][8];
+    float4 vA[UV], vB[UV];
+#pragma unroll
+    for (int u = 0; u < UK; ++u) {
+        const float* src = kg + (int64_t)min(j0 + sg + u * SG, max_seq - 1) * D + 8 * l8;
+        const float4 a = *reinterpret_cast<const float4*>(src);
+        const float4 b = *reinterpret_cast<const float4*>(src + 4);
+        kA[u][0] = a.x; kA[u][1] = a.y; kA[u][2] = a.z; kA[u][3] = a.w;
+        kA[u][4] = b.x; kA[u][5] = b.y; kA[u][6] = b.z; kA[u][7] = b.w;
+    }
+#pragma unroll
+    for (int u = 0; u < UV; ++u)
+        vA[u] = *reinterpret_cast<const float4*>(vg + (int64_t)min(j0 + pg + u * NG, max_seq - 1) * D +
+                                                 4 * c4);
     const int len = state[0];
     if (g == 0 && c == 0 && tid == 0) state[2] = len;
     if (len + m > max_seq) return;  // overflow: nothing appended; the merge reports it
-    const int j0 = c * C, j1 = min(j0 + C, len + m);
+    const int j1 = min(j0 + C, len + m);
     const int n = j1 - j0;
     if (n <= 0) {  // a chunk past the filled positions (a grid sized for max_seq): empty
         float* ms = part;
@@ -128,18 +157,6 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(
     float* sp = nv + m * D;
     float* red = sp + QB * C;
     float* stat = red + 4 * QB * D;
-    const float* kg = kc + (int64_t)g * max_seq * D;
-    const float* vg = vc + (int64_t)g * max_seq * D;
-
-    // score pass: group sg = tid / LP takes positions j0 + sg + SG u (+ UK SG per
-    // iteration), lane l8 = tid % LP dimensions 8 l8 .. 8 l8 + 7; p v pass: group
-    // pg = tid / D4 takes positions j0 + pg + NG u (+ UV NG per iteration), column
-    // c4 = tid % D4.  Cached positions (< len) come from HBM, requested one iteration
-    // ahead; the first iteration's k and v are requested before anything else, with
-    // the queries.  Positions >= len (new in this call) are read from LDS at use.
-    constexpr int UK = QB >= 8 ? 2 : 4, UV = QB >= 8 ? 4 : 8;
-    const int sg = tid / LP, l8 = tid % LP;
-    const int pg = tid / D4, c4 = tid % D4;
     const int nit_k = (n + UK * SG - 1) / (UK * SG), nit_v = (n + UV * NG - 1) / (UV * NG);
     auto load_k = [&](float (&kr)[UK][8], int it) {
 #pragma unroll
@@ -159,10 +176,6 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(
             vr[u] = *reinterpret_cast<const float4*>(vg + (int64_t)(j < len ? j : 0) * D + 4 * c4);
         }
     };
-    float kA[UK][8], kB[UK][8];
-    float4 vA[UV], vB[UV];
-    load_k(kA, 0);
-    load_v(vA, 0);
 
     // 1. rotated, scaled queries
     for (int i = tid; i < Q * HALF; i += kThreads) {

@@ -251,6 +251,9 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(
             }
         }
     }
+    // the p v pass's second iteration, requested now (the k registers are free) so
+    // its latency passes during the softmax
+    if (nit_v > 1) load_v(vB, 1);
     __syncthreads();
 
     // 4. per query: the chunk's max, exponentials and their sum (a wave per query)
@@ -296,7 +299,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(
             }
         };
         for (int it = 0; it < nit_v; it += 2) {
-            if (it + 1 < nit_v) load_v(vB, it + 1);
+            if (it > 0 && it + 1 < nit_v) load_v(vB, it + 1);
             accumulate(vA, it);
             if (it + 1 < nit_v) {
                 if (it + 2 < nit_v) load_v(vA, it + 2);

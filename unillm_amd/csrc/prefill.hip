@@ -78,10 +78,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int PBN = 256;         // output columns per workgroup
 constexpr int PBK = 64;          // k per step (two blocks)
-#ifndef PREFILL_WAVES
-#define PREFILL_WAVES 8
-#endif
-constexpr int kWaves = PREFILL_WAVES;  // waves per workgroup (8: two per SIMD)
+constexpr int kWaves = 8;        // waves per workgroup (two per SIMD)
 
 __device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
     uint32_t r;  // round to nearest even, lo in the low half

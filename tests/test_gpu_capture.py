@@ -68,8 +68,10 @@ def test_reserved_stream_captures_and_replays(m, path):
         with torch.cuda.stream(s):
             g.replay()
         s.synchronize()
-        # split k ranges meet by f32 atomics: equal up to their order
-        assert oracle.normwise_error(y.cpu().numpy(), eager.cpu().numpy()) < 1e-6, i
+        if path == PATH_PREFILL_MFMA:  # split k slabs summed in a fixed order: exact
+            assert np.array_equal(y.cpu().numpy(), eager.cpu().numpy()), i
+        else:  # batched decode: split k ranges meet by f32 atomics, in any order
+            assert oracle.normwise_error(y.cpu().numpy(), eager.cpu().numpy()) < 1e-6, i
         # eager work between replays; the second one grows the stream's workspace
         # (the captured buffer is retired, not freed, so the graph stays valid)
         with torch.cuda.stream(s):

@@ -5,8 +5,8 @@ MFMA paths' f16 copy of x in the library's fixed per-GPU scratch instead of the
 stream's workspace.  Each case makes two calls in a row on one weight, the second
 with fewer rows (the scratch keeps the first call's contents), and compares each
 with unillm_hip_qmatmul on the same input: bit for bit where every output is
-summed in one fixed order (GEMV, prefill without a k split), to f32 rounding
-where split k ranges meet by atomic adds.  Both also meet the oracle's 1e-3.
+summed in one fixed order (GEMV, prefill), to f32 rounding where the batched
+decode's split k ranges meet by atomic adds.  Both also meet the oracle's 1e-3.
 """
 import ctypes
 
@@ -38,7 +38,7 @@ CASES = [
     (Q4_0, 14336, 4096, 64, 16, PATH_DECODE_MFMA, False),
     (Q8_0, 4096, 11008, 33, 5, PATH_DECODE_MFMA, False),
     (Q4_0, 14336, 4096, 2048, 512, PATH_PREFILL_MFMA, True),
-    (Q4_0, 4096, 14336, 700, 130, PATH_PREFILL_MFMA, False),
+    (Q4_0, 4096, 14336, 700, 130, PATH_PREFILL_MFMA, True),
 ]
 
 

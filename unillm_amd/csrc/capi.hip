@@ -398,7 +398,7 @@ int qmatmul_impl(const unillm_qweight* w, const float* x_dev, int64_t m, float* 
             return fail(UNILLM_ERR_INVALID_ARG,
                         what + ": the no-allocation entry point takes x 16-byte aligned");
         const size_t need = path == UNILLM_PATH_DECODE_MFMA    ? decode_workspace_bytes(*w, m)
-                            : path == UNILLM_PATH_PREFILL_MFMA ? prefill_workspace_bytes(*w, m)
+                            : path == UNILLM_PATH_PREFILL_MFMA ? prefill_call_bytes(*w, m)
                                                                : 0;
         if (need > fixed_bytes)
             return fail(UNILLM_ERR_UNSUPPORTED,

@@ -670,14 +670,13 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
 
 // x[m, k] -> f16 rows in the fragment order (each aligned 8 as 0 2 1 3 4 6 5 7),
 // each row scaled by its power of two (f16_row_scale; the factor to undo it in
-// rs[row]); y row zeroed over [0, yn) when yn > 0 (a split k adds into it).  One
-// workgroup per row (64 .. 1024 threads, two groups of 8 a thread where the row
+// rs[row]).  One workgroup per row (64 .. 1024 threads, two groups of 8 a thread where the row
 // allows), one HBM read: a thread keeps its first two groups in registers (rows up
 // to 16384 elements); a longer row's further groups are read again for the
 // conversion.
 __global__ __launch_bounds__(1024) void xrows_kernel(const float* __restrict__ x, int64_t k,
-                                                     uint4* __restrict__ xh, float* __restrict__ rs,
-                                                     float* __restrict__ y, int64_t yn) {
+                                                     uint4* __restrict__ xh,
+                                                     float* __restrict__ rs) {
     __shared__ float red[16];
     const int64_t r = blockIdx.x, g8 = k / 8;
     const int t = threadIdx.x, nt = blockDim.x;
@@ -714,7 +713,6 @@ __global__ __launch_bounds__(1024) void xrows_kernel(const float* __restrict__ x
     for (int j = 0; j < 2; ++j)
         if (t + nt * j < g8) put(t + nt * j, a[j], b[j]);
     for (int64_t i = t + 2 * nt; i < g8; i += nt) put(i, xr[2 * i], xr[2 * i + 1]);
-    for (int64_t i = t; i < yn; i += nt) y[r * yn + i] = 0.0f;
 }
 
 // One workgroup per row r of x: the row's layer norm (two passes for the mean and
@@ -882,11 +880,11 @@ hipError_t launch_norm_convert(const float* x, int64_t m, int64_t k, const NormA
 }
 
 hipError_t launch_x_to_f16_rows(const float* x, int64_t m, int64_t k, void* out, float* rs,
-                                float* y, int64_t yn, hipStream_t s) {
+                                hipStream_t s) {
     if (m <= 0) return hipSuccess;
     // two groups of 8 a thread, whole waves, 64 .. 1024 threads
     const int nt = (int)std::min<int64_t>(1024, std::max<int64_t>(64, (k / 16 + 63) / 64 * 64));
-    xrows_kernel<<<(unsigned)m, nt, 0, s>>>(x, k, static_cast<uint4*>(out), rs, y, yn);
+    xrows_kernel<<<(unsigned)m, nt, 0, s>>>(x, k, static_cast<uint4*>(out), rs);
     return hipGetLastError();
 }
 

@@ -171,8 +171,8 @@ hipError_t launch_quantize(int qtype, const float* w, int64_t n, int64_t k, uint
 hipError_t launch_gemv(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t s,
                        int epi = kEpiStore, const NormArgs& norm = NormArgs{nullptr, nullptr, 0.f});
 // The MFMA paths take their x operand buffer from `ws` when it is given (at least
-// decode_workspace_bytes / prefill_workspace_bytes for this w and m), else from
-// the stream's workspace (slot 0).
+// decode_workspace_bytes / prefill_call_bytes for this w and m), else from the
+// stream's workspace (slot 0).
 hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float* y,
                               hipStream_t s, int epi = kEpiStore,
                               const NormArgs& norm = NormArgs{nullptr, nullptr, 0.f},
@@ -182,6 +182,9 @@ hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, floa
                                const NormArgs& norm = NormArgs{nullptr, nullptr, 0.f},
                                void* ws = nullptr);
 size_t decode_workspace_bytes(const QWeight& w, int64_t m);
+// The prefill's workspace: this call's own need, and a bound for every call of up
+// to m rows (the size a reserve takes).
+size_t prefill_call_bytes(const QWeight& w, int64_t m);
 size_t prefill_workspace_bytes(const QWeight& w, int64_t m);
 // Both MFMA paths address weight bytes with 32-bit offsets: weights under 4 GiB.
 inline bool mfma_supports(const QWeight& w) {
@@ -197,10 +200,10 @@ hipError_t launch_norm_convert(const float* x, int64_t m, int64_t k, const NormA
 // x[m, k] (k % 32 == 0) -> f16 rows (round to nearest even) in the decode kernel's
 // element order (each aligned 8 as 0 2 1 3 4 6 5 7), each row scaled by a power
 // of two that puts its largest magnitude in [2^14, 2^15); rs[row] <- the factor
-// that undoes it.  y row r zeroed over [0, yn) when yn > 0.  launch_norm_convert
-// with rs != nullptr (f16) scales its rows the same way.
+// that undoes it.  launch_norm_convert with rs != nullptr (f16) scales its rows the
+// same way.
 hipError_t launch_x_to_f16_rows(const float* x, int64_t m, int64_t k, void* out, float* rs,
-                                float* y, int64_t yn, hipStream_t s);
+                                hipStream_t s);
 // act[m, I] = silu(g[m, i]) * u[m, i] with g, u the two halves of each row of
 // gu[m, 2 I] (the SwiGLU of the MFMA paths, after their store)
 hipError_t launch_swiglu(const float* gu, int64_t m, int64_t I, float* act, hipStream_t s);

@@ -195,7 +195,8 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
                                                               int KB, int tiles_n, int tiles,
                                                               int units_pad, int S, int add,
                                                               float wscale, float oscale,
-                                                              const float* __restrict__ rs) {
+                                                              const float* __restrict__ rs,
+                                                              float* __restrict__ part) {
     static_assert(NW == 8, "the ring's load split assumes 8 waves");
     constexpr int QB = Ring<QT, BM>::QB;  // payload bytes per block
     // waves: RW row groups x CW column groups; wave (rw, cw) owns rows BM / RW * rw ..
@@ -463,10 +464,26 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
         }
     }
 
-    // ---- epilogue: lane holds C[4 (l / 16) + e][l % 16] of each 16 x 16 tile; the
-    // S k slices of a tile meet in y by f32 atomic adds onto zeros.  f16 operands: the
-    // output factor of row 16 i + 4 g + e is oscale times its row scale (from LDS:
-    // global loads here would wait for the stores before them) ----
+    // ---- epilogue: lane holds C[4 (l / 16) + e][l % 16] of each 16 x 16 tile.  One
+    // k slice (S = 1): f16 operands, so the output factor of row 16 i + 4 g + e is
+    // oscale times its row scale (from LDS: global loads here would wait for the
+    // stores before them).  S slices: each stores its raw sums to its slab of `part`
+    // ([S][M][N]); split_sum_kernel adds the slabs in slice order and scales them ----
+    if (S > 1) {
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int col = n0 + WC * cw + 16 * j + fr;
+            if (col >= N) continue;
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int row = m0 + WR * rw + 16 * i + 4 * g + e;
+                    if (row < M) part[((int64_t)sp * M + row) * N + col] = acc[i][j][e];
+                }
+        }
+        return;
+    }
     float4 rsc[TI];
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
@@ -487,22 +504,56 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
                 float* dst = y + (int64_t)row * N + col;
                 const float v =
                     acc[i][j][e] * (e == 0 ? rsc[i].x : e == 1 ? rsc[i].y : e == 2 ? rsc[i].z : rsc[i].w);
-                if (S == 1) *dst = add ? *dst + v : v;
-                else unsafeAtomicAdd(dst, v);  // onto zeros, or onto y with add
+                *dst = add ? *dst + v : v;
             }
     }
 }
 
+// y[r, c] (+)= (sum over the S slabs of part[s][r][c], in slice order) * rs[r] * oscale:
+// the k slices of a split prefill, in a fixed order (the result does not depend on
+// which slice finished first).  Four columns a thread when vec (n % 4 == 0 and y on
+// a 16-byte boundary).
+__global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict__ part, int S,
+                                                        int64_t M, int64_t N,
+                                                        const float* __restrict__ rs,
+                                                        float oscale, int add, int vec,
+                                                        float* __restrict__ y) {
+    const int64_t MN = M * N;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    if (vec) {
+        for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < MN / 4; q += stride) {
+            f32x4 v = *reinterpret_cast<const f32x4*>(part + 4 * q);
+            for (int sl = 1; sl < S; ++sl)
+                v += *reinterpret_cast<const f32x4*>(part + sl * MN + 4 * q);
+            v *= rs[4 * q / N] * oscale;
+            f32x4* dst = reinterpret_cast<f32x4*>(y + 4 * q);
+            *dst = add ? *dst + v : v;
+        }
+        return;
+    }
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < MN; i += stride) {
+        float v = part[i];
+        for (int sl = 1; sl < S; ++sl) v += part[sl * MN + i];
+        v *= rs[i / N] * oscale;
+        y[i] = add ? y[i] + v : v;
+    }
+}
+
+// x is addressed with 32-bit element offsets: a launch takes at most this many rows
+int64_t prefill_chunk_rows(int64_t k, int bm) {
+    return std::max<int64_t>(bm, ((int64_t)1 << 30) / k / bm * bm);
+}
+
 template <int QT, int BM>
 hipError_t launch_bm(const QWeight& w, const uint16_t* xb, const float* rs, int64_t m, float* y,
-                     int S, hipStream_t s, int add) {
-    // x is addressed with 32-bit element offsets: launch in row chunks below 2^30 elements
-    const int64_t chunk = std::max<int64_t>(BM, ((int64_t)1 << 30) / w.k / BM * BM);
-    if (m > chunk) {
+                     int S, float* part, hipStream_t s, int add) {
+    const int64_t chunk = prefill_chunk_rows(w.k, BM);
+    if (m > chunk) {  // row chunks below 2^30 elements (the plan never splits k here)
+        if (S != 1) return hipErrorInvalidValue;
         for (int64_t r = 0; r < m; r += chunk) {
             hipError_t e =
                 launch_bm<QT, BM>(w, xb + r * w.k, rs ? rs + r : nullptr, std::min(chunk, m - r),
-                                  y + r * w.n, S, s, add);
+                                  y + r * w.n, 1, nullptr, s, add);
             if (e != hipSuccess) return e;
         }
         return hipSuccess;
@@ -520,17 +571,26 @@ hipError_t launch_bm(const QWeight& w, const uint16_t* xb, const float* rs, int6
     const float wscale = ldexpf(1.0f, -w.f16_exp), oscale = ldexpf(1.0f, w.f16_exp);
     prefill_kernel<QT, BM, kWaves><<<units_pad, kWaves * 64, Ring<QT, BM>::BYTES, s>>>(
         w.base, w.row_bytes, xb, y, (int)m, (int)w.n, (int)w.kb, tiles_n, tiles, units_pad, S,
-        add, wscale, oscale, rs);
+        add, wscale, oscale, rs, part);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || S == 1) return e;
+    const int vec = w.n % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
+    const int64_t q = m * w.n / (vec ? 4 : 1);
+    const int blocks = (int)std::min<int64_t>((q + 255) / 256, 8 * device_info().cu_count);
+    split_sum_kernel<<<blocks, 256, 0, s>>>(part, S, m, w.n, rs, oscale, add, vec, y);
     return hipGetLastError();
 }
 
 // Tile rows and k split.  256-row tiles when they give at least one tile per CU,
 // else 128-row tiles; when even those leave most CUs idle (a short, deep
 // product), the k steps are split over up to 4 workgroups per tile, at least
-// 16 steps each.  Calls beyond the 32-bit x offsets (chunked) never split.
+// 16 steps each, whose raw sums meet in split_sum_kernel (slabs of the stream's
+// workspace).  Calls beyond the 32-bit x offsets (chunked) never split.
 struct PrefillPlan {
     int bm, S;
 };
+// the most tiles that still count as leaving most CUs idle
+int64_t split_tiles_max() { return (device_info().cu_count - 1) / 2; }
 PrefillPlan prefill_plan(const QWeight& w, int64_t m) {
     const int64_t cus = device_info().cu_count;
     const int64_t tiles_n = (w.n + PBN - 1) / PBN;
@@ -538,15 +598,31 @@ PrefillPlan prefill_plan(const QWeight& w, int64_t m) {
     const int64_t tiles = (m + 127) / 128 * tiles_n;
     const int64_t ksteps = (w.kb + 1) / 2;
     int64_t S = 1;
-    if (2 * tiles < cus && m * w.k < ((int64_t)1 << 30))
+    if (tiles <= split_tiles_max() && m <= prefill_chunk_rows(w.k, 128))
         S = std::max<int64_t>(1, std::min<int64_t>({4, cus / tiles, ksteps / 16}));
     return {128, (int)S};
 }
 
+size_t up256(size_t b) { return (b + 255) / 256 * 256; }
+
 }  // namespace
 
+// Workspace: x as f16 rows | their scales | the split slabs ([S][m][n] f32).  The
+// call's own need, and a bound for every m' <= m (the slabs of 4 slices of the
+// largest m' that can split), so that a reserve for m covers every shorter call.
+size_t prefill_call_bytes(const QWeight& w, int64_t m) {
+    const PrefillPlan plan = prefill_plan(w, m);
+    const size_t slabs = plan.S > 1 ? (size_t)plan.S * m * w.n * sizeof(float) : 0;
+    return up256((size_t)m * (size_t)w.k * 2) + up256((size_t)m * sizeof(float)) + slabs;
+}
+
 size_t prefill_workspace_bytes(const QWeight& w, int64_t m) {
-    return ((size_t)m * (size_t)w.k * 2 + 255) / 256 * 256 + (size_t)m * sizeof(float);
+    const int64_t tiles_n = (w.n + PBN - 1) / PBN;
+    int64_t msplit = std::min<int64_t>(128 * (split_tiles_max() / tiles_n),
+                                       prefill_chunk_rows(w.k, 128));
+    if ((w.kb + 1) / 2 < 32) msplit = 0;  // fewer than 2 x 16 k steps: never split
+    const size_t slabs = (size_t)4 * std::min(m, msplit) * w.n * sizeof(float);
+    return up256((size_t)m * (size_t)w.k * 2) + up256((size_t)m * sizeof(float)) + slabs;
 }
 
 hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, float* y,
@@ -555,31 +631,32 @@ hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, floa
     if (!mfma_supports(w)) return hipErrorInvalidValue;
     // x as f16 rows with their power-of-two scales in the workspace: the GEMM
     // re-reads x once per 256-column tile, so it reads half the bytes, and no
-    // conversion sits in its inner loop.  The conversion zeroes y for a split k.
+    // conversion sits in its inner loop.  A split k's slabs follow.
     const PrefillPlan plan = prefill_plan(w, m);
-    const size_t xbytes = ((size_t)m * (size_t)w.k * 2 + 255) / 256 * 256;
+    const size_t xbytes = up256((size_t)m * (size_t)w.k * 2);
     hipError_t e = hipSuccess;
-    if (!ws && (e = stream_workspace(s, prefill_workspace_bytes(w, m), &ws)) != hipSuccess)
-        return e;
+    if (!ws && (e = stream_workspace(s, prefill_call_bytes(w, m), &ws)) != hipSuccess) return e;
     float* rs = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + xbytes);
+    float* part =
+        plan.S > 1 ? reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + xbytes +
+                                              up256((size_t)m * sizeof(float)))
+                   : nullptr;
     const int add = epi == kEpiAdd;
-    const int64_t yn = plan.S > 1 && !add ? w.n : 0;
-    e = norm.gamma ? launch_norm_convert(x, m, w.k, norm, ws, y, yn, s, rs)
-                   : launch_x_to_f16_rows(x, m, w.k, ws, rs, y, yn, s);
+    e = norm.gamma ? launch_norm_convert(x, m, w.k, norm, ws, y, 0, s, rs)
+                   : launch_x_to_f16_rows(x, m, w.k, ws, rs, s);
     if (e != hipSuccess) return e;
     const uint16_t* xb = static_cast<const uint16_t*>(ws);
-    if (w.qtype == UNILLM_QTYPE_Q4_K)
-        return plan.bm == 256 ? launch_bm<UNILLM_QTYPE_Q4_K, 256>(w, xb, rs, m, y, 1, s, add)
-                              : launch_bm<UNILLM_QTYPE_Q4_K, 128>(w, xb, rs, m, y, plan.S, s, add);
-    if (w.qtype == UNILLM_QTYPE_Q6_K)
-        return plan.bm == 256 ? launch_bm<UNILLM_QTYPE_Q6_K, 256>(w, xb, rs, m, y, 1, s, add)
-                              : launch_bm<UNILLM_QTYPE_Q6_K, 128>(w, xb, rs, m, y, plan.S, s, add);
-    const bool q4 = w.qtype == UNILLM_QTYPE_Q4_0;
-    if (plan.bm == 256)
-        return q4 ? launch_bm<UNILLM_QTYPE_Q4_0, 256>(w, xb, rs, m, y, 1, s, add)
-                  : launch_bm<UNILLM_QTYPE_Q8_0, 256>(w, xb, rs, m, y, 1, s, add);
-    return q4 ? launch_bm<UNILLM_QTYPE_Q4_0, 128>(w, xb, rs, m, y, plan.S, s, add)
-              : launch_bm<UNILLM_QTYPE_Q8_0, 128>(w, xb, rs, m, y, plan.S, s, add);
+#define UNILLM_PREFILL_LAUNCH(QTYPE)                                                          \
+    return plan.bm == 256 ? launch_bm<QTYPE, 256>(w, xb, rs, m, y, 1, nullptr, s, add)       \
+                          : launch_bm<QTYPE, 128>(w, xb, rs, m, y, plan.S, part, s, add)
+    switch (w.qtype) {
+        case UNILLM_QTYPE_Q4_0: UNILLM_PREFILL_LAUNCH(UNILLM_QTYPE_Q4_0);
+        case UNILLM_QTYPE_Q8_0: UNILLM_PREFILL_LAUNCH(UNILLM_QTYPE_Q8_0);
+        case UNILLM_QTYPE_Q4_K: UNILLM_PREFILL_LAUNCH(UNILLM_QTYPE_Q4_K);
+        case UNILLM_QTYPE_Q6_K: UNILLM_PREFILL_LAUNCH(UNILLM_QTYPE_Q6_K);
+        default: return hipErrorInvalidValue;
+    }
+#undef UNILLM_PREFILL_LAUNCH
 }
 
 }  // namespace unillm

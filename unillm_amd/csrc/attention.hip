@@ -114,11 +114,12 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(
     // length included: rows clamped into the cache, and a row at or past the filled
     // length is never used (new positions are read from LDS, positions past the
     // chunk's end are masked), so the length's latency and theirs overlap.
-    // positions a thread per iteration: one query a kv head (QB = 1) takes the shallow
-    // loop (100 VGPRs, five waves a SIMD): a 32-position chunk is one iteration with no
-    // clamped repeats, and the whole Llama-2-7B decode step ran 1 % faster at L 1024 and
-    // L 4096 (KV from HBM); deeper loops (4 / 8, 8 / 16) were 8-20 % slower at L 1024
-    constexpr int UK = QB >= 8 || QB == 1 ? 2 : 4, UV = QB >= 8 || QB == 1 ? 4 : 8;
+    // positions a thread per iteration, 2 of k and 4 of v: the registers leave room for
+    // more waves (one query a kv head: 100 VGPRs, five waves a SIMD), and a 32-position
+    // chunk is one iteration with no clamped repeats.  Against 4 / 8: the whole
+    // Llama-2-7B decode step 1 % faster at L 1024 and L 4096 (KV from HBM), GQA 32/8
+    // calls 7-10 % faster; deeper loops (8 / 16) were 8-20 % slower at L 1024
+    constexpr int UK = 2, UV = 4;
     const int sg = tid / LP, l8 = tid % LP;
     const int pg = tid / D4, c4 = tid % D4;
     const int j0 = c * C;

@@ -31,7 +31,9 @@ def _call(fn, ql, x, n, stream):
     return y
 
 
-# (qtype, n, k, first m, second m, path both calls take, exact)
+# (qtype, n, k, first m, second m, path both calls take, exact).  Not exact: the
+# batched decode's split k meets by atomics; a prefill whose k split does not fit
+# the scratch runs unsplit there, so the two agree to f32 rounding.
 CASES = [
     (Q4_0, 4096, 4096, 4, 1, PATH_GEMV, True),
     (Q8_0, 5632, 2048, 2, 1, PATH_GEMV, True),
@@ -39,6 +41,9 @@ CASES = [
     (Q8_0, 4096, 11008, 33, 5, PATH_DECODE_MFMA, False),
     (Q4_0, 14336, 4096, 2048, 512, PATH_PREFILL_MFMA, True),
     (Q4_0, 4096, 14336, 700, 130, PATH_PREFILL_MFMA, True),
+    # the library call splits k over 256-row tiles, whose slabs do not fit the
+    # scratch beside x: the no-allocation call runs the tiles unsplit
+    (Q4_0, 4096, 14336, 2048, 1100, PATH_PREFILL_MFMA, False),
 ]
 
 
@@ -62,7 +67,8 @@ def test_noalloc_matches_qmatmul_twice(qtype, n, k, m1, m2, path, exact):
         if exact:
             assert np.array_equal(a, b), (call, m)
         else:
-            assert oracle.normwise_error(a, b) < 1e-6, (call, m)
+            # the same k steps grouped differently in f32: ~1e-6 at these k
+            assert oracle.normwise_error(a, b) < 1e-5, (call, m)
         rows = np.arange(m) if m <= 64 else np.array([0, 1, m // 2, m - 1])
         ref = oracle.qmatmul_f64(qtype, blocks, xh[rows], n, k)
         assert oracle.normwise_error(a[rows], ref) < 1e-3, (call, m)

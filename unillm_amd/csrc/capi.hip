@@ -398,7 +398,7 @@ int qmatmul_impl(const unillm_qweight* w, const float* x_dev, int64_t m, float* 
             return fail(UNILLM_ERR_INVALID_ARG,
                         what + ": the no-allocation entry point takes x 16-byte aligned");
         const size_t need = path == UNILLM_PATH_DECODE_MFMA    ? decode_workspace_bytes(*w, m)
-                            : path == UNILLM_PATH_PREFILL_MFMA ? prefill_call_bytes(*w, m)
+                            : path == UNILLM_PATH_PREFILL_MFMA ? prefill_call_bytes(*w, m, fixed_bytes)
                                                                : 0;
         if (need > fixed_bytes)
             return fail(UNILLM_ERR_UNSUPPORTED,
@@ -439,7 +439,7 @@ int qmatmul_impl(const unillm_qweight* w, const float* x_dev, int64_t m, float* 
             e = launch_decode_mfma(*w, x_dev, m, out, s, run_epi, norm, fixed_ws);
             break;
         case UNILLM_PATH_PREFILL_MFMA:
-            e = launch_prefill_mfma(*w, x_dev, m, out, s, run_epi, norm, fixed_ws);
+            e = launch_prefill_mfma(*w, x_dev, m, out, s, run_epi, norm, fixed_ws, fixed_bytes);
             break;
         default:
             return fail(UNILLM_ERR_INVALID_ARG, what + ": unknown path " + std::to_string(path));

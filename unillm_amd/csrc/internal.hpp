@@ -180,11 +180,12 @@ hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float
 hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, float* y,
                                hipStream_t s, int epi = kEpiStore,
                                const NormArgs& norm = NormArgs{nullptr, nullptr, 0.f},
-                               void* ws = nullptr);
+                               void* ws = nullptr, size_t ws_bytes = 0);
 size_t decode_workspace_bytes(const QWeight& w, int64_t m);
-// The prefill's workspace: this call's own need, and a bound for every call of up
-// to m rows (the size a reserve takes).
-size_t prefill_call_bytes(const QWeight& w, int64_t m);
+// The prefill's workspace: this call's own need (cap > 0: in a fixed workspace of
+// cap bytes, which may pick a plan without a k split), and a bound for every call
+// of up to m rows (the size a reserve takes).
+size_t prefill_call_bytes(const QWeight& w, int64_t m, size_t cap = 0);
 size_t prefill_workspace_bytes(const QWeight& w, int64_t m);
 // Both MFMA paths address weight bytes with 32-bit offsets: weights under 4 GiB.
 inline bool mfma_supports(const QWeight& w) {

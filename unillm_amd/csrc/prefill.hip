@@ -581,39 +581,57 @@ hipError_t launch_bm(const QWeight& w, const uint16_t* xb, const float* rs, int6
     return hipGetLastError();
 }
 
-// Tile rows and k split.  256-row tiles when they give at least one tile per CU,
-// else 128-row tiles; when even those leave most CUs idle (a short, deep
-// product), the k steps are split over up to 4 workgroups per tile, at least
-// 16 steps each, whose raw sums meet in split_sum_kernel (slabs of the stream's
-// workspace).  Calls beyond the 32-bit x offsets (chunked) never split.
+// Tile rows and k split.  256-row tiles when they give at least one tile per CU.
+// A deep product (128 k steps or more) whose 256-row tiles fill 3/8 to 1/2 of the
+// CUs takes those tiles with the k steps split in two (m2048 k14336 n4096: 128
+// tiles, 256 workgroups; Q4_0 776-796 -> 866 TFLOP/s a call, Q8_0 759-774 -> 897-902
+// against one 128-row tile a CU).  Else 128-row tiles; when even those leave most
+// CUs idle (a short, deep product), the k steps are split over up to 4 workgroups
+// per tile, at least 16 steps each.  Split slices' raw sums meet in
+// split_sum_kernel (slabs of the stream's workspace).  Calls beyond the 32-bit x
+// offsets (chunked) never split.
 struct PrefillPlan {
     int bm, S;
 };
 // the most tiles that still count as leaving most CUs idle
 int64_t split_tiles_max() { return (device_info().cu_count - 1) / 2; }
-PrefillPlan prefill_plan(const QWeight& w, int64_t m) {
+size_t up256(size_t b) { return (b + 255) / 256 * 256; }
+
+// The workspace a plan takes: x as f16 rows | their scales | the split slabs
+// ([S][m][n] f32)
+size_t plan_bytes(const QWeight& w, int64_t m, int S) {
+    const size_t slabs = S > 1 ? (size_t)S * m * w.n * sizeof(float) : 0;
+    return up256((size_t)m * (size_t)w.k * 2) + up256((size_t)m * sizeof(float)) + slabs;
+}
+
+// cap > 0: a caller's fixed workspace of cap bytes; a split plan that does not fit
+// falls back to the same rows' tiles unsplit
+PrefillPlan prefill_plan(const QWeight& w, int64_t m, size_t cap = 0) {
     const int64_t cus = device_info().cu_count;
     const int64_t tiles_n = (w.n + PBN - 1) / PBN;
-    if ((m + 255) / 256 * tiles_n >= cus) return {256, 1};
-    const int64_t tiles = (m + 127) / 128 * tiles_n;
+    const int64_t t256 = (m + 255) / 256 * tiles_n;
+    if (t256 >= cus) return {256, 1};
     const int64_t ksteps = (w.kb + 1) / 2;
+    const bool fits2 = cap == 0 || plan_bytes(w, m, 2) <= cap;
+    if (ksteps >= 128 && 2 * t256 <= cus && 8 * t256 >= 3 * cus &&
+        m <= prefill_chunk_rows(w.k, 256) && fits2)
+        return {256, 2};
+    const int64_t tiles = (m + 127) / 128 * tiles_n;
     int64_t S = 1;
     if (tiles <= split_tiles_max() && m <= prefill_chunk_rows(w.k, 128))
         S = std::max<int64_t>(1, std::min<int64_t>({4, cus / tiles, ksteps / 16}));
+    if (S > 1 && cap > 0 && plan_bytes(w, m, (int)S) > cap) S = 1;
     return {128, (int)S};
 }
 
-size_t up256(size_t b) { return (b + 255) / 256 * 256; }
-
 }  // namespace
 
-// Workspace: x as f16 rows | their scales | the split slabs ([S][m][n] f32).  The
-// call's own need, and a bound for every m' <= m (the slabs of 4 slices of the
-// largest m' that can split), so that a reserve for m covers every shorter call.
-size_t prefill_call_bytes(const QWeight& w, int64_t m) {
-    const PrefillPlan plan = prefill_plan(w, m);
-    const size_t slabs = plan.S > 1 ? (size_t)plan.S * m * w.n * sizeof(float) : 0;
-    return up256((size_t)m * (size_t)w.k * 2) + up256((size_t)m * sizeof(float)) + slabs;
+// The call's own need (for a caller's fixed workspace of cap bytes, cap > 0, the
+// plan that fits it where one does), and a bound for every m' <= m (the slabs of 4
+// slices of the largest m' that can split), so that a reserve for m covers every
+// shorter call.
+size_t prefill_call_bytes(const QWeight& w, int64_t m, size_t cap) {
+    return plan_bytes(w, m, prefill_plan(w, m, cap).S);
 }
 
 size_t prefill_workspace_bytes(const QWeight& w, int64_t m) {
@@ -621,21 +639,27 @@ size_t prefill_workspace_bytes(const QWeight& w, int64_t m) {
     int64_t msplit = std::min<int64_t>(128 * (split_tiles_max() / tiles_n),
                                        prefill_chunk_rows(w.k, 128));
     if ((w.kb + 1) / 2 < 32) msplit = 0;  // fewer than 2 x 16 k steps: never split
+    if ((w.kb + 1) / 2 >= 128)  // 256-row tiles split in two, up to half the CUs' worth
+        msplit = std::max<int64_t>(
+            msplit, std::min<int64_t>(256 * (device_info().cu_count / 2 / tiles_n),
+                                      prefill_chunk_rows(w.k, 256)));
     const size_t slabs = (size_t)4 * std::min(m, msplit) * w.n * sizeof(float);
     return up256((size_t)m * (size_t)w.k * 2) + up256((size_t)m * sizeof(float)) + slabs;
 }
 
 hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, float* y,
-                               hipStream_t s, int epi, const NormArgs& norm, void* ws) {
+                               hipStream_t s, int epi, const NormArgs& norm, void* ws,
+                               size_t ws_bytes) {
     // weight bytes are addressed with 32-bit offsets (pcol_off, ssrc)
     if (!mfma_supports(w)) return hipErrorInvalidValue;
     // x as f16 rows with their power-of-two scales in the workspace: the GEMM
     // re-reads x once per 256-column tile, so it reads half the bytes, and no
     // conversion sits in its inner loop.  A split k's slabs follow.
-    const PrefillPlan plan = prefill_plan(w, m);
+    const PrefillPlan plan = prefill_plan(w, m, ws ? ws_bytes : 0);
     const size_t xbytes = up256((size_t)m * (size_t)w.k * 2);
     hipError_t e = hipSuccess;
-    if (!ws && (e = stream_workspace(s, prefill_call_bytes(w, m), &ws)) != hipSuccess) return e;
+    if (ws && plan_bytes(w, m, plan.S) > ws_bytes) return hipErrorInvalidValue;
+    if (!ws && (e = stream_workspace(s, plan_bytes(w, m, plan.S), &ws)) != hipSuccess) return e;
     float* rs = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + xbytes);
     float* part =
         plan.S > 1 ? reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + xbytes +
@@ -647,7 +671,7 @@ hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, floa
     if (e != hipSuccess) return e;
     const uint16_t* xb = static_cast<const uint16_t*>(ws);
 #define UNILLM_PREFILL_LAUNCH(QTYPE)                                                          \
-    return plan.bm == 256 ? launch_bm<QTYPE, 256>(w, xb, rs, m, y, 1, nullptr, s, add)       \
+    return plan.bm == 256 ? launch_bm<QTYPE, 256>(w, xb, rs, m, y, plan.S, part, s, add)     \
                           : launch_bm<QTYPE, 128>(w, xb, rs, m, y, plan.S, part, s, add)
     switch (w.qtype) {
         case UNILLM_QTYPE_Q4_0: UNILLM_PREFILL_LAUNCH(UNILLM_QTYPE_Q4_0);

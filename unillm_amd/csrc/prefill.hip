@@ -585,16 +585,16 @@ hipError_t launch_bm(const QWeight& w, const uint16_t* xb, const float* rs, int6
 // A deep product (128 k steps or more) whose 256-row tiles fill 3/8 to 1/2 of the
 // CUs takes those tiles with the k steps split in two (m2048 k14336 n4096: 128
 // tiles, 256 workgroups; Q4_0 776-796 -> 866 TFLOP/s a call, Q8_0 759-774 -> 897-902
-// against one 128-row tile a CU).  Else 128-row tiles; when even those leave most
-// CUs idle (a short, deep product), the k steps are split over up to 4 workgroups
+// against one 128-row tile a CU).  Else 128-row tiles; when those fill at most half
+// the CUs (a short, deep product), the k steps are split over up to 4 workgroups
 // per tile, at least 16 steps each.  Split slices' raw sums meet in
 // split_sum_kernel (slabs of the stream's workspace).  Calls beyond the 32-bit x
 // offsets (chunked) never split.
 struct PrefillPlan {
     int bm, S;
 };
-// the most tiles that still count as leaving most CUs idle
-int64_t split_tiles_max() { return (device_info().cu_count - 1) / 2; }
+// the most 128-row tiles that split their k steps: half the CUs or fewer
+int64_t split_tiles_max() { return device_info().cu_count / 2; }
 size_t up256(size_t b) { return (b + 255) / 256 * 256; }
 
 // The workspace a plan takes: x as f16 rows | their scales | the split slabs

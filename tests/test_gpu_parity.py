@@ -266,6 +266,25 @@ def test_prefill_large_tiles(qtype, m, k, n):
     assert np.array_equal(y2.cpu().numpy(), 2.0 * y)  # enough tiles: no k split
 
 
+@pytest.mark.parametrize("qtype,m,k,n", [(Q4_0, 65, 11008, 4096), (Q8_0, 100, 14336, 4096)])
+def test_prefill_short_deep_split(qtype, m, k, n):
+    # a short, deep product: 16 tiles of 128 rows, the k steps split over up to 16
+    # workgroups a tile, the slices' sums added in slice order
+    blocks, x = _case(qtype, m, n, k, seed=m + k)
+    ql = QuantLinear.from_blocks(qtype, n, k, blocks)
+    y = _run(ql, x, PATH_PREFILL_MFMA)
+    rows = np.array([0, 1, m // 2, m - 1])
+    ref = oracle.qmatmul_f64(qtype, blocks, x[rows], n, k)
+    assert oracle.normwise_error(y[rows], ref) < 1e-3
+    xd = _dev(x)
+    y2 = ql.forward(xd * 2.0, path=PATH_PREFILL_MFMA)
+    torch.cuda.synchronize()
+    assert np.array_equal(y2.cpu().numpy(), 2.0 * y)  # scaling exact, split or not
+    y3 = ql.forward(xd, path=PATH_PREFILL_MFMA)
+    torch.cuda.synchronize()
+    assert np.array_equal(y3.cpu().numpy(), y)  # repeatable bit for bit
+
+
 @pytest.mark.parametrize("qtype,m,k,path", [(Q4_0, 96, 1024, PATH_PREFILL_MFMA),
                                              (Q8_0, 96, 1024, PATH_PREFILL_MFMA),
                                              (Q4_0, 5, 4096, PATH_DECODE_MFMA),

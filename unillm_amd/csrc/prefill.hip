@@ -586,7 +586,7 @@ hipError_t launch_bm(const QWeight& w, const uint16_t* xb, const float* rs, int6
 // CUs takes those tiles with the k steps split in two (m2048 k14336 n4096: 128
 // tiles, 256 workgroups; Q4_0 776-796 -> 866 TFLOP/s a call, Q8_0 759-774 -> 897-902
 // against one 128-row tile a CU).  Else 128-row tiles; when those fill at most half
-// the CUs (a short, deep product), the k steps are split over up to 4 workgroups
+// the CUs (a short, deep product), the k steps are split over up to 16 workgroups
 // per tile, at least 16 steps each.  Split slices' raw sums meet in
 // split_sum_kernel (slabs of the stream's workspace).  Calls beyond the 32-bit x
 // offsets (chunked) never split.
@@ -595,6 +595,8 @@ struct PrefillPlan {
 };
 // the most 128-row tiles that split their k steps: half the CUs or fewer
 int64_t split_tiles_max() { return device_info().cu_count / 2; }
+// the most slices a k range splits into
+constexpr int64_t kMaxSlices = 16;
 size_t up256(size_t b) { return (b + 255) / 256 * 256; }
 
 // The workspace a plan takes: x as f16 rows | their scales | the split slabs
@@ -619,7 +621,7 @@ PrefillPlan prefill_plan(const QWeight& w, int64_t m, size_t cap = 0) {
     const int64_t tiles = (m + 127) / 128 * tiles_n;
     int64_t S = 1;
     if (tiles <= split_tiles_max() && m <= prefill_chunk_rows(w.k, 128))
-        S = std::max<int64_t>(1, std::min<int64_t>({4, cus / tiles, ksteps / 16}));
+        S = std::max<int64_t>(1, std::min<int64_t>({kMaxSlices, cus / tiles, ksteps / 16}));
     if (S > 1 && cap > 0 && plan_bytes(w, m, (int)S) > cap) S = 1;
     return {128, (int)S};
 }
@@ -635,15 +637,15 @@ size_t prefill_call_bytes(const QWeight& w, int64_t m, size_t cap) {
 }
 
 size_t prefill_workspace_bytes(const QWeight& w, int64_t m) {
+    // slices x rows of any split: at most kMaxSlices m, and at most 128 CUs / (column
+    // tiles) with 128-row tiles (S <= CUs / tiles) or 256 CUs / (column tiles) with
+    // 256-row tiles split in two (those tiles fill at most half the CUs)
     const int64_t tiles_n = (w.n + PBN - 1) / PBN;
-    int64_t msplit = std::min<int64_t>(128 * (split_tiles_max() / tiles_n),
-                                       prefill_chunk_rows(w.k, 128));
-    if ((w.kb + 1) / 2 < 32) msplit = 0;  // fewer than 2 x 16 k steps: never split
-    if ((w.kb + 1) / 2 >= 128)  // 256-row tiles split in two, up to half the CUs' worth
-        msplit = std::max<int64_t>(
-            msplit, std::min<int64_t>(256 * (device_info().cu_count / 2 / tiles_n),
-                                      prefill_chunk_rows(w.k, 256)));
-    const size_t slabs = (size_t)4 * std::min(m, msplit) * w.n * sizeof(float);
+    const int64_t sm = (w.kb + 1) / 2 < 32
+                           ? 0  // fewer than 2 x 16 k steps: never split
+                           : std::min<int64_t>(kMaxSlices * m,
+                                               256 * device_info().cu_count / tiles_n);
+    const size_t slabs = (size_t)sm * w.n * sizeof(float);
     return up256((size_t)m * (size_t)w.k * 2) + up256((size_t)m * sizeof(float)) + slabs;
 }
 

@@ -621,7 +621,7 @@ PrefillPlan prefill_plan(const QWeight& w, int64_t m, size_t cap = 0) {
     const int64_t tiles = (m + 127) / 128 * tiles_n;
     int64_t S = 1;
     if (tiles <= split_tiles_max() && m <= prefill_chunk_rows(w.k, 128))
-        S = std::max<int64_t>(1, std::min<int64_t>({kMaxSlices, cus / tiles, ksteps / 16}));
+        S = std::max<int64_t>(1, std::min<int64_t>({kMaxSlices, cus / tiles, ksteps / 8}));
     if (S > 1 && cap > 0 && plan_bytes(w, m, (int)S) > cap) S = 1;
     return {128, (int)S};
 }
@@ -641,8 +641,8 @@ size_t prefill_workspace_bytes(const QWeight& w, int64_t m) {
     // tiles) with 128-row tiles (S <= CUs / tiles) or 256 CUs / (column tiles) with
     // 256-row tiles split in two (those tiles fill at most half the CUs)
     const int64_t tiles_n = (w.n + PBN - 1) / PBN;
-    const int64_t sm = (w.kb + 1) / 2 < 32
-                           ? 0  // fewer than 2 x 16 k steps: never split
+    const int64_t sm = (w.kb + 1) / 2 < 16
+                           ? 0  // fewer than 2 x 8 k steps: never split
                            : std::min<int64_t>(kMaxSlices * m,
                                                256 * device_info().cu_count / tiles_n);
     const size_t slabs = (size_t)sm * w.n * sizeof(float);

@@ -266,14 +266,18 @@ def test_prefill_large_tiles(qtype, m, k, n):
     assert np.array_equal(y2.cpu().numpy(), 2.0 * y)  # enough tiles: no k split
 
 
-@pytest.mark.parametrize("qtype,m,k,n", [(Q4_0, 65, 11008, 4096), (Q8_0, 100, 14336, 4096)])
+@pytest.mark.parametrize("qtype,m,k,n", [(Q4_0, 65, 11008, 4096), (Q8_0, 100, 14336, 4096),
+                                         (Q4_0, 768, 14336, 4096), (Q8_0, 1100, 14336, 4096),
+                                         (Q4_0, 500, 11008, 4096)])
 def test_prefill_short_deep_split(qtype, m, k, n):
     # a short, deep product: 16 tiles of 128 rows, the k steps split over up to 16
-    # workgroups a tile, the slices' sums added in slice order
+    # workgroups a tile; or (m > 256) 256-row tiles filling at most half the CUs,
+    # the k steps split over up to CUs / tiles workgroups (m768: 48 tiles in 5
+    # slices, m1100: 80 in 3, m500: 32 in 8).  The slices' sums add in slice order.
     blocks, x = _case(qtype, m, n, k, seed=m + k)
     ql = QuantLinear.from_blocks(qtype, n, k, blocks)
     y = _run(ql, x, PATH_PREFILL_MFMA)
-    rows = np.array([0, 1, m // 2, m - 1])
+    rows = np.unique([0, 1, min(255, m - 1), min(256, m - 1), m // 2, m - 1])
     ref = oracle.qmatmul_f64(qtype, blocks, x[rows], n, k)
     assert oracle.normwise_error(y[rows], ref) < 1e-3
     xd = _dev(x)

@@ -40,9 +40,10 @@ CASES = [
     (Q4_0, 14336, 4096, 64, 16, PATH_DECODE_MFMA, False),
     (Q8_0, 4096, 11008, 33, 5, PATH_DECODE_MFMA, False),
     (Q4_0, 14336, 4096, 2048, 512, PATH_PREFILL_MFMA, True),
-    (Q4_0, 4096, 14336, 700, 130, PATH_PREFILL_MFMA, True),
+    # 128-row tiles with k split 5 ways, then 8 ways: the same plans in both calls
+    (Q4_0, 4096, 14336, 300, 130, PATH_PREFILL_MFMA, True),
     # the library call splits k over 256-row tiles, whose slabs do not fit the
-    # scratch beside x: the no-allocation call runs the tiles unsplit
+    # scratch beside x: the no-allocation call runs 128-row tiles unsplit
     (Q4_0, 4096, 14336, 2048, 1100, PATH_PREFILL_MFMA, False),
 ]
 

@@ -582,12 +582,16 @@ hipError_t launch_bm(const QWeight& w, const uint16_t* xb, const float* rs, int6
 }
 
 // Tile rows and k split.  256-row tiles when they give at least one tile per CU.
-// A deep product (128 k steps or more) whose 256-row tiles fill 3/8 to 1/2 of the
-// CUs takes those tiles with the k steps split in two (m2048 k14336 n4096: 128
-// tiles, 256 workgroups; Q4_0 776-796 -> 866 TFLOP/s a call, Q8_0 759-774 -> 897-902
-// against one 128-row tile a CU).  Else 128-row tiles; when those fill at most half
-// the CUs (a short, deep product), the k steps are split over up to 16 workgroups
-// per tile, at least 16 steps each.  Split slices' raw sums meet in
+// A deep product (128 k steps or more) whose 256-row tiles fill at most half the
+// CUs takes those tiles with the k steps split over up to CUs / tiles workgroups, at
+// least 16 steps each: where the tiles fill 3/8 to 1/2 of the CUs (a split in two:
+// m2048 k14336 n4096, 128 tiles, 256 workgroups; Q4_0 776-796 -> 866 TFLOP/s a call,
+// Q8_0 759-774 -> 897-902 against one 128-row tile a CU), and for m > 256 where
+// plan_cost rates them no dearer than the 128-row plan (m1024 k14336 n4096, 64 tiles in
+// 4 slices: Q4_0 163-169 -> 154-156 us a call against 128 tiles of 128 rows in 2;
+// m768, 48 tiles in 5: 159-161 -> 126-127).  Else 128-row tiles; when those fill at
+// most half the CUs (a short, deep product), the k steps are split over up to 16
+// workgroups per tile, at least 8 steps each.  Split slices' raw sums meet in
 // split_sum_kernel (slabs of the stream's workspace).  Calls beyond the 32-bit x
 // offsets (chunked) never split.
 struct PrefillPlan {
@@ -606,23 +610,34 @@ size_t plan_bytes(const QWeight& w, int64_t m, int S) {
     return up256((size_t)m * (size_t)w.k * 2) + up256((size_t)m * sizeof(float)) + slabs;
 }
 
+// The busiest CU's share of a plan: rounds x rows x k steps a workgroup, a 128-row
+// tile's rows counted at 8/7 of a 256-row tile's (770 against 889 TFLOP/s a kernel,
+// Q4_0 m512 and m2048 at k4096 n14336, unsplit)
+int64_t plan_cost(int64_t tiles, int64_t S, int bm, int64_t ksteps, int64_t cus) {
+    const int64_t rounds = (tiles * S + cus - 1) / cus;
+    return rounds * bm * ((ksteps + S - 1) / S) * (bm == 128 ? 8 : 7);
+}
+
 // cap > 0: a caller's fixed workspace of cap bytes; a split plan that does not fit
-// falls back to the same rows' tiles unsplit
+// falls back to a plan that does (at worst the 128-row tiles unsplit)
 PrefillPlan prefill_plan(const QWeight& w, int64_t m, size_t cap = 0) {
     const int64_t cus = device_info().cu_count;
     const int64_t tiles_n = (w.n + PBN - 1) / PBN;
     const int64_t t256 = (m + 255) / 256 * tiles_n;
     if (t256 >= cus) return {256, 1};
     const int64_t ksteps = (w.kb + 1) / 2;
-    const bool fits2 = cap == 0 || plan_bytes(w, m, 2) <= cap;
-    if (ksteps >= 128 && 2 * t256 <= cus && 8 * t256 >= 3 * cus &&
-        m <= prefill_chunk_rows(w.k, 256) && fits2)
-        return {256, 2};
     const int64_t tiles = (m + 127) / 128 * tiles_n;
     int64_t S = 1;
     if (tiles <= split_tiles_max() && m <= prefill_chunk_rows(w.k, 128))
         S = std::max<int64_t>(1, std::min<int64_t>({kMaxSlices, cus / tiles, ksteps / 8}));
     if (S > 1 && cap > 0 && plan_bytes(w, m, (int)S) > cap) S = 1;
+    if (ksteps >= 128 && 2 * t256 <= cus && m <= prefill_chunk_rows(w.k, 256)) {
+        const int64_t S2 = std::min<int64_t>({kMaxSlices, cus / t256, ksteps / 16});
+        const bool cheaper =
+            m > 256 && plan_cost(t256, S2, 256, ksteps, cus) <= plan_cost(tiles, S, 128, ksteps, cus);
+        if ((8 * t256 >= 3 * cus || cheaper) && (cap == 0 || plan_bytes(w, m, (int)S2) <= cap))
+            return {256, (int)S2};
+    }
     return {128, (int)S};
 }
 
@@ -639,7 +654,7 @@ size_t prefill_call_bytes(const QWeight& w, int64_t m, size_t cap) {
 size_t prefill_workspace_bytes(const QWeight& w, int64_t m) {
     // slices x rows of any split: at most kMaxSlices m, and at most 128 CUs / (column
     // tiles) with 128-row tiles (S <= CUs / tiles) or 256 CUs / (column tiles) with
-    // 256-row tiles split in two (those tiles fill at most half the CUs)
+    // 256-row tiles (S <= CUs / tiles)
     const int64_t tiles_n = (w.n + PBN - 1) / PBN;
     const int64_t sm = (w.kb + 1) / 2 < 16
                            ? 0  // fewer than 2 x 8 k steps: never split

@@ -252,13 +252,15 @@ def test_lm_head_error_text():
 
 
 @pytest.mark.parametrize("qtype,m,k,n", [(Q4_0, 2048, 4096, 14336), (Q8_0, 1100, 4128, 14000),
-                                         (Q4_0, 1100, 4128, 14000)])
+                                         (Q4_0, 1100, 4128, 14000), (Q4_0, 768, 4096, 14336),
+                                         (Q8_0, 1100, 4096, 11008), (Q4_0, 300, 4096, 22016)])
 def test_prefill_large_tiles(qtype, m, k, n):
-    # enough tiles for the 256-row tile shape; ragged m and n, odd blocks per row
+    # 256-row tiles unsplit: one a CU or more, or (m768, m1100, m300 here) one round
+    # of them against two of 128-row tiles; ragged m and n, odd blocks per row
     blocks, x = _case(qtype, m, n, k, seed=m + n + k)
     ql = QuantLinear.from_blocks(qtype, n, k, blocks)
     y = _run(ql, x, PATH_AUTO)
-    rows = np.array([0, 1, 255, 256, 1023, m - 77, m - 1])
+    rows = np.unique(np.minimum([0, 1, 255, 256, 1023, m - 77, m - 1], m - 1))
     ref = oracle.qmatmul_f64(qtype, blocks, x[rows], n, k)
     assert oracle.normwise_error(y[rows], ref) < 1e-3
     y2 = ql.forward(_dev(x) * 2.0)

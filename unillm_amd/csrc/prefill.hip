@@ -591,7 +591,8 @@ hipError_t launch_bm(const QWeight& w, const uint16_t* xb, const float* rs, int6
 // 4 slices: Q4_0 163-169 -> 154-156 us a call against 128 tiles of 128 rows in 2;
 // m768, 48 tiles in 5: 159-161 -> 126-127).  Else 128-row tiles; when those fill at
 // most half the CUs (a short, deep product), the k steps are split over up to 16
-// workgroups per tile, at least 8 steps each.  Split slices' raw sums meet in
+// workgroups per tile, at least 8 steps each; unless (m > 256) plan_cost rates the
+// 256-row tiles unsplit cheaper.  Split slices' raw sums meet in
 // split_sum_kernel (slabs of the stream's workspace).  Calls beyond the 32-bit x
 // offsets (chunked) never split.
 struct PrefillPlan {
@@ -638,6 +639,11 @@ PrefillPlan prefill_plan(const QWeight& w, int64_t m, size_t cap = 0) {
         if ((8 * t256 >= 3 * cus || cheaper) && (cap == 0 || plan_bytes(w, m, (int)S2) <= cap))
             return {256, (int)S2};
     }
+    // fewer 256-row tiles than CUs, but one round of them against two of 128-row
+    // tiles (k4096 n14336 m1024: 224 tiles against 448; Q4_0 166-171 -> 134 us a
+    // call, 20-25 % on every shape it picks)
+    if (m > 256 && plan_cost(t256, 1, 256, ksteps, cus) < plan_cost(tiles, S, 128, ksteps, cus))
+        return {256, 1};
     return {128, (int)S};
 }
 

@@ -252,11 +252,14 @@ def test_lm_head_error_text():
 
 
 @pytest.mark.parametrize("qtype,m,k,n", [(Q4_0, 2048, 4096, 14336), (Q8_0, 1100, 4128, 14000),
-                                         (Q4_0, 1100, 4128, 14000), (Q4_0, 768, 4096, 14336),
-                                         (Q8_0, 1100, 4096, 11008), (Q4_0, 300, 4096, 22016)])
+                                         (Q4_0, 1200, 4128, 14000), (Q4_0, 768, 4096, 14336),
+                                         (Q8_0, 1100, 4096, 11008), (Q4_0, 300, 4096, 22016),
+                                         (Q4_0, 1100, 4096, 14336)])
 def test_prefill_large_tiles(qtype, m, k, n):
-    # 256-row tiles unsplit: one a CU or more, or (m768, m1100, m300 here) one round
-    # of them against two of 128-row tiles; ragged m and n, odd blocks per row
+    # tiles unsplit: 256 rows, one a CU or more (m2048, m1200), or one round of them
+    # against two of 128-row tiles (m768, m1100 at k4096 n11008, m300); 128 rows
+    # where they take as many rounds as 256-row ones (m1100 at n14000 and n14336).
+    # Ragged m and n, odd blocks per row.
     blocks, x = _case(qtype, m, n, k, seed=m + n + k)
     ql = QuantLinear.from_blocks(qtype, n, k, blocks)
     y = _run(ql, x, PATH_AUTO)

@@ -581,7 +581,8 @@ hipError_t launch_bm(const QWeight& w, const uint16_t* xb, const float* rs, int6
     return hipGetLastError();
 }
 
-// Tile rows and k split.  256-row tiles when they give at least one tile per CU.
+// Tile rows and k split.  256-row tiles when they give at least one tile per CU,
+// unless 128-row tiles take no more rounds.
 // A deep product (128 k steps or more) whose 256-row tiles fill at most half the
 // CUs takes those tiles with the k steps split over up to CUs / tiles workgroups, at
 // least 16 steps each: where the tiles fill 3/8 to 1/2 of the CUs (a split in two:
@@ -625,9 +626,14 @@ PrefillPlan prefill_plan(const QWeight& w, int64_t m, size_t cap = 0) {
     const int64_t cus = device_info().cu_count;
     const int64_t tiles_n = (w.n + PBN - 1) / PBN;
     const int64_t t256 = (m + 255) / 256 * tiles_n;
-    if (t256 >= cus) return {256, 1};
     const int64_t ksteps = (w.kb + 1) / 2;
     const int64_t tiles = (m + 127) / 128 * tiles_n;
+    // a tile a CU or more: 128-row tiles where they take no more rounds, each half
+    // as long (k4096 n14336 m1100: 504 tiles against 280, two rounds each; Q4_0
+    // 233 -> 187-189 us a call, Q8_0 231-233 -> 205-207; a third round loses)
+    if (t256 >= cus)
+        return (tiles + cus - 1) / cus <= (t256 + cus - 1) / cus ? PrefillPlan{128, 1}
+                                                                 : PrefillPlan{256, 1};
     int64_t S = 1;
     if (tiles <= split_tiles_max() && m <= prefill_chunk_rows(w.k, 128))
         S = std::max<int64_t>(1, std::min<int64_t>({kMaxSlices, cus / tiles, ksteps / 8}));

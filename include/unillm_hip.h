@@ -124,9 +124,10 @@ int unillm_hip_qmatmul(const unillm_qweight* w, const float* x_dev, int64_t m, f
  * unillm_hip_qmatmul (same kernels); the MFMA paths keep their f16 copy of x in
  * a 64 MiB scratch array that the library holds on each GPU from load to process
  * end, instead of the stream's workspace.  Limits: x 16-byte aligned; the scratch
- * takes m * k * 2 bytes (+ 4 m for prefill, + S * m * n * 4 when a deep prefill
- * splits k into S <= 4 slices; a split that would not fit runs unsplit, agreeing
- * with unillm_hip_qmatmul to f32 rounding): calls beyond 64 MiB fail with
+ * takes m * k * 2 bytes (+ 4 m for prefill, + S * m * n * 4 when a prefill
+ * splits k into S <= 16 slices; a split that would not fit gives way to the
+ * 128-row plan that fits, at worst unsplit, agreeing with unillm_hip_qmatmul to
+ * f32 rounding): calls beyond 64 MiB fail with
  * UNILLM_ERR_UNSUPPORTED before any launch.  All calls on one GPU share its
  * scratch: calls that overlap in time on one GPU (concurrent streams, or threads
  * without ordering) race and must not be issued. */

@@ -134,3 +134,28 @@ def test_attention_reserve_covers_every_shorter_call():
         s.synchronize()
         assert torch.equal(out, eager), m
         del g
+
+
+@pytest.mark.parametrize("n,k", [(4096, 14336), (14336, 4096)])
+def test_qmatmul_reserve_covers_every_shorter_call(n, k):
+    # Reserving for 2048 rows covers every shorter prefill, whatever its plan:
+    # 128-row tiles split up to 16 ways (m65-300), 256-row tiles split up to 8 ways
+    # (deep k, m500-1536), unsplit tiles of either height.  Each call is captured
+    # first, so a workspace that had to grow would fail the capture; its replay then
+    # matches an eager call bit for bit.
+    _, ql = _weight(n, k, seed=50 + k)
+    s = torch.cuda.Stream()
+    ql.reserve(2048, stream=s)
+    for m in (65, 100, 130, 256, 300, 500, 600, 700, 768, 1024, 1100, 1280, 1536, 2048):
+        print(f"reserve covers n={n} k={k} m={m}", flush=True)
+        x = _x(m, k, seed=51 + m)
+        y = torch.empty(m, n, device="cuda")
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s, capture_error_mode="thread_local"):
+            ql.forward(x, out=y, path=PATH_PREFILL_MFMA, stream=s)
+        with torch.cuda.stream(s):
+            g.replay()
+            eager = ql.forward(x, path=PATH_PREFILL_MFMA, stream=s)
+        s.synchronize()
+        assert torch.equal(y, eager), m
+        del g

@@ -494,6 +494,7 @@ def extra_configs(torch, QuantLinear, gen, stream, only):
                 "note": "norms, residual adds and SwiGLU fused into the same 4 launches a layer"}
         if "e2e" in want:
             res.update(decode_step_e2e(torch, layers, head, gen, stream, timer))
+            res.update(prompt_step_e2e(torch, layers, head, gen, stream, timer))
         del layers, head
     torch.cuda.synchronize()
     return res
@@ -559,6 +560,54 @@ def decode_step_e2e(torch, layers, head, gen, stream, timer):
             "launches_per_step": 6 * 32 + 1,
             "note": "norm+QKV, attention, o+residual, norm+gate_up+SwiGLU, down+residual a layer; "
                     "final norm + Q8_0 lm_head; HIP-graph replay"}
+        del caches
+    return res
+
+
+def prompt_step_e2e(torch, layers, head, gen, stream, timer):
+    """A whole Llama-2-7B prompt step: m tokens into empty KV caches, per layer
+    input_layernorm + QKV, attention (RoPE, append, causal softmax over the prompt:
+    32 heads, hd 128, f32 cache), o_proj + residual, post_attention_layernorm +
+    gate_up + SwiGLU, down + residual; then the final norm + lm_head on the last
+    position only, as the reference's forward does.  Eager launches; the caches are
+    rewound and the residual restarted outside each timed pass."""
+    from unillm_amd import KvCache
+    H, D = 32, 128
+    res = {}
+    gam = torch.ones(4096, device="cuda")
+    logits = torch.empty(1, 32000, device="cuda")
+    for m in (512, 2048):
+        h = torch.empty(m, 4096, device="cuda")
+        qkv_out = torch.empty(m, 3 * 4096, device="cuda")
+        att = torch.empty(m, 4096, device="cuda")
+        act = torch.empty(m, 11008, device="cuda")
+        caches = [KvCache(H, D, m) for _ in layers]
+
+        def step():
+            for (qkv, o, gu, down), kv in zip(layers, caches):
+                qkv.forward_norm(h, gam, eps=1e-6, out=qkv_out, stream=stream)
+                kv.attention(qkv_out, H, out=att, stream=stream)
+                o.forward_add(att, h, stream=stream)
+                gu.forward_swiglu(h, out=act, stream=stream, norm=(gam, None, 1e-6))
+                down.forward_add(act, h, stream=stream)
+            head.forward_norm(h[m - 1:], gam, eps=1e-6, out=logits, stream=stream)
+
+        def sample():
+            for kv in caches:
+                kv.truncate(0)
+            h.normal_(generator=gen)
+            return timer.run(step, 1)
+
+        with torch.cuda.stream(stream):
+            sample()
+            ms = float(np.median([sample() for _ in range(5)]))
+        flops = 32 * 2 * m * 4096 * (12288 + 4096 + 22016 + 11008)  # the linear layers
+        res[f"llama2_7b_prompt_step_e2e_m{m}"] = {
+            "ms_per_step": round(ms, 3), "tokens/s": round(m * 1e3 / ms, 1),
+            "linear_TFLOP/s": round(flops / ms / 1e9, 1),
+            "note": "norm+QKV, attention over the prompt, o+residual, norm+gate_up+SwiGLU, "
+                    "down+residual a layer into empty caches; final norm + Q8_0 lm_head on "
+                    "the last position; eager launches"}
         del caches
     return res
 

@@ -395,7 +395,8 @@ int oracle_attention_decode(const float* qkv, int64_t m, int64_t n_heads, int64_
             memcpy(v_cache + (g * max_seq + len + t) * D, r + (H + KVH + g) * D,
                    sizeof(float) * (size_t)D);
     }
-    const double scale = 1.0 / sqrt((double)D);
+    /* LlamaAttention::new keeps 1 / sqrt(hd) in f32 (llama.rs:890); scores are scaled by it */
+    const double scale = (double)(1.0f / sqrtf((float)D));
     double* sc = (double*)malloc(sizeof(double) * (size_t)(len + m));
     for (int64_t t = 0; t < m; ++t)
         for (int64_t h = 0; h < H; ++h) {

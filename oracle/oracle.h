@@ -52,6 +52,13 @@
  *   candle-semantics   : loose bound (~1e-2 normwise) against the f64 oracle;
  *   CPU path             bit-identity with candle's SIMD summation order is
  *                        not claimed (timing baseline only).
+ *   attention          : closed forms (one position returns v, equal keys
+ *                        average, RoPE known answers, relative-position
+ *                        invariance, causality) and, for the softmax's scale and
+ *                        base, an independent numpy restatement of
+ *                        forward_with_cache's tensor steps
+ *                        (tests/golden/llama_attention_np.py) on random keys,
+ *                        to 1e-12, with planted wrong scales / bases shown to fail
  */
 #ifndef UNILLM_ORACLE_H
 #define UNILLM_ORACLE_H
@@ -101,7 +108,8 @@ int oracle_candle_qmatmul(int qtype, const uint8_t* blocks, const float* x,
  *   inv_freq = 1 / theta^(2i / hd) and angle = pos * inv_freq in f32) at
  *   positions len .. len + m - 1; k, v appended to k_cache / v_cache
  *   ([KVH][max_seq][hd], updated in place); head h reads kv head h / (H / KVH);
- *   out[m, H hd] = softmax(q k^T / sqrt(hd) + causal mask) v, in f64. */
+ *   out[m, H hd] = softmax(q k^T * scale + causal mask) v, in f64, with
+ *   scale = 1 / sqrt(hd) formed in f32 as LlamaAttention::new does (llama.rs:890). */
 int oracle_attention_decode(const float* qkv, int64_t m, int64_t n_heads, int64_t n_kv_heads,
                             int64_t head_dim, float rope_theta, float* k_cache, float* v_cache,
                             int64_t max_seq, int64_t len, double* out);

@@ -18,8 +18,10 @@ which tensors stay quantized (weight_loader_core.rs:554).
 
 tiny_llama_q4_0.step: the logits of LlamaModelV2::forward_with_cache
 (llama.rs:421-462) over three calls on one cache (a 12-token prompt, then two
-single tokens), computed in f64 from the oracle's pieces: its exact dequant, its
-attention with a KV cache, and numpy for the layer norms, SwiGLU and residuals.
+single tokens), computed in f64: the oracle's exact dequant, the attention with a
+KV cache from llama_attention_np.py (a numpy restatement of forward_with_cache's
+attention, independent of the oracle's), and numpy for the layer norms, SwiGLU
+and residuals.
 Layout: "USTP", u32 vocab, u32 n_steps; per step u32 m, i32 ids[m],
 f64 logits[m * vocab].
 
@@ -116,7 +118,8 @@ def write_steps(tensors, stem) -> None:
     """The f64 logits of forward_with_cache (llama.rs:421-462; the decoder layer
     llama.rs:654-680) for the calls in STEPS, one cache across them."""
     sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
-    import oracle  # test infrastructure: exact dequant, attention with a KV cache
+    import oracle  # test infrastructure: exact dequant
+    from llama_attention_np import KvCacheNp, forward_with_cache_attention
 
     W = {}
     for name, ttype, shape, raw, deq in tensors:
@@ -127,26 +130,22 @@ def write_steps(tensors, stem) -> None:
             blocks = np.frombuffer(raw, dtype=np.uint8)
             W[hf_name(name)] = oracle.dequant(ttype, blocks, n, k).astype(np.float64)
     hd = HIDDEN // HEADS
-    max_seq = sum(len(s) for s in STEPS)
-    caches = [(np.zeros((KV_HEADS, max_seq, hd), np.float32),
-               np.zeros((KV_HEADS, max_seq, hd), np.float32)) for _ in range(LAYERS)]
-    length = 0
+    caches = [KvCacheNp(HEADS, hd) for _ in range(LAYERS)]
     blob = b"USTP" + struct.pack("<II", VOCAB, len(STEPS))
     for ids in STEPS:
         h = W["model.embed_tokens.weight"][ids]
-        for i, (kc, vc) in enumerate(caches):
+        for i, cache in enumerate(caches):
             p = f"model.layers.{i}."
             xn = layer_norm(h, W[p + "input_layernorm.weight"], 1e-6)
             qkv = np.concatenate([xn @ W[p + f"self_attn.{t}_proj.weight"].T for t in "qkv"],
                                  axis=1)
-            att = oracle.attention_decode(qkv.astype(np.float32), HEADS, KV_HEADS, hd,
-                                          ROPE_BASE, kc, vc, length)
+            att = forward_with_cache_attention(qkv.astype(np.float32), HEADS, KV_HEADS, hd,
+                                               ROPE_BASE, cache)
             h = h + att @ W[p + "self_attn.o_proj.weight"].T
             xn = layer_norm(h, W[p + "post_attention_layernorm.weight"], 1e-6)
             g = xn @ W[p + "mlp.gate_proj.weight"].T
             u = xn @ W[p + "mlp.up_proj.weight"].T
             h = h + (g / (1.0 + np.exp(-g)) * u) @ W[p + "mlp.down_proj.weight"].T
-        length += len(ids)
         logits = layer_norm(h, W["model.norm.weight"], NORM_EPS) @ W["lm_head.weight"].T
         blob += struct.pack("<I", len(ids)) + struct.pack(f"<{len(ids)}i", *ids)
         blob += logits.astype("<f8").tobytes()

@@ -7,6 +7,9 @@ numpy's float16 conversions and float64 matmul (library routines), exhaustive
 closed forms, the reference's layout-neutral known-answer tests, and the
 independent numpy restatement whose output is committed in tests/golden/.
 """
+import os
+import sys
+
 import numpy as np
 import pytest
 
@@ -489,3 +492,63 @@ def test_attention_causal_and_gqa_heads():
 def test_attention_overflow_rejected():
     with pytest.raises(ValueError):
         _attn(np.zeros((3, 4 * 8), np.float32), 2, 1, 8, max_seq=4, length=2)
+
+
+# ---- the attention softmax against an independent restatement --------------------------------
+# tests/golden/llama_attention_np.py restates forward_with_cache's attention (llama.rs:827-883,
+# 890, 1108-1148) in numpy's tensor form; random, non-uniform keys make the softmax temperature
+# and base visible, which the closed-form checks above are blind to.
+
+def _np_attention():
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+    import llama_attention_np
+    return llama_attention_np
+
+
+def _attention_case(H, KVH, D, L, m, seed, theta=10000.0, scale=None, exp=np.exp):
+    """The oracle and the restatement on the same cache prefix and new tokens."""
+    ref = _np_attention()
+    max_seq = L + m + 3
+    pre = oracle.normal(L * (H + 2 * KVH) * D, seed=seed).reshape(L, -1) if L else None
+    qkv = oracle.normal(m * (H + 2 * KVH) * D, seed=seed + 1).reshape(m, -1)
+    k = np.zeros((KVH, max_seq, D), np.float32)
+    v = np.zeros((KVH, max_seq, D), np.float32)
+    cache = ref.KvCacheNp(H, D)
+    if L:  # fill the prefix through both: one prompt call of L tokens
+        oracle.attention_decode(pre, H, KVH, D, theta, k, v, 0)
+        ref.forward_with_cache_attention(pre, H, KVH, D, theta, cache)
+    got = oracle.attention_decode(qkv, H, KVH, D, theta, k, v, L)
+    want = ref.forward_with_cache_attention(qkv, H, KVH, D, theta, cache, scale=scale, exp=exp)
+    # the cache contents agree too (GQA: every query head of kv head g holds g's rows)
+    for h in range(H):
+        assert np.array_equal(cache.k[h], k[h // (H // KVH), :L + m])
+        assert np.array_equal(cache.v[h], v[h // (H // KVH), :L + m])
+    return got, want
+
+
+@pytest.mark.parametrize("D", [8, 64])
+@pytest.mark.parametrize("L", [1, 5, 33])
+@pytest.mark.parametrize("m", [1, 3])
+def test_attention_matches_numpy_restatement(D, L, m):
+    got, want = _attention_case(4, 2, D, L, m, seed=1000 + 7 * D + L + m)
+    # non-uniform weights: the scores spread over more than a unit
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_attention_restatement_covers_mha_and_mqa():
+    for H, KVH in ((4, 4), (4, 1)):
+        got, want = _attention_case(H, KVH, 64, 9, 2, seed=77)
+        np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("mistake", ["scale 1/hd", "scale 1", "f64 scale", "exp2"])
+def test_attention_comparison_catches_planted_softmax_mistakes(mistake):
+    """A wrong temperature or base planted in the restatement (on the CPU) must
+    fail the comparison above: the check has the power to see it.  The f64 scale
+    1/sqrt(hd) is the reference's f32 scale rounded differently: at hd 8 it moves
+    results by ~1e-8, which the 1e-12 comparison sees."""
+    D = 8 if mistake == "f64 scale" else 64
+    scale = {"scale 1/hd": 1.0 / D, "scale 1": 1.0, "f64 scale": 1.0 / np.sqrt(D)}.get(mistake)
+    exp = np.exp2 if mistake == "exp2" else np.exp
+    got, want = _attention_case(4, 2, D, 5, 3, seed=4242, scale=scale, exp=exp)
+    assert not np.allclose(got, want, rtol=1e-12, atol=1e-12)

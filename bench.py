@@ -184,7 +184,7 @@ def cpu_baseline():
             break
     med = float(np.median(times))
     return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": threads,
-            "kind": "port",
+            "cpu": cpu_model(), "kind": "port",
             "sample": f"one Llama-2-7B layer's 5 Q4_0 GEMVs at m=1 ({nbytes / 1e6:.1f} MB), "
                       f"median of {len(times)} passes after 3 warm-ups, "
                       "candle QMatMul semantics restated in C (oracle/oracle.c), OpenMP",
@@ -192,6 +192,18 @@ def cpu_baseline():
 
 
 _CPU_WEIGHTS = {}
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), for every cpu_baseline."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_rows(qtype, n, k, rows, budget_s=1.5, seed=0):
@@ -225,7 +237,8 @@ def extra_cpu_baselines(extra):
     times as long); the stack times one layer's four projections and the lm_head
     (32 identical layers)."""
     def entry(value, unit, cores, sample):
-        return {"value": round(value, 3), "unit": unit, "cores": cores, "kind": "port",
+        return {"value": round(value, 3), "unit": unit, "cores": cores, "cpu": cpu_model(),
+                "kind": "port",
                 "sample": sample + "; candle QMatMul semantics restated in C (oracle/oracle.c), "
                                    "OpenMP over columns, median of timed calls"}
 
@@ -568,15 +581,16 @@ def prompt_step_e2e(torch, layers, head, gen, stream, timer):
     """A whole Llama-2-7B prompt step: m tokens into empty KV caches, per layer
     input_layernorm + QKV, attention (RoPE, append, causal softmax over the prompt:
     32 heads, hd 128, f32 cache), o_proj + residual, post_attention_layernorm +
-    gate_up + SwiGLU, down + residual; then the final norm + lm_head on the last
-    position only, as the reference's forward does.  Eager launches; the caches are
+    gate_up + SwiGLU, down + residual; then the final norm + lm_head over all m
+    positions, as LlamaModelV2::forward_with_cache does (llama.rs:445-449; generate
+    narrows to the last position afterwards).  Eager launches; the caches are
     rewound and the residual restarted outside each timed pass."""
     from unillm_amd import KvCache
     H, D = 32, 128
     res = {}
     gam = torch.ones(4096, device="cuda")
-    logits = torch.empty(1, 32000, device="cuda")
     for m in (512, 2048):
+        logits = torch.empty(m, 32000, device="cuda")
         h = torch.empty(m, 4096, device="cuda")
         qkv_out = torch.empty(m, 3 * 4096, device="cuda")
         att = torch.empty(m, 4096, device="cuda")
@@ -590,7 +604,7 @@ def prompt_step_e2e(torch, layers, head, gen, stream, timer):
                 o.forward_add(att, h, stream=stream)
                 gu.forward_swiglu(h, out=act, stream=stream, norm=(gam, None, 1e-6))
                 down.forward_add(act, h, stream=stream)
-            head.forward_norm(h[m - 1:], gam, eps=1e-6, out=logits, stream=stream)
+            head.forward_norm(h, gam, eps=1e-6, out=logits, stream=stream)
 
         def sample():
             for kv in caches:
@@ -601,13 +615,14 @@ def prompt_step_e2e(torch, layers, head, gen, stream, timer):
         with torch.cuda.stream(stream):
             sample()
             ms = float(np.median([sample() for _ in range(5)]))
-        flops = 32 * 2 * m * 4096 * (12288 + 4096 + 22016 + 11008)  # the linear layers
+        # the linear layers and the lm_head
+        flops = 2 * m * 4096 * (32 * (12288 + 4096 + 22016 + 11008) + 32000)
         res[f"llama2_7b_prompt_step_e2e_m{m}"] = {
             "ms_per_step": round(ms, 3), "tokens/s": round(m * 1e3 / ms, 1),
             "linear_TFLOP/s": round(flops / ms / 1e9, 1),
             "note": "norm+QKV, attention over the prompt, o+residual, norm+gate_up+SwiGLU, "
                     "down+residual a layer into empty caches; final norm + Q8_0 lm_head on "
-                    "the last position; eager launches"}
+                    "all m positions (forward_with_cache); eager launches"}
         del caches
     return res
 
@@ -695,6 +710,9 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "kernel": "gemv_kernel<Q4_0, M=1>",
                      "avg_launch_us": round(kern_ms * 1e3, 3),
+                     "avg_launch_us_source": "HIP events around the timed graph replays on "
+                                             "the launch stream / launches (launch gaps "
+                                             "included), not rocprof kernel durations",
                      "bytes_per_launch": nbytes // launches,
                      "traffic_source": traffic_src},
         "cpu_baseline": cpu,

@@ -58,6 +58,7 @@ extern "C" {
 
 typedef struct unillm_qweight unillm_qweight;
 typedef struct unillm_kv_cache unillm_kv_cache;
+typedef struct unillm_graph unillm_graph;
 
 /* Select and check the device (must be gfx950).  Replaces the device choice the
  * reference makes with `Device` (crates/runtime/src/tensor_core.rs:39-44), to
@@ -183,8 +184,9 @@ int unillm_hip_qmatmul_norm_swiglu(const unillm_qweight* w, const float* x_dev,
 int unillm_hip_select_path(const unillm_qweight* w, int64_t m);
 
 /* Grow `stream`'s workspace to what any qmatmul / _add / _norm call on w with up
- * to m rows needs (and, with swiglu != 0, the _swiglu / _norm_swiglu calls), so
- * such calls can then be captured into a HIP graph.  No counterpart in the
+ * to m rows needs (and, with swiglu != 0, the _swiglu / _norm_swiglu calls), x
+ * on any 4-byte boundary included, so such calls can then be captured into a
+ * HIP graph.  No counterpart in the
  * reference (candle allocates per call and has no graphs): it serves callers
  * that capture.  Allocates stream-ordered on `stream`; not while capturing. */
 int unillm_hip_qmatmul_reserve(const unillm_qweight* w, int64_t m, int swiglu, void* stream);
@@ -228,7 +230,9 @@ int unillm_hip_kv_cache_truncate(unillm_kv_cache* c, int64_t len);
  * advance it there, so a captured call appends at the next position on every
  * replay (a decode step captured once serves successive tokens).  A replayed
  * call past max_seq appends nothing, writes NaN and makes the next length query
- * or eager call fail with the overflow message; clear / truncate reset it. */
+ * or eager call fail with the overflow message; clear / truncate reset it.
+ * Alignment: qkv_dev 16 bytes; out_dev 4 bytes on a decode step, 16 bytes on a
+ * longer call (its kernels store 16 bytes at a time). */
 int unillm_hip_attention_decode(unillm_kv_cache* c, const float* qkv_dev, int64_t m,
                                 int64_t n_heads, float* out_dev, void* stream);
 
@@ -257,6 +261,23 @@ int unillm_hip_free(void* ptr);
 int unillm_hip_memcpy_htod(void* dst_dev, const void* src_host, size_t bytes);
 int unillm_hip_memcpy_dtoh(void* dst_host, const void* src_dev, size_t bytes);
 int unillm_hip_synchronize(void);
+
+/* Streams and HIP graphs for bindings without a HIP runtime of their own.  No
+ * counterpart in the reference (candle runs eagerly): they serve a decode step
+ * captured once and replayed per token, the loop of generate_with_cache
+ * (crates/runtime/src/models_v2/llama.rs:525-559).  Capture: reserve the
+ * workspaces of every call first (unillm_hip_qmatmul_reserve,
+ * unillm_hip_attention_reserve), call graph_begin on a stream from
+ * stream_create, issue the calls on it (nothing runs), then graph_end.  A
+ * replay (graph_launch, on any stream) runs the captured calls on the buffers
+ * they were given; attention calls append at the cache's current length. */
+int unillm_hip_stream_create(void** stream);
+int unillm_hip_stream_destroy(void* stream);
+int unillm_hip_stream_synchronize(void* stream);
+int unillm_hip_graph_begin(void* stream);
+int unillm_hip_graph_end(void* stream, unillm_graph** out);
+int unillm_hip_graph_launch(const unillm_graph* g, void* stream);
+int unillm_hip_graph_destroy(unillm_graph* g);
 
 #ifdef __cplusplus
 }

@@ -5,7 +5,8 @@
 //   test_host gpu <file.gguf> <file.expect>      load to the device + forward parity
 //   test_host cpu-kq / gpu-kq <q4_k_m.gguf> <.expect>   the Q4_K / Q6_K file: plan,
 //                                                 parity, QKV and gate+up fusion
-//   test_host gpu-step <file.gguf> <file.step>   LlamaModel::forward_with_cache logits
+//   test_host gpu-step <file.gguf> <file.step>   LlamaModel::forward_with_cache logits,
+//                                                 eager and as a captured decode step
 //
 // The .gguf / .expect pairs are written by tests/golden/make_gguf.py.
 #include <cmath>
@@ -299,6 +300,36 @@ static void test_gpu_step(const std::string& gguf, const std::string& step_path)
                     ea, eb);
         CHECK(ea < 1e-3 && eb < 1e-3);
         CHECK(c1.seq_len() == len && c2.seq_len() == len);
+    }
+    // The single tokens again through a captured decode step (the loop of
+    // generate_with_cache, llama.rs:525-559): the prompt eagerly, then one HIP graph
+    // captured once and replayed per token, each replay appending at the next position
+    // of every layer's cache.  Then the last token rolled back and run eagerly: the
+    // same logits.
+    for (const LlamaModel* model : {&fused, &split}) {
+        KVCache c = model->new_cache(64);
+        model->forward_with_cache(ids[0], c);
+        int64_t n = (int64_t)ids[0].size();
+        CapturedDecodeStep step(*model, c);
+        CHECK(c.seq_len() == n);  // capturing runs nothing
+        std::vector<float> last;
+        for (uint32_t s = 1; s < nsteps; ++s) {
+            CHECK(ids[s].size() == 1);
+            last = step.run(ids[s][0]).to_host();
+            ++n;
+            const double e = normwise(last, ref[s]);
+            std::printf("  captured step %u: normwise %.3g (%s)\n", s, e,
+                        model == &fused ? "fused" : "unfused");
+            CHECK(e < 1e-3);
+            CHECK(c.seq_len() == n);
+            for (size_t L = 0; L < c.num_layers(); ++L) CHECK(c.layer(L).seq_len() == n);
+        }
+        for (size_t L = 0; L < c.num_layers(); ++L) c.layer_mut(L).truncate(n - 1);
+        const std::vector<float> eager =
+            model->forward_with_cache({ids[nsteps - 1][0]}, c).to_host();
+        const std::vector<double> last64(last.begin(), last.end());
+        CHECK(normwise(eager, last64) < 1e-5);
+        CHECK(c.seq_len() == n);
     }
     // argument errors
     CHECK(throws_with([&] { fused.forward_with_cache({}, c1); }, "no input tokens"));

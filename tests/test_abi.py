@@ -89,3 +89,15 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_capi, "LIB_PATH", str(tmp_path / "nope.so"))
     with pytest.raises(ImportError, match="no CPU fallback"):
         _capi.lib()
+
+
+def test_graph_and_stream_entry_points_reject_null_on_the_host(lib):
+    # no GPU needed: every check below fails before the library touches a device
+    assert lib.unillm_hip_graph_begin(None) == _capi.ERR_INVALID_ARG
+    assert "null stream" in _capi.last_error()
+    out = ctypes.c_void_p(1)
+    assert lib.unillm_hip_graph_end(None, ctypes.byref(out)) == _capi.ERR_INVALID_ARG
+    assert lib.unillm_hip_graph_launch(None, None) == _capi.ERR_INVALID_ARG
+    assert lib.unillm_hip_graph_destroy(None) == _capi.OK
+    assert lib.unillm_hip_stream_destroy(None) == _capi.OK
+    assert lib.unillm_hip_stream_create(None) == _capi.ERR_INVALID_ARG

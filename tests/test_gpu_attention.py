@@ -128,6 +128,30 @@ def test_attention_overflow_and_limits():
     assert kv.seq_len == 0
 
 
+def test_attention_out_offset_by_one_float():
+    # out on a 4-byte boundary: a decode step stores per float and matches the
+    # oracle; a prompt-length call (16-byte stores) is refused before any launch
+    H, KVH, D = 8, 2, 64
+    w = (H + 2 * KVH) * D
+    kv = KvCache(KVH, D, 64)
+    kc = np.zeros((KVH, 64, D), np.float32)
+    vc = np.zeros((KVH, 64, D), np.float32)
+    for pos, m in enumerate((1, 2)):
+        length = kv.seq_len
+        qkv = oracle.normal(m * w, seed=60 + pos).reshape(m, w)
+        buf = torch.full((m * H * D + 1,), 7.0, device="cuda")
+        kv.attention(torch.from_numpy(qkv).cuda(), H, out=buf[1:].view(m, H * D))
+        ref = oracle.attention_decode(qkv, H, KVH, D, 10000.0, kc, vc, length)
+        got = buf.cpu().numpy()
+        assert got[0] == 7.0
+        assert oracle.normwise_error(got[1:].reshape(m, H * D), ref) < 1e-4
+    buf = torch.zeros(20 * H * D + 1, device="cuda")
+    with pytest.raises(HipError, match="16-byte aligned"):
+        kv.attention(torch.zeros(20, w, device="cuda"), H, out=buf[1:].view(20, H * D))
+    assert kv.seq_len == 3
+    assert not bool(buf.any())
+
+
 # ---- prompt-length calls (the prefill of generate_with_cache, llama.rs:488-497) ---------------
 
 @pytest.mark.parametrize("H,KVH,D,steps", [
@@ -249,6 +273,20 @@ def test_replay_past_max_seq_reports_overflow():
     assert bool(torch.isnan(out).all())
     with pytest.raises(HipError, match="KV cache overflow"):
         kv.seq_len
+    # the overflowing replay appended nothing: truncating keeps the intact prefix and
+    # clears the flag, and an eager call continues from it
+    kc = np.zeros((KVH, 3, D), np.float32)
+    vc = np.zeros((KVH, 3, D), np.float32)
+    q0 = qkv.cpu().numpy()
+    for pos in range(2):
+        oracle.attention_decode(q0, H, KVH, D, 10000.0, kc, vc, pos)
+    kv.truncate(2)
+    assert kv.seq_len == 2
+    t = oracle.normal(w, seed=6).reshape(1, w)
+    o = kv.attention(torch.from_numpy(t).cuda(), H).cpu().numpy()
+    ref = oracle.attention_decode(t, H, KVH, D, 10000.0, kc, vc, 2)
+    assert oracle.normwise_error(o, ref) < 1e-4
+    assert kv.seq_len == 3
     kv.clear()
     assert kv.seq_len == 0
     del g

@@ -13,7 +13,8 @@ import torch
 
 import oracle
 from oracle import Q4_0
-from unillm_amd import PATH_DECODE_MFMA, PATH_PREFILL_MFMA, HipError, KvCache, QuantLinear
+from unillm_amd import (PATH_DECODE_MFMA, PATH_GEMV, PATH_PREFILL_MFMA, HipError, KvCache,
+                        QuantLinear)
 
 pytestmark = pytest.mark.gpu
 
@@ -76,6 +77,35 @@ def test_reserved_stream_captures_and_replays(m, path):
         # (the captured buffer is retired, not freed, so the graph stays valid)
         with torch.cuda.stream(s):
             ql.forward(big if i == 1 else x, path=PATH_PREFILL_MFMA, stream=s)
+        s.synchronize()
+    del g
+
+
+@pytest.mark.parametrize("m,path", [(1, PATH_GEMV), (16, PATH_DECODE_MFMA),
+                                    (300, PATH_PREFILL_MFMA)])
+def test_reserved_stream_captures_x_on_a_4_byte_boundary(m, path):
+    # x one float past a 16-byte boundary is first copied into an aligned workspace:
+    # the reserve covers that copy too, on every path
+    n, k = 1024, 2048
+    blocks, ql = _weight(n, k, seed=61 + m)
+    s = torch.cuda.Stream()
+    ql.reserve(m, stream=s)
+    buf = torch.empty(m * k + 1, device="cuda")
+    x = buf[1:].view(m, k)
+    x.copy_(_x(m, k, seed=62 + m))
+    y = torch.empty(m, n, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s, capture_error_mode="thread_local"):
+        ql.forward(x, out=y, path=path, stream=s)
+    ref = oracle.qmatmul_f64(Q4_0, blocks, x.cpu().numpy(), n, k)
+    for i in range(3):
+        y.zero_()
+        with torch.cuda.stream(s):
+            g.replay()
+        s.synchronize()
+        assert oracle.normwise_error(y.cpu().numpy(), ref) < 1e-3, i
+        with torch.cuda.stream(s):  # eager work between replays
+            ql.forward(x, path=path, stream=s)
         s.synchronize()
     del g
 

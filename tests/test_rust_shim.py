@@ -26,6 +26,8 @@ C_TO_RUST = {
     "unillm_qweight**": "*mut *mut unillm_qweight",
     "const unillm_kv_cache*": "*const unillm_kv_cache",
     "unillm_kv_cache*": "*mut unillm_kv_cache", "unillm_kv_cache**": "*mut *mut unillm_kv_cache",
+    "const unillm_graph*": "*const unillm_graph", "unillm_graph*": "*mut unillm_graph",
+    "unillm_graph**": "*mut *mut unillm_graph",
 }
 
 

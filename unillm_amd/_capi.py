@@ -81,6 +81,13 @@ SIGNATURES = {
     "unillm_hip_memcpy_htod": ([P, P, ctypes.c_size_t], ctypes.c_int),
     "unillm_hip_memcpy_dtoh": ([P, P, ctypes.c_size_t], ctypes.c_int),
     "unillm_hip_synchronize": ([], ctypes.c_int),
+    "unillm_hip_stream_create": ([ctypes.POINTER(P)], ctypes.c_int),
+    "unillm_hip_stream_destroy": ([P], ctypes.c_int),
+    "unillm_hip_stream_synchronize": ([P], ctypes.c_int),
+    "unillm_hip_graph_begin": ([P], ctypes.c_int),
+    "unillm_hip_graph_end": ([P, ctypes.POINTER(P)], ctypes.c_int),
+    "unillm_hip_graph_launch": ([P, P], ctypes.c_int),
+    "unillm_hip_graph_destroy": ([P], ctypes.c_int),
 }
 
 

@@ -9,8 +9,6 @@ are disabled (-packed-fp32-ops) on every device pass.
 The C++ host layer (unillm_amd/host: GGUF reader, loader, QuantLinear) uses
 only the C ABI, so g++ builds it into libunillm_host.so, linked against
 libunillm_hip.so; its test program tests/cpp/test_host is built beside it.
-unillm_amd/probe/{stream_probe,decode_probe} (measurement only: the decode
-GEMV's streaming ceiling, the batched decode's weight stream) are built last.
 """
 from __future__ import annotations
 
@@ -29,9 +27,6 @@ SOURCES = ["capi.hip", "weights.hip", "gemv.hip", "decode.hip", "prefill.hip", "
 HOST_SOURCES = ["gguf.cpp", "unillm_host.cpp"]
 HOST_LIB = os.path.join(HERE, "libunillm_host.so")
 HOST_TEST = os.path.join(os.path.dirname(HERE), "tests", "cpp", "test_host")
-# measurement infrastructure (not part of the library): the HBM streaming-ceiling probe
-PROBES = [os.path.join(HERE, "probe", p)
-          for p in ("stream_probe", "decode_probe", "step_probe", "prefill_probe")]
 CXX = os.environ.get("CXX", "g++")
 CXXFLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
 FLAGS = [
@@ -66,7 +61,6 @@ def build(verbose: bool = False) -> str:
     if verbose:
         print(f"built {LIB}")
     build_host(verbose)
-    build_probe(verbose)
     return LIB
 
 
@@ -89,17 +83,6 @@ def build_host(verbose: bool = False) -> str:
     if verbose:
         print(f"built {HOST_LIB} and {HOST_TEST}")
     return HOST_LIB
-
-
-def build_probe(verbose: bool = False) -> None:
-    """unillm_amd/probe: the decode GEMV's streaming-ceiling probe, the batched
-    decode's weight-stream probe, the headline step's chain probe and the prefill
-    loop's skeleton probe (measurement only)."""
-    for probe in PROBES:
-        _run([HIPCC, *FLAGS, "-o", probe, probe + ".hip", "-L" + HERE, "-lunillm_hip",
-              "-Wl,-rpath,$ORIGIN/.."])
-        if verbose:
-            print(f"built {probe}")
 
 
 if __name__ == "__main__":

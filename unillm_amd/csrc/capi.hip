@@ -510,6 +510,8 @@ int unillm_hip_qmatmul_reserve(const unillm_qweight* w, int64_t m, int swiglu, v
     // slot 1: the [gate | up] product of a SwiGLU call off the GEMV path
     if (e == hipSuccess && swiglu)
         e = stream_workspace(s, (size_t)m * (size_t)w->n * sizeof(float), &p, 1);
+    // slot 3: the aligned copy of an x that sits only on a 4-byte boundary (any path)
+    if (e == hipSuccess) e = stream_workspace(s, (size_t)m * (size_t)w->k * sizeof(float), &p, 3);
     return e == hipSuccess ? UNILLM_OK : fail_launch(e, "reserve");
 }
 
@@ -608,8 +610,10 @@ int unillm_hip_kv_cache_destroy(unillm_kv_cache* c) {
 namespace {
 // The cache's device state after all work issued so far on `s` (s == nullptr and
 // device_wide: after all work on the device): refreshes the host's copy of the length.
-// A replayed call that overflowed is reported with the reference's message.
-int refresh_length(unillm_kv_cache* c, hipStream_t s, bool device_wide) {
+// A replayed call that overflowed is reported with the reference's message, unless
+// report_overflow is false (a truncate, which clears the flag, reads the length only).
+int refresh_length(unillm_kv_cache* c, hipStream_t s, bool device_wide,
+                   bool report_overflow = true) {
     int st[2] = {0, 0};
     hipError_t e = device_wide ? hipDeviceSynchronize() : hipSuccess;
     if (e == hipSuccess) e = hipMemcpyAsync(st, c->state, sizeof(st), hipMemcpyDeviceToHost, s);
@@ -619,7 +623,7 @@ int refresh_length(unillm_kv_cache* c, hipStream_t s, bool device_wide) {
     // once a call on this cache has been captured, replays may run at any time
     // between calls: the host copy is read back before every later use
     c->len_stale = c->captured;
-    if (st[1])
+    if (st[1] && report_overflow)
         return fail(UNILLM_ERR_INVALID_ARG,
                     "KV cache append failed: KV cache overflow in a replayed call: current_len=" +
                         std::to_string(st[0]) + ", max_seq_len=" + std::to_string(c->max_seq));
@@ -654,8 +658,10 @@ int unillm_hip_kv_cache_clear(unillm_kv_cache* c) {
 
 int unillm_hip_kv_cache_truncate(unillm_kv_cache* c, int64_t len) {
     if (!c) return fail(UNILLM_ERR_INVALID_ARG, "cache is NULL");
+    // a replay that overflowed appended nothing: the length it left is intact, and
+    // set_length below clears the flag, so truncating recovers the prefix
     if (c->len_stale) {
-        if (int rc = refresh_length(c, nullptr, true)) return rc;
+        if (int rc = refresh_length(c, nullptr, true, false)) return rc;
     }
     if (len < 0 || len > c->len)
         return fail(UNILLM_ERR_INVALID_ARG, "KV cache truncate: length " + std::to_string(len) +
@@ -679,6 +685,12 @@ int unillm_hip_attention_decode(unillm_kv_cache* c, const float* qkv_dev, int64_
     if (e != hipSuccess) return fail_hip(e, "attention: hipStreamIsCapturing");
     const bool capturing = cs != hipStreamCaptureStatusNone;
     const bool decode = m * (n_heads / c->n_kv_heads) <= attention_max_queries();
+    // the prompt kernels store out 16 bytes at a time
+    if (!decode && !aligned16(out_dev))
+        return fail(UNILLM_ERR_INVALID_ARG,
+                    "attention: a prompt-length call (more than " +
+                        std::to_string(attention_max_queries()) +
+                        " queries a kv head) takes out 16-byte aligned");
     if (capturing) {
         // the kernels read the length from the device at each replay: the grid covers
         // the longest the cache holds, and the host's copy is unknown afterwards
@@ -739,6 +751,66 @@ int unillm_hip_synchronize(void) {
     if (int rc = ensure_init()) return rc;
     hipError_t e = hipDeviceSynchronize();
     return e == hipSuccess ? UNILLM_OK : fail_hip(e, "hipDeviceSynchronize");
+}
+
+int unillm_hip_stream_create(void** stream) {
+    if (!stream) return fail(UNILLM_ERR_INVALID_ARG, "stream is NULL");
+    *stream = nullptr;
+    if (int rc = ensure_init()) return rc;
+    hipStream_t s = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);  // default priority
+    if (e != hipSuccess) return fail_hip(e, "hipStreamCreate");
+    *stream = s;
+    return UNILLM_OK;
+}
+
+int unillm_hip_stream_destroy(void* stream) {
+    if (!stream) return UNILLM_OK;
+    hipError_t e = hipStreamDestroy(static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? UNILLM_OK : fail_hip(e, "hipStreamDestroy");
+}
+
+int unillm_hip_stream_synchronize(void* stream) {
+    if (int rc = ensure_init()) return rc;
+    hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? UNILLM_OK : fail_hip(e, "hipStreamSynchronize");
+}
+
+int unillm_hip_graph_begin(void* stream) {
+    if (!stream)
+        return fail(UNILLM_ERR_INVALID_ARG, "graph capture needs a stream (not the null stream)");
+    if (int rc = ensure_init()) return rc;
+    // thread-local mode: other threads' HIP calls do not invalidate the capture
+    hipError_t e = hipStreamBeginCapture(static_cast<hipStream_t>(stream),
+                                         hipStreamCaptureModeThreadLocal);
+    return e == hipSuccess ? UNILLM_OK : fail_hip(e, "hipStreamBeginCapture");
+}
+
+int unillm_hip_graph_end(void* stream, unillm_graph** out) {
+    if (!stream || !out) return fail(UNILLM_ERR_INVALID_ARG, "stream or out is NULL");
+    *out = nullptr;
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(static_cast<hipStream_t>(stream), &g);
+    if (e != hipSuccess) return fail_hip(e, "hipStreamEndCapture");
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return fail_hip(e, "hipGraphInstantiate");
+    *out = reinterpret_cast<unillm_graph*>(x);
+    return UNILLM_OK;
+}
+
+int unillm_hip_graph_launch(const unillm_graph* g, void* stream) {
+    if (!g) return fail(UNILLM_ERR_INVALID_ARG, "graph is NULL");
+    hipError_t e = hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(const_cast<unillm_graph*>(g)),
+                                  static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? UNILLM_OK : fail_hip(e, "hipGraphLaunch");
+}
+
+int unillm_hip_graph_destroy(unillm_graph* g) {
+    if (!g) return UNILLM_OK;
+    hipError_t e = hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(g));
+    return e == hipSuccess ? UNILLM_OK : fail_hip(e, "hipGraphExecDestroy");
 }
 
 }  // extern "C"

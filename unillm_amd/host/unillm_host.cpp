@@ -538,14 +538,22 @@ void LayerKVCache::truncate(int64_t len) { check_msg(unillm_hip_kv_cache_truncat
 Tensor LayerKVCache::attend(const Tensor& qkv, int64_t n_heads, void* stream) {
     if (!qkv.device().is_hip() || qkv.shape().size() != 2)
         throw Error("attention: qkv must be a [m, (n_heads + 2 n_kv_heads) head_dim] HIP tensor");
+    Tensor out = Tensor::empty({qkv.dim(0), n_heads * head_dim_}, qkv.device());
+    attend_into(qkv, n_heads, out, stream);
+    return out;
+}
+
+void LayerKVCache::attend_into(const Tensor& qkv, int64_t n_heads, Tensor& out, void* stream) {
+    if (!qkv.device().is_hip() || qkv.shape().size() != 2)
+        throw Error("attention: qkv must be a [m, (n_heads + 2 n_kv_heads) head_dim] HIP tensor");
     if (n_heads < 1 || qkv.dim(-1) != (n_heads + 2 * n_kv_heads_) * head_dim_)
         throw Error("attention: qkv width " + std::to_string(qkv.dim(-1)) + " is not (" +
                     std::to_string(n_heads) + " + 2 x " + std::to_string(n_kv_heads_) + ") x " +
                     std::to_string(head_dim_));
     const int64_t m = qkv.dim(0);
-    Tensor out = Tensor::empty({m, n_heads * head_dim_}, qkv.device());
+    if (!out.device().is_hip() || out.numel() != m * n_heads * head_dim_)
+        throw Error("attention: out must be a HIP tensor of [m, n_heads head_dim]");
     check_msg(unillm_hip_attention_decode(c_, qkv.data(), m, n_heads, out.data_mut(), stream));
-    return out;
 }
 
 KVCache KVCache::with_capacity(size_t num_layers, int64_t n_kv_heads, int64_t head_dim,
@@ -648,15 +656,8 @@ KVCache LlamaModel::new_cache(int64_t max_seq_len) const {
                                   w_.config.rope_theta);
 }
 
-Tensor LlamaModel::forward_with_cache(const std::vector<int32_t>& input_ids, KVCache& cache,
-                                      void* stream) const {
-    const int64_t m = (int64_t)input_ids.size();
-    if (m == 0) throw Error("forward_with_cache: no input tokens");
-    if (cache.num_layers() != layers_.size())
-        throw Error("forward_with_cache: the cache has " + std::to_string(cache.num_layers()) +
-                    " layers, the model " + std::to_string(layers_.size()));
-    // 1. token embedding (ops_fn::embedding: rows of the table)
-    const int64_t vocab = embed_.dim(0);
+std::vector<float> LlamaModel::embed_rows(const std::vector<int32_t>& input_ids) const {
+    const int64_t m = (int64_t)input_ids.size(), vocab = embed_.dim(0);
     std::vector<float> rows((size_t)(m * hidden_));
     const float* table = embed_.data();
     for (int64_t t = 0; t < m; ++t) {
@@ -667,40 +668,126 @@ Tensor LlamaModel::forward_with_cache(const std::vector<int32_t>& input_ids, KVC
         std::copy(table + (int64_t)id * hidden_, table + ((int64_t)id + 1) * hidden_,
                   rows.begin() + t * hidden_);
     }
-    Tensor h = Tensor::from_host(rows, {m, hidden_}, Device::hip(0));
-    // 2. the decoder layers
+    return rows;
+}
+
+LlamaModel::StepBuffers LlamaModel::step_buffers(int64_t m) const {
+    const Device d = Device::hip(0);
+    StepBuffers b;
+    b.m = m;
+    b.h = Tensor::empty({m, hidden_}, d);
+    b.qkv = Tensor::empty({m, hidden_ + 2 * kv_heads_ * head_dim_}, d);
+    b.att = Tensor::empty({m, hidden_}, d);
+    b.act = Tensor::empty({m, (int64_t)w_.config.intermediate_size}, d);
+    b.logits = Tensor::empty({m, lm_head_->n()}, d);
+    return b;
+}
+
+void LlamaModel::forward_layers(StepBuffers& b, KVCache& cache, void* stream) const {
+    const int64_t m = b.m;
+    if (cache.num_layers() != layers_.size())
+        throw Error("forward_with_cache: the cache has " + std::to_string(cache.num_layers()) +
+                    " layers, the model " + std::to_string(layers_.size()));
+    // 2. the decoder layers (llama.rs:654-680)
     const int64_t kvw = kv_heads_ * head_dim_, width = hidden_ + 2 * kvw;
+    float* h = b.h.data_mut();
     for (size_t L = 0; L < layers_.size(); ++L) {
         const Layer& l = layers_[L];
-        Tensor qkv;
-        if (l.qkv) {
-            qkv = l.qkv->forward_norm(h, l.in_norm, nullptr, 1e-6f, stream);
+        if (l.qkv) {  // input_layernorm fused into the q/k/v projection
+            check_qmatmul(unillm_hip_qmatmul_norm(l.qkv->handle(), h, l.in_norm.data(), nullptr,
+                                                  1e-6f, m, b.qkv.data_mut(), stream),
+                          "QMatMul forward failed");
         } else {  // parts of different GGUF types: each part into its columns, a row at a time
-            qkv = Tensor::empty({m, width}, Device::hip(0));
             const std::pair<const QuantLinear*, int64_t> parts[3] = {
                 {l.q.get(), 0}, {l.k.get(), hidden_}, {l.v.get(), hidden_ + kvw}};
             for (int64_t t = 0; t < m; ++t)
                 for (const auto& [q, off] : parts)
-                    check_qmatmul(unillm_hip_qmatmul_norm(q->handle(), h.data() + t * hidden_,
+                    check_qmatmul(unillm_hip_qmatmul_norm(q->handle(), h + t * hidden_,
                                                           l.in_norm.data(), nullptr, 1e-6f, 1,
-                                                          qkv.data_mut() + t * width + off,
+                                                          b.qkv.data_mut() + t * width + off,
                                                           stream),
                                   "QMatMul forward failed");
         }
-        const Tensor att = cache.layer_mut(L).attend(qkv, heads_, stream);
-        l.o->forward_add(att, h, stream);
-        const Tensor act = l.gate_up->forward_norm_swiglu(h, l.post_norm, nullptr, 1e-6f, stream);
-        l.down->forward_add(act, h, stream);
+        cache.layer_mut(L).attend_into(b.qkv, heads_, b.att, stream);
+        check_qmatmul(unillm_hip_qmatmul_add(l.o->handle(), b.att.data(), m, h, stream),
+                      "QMatMul forward failed");
+        check_qmatmul(unillm_hip_qmatmul_norm_swiglu(l.gate_up->handle(), h, l.post_norm.data(),
+                                                     nullptr, 1e-6f, m, b.act.data_mut(), stream),
+                      "QMatMul forward failed");
+        check_qmatmul(unillm_hip_qmatmul_add(l.down->handle(), b.act.data(), m, h, stream),
+                      "QMatMul forward failed");
     }
-    // 3. final norm fused into the head (lm_head_forward's error context)
+    // 3. final norm fused into the head (lm_head_forward's error context, llama.rs:399)
+    check_qmatmul(unillm_hip_qmatmul_norm(lm_head_->handle(), h, norm_.data(), nullptr,
+                                          w_.config.rms_norm_eps, m, b.logits.data_mut(), stream),
+                  "QMatMul lm_head forward failed");
+}
+
+Tensor LlamaModel::forward_with_cache(const std::vector<int32_t>& input_ids, KVCache& cache,
+                                      void* stream) const {
+    const int64_t m = (int64_t)input_ids.size();
+    if (m == 0) throw Error("forward_with_cache: no input tokens");
+    if (cache.num_layers() != layers_.size())
+        throw Error("forward_with_cache: the cache has " + std::to_string(cache.num_layers()) +
+                    " layers, the model " + std::to_string(layers_.size()));
+    // 1. token embedding (ops_fn::embedding: rows of the table); the outputs are
+    // freshly allocated per call, as the reference's are
+    const std::vector<float> rows = embed_rows(input_ids);
+    StepBuffers b = step_buffers(m);
+    b.h = Tensor::from_host(rows, {m, hidden_}, Device::hip(0));
+    forward_layers(b, cache, stream);
+    return b.logits;
+}
+
+// ---- CapturedDecodeStep --------------------------------------------------------------------
+CapturedDecodeStep::CapturedDecodeStep(const LlamaModel& model, KVCache& cache)
+    : model_(model), b_(model.step_buffers(1)) {
+    if (cache.num_layers() != model.layers_.size())
+        throw Error("CapturedDecodeStep: the cache has " + std::to_string(cache.num_layers()) +
+                    " layers, the model " + std::to_string(model.layers_.size()));
+    check_msg(unillm_hip_stream_create(&stream_));
     try {
-        return lm_head_->forward_norm(h, norm_, nullptr, w_.config.rms_norm_eps, stream);
-    } catch (const Error& e) {
-        std::string msg = e.what();
-        const std::string p = "QMatMul forward failed: ";
-        if (msg.compare(0, p.size(), p) == 0) msg = msg.substr(p.size());
-        throw Error("QMatMul lm_head forward failed: " + msg);
+        // a capture cannot allocate: every call's workspace is grown first, on this stream
+        for (size_t L = 0; L < model.layers_.size(); ++L) {
+            const LlamaModel::Layer& l = model.layers_[L];
+            for (const auto* q : {l.qkv.get(), l.q.get(), l.k.get(), l.v.get(), l.o.get(),
+                                  l.down.get()})
+                if (q) check_msg(unillm_hip_qmatmul_reserve(q->handle(), 1, 0, stream_));
+            check_msg(unillm_hip_qmatmul_reserve(l.gate_up->handle(), 1, 1, stream_));
+            check_msg(unillm_hip_attention_reserve(cache.layer(L).handle(), 1, model.heads_,
+                                                   stream_));
+        }
+        check_msg(unillm_hip_qmatmul_reserve(model.lm_head_->handle(), 1, 0, stream_));
+        check_msg(unillm_hip_stream_synchronize(stream_));
+        check_msg(unillm_hip_graph_begin(stream_));
+        try {
+            model.forward_layers(b_, cache, stream_);
+        } catch (...) {
+            unillm_graph* g = nullptr;  // end the failed capture; its graph is discarded
+            if (unillm_hip_graph_end(stream_, &g) == UNILLM_OK) unillm_hip_graph_destroy(g);
+            throw;
+        }
+        check_msg(unillm_hip_graph_end(stream_, &graph_));
+    } catch (...) {
+        unillm_hip_stream_destroy(stream_);
+        throw;
     }
+}
+
+CapturedDecodeStep::~CapturedDecodeStep() {
+    if (stream_) unillm_hip_stream_synchronize(stream_);
+    unillm_hip_graph_destroy(graph_);
+    unillm_hip_stream_destroy(stream_);
+}
+
+const Tensor& CapturedDecodeStep::run(int32_t token) {
+    const std::vector<float> row = model_.embed_rows({token});
+    // the previous replay reads and rewrites h: it must be done before the new row lands
+    check_msg(unillm_hip_stream_synchronize(stream_));
+    check_msg(unillm_hip_memcpy_htod(b_.h.data_mut(), row.data(), row.size() * sizeof(float)));
+    check_msg(unillm_hip_graph_launch(graph_, stream_));
+    check_msg(unillm_hip_stream_synchronize(stream_));
+    return b_.logits;
 }
 
 }  // namespace unillm

@@ -173,6 +173,8 @@ public:
     // (LayerKVCache::append, kv_cache.rs:91-130, including its overflow error), causal
     // softmax attention -> [m, n_heads head_dim], freshly allocated.
     Tensor attend(const Tensor& qkv, int64_t n_heads, void* stream = nullptr);
+    // attend into a caller's HIP buffer of m * n_heads * head_dim floats (no allocation).
+    void attend_into(const Tensor& qkv, int64_t n_heads, Tensor& out, void* stream = nullptr);
 
     int64_t n_kv_heads() const { return n_kv_heads_; }
     int64_t head_dim() const { return head_dim_; }
@@ -289,6 +291,8 @@ public:
 // The weights must hold the fused gate_up handle of every layer (load with
 // LoadOptions::fuse_gate_up); q/k/v use the fused qkv handle where the loader made
 // one, else the three projections run a token at a time into the qkv rows.
+class CapturedDecodeStep;
+
 class LlamaModel {
 public:
     explicit LlamaModel(ModelWeights weights);  // throws if a tensor is missing
@@ -306,16 +310,57 @@ public:
                               void* stream = nullptr) const;
 
 private:
+    friend class CapturedDecodeStep;
     struct Layer {
         Tensor in_norm, post_norm;  // HIP, hidden_size each
         std::shared_ptr<QuantLinear> qkv, q, k, v, o, gate_up, down;
     };
+    // The device buffers of one call of m tokens: h holds the embedded rows and is the
+    // residual stream the layers add into; qkv, att and act are the per-layer
+    // intermediates (reused by every layer); logits [m, vocab].
+    struct StepBuffers {
+        int64_t m = 0;
+        Tensor h, qkv, att, act, logits;
+    };
+    StepBuffers step_buffers(int64_t m) const;
+    // The embedding rows of input_ids (ops_fn::embedding), on the host.
+    std::vector<float> embed_rows(const std::vector<int32_t>& input_ids) const;
+    // Steps 2 and 3 of forward_with_cache on b.h: launches only, into b's buffers (no
+    // allocation), so a step can be captured into a HIP graph.
+    void forward_layers(StepBuffers& b, KVCache& cache, void* stream) const;
     ModelWeights w_;
     int64_t hidden_ = 0, heads_ = 0, kv_heads_ = 0, head_dim_ = 0;
     Tensor embed_;  // host [vocab, hidden] (shares w_'s storage)
     std::vector<Layer> layers_;
     Tensor norm_;  // HIP
     std::shared_ptr<QuantLinear> lm_head_;
+};
+
+// The loop of LlamaModelV2::generate_with_cache (llama.rs:525-559) a token at a time,
+// as a HIP graph: one m = 1 call of forward_with_cache (every layer's norm + q/k/v,
+// attention with the layer's cache, o_proj + residual, norm + gate_up + SwiGLU,
+// down + residual, then the final norm + lm_head) captured once over device buffers of
+// its own, and replayed per token.  The attention kernels read and advance each
+// layer's cache length on the device, so replay i appends at the position the cache
+// holds then.  The model and the cache must outlive the step; other calls on the cache
+// (an eager prompt first, a truncate between tokens) keep working.
+class CapturedDecodeStep {
+public:
+    // Reserves the workspaces and captures on a stream of its own (nothing runs).
+    CapturedDecodeStep(const LlamaModel& model, KVCache& cache);
+    ~CapturedDecodeStep();
+    CapturedDecodeStep(const CapturedDecodeStep&) = delete;
+    CapturedDecodeStep& operator=(const CapturedDecodeStep&) = delete;
+    // Copies token's embedding row into the step's input and replays the graph:
+    // logits [1, vocab] on the device (the step's own buffer, rewritten by the next
+    // run); the cache grows by one.  Waits for the previous replay first.
+    const Tensor& run(int32_t token);
+
+private:
+    const LlamaModel& model_;
+    void* stream_ = nullptr;
+    unillm_graph* graph_ = nullptr;
+    LlamaModel::StepBuffers b_;
 };
 
 }  // namespace unillm

@@ -39,6 +39,11 @@ pub mod sys {
     pub struct unillm_kv_cache {
         _private: [u8; 0],
     }
+    /// Opaque instantiated HIP graph.
+    #[repr(C)]
+    pub struct unillm_graph {
+        _private: [u8; 0],
+    }
 
     pub const UNILLM_QTYPE_Q4_0: c_int = 2;
     pub const UNILLM_QTYPE_Q8_0: c_int = 8;
@@ -112,6 +117,13 @@ pub mod sys {
         pub fn unillm_hip_memcpy_dtoh(dst_host: *mut c_void, src_dev: *const c_void,
                                       bytes: usize) -> c_int;
         pub fn unillm_hip_synchronize() -> c_int;
+        pub fn unillm_hip_stream_create(stream: *mut *mut c_void) -> c_int;
+        pub fn unillm_hip_stream_destroy(stream: *mut c_void) -> c_int;
+        pub fn unillm_hip_stream_synchronize(stream: *mut c_void) -> c_int;
+        pub fn unillm_hip_graph_begin(stream: *mut c_void) -> c_int;
+        pub fn unillm_hip_graph_end(stream: *mut c_void, out: *mut *mut unillm_graph) -> c_int;
+        pub fn unillm_hip_graph_launch(g: *const unillm_graph, stream: *mut c_void) -> c_int;
+        pub fn unillm_hip_graph_destroy(g: *mut unillm_graph) -> c_int;
     }
 }
 

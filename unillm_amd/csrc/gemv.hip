@@ -422,7 +422,8 @@ constexpr int gemv_threads() {
 // (x - mean) / sqrt(var + eps) * gamma (+ beta), var the mean of the squared
 // deviations (the reference's ops_fn::layer_norm before the projections,
 // tensor_core.rs:973-1008).  Every workgroup reads all of x anyway, so each
-// computes the row statistics itself: two block reductions, no extra launch.
+// computes the row statistics itself (one barrier, gamma and beta requested with x),
+// no extra launch.
 template <int QT, int M, int NB, int R, int THREADS, bool PAIR = false, bool NORM = false>
 __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict__ base,
                                                        int64_t rb,
@@ -489,6 +490,26 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
               *reinterpret_cast<const float4*>(xb + o1));
     }
 
+    // gamma and beta of this thread's quarters (the norm), requested with x
+    float gmv[NORM ? PASSES : 1][8], btv[NORM ? PASSES : 1][8];
+    if constexpr (NORM) {
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            if (wave0 + p * THREADS >= nq) continue;
+            const int q = min((int)threadIdx.x + p * THREADS, nq - 1);
+            const int blk = q >> 2;
+            const int m = blk / KB;
+            const int64_t e = (int64_t)(blk - m * KB) * QK;
+            int o0, o1;
+            quarter_offsets<QT>(q & 3, o0, o1);
+            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+            order(gmv[p], *reinterpret_cast<const float4*>(norm.gamma + e + o0),
+                  *reinterpret_cast<const float4*>(norm.gamma + e + o1));
+            order(btv[p], norm.beta ? *reinterpret_cast<const float4*>(norm.beta + e + o0) : z,
+                  norm.beta ? *reinterpret_cast<const float4*>(norm.beta + e + o1) : z);
+        }
+    }
+
     // 2. the first chunk of weights: one chunk per wave keeps the memory
     //    pipeline busy while x arrives and is turned into digits, without
     //    filling it -- instructions issue in order, and once weight loads back
@@ -497,31 +518,17 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     Chunk<QT, NB, R> a, b;
     load_chunk<QT, NB, R, PAIR>(a, base, (uint32_t)rb, wrow, waves, 0, jlast, poff, soff, hoff, I);
 
-    // 2b. the layer norm of x: row means, then the mean squared deviations (the
-    //     reference's two passes), each summed by DPP within a wave and over the
-    //     waves in LDS (separate arrays: one barrier each); only real quarters
-    //     count.  gamma and beta are read after the sums, so the loads issued
-    //     before the first weights stay x alone.
+    // 2b. the layer norm of x.  Each wave takes its elements' count, mean and sum
+    //     of squared deviations from that mean (two DPP sums, no barrier); the
+    //     waves' triples meet in LDS behind one barrier and combine exactly
+    //     (Chan et al.: M2 = sum M2_w + sum n_w (mean_w - mean)^2).  Two passes
+    //     over the data within a wave, as the reference's two passes.
     if constexpr (NORM) {
-        __shared__ float red[2][M * WAVES];
+        __shared__ float red[3][M * WAVES];
         const int wv = threadIdx.x >> 6;
-        auto block_sum = [&](float (&acc)[M], float (&out)[M], float* r) {
+        float s[M], c[M];
 #pragma unroll
-            for (int mm = 0; mm < M; ++mm) {
-                const float t = wave_sum(acc[mm]);
-                if (lane == 0) r[mm * WAVES + wv] = t;
-            }
-            __syncthreads();
-#pragma unroll
-            for (int mm = 0; mm < M; ++mm) {
-                float t = 0.0f;
-                for (int w2 = 0; w2 < WAVES; ++w2) t += r[mm * WAVES + w2];
-                out[mm] = t;
-            }
-        };
-        float acc[M], mean[M], sd[M];
-#pragma unroll
-        for (int mm = 0; mm < M; ++mm) acc[mm] = 0.0f;
+        for (int mm = 0; mm < M; ++mm) s[mm] = c[mm] = 0.0f;
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             if (wave0 + p * THREADS >= nq) continue;
@@ -531,52 +538,69 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
 #pragma unroll
             for (int j = 0; j < 8; ++j) t += v[p][j];
 #pragma unroll
-            for (int mm = 0; mm < M; ++mm) acc[mm] += q < nq && m == mm ? t : 0.0f;
+            for (int mm = 0; mm < M; ++mm) {
+                s[mm] += q < nq && m == mm ? t : 0.0f;
+                c[mm] += q < nq && m == mm ? 8.0f : 0.0f;
+            }
         }
-        block_sum(acc, mean, red[0]);
+        float mw[M], nw[M];
 #pragma unroll
         for (int mm = 0; mm < M; ++mm) {
-            mean[mm] = mean[mm] / (float)K;
-            acc[mm] = 0.0f;
+            nw[mm] = wave_sum(c[mm]);
+            const float sw = wave_sum(s[mm]);
+            mw[mm] = nw[mm] > 0.0f ? sw / nw[mm] : 0.0f;
+            s[mm] = 0.0f;
         }
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             if (wave0 + p * THREADS >= nq) continue;
             const int q = (int)threadIdx.x + p * THREADS;
             const int m = min(q, nq - 1) / (4 * KB);
-            float mu = mean[0];
+            float mu = mw[0];
 #pragma unroll
-            for (int mm = 1; mm < M; ++mm) mu = m == mm ? mean[mm] : mu;
+            for (int mm = 1; mm < M; ++mm) mu = m == mm ? mw[mm] : mu;
             float t = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) t += (v[p][j] - mu) * (v[p][j] - mu);
 #pragma unroll
-            for (int mm = 0; mm < M; ++mm) acc[mm] += q < nq && m == mm ? t : 0.0f;
+            for (int mm = 0; mm < M; ++mm) s[mm] += q < nq && m == mm ? t : 0.0f;
         }
-        block_sum(acc, sd, red[1]);
 #pragma unroll
-        for (int mm = 0; mm < M; ++mm) sd[mm] = sqrtf(sd[mm] / (float)K + norm.eps);
+        for (int mm = 0; mm < M; ++mm) {
+            const float m2 = wave_sum(s[mm]);
+            if (lane == 0) {
+                red[0][mm * WAVES + wv] = nw[mm];
+                red[1][mm * WAVES + wv] = mw[mm];
+                red[2][mm * WAVES + wv] = m2;
+            }
+        }
+        __syncthreads();
+        float mean[M], sd[M];
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) {
+            float sum = 0.0f;
+            for (int w2 = 0; w2 < WAVES; ++w2) sum += red[0][mm * WAVES + w2] * red[1][mm * WAVES + w2];
+            mean[mm] = sum / (float)K;
+            float m2 = 0.0f;
+            for (int w2 = 0; w2 < WAVES; ++w2) {
+                const float d = red[1][mm * WAVES + w2] - mean[mm];
+                m2 += red[2][mm * WAVES + w2] + red[0][mm * WAVES + w2] * d * d;
+            }
+            sd[mm] = sqrtf(m2 / (float)K + norm.eps);
+        }
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             if (wave0 + p * THREADS >= nq) continue;
             const int q = min((int)threadIdx.x + p * THREADS, nq - 1);
-            const int blk = q >> 2;
-            const int m = blk / KB;
+            const int m = (q >> 2) / KB;
             float mu = mean[0], sg = sd[0];
 #pragma unroll
             for (int mm = 1; mm < M; ++mm) {
                 mu = m == mm ? mean[mm] : mu;
                 sg = m == mm ? sd[mm] : sg;
             }
-            int o0, o1;
-            quarter_offsets<QT>(q & 3, o0, o1);
-            const int64_t e = (int64_t)(blk - m * KB) * QK;
-            float g[8], bb[8];
-            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-            order(g, *reinterpret_cast<const float4*>(norm.gamma + e + o0),
-                  *reinterpret_cast<const float4*>(norm.gamma + e + o1));
-            order(bb, norm.beta ? *reinterpret_cast<const float4*>(norm.beta + e + o0) : z,
-                  norm.beta ? *reinterpret_cast<const float4*>(norm.beta + e + o1) : z);
+            const float (&g)[8] = gmv[p];
+            const float (&bb)[8] = btv[p];
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[p][j] = (v[p][j] - mu) / sg * g[j] + bb[j];
         }

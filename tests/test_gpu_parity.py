@@ -398,6 +398,45 @@ def test_x_on_4_byte_boundary(m, path):
     assert oracle.normwise_error(b, oracle.qmatmul_f64(Q4_0, blocks, x, n, k)) < 1e-3
 
 
+def test_batched_decode_back_to_back_calls_on_one_stream():
+    # Batched decode at m <= 16 runs in one launch: k slice 0 of each row group zeroes
+    # y's tile and raises a flag, the other slices add after it, and the last slice
+    # resets the flag for the next launch.  Calls of different shapes, widths and
+    # qtypes issued back to back on one stream (no synchronisation between them) must
+    # each match the oracle; a stale flag would let a slice add onto y's old contents.
+    cases = [(Q4_0, 9, 4096, 2048), (Q8_0, 16, 1000, 4096), (Q4_0, 5, 12288, 4096),
+             (Q4_0, 16, 300, 11008), (Q8_0, 7, 4096, 1024), (Q4_0, 16, 4096, 2048)]
+    runs = []
+    for i, (qtype, m, n, k) in enumerate(cases):
+        blocks, x = _case(qtype, m, n, k, seed=300 + i)
+        ql = QuantLinear.from_blocks(qtype, n, k, blocks)
+        assert ql.select_path(m) == PATH_DECODE_MFMA
+        runs.append((qtype, m, n, k, blocks, x, ql, _dev(x)))
+    outs = []
+    for rep in range(3):
+        ys = [torch.full((m, n), float("nan"), device="cuda") for _, m, n, *_ in runs]
+        for (qtype, m, n, k, blocks, x, ql, xd), y in zip(runs, ys):
+            ql.forward(xd, out=y)
+        torch.cuda.synchronize()
+        outs.append([y.cpu().numpy() for y in ys])
+    for i, (qtype, m, n, k, blocks, x, ql, xd) in enumerate(runs):
+        ref = oracle.qmatmul_f64(qtype, blocks, x, n, k)
+        assert oracle.normwise_error(outs[0][i], ref) < 1e-3, cases[i]
+        for rep in (1, 2):  # the adds' order may vary: f32 rounding, not bitwise
+            assert oracle.normwise_error(outs[rep][i], outs[0][i]) < 1e-6, (cases[i], rep)
+
+
+def test_batched_decode_grid_larger_than_the_device():
+    # 300 row groups, k split in 2 (16 chunks of 128, at most 8 a slice): 600
+    # workgroups, more than run at once (two a CU), so the call takes the two
+    # launches (y zeroed by the first) instead of the one-launch kernel
+    m, n, k = 16, 38400, 2048
+    blocks, x = _case(Q4_0, m, n, k, seed=77)
+    ql = QuantLinear.from_blocks(Q4_0, n, k, blocks)
+    y = _run(ql, x, PATH_DECODE_MFMA)
+    assert oracle.normwise_error(y, oracle.qmatmul_f64(Q4_0, blocks, x, n, k)) < 1e-3
+
+
 def test_repeat_calls_deterministic():
     # GEMV (m <= 4) and prefill compute every output in one fixed order: bitwise
     # repeatable, also where the prefill splits k over workgroups (m = 130 here: 32

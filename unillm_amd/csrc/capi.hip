@@ -27,6 +27,9 @@ namespace {
 // hipGetSymbolAddress returns at init, kept per device in g_scratch_ptr.
 constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
 __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+// Its last kNoAllocSyncBytes hold the batched decode's arrival tickets (cleared at
+// init, and every launch leaves them zero); the x operand uses the rest.
+constexpr size_t kNoAllocSyncBytes = (size_t)256 << 10;
 std::vector<void*> g_scratch_ptr;  // by device index; nullptr before that device's init
 
 thread_local std::string g_last_error;
@@ -77,6 +80,11 @@ int do_init(int device) {
     if ((e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch))) != hipSuccess)
         return fail_hip(e, "hipGetSymbolAddress (no-allocation scratch)");
     if (!sp) return fail(UNILLM_ERR_HIP, "hipGetSymbolAddress returned no address for scratch");
+    // the tickets at its tail start at zero (a device global is zero at load as well)
+    if ((e = hipMemset(static_cast<uint8_t*>(sp) + kNoAllocScratchBytes - kNoAllocSyncBytes, 0,
+                       kNoAllocSyncBytes)) != hipSuccess ||
+        (e = hipDeviceSynchronize()) != hipSuccess)
+        return fail_hip(e, "clearing the no-allocation tickets");
     g_scratch_ptr.assign((size_t)count, nullptr);
     g_scratch_ptr[(size_t)device] = sp;
     g_device = device;
@@ -209,6 +217,8 @@ hipError_t stream_workspace(hipStream_t s, size_t bytes, void** out, int slot) {
         const size_t want = std::max({bytes, (size_t)1 << 20, 2 * w.bytes});
         void* nb = nullptr;
         if ((e = hipMallocAsync(&nb, want, s)) != hipSuccess) return e;
+        // the tickets start at zero (never under capture: growth is refused there)
+        if (slot == kSyncSlot && (e = hipMemsetAsync(nb, 0, want, s)) != hipSuccess) return e;
         if (w.buf) g_ws_retired.push_back(w.buf);
         w.buf = nb;
         w.bytes = want;
@@ -393,18 +403,23 @@ int qmatmul_impl(const unillm_qweight* w, const float* x_dev, int64_t m, float* 
     // x not on a 16-byte boundary (candle takes any contiguous f32): the kernels
     // load x 16 bytes at a time, so it is first copied, stream-ordered, into an
     // aligned workspace (slot 3)
+    void* fixed_sync = nullptr;
     if (fixed_ws) {
         if (!aligned16(x_dev))
             return fail(UNILLM_ERR_INVALID_ARG,
                         what + ": the no-allocation entry point takes x 16-byte aligned");
-        const size_t need = path == UNILLM_PATH_DECODE_MFMA    ? decode_workspace_bytes(*w, m)
+        // the tickets at the scratch's tail, the x operand in the rest
+        fixed_bytes -= kNoAllocSyncBytes;
+        fixed_sync = static_cast<uint8_t*>(fixed_ws) + fixed_bytes;
+        const size_t need = path == UNILLM_PATH_DECODE_MFMA ? decode_workspace_bytes(*w, m, norm)
                             : path == UNILLM_PATH_PREFILL_MFMA ? prefill_call_bytes(*w, m, fixed_bytes)
                                                                : 0;
-        if (need > fixed_bytes)
+        if (need > fixed_bytes ||
+            (path == UNILLM_PATH_DECODE_MFMA && decode_sync_bytes(*w) > kNoAllocSyncBytes))
             return fail(UNILLM_ERR_UNSUPPORTED,
                         what + ": this call needs " + std::to_string(need) +
                             " bytes of scratch; the no-allocation entry point holds " +
-                            std::to_string(fixed_bytes) + " (m * k too large)");
+                            std::to_string(fixed_bytes) + " (m * k or n too large)");
     }
     if (!aligned16(x_dev)) {
         void* xa = nullptr;
@@ -436,7 +451,7 @@ int qmatmul_impl(const unillm_qweight* w, const float* x_dev, int64_t m, float* 
         case UNILLM_PATH_DECODE_MFMA:
             if (m > kDecodeMaxM)
                 return fail(UNILLM_ERR_UNSUPPORTED, what + ": decode MFMA path takes m <= 64");
-            e = launch_decode_mfma(*w, x_dev, m, out, s, run_epi, norm, fixed_ws);
+            e = launch_decode_mfma(*w, x_dev, m, out, s, run_epi, norm, fixed_ws, fixed_sync);
             break;
         case UNILLM_PATH_PREFILL_MFMA:
             e = launch_prefill_mfma(*w, x_dev, m, out, s, run_epi, norm, fixed_ws, fixed_bytes);
@@ -502,11 +517,17 @@ int unillm_hip_qmatmul_reserve(const unillm_qweight* w, int64_t m, int swiglu, v
     if (m > (int64_t)INT32_MAX / 2) return fail(UNILLM_ERR_INVALID_ARG, "reserve: m too large");
     if (int rc = ensure_init()) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    // slot 0: the x operand of either MFMA path at any m' <= m (both sizes grow with m)
-    const size_t x0 = std::max(decode_workspace_bytes(*w, std::min<int64_t>(m, kDecodeMaxM)),
-                               prefill_workspace_bytes(*w, m));
+    // slot 0: the x operand of either MFMA path at any m' <= m (both sizes grow with m;
+    // the batched decode's with a fused norm bounds the one without)
+    const float unused_gamma = 0.0f;
+    const NormArgs any_norm{&unused_gamma, nullptr, 0.0f};
+    const size_t x0 =
+        std::max(decode_workspace_bytes(*w, std::min<int64_t>(m, kDecodeMaxM), any_norm),
+                 prefill_workspace_bytes(*w, m));
     void* p = nullptr;
     hipError_t e = stream_workspace(s, x0, &p, 0);
+    // the batched decode's arrival tickets
+    if (e == hipSuccess) e = stream_workspace(s, decode_sync_bytes(*w), &p, kSyncSlot);
     // slot 1: the [gate | up] product of a SwiGLU call off the GEMV path
     if (e == hipSuccess && swiglu)
         e = stream_workspace(s, (size_t)m * (size_t)w->n * sizeof(float), &p, 1);

@@ -625,6 +625,344 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
     }
 }
 
+// ---- one launch for up to 16 tokens (decode_x_kernel) ---------------------------------------
+// The same product as decode_kernel at m <= 16, with x read as f32 by the kernel itself:
+// each workgroup turns its k slice of the m rows of x into f16 in LDS (the slice's
+// power-of-two scale per row, as xprep_kernel computes it) while its first weight
+// chunks stream in, so no conversion launch runs before it.  The ring then carries
+// weights only.  A k range split over S workgroups meets in y as decode_kernel's
+// does, by f32 atomic adds; y is zeroed by the row group's k slice 0 at its start,
+// which then raises the group's flag (after its prologue, long before any slice
+// finishes).  Each slice checks the flag before it adds; the last to pass resets the
+// flag for the next launch (the words live in the stream's workspace, zeroed when it
+// is allocated).  The host takes this kernel only where every workgroup of the grid
+// fits on the device at once, so each wait is on a workgroup that runs; it is
+// bounded all the same.
+constexpr int kXinMaxM = 16;
+constexpr int kXinRowBytes = 256;  // one 128-k chunk of one row, f16
+constexpr int kXinArea = kMaxSliceChunks * kXinMaxM * kXinRowBytes;  // 32 KiB
+constexpr int kSyncStride = 32;    // u32 words between counters (128-byte lines)
+constexpr int kSyncPoll = 1 << 20;
+
+template <int QT>
+struct XinStage {
+    static constexpr int QB = Stage<QT, 1>::QB;
+    static constexpr int P = DROWS * 4 * QB;         // the chunk's weight payloads
+    static constexpr int PD = 32 * 4 * QB / 1024;    // direct loads per wave (2 / 4)
+    static constexpr int LPR = 4 * QB / 16;
+    static constexpr int RPI = 64 / LPR;
+    static constexpr int SCALES = Stage<QT, 1>::SCALES;
+    static constexpr int HDR = Stage<QT, 1>::HDR;
+    static constexpr int D = QB == 16 ? 4 : 2;       // two workgroups a CU
+    static constexpr int LDS = kXinArea + D * P + SCALES + HDR + 64 * 4;
+};
+
+// Sync words per row group (128-byte lines apart): [0] y's tile is zero, [32] slices
+// past the flag, [64] unused.
+size_t xin_sync_bytes(int64_t groups) { return (size_t)(groups + 1) * 3 * kSyncStride * 4; }
+
+template <int QT>
+__global__ __launch_bounds__(256) void decode_x_kernel(const uint8_t* __restrict__ base, int64_t rb,
+                                                       const float* __restrict__ x,
+                                                       float* __restrict__ y, int M, int N, int KB,
+                                                       int S, float wscale, float oscale, int add,
+                                                       unsigned* __restrict__ sync) {
+    using ST = XinStage<QT>;
+    constexpr int QB = ST::QB, D = ST::D;
+    constexpr bool Q4 = QT == UNILLM_QTYPE_Q4_0 || QT == UNILLM_QTYPE_Q4_K;
+    constexpr bool K4 = QT == UNILLM_QTYPE_Q4_K, K6 = QT == UNILLM_QTYPE_Q6_K;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    uint8_t* const xarea = lds;
+    uint8_t* const ring = lds + kXinArea;
+    uint8_t* const scl = ring + D * ST::P;
+    uint8_t* const hdr = scl + ST::SCALES;
+    float* const facs = reinterpret_cast<float*>(hdr + ST::HDR);  // [16] the rows' factors
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, col = lane & 31;
+    const int K = KB * QK;
+    const int rg = blockIdx.x / S, sp = blockIdx.x % S;
+    const int chunks = (KB + 3) / 4;
+    const int c0 = (int)((int64_t)sp * chunks / S), c1 = (int)((int64_t)(sp + 1) * chunks / S);
+    const int nch = c1 - c0;
+    const int row0 = rg * DROWS + 32 * wv;
+    const uint32_t sbase = (uint32_t)KB * QB;
+
+    // ---- x: row r = tid / 16 of the slice, groups of 8 elements g = tid % 16 + 16 i
+    // (chunk i, group g % 16 of its 16); requested first.  Rows past m, chunks past the
+    // slice and elements past k are not read: zero. ----
+    // ---- k slice 0 of a split that stores: y's tile of this row group to zero first
+    // (device-coherent stores; the flag follows once they are complete) ----
+    const bool zero_tile = S > 1 && !add && sp == 0;
+    if (zero_tile) {
+        for (int i = tid; i < M * DROWS; i += 256) {
+            const int t = i / DROWS, n = rg * DROWS + i % DROWS;
+            if (n < N)
+                __hip_atomic_store(reinterpret_cast<unsigned*>(y + (int64_t)t * N + n), 0u,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+
+    const int xr = tid >> 4, xg = tid & 15;
+    float4 xv[kMaxSliceChunks][2];
+#pragma unroll
+    for (int i = 0; i < kMaxSliceChunks; ++i) {
+        const int e = (c0 + i) * 128 + 8 * xg;
+        xv[i][0] = xv[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (xr < M && i < nch && e < K) {
+            const float4* src = reinterpret_cast<const float4*>(x + (int64_t)xr * K + e);
+            xv[i][0] = src[0];
+            xv[i][1] = src[1];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // x requested before every direct load
+
+
+    // ---- the slice's weight scales and K-quant headers (as decode_kernel) ----
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int f = 64 * i + lane;
+        const int r = f >> 4, dw = f & 15;
+        const int jj = min(((dw >> 1) - r) & 7, nch - 1);
+        const uint32_t g = (uint32_t)min(row0 + r, N - 1) * (uint32_t)rb + sbase +
+                           8u * (uint32_t)(c0 + jj) + 4u * (uint32_t)(dw & 1);
+        dma4(base + g, scl + wv * 2048 + i * 256);
+    }
+    if constexpr (K4 || K6) {
+        const int g0 = c0 >> 1, glast = (c1 - 1) >> 1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int f = 64 * i + lane;
+            const int r = f >> 3, grp = min(g0 + (f & 7), glast);
+            const uint32_t g = (uint32_t)min(row0 + r, N - 1) * (uint32_t)rb +
+                               (uint32_t)KB * (QB + 2u) + 4u * (uint32_t)grp;
+            dma4(base + g, hdr + wv * 1024 + i * 256);
+        }
+    }
+
+    // ---- weight payloads: the ring's direct loads (decode_kernel's layout) ----
+    auto swz = [](int r) { return (Q4 ? (r >> 1) & 3 : r & 7) ^ ((r >> 3) & 1); };
+    uint32_t poff[ST::PD];
+#pragma unroll
+    for (int i = 0; i < ST::PD; ++i) {
+        const int r = ST::RPI * i + lane / ST::LPR;
+        const int piece = (lane % ST::LPR) ^ swz(r);
+        poff[i] = (uint32_t)min(row0 + r, N - 1) * (uint32_t)rb + (uint32_t)(16 * piece);
+    }
+    auto issue = [&](int j) {
+        const uint32_t c = (uint32_t)(c0 + min(j, nch - 1));
+        uint8_t* st = ring + (j % D) * ST::P;
+#pragma unroll
+        for (int i = 0; i < ST::PD; ++i)
+            dma16(base + poff[i] + c * (4 * QB), st + (ST::PD * wv + i) * 1024);
+    };
+    // D - 1 stages whatever the slice length (a fixed count of direct loads after the x
+    // loads, so the waits for x count past them; stages past the slice repeat its last
+    // chunk into slots that are never read, and the last chunk's wait drains them)
+#pragma unroll
+    for (int j = 0; j < D - 1; ++j) issue(j);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- x to f16 in LDS: the row's largest magnitude over the 16 lanes of its
+    // DPP row, the power of two that puts it in [2^14, 2^15), the factor that undoes
+    // it into facs[r]; groups in the fragment order 0 2 1 3 4 6 5 7, 16-byte group g
+    // of row r at slot g ^ r of the chunk's row (the reads below are conflict-free).
+    // Asm stores: the compiler would otherwise wait for the direct loads first. ----
+    {
+        auto amax4 = [](float4 v) {
+            return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        };
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kMaxSliceChunks; ++i) mx = fmaxf(mx, fmaxf(amax4(xv[i][0]), amax4(xv[i][1])));
+        mx = fmaxf(mx, dpp_mov<0xB1>(mx));   // quad_perm [1,0,3,2]
+        mx = fmaxf(mx, dpp_mov<0x4E>(mx));   // quad_perm [2,3,0,1]
+        mx = fmaxf(mx, dpp_mov<0x141>(mx));  // row_half_mirror
+        mx = fmaxf(mx, dpp_mov<0x140>(mx));  // row_mirror: the 16-lane row's max
+        int e = 0;
+        const bool ok = mx > 0.0f && mx <= 3.402823466e38f;
+        if (ok) (void)frexpf(mx, &e);
+        e = e < -111 ? -111 : e;
+        const float sc = ok ? ldexpf(1.0f, 15 - e) : 1.0f;
+        if (xg == 0) {
+            const float f = ok ? ldexpf(1.0f, e - 15) : 1.0f;
+            asm volatile("ds_write_b32 %0, %1" ::"v"((uint32_t)(uintptr_t)(facs + xr)), "v"(f));
+        }
+        // every chunk position is written (zeros past the slice): no divergent loop
+#pragma unroll
+        for (int i = 0; i < kMaxSliceChunks; ++i) {
+            const float4 a = xv[i][0], b = xv[i][1];
+            const lds_u32x4 v = {pk_f16(a.x * sc, a.z * sc), pk_f16(a.y * sc, a.w * sc),
+                                 pk_f16(b.x * sc, b.z * sc), pk_f16(b.y * sc, b.w * sc)};
+            const uint32_t addr = (uint32_t)(uintptr_t)xarea +
+                                  (uint32_t)(i * kXinMaxM * kXinRowBytes + xr * kXinRowBytes +
+                                             16 * (xg ^ xr));
+            asm volatile("ds_write_b128 %0, %1" ::"v"(addr), "v"(v));
+        }
+    }
+    if (zero_tile) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the zeros have landed
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    unsigned* const flag = sync + (size_t)rg * 3 * kSyncStride;
+    if (zero_tile && tid == 0)
+        __hip_atomic_store(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    f32x16 acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+
+    // LDS offsets: x of token row min(col, 15) (tokens 16 .. 31 of the MFMA tile are
+    // padding whose outputs are never stored), payloads as decode_kernel
+    const int xrow = min(col, kXinMaxM - 1);
+    uint32_t xo[8];
+#pragma unroll
+    for (int hp = 0; hp < 2; ++hp)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int i = 2 * hp + q / 2;
+            const int g = Q4 ? 8 * hp + 4 * h + q : 4 * i + 2 * h + (q & 1);
+            xo[4 * hp + q] = (uint32_t)(xrow * kXinRowBytes + 16 * (g ^ xrow));
+        }
+    uint32_t po[4];
+    const int prow = 32 * wv + col;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int piece = Q4 ? (2 * (i & 1) + h) : 2 * i + h;
+        po[i] = (uint32_t)(prow * 4 * QB + 16 * (piece ^ swz(col)));
+    }
+    const uint32_t ring0 = (uint32_t)(uintptr_t)ring;
+    const uint32_t x0 = (uint32_t)(uintptr_t)xarea;
+    const uint32_t srow = (uint32_t)(uintptr_t)scl + (uint32_t)(wv * 2048 + col * 64);
+    const uint32_t hrow = (uint32_t)(uintptr_t)hdr + (uint32_t)(wv * 1024 + col * 32);
+
+    auto compute = [&](int j) {
+        const uint32_t st = ring0 + (uint32_t)((j % D) * ST::P);
+        const uint32_t xs = x0 + (uint32_t)(j * kXinMaxM * kXinRowBytes);
+        const int kb0 = 4 * (c0 + j);
+        const uint32_t sa = srow + 8 * ((j + col) & 7);
+        float gd = 0.0f, gm = 0.0f;
+        if constexpr (K4 || K6) {
+            uint32_t hd;
+            asm volatile("ds_read_b32 %0, %1\n s_waitcnt lgkmcnt(0)"
+                         : "=&v"(hd)
+                         : "v"(hrow + 4u * (uint32_t)(((c0 + j) >> 1) - (c0 >> 1))));
+            gd = __half2float(__ushort_as_half((uint16_t)hd)) * wscale;
+            gm = __half2float(__ushort_as_half((uint16_t)(hd >> 16))) * wscale;
+        }
+#pragma unroll
+        for (int hp = 0; hp < 2; ++hp) {
+            lds_u32x4 xa[1][4];
+            u32x4 pw[2];
+            lds_u32x2 scp;
+            read_half<Q4, 1>(xa, pw, scp, xs + xo[4 * hp], xs + xo[4 * hp + 1], xs + xo[4 * hp + 2],
+                             xs + xo[4 * hp + 3], st + po[Q4 ? hp : 2 * hp],
+                             st + po[Q4 ? hp : 2 * hp + 1], sa);
+            if constexpr (Q4) {
+                const uint16_t sb = (uint16_t)(scp[hp] >> (16 * h));
+                const bool ok = kb0 + 2 * hp + h < KB;
+                f16x8 b[4];
+                if constexpr (K4) {
+                    const float sv = ok ? gd * (float)(sb & 0xFFu) : 0.0f;
+                    const float ov = ok ? gm * (float)(sb >> 8) : 0.0f;
+                    const _Float16 s1 = (_Float16)sv, s16 = (_Float16)(sv * 0.0625f),
+                                   o1 = (_Float16)ov;
+                    const f16x2 sh = {s1, s1}, sh16 = {s16, s16}, oh = {o1, o1};
+                    dequant_q4k(pw[0], sh, sh16, oh, b);
+                } else {
+                    const float dv = ok ? __half2float(__ushort_as_half(sb)) * wscale : 0.0f;
+                    const _Float16 d = (_Float16)dv, d16 = (_Float16)(dv * 0.0625f);
+                    const f16x2 dh = {d, d}, dh16 = {d16, d16};
+                    dequant_q4(pw[0], dh, dh16, b);
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, xa[0][q]),
+                                                                 b[q], acc, 0, 0, 0);
+            } else {
+#pragma unroll
+                for (int bi = 0; bi < 2; ++bi) {
+                    const uint16_t sb = (uint16_t)(scp[hp] >> (16 * bi));
+                    const bool ok = kb0 + 2 * hp + bi < KB;
+                    const float dv = !ok ? 0.0f
+                                     : K6 ? gd * (float)(int8_t)(sb >> (8 * h))
+                                          : __half2float(__ushort_as_half(sb)) * wscale;
+                    const _Float16 d = (_Float16)dv;
+                    const f16x2 dh = {d, d};
+                    f16x8 b0, b1;
+                    dequant_q8(pw[bi], dh, b0, b1);
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                        __builtin_bit_cast(f16x8, xa[0][2 * bi]), b0, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                        __builtin_bit_cast(f16x8, xa[0][2 * bi + 1]), b1, acc, 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    for (int j = 0; j < nch; ++j) {
+        wait_chunks<ST::PD, D - 2>(min(D - 2, nch - 1 - j));
+        __builtin_amdgcn_s_barrier();
+        if (j + D - 1 < nch) issue(j + D - 1);
+        compute(j);
+    }
+
+    // ---- epilogue: acc[r] = C[token 8 (r / 4) + 4 h + r % 4][row row0 + col] ----
+    // Tokens past m (and the tile's padding rows 16 .. 31) are not stored.
+    const int n = row0 + col;
+    float fv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int t = 8 * (r / 4) + 4 * h + (r % 4);
+        fv[r] = facs[min(t, kXinMaxM - 1)] * oscale;  // plain read: no direct load is in flight
+    }
+    auto each = [&](auto&& f) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int t = 8 * (r / 4) + 4 * h + (r % 4);
+            if (t < M && n < N) f(y + (int64_t)t * N + n, acc[r] * fv[r]);
+        }
+    };
+    if (S == 1) {
+        each([&](float* dst, float v) { *dst = add ? *dst + v : v; });
+    } else if (add) {
+        each([&](float* dst, float v) { unsafeAtomicAdd(dst, v); });
+    } else {
+        // slice 0 zeroed the tile and raised the flag after its prologue: the wait is
+        // normally over at the first look
+        if (tid == 0) {
+            for (int it = 0; it < kSyncPoll; ++it) {
+                if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        __syncthreads();
+        each([&](float* dst, float v) { unsafeAtomicAdd(dst, v); });
+        if (tid == 0 && __hip_atomic_fetch_add(flag + kSyncStride, 1u, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT) == (unsigned)S - 1) {
+            // every slice of this row group is past the flag: reset for the next launch
+            __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(flag + kSyncStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+template <int QT>
+hipError_t launch_x(const QWeight& w, const float* x, int64_t m, float* y, int S, hipStream_t s,
+                    int add, unsigned* sync) {
+    using ST = XinStage<QT>;
+    static const bool attr = hipFuncSetAttribute((const void*)decode_x_kernel<QT>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 ST::LDS) == hipSuccess;
+    if (!attr) return hipErrorInvalidValue;
+    const float wscale = ldexpf(1.0f, -w.f16_exp), oscale = ldexpf(1.0f, w.f16_exp);
+    const int groups = (int)((w.n + DROWS - 1) / DROWS);
+    decode_x_kernel<QT><<<groups * S, 256, ST::LDS, s>>>(w.base, w.row_bytes, x, y, (int)m,
+                                                         (int)w.n, (int)w.kb, S, wscale, oscale,
+                                                         add, sync);
+    return hipGetLastError();
+}
+
 template <int QT, int MT2>
 hipError_t launch_mt(const QWeight& w, const _Float16* xh, const float* rf, int64_t m, float* y,
                      int S, hipStream_t s, int add) {
@@ -899,26 +1237,63 @@ int decode_split(const QWeight& w, int64_t m) {
                          : (wide ? Stage<UNILLM_QTYPE_Q8_0, 2>::LDS : Stage<UNILLM_QTYPE_Q8_0, 1>::LDS);
     return choose_split(w, lds, wide);
 }
+int xin_lds(const QWeight& w) {
+    switch (w.qtype) {
+        case UNILLM_QTYPE_Q4_0: return XinStage<UNILLM_QTYPE_Q4_0>::LDS;
+        case UNILLM_QTYPE_Q8_0: return XinStage<UNILLM_QTYPE_Q8_0>::LDS;
+        case UNILLM_QTYPE_Q4_K: return XinStage<UNILLM_QTYPE_Q4_K>::LDS;
+        default: return XinStage<UNILLM_QTYPE_Q6_K>::LDS;
+    }
+}
+int xin_split(const QWeight& w) { return choose_split(w, xin_lds(w), false); }
+// The one-launch kernel takes m <= 16 without a fused layer norm (the norm needs
+// the whole row's statistics: its conversion stays a launch of its own), and only
+// where its whole grid fits on the device at once (a slice may wait for slice 0 of
+// its row group), else the two launches (y zeroed by the first).
+bool decode_one_launch(const QWeight& w, int64_t m, const NormArgs& norm) {
+    if (m > kXinMaxM || norm.gamma) return false;
+    const int64_t groups = (w.n + DROWS - 1) / DROWS;
+    const int64_t per_cu = std::max(1, device_info().max_lds_cu / xin_lds(w));
+    return groups * xin_split(w) <= (int64_t)device_info().cu_count * per_cu;
+}
 // x as f16 (m k 2 bytes, padded to 256), then the slice factors rf[S][64]
 size_t decode_x_bytes(const QWeight& w, int64_t m) {
     return ((size_t)m * (size_t)w.k * 2 + 255) / 256 * 256;
 }
 }  // namespace
 
-size_t decode_workspace_bytes(const QWeight& w, int64_t m) {
+size_t decode_workspace_bytes(const QWeight& w, int64_t m, const NormArgs& norm) {
+    if (decode_one_launch(w, m, norm)) return 0;
     return decode_x_bytes(w, m) + (size_t)decode_split(w, m) * 64 * sizeof(float);
 }
 
+size_t decode_sync_bytes(const QWeight& w) { return xin_sync_bytes((w.n + DROWS - 1) / DROWS); }
+
 hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float* y,
-                              hipStream_t s, int epi, const NormArgs& norm, void* ws) {
+                              hipStream_t s, int epi, const NormArgs& norm, void* ws,
+                              void* sync_ws) {
     // 32-bit offsets: x in f16 elements, weight bytes
     if ((uint64_t)m * (uint64_t)w.k >= (1ull << 31) || !mfma_supports(w) || m > 64)
         return hipErrorInvalidValue;
     const bool q4 = w.qtype == UNILLM_QTYPE_Q4_0, k4 = w.qtype == UNILLM_QTYPE_Q4_K,
                k6 = w.qtype == UNILLM_QTYPE_Q6_K, wide = m > 32;
-    const int S = decode_split(w, m);
     hipError_t e = hipSuccess;
-    if (!ws && (e = stream_workspace(s, decode_workspace_bytes(w, m), &ws)) != hipSuccess)
+    if (decode_one_launch(w, m, norm)) {
+        // x converted by the kernel itself; the stream's workspace holds the row groups'
+        // arrival tickets (zeroed when allocated, reset by each launch)
+        const int S = xin_split(w);
+        const int add = epi == kEpiAdd;
+        void* sy = sync_ws;
+        if (!sy && (e = stream_workspace(s, decode_sync_bytes(w), &sy, kSyncSlot)) != hipSuccess)
+            return e;
+        unsigned* sync = static_cast<unsigned*>(sy);
+        if (k4) return launch_x<UNILLM_QTYPE_Q4_K>(w, x, m, y, S, s, add, sync);
+        if (k6) return launch_x<UNILLM_QTYPE_Q6_K>(w, x, m, y, S, s, add, sync);
+        return q4 ? launch_x<UNILLM_QTYPE_Q4_0>(w, x, m, y, S, s, add, sync)
+                  : launch_x<UNILLM_QTYPE_Q8_0>(w, x, m, y, S, s, add, sync);
+    }
+    const int S = decode_split(w, m);
+    if (!ws && (e = stream_workspace(s, decode_workspace_bytes(w, m, norm), &ws)) != hipSuccess)
         return e;
     float* rf = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + decode_x_bytes(w, m));
     const int add = epi == kEpiAdd;

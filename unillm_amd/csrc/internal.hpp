@@ -152,7 +152,10 @@ const DeviceInfo& device_info();
 // host threads are ordered by the stream, the map by a mutex.
 // Slot 0 holds x in the MFMA paths' operand type; slot 1 the [gate | up] outputs
 // of a SwiGLU call off the GEMV path (both live during that call); slot 2 the
-// rotated queries and the per-chunk partials of decode attention.
+// rotated queries and the per-chunk partials of decode attention; slot 3 an
+// aligned copy of x; slot kSyncSlot the batched decode's arrival tickets, zeroed
+// when allocated (every launch leaves them zero again).
+constexpr int kSyncSlot = 4;
 hipError_t stream_workspace(hipStream_t s, size_t bytes, void** out, int slot = 0);
 // UNILLM_DEBUG_LAUNCH=1 prints each kernel's launch shape to stderr.
 bool debug_launch();
@@ -173,15 +176,21 @@ hipError_t launch_gemv(const QWeight& w, const float* x, int64_t m, float* y, hi
 // The MFMA paths take their x operand buffer from `ws` when it is given (at least
 // decode_workspace_bytes / prefill_call_bytes for this w and m), else from the
 // stream's workspace (slot 0).
+// sync_ws: the arrival tickets of the one-launch batched decode (m <= 16 without a
+// norm; at least decode_sync_bytes, zero), else the stream's slot kSyncSlot.
 hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float* y,
                               hipStream_t s, int epi = kEpiStore,
                               const NormArgs& norm = NormArgs{nullptr, nullptr, 0.f},
-                              void* ws = nullptr);
+                              void* ws = nullptr, void* sync_ws = nullptr);
 hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, float* y,
                                hipStream_t s, int epi = kEpiStore,
                                const NormArgs& norm = NormArgs{nullptr, nullptr, 0.f},
                                void* ws = nullptr, size_t ws_bytes = 0);
-size_t decode_workspace_bytes(const QWeight& w, int64_t m);
+// The batched decode's x operand workspace (0 where the kernel converts x itself),
+// and its arrival tickets.
+// (no default for norm: the size depends on it)
+size_t decode_workspace_bytes(const QWeight& w, int64_t m, const NormArgs& norm);
+size_t decode_sync_bytes(const QWeight& w);
 // The prefill's workspace: this call's own need (cap > 0: in a fixed workspace of
 // cap bytes, which may pick a plan without a k split), and a bound for every call
 // of up to m rows (the size a reserve takes).

@@ -640,11 +640,14 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
 // bounded all the same.
 constexpr int kXinMaxM = 16;
 constexpr int kXinRowBytes = 256;  // one 128-k chunk of one row, f16
-constexpr int kXinArea = kMaxSliceChunks * kXinMaxM * kXinRowBytes;  // 32 KiB
+constexpr int kXinLdsBudget = 80 * 1024;  // two workgroups a CU (160 KiB)
 constexpr int kSyncStride = 32;    // u32 words between counters (128-byte lines)
 constexpr int kSyncPoll = 1 << 20;
 
-template <int QT>
+// XC: the chunks of x the LDS holds (a slice's length at most: 4 or kMaxSliceChunks);
+// the ring takes as many weight stages as the rest of the budget holds, so a short
+// slice is requested whole in the prologue.
+template <int QT, int XC>
 struct XinStage {
     static constexpr int QB = Stage<QT, 1>::QB;
     static constexpr int P = DROWS * 4 * QB;         // the chunk's weight payloads
@@ -653,27 +656,33 @@ struct XinStage {
     static constexpr int RPI = 64 / LPR;
     static constexpr int SCALES = Stage<QT, 1>::SCALES;
     static constexpr int HDR = Stage<QT, 1>::HDR;
-    static constexpr int D = QB == 16 ? 4 : 2;       // two workgroups a CU
-    static constexpr int LDS = kXinArea + D * P + SCALES + HDR + 64 * 4;
+    static constexpr int XAREA = XC * kXinMaxM * kXinRowBytes;
+    static constexpr int D = (kXinLdsBudget - XAREA - SCALES - HDR - 64 * 4) / P;
+    static constexpr int LDS = XAREA + D * P + SCALES + HDR + 64 * 4;
+    static_assert(D >= 2 && XC <= kMaxSliceChunks, "ring of at least two stages");
 };
 
 // Sync words per row group (128-byte lines apart): [0] y's tile is zero, [32] slices
 // past the flag, [64] unused.
 size_t xin_sync_bytes(int64_t groups) { return (size_t)(groups + 1) * 3 * kSyncStride * 4; }
 
-template <int QT>
+template <int QT, int XC>
 __global__ __launch_bounds__(256) void decode_x_kernel(const uint8_t* __restrict__ base, int64_t rb,
                                                        const float* __restrict__ x,
                                                        float* __restrict__ y, int M, int N, int KB,
                                                        int S, float wscale, float oscale, int add,
                                                        unsigned* __restrict__ sync) {
-    using ST = XinStage<QT>;
+    // every argument in registers behind one wait (left to itself the compiler fetches
+    // them one branch at a time, a round trip each)
+    asm volatile("" ::"s"(base), "s"(rb), "s"(x), "s"(y), "s"(M), "s"(N), "s"(KB), "s"(S),
+                 "s"(wscale), "s"(oscale), "s"(add), "s"(sync));
+    using ST = XinStage<QT, XC>;
     constexpr int QB = ST::QB, D = ST::D;
     constexpr bool Q4 = QT == UNILLM_QTYPE_Q4_0 || QT == UNILLM_QTYPE_Q4_K;
     constexpr bool K4 = QT == UNILLM_QTYPE_Q4_K, K6 = QT == UNILLM_QTYPE_Q6_K;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     uint8_t* const xarea = lds;
-    uint8_t* const ring = lds + kXinArea;
+    uint8_t* const ring = lds + ST::XAREA;
     uint8_t* const scl = ring + D * ST::P;
     uint8_t* const hdr = scl + ST::SCALES;
     float* const facs = reinterpret_cast<float*>(hdr + ST::HDR);  // [16] the rows' factors
@@ -689,9 +698,6 @@ __global__ __launch_bounds__(256) void decode_x_kernel(const uint8_t* __restrict
     const int row0 = rg * DROWS + 32 * wv;
     const uint32_t sbase = (uint32_t)KB * QB;
 
-    // ---- x: row r = tid / 16 of the slice, groups of 8 elements g = tid % 16 + 16 i
-    // (chunk i, group g % 16 of its 16); requested first.  Rows past m, chunks past the
-    // slice and elements past k are not read: zero. ----
     // ---- k slice 0 of a split that stores: y's tile of this row group to zero first
     // (device-coherent stores; the flag follows once they are complete) ----
     const bool zero_tile = S > 1 && !add && sp == 0;
@@ -704,10 +710,13 @@ __global__ __launch_bounds__(256) void decode_x_kernel(const uint8_t* __restrict
         }
     }
 
+    // ---- x: row r = tid / 16 of the slice, groups of 8 elements g = tid % 16 + 16 i
+    // (chunk i, group g % 16 of its 16); requested first.  Rows past m, chunks past the
+    // slice and elements past k are not read: zero. ----
     const int xr = tid >> 4, xg = tid & 15;
-    float4 xv[kMaxSliceChunks][2];
+    float4 xv[XC][2];
 #pragma unroll
-    for (int i = 0; i < kMaxSliceChunks; ++i) {
+    for (int i = 0; i < XC; ++i) {
         const int e = (c0 + i) * 128 + 8 * xg;
         xv[i][0] = xv[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (xr < M && i < nch && e < K) {
@@ -757,11 +766,11 @@ __global__ __launch_bounds__(256) void decode_x_kernel(const uint8_t* __restrict
         for (int i = 0; i < ST::PD; ++i)
             dma16(base + poff[i] + c * (4 * QB), st + (ST::PD * wv + i) * 1024);
     };
-    // D - 1 stages whatever the slice length (a fixed count of direct loads after the x
-    // loads, so the waits for x count past them; stages past the slice repeat its last
-    // chunk into slots that are never read, and the last chunk's wait drains them)
+    // the first D - 1 chunks of the slice (each later one is requested D - 1 chunks
+    // ahead of its use, so the chunk waits below count exactly what is in flight)
 #pragma unroll
-    for (int j = 0; j < D - 1; ++j) issue(j);
+    for (int j = 0; j < D - 1; ++j)
+        if (j < nch) issue(j);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- x to f16 in LDS: the row's largest magnitude over the 16 lanes of its
@@ -775,7 +784,7 @@ __global__ __launch_bounds__(256) void decode_x_kernel(const uint8_t* __restrict
         };
         float mx = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kMaxSliceChunks; ++i) mx = fmaxf(mx, fmaxf(amax4(xv[i][0]), amax4(xv[i][1])));
+        for (int i = 0; i < XC; ++i) mx = fmaxf(mx, fmaxf(amax4(xv[i][0]), amax4(xv[i][1])));
         mx = fmaxf(mx, dpp_mov<0xB1>(mx));   // quad_perm [1,0,3,2]
         mx = fmaxf(mx, dpp_mov<0x4E>(mx));   // quad_perm [2,3,0,1]
         mx = fmaxf(mx, dpp_mov<0x141>(mx));  // row_half_mirror
@@ -791,7 +800,7 @@ __global__ __launch_bounds__(256) void decode_x_kernel(const uint8_t* __restrict
         }
         // every chunk position is written (zeros past the slice): no divergent loop
 #pragma unroll
-        for (int i = 0; i < kMaxSliceChunks; ++i) {
+        for (int i = 0; i < XC; ++i) {
             const float4 a = xv[i][0], b = xv[i][1];
             const lds_u32x4 v = {pk_f16(a.x * sc, a.z * sc), pk_f16(a.y * sc, a.w * sc),
                                  pk_f16(b.x * sc, b.z * sc), pk_f16(b.y * sc, b.w * sc)};
@@ -947,17 +956,17 @@ __global__ __launch_bounds__(256) void decode_x_kernel(const uint8_t* __restrict
     }
 }
 
-template <int QT>
+template <int QT, int XC>
 hipError_t launch_x(const QWeight& w, const float* x, int64_t m, float* y, int S, hipStream_t s,
                     int add, unsigned* sync) {
-    using ST = XinStage<QT>;
-    static const bool attr = hipFuncSetAttribute((const void*)decode_x_kernel<QT>,
+    using ST = XinStage<QT, XC>;
+    static const bool attr = hipFuncSetAttribute((const void*)decode_x_kernel<QT, XC>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  ST::LDS) == hipSuccess;
     if (!attr) return hipErrorInvalidValue;
     const float wscale = ldexpf(1.0f, -w.f16_exp), oscale = ldexpf(1.0f, w.f16_exp);
     const int groups = (int)((w.n + DROWS - 1) / DROWS);
-    decode_x_kernel<QT><<<groups * S, 256, ST::LDS, s>>>(w.base, w.row_bytes, x, y, (int)m,
+    decode_x_kernel<QT, XC><<<groups * S, 256, ST::LDS, s>>>(w.base, w.row_bytes, x, y, (int)m,
                                                          (int)w.n, (int)w.kb, S, wscale, oscale,
                                                          add, sync);
     return hipGetLastError();
@@ -1237,15 +1246,27 @@ int decode_split(const QWeight& w, int64_t m) {
                          : (wide ? Stage<UNILLM_QTYPE_Q8_0, 2>::LDS : Stage<UNILLM_QTYPE_Q8_0, 1>::LDS);
     return choose_split(w, lds, wide);
 }
+// The larger of the two LDS layouts (XC = 8); both fit two workgroups a CU.
 int xin_lds(const QWeight& w) {
     switch (w.qtype) {
-        case UNILLM_QTYPE_Q4_0: return XinStage<UNILLM_QTYPE_Q4_0>::LDS;
-        case UNILLM_QTYPE_Q8_0: return XinStage<UNILLM_QTYPE_Q8_0>::LDS;
-        case UNILLM_QTYPE_Q4_K: return XinStage<UNILLM_QTYPE_Q4_K>::LDS;
-        default: return XinStage<UNILLM_QTYPE_Q6_K>::LDS;
+        case UNILLM_QTYPE_Q4_0: return XinStage<UNILLM_QTYPE_Q4_0, kMaxSliceChunks>::LDS;
+        case UNILLM_QTYPE_Q8_0: return XinStage<UNILLM_QTYPE_Q8_0, kMaxSliceChunks>::LDS;
+        case UNILLM_QTYPE_Q4_K: return XinStage<UNILLM_QTYPE_Q4_K, kMaxSliceChunks>::LDS;
+        default: return XinStage<UNILLM_QTYPE_Q6_K, kMaxSliceChunks>::LDS;
     }
 }
-int xin_split(const QWeight& w) { return choose_split(w, xin_lds(w), false); }
+// k split S of the one-launch kernel: the fewest slices of at most kMaxSliceChunks
+// chunks, then more while slices keep at least 4 chunks and the grid still fits the
+// device at once (a round count of workgroups a CU evens the tail), at most 16 (more
+// partial sums of one output contend in the adds).
+int xin_split(const QWeight& w) {
+    const int64_t groups = (w.n + DROWS - 1) / DROWS, chunks = (w.kb + 3) / 4;
+    const int64_t slots =
+        (int64_t)device_info().cu_count * std::max(1, device_info().max_lds_cu / xin_lds(w));
+    int64_t S = (chunks + kMaxSliceChunks - 1) / kMaxSliceChunks;
+    while (S < 16 && chunks >= 4 * (S + 1) && groups * (S + 1) <= slots) ++S;
+    return (int)S;
+}
 // The one-launch kernel takes m <= 16 without a fused layer norm (the norm needs
 // the whole row's statistics: its conversion stays a launch of its own), and only
 // where its whole grid fits on the device at once (a slice may wait for slice 0 of
@@ -1287,10 +1308,19 @@ hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float
         if (!sy && (e = stream_workspace(s, decode_sync_bytes(w), &sy, kSyncSlot)) != hipSuccess)
             return e;
         unsigned* sync = static_cast<unsigned*>(sy);
-        if (k4) return launch_x<UNILLM_QTYPE_Q4_K>(w, x, m, y, S, s, add, sync);
-        if (k6) return launch_x<UNILLM_QTYPE_Q6_K>(w, x, m, y, S, s, add, sync);
-        return q4 ? launch_x<UNILLM_QTYPE_Q4_0>(w, x, m, y, S, s, add, sync)
-                  : launch_x<UNILLM_QTYPE_Q8_0>(w, x, m, y, S, s, add, sync);
+        // slices of at most 4 chunks: the short x area and the deeper ring
+        const bool short_slices = ((w.kb + 3) / 4 + S - 1) / S <= 4;
+        if (k4)
+            return short_slices ? launch_x<UNILLM_QTYPE_Q4_K, 4>(w, x, m, y, S, s, add, sync)
+                                : launch_x<UNILLM_QTYPE_Q4_K, 8>(w, x, m, y, S, s, add, sync);
+        if (k6)
+            return short_slices ? launch_x<UNILLM_QTYPE_Q6_K, 4>(w, x, m, y, S, s, add, sync)
+                                : launch_x<UNILLM_QTYPE_Q6_K, 8>(w, x, m, y, S, s, add, sync);
+        if (q4)
+            return short_slices ? launch_x<UNILLM_QTYPE_Q4_0, 4>(w, x, m, y, S, s, add, sync)
+                                : launch_x<UNILLM_QTYPE_Q4_0, 8>(w, x, m, y, S, s, add, sync);
+        return short_slices ? launch_x<UNILLM_QTYPE_Q8_0, 4>(w, x, m, y, S, s, add, sync)
+                            : launch_x<UNILLM_QTYPE_Q8_0, 8>(w, x, m, y, S, s, add, sync);
     }
     const int S = decode_split(w, m);
     if (!ws && (e = stream_workspace(s, decode_workspace_bytes(w, m, norm), &ws)) != hipSuccess)

@@ -17,8 +17,8 @@
  *     (candle reverses ne into shape [n, k]).  x is [m, k] f32 row-major and
  *     y = x . dequant(W)^T is [m, n] f32 row-major.
  *   - Preconditions checked on the host before any launch: k % 32 == 0
- *     (k % 256 == 0 for Q4_K, Q6_K), n >= 1, k >= 32, m >= 0, non-null pointers,
- *     known qtype.
+ *     (k % 256 == 0 for Q4_K, Q6_K; any k >= 1 for the dense types), n >= 1,
+ *     m >= 0, non-null pointers, known qtype.
  *   - Streams: a `void* stream` is a hipStream_t (NULL = the null stream).
  *     Compute calls are asynchronous on that stream and never synchronise.
  *   - Ownership: a qweight owns its device copy of the weights and is
@@ -42,6 +42,14 @@ extern "C" {
 #define UNILLM_QTYPE_Q8_0 8
 #define UNILLM_QTYPE_Q4_K 12
 #define UNILLM_QTYPE_Q6_K 14
+/* Dense projection weights (GGML F32 / F16 / BF16).  candle's QMatMul::from_arc
+ * dequantizes such a tensor to f32 and multiplies in f32 (its Tensor variant);
+ * the reference's loader wraps every *_proj / lm_head tensor in a QMatMul whatever
+ * its type (crates/runtime/src/weight_loader_core.rs:554-571).  Stored here as f32
+ * rows (F16 and BF16 widen exactly) and multiplied by an f32 GEMM; any k >= 1. */
+#define UNILLM_QTYPE_F32 0
+#define UNILLM_QTYPE_F16 1
+#define UNILLM_QTYPE_BF16 30
 
 #define UNILLM_OK 0
 #define UNILLM_ERR_INVALID_ARG (-1)
@@ -55,6 +63,7 @@ extern "C" {
 #define UNILLM_PATH_GEMV 1         /* fused dequant + GEMV (VALU int8 dot), m <= 4 */
 #define UNILLM_PATH_DECODE_MFMA 2  /* batched decode, f16 MFMA, fp32 accumulate */
 #define UNILLM_PATH_PREFILL_MFMA 3 /* prefill, LDS-staged f16 MFMA (x rows scaled by powers of two), fp32 accumulate */
+#define UNILLM_PATH_DENSE 4        /* dense weights: f32 GEMM (rocBLAS), the only path they take */
 
 typedef struct unillm_qweight unillm_qweight;
 typedef struct unillm_kv_cache unillm_kv_cache;

@@ -418,6 +418,54 @@ static void test_gpu_kv() {
     }
 }
 
+// Dense projections (tiny_llama_f16: F16, layer 0's o_proj F32, layer 1's down_proj
+// BF16), the variant candle's QMatMul::from_arc keeps as a dequantized f32 tensor:
+// every projection and lm_head against the f64 expectations at 1e-5 (an f32 GEMM of
+// the exactly widened weights), the types kept, and same-typed groups fused at load.
+static void test_gpu_dense(const std::string& gguf, const std::vector<Expect>& ex) {
+    GgufWeightLoader loader;
+    const ModelWeights w = loader.load_weights(gguf);
+    CHECK(w.quantized_tensors.size() == 15);
+    CHECK(w.get_quantized("model.layers.0.self_attn.o_proj.weight")->qtype() == GGML_F32);
+    CHECK(w.get_quantized("model.layers.1.mlp.down_proj.weight")->qtype() == GGML_BF16);
+    CHECK(w.get_quantized("lm_head.weight")->qtype() == GGML_F16);
+    CHECK(w.tensors.at("model.embed_tokens.weight").shape() == std::vector<int64_t>({128, 128}));
+    std::map<std::string, std::vector<float>> ys;
+    for (const Expect& e : ex) {
+        if (!e.quantized) continue;
+        auto q = w.get_quantized(e.hf_name);
+        CHECK(q != nullptr);
+        if (!q) continue;
+        const Tensor x = Tensor::from_host(e.x, {(int64_t)e.m, (int64_t)e.k}, Device::hip(0));
+        ys[e.hf_name] = q->forward(x).to_host();
+        const double err = normwise(ys[e.hf_name], e.y);
+        if (err >= 1e-5) std::fprintf(stderr, "  %s: normwise %.3g\n", e.hf_name.c_str(), err);
+        CHECK(err < 1e-5);
+    }
+    // q / k / v and gate / up share their type in both layers: all four groups fuse, and a
+    // fused handle's column slices equal its parts' products (the same f32 GEMM per row)
+    LoadOptions opt;
+    opt.fuse_qkv = opt.fuse_gate_up = true;
+    const ModelWeights fw = loader.load_weights(gguf, opt);
+    CHECK(fw.fused_parts.size() == 4);
+    auto qkv = fw.get_quantized("model.layers.1.self_attn.qkv_proj.weight");
+    CHECK(qkv != nullptr && qkv->qtype() == GGML_F16 && qkv->n() == 256);
+    if (qkv) {
+        const Expect* eq = nullptr;
+        for (const Expect& e : ex)
+            if (e.hf_name == "model.layers.1.self_attn.q_proj.weight") eq = &e;
+        CHECK(eq != nullptr);
+        if (eq) {
+            const Tensor x = Tensor::from_host(eq->x, {(int64_t)eq->m, 128}, Device::hip(0));
+            const std::vector<float> y = qkv->forward(x).to_host();
+            std::vector<float> q_cols;
+            for (uint32_t r = 0; r < eq->m; ++r)
+                q_cols.insert(q_cols.end(), y.begin() + r * 256, y.begin() + r * 256 + 128);
+            CHECK(normwise(q_cols, eq->y) < 1e-5);
+        }
+    }
+}
+
 static void test_cpu_kq(const std::string& gguf, const std::vector<Expect>& ex) {
     const GgufFile f = GgufFile::open(gguf);
     const GgufModelConfig c = GgufWeightLoader::config_from(f);
@@ -569,6 +617,7 @@ int main(int argc, char** argv) {
         else if (mode == "gpu") test_gpu(argv[2], ex);
         else if (mode == "cpu-kq") test_cpu_kq(argv[2], ex);
         else if (mode == "gpu-kq") test_gpu_kq(argv[2], ex);
+        else if (mode == "gpu-dense") test_gpu_dense(argv[2], ex);
         else if (mode == "gpu-step") test_gpu_step(argv[2], argv[3]);
         else return 2;
     } catch (const std::exception& e) {

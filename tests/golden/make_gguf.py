@@ -25,6 +25,12 @@ and residuals.
 Layout: "USTP", u32 vocab, u32 n_steps; per step u32 m, i32 ids[m],
 f64 logits[m * vocab].
 
+tiny_llama_f16.gguf is the tiny_llama_q4_0 architecture with dense projections,
+the variant candle's QMatMul::from_arc keeps as a dequantized f32 tensor: F16
+everywhere (token_embd and output too) except layer 0's attn_output (F32) and
+layer 1's ffn_down (BF16); .expect and .step as above, from the exact widened
+weights.
+
 tiny_llama_q4_k_m.gguf has the tensor types llama.cpp's Q4_K_M mix uses:
 Q4_K projections and token_embd, Q6_K for output.weight and for layer 0's
 attn_v / ffn_down.  Its blocks are random valid Q4_K / Q6_K blocks (the
@@ -42,7 +48,8 @@ from make_golden import dequant, quantize_q4_0, quantize_q8_0
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ALIGN = 32
-T_F32, T_F16, T_Q4_0, T_Q8_0, T_Q4_K, T_Q6_K = 0, 1, 2, 8, 12, 14
+T_F32, T_F16, T_Q4_0, T_Q8_0, T_Q4_K, T_Q6_K, T_BF16 = 0, 1, 2, 8, 12, 14, 30
+DENSE = (T_F32, T_F16, T_BF16)
 V_UINT32, V_FLOAT32, V_STRING, V_ARRAY = 4, 6, 8, 9
 
 HIDDEN, INTER, VOCAB, LAYERS = 128, 96, 128, 2
@@ -105,6 +112,51 @@ def main() -> None:
           heads=(HEADS, KV_HEADS), rope_base=ROPE_BASE)
     write_steps(tensors, "tiny_llama_q4_0")
     main_kq()
+    main_dense()
+
+
+def dense_bytes(w: np.ndarray, ttype: int):
+    """GGUF bytes of a dense tensor and its exact values (f32 holds F16 and BF16)."""
+    if ttype == T_F32:
+        return w.astype(np.float32).tobytes(), w.astype(np.float32)
+    if ttype == T_F16:
+        h = w.astype(np.float16)
+        return h.tobytes(), h.astype(np.float32)
+    u = w.astype(np.float32).view(np.uint32).astype(np.uint64)  # BF16: round to nearest even
+    b = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return b.tobytes(), (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def main_dense() -> None:
+    """The tiny Llama with dense (F32 / F16 / BF16) projections."""
+    rng = np.random.default_rng(13)
+    tensors = []
+
+    def add_d(name, ttype, n, k, std=0.02):
+        raw, exact = dense_bytes(rng.normal(0.0, std, size=(n, k)), ttype)
+        tensors.append((name, ttype, (n, k), raw, exact))
+
+    def add_f32(name, n):
+        v = (1.0 + rng.normal(0, 0.1, size=n)).astype(np.float32)
+        tensors.append((name, T_F32, (n,), v.tobytes(), v))
+
+    add_d("token_embd.weight", T_F16, VOCAB, HIDDEN, std=1.0)
+    for i in range(LAYERS):
+        p = f"blk.{i}."
+        add_f32(p + "attn_norm.weight", HIDDEN)
+        add_d(p + "attn_q.weight", T_F16, HIDDEN, HIDDEN)
+        add_d(p + "attn_k.weight", T_F16, HIDDEN // 2, HIDDEN)
+        add_d(p + "attn_v.weight", T_F16, HIDDEN // 2, HIDDEN)
+        add_d(p + "attn_output.weight", T_F32 if i == 0 else T_F16, HIDDEN, HIDDEN)
+        add_f32(p + "ffn_norm.weight", HIDDEN)
+        add_d(p + "ffn_gate.weight", T_F16, INTER, HIDDEN)
+        add_d(p + "ffn_up.weight", T_F16, INTER, HIDDEN)
+        add_d(p + "ffn_down.weight", T_BF16 if i == 1 else T_F16, HIDDEN, INTER)
+    add_f32("output_norm.weight", HIDDEN)
+    add_d("output.weight", T_F16, VOCAB, HIDDEN)
+    write(tensors, "tiny_llama_f16", HIDDEN, INTER, LAYERS, rng, npz=False,
+          heads=(HEADS, KV_HEADS), rope_base=ROPE_BASE)
+    write_steps(tensors, "tiny_llama_f16")
 
 
 def layer_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
@@ -123,7 +175,7 @@ def write_steps(tensors, stem) -> None:
 
     W = {}
     for name, ttype, shape, raw, deq in tensors:
-        if ttype == T_F32:
+        if ttype in DENSE:  # the exact values (F16 / BF16 widened)
             W[hf_name(name)] = deq.astype(np.float64)
         else:
             n, k = shape
@@ -229,7 +281,7 @@ def write(tensors, stem, hidden, inter, layers, rng, npz, heads=(4, 2), rope_bas
         mapped = hf_name(name)
         names.append(name)
         hf.append(mapped)
-        if ttype != T_F32 and ("_proj.weight" in mapped or "lm_head.weight" in mapped):
+        if "_proj.weight" in mapped or "lm_head.weight" in mapped:
             n, k = shape
             x = rng.normal(0, 1, size=(3, k)).astype(np.float32)
             key = mapped.replace(".", "_")

@@ -27,6 +27,8 @@ def test_header_constants_match_binding():
                          ("UNILLM_PATH_GEMV", _capi.PATH_GEMV),
                          ("UNILLM_PATH_DECODE_MFMA", _capi.PATH_DECODE_MFMA),
                          ("UNILLM_PATH_PREFILL_MFMA", _capi.PATH_PREFILL_MFMA),
+                         ("UNILLM_QTYPE_F32", _capi.F32), ("UNILLM_QTYPE_F16", _capi.F16),
+                         ("UNILLM_QTYPE_BF16", _capi.BF16), ("UNILLM_PATH_DENSE", _capi.PATH_DENSE),
                          ("UNILLM_ERR_INVALID_ARG", _capi.ERR_INVALID_ARG),
                          ("UNILLM_ERR_UNSUPPORTED", _capi.ERR_UNSUPPORTED)]:
         assert f"#define {macro} {value}" in text or f"#define {macro} ({value})" in text, macro
@@ -51,6 +53,22 @@ def test_create_rejects_bad_shape(lib, n, k):
     rc, _ = _create(lib, _capi.Q4_0, n, k, 18)
     assert rc == _capi.ERR_INVALID_ARG
     assert "multiple of 32" in _capi.last_error()
+
+
+@pytest.mark.parametrize("qtype,esize", [(_capi.F32, 4), (_capi.F16, 2), (_capi.BF16, 2)])
+def test_dense_create_checks_shape_and_bytes_on_the_host(lib, qtype, esize):
+    # dense weights take any k >= 1 (candle's dequantized QMatMul has no block size),
+    # and n * k elements of their GGUF type; both are checked before any device work
+    rc, _ = _create(lib, qtype, 0, 7, esize)
+    assert rc == _capi.ERR_INVALID_ARG and "need n, k >= 1" in _capi.last_error()
+    rc, _ = _create(lib, qtype, 3, 7, 3 * 7 * esize + 1)
+    assert rc == _capi.ERR_INVALID_ARG and "nbytes" in _capi.last_error()
+
+
+def test_dense_types_have_one_element_blocks():
+    for q, esize in ((_capi.F32, 4), (_capi.F16, 2), (_capi.BF16, 2)):
+        assert _capi.BLOCK_ELEMS[q] == 1 and _capi.BLOCK_BYTES[q] == esize
+        assert q in _capi.DENSE
 
 
 def test_create_rejects_wrong_byte_count(lib):

@@ -4,7 +4,8 @@ files (CPU), then loading the tiny GGUFs onto the device and QMatMul::forward
 parity against the committed expectations, load-time QKV / gate+up fusion, and
 the KV-cache mirror (LayerKVCache / KVCache with closed-form attention checks and
 the reference's overflow message), and LlamaModel::forward_with_cache over the
-tiny Q4_0 model against the f64 logits of tests/golden/tiny_llama_q4_0.step (GPU)."""
+tiny Q4_0 model against the f64 logits of tests/golden/tiny_llama_q4_0.step (GPU);
+the same for tiny_llama_f16 (dense F16 / F32 / BF16 projections)."""
 import os
 import subprocess
 
@@ -45,3 +46,15 @@ def test_host_k_quants_gpu():
 @pytest.mark.gpu
 def test_host_model_step_gpu():
     _run("gpu-step", data=".step")
+
+
+@pytest.mark.gpu
+def test_host_dense_gpu():
+    # F16 / F32 / BF16 projections (candle's dequantized QMatMul), loaded and fused
+    _run("gpu-dense", "tiny_llama_f16")
+
+
+@pytest.mark.gpu
+def test_host_dense_model_step_gpu():
+    # the whole step, eager and captured, on the dense model against its f64 logits
+    _run("gpu-step", "tiny_llama_f16", data=".step")

@@ -93,6 +93,8 @@ def test_build_rs_matches_build_py():
     assert sources == build.SOURCES
     flags = re.findall(r'"([^"]+)"', re.search(r"const FLAGS.*?\];", text, re.S).group(0))
     assert flags == build.FLAGS
+    libs = re.findall(r'"([^"]+)"', re.search(r"const LIBS.*?\];", text, re.S).group(0))
+    assert libs == build.LIBS
     assert "--offload-arch=gfx950" in flags and "-packed-fp32-ops" in flags
     assert '"-shared"' in text
 

@@ -6,13 +6,14 @@ it with ctypes (``unillm_amd._capi``) and mirrors the reference's call
 surface for this path (``QuantLinear``, the `Arc<QMatMul>` of
 crates/runtime/src/model_core.rs:134).
 """
-from ._capi import (BLOCK_BYTES, BLOCK_ELEMS, ERR_HIP, ERR_INVALID_ARG, ERR_UNSUPPORTED, OK, PATH_AUTO,
-                    PATH_DECODE_MFMA, PATH_GEMV, PATH_PREFILL_MFMA, QK, Q4_0, Q4_K, Q6_K, Q8_0,
-                    HipError)
+from ._capi import (BF16, BLOCK_BYTES, BLOCK_ELEMS, ERR_HIP, ERR_INVALID_ARG, ERR_UNSUPPORTED, F16, F32,
+                    OK, PATH_AUTO, PATH_DECODE_MFMA, PATH_DENSE, PATH_GEMV, PATH_PREFILL_MFMA, QK,
+                    Q4_0, Q4_K, Q6_K, Q8_0, HipError)
 
 __all__ = [
-    "BLOCK_BYTES", "BLOCK_ELEMS", "ERR_HIP", "ERR_INVALID_ARG", "ERR_UNSUPPORTED", "OK", "PATH_AUTO",
-    "PATH_DECODE_MFMA", "PATH_GEMV", "PATH_PREFILL_MFMA", "QK", "Q4_0", "Q4_K", "Q6_K", "Q8_0",
+    "BF16", "BLOCK_BYTES", "BLOCK_ELEMS", "ERR_HIP", "ERR_INVALID_ARG", "ERR_UNSUPPORTED", "F16", "F32",
+    "OK", "PATH_AUTO", "PATH_DECODE_MFMA", "PATH_DENSE", "PATH_GEMV", "PATH_PREFILL_MFMA", "QK",
+    "Q4_0", "Q4_K", "Q6_K", "Q8_0",
     "HipError",
     "QuantLinear", "quantize_blocks", "lm_head_forward", "KvCache",
 ]

@@ -23,7 +23,10 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libunillm_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["capi.hip", "weights.hip", "gemv.hip", "decode.hip", "prefill.hip", "attention.hip"]
+SOURCES = ["capi.hip", "weights.hip", "gemv.hip", "decode.hip", "prefill.hip", "attention.hip",
+           "dense.hip"]
+# the dense (F32 / F16 / BF16) weights' f32 GEMM
+LIBS = ["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]
 HOST_SOURCES = ["gguf.cpp", "unillm_host.cpp"]
 HOST_LIB = os.path.join(HERE, "libunillm_host.so")
 HOST_TEST = os.path.join(os.path.dirname(HERE), "tests", "cpp", "test_host")
@@ -53,7 +56,7 @@ def build(verbose: bool = False) -> str:
     with cf.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs, *LIBS]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")

@@ -102,13 +102,23 @@ int ensure_init() {
 
 bool valid_qtype(int q) {
     return q == UNILLM_QTYPE_Q4_0 || q == UNILLM_QTYPE_Q8_0 || q == UNILLM_QTYPE_Q4_K ||
-           q == UNILLM_QTYPE_Q6_K;
+           q == UNILLM_QTYPE_Q6_K || is_dense(q);
 }
 
 int check_shape(int qtype, int64_t n, int64_t k) {
     if (!valid_qtype(qtype))
-        return fail(UNILLM_ERR_UNSUPPORTED, "unsupported qtype " + std::to_string(qtype) +
-                                                " (want 2 = Q4_0, 8 = Q8_0, 12 = Q4_K, 14 = Q6_K)");
+        return fail(UNILLM_ERR_UNSUPPORTED,
+                    "unsupported qtype " + std::to_string(qtype) +
+                        " (want 2 = Q4_0, 8 = Q8_0, 12 = Q4_K, 14 = Q6_K, or dense 0 = F32, "
+                        "1 = F16, 30 = BF16)");
+    if (is_dense(qtype)) {
+        if (n < 1 || k < 1)
+            return fail(UNILLM_ERR_INVALID_ARG, "bad weight shape [" + std::to_string(n) + ", " +
+                                                    std::to_string(k) + "]: need n, k >= 1");
+        if (n > (int64_t)INT32_MAX || k > (int64_t)INT32_MAX)
+            return fail(UNILLM_ERR_INVALID_ARG, "weight shape too large");
+        return UNILLM_OK;
+    }
     const int64_t blk = gguf_block_elems(qtype);
     if (n < 1 || k < blk || k % blk != 0)
         return fail(UNILLM_ERR_INVALID_ARG, "bad weight shape [" + std::to_string(n) + ", " +
@@ -122,6 +132,12 @@ int check_shape(int qtype, int64_t n, int64_t k) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// GGUF bytes of an [n, k] tensor of this type
+size_t gguf_bytes(int qtype, int64_t n, int64_t k) {
+    if (is_dense(qtype)) return (size_t)n * (size_t)k * (size_t)dense_elem_bytes(qtype);
+    return (size_t)(n * (k / gguf_block_elems(qtype))) * gguf_block_bytes(qtype);
+}
+
 int alloc_weight(int qtype, int64_t n, int64_t k, QWeight** out) {
     QWeight* w = new (std::nothrow) QWeight{};
     if (!w) return fail(UNILLM_ERR_OUT_OF_MEMORY, "host allocation failed");
@@ -129,8 +145,8 @@ int alloc_weight(int qtype, int64_t n, int64_t k, QWeight** out) {
     w->device = g_device;
     w->n = n;
     w->k = k;
-    w->kb = k / QK;
-    w->row_bytes = row_bytes_for(qtype, w->kb);
+    w->kb = is_dense(qtype) ? 0 : k / QK;
+    w->row_bytes = is_dense(qtype) ? 4 * k : row_bytes_for(qtype, w->kb);
     // + a 256-byte tail slot for the scale reduction run at create
     w->bytes = (((size_t)n * (size_t)w->row_bytes + 255) & ~(size_t)255) + 256;
     void* mem = nullptr;
@@ -159,6 +175,11 @@ int finish_weight(QWeight* w, hipStream_t s) {
     uint32_t* slot = reinterpret_cast<uint32_t*>(w->base + w->bytes - 256);
     uint32_t bits[2] = {0, 0};
     hipError_t e;
+    if (is_dense(w->qtype)) {  // f32 rows: no scales to range
+        w->f16_exp = 0;
+        if ((e = hipStreamSynchronize(s)) != hipSuccess) return fail_hip(e, "weight upload");
+        return UNILLM_OK;
+    }
     if ((e = hipMemsetAsync(slot, 0, sizeof(bits), s)) != hipSuccess)
         return fail_hip(e, "hipMemsetAsync");
     if ((e = launch_scale_absmax(*w, slot, s)) != hipSuccess) return fail_hip(e, "scale scan");
@@ -261,7 +282,7 @@ int unillm_hip_qweight_create(int qtype, int64_t n, int64_t k, const void* host_
     if (int rc = check_shape(qtype, n, k)) return rc;
     if (!host_blocks) return fail(UNILLM_ERR_INVALID_ARG, "host_blocks is NULL");
     if (layout_flags != 0) return fail(UNILLM_ERR_INVALID_ARG, "layout_flags must be 0");
-    const size_t want = (size_t)(n * (k / gguf_block_elems(qtype))) * gguf_block_bytes(qtype);
+    const size_t want = gguf_bytes(qtype, n, k);
     if (nbytes != want)
         return fail(UNILLM_ERR_INVALID_ARG, "nbytes " + std::to_string(nbytes) + " != " +
                                                 std::to_string(want) + " for this shape");
@@ -274,8 +295,9 @@ int unillm_hip_qweight_create(int qtype, int64_t n, int64_t k, const void* host_
     if (rc == UNILLM_OK) {
         if ((e = hipMemcpy(staging, host_blocks, want, hipMemcpyHostToDevice)) != hipSuccess)
             rc = fail_hip(e, "hipMemcpy (upload)");
-        else if ((e = launch_repack(*w, static_cast<const uint8_t*>(staging), nullptr)) !=
-                 hipSuccess)
+        else if ((e = is_dense(qtype) ? launch_dense_upload(*w, staging, nullptr)
+                                      : launch_repack(*w, static_cast<const uint8_t*>(staging),
+                                                      nullptr)) != hipSuccess)
             rc = fail_hip(e, "repack launch");
         else
             rc = finish_weight(w, nullptr);
@@ -300,17 +322,20 @@ int unillm_hip_qweight_create_device(int qtype, int64_t n, int64_t k, const void
     if (int rc = check_shape(qtype, n, k)) return rc;
     if (!dev_blocks) return fail(UNILLM_ERR_INVALID_ARG, "dev_blocks is NULL");
     if (layout_flags != 0) return fail(UNILLM_ERR_INVALID_ARG, "layout_flags must be 0");
-    const size_t want = (size_t)(n * (k / gguf_block_elems(qtype))) * gguf_block_bytes(qtype);
+    const size_t want = gguf_bytes(qtype, n, k);
     if (nbytes != want)
         return fail(UNILLM_ERR_INVALID_ARG, "nbytes " + std::to_string(nbytes) + " != " +
                                                 std::to_string(want) + " for this shape");
-    if (((uintptr_t)dev_blocks & 1u) != 0)
-        return fail(UNILLM_ERR_INVALID_ARG, "dev_blocks must be 2-byte aligned");
+    if (((uintptr_t)dev_blocks & (qtype == UNILLM_QTYPE_F32 ? 3u : 1u)) != 0)
+        return fail(UNILLM_ERR_INVALID_ARG, qtype == UNILLM_QTYPE_F32
+                                                ? "dev_blocks must be 4-byte aligned"
+                                                : "dev_blocks must be 2-byte aligned");
     if (int rc = ensure_init()) return rc;
     QWeight* w = nullptr;
     if (int rc = alloc_weight(qtype, n, k, &w)) return rc;
-    hipError_t e = launch_repack(*w, static_cast<const uint8_t*>(dev_blocks),
-                                 static_cast<hipStream_t>(stream));
+    hipError_t e = is_dense(qtype) ? launch_dense_upload(*w, dev_blocks, static_cast<hipStream_t>(stream))
+                                   : launch_repack(*w, static_cast<const uint8_t*>(dev_blocks),
+                                                   static_cast<hipStream_t>(stream));
     int rc = e == hipSuccess ? finish_weight(w, static_cast<hipStream_t>(stream))
                              : fail_hip(e, "repack launch");
     if (rc != UNILLM_OK) {
@@ -341,6 +366,7 @@ int unillm_hip_qweight_info(const unillm_qweight* w, int* qtype, int64_t* n, int
 
 int unillm_hip_select_path(const unillm_qweight* w, int64_t m) {
     if (!w || m < 0) return fail(UNILLM_ERR_INVALID_ARG, "bad arguments to select_path");
+    if (is_dense(w->qtype)) return UNILLM_PATH_DENSE;
     if (gemv_supports(*w, m)) return UNILLM_PATH_GEMV;
     if (m <= kDecodeMaxM) return UNILLM_PATH_DECODE_MFMA;
     return UNILLM_PATH_PREFILL_MFMA;
@@ -359,6 +385,47 @@ int fail_launch(hipError_t e, const std::string& what) {
                         "reserve it before capture (unillm_hip_qmatmul_reserve / "
                         "unillm_hip_attention_reserve) or make the same call once eagerly");
     return fail_hip(e, what.c_str());
+}
+
+// A dense weight's call: the layer norm (if any) into the stream's workspace (slot 0),
+// the f32 GEMM, and for SwiGLU the product into slot 1 and the elementwise pass.
+int dense_impl(const unillm_qweight* w, const float* x, int64_t m, float* y, int path,
+               hipStream_t s, int epi, const NormArgs& norm, const std::string& what,
+               void* fixed_ws) {
+    if (path != UNILLM_PATH_AUTO && path != UNILLM_PATH_DENSE)
+        return fail(UNILLM_ERR_UNSUPPORTED,
+                    what + ": a dense (F32 / F16 / BF16) weight takes the dense path only");
+    if (fixed_ws)
+        return fail(UNILLM_ERR_UNSUPPORTED,
+                    what + ": the no-allocation entry point takes quantized weights only "
+                           "(the dense path's GEMM library)");
+    if (m > (int64_t)INT32_MAX)
+        return fail(UNILLM_ERR_INVALID_ARG, what + ": m too large for the f32 GEMM");
+    hipError_t e = hipSuccess;
+    auto failed = [&](const std::string& where) {
+        const std::string d = dense_error();
+        if (e == hipErrorUnknown && !d.empty()) return fail(UNILLM_ERR_HIP, what + ": " + d);
+        return fail_launch(e, what + ": " + where);
+    };
+    if (norm.gamma) {
+        void* xn = nullptr;
+        if ((e = stream_workspace(s, (size_t)m * (size_t)w->k * sizeof(float), &xn, 0)) != hipSuccess)
+            return failed("workspace");
+        if ((e = launch_norm_rows(x, m, w->k, norm, static_cast<float*>(xn), s)) != hipSuccess)
+            return failed("layer norm launch");
+        x = static_cast<const float*>(xn);
+    }
+    float* out = y;
+    if (epi == kEpiSwiglu) {
+        void* ws = nullptr;
+        if ((e = stream_workspace(s, (size_t)m * (size_t)w->n * sizeof(float), &ws, 1)) != hipSuccess)
+            return failed("workspace");
+        out = static_cast<float*>(ws);
+    }
+    if ((e = launch_dense(*w, x, m, out, s, epi == kEpiAdd)) != hipSuccess) return failed("f32 GEMM");
+    if (out != y && (e = launch_swiglu(out, m, w->n / 2, y, s)) != hipSuccess)
+        return failed("SwiGLU launch");
+    return UNILLM_OK;
 }
 
 // The matmul on `path` with epilogue `epi` (kEpiStore / kEpiAdd; kEpiSwiglu runs
@@ -384,7 +451,7 @@ int qmatmul_impl(const unillm_qweight* w, const float* x_dev, int64_t m, float* 
                        !(norm.eps >= 0.0f)))
         return fail(UNILLM_ERR_INVALID_ARG,
                     what + ": norm weight / bias must be 16-byte aligned, eps >= 0");
-    if (path == UNILLM_PATH_AUTO) {
+    if (path == UNILLM_PATH_AUTO && !is_dense(w->qtype)) {
         path = unillm_hip_select_path(w, m);
         // a fused layer norm on the GEMV takes k <= 8192; past it, batched decode
         if (norm.gamma && path == UNILLM_PATH_GEMV && !gemv_supports_norm(*w, m))
@@ -400,6 +467,7 @@ int qmatmul_impl(const unillm_qweight* w, const float* x_dev, int64_t m, float* 
     if (int rc = ensure_init()) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipError_t e;
+    if (is_dense(w->qtype)) return dense_impl(w, x_dev, m, y_dev, path, s, epi, norm, what, fixed_ws);
     // x not on a 16-byte boundary (candle takes any contiguous f32): the kernels
     // load x 16 bytes at a time, so it is first copied, stream-ordered, into an
     // aligned workspace (slot 3)
@@ -517,6 +585,16 @@ int unillm_hip_qmatmul_reserve(const unillm_qweight* w, int64_t m, int swiglu, v
     if (m > (int64_t)INT32_MAX / 2) return fail(UNILLM_ERR_INVALID_ARG, "reserve: m too large");
     if (int rc = ensure_init()) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (is_dense(w->qtype)) {
+        // the f32 GEMM's handle, slot 0 (a fused norm's rows), slot 1 (SwiGLU's product)
+        void* p = nullptr;
+        hipError_t e = dense_prepare(s);
+        if (e == hipSuccess)
+            e = stream_workspace(s, (size_t)m * (size_t)w->k * sizeof(float), &p, 0);
+        if (e == hipSuccess && swiglu)
+            e = stream_workspace(s, (size_t)m * (size_t)w->n * sizeof(float), &p, 1);
+        return e == hipSuccess ? UNILLM_OK : fail_launch(e, "reserve");
+    }
     // slot 0: the x operand of either MFMA path at any m' <= m (both sizes grow with m;
     // the batched decode's with a fused norm bounds the one without)
     const float unused_gamma = 0.0f;
@@ -552,14 +630,17 @@ int unillm_hip_dequant(const unillm_qweight* w, float* out_dev, void* stream) {
     if (!w || !out_dev) return fail(UNILLM_ERR_INVALID_ARG, "weight or out is NULL");
     if (!aligned16(out_dev)) return fail(UNILLM_ERR_INVALID_ARG, "out must be 16-byte aligned");
     if (int rc = ensure_init()) return rc;
-    hipError_t e = launch_dequant(*w, out_dev, static_cast<hipStream_t>(stream));
+    hipError_t e = is_dense(w->qtype)
+                       ? hipMemcpyAsync(out_dev, w->base, (size_t)w->n * (size_t)w->k * sizeof(float),
+                                        hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream))
+                       : launch_dequant(*w, out_dev, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? UNILLM_OK : fail_hip(e, "dequant launch");
 }
 
 int unillm_hip_quantize(int qtype, const float* w_dev, int64_t n, int64_t k, void* blocks_dev,
                         void* stream) {
     if (int rc = check_shape(qtype, n, k)) return rc;
-    if (is_kquant(qtype))
+    if (is_kquant(qtype) || is_dense(qtype))
         return fail(UNILLM_ERR_UNSUPPORTED, "the device quantizer covers Q4_0 and Q8_0 only");
     if (!w_dev || !blocks_dev) return fail(UNILLM_ERR_INVALID_ARG, "w or blocks is NULL");
     if (!aligned16(w_dev)) return fail(UNILLM_ERR_INVALID_ARG, "w must be 16-byte aligned");

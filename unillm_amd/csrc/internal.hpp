@@ -218,6 +218,22 @@ hipError_t launch_x_to_f16_rows(const float* x, int64_t m, int64_t k, void* out,
 // gu[m, 2 I] (the SwiGLU of the MFMA paths, after their store)
 hipError_t launch_swiglu(const float* gu, int64_t m, int64_t I, float* act, hipStream_t s);
 
+// Dense (F32 / F16 / BF16) weights: f32 rows [n][k] at base (row_bytes = 4 k).
+bool is_dense(int qtype);
+int dense_elem_bytes(int qtype);
+// the weight's f32 rows from its GGUF elements at src (device memory), on s
+hipError_t launch_dense_upload(const QWeight& w, const void* src, hipStream_t s);
+// y = x W^T (add: y += x W^T) in f32; the GEMM's handle is created on first use
+// (dense_prepare creates it ahead, outside any capture)
+hipError_t launch_dense(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t s,
+                        int add);
+hipError_t dense_prepare(hipStream_t s);
+// the layer norm of each row of x into out (f32), ops_fn::layer_norm's two passes
+hipError_t launch_norm_rows(const float* x, int64_t m, int64_t k, const NormArgs& norm,
+                            float* out, hipStream_t s);
+// the message of the last failing dense call on this thread
+std::string dense_error();
+
 // Attention (attention.hip): RoPE at positions len .. len + m - 1 on the fused QKV
 // rows qkv[m, (H + 2 KVH) hd], k / v appended to the cache, causal softmax
 // attention into out[m, H hd]; the kernels read len from kv.state[0] and advance

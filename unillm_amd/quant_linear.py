@@ -20,7 +20,7 @@ import numpy as np
 import torch
 
 from . import _capi
-from ._capi import BLOCK_BYTES, BLOCK_ELEMS, QK, Q4_0, Q4_K, Q6_K, Q8_0, HipError
+from ._capi import BF16, BLOCK_BYTES, BLOCK_ELEMS, F16, F32, QK, Q4_0, Q4_K, Q6_K, Q8_0, HipError
 
 
 def _stream_ptr(stream: torch.cuda.Stream | None) -> int:
@@ -41,7 +41,8 @@ class QuantLinear:
     @classmethod
     def from_blocks(cls, qtype: int, n: int, k: int, blocks) -> "QuantLinear":
         """From GGUF block bytes in host memory (n * k/32 blocks of 18 / 34 B, or
-        n * k/256 blocks of 144 / 210 B for Q4_K / Q6_K)."""
+        n * k/256 blocks of 144 / 210 B for Q4_K / Q6_K; a dense F32 / F16 / BF16
+        tensor's n * k elements)."""
         buf = np.ascontiguousarray(np.frombuffer(memoryview(blocks), dtype=np.uint8))
         h = ctypes.c_void_p()
         _capi.check(_capi.lib().unillm_hip_qweight_create(
@@ -59,6 +60,18 @@ class QuantLinear:
             qtype, n, k, blocks.data_ptr(), blocks.numel(), 0, _stream_ptr(stream),
             ctypes.byref(h)))
         return cls(h.value, qtype, n, k)
+
+    @classmethod
+    def from_dense(cls, w: torch.Tensor,
+                   stream: torch.cuda.Stream | None = None) -> "QuantLinear":
+        """A dense [n, k] device tensor (float32, float16 or bfloat16), kept as f32 rows
+        and multiplied in f32, as candle's QMatMul keeps a dense GGUF tensor."""
+        qtype = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}.get(w.dtype)
+        if qtype is None or w.dim() != 2 or not w.is_cuda:
+            raise ValueError("w must be a 2-D float32 / float16 / bfloat16 device tensor")
+        w = w.contiguous()
+        return cls.from_device_blocks(qtype, w.shape[0], w.shape[1],
+                                      w.view(-1).view(torch.uint8), stream)
 
     @classmethod
     def quantize(cls, qtype: int, w: torch.Tensor,
@@ -202,8 +215,8 @@ class QuantLinear:
             pass
 
     def __repr__(self) -> str:
-        name = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}.get(self.qtype,
-                                                                         str(self.qtype))
+        name = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", F32: "F32", F16: "F16",
+                BF16: "BF16"}.get(self.qtype, str(self.qtype))
         return f"QuantLinear({name}, n={self.n}, k={self.k})"
 
 

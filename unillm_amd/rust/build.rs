@@ -18,7 +18,12 @@ const SOURCES: &[&str] = &[
     "decode.hip",
     "prefill.hip",
     "attention.hip",
+    "dense.hip",
 ];
+
+// Libraries the link adds: the dense (F32 / F16 / BF16) weights' f32 GEMM.  Keep in step
+// with LIBS in unillm_amd/build.py.
+const LIBS: &[&str] = &["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"];
 
 const FLAGS: &[&str] = &[
     "--offload-arch=gfx950",
@@ -77,7 +82,8 @@ fn main() {
         Command::new(&hipcc)
             .args(["--offload-arch=gfx950", "-shared", "-fPIC", "-o"])
             .arg(&lib)
-            .args(&objs),
+            .args(&objs)
+            .args(LIBS),
         "hipcc -shared",
     );
     println!("cargo:rustc-link-search=native={}", out.display());

@@ -49,6 +49,9 @@ pub mod sys {
     pub const UNILLM_QTYPE_Q8_0: c_int = 8;
     pub const UNILLM_QTYPE_Q4_K: c_int = 12;
     pub const UNILLM_QTYPE_Q6_K: c_int = 14;
+    pub const UNILLM_QTYPE_F32: c_int = 0;
+    pub const UNILLM_QTYPE_F16: c_int = 1;
+    pub const UNILLM_QTYPE_BF16: c_int = 30;
 
     pub const UNILLM_OK: c_int = 0;
     pub const UNILLM_ERR_INVALID_ARG: c_int = -1;
@@ -61,6 +64,7 @@ pub mod sys {
     pub const UNILLM_PATH_GEMV: c_int = 1;
     pub const UNILLM_PATH_DECODE_MFMA: c_int = 2;
     pub const UNILLM_PATH_PREFILL_MFMA: c_int = 3;
+    pub const UNILLM_PATH_DENSE: c_int = 4;
 
     extern "C" {
         pub fn unillm_hip_init(device: c_int) -> c_int;
@@ -249,7 +253,8 @@ impl Drop for DeviceBuffer {
 
 // ---- the quantized projection --------------------------------------------------------------
 
-/// GGUF block types the device takes (ggml type ids).
+/// GGUF tensor types the device takes (ggml type ids): the block types, and the dense
+/// F32 / F16 / BF16 that candle keeps as a dequantized f32 QMatMul.
 #[derive(Debug, Clone, Copy, PartialEq, Eq)]
 #[allow(non_camel_case_types)]
 pub enum QType {
@@ -257,6 +262,9 @@ pub enum QType {
     Q8_0 = 8,
     Q4_K = 12,
     Q6_K = 14,
+    F32 = 0,
+    F16 = 1,
+    BF16 = 30,
 }
 
 impl QType {
@@ -267,6 +275,9 @@ impl QType {
             8 => Some(Self::Q8_0),
             12 => Some(Self::Q4_K),
             14 => Some(Self::Q6_K),
+            0 => Some(Self::F32),
+            1 => Some(Self::F16),
+            30 => Some(Self::BF16),
             _ => None,
         }
     }
@@ -279,6 +290,7 @@ pub enum Path {
     Gemv = 1,
     DecodeMfma = 2,
     PrefillMfma = 3,
+    Dense = 4,
 }
 
 /// One GGUF weight [n, k] resident on the device; immutable after creation, so shared
@@ -334,6 +346,7 @@ impl QuantLinear {
             1 => Ok(Path::Gemv),
             2 => Ok(Path::DecodeMfma),
             3 => Ok(Path::PrefillMfma),
+            4 => Ok(Path::Dense),
             _ => check(p).map(|_| Path::Auto),
         }
     }

@@ -79,8 +79,9 @@ int unillm_hip_init(int device);
 const char* unillm_hip_last_error(void);
 
 /* Upload one GGUF Q4_0 / Q8_0 / Q4_K / Q6_K tensor ([n, k]: n * k/32 blocks of
- * 18 / 34 B, or n * k/256 blocks of 144 / 210 B)
- * to the device, repacked there into the kernels' layout.  Replaces
+ * 18 / 34 B, or n * k/256 blocks of 144 / 210 B), or a dense F32 / F16 / BF16 one
+ * (n * k elements of 4 / 2 / 2 B), to the device, repacked there into the kernels'
+ * layout (dense: f32 rows).  Replaces
  * `QMatMul::from_arc(Arc::new(qtensor))` at
  * crates/runtime/src/weight_loader_core.rs:569-571 (the QTensor read at :545).
  * layout_flags must be 0 (reserved). */

@@ -170,7 +170,7 @@ def cpu_baseline():
 
     def one_pass():
         for b, x, n, k in host:
-            oracle.candle_qmatmul(Q4_0, b, x, n, k, nthreads=threads)
+            oracle.candle_qmatmul(Q4_0, b, x, n, k, nthreads=threads, timing=True)
 
     for _ in range(3):
         one_pass()
@@ -184,7 +184,7 @@ def cpu_baseline():
             break
     med = float(np.median(times))
     return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": threads,
-            "cpu": cpu_model(), "kind": "port",
+            "cpu": cpu_model(), "build": oracle.timing_lib()[1], "kind": "port",
             "sample": f"one Llama-2-7B layer's 5 Q4_0 GEMVs at m=1 ({nbytes / 1e6:.1f} MB), "
                       f"median of {len(times)} passes after 3 warm-ups, "
                       "candle QMatMul semantics restated in C (oracle/oracle.c), OpenMP",
@@ -220,12 +220,12 @@ def cpu_rows(qtype, n, k, rows, budget_s=1.5, seed=0):
             qtype, rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
     w = _CPU_WEIGHTS[(qtype, n, k)]
     x = rng.standard_normal((rows, k), dtype=np.float32)
-    oracle.candle_qmatmul(qtype, w, x, n, k, nthreads=threads)  # warm-up
+    oracle.candle_qmatmul(qtype, w, x, n, k, nthreads=threads, timing=True)  # warm-up
     times = []
     t_end = time.perf_counter() + budget_s
     while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
         t0 = time.perf_counter()
-        oracle.candle_qmatmul(qtype, w, x, n, k, nthreads=threads)
+        oracle.candle_qmatmul(qtype, w, x, n, k, nthreads=threads, timing=True)
         times.append(time.perf_counter() - t0)
     return float(np.median(times)), threads
 
@@ -236,9 +236,11 @@ def extra_cpu_baselines(extra):
     times 8 rows (the reference's row loop costs the same per row, so m rows take m
     times as long); the stack times one layer's four projections and the lm_head
     (32 identical layers)."""
+    import oracle
+
     def entry(value, unit, cores, sample):
         return {"value": round(value, 3), "unit": unit, "cores": cores, "cpu": cpu_model(),
-                "kind": "port",
+                "build": oracle.timing_lib()[1], "kind": "port",
                 "sample": sample + "; candle QMatMul semantics restated in C (oracle/oracle.c), "
                                    "OpenMP over columns, median of timed calls"}
 

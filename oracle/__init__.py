@@ -108,14 +108,47 @@ def qmatmul_f64(qtype: int, blocks: np.ndarray, x: np.ndarray, n: int, k: int,
     return y
 
 
+_timing = None
+
+
+def _host_has_avx512() -> bool:
+    try:
+        with open("/proc/cpuinfo") as f:
+            flags = next((l.split(":", 1)[1].split() for l in f if l.startswith("flags")), [])
+    except OSError:
+        return False
+    return all(x in flags for x in ("avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"))
+
+
+def timing_lib() -> tuple[ctypes.CDLL, str]:
+    """The timing copy of the library for this host (bench.py's CPU baseline only):
+    FMA contraction on, x86-64-v4 where the CPU has AVX-512, else v3; and its flags."""
+    global _timing
+    if _timing is None:
+        v = "v4" if _host_has_avx512() else "v3"
+        path = os.path.join(_HERE, f"liboracle_timing_{v}.so")
+        if not os.path.exists(path):
+            build()
+        l = ctypes.CDLL(path)
+        l.oracle_candle_qmatmul.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                            ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                            ctypes.c_void_p, ctypes.c_int]
+        l.oracle_candle_qmatmul.restype = ctypes.c_int
+        _timing = (l, f"gcc -O3 -march=x86-64-{v} -ffp-contract=fast -fopenmp")
+    return _timing
+
+
 def candle_qmatmul(qtype: int, blocks: np.ndarray, x: np.ndarray, n: int, k: int,
-                   nthreads: int = 0) -> np.ndarray:
-    """candle CPU QMatMul semantics (Q8_0 activations, integer block dots)."""
+                   nthreads: int = 0, timing: bool = False) -> np.ndarray:
+    """candle CPU QMatMul semantics (Q8_0 activations, integer block dots).  timing:
+    run the timing build (FMA contraction, the host's widest vectors) -- bench.py's CPU
+    baseline; results agree with the checker's to f32 rounding."""
     blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
     x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, k)
     m = x.shape[0]
     y = np.empty((m, n), dtype=np.float32)
-    if lib().oracle_candle_qmatmul(qtype, _ptr(blocks), _ptr(x), m, n, k, _ptr(y), nthreads) != 0:
+    l = timing_lib()[0] if timing else lib()
+    if l.oracle_candle_qmatmul(qtype, _ptr(blocks), _ptr(x), m, n, k, _ptr(y), nthreads) != 0:
         raise ValueError("oracle_candle_qmatmul rejected its arguments")
     return y
 

@@ -150,6 +150,39 @@ def test_layer_norm_matmul(qtype, m, n, k, path, bias, offset):
     assert oracle.normwise_error(y.cpu().numpy(), ref) < tol
 
 
+@pytest.mark.parametrize("qtype,m,n,k,bias,offset", [
+    (Q4_0, 16, 4096, 4096, True, 0.0),
+    (Q8_0, 7, 12288, 4096, False, 50.0),
+    (Q4_K, 9, 40000, 1024, True, 0.0),    # more output rows than the device has CUs
+    (Q6_K, 16, 640, 2048, False, 20.0),
+    (Q4_0, 3, 1000, 4128, True, 0.0),     # k: 32 chunks of 128 and one block
+    (Q8_0, 16, 512, 256, False, 0.0)])    # k: two chunks
+def test_layer_norm_batched_decode_shapes(qtype, m, n, k, bias, offset):
+    # the fused layer norm at m <= 16 on the batched decode, over k splits of 1 to 8
+    # slices and ragged k.  Against the f64 reference, and against the same product
+    # of x normalized first (torch, f32): the f16 operands then differ only where an
+    # f32 rounding crosses an f16 one
+    blocks = _blocks(qtype, n, k, seed=7 * n + k)
+    rng = np.random.default_rng(m + n)
+    x = (oracle.normal(m * k, seed=k + 3 * m).reshape(m, k) + offset).astype(np.float32)
+    gamma = (1.0 + 0.1 * rng.normal(size=k)).astype(np.float32)
+    beta = (0.1 * rng.normal(size=k)).astype(np.float32) if bias else None
+    ql = QuantLinear.from_blocks(qtype, n, k, blocks)
+    assert ql.select_path(m) == PATH_DECODE_MFMA
+    print(f"norm in launch qtype={qtype} m={m} n={n} k={k}", flush=True)
+    xd, gd = _dev(x), _dev(gamma)
+    bd = _dev(beta) if bias else None
+    y = ql.forward_norm(xd, gd, bd, eps=1e-5).cpu().numpy()
+    xn = _layer_norm(x, gamma, beta, 1e-5)
+    ref = oracle.qmatmul_f64(qtype, blocks, xn.astype(np.float32), n, k)
+    assert oracle.normwise_error(y, ref) < 1e-3
+    xt = torch.nn.functional.layer_norm(xd, (k,), gd, bd, eps=1e-5)
+    assert oracle.normwise_error(y, ql.forward(xt).cpu().numpy()) < 1e-4
+    # a second call: the same up to the order of the k slices' f32 adds
+    y2 = ql.forward_norm(xd, gd, bd, eps=1e-5).cpu().numpy()
+    assert oracle.normwise_error(y2, y) < 1e-5
+
+
 @pytest.mark.parametrize("qtype,m,i_rows,k", [(Q4_0, 1, 1376, 4096), (Q4_K, 16, 300, 2048)])
 def test_layer_norm_swiglu(qtype, m, i_rows, k):
     # post_attention_layernorm + gate + up + SwiGLU in one call (m = 1: the GEMV

@@ -575,34 +575,35 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
             }
         }
         __syncthreads();
-        float mean[M], sd[M];
+        // lane w2 < WAVES takes wave w2's triple; a wave sum combines them
+        float mean[M], rsd[M];
 #pragma unroll
         for (int mm = 0; mm < M; ++mm) {
-            float sum = 0.0f;
-            for (int w2 = 0; w2 < WAVES; ++w2) sum += red[0][mm * WAVES + w2] * red[1][mm * WAVES + w2];
-            mean[mm] = sum / (float)K;
-            float m2 = 0.0f;
-            for (int w2 = 0; w2 < WAVES; ++w2) {
-                const float d = red[1][mm * WAVES + w2] - mean[mm];
-                m2 += red[2][mm * WAVES + w2] + red[0][mm * WAVES + w2] * d * d;
-            }
-            sd[mm] = sqrtf(m2 / (float)K + norm.eps);
+            const bool mine = lane < WAVES;
+            const int li = mm * WAVES + (mine ? lane : 0);
+            const float n_l = mine ? red[0][li] : 0.0f, mu_l = mine ? red[1][li] : 0.0f,
+                        q_l = mine ? red[2][li] : 0.0f;
+            mean[mm] = wave_sum(n_l * mu_l) / (float)K;
+            const float d = mu_l - mean[mm];
+            // one reciprocal a row, a product an element (within an f32 rounding of
+            // the quotient, far below what the x digits keep)
+            rsd[mm] = 1.0f / sqrtf(wave_sum(q_l + n_l * d * d) / (float)K + norm.eps);
         }
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             if (wave0 + p * THREADS >= nq) continue;
             const int q = min((int)threadIdx.x + p * THREADS, nq - 1);
             const int m = (q >> 2) / KB;
-            float mu = mean[0], sg = sd[0];
+            float mu = mean[0], rs = rsd[0];
 #pragma unroll
             for (int mm = 1; mm < M; ++mm) {
                 mu = m == mm ? mean[mm] : mu;
-                sg = m == mm ? sd[mm] : sg;
+                rs = m == mm ? rsd[mm] : rs;
             }
             const float (&g)[8] = gmv[p];
             const float (&bb)[8] = btv[p];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[p][j] = (v[p][j] - mu) / sg * g[j] + bb[j];
+            for (int j = 0; j < 8; ++j) v[p][j] = (v[p][j] - mu) * rs * g[j] + bb[j];
         }
     }
 

@@ -909,9 +909,13 @@ __global__ __launch_bounds__(256) void decode_x_kernel(const uint8_t* __restrict
         }
     };
 
+    // Each wave reads only what its own direct loads wrote (its rows' payloads, scales
+    // and headers; x is in LDS already), so its own load count is the only wait: no
+    // barrier, and the waves do not wait for each other chunk by chunk.  The slot a
+    // chunk's loads overwrite was last read by this wave's previous chunk, whose reads
+    // completed before its MFMAs.
     for (int j = 0; j < nch; ++j) {
         wait_chunks<ST::PD, D - 2>(min(D - 2, nch - 1 - j));
-        __builtin_amdgcn_s_barrier();
         if (j + D - 1 < nch) issue(j + D - 1);
         compute(j);
     }

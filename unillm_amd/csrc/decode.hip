@@ -97,11 +97,13 @@ __device__ __forceinline__ float wave_sum(float v) {
     return wave_reduce(v, [](float a, float b) { return a + b; });
 }
 
-// (a & mask) | bits in one instruction (the compiler splits it in two).
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(bits));
-    return r;
+// A signed nibble pair of w (mask 0x000F000F: bits 0 .. 3 and 16 .. 19; 0x00F000F0:
+// bits 4 .. 7 and 20 .. 23) flipped to q = s + 8 under the f16 exponent 0x6400:
+// ((w ^ 0x88888888) & mask) | 0x64006400 as one v_bitop3 ((w & mask) ^ k, k the
+// masked flip bits and the exponent bits, which the mask leaves clear).
+constexpr uint32_t kNibLo = 0x000F000Fu, kNibHi = 0x00F000F0u;
+__device__ __forceinline__ uint32_t nib_f16(uint32_t w, uint32_t mask) {
+    return (w & mask) ^ ((0x88888888u & mask) | 0x64006400u);
 }
 
 // f16 pair (v - bias) * dh, v holding two f16 1024 + code: exact but the last step.
@@ -118,17 +120,15 @@ __device__ __forceinline__ uint32_t scale2(uint32_t v, f16x2 bias, f16x2 dh) {
 __device__ __forceinline__ void dequant_q4(u32x4 raw, f16x2 dh, f16x2 dh16, f16x8 (&f)[4]) {
     const f16x2 blo = {(_Float16)1032.0f, (_Float16)1032.0f};
     const f16x2 bhi = {(_Float16)1152.0f, (_Float16)1152.0f};
-    const uint32_t magic = 0x64006400u;
     u32x4 o[4];
 #pragma unroll
     for (int d = 0; d < 4; ++d) {  // bytes 4d .. 4d + 3: elements 4d .. (low), 16 + 4d .. (high)
-        const uint32_t w = raw[d] ^ 0x88888888u;  // signed nibble -> q
-        const uint32_t w8 = w >> 8;
+        const uint32_t w = raw[d], w8 = w >> 8;
         const int lo = d / 2, e = 2 * (d % 2);
-        o[lo][e] = scale2(and_or(w, 0x000F000Fu, magic), blo, dh);          // bytes 0, 2 low
-        o[lo][e + 1] = scale2(and_or(w8, 0x000F000Fu, magic), blo, dh);     // bytes 1, 3 low
-        o[2 + lo][e] = scale2(and_or(w, 0x00F000F0u, magic), bhi, dh16);    // bytes 0, 2 high
-        o[2 + lo][e + 1] = scale2(and_or(w8, 0x00F000F0u, magic), bhi, dh16);  // bytes 1, 3 high
+        o[lo][e] = scale2(nib_f16(w, kNibLo), blo, dh);             // bytes 0, 2 low
+        o[lo][e + 1] = scale2(nib_f16(w8, kNibLo), blo, dh);        // bytes 1, 3 low
+        o[2 + lo][e] = scale2(nib_f16(w, kNibHi), bhi, dh16);       // bytes 0, 2 high
+        o[2 + lo][e + 1] = scale2(nib_f16(w8, kNibHi), bhi, dh16);  // bytes 1, 3 high
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) f[q] = __builtin_bit_cast(f16x8, o[q]);
@@ -140,20 +140,18 @@ __device__ __forceinline__ void dequant_q4(u32x4 raw, f16x2 dh, f16x2 dh16, f16x
 __device__ __forceinline__ void dequant_q4k(u32x4 raw, f16x2 sh, f16x2 sh16, f16x2 oh,
                                             f16x8 (&f)[4]) {
     const f16x2 b = {(_Float16)1024.0f, (_Float16)1024.0f};
-    const uint32_t magic = 0x64006400u;
     auto fma2 = [&](uint32_t v, f16x2 sc) {
         return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, v) - b) * sc - oh);
     };
     u32x4 o[4];
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-        const uint32_t w = raw[d] ^ 0x88888888u;  // signed nibble -> q
-        const uint32_t w8 = w >> 8;
+        const uint32_t w = raw[d], w8 = w >> 8;
         const int lo = d / 2, e = 2 * (d % 2);
-        o[lo][e] = fma2(and_or(w, 0x000F000Fu, magic), sh);
-        o[lo][e + 1] = fma2(and_or(w8, 0x000F000Fu, magic), sh);
-        o[2 + lo][e] = fma2(and_or(w, 0x00F000F0u, magic), sh16);
-        o[2 + lo][e + 1] = fma2(and_or(w8, 0x00F000F0u, magic), sh16);
+        o[lo][e] = fma2(nib_f16(w, kNibLo), sh);
+        o[lo][e + 1] = fma2(nib_f16(w8, kNibLo), sh);
+        o[2 + lo][e] = fma2(nib_f16(w, kNibHi), sh16);
+        o[2 + lo][e + 1] = fma2(nib_f16(w8, kNibHi), sh16);
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) f[q] = __builtin_bit_cast(f16x8, o[q]);

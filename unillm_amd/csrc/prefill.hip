@@ -86,13 +86,6 @@ __device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
     return r;
 }
 
-// (a & mask) | bits in one instruction (the compiler splits it in two)
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(mask), "v"(bits));
-    return r;
-}
-
 // f16 pair (v - bias) * sc, v holding two f16 1024 + code: exact but the last step
 __device__ __forceinline__ uint32_t scale2(uint32_t v, f16x2 bias, f16x2 sc) {
     return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, v) - bias) * sc);
@@ -126,9 +119,11 @@ __device__ __forceinline__ f16x8 dequant8_f16(u32x2 raw, uint32_t mask, f16x2 bi
     for (int h = 0; h < 2; ++h) {
         uint32_t p0, p1;
         if constexpr (kNib) {
-            const uint32_t w = raw[h] ^ 0x88888888u;  // signed nibbles -> q
-            p0 = and_or(w, mask, 0x64006400u);         // bytes 0, 2
-            p1 = and_or(w >> 8, mask, 0x64006400u);    // bytes 1, 3
+            // signed nibbles flipped to q under the f16 exponent 0x6400:
+            // ((w ^ 0x88888888) & mask) | 0x64006400 as one v_bitop3 each
+            const uint32_t kx = (0x88888888u & mask) | 0x64006400u;
+            p0 = (raw[h] & mask) ^ kx;           // bytes 0, 2
+            p1 = ((raw[h] >> 8) & mask) ^ kx;    // bytes 1, 3
         } else {
             const uint32_t w = raw[h] ^ 0x80808080u;  // int8 -> q + 128
             p0 = __builtin_amdgcn_perm(0x64646464u, w, 0x04020400u);

@@ -178,6 +178,27 @@ def test_baseline_decode_shapes_m1(qtype, k, n):
     assert np.array_equal(_run(ql, -x, PATH_AUTO), -y)
 
 
+@pytest.mark.parametrize("qtype,k,n", [(Q4_0, 4096, 5000), (Q8_0, 2048, 5632),
+                                       (Q8_0, 1024, 8191), (Q4_0, 11008, 2049)])
+def test_gemv_partial_second_round(qtype, k, n):
+    # more rows than waves, fewer than twice as many: the waves holding a second row
+    # are numbered across the workgroups (every row still computed exactly once)
+    blocks, x = _case(qtype, 1, n, k, seed=3 * n + k)
+    ql = QuantLinear.from_blocks(qtype, n, k, blocks)
+    assert ql.select_path(1) == PATH_GEMV
+    ref = oracle.qmatmul_f64(qtype, blocks, x, n, k)
+    xd = _dev(x)
+    print(f"gemv partial round qtype={qtype} k={k} n={n}", flush=True)
+    y = ql.forward(xd).cpu().numpy()
+    assert oracle.normwise_error(y, ref) < 1e-4
+    # every row, not only on average: no row left out or written twice
+    assert np.all(np.abs(y - ref) <= 1e-4 * np.abs(ref).max())
+    y0 = oracle.normal(n, seed=n).reshape(1, n).astype(np.float32)
+    ya = _dev(y0)
+    ql.forward_add(xd, ya)
+    assert np.array_equal(ya.cpu().numpy(), y0 + y)
+
+
 @pytest.mark.parametrize("m", [4, 16, 64])
 @pytest.mark.parametrize("n", [4096, 14336])
 def test_baseline_batched_decode(m, n):

@@ -424,7 +424,11 @@ constexpr int gemv_threads() {
 // tensor_core.rs:973-1008).  Every workgroup reads all of x anyway, so each
 // computes the row statistics itself (one barrier, gamma and beta requested with x),
 // no extra launch.
-template <int QT, int M, int NB, int R, int THREADS, bool PAIR = false, bool NORM = false>
+// XW: waves numbered across the workgroups (wave w of workgroup b is b + w grid), so
+// that the waves holding one row more than the others (a partial last round) spread
+// over every CU instead of filling the first CUs.
+template <int QT, int M, int NB, int R, int THREADS, bool PAIR = false, bool NORM = false,
+          bool XW = false>
 __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict__ base,
                                                        int64_t rb,
                                                        const float* __restrict__ x,
@@ -438,7 +442,9 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     constexpr int PASSES = (M * NB * 256 + THREADS - 1) / THREADS;  // quarter-blocks per thread
     extern __shared__ uint32_t xlds[];
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * WAVES + (threadIdx.x >> 6));
+    const int wave = __builtin_amdgcn_readfirstlane(
+        XW ? (int)(threadIdx.x >> 6) * (int)gridDim.x + (int)blockIdx.x
+           : (int)(blockIdx.x * WAVES + (threadIdx.x >> 6)));
     const int waves = gridDim.x * WAVES;
     const int64_t K = (int64_t)KB * QK;
     // this wave's rows: wave, wave + waves, ... (counts differ by at most one);
@@ -652,7 +658,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
 // The norm variants exist for k <= 8192 (NB <= 4): the layer-normed inputs
 // feed QKV and gate/up, whose k is the hidden size; larger k with a norm runs
 // on the batched-decode path (gemv_supports_norm).
-template <int QT, int M, int NB, int R, bool PAIR = false>
+template <int QT, int M, int NB, int R, bool PAIR = false, bool XW = false>
 hipError_t launch_r(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st,
                     int waves, int add, const NormArgs& norm) {
     constexpr int THREADS = gemv_threads<QT, M, NB>();
@@ -666,7 +672,7 @@ hipError_t launch_r(const QWeight& w, const float* x, int64_t m, float* y, hipSt
         else
             return hipErrorInvalidValue;
     } else {
-        gemv_kernel<QT, M, NB, R, THREADS, PAIR><<<grid, THREADS, lds, st>>>(
+        gemv_kernel<QT, M, NB, R, THREADS, PAIR, false, XW><<<grid, THREADS, lds, st>>>(
             w.base, w.row_bytes, x, y, (int)w.n, (int)w.kb, (int)m, add, norm);
     }
     return hipGetLastError();
@@ -716,6 +722,13 @@ hipError_t launch_nb(const QWeight& w, const float* x, int64_t m, float* y, hipS
         return launch_r<QT, M, NB, RMAX>(w, x, m, y, st, (int)waves, add, norm);
     if (RMAX >= 2 && rows > 2)
         return launch_r<QT, M, NB, (RMAX >= 2 ? 2 : 1)>(w, x, m, y, st, (int)waves, add, norm);
+    if constexpr (M == 1) {
+        // at most two rows a wave with a partial second round (the Q8_0 k 2048 n 5632
+        // GEMV: 1536 of 4096 waves hold two rows): the two-row waves across all CUs
+        const int64_t all = (waves + WAVES - 1) / WAVES * WAVES;
+        if (!norm.gamma && rows == 2 && w.n % all != 0)
+            return launch_r<QT, M, NB, 1, false, true>(w, x, m, y, st, (int)waves, add, norm);
+    }
     return launch_r<QT, M, NB, 1>(w, x, m, y, st, (int)waves, add, norm);
 }
 

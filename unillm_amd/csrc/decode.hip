@@ -683,7 +683,8 @@ __global__ __launch_bounds__(256) void decode_x_kernel(const uint8_t* __restrict
     uint8_t* const ring = lds + ST::XAREA;
     uint8_t* const scl = ring + D * ST::P;
     uint8_t* const hdr = scl + ST::SCALES;
-    float* const facs = reinterpret_cast<float*>(hdr + ST::HDR);  // [16] the rows' factors
+    // [16] the rows' factors; [32] NaN when the epilogue's wait gave up (64 floats held)
+    float* const facs = reinterpret_cast<float*>(hdr + ST::HDR);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -940,15 +941,20 @@ __global__ __launch_bounds__(256) void decode_x_kernel(const uint8_t* __restrict
         each([&](float* dst, float v) { unsafeAtomicAdd(dst, v); });
     } else {
         // slice 0 zeroed the tile and raised the flag after its prologue: the wait is
-        // normally over at the first look
+        // normally over at the first look.  A wait that gives up (which needs slice 0
+        // not to run, and the host launches only grids that are resident at once) adds
+        // NaN, so that the result is visibly wrong rather than silently so.
         if (tid == 0) {
-            for (int it = 0; it < kSyncPoll; ++it) {
-                if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
-                __builtin_amdgcn_s_sleep(2);
+            unsigned seen = 0;
+            for (int it = 0; it < kSyncPoll && !seen; ++it) {
+                seen = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (!seen) __builtin_amdgcn_s_sleep(2);
             }
+            facs[32] = seen ? 0.0f : __builtin_nanf("");
         }
         __syncthreads();
-        each([&](float* dst, float v) { unsafeAtomicAdd(dst, v); });
+        const float give_up = facs[32];
+        each([&](float* dst, float v) { unsafeAtomicAdd(dst, v + give_up); });
         if (tid == 0 && __hip_atomic_fetch_add(flag + kSyncStride, 1u, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT) == (unsigned)S - 1) {
             // every slice of this row group is past the flag: reset for the next launch

@@ -168,3 +168,74 @@ def test_random_attention_sequence(seq):
         assert np.isfinite(out).all()
         assert oracle.normwise_error(out, ref) < 1e-4
     kv.close()
+
+
+def _capture_cases(count, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        qt = [Q4_0, Q8_0, Q4_K, Q6_K][int(rng.choice(4, p=[0.4, 0.3, 0.15, 0.15]))]
+        unit = 256 if qt in (Q4_K, Q6_K) else 32
+        r = rng.random()
+        m = int(rng.integers(1, 5) if r < 0.3 else rng.integers(5, 17) if r < 0.55
+                else rng.integers(17, 65) if r < 0.75 else rng.integers(65, 600))
+        k = int(rng.integers(1, 12000 // unit + 1)) * unit
+        n = int(rng.integers(1, 6000))
+        while n * k > 8e6:
+            n = max(1, n // 2)
+        op = str(rng.choice(["fwd", "add", "swiglu", "norm", "normswiglu"]))
+        if op.endswith("swiglu") and n % 2:
+            n += 1
+        out.append((i, qt, m, n, k, op, int(rng.integers(1 << 30))))
+    return out
+
+
+@pytest.mark.parametrize("case", _capture_cases(60, seed=20261204), ids=lambda c: f"g{c[0]}")
+def test_random_capture_replays_match_eager(case):
+    """reserve, then one call captured into a HIP graph on its own stream: three replays
+    with eager work between them, each equal to the eager call (to f32 rounding where
+    the batched decode's split k adds by atomics; bitwise elsewhere)."""
+    i, qt, m, n, k, op, seed = case
+    print(f"random capture {case}", flush=True)
+    crng = np.random.default_rng(seed + 3)
+    ql = QuantLinear.from_blocks(qt, n, k, _blocks(qt, n, k, seed))
+    x = torch.from_numpy(oracle.normal(m * k, seed=seed + 1).reshape(m, k)).cuda()
+    g = torch.from_numpy((1.0 + 0.1 * crng.standard_normal(k)).astype(np.float32)).cuda()
+    b = torch.from_numpy((0.1 * crng.standard_normal(k)).astype(np.float32)).cuda()
+    nout = n // 2 if op.endswith("swiglu") else n
+    y0 = torch.from_numpy(crng.standard_normal((m, nout)).astype(np.float32)).cuda()
+    s = torch.cuda.Stream()
+    ql.reserve(m, swiglu=op.endswith("swiglu"), stream=s)
+
+    def call(out):
+        if op == "fwd":
+            ql.forward(x, out=out, stream=s)
+        elif op == "add":
+            ql.forward_add(x, out, stream=s)
+        elif op == "norm":
+            ql.forward_norm(x, g, b, eps=1e-6, out=out, stream=s)
+        elif op == "swiglu":
+            ql.forward_swiglu(x, out=out, stream=s)
+        else:
+            ql.forward_swiglu(x, out=out, stream=s, norm=(g, b, 1e-6))
+
+    with torch.cuda.stream(s):
+        eager = y0.clone()
+        call(eager)
+    s.synchronize()
+    out = torch.empty(m, nout, device="cuda")
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr, stream=s, capture_error_mode="thread_local"):
+        call(out)
+    scale = max(eager.abs().max().item(), 1e-30)
+    for rep in range(3):
+        out.copy_(y0)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            gr.replay()
+        s.synchronize()
+        assert (out - eager).abs().max().item() <= 1e-6 * scale, rep
+        with torch.cuda.stream(s):  # eager work between replays
+            ql.forward(x, stream=s)
+        s.synchronize()
+    del gr

@@ -75,6 +75,42 @@ def test_noalloc_matches_qmatmul_twice(qtype, n, k, m1, m2, path, exact):
         assert oracle.normwise_error(a[rows], ref) < 1e-3, (call, m)
 
 
+
+def _random_cases(count, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        qtype = Q4_0 if rng.random() < 0.6 else Q8_0
+        r = rng.random()
+        m1 = int(rng.integers(1, 5) if r < 0.3 else rng.integers(5, 65) if r < 0.65
+                 else rng.integers(65, 700))
+        k = int(rng.integers(1, 12000 // 32 + 1)) * 32
+        n = int(rng.integers(1, 6000))
+        while n * k > 8e6:
+            n = max(1, n // 2)
+        out.append((i, qtype, n, k, m1, int(rng.integers(1, m1 + 1)), int(rng.integers(1 << 30))))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_cases(40, seed=20261205), ids=lambda c: f"r{c[0]}")
+def test_noalloc_matches_qmatmul_random_shapes(case):
+    # seeded random shapes over every path, two calls in a row (the second no larger),
+    # each against unillm_hip_qmatmul on the same input to f32 rounding
+    i, qtype, n, k, m1, m2, seed = case
+    print(f"noalloc random {case}", flush=True)
+    lib = _capi.lib()
+    w = oracle.normal(n * k, seed=seed, std=0.02).reshape(n, k)
+    ql = QuantLinear.from_blocks(qtype, n, k, oracle.quantize(qtype, w))
+    s = torch.cuda.Stream()
+    for call, m in enumerate((m1, m2)):
+        x = torch.from_numpy(oracle.normal(m * k, seed=seed + 1 + call).reshape(m, k)).cuda()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            a = _call(lib.unillm_hip_qmatmul_noalloc, ql, x, n, s)
+            b = _call(lib.unillm_hip_qmatmul, ql, x, n, s)
+        s.synchronize()
+        assert oracle.normwise_error(a.cpu().numpy(), b.cpu().numpy()) < 1e-5, (call, m)
+
 def test_noalloc_under_graph_capture_without_reserve():
     # the case it exists for: a fresh stream (no workspace) captured straight away
     lib = _capi.lib()

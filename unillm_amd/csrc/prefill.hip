@@ -37,7 +37,7 @@
 //     stage (vmcnt in issue order) and meets the other waves at a bare
 //     s_barrier.
 // Measured limits (m2048 k4096 n14336).  The loop alone -- these LDS reads, the MFMAs
-// and a barrier a step, on operands already in LDS (unillm_amd/probe/prefill_probe.hip)
+// and a barrier a step, on operands already in LDS (a standalone probe, not built here)
 // -- keeps the matrix cores 87-92 % busy.  Bringing each step's 42 KiB of operands
 // from L2 into LDS costs about a quarter of the cycles however it is done (direct
 // loads or through VGPRs, waited on or not): 68 %.  The dequant VALU does not overlap

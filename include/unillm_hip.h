@@ -17,7 +17,7 @@
  *     (candle reverses ne into shape [n, k]).  x is [m, k] f32 row-major and
  *     y = x . dequant(W)^T is [m, n] f32 row-major.
  *   - Preconditions checked on the host before any launch: k % 32 == 0
- *     (k % 256 == 0 for Q4_K, Q6_K; any k >= 1 for the dense types), n >= 1,
+ *     (k % 256 == 0 for Q4_K, Q5_K, Q6_K; any k >= 1 for the dense types), n >= 1,
  *     m >= 0, non-null pointers, known qtype.
  *   - Streams: a `void* stream` is a hipStream_t (NULL = the null stream).
  *     Compute calls are asynchronous on that stream and never synchronise.
@@ -35,12 +35,15 @@
 extern "C" {
 #endif
 
-/* GGML type ids as GGUF stores them (candle GgmlDType::Q4_0 / Q8_0 / Q4K / Q6K;
- * the reference maps Q4K at crates/runtime/src/weight_loader_core.rs:481; Q6K is
- * what GGUF Q4_K_M files use for output.weight and some attn_v / ffn_down). */
+/* GGML type ids as GGUF stores them (candle GgmlDType::Q4_0 / Q8_0 / Q4K / Q5K /
+ * Q6K; the reference maps Q4K at crates/runtime/src/weight_loader_core.rs:481 and
+ * hands every type to QMatMul::from_arc at :569-571; Q5K holds the projections of
+ * GGUF Q5_K_M files, Q6K what Q4_K_M / Q5_K_M files use for output.weight and some
+ * attn_v / ffn_down). */
 #define UNILLM_QTYPE_Q4_0 2
 #define UNILLM_QTYPE_Q8_0 8
 #define UNILLM_QTYPE_Q4_K 12
+#define UNILLM_QTYPE_Q5_K 13
 #define UNILLM_QTYPE_Q6_K 14
 /* Dense projection weights (GGML F32 / F16 / BF16).  candle's QMatMul::from_arc
  * dequantizes such a tensor to f32 and multiplies in f32 (its Tensor variant);
@@ -78,8 +81,8 @@ int unillm_hip_init(int device);
 /* Message of the last error on the calling thread ("" if none). */
 const char* unillm_hip_last_error(void);
 
-/* Upload one GGUF Q4_0 / Q8_0 / Q4_K / Q6_K tensor ([n, k]: n * k/32 blocks of
- * 18 / 34 B, or n * k/256 blocks of 144 / 210 B), or a dense F32 / F16 / BF16 one
+/* Upload one GGUF Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K tensor ([n, k]: n * k/32 blocks
+ * of 18 / 34 B, or n * k/256 blocks of 144 / 176 / 210 B), or a dense F32 / F16 / BF16 one
  * (n * k elements of 4 / 2 / 2 B), to the device, repacked there into the kernels'
  * layout (dense: f32 rows).  Replaces
  * `QMatMul::from_arc(Arc::new(qtensor))` at
@@ -164,7 +167,7 @@ int unillm_hip_qmatmul_add(const unillm_qweight* w, const float* x_dev, int64_t 
  * handle fused at load.  Replaces the two quantized_matmul calls and
  * ops_fn::fused_swiglu of LlamaMLP::forward (llama.rs:1275-1283;
  * tensor_core.rs:1385-1396: candle silu(v) = v / (1 + e^-v)).  On the GEMV path
- * (m = 1: k <= 8192 for Q4_0 / Q4_K, 4096 for Q8_0 / Q6_K; half that at m = 2,
+ * (m = 1: k <= 8192 for Q4_0 / Q4_K, 4096 for Q8_0 / Q5_K / Q6_K; half that at m = 2,
  * a quarter at m = 3, 4) the gate and up rows meet in one wave and the
  * activation is its epilogue; otherwise the
  * [m, 2 I] product goes to a per-stream workspace and one elementwise pass
@@ -260,7 +263,7 @@ int unillm_hip_dequant(const unillm_qweight* w, float* out_dev, void* stream);
 /* GGML reference quantizer on the device: w[n, k] f32 -> GGUF block bytes
  * (n * k/32 blocks of 18 / 34 B), bit-exact with GGML quantize_row_q4_0/q8_0
  * (candle QTensor::quantize; used by the reference only to make GGUF files).
- * Q4_K / Q6_K are refused with UNILLM_ERR_UNSUPPORTED (their GGML quantizers
+ * Q4_K / Q5_K / Q6_K are refused with UNILLM_ERR_UNSUPPORTED (their GGML quantizers
  * search scales iteratively and are not on this path). */
 int unillm_hip_quantize(int qtype, const float* w_dev, int64_t n, int64_t k, void* blocks_dev,
                         void* stream);

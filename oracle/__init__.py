@@ -19,10 +19,11 @@ import numpy as np
 Q4_0 = 2
 Q8_0 = 8
 Q4_K = 12
+Q5_K = 13
 Q6_K = 14
 QK = 32
-BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}
-BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liboracle.so")
@@ -174,7 +175,7 @@ def elementwise_error(y: np.ndarray, ref: np.ndarray, floor: float = 1e-3) -> fl
 
 
 # ---- K-quant test data ---------------------------------------------------------------------
-# GGML has no simple reference quantizer for Q4_K / Q6_K (quantize_row_q4_K_ref
+# GGML has no simple reference quantizer for Q4_K / Q5_K / Q6_K (quantize_row_q4_K_ref
 # searches scales iteratively); the parity tests need valid blocks, not GGML's
 # choice of them, so blocks are drawn directly: random codes and 6- / 8-bit
 # scales under f16 super-block scales sized like N(0, 0.02) weights.
@@ -203,6 +204,19 @@ def random_q4_k(n: int, k: int, seed: int) -> np.ndarray:
     nb = n * (k // 256)
     blk = rng.integers(0, 256, size=(nb, 144), dtype=np.uint8)  # scales[12] and qs: any bytes
     d = (np.abs(rng.normal(0, 1, nb)) * 4e-5 + 1e-5).astype(np.float16)
+    dmin = (np.abs(rng.normal(0, 1, nb)) * 2e-4 + 1e-5).astype(np.float16)
+    blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    blk[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)
+    return blk.reshape(n, -1)
+
+
+def random_q5_k(n: int, k: int, seed: int) -> np.ndarray:
+    """[n, k/256 * 176] valid Q5_K blocks, weights of roughly N(0, 0.02) size."""
+    assert k % 256 == 0
+    rng = np.random.default_rng(seed)
+    nb = n * (k // 256)
+    blk = rng.integers(0, 256, size=(nb, 176), dtype=np.uint8)  # scales, qh, qs: any bytes
+    d = (np.abs(rng.normal(0, 1, nb)) * 2e-5 + 5e-6).astype(np.float16)
     dmin = (np.abs(rng.normal(0, 1, nb)) * 2e-4 + 1e-5).astype(np.float16)
     blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
     blk[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)

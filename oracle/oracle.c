@@ -19,7 +19,7 @@
 
 int oracle_block_elems(int qtype) {
     if (qtype == ORACLE_Q4_0 || qtype == ORACLE_Q8_0) return 32;
-    if (qtype == ORACLE_Q4_K || qtype == ORACLE_Q6_K) return 256;
+    if (qtype == ORACLE_Q4_K || qtype == ORACLE_Q5_K || qtype == ORACLE_Q6_K) return 256;
     return 0;
 }
 
@@ -30,10 +30,12 @@ size_t oracle_block_bytes(int qtype) {
      * Q4_K: 2 + 2 + 12 + 128 = 144 B; Q6_K: 128 + 64 + 16 + 2 = 210 B (GGML
      * block_q4_K / block_q6_K; the in-repo Q4_KBlock, block.rs:100-110, has
      * the same size but a simplified scale packing, block.rs:124-139, and is
-     * not what candle's Q4K reads). */
+     * not what candle's Q4K reads).  Q5_K: 2 + 2 + 12 + 32 + 128 = 176 B (GGML
+     * block_q5_K). */
     if (qtype == ORACLE_Q4_0) return 18;
     if (qtype == ORACLE_Q8_0) return 34;
     if (qtype == ORACLE_Q4_K) return 144;
+    if (qtype == ORACLE_Q5_K) return 176;
     if (qtype == ORACLE_Q6_K) return 210;
     return 0;
 }
@@ -178,6 +180,33 @@ static void dequant_q4_k(const uint8_t* blk, float* y) {
     }
 }
 
+/* GGML dequantize_row_q5_K, one 256-weight block (BlockQ5K::to_float in candle;
+ * GGUF Q5_K_M files hold their projections in it): Q4_K's scales, mins and
+ * nibbles plus a fifth bit per weight in qh[32].  Weight l of sub-block 2 g
+ * (g = 0..3, l = 0..31) takes the low nibble of qs[32 g + l] and bit 2 g of
+ * qh[l]; weight l of sub-block 2 g + 1 the high nibble and bit 2 g + 1.  As for
+ * Q4_K, (d sc) q is exact in f32 (q < 32) and the subtraction rounds once. */
+static void dequant_q5_k(const uint8_t* blk, float* y) {
+    const float d = oracle_f16_to_f32(rd16(blk));
+    const float dmin = oracle_f16_to_f32(rd16(blk + 2));
+    const uint8_t* scales = blk + 4;
+    const uint8_t* qh = blk + 16;
+    const uint8_t* q = blk + 48;
+    for (int g = 0; g < 4; ++g) {
+        int sc, m;
+        q4_k_scale_min(2 * g, scales, &sc, &m);
+        const float d1 = d * (float)sc, m1 = dmin * (float)m;
+        q4_k_scale_min(2 * g + 1, scales, &sc, &m);
+        const float d2 = d * (float)sc, m2 = dmin * (float)m;
+        for (int l = 0; l < 32; ++l) {
+            const int q1 = (q[32 * g + l] & 0x0F) | (((qh[l] >> (2 * g)) & 1) << 4);
+            const int q2 = (q[32 * g + l] >> 4) | (((qh[l] >> (2 * g + 1)) & 1) << 4);
+            y[64 * g + l] = d1 * (float)q1 - m1;
+            y[64 * g + 32 + l] = d2 * (float)q2 - m2;
+        }
+    }
+}
+
 /* GGML dequantize_row_q6_K, one 256-weight block: two halves of 128 weights,
  * each from 64 bytes of ql, 32 of qh and 8 scales; weight l + 32 t of a half
  * (t = 0..3, l = 0..31) has q = (ql nibble) | (2 bits of qh[l]) << 4, scale
@@ -210,6 +239,10 @@ static void dequant_q6_k(const uint8_t* blk, float* y) {
 static void dequant_block(int qtype, const uint8_t* blk, float* y) {
     if (qtype == ORACLE_Q4_K) {
         dequant_q4_k(blk, y);
+        return;
+    }
+    if (qtype == ORACLE_Q5_K) {
+        dequant_q5_k(blk, y);
         return;
     }
     if (qtype == ORACLE_Q6_K) {

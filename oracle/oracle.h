@@ -22,6 +22,11 @@
  *        scales[] (get_scale_min_k4); group g = 0..3 of 64 weights uses
  *        qs[32 g .. 32 g + 31]: low nibbles -> sub-block 2 g, high -> 2 g + 1;
  *        w = (d * sc_j) * q - (dmin * m_j)       (dequantize_row_q4_K)
+ *   Q5_K block (176 B / 256 weights, GGML block_q5_K, candle GgmlDType::Q5K):
+ *        { f16 d; f16 dmin; u8 scales[12]; u8 qh[32]; u8 qs[128]; }
+ *        Q4_K's scales, mins and nibbles; weight l of sub-block j takes bit j
+ *        of qh[l] as its fifth bit: q = nibble | bit << 4, 0..31;
+ *        w = (d * sc_j) * q - (dmin * m_j)       (dequantize_row_q5_K)
  *   Q6_K block (210 B / 256 weights, GGML block_q6_K):
  *        { u8 ql[128]; u8 qh[64]; i8 scales[16]; f16 d; }
  *        w = (d * scales[s]) * (q - 32), q 6-bit from ql (4) and qh (2)
@@ -38,7 +43,7 @@
  *   dequant            : closed form, exhaustive over all scales x all codes;
  *                        the reference's layout-neutral known answers
  *                        (simd/quant/block.rs:398-423, q4_0.rs:131-178).
- *                        Q4_K / Q6_K: one-hot blocks that expose every index
+ *                        Q4_K / Q5_K / Q6_K: one-hot blocks that expose every index
  *                        (which byte, nibble, scale and min each weight uses),
  *                        the 6-bit scale packing as the inverse of GGML's
  *                        packer over all 64 x 64 values per sub-block, and an
@@ -74,11 +79,12 @@ extern "C" {
 #define ORACLE_Q4_0 2
 #define ORACLE_Q8_0 8
 #define ORACLE_Q4_K 12
+#define ORACLE_Q5_K 13
 #define ORACLE_Q6_K 14
 
-/* weights per block: 32 (Q4_0, Q8_0) or 256 (Q4_K, Q6_K); 0 for unknown types */
+/* weights per block: 32 (Q4_0, Q8_0) or 256 (Q4_K, Q5_K, Q6_K); 0 for unknown types */
 int oracle_block_elems(int qtype);
-/* bytes per block: 18 (Q4_0), 34 (Q8_0), 144 (Q4_K), 210 (Q6_K); 0 for unknown */
+/* bytes per block: 18 (Q4_0), 34 (Q8_0), 144 (Q4_K), 176 (Q5_K), 210 (Q6_K); 0 for unknown */
 size_t oracle_block_bytes(int qtype);
 
 /* IEEE binary16 <-> binary32 (round to nearest even, subnormals, inf, nan) */

@@ -3,8 +3,9 @@
 //
 //   test_host cpu <file.gguf> <file.expect>      parsing, name map, plan, errors
 //   test_host gpu <file.gguf> <file.expect>      load to the device + forward parity
-//   test_host cpu-kq / gpu-kq <q4_k_m.gguf> <.expect>   the Q4_K / Q6_K file: plan,
-//                                                 parity, QKV and gate+up fusion
+//   test_host cpu-kq / gpu-kq <q4_k_m.gguf> <.expect>   the Q4_K / Q6_K file (or the
+//                                                 Q5_K / Q6_K one): plan, parity, QKV
+//                                                 and gate+up fusion
 //   test_host gpu-step <file.gguf> <file.step>   LlamaModel::forward_with_cache logits,
 //                                                 eager and as a captured decode step
 //
@@ -466,20 +467,30 @@ static void test_gpu_dense(const std::string& gguf, const std::vector<Expect>& e
     }
 }
 
+// The file's main K-quant type (Q4_K in the Q4_K_M mix, Q5_K in the Q5_K_M one): that
+// of blk.1.attn_q.weight.
+static uint32_t main_ktype(const GgufFile& f) {
+    for (const auto& t : f.tensors())
+        if (t.name == "blk.1.attn_q.weight") return t.type;
+    return 0;
+}
+
 static void test_cpu_kq(const std::string& gguf, const std::vector<Expect>& ex) {
     const GgufFile f = GgufFile::open(gguf);
     const GgufModelConfig c = GgufWeightLoader::config_from(f);
     CHECK(c.hidden_size == 256 && c.intermediate_size == 512 && c.num_hidden_layers == 2);
+    const uint32_t kt = main_ktype(f);
+    CHECK(kt == GGML_Q4_K || kt == GGML_Q5_K);
     GgufWeightLoader loader;
     const auto plan = loader.plan(f);
-    size_t n4 = 0, n6 = 0;
+    size_t nk = 0, n6 = 0;
     for (size_t i = 0; i < plan.size() && i < ex.size(); ++i) {
         CHECK(plan[i].type == ex[i].type);
         CHECK(plan[i].quantized == (ex[i].quantized != 0));
-        n4 += plan[i].type == GGML_Q4_K;
+        nk += plan[i].type == kt;
         n6 += plan[i].type == GGML_Q6_K;
     }
-    CHECK(n4 == 12 + 1 && n6 == 3);  // token_embd Q4_K; attn_v.0, ffn_down.0, output Q6_K
+    CHECK(nk == 12 + 1 && n6 == 3);  // token_embd kt; attn_v.0, ffn_down.0, output Q6_K
     const GgufTensorInfo* q = nullptr;
     for (const auto& t : f.tensors())
         if (t.name == "output.weight") q = &t;
@@ -491,7 +502,8 @@ static void test_gpu_kq(const std::string& gguf, const std::vector<Expect>& ex) 
     const ModelWeights w = loader.load_weights(gguf);
     CHECK(w.quantized_tensors.size() == 15 && w.fused_parts.empty());
     CHECK(w.get_quantized("lm_head.weight")->qtype() == GGML_Q6_K);
-    CHECK(w.get_quantized("model.layers.1.mlp.down_proj.weight")->qtype() == GGML_Q4_K);
+    CHECK(w.get_quantized("model.layers.1.mlp.down_proj.weight")->qtype() ==
+          (int)main_ktype(GgufFile::open(gguf)));
     CHECK(w.tensors.at("model.embed_tokens.weight").shape() == std::vector<int64_t>({256, 256}));
     std::map<std::string, std::vector<float>> ys;
     for (const Expect& e : ex) {
@@ -505,7 +517,7 @@ static void test_gpu_kq(const std::string& gguf, const std::vector<Expect>& ex) 
         if (err >= 1e-3) std::fprintf(stderr, "  %s: normwise %.3g\n", e.hf_name.c_str(), err);
         CHECK(err < 1e-3);
     }
-    // fusion: layer 1 (all Q4_K) fuses q/k/v and gate/up; layer 0 keeps q/k/v apart
+    // fusion: layer 1 (all one type) fuses q/k/v and gate/up; layer 0 keeps q/k/v apart
     // (its attn_v is Q6_K) but fuses gate/up
     LoadOptions opt;
     opt.fuse_qkv = opt.fuse_gate_up = true;

@@ -1,4 +1,5 @@
-"""Write tests/golden/tiny_llama_q4_0.gguf, tiny_llama_q4_k_m.gguf and their expected outputs.
+"""Write tests/golden/tiny_llama_q4_0.gguf, tiny_llama_q4_k_m.gguf, tiny_llama_q5_k_m.gguf and
+their expected outputs.
 
 A minimal GGUF v3 file in the layout llama.cpp writes for a Llama model:
 2 blocks of attn_q/k/v/output + ffn_gate/up/down (Q4_0), token_embd (Q8_0),
@@ -35,6 +36,9 @@ tiny_llama_q4_k_m.gguf has the tensor types llama.cpp's Q4_K_M mix uses:
 Q4_K projections and token_embd, Q6_K for output.weight and for layer 0's
 attn_v / ffn_down.  Its blocks are random valid Q4_K / Q6_K blocks (the
 oracle's generators) and its expectations the oracle's f64 matmul.
+tiny_llama_q5_k_m.gguf is the same mix with Q5_K in place of Q4_K (llama.cpp's
+Q5_K_M: Q5_K projections and token_embd, Q6_K for output.weight and layer 0's
+attn_v / ffn_down).
 """
 from __future__ import annotations
 
@@ -48,7 +52,7 @@ from make_golden import dequant, quantize_q4_0, quantize_q8_0
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ALIGN = 32
-T_F32, T_F16, T_Q4_0, T_Q8_0, T_Q4_K, T_Q6_K, T_BF16 = 0, 1, 2, 8, 12, 14, 30
+T_F32, T_F16, T_Q4_0, T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K, T_BF16 = 0, 1, 2, 8, 12, 13, 14, 30
 DENSE = (T_F32, T_F16, T_BF16)
 V_UINT32, V_FLOAT32, V_STRING, V_ARRAY = 4, 6, 8, 9
 
@@ -112,6 +116,7 @@ def main() -> None:
           heads=(HEADS, KV_HEADS), rope_base=ROPE_BASE)
     write_steps(tensors, "tiny_llama_q4_0")
     main_kq()
+    main_kq(T_Q5_K)
     main_dense()
 
 
@@ -205,19 +210,21 @@ def write_steps(tensors, stem) -> None:
         f.write(blob)
 
 
-def main_kq() -> None:
-    """The Q4_K_M-style file (k a multiple of 256)."""
+def main_kq(kt: int = T_Q4_K) -> None:
+    """The Q4_K_M-style file (kt = T_Q4_K) or the Q5_K_M-style one (kt = T_Q5_K); k a
+    multiple of 256."""
     sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
     import oracle  # test infrastructure: random K-quant blocks and their exact dequant
 
     hidden, inter, layers = 256, 512, 2
-    rng = np.random.default_rng(11)
+    rng = np.random.default_rng(11 if kt == T_Q4_K else 13)
     tensors = []
-    seed = [100]
+    seed = [100 if kt == T_Q4_K else 200]
 
     def add_k(name, qtype, n, k):
         seed[0] += 1
-        gen = oracle.random_q4_k if qtype == T_Q4_K else oracle.random_q6_k
+        gen = {T_Q4_K: oracle.random_q4_k, T_Q5_K: oracle.random_q5_k,
+               T_Q6_K: oracle.random_q6_k}[qtype]
         blocks = gen(n, k, seed[0])
         tensors.append((name, qtype, (n, k), blocks.tobytes(), oracle.dequant(qtype, blocks, n, k)))
 
@@ -225,21 +232,22 @@ def main_kq() -> None:
         v = (1.0 + rng.normal(0, 0.1, size=n)).astype(np.float32)
         tensors.append((name, T_F32, (n,), v.tobytes(), v))
 
-    add_k("token_embd.weight", T_Q4_K, 256, hidden)
+    add_k("token_embd.weight", kt, 256, hidden)
     for i in range(layers):
         p = f"blk.{i}."
         add_f32(p + "attn_norm.weight", hidden)
-        add_k(p + "attn_q.weight", T_Q4_K, hidden, hidden)
-        add_k(p + "attn_k.weight", T_Q4_K, hidden // 2, hidden)
-        add_k(p + "attn_v.weight", T_Q6_K if i == 0 else T_Q4_K, hidden // 2, hidden)
-        add_k(p + "attn_output.weight", T_Q4_K, hidden, hidden)
+        add_k(p + "attn_q.weight", kt, hidden, hidden)
+        add_k(p + "attn_k.weight", kt, hidden // 2, hidden)
+        add_k(p + "attn_v.weight", T_Q6_K if i == 0 else kt, hidden // 2, hidden)
+        add_k(p + "attn_output.weight", kt, hidden, hidden)
         add_f32(p + "ffn_norm.weight", hidden)
-        add_k(p + "ffn_gate.weight", T_Q4_K, inter, hidden)
-        add_k(p + "ffn_up.weight", T_Q4_K, inter, hidden)
-        add_k(p + "ffn_down.weight", T_Q6_K if i == 0 else T_Q4_K, hidden, inter)
+        add_k(p + "ffn_gate.weight", kt, inter, hidden)
+        add_k(p + "ffn_up.weight", kt, inter, hidden)
+        add_k(p + "ffn_down.weight", T_Q6_K if i == 0 else kt, hidden, inter)
     add_f32("output_norm.weight", hidden)
     add_k("output.weight", T_Q6_K, 256, hidden)
-    write(tensors, "tiny_llama_q4_k_m", hidden, inter, layers, rng, npz=False)
+    stem = "tiny_llama_q4_k_m" if kt == T_Q4_K else "tiny_llama_q5_k_m"
+    write(tensors, stem, hidden, inter, layers, rng, npz=False)
 
 
 def write(tensors, stem, hidden, inter, layers, rng, npz, heads=(4, 2), rope_base=None) -> None:

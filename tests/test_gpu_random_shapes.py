@@ -1,7 +1,7 @@
 """Randomized parity: seeded random shapes, paths, epilogues and KV-cache step sequences.
 
 The other GPU tests pin chosen shapes (the BASELINE configs, tile and split
-boundaries, edge sizes).  These draw (qtype, m, n, k, path, epilogue, x offset,
+boundaries, edge sizes).  These draw (qtype of the five, m, n, k, path, epilogue, x offset,
 x magnitude) and attention (heads, kv heads, head dim, RoPE theta, capacity, step
 sizes, truncations) from a fixed seed, so every case is reproducible from its id,
 and check each call against the f64 oracle at the same bars as the fixed tests:
@@ -17,7 +17,7 @@ import pytest
 import torch
 
 import oracle
-from oracle import Q4_0, Q4_K, Q6_K, Q8_0
+from oracle import Q4_0, Q4_K, Q5_K, Q6_K, Q8_0
 from unillm_amd import HipError, KvCache, QuantLinear
 from unillm_amd import _capi
 
@@ -30,8 +30,8 @@ def _matmul_cases(count, seed):
     rng = np.random.default_rng(seed)
     out = []
     for i in range(count):
-        qt = [Q4_0, Q8_0, Q4_K, Q6_K][int(rng.choice(4, p=[0.4, 0.3, 0.15, 0.15]))]
-        unit = 256 if qt in (Q4_K, Q6_K) else 32
+        qt = [Q4_0, Q8_0, Q4_K, Q5_K, Q6_K][int(rng.choice(5, p=[0.35, 0.25, 0.15, 0.15, 0.1]))]
+        unit = 256 if qt in (Q4_K, Q5_K, Q6_K) else 32
         r = rng.random()
         m = int(rng.integers(1, 5) if r < 0.3 else rng.integers(5, 17) if r < 0.55
                 else rng.integers(17, 65) if r < 0.75 else rng.integers(65, 400))
@@ -51,6 +51,8 @@ def _matmul_cases(count, seed):
 def _blocks(qt, n, k, seed):
     if qt == Q4_K:
         return oracle.random_q4_k(n, k, seed)
+    if qt == Q5_K:
+        return oracle.random_q5_k(n, k, seed)
     if qt == Q6_K:
         return oracle.random_q6_k(n, k, seed)
     return oracle.quantize(qt, oracle.normal(n * k, seed=seed, std=0.02).reshape(n, k))
@@ -174,8 +176,8 @@ def _capture_cases(count, seed):
     rng = np.random.default_rng(seed)
     out = []
     for i in range(count):
-        qt = [Q4_0, Q8_0, Q4_K, Q6_K][int(rng.choice(4, p=[0.4, 0.3, 0.15, 0.15]))]
-        unit = 256 if qt in (Q4_K, Q6_K) else 32
+        qt = [Q4_0, Q8_0, Q4_K, Q5_K, Q6_K][int(rng.choice(5, p=[0.35, 0.25, 0.15, 0.15, 0.1]))]
+        unit = 256 if qt in (Q4_K, Q5_K, Q6_K) else 32
         r = rng.random()
         m = int(rng.integers(1, 5) if r < 0.3 else rng.integers(5, 17) if r < 0.55
                 else rng.integers(17, 65) if r < 0.75 else rng.integers(65, 600))

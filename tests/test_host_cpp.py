@@ -5,7 +5,9 @@ parity against the committed expectations, load-time QKV / gate+up fusion, and
 the KV-cache mirror (LayerKVCache / KVCache with closed-form attention checks and
 the reference's overflow message), and LlamaModel::forward_with_cache over the
 tiny Q4_0 model against the f64 logits of tests/golden/tiny_llama_q4_0.step (GPU);
-the same for tiny_llama_f16 (dense F16 / F32 / BF16 projections)."""
+the same for tiny_llama_f16 (dense F16 / F32 / BF16 projections).  The K-quant files
+(tiny_llama_q4_k_m: Q4_K + Q6_K; tiny_llama_q5_k_m: Q5_K + Q6_K) are checked for their
+plan, per-tensor parity and fusion."""
 import os
 import subprocess
 
@@ -41,6 +43,15 @@ def test_host_k_quants_cpu():
 @pytest.mark.gpu
 def test_host_k_quants_gpu():
     _run("gpu-kq", "tiny_llama_q4_k_m")
+
+
+def test_host_q5_k_m_cpu():
+    _run("cpu-kq", "tiny_llama_q5_k_m")
+
+
+@pytest.mark.gpu
+def test_host_q5_k_m_gpu():
+    _run("gpu-kq", "tiny_llama_q5_k_m")
 
 
 @pytest.mark.gpu

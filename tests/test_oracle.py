@@ -237,9 +237,9 @@ def test_fill_normal_is_deterministic_and_normal():
     assert not np.array_equal(a[:1000], oracle.normal(1000, seed=6))
 
 
-# ---- Q4_K / Q6_K (GGML block_q4_K / block_q6_K) ---------------------------------------------
+# ---- Q4_K / Q5_K / Q6_K (GGML block_q4_K / block_q5_K / block_q6_K) ---------------------------------------------
 
-from oracle import Q4_K, Q6_K  # noqa: E402
+from oracle import Q4_K, Q5_K, Q6_K  # noqa: E402
 
 
 def _q4k_block(d, dmin, sc, m, qs) -> np.ndarray:
@@ -322,6 +322,82 @@ def test_q4_k_random_blocks_match_numpy_decoder():
     assert np.array_equal(got.reshape(-1, 256), _numpy_q4_k(blocks))
 
 
+def _q5k_block(d, dmin, sc, m, qh, qs) -> np.ndarray:
+    b = np.zeros(176, np.uint8)
+    b[0:2] = np.array([d], np.float16).view(np.uint8)
+    b[2:4] = np.array([dmin], np.float16).view(np.uint8)
+    b[4:16] = oracle.pack_q4_k_scales(sc, m)
+    b[16:48] = np.asarray(qh, np.uint8)
+    b[48:] = np.asarray(qs, np.uint8)
+    return b
+
+
+def test_q5_k_code_positions_one_hot():
+    # d = 1, scales 1, mins 0: weight = code.  Nibbles as Q4_K (byte b of qs: low
+    # -> weight 64 (b // 32) + b % 32, high -> + 32); bit j of qh[l] adds 16 to
+    # weight 32 j + l.
+    cases, want = [], []
+    for b in range(128):
+        for hi in range(2):
+            qs = np.zeros(128, np.uint8)
+            qs[b] = 0x50 if hi else 0x05
+            cases.append(_q5k_block(1.0, 0.0, [1] * 8, [0] * 8, np.zeros(32, np.uint8), qs))
+            e = np.zeros(256, np.float32)
+            e[64 * (b // 32) + b % 32 + 32 * hi] = 5.0
+            want.append(e)
+    for l in range(32):
+        for j in range(8):
+            qh = np.zeros(32, np.uint8)
+            qh[l] = 1 << j
+            cases.append(_q5k_block(1.0, 0.0, [1] * 8, [0] * 8, qh, np.zeros(128, np.uint8)))
+            e = np.zeros(256, np.float32)
+            e[32 * j + l] = 16.0
+            want.append(e)
+    got = oracle.dequant(Q5_K, np.stack(cases), len(cases), 256)
+    assert np.array_equal(got, np.stack(want))
+
+
+def test_q5_k_scale_min_and_full_code_range():
+    # all codes 31 (nibble 15, every qh bit set), scale of sub-block j = j + 1:
+    # weights of sub-block j = 31 (j + 1); then all codes 0 with dmin 1 and min
+    # 2 j + 1: -(2 j + 1).  The scale packing is Q4_K's (pinned above).
+    got = oracle.dequant(Q5_K, _q5k_block(1.0, 0.0, range(1, 9), [0] * 8, [0xFF] * 32,
+                                          [0xFF] * 128), 1, 256)
+    assert np.array_equal(got[0], 31.0 * np.repeat(np.arange(1, 9, dtype=np.float32), 32))
+    got = oracle.dequant(Q5_K, _q5k_block(1.0, 1.0, [1] * 8, range(1, 17, 2), [0] * 32,
+                                          [0] * 128), 1, 256)
+    assert np.array_equal(got[0], -np.repeat(np.arange(1, 17, 2, dtype=np.float32), 32))
+
+
+def _numpy_q5_k(blocks: np.ndarray) -> np.ndarray:
+    """Independent decoding: Q4_K's fields by bit position, the fifth bits by
+    unpacking qh to [32 weights][8 sub-blocks]."""
+    b = blocks.reshape(-1, 176)
+    as_q4k = np.concatenate([b[:, 0:16], b[:, 48:176]], axis=1)   # d, dmin, scales, qs
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    dmin = b[:, 2:4].copy().view(np.float16).astype(np.float32)[:, 0]
+    bits = np.unpackbits(b[:, 4:16], axis=1, bitorder="little")
+    def field(byte, lo, width):
+        return sum(bits[:, 8 * byte + lo + t].astype(np.int64) << t for t in range(width))
+    sc = np.stack([field(j, 0, 6) if j < 4 else field(j + 4, 0, 4) | (field(j - 4, 6, 2) << 4)
+                   for j in range(8)], 1)
+    m = np.stack([field(j + 4, 0, 6) if j < 4 else field(j + 4, 4, 4) | (field(j, 6, 2) << 4)
+                  for j in range(8)], 1)
+    q = as_q4k[:, 16:].reshape(-1, 4, 32)
+    lo = np.concatenate([q & 15, q >> 4], axis=2).reshape(-1, 8, 32).astype(np.int32)
+    hb = np.unpackbits(b[:, 16:48].reshape(-1, 32, 1), axis=2, bitorder="little")  # [nb][l][j]
+    codes = (lo + 16 * hb.transpose(0, 2, 1).astype(np.int32)).astype(np.float32)
+    s1 = (d[:, None] * sc.astype(np.float32))[:, :, None]
+    m1 = (dmin[:, None] * m.astype(np.float32))[:, :, None]
+    return (s1 * codes - m1).astype(np.float32).reshape(-1, 256)
+
+
+def test_q5_k_random_blocks_match_numpy_decoder():
+    blocks = oracle.random_q5_k(64, 1024, seed=11)
+    got = oracle.dequant(Q5_K, blocks, 64, 1024)
+    assert np.array_equal(got.reshape(-1, 256), _numpy_q5_k(blocks))
+
+
 def _q6k_block(d, sc, ql, qh) -> np.ndarray:
     b = np.zeros(210, np.uint8)
     b[0:128] = np.asarray(ql, np.uint8)
@@ -390,10 +466,10 @@ def test_q6_k_random_blocks_match_numpy_decoder():
     assert np.array_equal(got.reshape(-1, 256), _numpy_q6_k(blocks))
 
 
-@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+@pytest.mark.parametrize("qtype", [Q4_K, Q5_K, Q6_K])
 def test_qmatmul_f64_k_quants_match_numpy_float64(qtype):
     n, k, m = 29, 512, 3
-    gen = oracle.random_q4_k if qtype == Q4_K else oracle.random_q6_k
+    gen = {Q4_K: oracle.random_q4_k, Q5_K: oracle.random_q5_k, Q6_K: oracle.random_q6_k}[qtype]
     blocks = gen(n, k, seed=12)
     x = oracle.normal(m * k, seed=13).reshape(m, k)
     want = x.astype(np.float64) @ oracle.dequant(qtype, blocks, n, k).astype(np.float64).T

@@ -102,14 +102,14 @@ int ensure_init() {
 
 bool valid_qtype(int q) {
     return q == UNILLM_QTYPE_Q4_0 || q == UNILLM_QTYPE_Q8_0 || q == UNILLM_QTYPE_Q4_K ||
-           q == UNILLM_QTYPE_Q6_K || is_dense(q);
+           q == UNILLM_QTYPE_Q5_K || q == UNILLM_QTYPE_Q6_K || is_dense(q);
 }
 
 int check_shape(int qtype, int64_t n, int64_t k) {
     if (!valid_qtype(qtype))
         return fail(UNILLM_ERR_UNSUPPORTED,
                     "unsupported qtype " + std::to_string(qtype) +
-                        " (want 2 = Q4_0, 8 = Q8_0, 12 = Q4_K, 14 = Q6_K, or dense 0 = F32, "
+                        " (want 2 = Q4_0, 8 = Q8_0, 12 = Q4_K, 13 = Q5_K, 14 = Q6_K, or dense 0 = F32, "
                         "1 = F16, 30 = BF16)");
     if (is_dense(qtype)) {
         if (n < 1 || k < 1)
@@ -190,8 +190,10 @@ int finish_weight(QWeight* w, hipStream_t s) {
         return __half2float(__ushort_as_half((unsigned short)(b > 0x7BFFu ? 0x7BFFu : b)));
     };
     // |code| <= 8 (Q4_0) or 128 (Q8_0); Q4_K: |(d sc) q - dmin m| <= 63 (15 |d| + |dmin|);
-    // Q6_K: |(d sc)(q - 32)| <= 128 * 32 |d|; f16 holds magnitudes up to 65504
+    // Q5_K: 63 (31 |d| + |dmin|); Q6_K: |(d sc)(q - 32)| <= 128 * 32 |d|; f16 holds
+    // magnitudes up to 65504
     const float wmax = w->qtype == UNILLM_QTYPE_Q4_K   ? 63.0f * (15.0f * f16max(bits[0]) + f16max(bits[1]))
+                       : w->qtype == UNILLM_QTYPE_Q5_K ? 63.0f * (31.0f * f16max(bits[0]) + f16max(bits[1]))
                        : w->qtype == UNILLM_QTYPE_Q6_K ? 4096.0f * f16max(bits[0])
                        : f16max(bits[0]) * (w->qtype == UNILLM_QTYPE_Q4_0 ? 8.0f : 128.0f);
     // the largest power-of-two scaling that keeps every dequantized weight in

@@ -177,6 +177,29 @@ __device__ __forceinline__ void dequant_q8(u32x4 raw, f16x2 dh, f16x8& f0, f16x8
     f1 = __builtin_bit_cast(f16x8, b);
 }
 
+// Q5_K: as dequant_q8 for the int8 codes c = q - 16, with the block's f16 scale s =
+// d sc 2^-E and min o = dmin m 2^-E: (1024 + c + 128 - 1136) s - o = q s - o (s and o
+// rounded to f16 once each, as Q4_K's).
+__device__ __forceinline__ void dequant_q8m(u32x4 raw, f16x2 sh, f16x2 oh, f16x8& f0, f16x8& f1) {
+    const f16x2 bias = {(_Float16)1136.0f, (_Float16)1136.0f};
+    const uint32_t magic = 0x64646464u;
+    auto fma2 = [&](uint32_t v) {
+        return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, v) - bias) * sh - oh);
+    };
+    u32x4 a, b;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const uint32_t w = raw[d] ^ 0x80808080u;  // int8 -> c + 128
+        const uint32_t p02 = __builtin_amdgcn_perm(magic, w, 0x04020400u);
+        const uint32_t p13 = __builtin_amdgcn_perm(magic, w, 0x04030401u);
+        u32x4& o = d < 2 ? a : b;
+        o[2 * (d & 1)] = fma2(p02);
+        o[2 * (d & 1) + 1] = fma2(p13);
+    }
+    f0 = __builtin_bit_cast(f16x8, a);
+    f1 = __builtin_bit_cast(f16x8, b);
+}
+
 }  // namespace
 
 // The power-of-two scale of an f16 operand row (or slice) whose largest magnitude is
@@ -266,7 +289,8 @@ constexpr int kMaxSplit1 = 8, kMaxSplit2 = 4;
 
 template <int QT, int MT2>
 struct Stage {
-    static constexpr int QB = QT == UNILLM_QTYPE_Q8_0 || QT == UNILLM_QTYPE_Q6_K ? 32 : 16;
+    static constexpr int QB =
+        QT == UNILLM_QTYPE_Q8_0 || QT == UNILLM_QTYPE_Q5_K || QT == UNILLM_QTYPE_Q6_K ? 32 : 16;
     static constexpr int TOK = 32 * MT2;
     static constexpr int X = TOK * 256;
     static constexpr int P = DROWS * 4 * QB;
@@ -280,7 +304,8 @@ struct Stage {
     // K-quants: the slice's group headers, per wave [32 rows][8 x 4 B] (a slice of
     // at most 8 chunks touches at most 5 groups of 2 chunks)
     static constexpr int HDR =
-        QT == UNILLM_QTYPE_Q4_K || QT == UNILLM_QTYPE_Q6_K ? 4 * 32 * 32 : 0;
+        QT == UNILLM_QTYPE_Q4_K || QT == UNILLM_QTYPE_Q5_K || QT == UNILLM_QTYPE_Q6_K ? 4 * 32 * 32
+                                                                                     : 0;
     // depth: as deep as keeps two workgroups per CU, where the stage allows
     static constexpr int D = BYTES <= 16384 ? 4 : 3;
     static constexpr int LDS = D * BYTES + SCALES + HDR;
@@ -362,9 +387,10 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
                                                      int S, float wscale, float oscale, int add) {
     using ST = Stage<QT, MT2>;
     constexpr int QB = ST::QB, D = ST::D, LPC = ST::LPC;
-    // 4-bit codes: Q4_0 and Q4_K; byte codes: Q8_0 and Q6_K (repacked to int8)
+    // 4-bit codes: Q4_0 and Q4_K; byte codes: Q8_0, Q5_K and Q6_K (repacked to int8)
     constexpr bool Q4 = QT == UNILLM_QTYPE_Q4_0 || QT == UNILLM_QTYPE_Q4_K;
     constexpr bool K4 = QT == UNILLM_QTYPE_Q4_K, K6 = QT == UNILLM_QTYPE_Q6_K;
+    constexpr bool K5 = QT == UNILLM_QTYPE_Q5_K;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     uint8_t* const ring = lds;
     uint8_t* const scl = lds + D * ST::BYTES;
@@ -408,10 +434,10 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
                            8u * (uint32_t)(c0 + jj) + 4u * (uint32_t)(dw & 1);
         dma4(base + g, scl + wv * 2048 + i * 256);
     }
-    // ---- K-quants: the slice's group headers (Q4_K d | dmin << 16, Q6_K d), 8
+    // ---- K-quants: the slice's group headers (Q4_K, Q5_K d | dmin << 16, Q6_K d), 8
     // positions of 4 bytes a row; lane -> flat dword f = 64 i + lane = row f / 8,
     // position f % 8 = group c0 / 2 + position (clamped to the slice's last group) ----
-    if constexpr (K4 || K6) {
+    if constexpr (K4 || K5 || K6) {
         const int g0 = c0 >> 1, glast = (c1 - 1) >> 1;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -502,7 +528,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
         const uint32_t sa = srow + 8 * ((j + col) & 7);
         // Q4_K: the chunk's group header (the 4 blocks of a chunk share one group)
         float gd = 0.0f, gm = 0.0f;
-        if constexpr (K4 || K6) {
+        if constexpr (K4 || K5 || K6) {
             uint32_t hd;
             asm volatile("ds_read_b32 %0, %1\n s_waitcnt lgkmcnt(0)"
                          : "=&v"(hd)
@@ -549,13 +575,21 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
                     const uint16_t sb = (uint16_t)(scp[hp] >> (16 * bi));
                     const bool ok = kb0 + 2 * hp + bi < KB;
                     // Q6_K: sb = the two int8 scales; this lane's 16 weights take half h's
-                    const float dv = !ok ? 0.0f
-                                     : K6 ? gd * (float)(int8_t)(sb >> (8 * h))
-                                          : __half2float(__ushort_as_half(sb)) * wscale;
-                    const _Float16 d = (_Float16)dv;
-                    const f16x2 dh = {d, d};
                     f16x8 b0, b1;
-                    dequant_q8(pw[bi], dh, b0, b1);
+                    if constexpr (K5) {
+                        // sb = sc | m << 8: s = d sc 2^-E, o = dmin m 2^-E, each once to f16
+                        const _Float16 s1 = (_Float16)(ok ? gd * (float)(sb & 0xFFu) : 0.0f);
+                        const _Float16 o1 = (_Float16)(ok ? gm * (float)(sb >> 8) : 0.0f);
+                        const f16x2 sh = {s1, s1}, oh = {o1, o1};
+                        dequant_q8m(pw[bi], sh, oh, b0, b1);
+                    } else {
+                        const float dv = !ok ? 0.0f
+                                         : K6 ? gd * (float)(int8_t)(sb >> (8 * h))
+                                              : __half2float(__ushort_as_half(sb)) * wscale;
+                        const _Float16 d = (_Float16)dv;
+                        const f16x2 dh = {d, d};
+                        dequant_q8(pw[bi], dh, b0, b1);
+                    }
 #pragma unroll
                     for (int t = 0; t < MT2; ++t) {
                         acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
@@ -678,6 +712,7 @@ __global__ __launch_bounds__(256) void decode_x_kernel(const uint8_t* __restrict
     constexpr int QB = ST::QB, D = ST::D;
     constexpr bool Q4 = QT == UNILLM_QTYPE_Q4_0 || QT == UNILLM_QTYPE_Q4_K;
     constexpr bool K4 = QT == UNILLM_QTYPE_Q4_K, K6 = QT == UNILLM_QTYPE_Q6_K;
+    constexpr bool K5 = QT == UNILLM_QTYPE_Q5_K;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     uint8_t* const xarea = lds;
     uint8_t* const ring = lds + ST::XAREA;
@@ -737,7 +772,7 @@ __global__ __launch_bounds__(256) void decode_x_kernel(const uint8_t* __restrict
                            8u * (uint32_t)(c0 + jj) + 4u * (uint32_t)(dw & 1);
         dma4(base + g, scl + wv * 2048 + i * 256);
     }
-    if constexpr (K4 || K6) {
+    if constexpr (K4 || K5 || K6) {
         const int g0 = c0 >> 1, glast = (c1 - 1) >> 1;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -850,7 +885,7 @@ __global__ __launch_bounds__(256) void decode_x_kernel(const uint8_t* __restrict
         const int kb0 = 4 * (c0 + j);
         const uint32_t sa = srow + 8 * ((j + col) & 7);
         float gd = 0.0f, gm = 0.0f;
-        if constexpr (K4 || K6) {
+        if constexpr (K4 || K5 || K6) {
             uint32_t hd;
             asm volatile("ds_read_b32 %0, %1\n s_waitcnt lgkmcnt(0)"
                          : "=&v"(hd)
@@ -892,13 +927,21 @@ __global__ __launch_bounds__(256) void decode_x_kernel(const uint8_t* __restrict
                 for (int bi = 0; bi < 2; ++bi) {
                     const uint16_t sb = (uint16_t)(scp[hp] >> (16 * bi));
                     const bool ok = kb0 + 2 * hp + bi < KB;
-                    const float dv = !ok ? 0.0f
-                                     : K6 ? gd * (float)(int8_t)(sb >> (8 * h))
-                                          : __half2float(__ushort_as_half(sb)) * wscale;
-                    const _Float16 d = (_Float16)dv;
-                    const f16x2 dh = {d, d};
                     f16x8 b0, b1;
-                    dequant_q8(pw[bi], dh, b0, b1);
+                    if constexpr (K5) {
+                        // sb = sc | m << 8: s = d sc 2^-E, o = dmin m 2^-E, each once to f16
+                        const _Float16 s1 = (_Float16)(ok ? gd * (float)(sb & 0xFFu) : 0.0f);
+                        const _Float16 o1 = (_Float16)(ok ? gm * (float)(sb >> 8) : 0.0f);
+                        const f16x2 sh = {s1, s1}, oh = {o1, o1};
+                        dequant_q8m(pw[bi], sh, oh, b0, b1);
+                    } else {
+                        const float dv = !ok ? 0.0f
+                                         : K6 ? gd * (float)(int8_t)(sb >> (8 * h))
+                                              : __half2float(__ushort_as_half(sb)) * wscale;
+                        const _Float16 d = (_Float16)dv;
+                        const f16x2 dh = {d, d};
+                        dequant_q8(pw[bi], dh, b0, b1);
+                    }
                     acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(
                         __builtin_bit_cast(f16x8, xa[0][2 * bi]), b0, acc, 0, 0, 0);
                     acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(
@@ -1247,8 +1290,9 @@ namespace {
 // The k split of a batched-decode call of m rows on w (as the launch picks it).
 int decode_split(const QWeight& w, int64_t m) {
     const bool q4 = w.qtype == UNILLM_QTYPE_Q4_0, k4 = w.qtype == UNILLM_QTYPE_Q4_K,
-               k6 = w.qtype == UNILLM_QTYPE_Q6_K, wide = m > 32;
+               k5 = w.qtype == UNILLM_QTYPE_Q5_K, k6 = w.qtype == UNILLM_QTYPE_Q6_K, wide = m > 32;
     const int lds = k4   ? (wide ? Stage<UNILLM_QTYPE_Q4_K, 2>::LDS : Stage<UNILLM_QTYPE_Q4_K, 1>::LDS)
+                    : k5 ? (wide ? Stage<UNILLM_QTYPE_Q5_K, 2>::LDS : Stage<UNILLM_QTYPE_Q5_K, 1>::LDS)
                     : k6 ? (wide ? Stage<UNILLM_QTYPE_Q6_K, 2>::LDS : Stage<UNILLM_QTYPE_Q6_K, 1>::LDS)
                     : q4 ? (wide ? Stage<UNILLM_QTYPE_Q4_0, 2>::LDS : Stage<UNILLM_QTYPE_Q4_0, 1>::LDS)
                          : (wide ? Stage<UNILLM_QTYPE_Q8_0, 2>::LDS : Stage<UNILLM_QTYPE_Q8_0, 1>::LDS);
@@ -1260,6 +1304,7 @@ int xin_lds(const QWeight& w) {
         case UNILLM_QTYPE_Q4_0: return XinStage<UNILLM_QTYPE_Q4_0, kMaxSliceChunks>::LDS;
         case UNILLM_QTYPE_Q8_0: return XinStage<UNILLM_QTYPE_Q8_0, kMaxSliceChunks>::LDS;
         case UNILLM_QTYPE_Q4_K: return XinStage<UNILLM_QTYPE_Q4_K, kMaxSliceChunks>::LDS;
+        case UNILLM_QTYPE_Q5_K: return XinStage<UNILLM_QTYPE_Q5_K, kMaxSliceChunks>::LDS;
         default: return XinStage<UNILLM_QTYPE_Q6_K, kMaxSliceChunks>::LDS;
     }
 }
@@ -1305,7 +1350,7 @@ hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float
     if ((uint64_t)m * (uint64_t)w.k >= (1ull << 31) || !mfma_supports(w) || m > 64)
         return hipErrorInvalidValue;
     const bool q4 = w.qtype == UNILLM_QTYPE_Q4_0, k4 = w.qtype == UNILLM_QTYPE_Q4_K,
-               k6 = w.qtype == UNILLM_QTYPE_Q6_K, wide = m > 32;
+               k5 = w.qtype == UNILLM_QTYPE_Q5_K, k6 = w.qtype == UNILLM_QTYPE_Q6_K, wide = m > 32;
     hipError_t e = hipSuccess;
     if (decode_one_launch(w, m, norm)) {
         // x converted by the kernel itself; the stream's workspace holds the row groups'
@@ -1321,6 +1366,9 @@ hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float
         if (k4)
             return short_slices ? launch_x<UNILLM_QTYPE_Q4_K, 4>(w, x, m, y, S, s, add, sync)
                                 : launch_x<UNILLM_QTYPE_Q4_K, 8>(w, x, m, y, S, s, add, sync);
+        if (k5)
+            return short_slices ? launch_x<UNILLM_QTYPE_Q5_K, 4>(w, x, m, y, S, s, add, sync)
+                                : launch_x<UNILLM_QTYPE_Q5_K, 8>(w, x, m, y, S, s, add, sync);
         if (k6)
             return short_slices ? launch_x<UNILLM_QTYPE_Q6_K, 4>(w, x, m, y, S, s, add, sync)
                                 : launch_x<UNILLM_QTYPE_Q6_K, 8>(w, x, m, y, S, s, add, sync);
@@ -1349,6 +1397,9 @@ hipError_t launch_decode_mfma(const QWeight& w, const float* x, int64_t m, float
     if (k4)
         return wide ? launch_mt<UNILLM_QTYPE_Q4_K, 2>(w, xh, rf, m, y, S, s, add)
                     : launch_mt<UNILLM_QTYPE_Q4_K, 1>(w, xh, rf, m, y, S, s, add);
+    if (k5)
+        return wide ? launch_mt<UNILLM_QTYPE_Q5_K, 2>(w, xh, rf, m, y, S, s, add)
+                    : launch_mt<UNILLM_QTYPE_Q5_K, 1>(w, xh, rf, m, y, S, s, add);
     if (k6)
         return wide ? launch_mt<UNILLM_QTYPE_Q6_K, 2>(w, xh, rf, m, y, S, s, add)
                     : launch_mt<UNILLM_QTYPE_Q6_K, 1>(w, xh, rf, m, y, S, s, add);

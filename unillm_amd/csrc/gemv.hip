@@ -175,10 +175,19 @@ __device__ __forceinline__ void prep_q4(const float (&v)[8], int t, bool store,
     if (SUM && t == 0) dst[17] = __float_as_uint(xsum);
 }
 
-// Q8_0: v[j] = x[8u + j], u = quarter 0..3.
+// Q8_0: v[j] = x[8u + j], u = quarter 0..3.  SUM (Q5_K): dword 17 = the block's sum
+// of x, for the term (16 d sc - dmin m) sum x.
+template <bool SUM = false>
 __device__ __forceinline__ void prep_q8(const float (&v)[8], int u, bool store,
                                         uint32_t* __restrict__ dst) {
     const float amax = quad_absmax(v);
+    float xsum = 0.0f;
+    if constexpr (SUM) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xsum += v[j];
+        xsum += dpp_f32<0xB1>(xsum);
+        xsum += dpp_f32<0x4E>(xsum);
+    }
     // s = 2^e with max|x| / 127 < s
     int e = 0;
     (void)frexpf(amax * (1.0f / 127.0f), &e);
@@ -199,12 +208,17 @@ __device__ __forceinline__ void prep_q8(const float (&v)[8], int u, bool store,
     dst[8 + 2 * u] = pack_low_bytes(b1[0], b1[1], b1[2], b1[3]);
     dst[8 + 2 * u + 1] = pack_low_bytes(b1[4], b1[5], b1[6], b1[7]);
     if (u == 0) dst[16] = __float_as_uint(amax > 0.0f ? ldexpf(1.0f, e) * (1.0f / 254.0f) : 0.0f);
+    if (SUM && u == 0) dst[17] = __float_as_uint(xsum);
 }
 
 // The x elements a prep thread handles (q = 4 * block + quarter), as two float4 offsets.
-// Byte codes (Q8_0, and Q6_K repacked to int8) or nibbles (Q4_0, Q4_K).
+// Byte codes (Q8_0, and Q5_K / Q6_K repacked to int8) or nibbles (Q4_0, Q4_K).
 template <int QT>
-constexpr bool kByteCodes = QT == UNILLM_QTYPE_Q8_0 || QT == UNILLM_QTYPE_Q6_K;
+constexpr bool kByteCodes =
+    QT == UNILLM_QTYPE_Q8_0 || QT == UNILLM_QTYPE_Q5_K || QT == UNILLM_QTYPE_Q6_K;
+// K-quants with a per-block minimum (a sum-of-x term): Q4_K, Q5_K
+template <int QT>
+constexpr bool kHasMin = QT == UNILLM_QTYPE_Q4_K || QT == UNILLM_QTYPE_Q5_K;
 
 template <int QT>
 __device__ __forceinline__ void quarter_offsets(int quarter, int& o0, int& o1) {
@@ -222,7 +236,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 struct XBlock {
     u32x4 dg[4];  // 16 digit dwords, in record order
     float sx;     // 0 for a lane's clamped (duplicate) block
-    float xsum;   // Q4_K: sum of the block's x (0 for a clamped block)
+    float xsum;   // Q4_K, Q5_K: sum of the block's x (0 for a clamped block)
 };
 
 template <int QT>
@@ -232,7 +246,7 @@ __device__ __forceinline__ void load_xblock(const uint32_t* __restrict__ src, bo
 #pragma unroll
     for (int i = 0; i < 4; ++i) o.dg[i] = p[i];
     o.sx = valid ? __uint_as_float(src[16]) : 0.0f;
-    o.xsum = QT == UNILLM_QTYPE_Q4_K && valid ? __uint_as_float(src[17]) : 0.0f;
+    o.xsum = kHasMin<QT> && valid ? __uint_as_float(src[17]) : 0.0f;
 }
 
 // A wave's x records: read once from LDS into registers (M * NB records,
@@ -259,8 +273,8 @@ struct Payload {
 template <int QT, int NB, int R>
 struct Chunk {
     u32x4 q[R][NB][Payload<QT>::V];
-    uint16_t d[R][NB];  // f16 d; Q4_K: sc | m << 8; Q6_K: int8 scales of the two halves
-    uint32_t h[R][NB];  // Q4_K: d | dmin << 16 of the block's 256-weight group; Q6_K: d
+    uint16_t d[R][NB];  // f16 d; Q4_K, Q5_K: sc | m << 8; Q6_K: int8 scales of the two halves
+    uint32_t h[R][NB];  // Q4_K, Q5_K: d | dmin << 16 of the block's 256-weight group; Q6_K: d
 };
 
 // Weight addresses: base + row * rb + a lane offset, with the row offset
@@ -297,7 +311,7 @@ __device__ __forceinline__ void load_chunk(Chunk<QT, NB, R>& c, const uint8_t* _
                 c.q[r][i][v] = __builtin_nontemporal_load(
                     reinterpret_cast<const u32x4*>(base + ro + poff[i]) + v);
             c.d[r][i] = *reinterpret_cast<const uint16_t*>(base + ro + soff[i]);
-            if constexpr (QT == UNILLM_QTYPE_Q4_K || QT == UNILLM_QTYPE_Q6_K)
+            if constexpr (kHasMin<QT> || QT == UNILLM_QTYPE_Q6_K)
                 c.h[r][i] = *reinterpret_cast<const uint32_t*>(base + ro + hoff[i]);
         }
     }
@@ -364,12 +378,14 @@ __device__ __forceinline__ void compute_chunk(const Chunk<QT, NB, R>& c, const X
                     }
                     acc = a0 * 254 + a1;
                 }
-                if constexpr (QT == UNILLM_QTYPE_Q4_K) {
-                    // (d sc) (acc sx + 8 sum x) - (dmin m) sum x: acc is sum (q - 8) x
+                if constexpr (kHasMin<QT>) {
+                    // (d sc) (acc sx + c0 sum x) - (dmin m) sum x: acc is sum (q - c0) x,
+                    // c0 = 8 (Q4_K nibbles) or 16 (Q5_K bytes)
+                    constexpr float c0 = QT == UNILLM_QTYPE_Q5_K ? 16.0f : 8.0f;
                     const uint32_t h = c.h[r][i], sm = c.d[r][i];
                     const float s = __half2float(__ushort_as_half((uint16_t)h)) * (float)(sm & 0xFFu);
                     const float o = __half2float(__ushort_as_half((uint16_t)(h >> 16))) * (float)(sm >> 8);
-                    const float t = fmaf((float)acc, xb.sx, 8.0f * xb.xsum);
+                    const float t = fmaf((float)acc, xb.sx, c0 * xb.xsum);
                     part[m][r] = fmaf(-o, xb.xsum, fmaf(s, t, part[m][r]));
                 } else {
                     const float dw = __half2float(__ushort_as_half(c.d[r][i]));
@@ -621,7 +637,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
         if (wave0 + p * THREADS >= nq) continue;
         const int q = threadIdx.x + p * THREADS;
         uint32_t* dst = xlds + (size_t)(min(q, nq - 1) >> 2) * kXWords;
-        if constexpr (kByteCodes<QT>) prep_q8(v[p], q & 3, q < nq, dst);
+        if constexpr (kByteCodes<QT>) prep_q8<QT == UNILLM_QTYPE_Q5_K>(v[p], q & 3, q < nq, dst);
         else prep_q4<QT == UNILLM_QTYPE_Q4_K>(v[p], q & 3, q < nq, dst);
         __builtin_amdgcn_sched_barrier(0);  // one pass's temporaries live at a time
     }
@@ -755,14 +771,14 @@ hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipSt
 // NB = 7 at one row (K = 14336), 4 at two, 2 at four; Q8_0 payloads are twice
 // as wide, so it stops at NB = 4.  M * KB <= 512 also bounds the LDS (40 KiB).
 int64_t gemv_max_kb(int64_t m, int qtype) {
-    if (m <= 1) return qtype == UNILLM_QTYPE_Q8_0 || qtype == UNILLM_QTYPE_Q6_K ? 256 : 448;
+    if (m <= 1) return byte_codes(qtype) ? 256 : 448;
     if (m <= 2) return 256;
     return 128;
 }
 
 // The SwiGLU pair epilogue holds two chunks of one gate and one up row: the
 // tokens times the 128-bit payload loads of a row at most 4, past which it spills
-// (m = 1: Q4_0 / Q4_K k <= 8192, Q8_0 / Q6_K k <= 4096; halved per doubling of m).
+// (m = 1: Q4_0 / Q4_K k <= 8192, Q8_0 / Q5_K / Q6_K k <= 4096; halved per doubling of m).
 bool gemv_supports_swiglu(const QWeight& w, int64_t m) {
     const int64_t nbv = (w.kb + 63) / 64 * (qbytes(w.qtype) / 16);
     const int64_t mb = m <= 1 ? 1 : m <= 2 ? 2 : 4;  // the kernel's token count M
@@ -785,6 +801,11 @@ hipError_t launch_gemv(const QWeight& w, const float* x, int64_t m, float* y, hi
         if (m == 1) return launch_m<UNILLM_QTYPE_Q4_K, 1>(w, x, m, y, s, epi, norm);
         if (m == 2) return launch_m<UNILLM_QTYPE_Q4_K, 2>(w, x, m, y, s, epi, norm);
         return launch_m<UNILLM_QTYPE_Q4_K, 4>(w, x, m, y, s, epi, norm);
+    }
+    if (w.qtype == UNILLM_QTYPE_Q5_K) {
+        if (m == 1) return launch_m<UNILLM_QTYPE_Q5_K, 1>(w, x, m, y, s, epi, norm);
+        if (m == 2) return launch_m<UNILLM_QTYPE_Q5_K, 2>(w, x, m, y, s, epi, norm);
+        return launch_m<UNILLM_QTYPE_Q5_K, 4>(w, x, m, y, s, epi, norm);
     }
     if (w.qtype == UNILLM_QTYPE_Q6_K) {
         if (m == 1) return launch_m<UNILLM_QTYPE_Q6_K, 1>(w, x, m, y, s, epi, norm);

@@ -28,6 +28,12 @@
 // sc_lo scales weights 0 .. 15 of the block, sc_hi 16 .. 31 (GGML's scales[j]
 // covers weights 16 j .. 16 j + 15); w = (d sc) (q - 32), d sc exact in f32.
 // 34.5 B per 32 weights against GGUF's 26.25: the 6-bit codes take a byte each.
+//
+// Q5_K (GGML block_q5_K: Q4_K's d, dmin, scales and nibbles, plus a fifth bit
+// per weight) is repacked into Q8_0's frame with Q4_K's scale words and header:
+//   [kb x 32 B int8 codes q - 16][kb x u16 (sc | m << 8)][kb / 8 x u32 (d | dmin << 16)][pad]
+// in element order, so w = (d sc) q - dmin m = (d sc)(q - 16) + (16 d sc - dmin m).
+// 34.5 B per 32 weights against GGUF's 22: the 5-bit codes take a byte each.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -95,11 +101,13 @@ struct NormArgs {
 };
 
 inline bool is_kquant(int qtype) {
-    return qtype == UNILLM_QTYPE_Q4_K || qtype == UNILLM_QTYPE_Q6_K;
+    return qtype == UNILLM_QTYPE_Q4_K || qtype == UNILLM_QTYPE_Q5_K || qtype == UNILLM_QTYPE_Q6_K;
 }
-inline int qbytes(int qtype) {
-    return qtype == UNILLM_QTYPE_Q8_0 || qtype == UNILLM_QTYPE_Q6_K ? 32 : 16;
+// byte codes (one int8 a weight): Q8_0, and Q5_K / Q6_K as repacked
+inline bool byte_codes(int qtype) {
+    return qtype == UNILLM_QTYPE_Q8_0 || qtype == UNILLM_QTYPE_Q5_K || qtype == UNILLM_QTYPE_Q6_K;
 }
+inline int qbytes(int qtype) { return byte_codes(qtype) ? 32 : 16; }
 inline int64_t row_bytes_for(int qtype, int64_t kb) {
     const int64_t hdr = is_kquant(qtype) ? kb / 8 * 4 : 0;
     return (kb * (qbytes(qtype) + 2) + hdr + 15) / 16 * 16;
@@ -116,7 +124,7 @@ __host__ __device__ __forceinline__ const uint16_t* blk_scale(const uint8_t* bas
                                                                int64_t kb, int64_t row, int64_t b) {
     return reinterpret_cast<const uint16_t*>(base + row * rb + kb * QB) + b;
 }
-// K-quants: the u32 header of the 256-weight group holding block b (Q4_K:
+// K-quants: the u32 header of the 256-weight group holding block b (Q4_K, Q5_K:
 // d | dmin << 16; Q6_K: d), after the payload (QB bytes a block) and u16 planes.
 template <int QB>
 __host__ __device__ __forceinline__ const uint32_t* kq_header(const uint8_t* base, int64_t rb,
@@ -133,6 +141,7 @@ inline int gguf_block_bytes(int qtype) {
     switch (qtype) {
         case UNILLM_QTYPE_Q8_0: return 34;
         case UNILLM_QTYPE_Q4_K: return 144;
+        case UNILLM_QTYPE_Q5_K: return 176;
         case UNILLM_QTYPE_Q6_K: return 210;
         default: return 18;
     }
@@ -165,7 +174,7 @@ bool debug_launch();
 hipError_t launch_repack(const QWeight& w, const uint8_t* gguf, hipStream_t s);
 hipError_t launch_dequant(const QWeight& w, float* out, hipStream_t s);
 // max over the scale plane of (f16 bits & 0x7FFF), atomically max-ed into out[0]
-// (Q4_K: max |d| into out[0], max |dmin| into out[1]; Q6_K: max |d| into out[0])
+// (Q4_K, Q5_K: max |d| into out[0], max |dmin| into out[1]; Q6_K: max |d| into out[0])
 hipError_t launch_scale_absmax(const QWeight& w, uint32_t* out, hipStream_t s);
 hipError_t launch_quantize(int qtype, const float* w, int64_t n, int64_t k, uint8_t* out,
                            hipStream_t s);

@@ -91,7 +91,7 @@ __device__ __forceinline__ uint32_t scale2(uint32_t v, f16x2 bias, f16x2 sc) {
     return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, v) - bias) * sc);
 }
 
-// f16 pair (v - bias) * sc - off (Q4_K's block minimum)
+// f16 pair (v - bias) * sc - off (Q4_K's and Q5_K's block minimum)
 __device__ __forceinline__ uint32_t scale2o(uint32_t v, f16x2 bias, f16x2 sc, f16x2 off) {
     return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, v) - bias) * sc - off);
 }
@@ -107,7 +107,9 @@ __device__ __forceinline__ uint32_t scale2o(uint32_t v, f16x2 bias, f16x2 sc, f1
 //   Q4_K: the same with bias 1024, sc = d sc_b 2^-E (/ 16), minus off = dmin m_b
 //         2^-E (sc and off rounded to f16 once each, the weight once more);
 //   Q8_0 / Q6_K: a byte (int8 code, flipped to q + 128) as 1024 + q + 128, bias
-//         1152 (Q6_K: the code is q - 32, sc = d sc_half 2^-E).
+//         1152 (Q6_K: the code is q - 32, sc = d sc_half 2^-E);
+//   Q5_K: a byte (the code q - 16) as 1024 + q - 16 + 128, bias 1136, sc and off as
+//         Q4_K's.
 // About 1.75 VALU per weight (Q4_K 2.25), against ~3.25 for an fp32 dequant
 // rounded to bf16 (this kernel's earlier form).
 template <int QT>
@@ -129,7 +131,7 @@ __device__ __forceinline__ f16x8 dequant8_f16(u32x2 raw, uint32_t mask, f16x2 bi
             p0 = __builtin_amdgcn_perm(0x64646464u, w, 0x04020400u);
             p1 = __builtin_amdgcn_perm(0x64646464u, w, 0x04030401u);
         }
-        if constexpr (QT == UNILLM_QTYPE_Q4_K) {
+        if constexpr (QT == UNILLM_QTYPE_Q4_K || QT == UNILLM_QTYPE_Q5_K) {
             o[2 * h] = scale2o(p0, bias, sc, off);
             o[2 * h + 1] = scale2o(p1, bias, sc, off);
         } else {
@@ -163,9 +165,13 @@ __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
 template <int QT, int BM>
 struct Ring {
     static constexpr int QB =
-        QT == UNILLM_QTYPE_Q8_0 || QT == UNILLM_QTYPE_Q6_K ? 32 : 16;  // payload bytes per block
+        QT == UNILLM_QTYPE_Q8_0 || QT == UNILLM_QTYPE_Q5_K || QT == UNILLM_QTYPE_Q6_K
+            ? 32
+            : 16;  // payload bytes per block
     static constexpr bool K4 = QT == UNILLM_QTYPE_Q4_K, K6 = QT == UNILLM_QTYPE_Q6_K;
-    static constexpr bool KQ = K4 || K6;
+    // K-quants with Q4_K's scale words and minimum: Q4_K, Q5_K
+    static constexpr bool KM = K4 || QT == UNILLM_QTYPE_Q5_K;
+    static constexpr bool KQ = KM || K6;
     static constexpr int A = BM * 128;
     static constexpr int BP = PBN * 2 * QB;
     static constexpr int BS = 2 * PBN * 4;
@@ -292,6 +298,7 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
     const bool hnib = kNib && g >= 2;
     const uint32_t nmask = hnib ? 0x00F000F0u : 0x000F000Fu;
     const _Float16 bias1 = (_Float16)(QT == UNILLM_QTYPE_Q4_K                 ? 1024.0f
+                                      : QT == UNILLM_QTYPE_Q5_K               ? 1136.0f
                                       : QT == UNILLM_QTYPE_Q4_0 && !hnib ? 1032.0f
                                                                          : 1152.0f);
     const float lsc = hnib ? 0.0625f : 1.0f;
@@ -387,14 +394,14 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_kernel(const uint8_t* __re
                 op[j] = 0;
             }
         } else {
-            // the group header (Q4_K d | dmin << 16, Q6_K d) of each column tile, laid out
+            // the group header (Q4_K, Q5_K d | dmin << 16, Q6_K d) of each column tile, laid out
             // as the scales; sc[j] holds block 0's u16 in its low half, block 1's in its
-            // high: Q4_K sc | m << 8, Q6_K the int8 scales of the two 16-weight halves
+            // high: Q4_K, Q5_K sc | m << 8, Q6_K the int8 scales of the two 16-weight halves
 #pragma unroll
             for (int j = 0; j < TJ; ++j) {
                 const float dd =
                     bval[j] ? __half2float(__ushort_as_half((uint16_t)hd[j])) * wscale : 0.0f;
-                if constexpr (R::K4) {
+                if constexpr (R::KM) {
                     const float dm =
                         bval[j] ? __half2float(__ushort_as_half((uint16_t)(hd[j] >> 16))) * wscale
                                 : 0.0f;
@@ -701,6 +708,7 @@ hipError_t launch_prefill_mfma(const QWeight& w, const float* x, int64_t m, floa
         case UNILLM_QTYPE_Q4_0: UNILLM_PREFILL_LAUNCH(UNILLM_QTYPE_Q4_0);
         case UNILLM_QTYPE_Q8_0: UNILLM_PREFILL_LAUNCH(UNILLM_QTYPE_Q8_0);
         case UNILLM_QTYPE_Q4_K: UNILLM_PREFILL_LAUNCH(UNILLM_QTYPE_Q4_K);
+        case UNILLM_QTYPE_Q5_K: UNILLM_PREFILL_LAUNCH(UNILLM_QTYPE_Q5_K);
         case UNILLM_QTYPE_Q6_K: UNILLM_PREFILL_LAUNCH(UNILLM_QTYPE_Q6_K);
         default: return hipErrorInvalidValue;
     }

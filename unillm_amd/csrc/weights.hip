@@ -89,6 +89,45 @@ __global__ __launch_bounds__(256) void repack_q4k_kernel(const uint8_t* __restri
         make_uint4(words[0], words[1], words[2], words[3]);
 }
 
+// One thread per 32-weight sub-block j of GGUF Q5_K (176-byte blocks {f16 d; f16 dmin;
+// u8 scales[12]; u8 qh[32]; u8 qs[128]}: sub-block j = 2 g + h takes nibble h of
+// qs[32 g + l] and bit j of qh[l] for its weight l, GGML dequantize_row_q5_K) -> int8
+// codes q - 16 in element order, u16 (sc | m << 8) and for j = 0 the group header
+// u32 (d | dmin << 16), as Q4_K's.
+__global__ __launch_bounds__(256) void repack_q5k_kernel(const uint8_t* __restrict__ src,
+                                                         uint8_t* __restrict__ base, int64_t rb,
+                                                         int64_t kb, int64_t nblocks) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const int64_t row = i / kb, blk = i - row * kb;
+    const int j = (int)(blk & 7);
+    const uint8_t* b = src + (i >> 3) * 176;
+    uint32_t sc, m;
+    q4k_scale_min(j, b + 4, sc, m);
+    *const_cast<uint16_t*>(blk_scale<32>(base, rb, kb, row, blk)) = (uint16_t)(sc | (m << 8));
+    if (j == 0)
+        *const_cast<uint32_t*>(kq_header<32>(base, rb, kb, row, blk)) =
+            (uint32_t)ld_u16(b) | ((uint32_t)ld_u16(b + 2) << 16);
+    const uint8_t* qh = b + 16;
+    const uint8_t* qs = b + 48 + 32 * (j >> 1);
+    const int sh = 4 * (j & 1);
+    uint32_t words[8];
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int l = 4 * w + u;
+            const uint32_t q = (((uint32_t)qs[l] >> sh) & 15u) | ((((uint32_t)qh[l] >> j) & 1u) << 4);
+            v |= ((q - 16u) & 0xFFu) << (8 * u);
+        }
+        words[w] = v;
+    }
+    uint4* dst = reinterpret_cast<uint4*>(const_cast<uint8_t*>(blk_payload<32>(base, rb, row, blk)));
+    dst[0] = make_uint4(words[0], words[1], words[2], words[3]);
+    dst[1] = make_uint4(words[4], words[5], words[6], words[7]);
+}
+
 // One thread per 32-weight block of GGUF Q6_K (210-byte blocks {u8 ql[128];
 // u8 qh[64]; i8 scales[16]; f16 d}).  Weight e of a block (half h = e / 128,
 // r = e % 128, t = r / 32, l = r % 32): q = (nibble t / 2 of ql[64 h + 32 (t % 2)
@@ -133,17 +172,40 @@ __global__ __launch_bounds__(256) void repack_q6k_kernel(const uint8_t* __restri
 // block.  Every product is exact in f32, so any evaluation order is bit-exact.
 // Q4_K (dequantize_row_q4_K): w = (d sc) q - dmin m with q = nibble + 8; d sc
 // and (d sc) q are exact in f32, so the subtraction is the one rounding, fused
-// into a multiply-add or not.
+// into a multiply-add or not.  Q5_K (dequantize_row_q5_K) the same with q = code + 16.
 template <int QT>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ base,
                                                       int64_t rb, int64_t kb,
                                                       float* __restrict__ out,
                                                       int64_t nblocks) {
-    constexpr int QB = QT == UNILLM_QTYPE_Q8_0 || QT == UNILLM_QTYPE_Q6_K ? 32 : 16;
+    constexpr int QB =
+        QT == UNILLM_QTYPE_Q8_0 || QT == UNILLM_QTYPE_Q5_K || QT == UNILLM_QTYPE_Q6_K ? 32 : 16;
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nblocks) return;
     const int64_t row = i / kb, blk = i - row * kb;
     const uint16_t sw = *blk_scale<QB>(base, rb, kb, row, blk);
+    if constexpr (QT == UNILLM_QTYPE_Q5_K) {
+        // (d sc) q - dmin m with q = code + 16, as Q4_K: (d sc) q exact, one rounding
+        const uint32_t h = *kq_header<32>(base, rb, kb, row, blk);
+        const float s = __half2float(__ushort_as_half((uint16_t)h)) * (float)(sw & 0xFFu);
+        const float mn = __half2float(__ushort_as_half((uint16_t)(h >> 16))) * (float)(sw >> 8);
+        const uint4* q = reinterpret_cast<const uint4*>(blk_payload<QB>(base, rb, row, blk));
+        float4* o = reinterpret_cast<float4*>(out + i * QK);
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+            const uint4 qq = q[v];
+            const uint32_t w[4] = {qq.x, qq.y, qq.z, qq.w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                float f[4];
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    f[b] = s * (float)((int)(int8_t)(w[t] >> (8 * b)) + 16) - mn;
+                o[4 * v + t] = make_float4(f[0], f[1], f[2], f[3]);
+            }
+        }
+        return;
+    }
     if constexpr (QT == UNILLM_QTYPE_Q6_K) {
         // (d sc) (q - 32), as GGML evaluates it: d sc exact, the second product rounds once
         const float d = __half2float(__ushort_as_half((uint16_t)*kq_header<32>(base, rb, kb, row, blk)));
@@ -300,7 +362,9 @@ __global__ __launch_bounds__(256) void scale_absmax_kernel(const uint8_t* __rest
     if (threadIdx.x == 0) atomicMax(out, part[0]);
 }
 
-// Q4_K: max |d| and max |dmin| over the group headers, as f16 magnitude bits.
+// Q4_K (QB 16), Q5_K (QB 32): max |d| and max |dmin| over the group headers, as f16
+// magnitude bits.
+template <int QB>
 __global__ __launch_bounds__(256) void q4k_header_absmax_kernel(const uint8_t* __restrict__ base,
                                                                 int64_t rb, int64_t kb,
                                                                 int64_t count,
@@ -311,7 +375,7 @@ __global__ __launch_bounds__(256) void q4k_header_absmax_kernel(const uint8_t* _
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
          i += (int64_t)gridDim.x * blockDim.x) {
         const int64_t row = i / groups;
-        const uint32_t h = *q4k_header(base, rb, kb, row, 8 * (i - row * groups));
+        const uint32_t h = *kq_header<QB>(base, rb, kb, row, 8 * (i - row * groups));
         md = max(md, h & 0x7FFFu);
         mm = max(mm, (h >> 16) & 0x7FFFu);
     }
@@ -363,6 +427,8 @@ hipError_t launch_repack(const QWeight& w, const uint8_t* gguf, hipStream_t s) {
     const int64_t nb = w.n * w.kb;
     if (w.qtype == UNILLM_QTYPE_Q4_K)
         repack_q4k_kernel<<<grid_for(nb, 256), 256, 0, s>>>(gguf, w.base, w.row_bytes, w.kb, nb);
+    else if (w.qtype == UNILLM_QTYPE_Q5_K)
+        repack_q5k_kernel<<<grid_for(nb, 256), 256, 0, s>>>(gguf, w.base, w.row_bytes, w.kb, nb);
     else if (w.qtype == UNILLM_QTYPE_Q6_K)
         repack_q6k_kernel<<<grid_for(nb, 256), 256, 0, s>>>(gguf, w.base, w.row_bytes, w.kb, nb);
     else if (w.qtype == UNILLM_QTYPE_Q4_0)
@@ -376,7 +442,9 @@ hipError_t launch_scale_absmax(const QWeight& w, uint32_t* out, hipStream_t s) {
     const int64_t nb = w.n * w.kb;
     const unsigned grid = (unsigned)std::min<int64_t>(1024, (nb + 255) / 256);
     if (w.qtype == UNILLM_QTYPE_Q4_K)
-        q4k_header_absmax_kernel<<<grid, 256, 0, s>>>(w.base, w.row_bytes, w.kb, nb / 8, out);
+        q4k_header_absmax_kernel<16><<<grid, 256, 0, s>>>(w.base, w.row_bytes, w.kb, nb / 8, out);
+    else if (w.qtype == UNILLM_QTYPE_Q5_K)
+        q4k_header_absmax_kernel<32><<<grid, 256, 0, s>>>(w.base, w.row_bytes, w.kb, nb / 8, out);
     else if (w.qtype == UNILLM_QTYPE_Q6_K)
         q6k_header_absmax_kernel<<<grid, 256, 0, s>>>(w.base, w.row_bytes, w.kb, nb / 8, out);
     else if (w.qtype == UNILLM_QTYPE_Q4_0)
@@ -390,6 +458,9 @@ hipError_t launch_dequant(const QWeight& w, float* out, hipStream_t s) {
     const int64_t nb = w.n * w.kb;
     if (w.qtype == UNILLM_QTYPE_Q4_K)
         dequant_kernel<UNILLM_QTYPE_Q4_K><<<grid_for(nb, 256), 256, 0, s>>>(w.base, w.row_bytes,
+                                                                            w.kb, out, nb);
+    else if (w.qtype == UNILLM_QTYPE_Q5_K)
+        dequant_kernel<UNILLM_QTYPE_Q5_K><<<grid_for(nb, 256), 256, 0, s>>>(w.base, w.row_bytes,
                                                                             w.kb, out, nb);
     else if (w.qtype == UNILLM_QTYPE_Q6_K)
         dequant_kernel<UNILLM_QTYPE_Q6_K><<<grid_for(nb, 256), 256, 0, s>>>(w.base, w.row_bytes,

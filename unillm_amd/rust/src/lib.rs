@@ -1,5 +1,5 @@
 //! Rust bindings to `libunillm_hip.so`: GGUF quantized matmuls (Q4_0, Q8_0, Q4_K,
-//! Q6_K) and KV-cache attention on an MI355X (gfx950).
+//! Q5_K, Q6_K) and KV-cache attention on an MI355X (gfx950).
 //!
 //! * [`sys`] is the C ABI of `include/unillm_hip.h`, one declaration per function.
 //! * [`QuantLinear`] takes the slot of candle's `QMatMul` in the reference's
@@ -48,6 +48,7 @@ pub mod sys {
     pub const UNILLM_QTYPE_Q4_0: c_int = 2;
     pub const UNILLM_QTYPE_Q8_0: c_int = 8;
     pub const UNILLM_QTYPE_Q4_K: c_int = 12;
+    pub const UNILLM_QTYPE_Q5_K: c_int = 13;
     pub const UNILLM_QTYPE_Q6_K: c_int = 14;
     pub const UNILLM_QTYPE_F32: c_int = 0;
     pub const UNILLM_QTYPE_F16: c_int = 1;
@@ -261,6 +262,7 @@ pub enum QType {
     Q4_0 = 2,
     Q8_0 = 8,
     Q4_K = 12,
+    Q5_K = 13,
     Q6_K = 14,
     F32 = 0,
     F16 = 1,
@@ -274,6 +276,7 @@ impl QType {
             2 => Some(Self::Q4_0),
             8 => Some(Self::Q8_0),
             12 => Some(Self::Q4_K),
+            13 => Some(Self::Q5_K),
             14 => Some(Self::Q6_K),
             0 => Some(Self::F32),
             1 => Some(Self::F16),
@@ -570,6 +573,7 @@ mod tests {
         assert_eq!(QType::from_ggml(2), Some(QType::Q4_0));
         assert_eq!(QType::from_ggml(8), Some(QType::Q8_0));
         assert_eq!(QType::from_ggml(12), Some(QType::Q4_K));
+        assert_eq!(QType::from_ggml(13), Some(QType::Q5_K));
         assert_eq!(QType::from_ggml(14), Some(QType::Q6_K));
         assert_eq!(QType::from_ggml(3), None);
         assert_eq!(QType::Q4_0 as c_int, sys::UNILLM_QTYPE_Q4_0);

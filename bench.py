@@ -36,8 +36,9 @@ HBM_PEAK_GBS = 8000.0
 DENSE_PEAK_TFLOPS = 2516.6
 # MI355X f32 peak (the prompt attention kernel's f32 FMA work is priced against it)
 F32_PEAK_TFLOPS = 157.3
-Q4_0, Q8_0, Q4_K = 2, 8, 12
-BPB = {Q4_0: 18, Q8_0: 34, Q4_K: 18}  # GGUF bytes per 32 weights (Q4_K: 144 per 256)
+Q4_0, Q8_0, Q4_K, Q5_K = 2, 8, 12, 13
+# GGUF bytes per 32 weights (Q4_K: 144 per 256, Q5_K: 176 per 256)
+BPB = {Q4_0: 18, Q8_0: 34, Q4_K: 18, Q5_K: 22}
 
 LLAMA2_7B = [("qkv", 4096, 12288), ("o_proj", 4096, 4096), ("gate", 4096, 11008),
              ("up", 4096, 11008), ("down", 11008, 4096)]
@@ -56,7 +57,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default="", help="comma list of extra configs to run "
-                    "(q8_gemv,batched,prefill,stack,q4_k,attention,e2e) -- for profiling")
+                    "(q8_gemv,batched,prefill,stack,q4_k,q5_k,attention,e2e) -- for profiling")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 64 MiB once (device to device) and exit: the known-size "
                     "kernel that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
@@ -306,7 +307,7 @@ def extra_configs(torch, QuantLinear, gen, stream, only):
         return float(np.median(ts))
 
     want = set(only.split(",")) if only else {"q8_gemv", "batched", "prefill", "stack", "q4_k",
-                                              "attention", "e2e"}
+                                              "q5_k", "attention", "e2e"}
     if "q8_gemv" in want:
         n, k = 5632, 2048
         ws = rotate(Q8_0, n, k)
@@ -344,47 +345,49 @@ def extra_configs(torch, QuantLinear, gen, stream, only):
                         "TFLOP/s": round(tf, 1), "frac_dense": round(tf / DENSE_PEAK_TFLOPS, 3),
                         "us": round(ms * 1e3, 1)}
                 del ws
-    if "q4_k" in want:
-        # Q4_K (the next weight format: GGUF Q4_K_M tensors), random valid blocks drawn
-        # on the device -- no Q4_K quantizer is on the path
-        def q4k_weights(n, k, copies):
+    for kq, bb, label in ((Q4_K, 144, "q4_k"), (Q5_K, 176, "q5_k")):
+        if label not in want:
+            continue
+        # K-quants (GGUF Q4_K_M / Q5_K_M tensors), random valid blocks drawn on the
+        # device -- no K-quant quantizer is on the path
+        def kq_weights(n, k, copies):
             ws = []
             nb = n * (k // 256)
             for _ in range(copies):
-                blk = torch.randint(0, 256, (nb, 144), dtype=torch.uint8, device="cuda",
+                blk = torch.randint(0, 256, (nb, bb), dtype=torch.uint8, device="cuda",
                                     generator=gen)
                 for off, lo, span in ((0, 1e-5, 4e-5), (2, 1e-5, 2e-4)):  # d, dmin (f16)
                     v = (torch.rand(nb, device="cuda", generator=gen) * span + lo).half()
                     blk[:, off:off + 2] = v.view(torch.uint8).view(nb, 2)
-                ws.append(QuantLinear.from_device_blocks(Q4_K, n, k, blk.view(-1)))
+                ws.append(QuantLinear.from_device_blocks(kq, n, k, blk.view(-1)))
             return ws
 
         for name, k, n in LLAMA2_7B:
-            ws = q4k_weights(n, k, max(1, min(48, -(-(1 << 30) // wbytes(Q4_K, n, k)))))
+            ws = kq_weights(n, k, max(1, min(48, -(-(1 << 30) // wbytes(kq, n, k)))))
             x = torch.empty(1, k, device="cuda").normal_(generator=gen)
             y = torch.empty(1, n, device="cuda")
             ms = timed(ws, x, y)
-            b = wbytes(Q4_K, n, k) + 4 * k + 4 * n
-            res[f"q4_k_gemv_m1_{name}_k{k}_n{n}"] = {
+            b = wbytes(kq, n, k) + 4 * k + 4 * n
+            res[f"{label}_gemv_m1_{name}_k{k}_n{n}"] = {
                 "GB/s": round(b / ms / 1e6, 1), "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 3),
-                "us": round(ms * 1e3, 2)}
+                "us": round(ms * 1e3, 2), "path": ws[0].select_path(1)}
             del ws
-        ws = q4k_weights(14336, 4096, 32)
+        ws = kq_weights(14336, 4096, 32)
         for m in (16, 64):
             x = torch.empty(m, 4096, device="cuda").normal_(generator=gen)
             y = torch.empty(m, 14336, device="cuda")
             ms = timed(ws, x, y)
-            b = wbytes(Q4_K, 14336, 4096) + 4 * m * 4096 + 4 * m * 14336
-            res[f"q4_k_batched_m{m}_k4096_n14336"] = {
+            b = wbytes(kq, 14336, 4096) + 4 * m * 4096 + 4 * m * 14336
+            res[f"{label}_batched_m{m}_k4096_n14336"] = {
                 "GB/s": round(b / ms / 1e6, 1), "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 3),
                 "us": round(ms * 1e3, 2), "path": ws[0].select_path(m)}
         del ws
-        ws = q4k_weights(14336, 4096, 2)
+        ws = kq_weights(14336, 4096, 2)
         x = torch.empty(2048, 4096, device="cuda").normal_(generator=gen)
         y = torch.empty(2048, 14336, device="cuda")
         ms = timed(ws, x, y, path=PATH_PREFILL_MFMA)
         tf = 2 * 2048 * 14336 * 4096 / ms / 1e9
-        res["q4_k_prefill_m2048_k4096_n14336"] = {
+        res[f"{label}_prefill_m2048_k4096_n14336"] = {
             "TFLOP/s": round(tf, 1), "frac_dense": round(tf / DENSE_PEAK_TFLOPS, 3),
             "us": round(ms * 1e3, 1)}
         del ws

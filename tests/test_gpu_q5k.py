@@ -96,7 +96,7 @@ def test_q5k_gemv_parity(m, n, k):
 
 
 def test_q5k_gemv_limits_and_auto_path():
-    # byte codes: the GEMV takes k <= 4096 at one row, like Q8_0; longer rows go
+    # byte codes: the GEMV takes k <= 8192 at one row, like Q8_0; longer rows go
     # to the batched decode
     ql = QuantLinear.from_blocks(Q5_K, 64, 11008, oracle.random_q5_k(64, 11008, seed=5))
     assert ql.select_path(1) == PATH_DECODE_MFMA

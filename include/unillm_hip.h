@@ -42,6 +42,11 @@ extern "C" {
  * attn_v / ffn_down). */
 #define UNILLM_QTYPE_Q4_0 2
 #define UNILLM_QTYPE_Q8_0 8
+/* GGML Q5_0 ({f16 d; u8 qh[4]; u8 qs[16]}: 5-bit codes, (q - 16) d), e.g. the fallback
+ * type of K-quant mixes for tensors whose k is not a multiple of 256.  Its values
+ * are exactly int8 codes times an f16 d, so the device keeps it as a Q8_0 weight
+ * (unillm_hip_qweight_info still reports 6). */
+#define UNILLM_QTYPE_Q5_0 6
 #define UNILLM_QTYPE_Q4_K 12
 #define UNILLM_QTYPE_Q5_K 13
 #define UNILLM_QTYPE_Q6_K 14
@@ -81,8 +86,8 @@ int unillm_hip_init(int device);
 /* Message of the last error on the calling thread ("" if none). */
 const char* unillm_hip_last_error(void);
 
-/* Upload one GGUF Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K tensor ([n, k]: n * k/32 blocks
- * of 18 / 34 B, or n * k/256 blocks of 144 / 176 / 210 B), or a dense F32 / F16 / BF16 one
+/* Upload one GGUF Q4_0 / Q5_0 / Q8_0 / Q4_K / Q5_K / Q6_K tensor ([n, k]: n * k/32 blocks
+ * of 18 / 22 / 34 B, or n * k/256 blocks of 144 / 176 / 210 B), or a dense F32 / F16 / BF16 one
  * (n * k elements of 4 / 2 / 2 B), to the device, repacked there into the kernels'
  * layout (dense: f32 rows).  Replaces
  * `QMatMul::from_arc(Arc::new(qtensor))` at

@@ -19,11 +19,12 @@ import numpy as np
 Q4_0 = 2
 Q8_0 = 8
 Q4_K = 12
+Q5_0 = 6
 Q5_K = 13
 Q6_K = 14
 QK = 32
-BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
-BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q5_0: 22, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+BLOCK_ELEMS = {Q4_0: 32, Q5_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liboracle.so")
@@ -220,6 +221,18 @@ def random_q5_k(n: int, k: int, seed: int) -> np.ndarray:
     dmin = (np.abs(rng.normal(0, 1, nb)) * 2e-4 + 1e-5).astype(np.float16)
     blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
     blk[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)
+    return blk.reshape(n, -1)
+
+
+def random_q5_0(n: int, k: int, seed: int) -> np.ndarray:
+    """[n, k/32 * 22] valid Q5_0 blocks (random codes and fifth bits, f16 d sized like
+    N(0, 0.02) weights)."""
+    assert k % 32 == 0
+    rng = np.random.default_rng(seed)
+    nb = n * (k // 32)
+    blk = rng.integers(0, 256, size=(nb, 22), dtype=np.uint8)
+    d = (np.abs(rng.normal(0, 1, nb)) * 2e-3 + 1e-4).astype(np.float16)
+    blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
     return blk.reshape(n, -1)
 
 

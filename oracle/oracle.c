@@ -18,7 +18,7 @@
 #endif
 
 int oracle_block_elems(int qtype) {
-    if (qtype == ORACLE_Q4_0 || qtype == ORACLE_Q8_0) return 32;
+    if (qtype == ORACLE_Q4_0 || qtype == ORACLE_Q5_0 || qtype == ORACLE_Q8_0) return 32;
     if (qtype == ORACLE_Q4_K || qtype == ORACLE_Q5_K || qtype == ORACLE_Q6_K) return 256;
     return 0;
 }
@@ -33,6 +33,7 @@ size_t oracle_block_bytes(int qtype) {
      * not what candle's Q4K reads).  Q5_K: 2 + 2 + 12 + 32 + 128 = 176 B (GGML
      * block_q5_K). */
     if (qtype == ORACLE_Q4_0) return 18;
+    if (qtype == ORACLE_Q5_0) return 22; /* {f16 d; u8 qh[4]; u8 qs[16]} (GGML block_q5_0) */
     if (qtype == ORACLE_Q8_0) return 34;
     if (qtype == ORACLE_Q4_K) return 144;
     if (qtype == ORACLE_Q5_K) return 176;
@@ -250,6 +251,20 @@ static void dequant_block(int qtype, const uint8_t* blk, float* y) {
         return;
     }
     const float d = oracle_f16_to_f32(rd16(blk));
+    if (qtype == ORACLE_Q5_0) {
+        /* GGML dequantize_row_q5_0: the fifth bit of element j is bit j of the
+         * little-endian u32 qh; (q - 16) * d is exact in f32 */
+        const uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) |
+                            ((uint32_t)blk[4] << 16) | ((uint32_t)blk[5] << 24);
+        const uint8_t* qs = blk + 6;
+        for (int j = 0; j < 16; ++j) {
+            const int x0 = ((qs[j] & 0x0F) | (((qh >> j) & 1) << 4)) - 16;
+            const int x1 = ((qs[j] >> 4) | (((qh >> (j + 16)) & 1) << 4)) - 16;
+            y[j] = (float)x0 * d;
+            y[j + 16] = (float)x1 * d;
+        }
+        return;
+    }
     const uint8_t* qs = blk + 2;
     if (qtype == ORACLE_Q4_0) {
         for (int j = 0; j < 16; ++j) {

@@ -15,6 +15,9 @@
  *        w[j]    = ((qs[j] & 0xF) - 8) * d      j = 0..15
  *        w[j+16] = ((qs[j] >>  4) - 8) * d
  *   Q8_0 block (34 B / 32 weights): { f16 d; i8 qs[32]; }   w[j] = qs[j] * d
+ *   Q5_0 block (22 B / 32 weights): { f16 d; u8 qh[4]; u8 qs[16]; }  (dequantize_row_q5_0)
+ *        w[j]    = ((qs[j] & 0xF) | bit j of qh << 4) - 16) * d          j = 0..15
+ *        w[j+16] = ((qs[j] >>  4) | bit j + 16 of qh << 4) - 16) * d
  *   Q4_K block (144 B / 256 weights, GGML block_q4_K, candle GgmlDType::Q4K,
  *        mapped at weight_loader_core.rs:481):
  *        { f16 d; f16 dmin; u8 scales[12]; u8 qs[128]; }
@@ -77,14 +80,16 @@ extern "C" {
 
 #define ORACLE_QK 32
 #define ORACLE_Q4_0 2
+#define ORACLE_Q5_0 6
 #define ORACLE_Q8_0 8
 #define ORACLE_Q4_K 12
 #define ORACLE_Q5_K 13
 #define ORACLE_Q6_K 14
 
-/* weights per block: 32 (Q4_0, Q8_0) or 256 (Q4_K, Q5_K, Q6_K); 0 for unknown types */
+/* weights per block: 32 (Q4_0, Q5_0, Q8_0) or 256 (Q4_K, Q5_K, Q6_K); 0 for unknown types */
 int oracle_block_elems(int qtype);
-/* bytes per block: 18 (Q4_0), 34 (Q8_0), 144 (Q4_K), 176 (Q5_K), 210 (Q6_K); 0 for unknown */
+/* bytes per block: 18 (Q4_0), 22 (Q5_0), 34 (Q8_0), 144 (Q4_K), 176 (Q5_K), 210 (Q6_K); 0 for
+ * unknown */
 size_t oracle_block_bytes(int qtype);
 
 /* IEEE binary16 <-> binary32 (round to nearest even, subnormals, inf, nan) */

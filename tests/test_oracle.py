@@ -237,6 +237,72 @@ def test_fill_normal_is_deterministic_and_normal():
     assert not np.array_equal(a[:1000], oracle.normal(1000, seed=6))
 
 
+# ---- Q5_0 (GGML block_q5_0) -------------------------------------------------------------------
+
+from oracle import Q5_0  # noqa: E402
+
+
+def _q50_block(d, qh, qs) -> np.ndarray:
+    b = np.zeros(22, np.uint8)
+    b[0:2] = np.array([d], np.float16).view(np.uint8)
+    b[2:6] = np.array([qh], np.uint32).view(np.uint8)
+    b[6:] = np.asarray(qs, np.uint8)
+    return b
+
+
+def test_q5_0_code_positions_one_hot():
+    # d = 1, base code 16 (weight 0): nibble byte j -> element j (low) / j + 16
+    # (high); qh bit i -> element i, adding 16
+    cases, want = [], []
+    base_qs = np.zeros(16, np.uint8)
+    for j in range(16):
+        for hi in range(2):
+            qs = base_qs.copy()
+            qs[j] = 0x50 if hi else 0x05
+            cases.append(_q50_block(1.0, 0xFFFFFFFF, qs))  # every fifth bit set: q = 16 + code
+            e = np.zeros(32, np.float32)
+            e[j + 16 * hi] = 5.0
+            want.append(e)
+    for i in range(32):
+        cases.append(_q50_block(1.0, 0xFFFFFFFF & ~(1 << i), base_qs))
+        e = np.zeros(32, np.float32)
+        e[i] = -16.0
+        want.append(e)
+    got = oracle.dequant(Q5_0, np.stack(cases), len(cases), 32)
+    assert np.array_equal(got, np.stack(want))
+
+
+def test_q5_0_exhaustive_scales_and_codes():
+    # every f16 d against all 32 codes (element e holds code e): w = (e - 16) d exactly
+    qs = np.array([j | (j << 4) for j in range(16)], np.uint8)  # both nibbles of byte j: j
+    qh = 0xFFFF0000  # elements 16..31 get the fifth bit: codes 16 + j
+    codes = np.concatenate([np.arange(16), 16 + np.arange(16)]).astype(np.float32)
+    blocks = np.tile(_q50_block(0.0, qh, qs), (65536, 1))
+    blocks[:, 0:2] = np.arange(65536, dtype=np.uint16).view(np.uint8).reshape(-1, 2)
+    got = oracle.dequant(Q5_0, blocks, 65536, 32)
+    d = np.arange(65536, dtype=np.uint16).view(np.float16).astype(np.float32)[:, None]
+    with np.errstate(invalid="ignore"):  # inf * 0 for the code 16 of an infinite d
+        want = (codes[None, :] - 16.0) * d
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan], want[~nan])
+
+
+def _numpy_q5_0(blocks: np.ndarray) -> np.ndarray:
+    b = blocks.reshape(-1, 22)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    hb = np.unpackbits(b[:, 2:6], axis=1, bitorder="little").astype(np.int32)  # [nb][32]
+    qs = b[:, 6:].astype(np.int32)
+    lo = np.concatenate([qs & 15, qs >> 4], axis=1)
+    return ((lo | (hb << 4)) - 16).astype(np.float32) * d[:, None]
+
+
+def test_q5_0_random_blocks_match_numpy_decoder():
+    blocks = oracle.random_q5_0(64, 1024, seed=12)
+    got = oracle.dequant(Q5_0, blocks, 64, 1024)
+    assert np.array_equal(got.reshape(-1, 32), _numpy_q5_0(blocks))
+
+
 # ---- Q4_K / Q5_K / Q6_K (GGML block_q4_K / block_q5_K / block_q6_K) ---------------------------------------------
 
 from oracle import Q4_K, Q5_K, Q6_K  # noqa: E402
@@ -466,10 +532,11 @@ def test_q6_k_random_blocks_match_numpy_decoder():
     assert np.array_equal(got.reshape(-1, 256), _numpy_q6_k(blocks))
 
 
-@pytest.mark.parametrize("qtype", [Q4_K, Q5_K, Q6_K])
+@pytest.mark.parametrize("qtype", [Q4_K, Q5_K, Q6_K, Q5_0])
 def test_qmatmul_f64_k_quants_match_numpy_float64(qtype):
     n, k, m = 29, 512, 3
-    gen = {Q4_K: oracle.random_q4_k, Q5_K: oracle.random_q5_k, Q6_K: oracle.random_q6_k}[qtype]
+    gen = {Q4_K: oracle.random_q4_k, Q5_K: oracle.random_q5_k, Q6_K: oracle.random_q6_k,
+           Q5_0: oracle.random_q5_0}[qtype]
     blocks = gen(n, k, seed=12)
     x = oracle.normal(m * k, seed=13).reshape(m, k)
     want = x.astype(np.float64) @ oracle.dequant(qtype, blocks, n, k).astype(np.float64).T

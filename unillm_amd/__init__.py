@@ -8,12 +8,12 @@ crates/runtime/src/model_core.rs:134).
 """
 from ._capi import (BF16, BLOCK_BYTES, BLOCK_ELEMS, ERR_HIP, ERR_INVALID_ARG, ERR_UNSUPPORTED, F16, F32,
                     OK, PATH_AUTO, PATH_DECODE_MFMA, PATH_DENSE, PATH_GEMV, PATH_PREFILL_MFMA, QK,
-                    Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, HipError)
+                    Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0, HipError)
 
 __all__ = [
     "BF16", "BLOCK_BYTES", "BLOCK_ELEMS", "ERR_HIP", "ERR_INVALID_ARG", "ERR_UNSUPPORTED", "F16", "F32",
     "OK", "PATH_AUTO", "PATH_DECODE_MFMA", "PATH_DENSE", "PATH_GEMV", "PATH_PREFILL_MFMA", "QK",
-    "Q4_0", "Q4_K", "Q5_K", "Q6_K", "Q8_0",
+    "Q4_0", "Q4_K", "Q5_0", "Q5_K", "Q6_K", "Q8_0",
     "HipError",
     "QuantLinear", "quantize_blocks", "lm_head_forward", "KvCache",
 ]

@@ -15,6 +15,7 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "unillm_hip.h")
 Q4_0 = 2
 Q8_0 = 8
 Q4_K = 12
+Q5_0 = 6
 Q5_K = 13
 Q6_K = 14
 # dense projection weights (candle's dequantized f32 QMatMul): f32 rows on the device
@@ -25,8 +26,8 @@ DENSE = (F32, F16, BF16)
 QK = 32
 # GGUF block geometry: weights per block and bytes per block (a dense element is a
 # block of one)
-BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, F32: 1, F16: 1, BF16: 1}
-BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, F32: 4, F16: 2, BF16: 2}
+BLOCK_ELEMS = {Q4_0: 32, Q5_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, F32: 1, F16: 1, BF16: 1}
+BLOCK_BYTES = {Q4_0: 18, Q5_0: 22, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, F32: 4, F16: 2, BF16: 2}
 
 PATH_AUTO = 0
 PATH_GEMV = 1

@@ -101,15 +101,16 @@ int ensure_init() {
 }
 
 bool valid_qtype(int q) {
-    return q == UNILLM_QTYPE_Q4_0 || q == UNILLM_QTYPE_Q8_0 || q == UNILLM_QTYPE_Q4_K ||
-           q == UNILLM_QTYPE_Q5_K || q == UNILLM_QTYPE_Q6_K || is_dense(q);
+    return q == UNILLM_QTYPE_Q4_0 || q == UNILLM_QTYPE_Q5_0 || q == UNILLM_QTYPE_Q8_0 ||
+           q == UNILLM_QTYPE_Q4_K || q == UNILLM_QTYPE_Q5_K || q == UNILLM_QTYPE_Q6_K ||
+           is_dense(q);
 }
 
 int check_shape(int qtype, int64_t n, int64_t k) {
     if (!valid_qtype(qtype))
         return fail(UNILLM_ERR_UNSUPPORTED,
                     "unsupported qtype " + std::to_string(qtype) +
-                        " (want 2 = Q4_0, 8 = Q8_0, 12 = Q4_K, 13 = Q5_K, 14 = Q6_K, or dense 0 = F32, "
+                        " (want 2 = Q4_0, 6 = Q5_0, 8 = Q8_0, 12 = Q4_K, 13 = Q5_K, 14 = Q6_K, or dense 0 = F32, "
                         "1 = F16, 30 = BF16)");
     if (is_dense(qtype)) {
         if (n < 1 || k < 1)
@@ -141,12 +142,14 @@ size_t gguf_bytes(int qtype, int64_t n, int64_t k) {
 int alloc_weight(int qtype, int64_t n, int64_t k, QWeight** out) {
     QWeight* w = new (std::nothrow) QWeight{};
     if (!w) return fail(UNILLM_ERR_OUT_OF_MEMORY, "host allocation failed");
-    w->qtype = qtype;
+    // Q5_0 runs as Q8_0 (its int8 codes q - 16 times d): repacked into that frame
+    w->qtype = qtype == UNILLM_QTYPE_Q5_0 ? UNILLM_QTYPE_Q8_0 : qtype;
+    w->src_qtype = qtype;
     w->device = g_device;
     w->n = n;
     w->k = k;
     w->kb = is_dense(qtype) ? 0 : k / QK;
-    w->row_bytes = is_dense(qtype) ? 4 * k : row_bytes_for(qtype, w->kb);
+    w->row_bytes = is_dense(qtype) ? 4 * k : row_bytes_for(w->qtype, w->kb);
     // + a 256-byte tail slot for the scale reduction run at create
     w->bytes = (((size_t)n * (size_t)w->row_bytes + 255) & ~(size_t)255) + 256;
     void* mem = nullptr;
@@ -195,7 +198,9 @@ int finish_weight(QWeight* w, hipStream_t s) {
     const float wmax = w->qtype == UNILLM_QTYPE_Q4_K   ? 63.0f * (15.0f * f16max(bits[0]) + f16max(bits[1]))
                        : w->qtype == UNILLM_QTYPE_Q5_K ? 63.0f * (31.0f * f16max(bits[0]) + f16max(bits[1]))
                        : w->qtype == UNILLM_QTYPE_Q6_K ? 4096.0f * f16max(bits[0])
-                       : f16max(bits[0]) * (w->qtype == UNILLM_QTYPE_Q4_0 ? 8.0f : 128.0f);
+                       : f16max(bits[0]) * (w->qtype == UNILLM_QTYPE_Q4_0        ? 8.0f
+                                            : w->src_qtype == UNILLM_QTYPE_Q5_0 ? 16.0f
+                                                                                : 128.0f);
     // the largest power-of-two scaling that keeps every dequantized weight in
     // f16 range: small scales stay normal in f16 (also divided by 16)
     int E = 0;
@@ -359,7 +364,7 @@ int unillm_hip_qweight_destroy(unillm_qweight* w) {
 int unillm_hip_qweight_info(const unillm_qweight* w, int* qtype, int64_t* n, int64_t* k,
                             size_t* device_bytes) {
     if (!w) return fail(UNILLM_ERR_INVALID_ARG, "weight is NULL");
-    if (qtype) *qtype = w->qtype;
+    if (qtype) *qtype = w->src_qtype;
     if (n) *n = w->n;
     if (k) *k = w->k;
     if (device_bytes) *device_bytes = w->bytes;

@@ -13,6 +13,9 @@
 // count is GGUF's (18 or 34 B per 32 weights) plus at most 15 B of row
 // padding; dequant of this layout is bit-exact with the GGUF bytes.
 //
+// Q5_0 (GGML block_q5_0: f16 d, 32 fifth bits, 16 nibble bytes) holds int8 codes
+// q - 16 times d: it is repacked into Q8_0's frame and runs as Q8_0.
+//
 // Q4_K (GGML block_q4_K: 256 weights = 8 sub-blocks of 32 under one f16 d and
 // one f16 dmin, 6-bit scale sc_j and min m_j per sub-block) is repacked into the
 // same frame, one 32-weight sub-block per block:
@@ -45,7 +48,8 @@
 
 // The opaque handle of the C ABI is the weight descriptor itself.
 struct unillm_qweight {
-    int qtype;
+    int qtype;             // the layout and kernels' type (Q5_0 is held as Q8_0)
+    int src_qtype;         // the GGUF type the caller created it from
     int device;
     int64_t n, k, kb;      // kb = k / 32
     int64_t row_bytes;     // bytes per row: payloads, scales, padding
@@ -140,6 +144,7 @@ inline int gguf_block_elems(int qtype) { return is_kquant(qtype) ? 256 : QK; }
 inline int gguf_block_bytes(int qtype) {
     switch (qtype) {
         case UNILLM_QTYPE_Q8_0: return 34;
+        case UNILLM_QTYPE_Q5_0: return 22;
         case UNILLM_QTYPE_Q4_K: return 144;
         case UNILLM_QTYPE_Q5_K: return 176;
         case UNILLM_QTYPE_Q6_K: return 210;

@@ -41,6 +41,38 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
         dst[v] = make_uint4(words[4 * v], words[4 * v + 1], words[4 * v + 2], words[4 * v + 3]);
 }
 
+// One thread per GGUF Q5_0 block ({f16 d; u8 qh[4]; u8 qs[16]}, 22 B, 2-byte aligned):
+// element e's code is its nibble (low of qs[e] for e < 16, high of qs[e - 16] above)
+// plus bit e of the little-endian u32 qh as the fifth bit (GGML dequantize_row_q5_0)
+// -> Q8_0's frame: the int8 codes q - 16 in element order and d as the block's scale.
+__global__ __launch_bounds__(256) void repack_q5_0_kernel(const uint8_t* __restrict__ src,
+                                                          uint8_t* __restrict__ base, int64_t rb,
+                                                          int64_t kb, int64_t nblocks) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const int64_t row = i / kb, blk = i - row * kb;
+    const uint8_t* b = src + i * 22;
+    *const_cast<uint16_t*>(blk_scale<32>(base, rb, kb, row, blk)) = ld_u16(b);
+    const uint32_t qh = (uint32_t)ld_u16(b + 2) | ((uint32_t)ld_u16(b + 4) << 16);
+    const uint8_t* qs = b + 6;
+    uint32_t words[8];
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = 4 * w + u;
+            const uint32_t nib = e < 16 ? qs[e] & 15u : (uint32_t)qs[e - 16] >> 4;
+            const uint32_t q = nib | (((qh >> e) & 1u) << 4);
+            v |= ((q - 16u) & 0xFFu) << (8 * u);
+        }
+        words[w] = v;
+    }
+    uint4* dst = reinterpret_cast<uint4*>(const_cast<uint8_t*>(blk_payload<32>(base, rb, row, blk)));
+    dst[0] = make_uint4(words[0], words[1], words[2], words[3]);
+    dst[1] = make_uint4(words[4], words[5], words[6], words[7]);
+}
+
 // GGML get_scale_min_k4: 6-bit scale and min of sub-block j from scales[12].
 __device__ __forceinline__ void q4k_scale_min(int j, const uint8_t* q, uint32_t& sc, uint32_t& m) {
     if (j < 4) {
@@ -425,7 +457,9 @@ inline unsigned grid_for(int64_t items, int block) {
 
 hipError_t launch_repack(const QWeight& w, const uint8_t* gguf, hipStream_t s) {
     const int64_t nb = w.n * w.kb;
-    if (w.qtype == UNILLM_QTYPE_Q4_K)
+    if (w.src_qtype == UNILLM_QTYPE_Q5_0)
+        repack_q5_0_kernel<<<grid_for(nb, 256), 256, 0, s>>>(gguf, w.base, w.row_bytes, w.kb, nb);
+    else if (w.qtype == UNILLM_QTYPE_Q4_K)
         repack_q4k_kernel<<<grid_for(nb, 256), 256, 0, s>>>(gguf, w.base, w.row_bytes, w.kb, nb);
     else if (w.qtype == UNILLM_QTYPE_Q5_K)
         repack_q5k_kernel<<<grid_for(nb, 256), 256, 0, s>>>(gguf, w.base, w.row_bytes, w.kb, nb);

@@ -383,8 +383,8 @@ namespace {
 // the types a projection keeps on the device: the block types, and the dense F32 / F16 /
 // BF16 that candle's QMatMul::from_arc keeps as a dequantized f32 tensor
 bool device_qtype(uint32_t t) {
-    return t == GGML_Q4_0 || t == GGML_Q8_0 || t == GGML_Q4_K || t == GGML_Q5_K ||
-           t == GGML_Q6_K || t == GGML_F32 || t == GGML_F16 || t == GGML_BF16;
+    return t == GGML_Q4_0 || t == GGML_Q5_0 || t == GGML_Q8_0 || t == GGML_Q4_K ||
+           t == GGML_Q5_K || t == GGML_Q6_K || t == GGML_F32 || t == GGML_F16 || t == GGML_BF16;
 }
 
 // The fusable groups of one layer: {fused hf name, part hf names}.
@@ -456,7 +456,8 @@ ModelWeights GgufWeightLoader::load_weights(const std::string& path,
                 throw Error("Failed to create QMatMul for '" + t.name + "': " +
                             ggml_type_name(t.type) + " " + std::to_string(t.ne.size()) +
                             "-D weights are not supported on the HIP device "
-                            "(Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K / F32 / F16 / BF16 only)");
+                            "(Q4_0 / Q5_0 / Q8_0 / Q4_K / Q5_K / Q6_K / F32 / F16 / BF16 "
+                            "only)");
             w.quantized_tensors[hf] = QuantLinear::from_blocks(
                 (int)t.type, (int64_t)t.ne[1], (int64_t)t.ne[0], bytes.data(), bytes.size());
             continue;

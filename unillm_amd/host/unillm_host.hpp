@@ -262,7 +262,7 @@ class GgufWeightLoader {
 public:
     bool supports(const std::string& path) const;
     // Parses the file, uploads every *_proj / lm_head tensor to the device as
-    // a QuantLinear (Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, or the dense F32 / F16 / BF16) and
+    // a QuantLinear (Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, or the dense F32 / F16 / BF16) and
     // dequantizes the rest to host f32.
     ModelWeights load_weights(const std::string& path, const LoadOptions& opt = {}) const;
     // What load_weights would do, without any device work: hf name, shape,

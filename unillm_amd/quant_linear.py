@@ -1,4 +1,5 @@
-"""QuantLinear: a device-resident GGUF Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K weight and its forward.
+"""QuantLinear: a device-resident GGUF Q4_0 / Q5_0 / Q8_0 / Q4_K / Q5_K / Q6_K weight and its
+forward.
 
 It takes the slot that `Arc<QMatMul>` holds in unillm's
 `ModelWeights.quantized_tensors` (crates/runtime/src/model_core.rs:134) and
@@ -20,8 +21,8 @@ import numpy as np
 import torch
 
 from . import _capi
-from ._capi import (BF16, BLOCK_BYTES, BLOCK_ELEMS, F16, F32, QK, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0,
-                    HipError)
+from ._capi import (BF16, BLOCK_BYTES, BLOCK_ELEMS, F16, F32, QK, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K,
+                    Q8_0, HipError)
 
 
 def _stream_ptr(stream: torch.cuda.Stream | None) -> int:
@@ -41,7 +42,7 @@ class QuantLinear:
     # ---- construction (WeightLoaderCore's QMatMul::from_arc, weight_loader_core.rs:569)
     @classmethod
     def from_blocks(cls, qtype: int, n: int, k: int, blocks) -> "QuantLinear":
-        """From GGUF block bytes in host memory (n * k/32 blocks of 18 / 34 B, or
+        """From GGUF block bytes in host memory (n * k/32 blocks of 18 / 22 / 34 B, or
         n * k/256 blocks of 144 / 176 / 210 B for Q4_K / Q5_K / Q6_K; a dense F32 / F16 / BF16
         tensor's n * k elements)."""
         buf = np.ascontiguousarray(np.frombuffer(memoryview(blocks), dtype=np.uint8))
@@ -216,8 +217,8 @@ class QuantLinear:
             pass
 
     def __repr__(self) -> str:
-        name = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", F32: "F32",
-                F16: "F16", BF16: "BF16"}.get(self.qtype, str(self.qtype))
+        name = {Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K",
+                F32: "F32", F16: "F16", BF16: "BF16"}.get(self.qtype, str(self.qtype))
         return f"QuantLinear({name}, n={self.n}, k={self.k})"
 
 

@@ -1,4 +1,4 @@
-//! Rust bindings to `libunillm_hip.so`: GGUF quantized matmuls (Q4_0, Q8_0, Q4_K,
+//! Rust bindings to `libunillm_hip.so`: GGUF quantized matmuls (Q4_0, Q5_0, Q8_0, Q4_K,
 //! Q5_K, Q6_K) and KV-cache attention on an MI355X (gfx950).
 //!
 //! * [`sys`] is the C ABI of `include/unillm_hip.h`, one declaration per function.
@@ -47,6 +47,7 @@ pub mod sys {
 
     pub const UNILLM_QTYPE_Q4_0: c_int = 2;
     pub const UNILLM_QTYPE_Q8_0: c_int = 8;
+    pub const UNILLM_QTYPE_Q5_0: c_int = 6;
     pub const UNILLM_QTYPE_Q4_K: c_int = 12;
     pub const UNILLM_QTYPE_Q5_K: c_int = 13;
     pub const UNILLM_QTYPE_Q6_K: c_int = 14;
@@ -260,6 +261,7 @@ impl Drop for DeviceBuffer {
 #[allow(non_camel_case_types)]
 pub enum QType {
     Q4_0 = 2,
+    Q5_0 = 6,
     Q8_0 = 8,
     Q4_K = 12,
     Q5_K = 13,
@@ -274,6 +276,7 @@ impl QType {
     pub fn from_ggml(id: u32) -> Option<Self> {
         match id {
             2 => Some(Self::Q4_0),
+            6 => Some(Self::Q5_0),
             8 => Some(Self::Q8_0),
             12 => Some(Self::Q4_K),
             13 => Some(Self::Q5_K),
@@ -571,6 +574,7 @@ mod tests {
     #[test]
     fn qtype_ids_are_ggml_ids() {
         assert_eq!(QType::from_ggml(2), Some(QType::Q4_0));
+        assert_eq!(QType::from_ggml(6), Some(QType::Q5_0));
         assert_eq!(QType::from_ggml(8), Some(QType::Q8_0));
         assert_eq!(QType::from_ggml(12), Some(QType::Q4_K));
         assert_eq!(QType::from_ggml(13), Some(QType::Q5_K));

@@ -422,10 +422,14 @@ __device__ __forceinline__ void compute_chunk(const Chunk<QT, NB, R>& c, const X
 
 // Workgroup size: 1024 threads (128 VGPRs per lane) when the records and a
 // chunk fit that budget, else 512 (256 VGPRs).  Either way the launch puts
-// one workgroup on each CU, so the x digits are built once per CU.
+// one workgroup on each CU, so the x digits are built once per CU.  One block a
+// lane (k <= 2048) fits the budget up to four 128-bit records (M V <= 4): the
+// doubled waves hide more latency (Q4_0 m = 3, 4 at k2048 n14336: 9.26 -> 8.49 us a
+// call; Q8_0 m = 2 at k2048 n5632: 5.52 -> 5.38).  Two blocks at m = 2 (k4096)
+// measured mixed (n14336 -3 %, n4096 +3 %) and keep 512.
 template <int QT, int M, int NB>
 constexpr int gemv_threads() {
-    return M * NB * Payload<QT>::V <= 2 ? 1024 : 512;
+    return M * NB * Payload<QT>::V <= 2 || (NB == 1 && M * Payload<QT>::V <= 4) ? 1024 : 512;
 }
 
 // m_real <= M rows of x are used; rows m >= m_real repeat row m_real - 1 and
@@ -703,8 +707,9 @@ template <int QT, int M, int NB>
 hipError_t launch_nb(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st,
                      int epi, const NormArgs& norm) {
     constexpr int V = Payload<QT>::V;
-    constexpr int RMAX = NB * V >= 4 ? 1 : 4 / (NB * V);
     constexpr int THREADS = gemv_threads<QT, M, NB>();
+    // four rows a chunk at four tokens would spill in the 1024-thread budget
+    constexpr int RMAX = NB * V >= 4 ? 1 : M >= 4 && THREADS == 1024 ? 2 : 4 / (NB * V);
     constexpr int WAVES = THREADS / 64;
     int per_cu = 0;
     const size_t lds = (size_t)M * w.kb * kXWords * sizeof(uint32_t);

@@ -319,10 +319,13 @@ __device__ __forceinline__ void load_chunk(Chunk<QT, NB, R>& c, const uint8_t* _
 
 // Epilogue: y = sum (store), y += sum (the residual add, `add`), or with PAIR
 // y[m, L] = silu(gate) * up over the I logical rows (candle silu: v / (1 + e^-v)).
-template <int QT, int M, int NB, int R, bool PAIR = false>
+// KS (k split over a wave pair): the wave's half of each sum is added into the pair's
+// LDS slots ksum[j][m] instead, and the workgroup stores them after its last chunk.
+template <int QT, int M, int NB, int R, bool PAIR = false, bool KS = false>
 __device__ __forceinline__ void compute_chunk(const Chunk<QT, NB, R>& c, const XRegs<QT, M, NB>& xs,
                                               float* __restrict__ y, int w, int W, int j0,
-                                              int jcount, int N, int lane, int m_real, int add) {
+                                              int jcount, int N, int lane, int m_real, int add,
+                                              float* ksum = nullptr) {
     float part[M][R];
 #pragma unroll
     for (int m = 0; m < M; ++m)
@@ -398,7 +401,13 @@ __device__ __forceinline__ void compute_chunk(const Chunk<QT, NB, R>& c, const X
 #pragma unroll
         for (int r = 0; r < R; ++r) part[m][r] = wave_sum(part[m][r]);
     if (lane == 0) {
-        if constexpr (PAIR) {
+        if constexpr (KS) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (j0 + r < jcount)
+#pragma unroll
+                    for (int m = 0; m < M; ++m) atomicAdd(ksum + (j0 + r) * M + m, part[m][r]);
+        } else if constexpr (PAIR) {
             if (j0 < jcount)
 #pragma unroll
                 for (int m = 0; m < M; ++m)
@@ -447,25 +456,35 @@ constexpr int gemv_threads() {
 // XW: waves numbered across the workgroups (wave w of workgroup b is b + w grid), so
 // that the waves holding one row more than the others (a partial last round) spread
 // over every CU instead of filling the first CUs.
+// KS: the k range split over the two waves of a pair (waves 2 p and 2 p + 1 of a
+// workgroup): each takes NB blocks a lane of its half and the rows of "wave" p, so a
+// lane holds half the records and twice the waves fit a CU; the halves' sums meet in
+// LDS (after the x records: the workgroup's pairs x jmax rows x M floats) and are
+// stored after a workgroup barrier that follows every wave's last chunk.
 template <int QT, int M, int NB, int R, int THREADS, bool PAIR = false, bool NORM = false,
-          bool XW = false>
+          bool XW = false, bool KS = false>
 __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict__ base,
                                                        int64_t rb,
                                                        const float* __restrict__ x,
                                                        float* __restrict__ y, int N_rows, int KB,
                                                        int m_real, int add, NormArgs norm) {
     static_assert(!PAIR || R == 2, "the SwiGLU pair is one gate and one up row per chunk");
+    static_assert(!KS || (!PAIR && !NORM && !XW), "the k split takes the plain and add epilogues");
     constexpr int LR = PAIR ? 1 : R;  // logical rows per chunk
+    constexpr int KSF = KS ? 2 : 1;   // waves a row's k range is split over
     const int I = PAIR ? N_rows / 2 : 0;
     const int N = PAIR ? I : N_rows;  // logical rows (output columns)
     constexpr int WAVES = THREADS / 64;
-    constexpr int PASSES = (M * NB * 256 + THREADS - 1) / THREADS;  // quarter-blocks per thread
+    constexpr int RW = WAVES / KSF;  // row-owning waves (pairs with KS) per workgroup
+    constexpr int PASSES = (M * KSF * NB * 256 + THREADS - 1) / THREADS;  // quarter-blocks a thread
     extern __shared__ uint32_t xlds[];
     const int lane = threadIdx.x & 63;
+    const int half = KS ? (int)((threadIdx.x >> 6) & 1) : 0;  // KS: which half of k
     const int wave = __builtin_amdgcn_readfirstlane(
-        XW ? (int)(threadIdx.x >> 6) * (int)gridDim.x + (int)blockIdx.x
-           : (int)(blockIdx.x * WAVES + (threadIdx.x >> 6)));
-    const int waves = gridDim.x * WAVES;
+        XW   ? (int)(threadIdx.x >> 6) * (int)gridDim.x + (int)blockIdx.x
+        : KS ? (int)blockIdx.x * RW + (int)(threadIdx.x >> 7)
+             : (int)(blockIdx.x * WAVES + (threadIdx.x >> 6)));
+    const int waves = gridDim.x * RW;
     const int64_t K = (int64_t)KB * QK;
     // this wave's rows: wave, wave + waves, ... (counts differ by at most one);
     // wave-uniform, so every branch on them is a scalar branch
@@ -478,7 +497,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     uint32_t poff[NB], soff[NB], hoff[NB];  // this lane's byte offsets inside a row
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-        const int b = i * 64 + lane;
+        const int b = half * NB * 64 + i * 64 + lane;
         bval[i] = b < KB;
         bidx[i] = min(b, KB - 1);
         poff[i] = (uint32_t)bidx[i] * (16 * Payload<QT>::V);
@@ -515,6 +534,13 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
         order(v[p], *reinterpret_cast<const float4*>(xb + o0),
               *reinterpret_cast<const float4*>(xb + o1));
     }
+
+    // KS: the pairs' sum slots, zeroed before the records' barrier
+    const int jmax = (N + waves - 1) / waves;
+    float* const ksum_wg = reinterpret_cast<float*>(xlds + (size_t)M * KB * kXWords);
+    if constexpr (KS)
+        for (int i = threadIdx.x; i < RW * jmax * M; i += THREADS) ksum_wg[i] = 0.0f;
+    float* const ksum = ksum_wg + (KS ? (int)(threadIdx.x >> 7) : 0) * jmax * M;
 
     // gamma and beta of this thread's quarters (the norm), requested with x
     float gmv[NORM ? PASSES : 1][8], btv[NORM ? PASSES : 1][8];
@@ -658,20 +684,36 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     //    shared join would make the wait for chunk a cover chunk b as well).
     if (jcount > LR) {
         load_chunk<QT, NB, R, PAIR>(b, base, (uint32_t)rb, wrow, waves, LR, jlast, poff, soff, hoff, I);
-        compute_chunk<QT, M, NB, R, PAIR>(a, xs, y, wrow, waves, 0, jcount, N, lane, m_real, add);
-        compute_chunk<QT, M, NB, R, PAIR>(b, xs, y, wrow, waves, LR, jcount, N, lane, m_real, add);
+        compute_chunk<QT, M, NB, R, PAIR, KS>(a, xs, y, wrow, waves, 0, jcount, N, lane, m_real,
+                                              add, ksum);
+        compute_chunk<QT, M, NB, R, PAIR, KS>(b, xs, y, wrow, waves, LR, jcount, N, lane, m_real,
+                                              add, ksum);
         for (int j = 2 * LR; j < jcount; j += 2 * LR) {
             load_chunk<QT, NB, R, PAIR>(a, base, (uint32_t)rb, wrow, waves, j, jlast, poff, soff,
                                         hoff, I);
             load_chunk<QT, NB, R, PAIR>(b, base, (uint32_t)rb, wrow, waves, j + LR, jlast, poff,
                                         soff, hoff, I);
-            compute_chunk<QT, M, NB, R, PAIR>(a, xs, y, wrow, waves, j, jcount, N, lane, m_real,
-                                              add);
-            compute_chunk<QT, M, NB, R, PAIR>(b, xs, y, wrow, waves, j + LR, jcount, N, lane,
-                                              m_real, add);
+            compute_chunk<QT, M, NB, R, PAIR, KS>(a, xs, y, wrow, waves, j, jcount, N, lane,
+                                                  m_real, add, ksum);
+            compute_chunk<QT, M, NB, R, PAIR, KS>(b, xs, y, wrow, waves, j + LR, jcount, N, lane,
+                                                  m_real, add, ksum);
         }
     } else {
-        compute_chunk<QT, M, NB, R, PAIR>(a, xs, y, wrow, waves, 0, jcount, N, lane, m_real, add);
+        compute_chunk<QT, M, NB, R, PAIR, KS>(a, xs, y, wrow, waves, 0, jcount, N, lane, m_real,
+                                              add, ksum);
+    }
+    if constexpr (KS) {
+        // both halves of every pair are done: slot (pair p, row j, token m) -> y
+        __syncthreads();
+        for (int i = threadIdx.x; i < RW * jmax * M; i += THREADS) {
+            const int pl = i / (jmax * M), j = i / M % jmax, m = i % M;
+            const int pw = (int)blockIdx.x * RW + pl;
+            const int jc = pw < N ? (N - 1 - pw) / waves + 1 : 0;
+            if (j < jc && m < m_real) {
+                float* dst = y + (int64_t)m * N + pw + j * waves;
+                *dst = add ? *dst + ksum_wg[i] : ksum_wg[i];
+            }
+        }
     }
 }
 
@@ -753,12 +795,45 @@ hipError_t launch_nb(const QWeight& w, const float* x, int64_t m, float* y, hipS
     return launch_r<QT, M, NB, 1>(w, x, m, y, st, (int)waves, add, norm);
 }
 
+// Four tokens at two blocks a lane (k 2049 .. 4096, nibble codes): the k range split
+// over wave pairs (KS), so each lane holds one block's records and a workgroup of
+// 1024 threads fits a CU, as at k <= 2048.  One workgroup a CU, pairs as launch_nb
+// sizes waves.
+template <int QT, int M>
+hipError_t launch_ks(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st,
+                     int add) {
+    constexpr int THREADS = 1024, RW = THREADS / 128;  // row-owning pairs a workgroup
+    const int64_t cus = device_info().cu_count;
+    const int64_t want = std::max<int64_t>(w.n / 2, cus * RW);
+    const int64_t pairs = std::max<int64_t>(1, std::min<int64_t>({cus * RW, want, w.n}));
+    const int grid = (int)((pairs + RW - 1) / RW);
+    const int64_t jmax = (w.n + (int64_t)grid * RW - 1) / ((int64_t)grid * RW);
+    const size_t lds = (size_t)M * w.kb * kXWords * sizeof(uint32_t) +
+                       (size_t)RW * jmax * M * sizeof(float);
+    if (lds > (size_t)device_info().max_lds) return hipErrorInvalidValue;
+    if (debug_launch())
+        fprintf(stderr, "unillm gemv (k split): n=%lld kb=%lld m=%lld pairs=%lld rows=%lld\n",
+                (long long)w.n, (long long)w.kb, (long long)m, (long long)grid * RW,
+                (long long)jmax);
+    if (jmax > 2)
+        gemv_kernel<QT, M, 1, 2, THREADS, false, false, false, true><<<grid, THREADS, lds, st>>>(
+            w.base, w.row_bytes, x, y, (int)w.n, (int)w.kb, (int)m, add, NormArgs{});
+    else
+        gemv_kernel<QT, M, 1, 1, THREADS, false, false, false, true><<<grid, THREADS, lds, st>>>(
+            w.base, w.row_bytes, x, y, (int)w.n, (int)w.kb, (int)m, add, NormArgs{});
+    return hipGetLastError();
+}
+
 template <int QT, int M>
 hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st,
                     int epi, const NormArgs& norm) {
     switch ((int)((w.kb + 63) / 64)) {
         case 1: return launch_nb<QT, M, 1>(w, x, m, y, st, epi, norm);
-        case 2: return launch_nb<QT, M, 2>(w, x, m, y, st, epi, norm);
+        case 2:
+            if constexpr (M == 4 && Payload<QT>::V == 1)
+                if (epi != kEpiSwiglu && !norm.gamma)
+                    return launch_ks<QT, M>(w, x, m, y, st, epi == kEpiAdd);
+            return launch_nb<QT, M, 2>(w, x, m, y, st, epi, norm);
         case 3: if constexpr (M <= 2) return launch_nb<QT, M, 3>(w, x, m, y, st, epi, norm); break;
         case 4: if constexpr (M <= 2) return launch_nb<QT, M, 4>(w, x, m, y, st, epi, norm); break;
         case 5: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 5>(w, x, m, y, st, epi, norm); break;

@@ -795,10 +795,10 @@ hipError_t launch_nb(const QWeight& w, const float* x, int64_t m, float* y, hipS
     return launch_r<QT, M, NB, 1>(w, x, m, y, st, (int)waves, add, norm);
 }
 
-// Four tokens at two blocks a lane (k 2049 .. 4096, nibble codes): the k range split
-// over wave pairs (KS), so each lane holds one block's records and a workgroup of
-// 1024 threads fits a CU, as at k <= 2048.  One workgroup a CU, pairs as launch_nb
-// sizes waves.
+// Four tokens at two blocks a lane (k 2049 .. 4096): the k range split over wave pairs
+// (KS), so each lane holds one block's records and a workgroup of 1024 threads fits a
+// CU, as at k <= 2048 (Q6_K's header words would spill there: it keeps launch_nb).
+// One workgroup a CU, pairs as launch_nb sizes waves.
 template <int QT, int M>
 hipError_t launch_ks(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st,
                      int add) {
@@ -830,7 +830,7 @@ hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipSt
     switch ((int)((w.kb + 63) / 64)) {
         case 1: return launch_nb<QT, M, 1>(w, x, m, y, st, epi, norm);
         case 2:
-            if constexpr (M == 4 && Payload<QT>::V == 1)
+            if constexpr (M == 4 && QT != UNILLM_QTYPE_Q6_K)
                 if (epi != kEpiSwiglu && !norm.gamma)
                     return launch_ks<QT, M>(w, x, m, y, st, epi == kEpiAdd);
             return launch_nb<QT, M, 2>(w, x, m, y, st, epi, norm);

@@ -799,10 +799,12 @@ hipError_t launch_nb(const QWeight& w, const float* x, int64_t m, float* y, hipS
 // (KS), so each lane holds one block's records and a workgroup of 1024 threads fits a
 // CU, as at k <= 2048 (Q6_K's header words would spill there: it keeps launch_nb).
 // One workgroup a CU, pairs as launch_nb sizes waves.
-template <int QT, int M>
+template <int QT, int M, int NBH = 1>
 hipError_t launch_ks(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st,
                      int add) {
     constexpr int THREADS = 1024, RW = THREADS / 128;  // row-owning pairs a workgroup
+    constexpr int V = Payload<QT>::V;
+    constexpr int RMAX = NBH * V >= 4 ? 1 : M >= 4 ? 2 : 4 / (NBH * V);
     const int64_t cus = device_info().cu_count;
     const int64_t want = std::max<int64_t>(w.n / 2, cus * RW);
     const int64_t pairs = std::max<int64_t>(1, std::min<int64_t>({cus * RW, want, w.n}));
@@ -815,12 +817,19 @@ hipError_t launch_ks(const QWeight& w, const float* x, int64_t m, float* y, hipS
         fprintf(stderr, "unillm gemv (k split): n=%lld kb=%lld m=%lld pairs=%lld rows=%lld\n",
                 (long long)w.n, (long long)w.kb, (long long)m, (long long)grid * RW,
                 (long long)jmax);
-    if (jmax > 2)
-        gemv_kernel<QT, M, 1, 2, THREADS, false, false, false, true><<<grid, THREADS, lds, st>>>(
-            w.base, w.row_bytes, x, y, (int)w.n, (int)w.kb, (int)m, add, NormArgs{});
+    const NormArgs none{nullptr, nullptr, 0.f};
+    if (RMAX >= 4 && jmax > 4)
+        gemv_kernel<QT, M, NBH, RMAX, THREADS, false, false, false, true>
+            <<<grid, THREADS, lds, st>>>(w.base, w.row_bytes, x, y, (int)w.n, (int)w.kb, (int)m,
+                                         add, none);
+    else if (RMAX >= 2 && jmax > 2)
+        gemv_kernel<QT, M, NBH, (RMAX >= 2 ? 2 : 1), THREADS, false, false, false, true>
+            <<<grid, THREADS, lds, st>>>(w.base, w.row_bytes, x, y, (int)w.n, (int)w.kb, (int)m,
+                                         add, none);
     else
-        gemv_kernel<QT, M, 1, 1, THREADS, false, false, false, true><<<grid, THREADS, lds, st>>>(
-            w.base, w.row_bytes, x, y, (int)w.n, (int)w.kb, (int)m, add, NormArgs{});
+        gemv_kernel<QT, M, NBH, 1, THREADS, false, false, false, true>
+            <<<grid, THREADS, lds, st>>>(w.base, w.row_bytes, x, y, (int)w.n, (int)w.kb, (int)m,
+                                         add, none);
     return hipGetLastError();
 }
 

@@ -199,6 +199,32 @@ def test_gemv_partial_second_round(qtype, k, n):
     assert np.array_equal(ya.cpu().numpy(), y0 + y)
 
 
+@pytest.mark.parametrize("n", [393216, 393217])
+def test_gemv_k_split_many_rows(n):
+    # four tokens at k 4096 split k over wave pairs, each pair's row sums held in LDS
+    # beside the x records: 393216 rows (192 a pair over 2048 pairs) fill the 64 KiB a
+    # launch takes; one row more goes to one wave a row.  The weight repeats 3001
+    # distinct rows (a period no pair or wave count divides), so every row is checked.
+    m, k, period = 4, 4096, 3001
+    blocks, x = _case(Q4_0, m, period, k, seed=n)
+    rows = _dev(np.frombuffer(blocks, np.uint8).reshape(period, -1))
+    tiled = rows.repeat((n + period - 1) // period, 1)[:n].contiguous()
+    ql = QuantLinear.from_device_blocks(Q4_0, n, k, tiled.view(-1))
+    del rows, tiled
+    assert ql.select_path(m) == PATH_GEMV
+    ref = np.tile(oracle.qmatmul_f64(Q4_0, blocks, x, period, k),
+                  (1, (n + period - 1) // period))[:, :n]
+    xd = _dev(x)
+    print(f"gemv k split rows n={n}", flush=True)
+    y = ql.forward(xd).cpu().numpy()
+    assert np.all(np.abs(y - ref) <= 1e-4 * np.abs(ref).max())
+    y0 = oracle.normal(m * n, seed=5).reshape(m, n).astype(np.float32)
+    ya = _dev(y0)
+    ql.forward_add(xd, ya)
+    assert np.array_equal(ya.cpu().numpy(), y0 + y)
+    ql.close()
+
+
 @pytest.mark.parametrize("m", [4, 16, 64])
 @pytest.mark.parametrize("n", [4096, 14336])
 def test_baseline_batched_decode(m, n):

@@ -801,7 +801,8 @@ hipError_t launch_nb(const QWeight& w, const float* x, int64_t m, float* y, hipS
 // One workgroup a CU, pairs as launch_nb sizes waves.
 template <int QT, int M, int NBH = 1>
 hipError_t launch_ks(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st,
-                     int add) {
+                     int epi, const NormArgs& norm) {
+    const int add = epi == kEpiAdd;
     constexpr int THREADS = 1024, RW = THREADS / 128;  // row-owning pairs a workgroup
     constexpr int V = Payload<QT>::V;
     constexpr int RMAX = NBH * V >= 4 ? 1 : M >= 4 ? 2 : 4 / (NBH * V);
@@ -812,7 +813,9 @@ hipError_t launch_ks(const QWeight& w, const float* x, int64_t m, float* y, hipS
     const int64_t jmax = (w.n + (int64_t)grid * RW - 1) / ((int64_t)grid * RW);
     const size_t lds = (size_t)M * w.kb * kXWords * sizeof(uint32_t) +
                        (size_t)RW * jmax * M * sizeof(float);
-    if (lds > (size_t)device_info().max_lds) return hipErrorInvalidValue;
+    // x records and the pairs' sum slots past the 64 KiB a launch takes without a raised
+    // dynamic-LDS limit (past 393216 rows at k 4096): one wave a row, as for the other shapes
+    if (lds > 65536) return launch_nb<QT, M, 2 * NBH>(w, x, m, y, st, epi, norm);
     if (debug_launch())
         fprintf(stderr, "unillm gemv (k split): n=%lld kb=%lld m=%lld pairs=%lld rows=%lld\n",
                 (long long)w.n, (long long)w.kb, (long long)m, (long long)grid * RW,
@@ -841,7 +844,7 @@ hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipSt
         case 2:
             if constexpr (M == 4 && QT != UNILLM_QTYPE_Q6_K)
                 if (epi != kEpiSwiglu && !norm.gamma)
-                    return launch_ks<QT, M>(w, x, m, y, st, epi == kEpiAdd);
+                    return launch_ks<QT, M>(w, x, m, y, st, epi, norm);
             return launch_nb<QT, M, 2>(w, x, m, y, st, epi, norm);
         case 3: if constexpr (M <= 2) return launch_nb<QT, M, 3>(w, x, m, y, st, epi, norm); break;
         case 4: if constexpr (M <= 2) return launch_nb<QT, M, 4>(w, x, m, y, st, epi, norm); break;

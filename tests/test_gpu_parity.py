@@ -199,11 +199,31 @@ def test_gemv_partial_second_round(qtype, k, n):
     assert np.array_equal(ya.cpu().numpy(), y0 + y)
 
 
+@pytest.mark.parametrize("k,n", [(8224, 300), (11008, 4096), (12288, 2049)])
+def test_gemv_q8_0_one_token_deep_k(k, n):
+    # Q8_0 at one token past k 8192 (five or six blocks a lane): the k split over wave
+    # pairs, three blocks a lane a half; every row against the oracle, and the add
+    blocks, x = _case(Q8_0, 1, n, k, seed=k + 5 * n)
+    ql = QuantLinear.from_blocks(Q8_0, n, k, blocks)
+    assert ql.select_path(1) == PATH_GEMV
+    ref = oracle.qmatmul_f64(Q8_0, blocks, x, n, k)
+    xd = _dev(x)
+    print(f"gemv q8_0 deep k={k} n={n}", flush=True)
+    y = ql.forward(xd).cpu().numpy()
+    assert np.all(np.abs(y - ref) <= 1e-4 * np.abs(ref).max())
+    y0 = oracle.normal(n, seed=n + 1).reshape(1, n).astype(np.float32)
+    ya = _dev(y0)
+    ql.forward_add(xd, ya)
+    assert np.array_equal(ya.cpu().numpy(), y0 + y)
+    dec = ql.forward(xd, path=PATH_DECODE_MFMA).cpu().numpy()
+    assert oracle.normwise_error(dec, ref) < 1e-3
+
+
 @pytest.mark.parametrize("n", [393216, 393217])
 def test_gemv_k_split_many_rows(n):
     # four tokens at k 4096 split k over wave pairs, each pair's row sums held in LDS
     # beside the x records: 393216 rows (192 a pair over 2048 pairs) fill the 64 KiB a
-    # launch takes; one row more goes to one wave a row.  The weight repeats 3001
+    # launch takes; one row more takes more workgroups than CUs.  The weight repeats 3001
     # distinct rows (a period no pair or wave count divides), so every row is checked.
     m, k, period = 4, 4096, 3001
     blocks, x = _case(Q4_0, m, period, k, seed=n)

@@ -58,6 +58,7 @@ def test_q5_0_reports_its_type_and_keeps_q8_0_bytes():
 @pytest.mark.parametrize("m,n,k,path", [(1, 300, 4096, PATH_GEMV), (3, 129, 2048, PATH_GEMV),
                                         (4, 2049, 4096, PATH_GEMV),
                                         (1, 4096, 11008, PATH_DECODE_MFMA),
+                                        (1, 4096, 11008, PATH_GEMV),
                                         (16, 1000, 4096, PATH_DECODE_MFMA),
                                         (64, 512, 2048, PATH_DECODE_MFMA),
                                         (130, 512, 4096, PATH_PREFILL_MFMA),

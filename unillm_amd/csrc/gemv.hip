@@ -809,13 +809,16 @@ hipError_t launch_ks(const QWeight& w, const float* x, int64_t m, float* y, hipS
     const int64_t cus = device_info().cu_count;
     const int64_t want = std::max<int64_t>(w.n / 2, cus * RW);
     const int64_t pairs = std::max<int64_t>(1, std::min<int64_t>({cus * RW, want, w.n}));
-    const int grid = (int)((pairs + RW - 1) / RW);
+    // the x records and the pairs' sum slots stay within the 64 KiB a launch takes
+    // without a raised dynamic-LDS limit: past jcap rows a pair (393216 rows at four
+    // tokens and k 4096), more workgroups than CUs
+    const size_t xbytes = (size_t)M * w.kb * kXWords * sizeof(uint32_t);
+    const int64_t jcap = (int64_t)((65536 - xbytes) / ((size_t)RW * M * sizeof(float)));
+    const int64_t grid64 = std::max((pairs + RW - 1) / RW, (w.n + RW * jcap - 1) / (RW * jcap));
+    if (grid64 > INT32_MAX) return hipErrorInvalidValue;
+    const int grid = (int)grid64;
     const int64_t jmax = (w.n + (int64_t)grid * RW - 1) / ((int64_t)grid * RW);
-    const size_t lds = (size_t)M * w.kb * kXWords * sizeof(uint32_t) +
-                       (size_t)RW * jmax * M * sizeof(float);
-    // x records and the pairs' sum slots past the 64 KiB a launch takes without a raised
-    // dynamic-LDS limit (past 393216 rows at k 4096): one wave a row, as for the other shapes
-    if (lds > 65536) return launch_nb<QT, M, 2 * NBH>(w, x, m, y, st, epi, norm);
+    const size_t lds = xbytes + (size_t)RW * jmax * M * sizeof(float);
     if (debug_launch())
         fprintf(stderr, "unillm gemv (k split): n=%lld kb=%lld m=%lld pairs=%lld rows=%lld\n",
                 (long long)w.n, (long long)w.kb, (long long)m, (long long)grid * RW,
@@ -848,8 +851,18 @@ hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipSt
             return launch_nb<QT, M, 2>(w, x, m, y, st, epi, norm);
         case 3: if constexpr (M <= 2) return launch_nb<QT, M, 3>(w, x, m, y, st, epi, norm); break;
         case 4: if constexpr (M <= 2) return launch_nb<QT, M, 4>(w, x, m, y, st, epi, norm); break;
-        case 5: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 5>(w, x, m, y, st, epi, norm); break;
-        case 6: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 6>(w, x, m, y, st, epi, norm); break;
+        // Q8_0's frame (Q8_0, Q5_0) at one token, k 8193 .. 12288: the k split over wave
+        // pairs, three blocks a lane a half (the K-quants' header words would spill)
+        case 5:
+            if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 5>(w, x, m, y, st, epi, norm);
+            if constexpr (M == 1 && QT == UNILLM_QTYPE_Q8_0)
+                if (epi != kEpiSwiglu && !norm.gamma) return launch_ks<QT, M, 3>(w, x, m, y, st, epi, norm);
+            break;
+        case 6:
+            if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 6>(w, x, m, y, st, epi, norm);
+            if constexpr (M == 1 && QT == UNILLM_QTYPE_Q8_0)
+                if (epi != kEpiSwiglu && !norm.gamma) return launch_ks<QT, M, 3>(w, x, m, y, st, epi, norm);
+            break;
         case 7: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 7>(w, x, m, y, st, epi, norm); break;
         default: break;
     }
@@ -860,10 +873,11 @@ hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipSt
 
 // Largest K (in blocks) the GEMV path takes at m rows, set by the registers
 // two chunks of NB blocks per lane need (NB = ceil(KB / 64)): Q4_0 up to
-// NB = 7 at one row (K = 14336), 4 at two, 2 at four; Q8_0 payloads are twice
-// as wide, so it stops at NB = 4.  M * KB <= 512 also bounds the LDS (40 KiB).
+// NB = 7 at one row (K = 14336), 4 at two, 2 at four; byte-code payloads are twice
+// as wide, so one wave a row stops at NB = 4, and Q8_0's frame takes NB = 5, 6 at
+// one row (K = 12288) with the k split over wave pairs.  M * KB <= 512 also bounds the LDS (40 KiB).
 int64_t gemv_max_kb(int64_t m, int qtype) {
-    if (m <= 1) return byte_codes(qtype) ? 256 : 448;
+    if (m <= 1) return qtype == UNILLM_QTYPE_Q8_0 ? 384 : byte_codes(qtype) ? 256 : 448;
     if (m <= 2) return 256;
     return 128;
 }

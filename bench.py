@@ -319,6 +319,18 @@ def extra_configs(torch, QuantLinear, gen, stream, only):
                                            "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 3),
                                            "us": round(ms * 1e3, 2), "copies": len(ws)}
         del ws
+        # a Q8_0 down projection at Llama-2-7B's shape (past k 8192: the GEMV's k split)
+        n, k = 4096, 11008
+        ws = rotate(Q8_0, n, k)
+        x = torch.empty(1, k, device="cuda").normal_(generator=gen)
+        y = torch.empty(1, n, device="cuda")
+        ms = timed(ws, x, y)
+        b = wbytes(Q8_0, n, k) + 4 * k + 4 * n
+        res["q8_0_gemv_m1_k11008_n4096"] = {"GB/s": round(b / ms / 1e6, 1),
+                                            "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 3),
+                                            "us": round(ms * 1e3, 2), "copies": len(ws),
+                                            "path": ws[0].select_path(1)}
+        del ws
     if "batched" in want:
         for n in (4096, 14336):
             ws = rotate(Q4_0, n, 4096, max_copies=64)

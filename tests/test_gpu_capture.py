@@ -7,6 +7,8 @@ replay correctly, also after later eager calls have grown the buffer again.
 Replays are checked against eager calls, with eager work and synchronisations
 between them.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -14,7 +16,7 @@ import torch
 import oracle
 from oracle import Q4_0
 from unillm_amd import (PATH_DECODE_MFMA, PATH_GEMV, PATH_PREFILL_MFMA, HipError, KvCache,
-                        QuantLinear)
+                        QuantLinear, _capi)
 
 pytestmark = pytest.mark.gpu
 
@@ -31,7 +33,11 @@ def _x(m, k, seed):
 
 def test_capture_with_cold_workspace_fails_cleanly():
     _, ql = _weight(512, 1024, seed=11)
-    s = torch.cuda.Stream()  # a fresh stream: no workspace yet
+    # a stream no call has used, so it has no workspace yet (torch's pooled streams
+    # may carry one from earlier tests)
+    h = ctypes.c_void_p()
+    _capi.check(_capi.lib().unillm_hip_stream_create(ctypes.byref(h)))
+    s = torch.cuda.ExternalStream(h.value)
     x = _x(16, 1024, seed=12)
     y = torch.empty(16, 512, device="cuda")
     g = torch.cuda.CUDAGraph()

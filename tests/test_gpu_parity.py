@@ -158,8 +158,10 @@ def test_auto_path_selection():
     assert ql.select_path(5) == PATH_DECODE_MFMA
     assert ql.select_path(64) == PATH_DECODE_MFMA
     big = QuantLinear.from_blocks(Q4_0, 16, 11008, _case(Q4_0, 1, 16, 11008, seed=1)[0])
-    # 344 blocks per row: the x digits fit the registers at m = 1 only
-    assert big.select_path(1) == PATH_GEMV and big.select_path(2) == PATH_DECODE_MFMA
+    # 344 blocks per row: the x digits fit the registers at m = 1, and at m = 2 with k
+    # split over wave pairs; not at m = 3
+    assert big.select_path(1) == PATH_GEMV and big.select_path(2) == PATH_GEMV
+    assert big.select_path(3) == PATH_DECODE_MFMA
     assert ql.select_path(65) == PATH_PREFILL_MFMA
 
 
@@ -367,12 +369,12 @@ def test_prefill_short_deep_split(qtype, m, k, n):
                                              (Q4_0, 16, 4096, PATH_DECODE_MFMA),
                                              (Q8_0, 16, 11008, PATH_DECODE_MFMA),
                                              (Q4_0, 64, 4096, PATH_DECODE_MFMA),
-                                             (Q4_0, 2, 11008, PATH_DECODE_MFMA)])
+                                             (Q4_0, 3, 11008, PATH_DECODE_MFMA)])
 def test_rows_of_any_magnitude(qtype, m, k, path):
     # f16 operands with a power-of-two scale per row of x (prefill) or per row and k
     # slice (batched decode): rows far beyond the f16 range (|x| ~ 1e6 > 65504), rows
     # deep in its subnormals (~1e-7), an all-zero row and unit rows side by side, each
-    # as accurate as a unit row alone.  (Q4_0, 2, 11008): the down projection at m = 2,
+    # as accurate as a unit row alone.  (Q4_0, 3, 11008): the down projection at m = 3,
     # which auto-routes here (past the GEMV's k at that m)
     n = 256
     blocks, x = _case(qtype, m, n, k, seed=91 + m)

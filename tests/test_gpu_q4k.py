@@ -73,7 +73,7 @@ def _gemv_case(m, n, k, seed, scale=1.0):
 
 @pytest.mark.parametrize("m,n,k", [(1, 37, 256), (1, 300, 4096), (2, 300, 4096), (3, 129, 2048),
                                    (4, 257, 4096), (1, 4096, 11008), (1, 12288, 4096),
-                                   (1, 512, 14336), (2, 512, 8192)])
+                                   (1, 512, 14336), (2, 512, 8192), (2, 300, 11008)])
 def test_q4k_gemv_parity(m, n, k):
     blocks, x = _gemv_case(m, n, k, seed=7 * n + k)
     ql = QuantLinear.from_blocks(Q4_K, n, k, blocks)

@@ -84,7 +84,7 @@ def _case(m, n, k, seed, scale=1.0):
 
 @pytest.mark.parametrize("m,n,k", [(1, 37, 256), (1, 300, 4096), (2, 300, 4096), (3, 129, 2048),
                                    (4, 257, 4096), (1, 4096, 4096), (1, 12288, 4096),
-                                   (1, 5632, 2048), (2, 512, 2048)])
+                                   (1, 5632, 2048), (2, 512, 2048), (2, 300, 11008)])
 def test_q5k_gemv_parity(m, n, k):
     blocks, x = _case(m, n, k, seed=7 * n + k)
     ql = QuantLinear.from_blocks(Q5_K, n, k, blocks)

@@ -64,7 +64,8 @@ def _check(m, n, k, path, bar, seed):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 37, 256), (1, 300, 4096), (2, 300, 4096), (3, 129, 2048),
-                                   (4, 257, 4096), (1, 32000, 4096), (1, 512, 8192)])
+                                   (4, 257, 4096), (1, 32000, 4096), (1, 512, 8192),
+                                   (2, 300, 11008)])
 def test_q6k_gemv_parity(m, n, k):
     _check(m, n, k, PATH_GEMV, 1e-3, seed=7 * n + k + m)
 

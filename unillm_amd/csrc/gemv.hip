@@ -799,11 +799,11 @@ hipError_t launch_nb(const QWeight& w, const float* x, int64_t m, float* y, hipS
 // (KS), so each lane holds one block's records and a workgroup of 1024 threads fits a
 // CU, as at k <= 2048 (Q6_K's header words would spill there: it keeps launch_nb).
 // One workgroup a CU, pairs as launch_nb sizes waves.
-template <int QT, int M, int NBH = 1>
+template <int QT, int M, int NBH = 1, int THREADS = 1024>
 hipError_t launch_ks(const QWeight& w, const float* x, int64_t m, float* y, hipStream_t st,
                      int epi, const NormArgs& norm) {
     const int add = epi == kEpiAdd;
-    constexpr int THREADS = 1024, RW = THREADS / 128;  // row-owning pairs a workgroup
+    constexpr int RW = THREADS / 128;  // row-owning pairs a workgroup
     constexpr int V = Payload<QT>::V;
     constexpr int RMAX = NBH * V >= 4 ? 1 : M >= 4 ? 2 : 4 / (NBH * V);
     const int64_t cus = device_info().cu_count;
@@ -851,17 +851,22 @@ hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipSt
             return launch_nb<QT, M, 2>(w, x, m, y, st, epi, norm);
         case 3: if constexpr (M <= 2) return launch_nb<QT, M, 3>(w, x, m, y, st, epi, norm); break;
         case 4: if constexpr (M <= 2) return launch_nb<QT, M, 4>(w, x, m, y, st, epi, norm); break;
-        // Q8_0's frame (Q8_0, Q5_0) at one token, k 8193 .. 12288: the k split over wave
-        // pairs, three blocks a lane a half (the K-quants' header words would spill)
+        // k 8193 .. 12288 at one token for Q8_0's frame (Q8_0, Q5_0; the K-quants' header
+        // words would spill at 1024 threads) and at two tokens for every type (512
+        // threads): the k split over wave pairs, three blocks a lane a half
         case 5:
             if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 5>(w, x, m, y, st, epi, norm);
             if constexpr (M == 1 && QT == UNILLM_QTYPE_Q8_0)
                 if (epi != kEpiSwiglu && !norm.gamma) return launch_ks<QT, M, 3>(w, x, m, y, st, epi, norm);
+            if constexpr (M == 2)
+                if (epi != kEpiSwiglu && !norm.gamma) return launch_ks<QT, M, 3, 512>(w, x, m, y, st, epi, norm);
             break;
         case 6:
             if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 6>(w, x, m, y, st, epi, norm);
             if constexpr (M == 1 && QT == UNILLM_QTYPE_Q8_0)
                 if (epi != kEpiSwiglu && !norm.gamma) return launch_ks<QT, M, 3>(w, x, m, y, st, epi, norm);
+            if constexpr (M == 2)
+                if (epi != kEpiSwiglu && !norm.gamma) return launch_ks<QT, M, 3, 512>(w, x, m, y, st, epi, norm);
             break;
         case 7: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 7>(w, x, m, y, st, epi, norm); break;
         default: break;
@@ -874,11 +879,12 @@ hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipSt
 // Largest K (in blocks) the GEMV path takes at m rows, set by the registers
 // two chunks of NB blocks per lane need (NB = ceil(KB / 64)): Q4_0 up to
 // NB = 7 at one row (K = 14336), 4 at two, 2 at four; byte-code payloads are twice
-// as wide, so one wave a row stops at NB = 4, and Q8_0's frame takes NB = 5, 6 at
-// one row (K = 12288) with the k split over wave pairs.  M * KB <= 512 also bounds the LDS (40 KiB).
+// as wide, so one wave a row stops at NB = 4 at one row.  The k split over wave
+// pairs (three blocks a lane a half) takes NB = 5, 6 (K = 12288) for Q8_0's frame at
+// one row and for every type at two.  M * KB <= 512 also bounds the LDS (40 KiB).
 int64_t gemv_max_kb(int64_t m, int qtype) {
     if (m <= 1) return qtype == UNILLM_QTYPE_Q8_0 ? 384 : byte_codes(qtype) ? 256 : 448;
-    if (m <= 2) return 256;
+    if (m <= 2) return 384;
     return 128;
 }
 

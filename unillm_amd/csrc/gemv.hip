@@ -813,6 +813,7 @@ hipError_t launch_ks(const QWeight& w, const float* x, int64_t m, float* y, hipS
     // without a raised dynamic-LDS limit: past jcap rows a pair (393216 rows at four
     // tokens and k 4096), more workgroups than CUs
     const size_t xbytes = (size_t)M * w.kb * kXWords * sizeof(uint32_t);
+    if (xbytes + (size_t)RW * M * sizeof(float) > 65536) return hipErrorInvalidValue;
     const int64_t jcap = (int64_t)((65536 - xbytes) / ((size_t)RW * M * sizeof(float)));
     const int64_t grid64 = std::max((pairs + RW - 1) / RW, (w.n + RW * jcap - 1) / (RW * jcap));
     if (grid64 > INT32_MAX) return hipErrorInvalidValue;
@@ -881,7 +882,8 @@ hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipSt
 // NB = 7 at one row (K = 14336), 4 at two, 2 at four; byte-code payloads are twice
 // as wide, so one wave a row stops at NB = 4 at one row.  The k split over wave
 // pairs (three blocks a lane a half) takes NB = 5, 6 (K = 12288) for Q8_0's frame at
-// one row and for every type at two.  M * KB <= 512 also bounds the LDS (40 KiB).
+// one row and for every type at two.  M * KB <= 768 also bounds the x records in LDS
+// (60 KiB).
 int64_t gemv_max_kb(int64_t m, int qtype) {
     if (m <= 1) return qtype == UNILLM_QTYPE_Q8_0 ? 384 : byte_codes(qtype) ? 256 : 448;
     if (m <= 2) return 384;

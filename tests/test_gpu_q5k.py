@@ -96,16 +96,27 @@ def test_q5k_gemv_parity(m, n, k):
 
 
 def test_q5k_gemv_limits_and_auto_path():
-    # byte codes: the GEMV takes k <= 8192 at one row, like Q8_0; longer rows go
-    # to the batched decode
-    ql = QuantLinear.from_blocks(Q5_K, 64, 11008, oracle.random_q5_k(64, 11008, seed=5))
+    # byte codes: the GEMV takes k <= 12288 at one row (past 8192 with k split over
+    # wave pairs, the down projection's k 11008 among them), like Q8_0; longer rows
+    # go to the batched decode
+    ql = QuantLinear.from_blocks(Q5_K, 64, 14336, oracle.random_q5_k(64, 14336, seed=5))
     assert ql.select_path(1) == PATH_DECODE_MFMA
     with pytest.raises(HipError, match="GEMV path"):
-        ql.forward(torch.zeros(1, 11008, device="cuda"), path=PATH_GEMV)
+        ql.forward(torch.zeros(1, 14336, device="cuda"), path=PATH_GEMV)
     m, n, k = 1, 300, 11008
     blocks, x = _case(m, n, k, seed=9)
-    y = QuantLinear.from_blocks(Q5_K, n, k, blocks).forward(_dev(x))
-    assert oracle.normwise_error(y.cpu().numpy(), oracle.qmatmul_f64(Q5_K, blocks, x, n, k)) < 1e-3
+    ql = QuantLinear.from_blocks(Q5_K, n, k, blocks)
+    assert ql.select_path(1) == PATH_GEMV
+    ref = oracle.qmatmul_f64(Q5_K, blocks, x, n, k)
+    xd = _dev(x)
+    y = ql.forward(xd).cpu().numpy()
+    assert oracle.normwise_error(y, ref) < 1e-3
+    y0 = oracle.normal(n, seed=3).reshape(1, n).astype(np.float32)
+    ya = _dev(y0)
+    ql.forward_add(xd, ya)
+    assert np.array_equal(ya.cpu().numpy(), y0 + y)
+    y = ql.forward(xd, path=PATH_DECODE_MFMA).cpu().numpy()
+    assert oracle.normwise_error(y, ref) < 1e-3
 
 
 def test_q5k_gemv_x_range_and_zero_mins():

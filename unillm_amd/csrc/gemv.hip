@@ -852,13 +852,16 @@ hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipSt
             return launch_nb<QT, M, 2>(w, x, m, y, st, epi, norm);
         case 3: if constexpr (M <= 2) return launch_nb<QT, M, 3>(w, x, m, y, st, epi, norm); break;
         case 4: if constexpr (M <= 2) return launch_nb<QT, M, 4>(w, x, m, y, st, epi, norm); break;
-        // k 8193 .. 12288 at one token for Q8_0's frame (Q8_0, Q5_0; the K-quants' header
-        // words would spill at 1024 threads) and at two tokens for every type (512
-        // threads): the k split over wave pairs, three blocks a lane a half
+        // k 8193 .. 12288 at one token for the byte codes (1024 threads for Q8_0's frame,
+        // Q8_0 and Q5_0; 512 for Q5_K and Q6_K, whose header words would spill at 1024)
+        // and at two tokens for every type (512 threads): the k split over wave pairs,
+        // three blocks a lane a half
         case 5:
             if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 5>(w, x, m, y, st, epi, norm);
             if constexpr (M == 1 && QT == UNILLM_QTYPE_Q8_0)
                 if (epi != kEpiSwiglu && !norm.gamma) return launch_ks<QT, M, 3>(w, x, m, y, st, epi, norm);
+            if constexpr (M == 1 && kByteCodes<QT> && QT != UNILLM_QTYPE_Q8_0)
+                if (epi != kEpiSwiglu && !norm.gamma) return launch_ks<QT, M, 3, 512>(w, x, m, y, st, epi, norm);
             if constexpr (M == 2)
                 if (epi != kEpiSwiglu && !norm.gamma) return launch_ks<QT, M, 3, 512>(w, x, m, y, st, epi, norm);
             break;
@@ -866,6 +869,8 @@ hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipSt
             if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 6>(w, x, m, y, st, epi, norm);
             if constexpr (M == 1 && QT == UNILLM_QTYPE_Q8_0)
                 if (epi != kEpiSwiglu && !norm.gamma) return launch_ks<QT, M, 3>(w, x, m, y, st, epi, norm);
+            if constexpr (M == 1 && kByteCodes<QT> && QT != UNILLM_QTYPE_Q8_0)
+                if (epi != kEpiSwiglu && !norm.gamma) return launch_ks<QT, M, 3, 512>(w, x, m, y, st, epi, norm);
             if constexpr (M == 2)
                 if (epi != kEpiSwiglu && !norm.gamma) return launch_ks<QT, M, 3, 512>(w, x, m, y, st, epi, norm);
             break;
@@ -881,11 +886,11 @@ hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipSt
 // two chunks of NB blocks per lane need (NB = ceil(KB / 64)): Q4_0 up to
 // NB = 7 at one row (K = 14336), 4 at two, 2 at four; byte-code payloads are twice
 // as wide, so one wave a row stops at NB = 4 at one row.  The k split over wave
-// pairs (three blocks a lane a half) takes NB = 5, 6 (K = 12288) for Q8_0's frame at
-// one row and for every type at two.  M * KB <= 768 also bounds the x records in LDS
+// pairs (three blocks a lane a half) takes NB = 5, 6 (K = 12288) for the byte codes
+// at one row and for every type at two.  M * KB <= 768 also bounds the x records in LDS
 // (60 KiB).
 int64_t gemv_max_kb(int64_t m, int qtype) {
-    if (m <= 1) return qtype == UNILLM_QTYPE_Q8_0 ? 384 : byte_codes(qtype) ? 256 : 448;
+    if (m <= 1) return byte_codes(qtype) ? 384 : 448;
     if (m <= 2) return 384;
     return 128;
 }

@@ -201,10 +201,11 @@ def test_gemv_partial_second_round(qtype, k, n):
     assert np.array_equal(ya.cpu().numpy(), y0 + y)
 
 
-@pytest.mark.parametrize("k,n", [(8224, 300), (11008, 4096), (12288, 2049)])
+@pytest.mark.parametrize("k,n", [(8224, 300), (11008, 4096), (12288, 2049), (14336, 4096),
+                                 (16384, 300)])
 def test_gemv_q8_0_one_token_deep_k(k, n):
-    # Q8_0 at one token past k 8192 (five or six blocks a lane): the k split over wave
-    # pairs, three blocks a lane a half; every row against the oracle, and the add
+    # Q8_0 at one token past k 8192 (five to eight blocks a lane): the k split over wave
+    # pairs, three or four blocks a lane a half; every row against the oracle, and the add
     blocks, x = _case(Q8_0, 1, n, k, seed=k + 5 * n)
     ql = QuantLinear.from_blocks(Q8_0, n, k, blocks)
     assert ql.select_path(1) == PATH_GEMV

@@ -96,14 +96,18 @@ def test_q5k_gemv_parity(m, n, k):
 
 
 def test_q5k_gemv_limits_and_auto_path():
-    # byte codes: the GEMV takes k <= 12288 at one row (past 8192 with k split over
-    # wave pairs, the down projection's k 11008 among them), like Q8_0; longer rows
-    # go to the batched decode
-    ql = QuantLinear.from_blocks(Q5_K, 64, 14336, oracle.random_q5_k(64, 14336, seed=5))
+    # byte codes: the GEMV takes k <= 16384 at one row (past 8192 with k split over
+    # wave pairs, the down projections' k 11008 and 14336 among them), like Q8_0;
+    # longer rows go to the batched decode
+    ql = QuantLinear.from_blocks(Q5_K, 64, 16640, oracle.random_q5_k(64, 16640, seed=5))
     assert ql.select_path(1) == PATH_DECODE_MFMA
     with pytest.raises(HipError, match="GEMV path"):
-        ql.forward(torch.zeros(1, 14336, device="cuda"), path=PATH_GEMV)
-    m, n, k = 1, 300, 11008
+        ql.forward(torch.zeros(1, 16640, device="cuda"), path=PATH_GEMV)
+    _gemv_deep_k(1, 300, 11008)
+    _gemv_deep_k(1, 257, 14336)
+
+
+def _gemv_deep_k(m, n, k):
     blocks, x = _case(m, n, k, seed=9)
     ql = QuantLinear.from_blocks(Q5_K, n, k, blocks)
     assert ql.select_path(1) == PATH_GEMV

@@ -65,15 +65,16 @@ def _check(m, n, k, path, bar, seed):
 
 @pytest.mark.parametrize("m,n,k", [(1, 37, 256), (1, 300, 4096), (2, 300, 4096), (3, 129, 2048),
                                    (4, 257, 4096), (1, 32000, 4096), (1, 512, 8192),
-                                   (2, 300, 11008), (1, 300, 11008), (1, 2049, 12288)])
+                                   (2, 300, 11008), (1, 300, 11008), (1, 2049, 12288),
+                                   (1, 300, 14336), (1, 129, 16384)])
 def test_q6k_gemv_parity(m, n, k):
     _check(m, n, k, PATH_GEMV, 1e-3, seed=7 * n + k + m)
 
 
 @pytest.mark.parametrize("m,n,k", [(5, 257, 256), (16, 1024, 4096), (33, 129, 2048),
-                                   (64, 512, 4096), (16, 257, 11008), (1, 512, 14336)])
+                                   (64, 512, 4096), (16, 257, 11008), (1, 512, 16640)])
 def test_q6k_decode_parity(m, n, k):
-    # (1, 512, 14336): k beyond the GEMV's reach at m = 1 (ffn_down) -> batched decode
+    # (1, 512, 16640): k beyond the GEMV's reach at m = 1 -> batched decode
     _check(m, n, k, PATH_DECODE_MFMA, 1e-3, seed=5 * m + n + k)
 
 

@@ -874,7 +874,14 @@ hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipSt
             if constexpr (M == 2)
                 if (epi != kEpiSwiglu && !norm.gamma) return launch_ks<QT, M, 3, 512>(w, x, m, y, st, epi, norm);
             break;
-        case 7: if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 7>(w, x, m, y, st, epi, norm); break;
+        case 7:
+            if constexpr (M == 1 && !kByteCodes<QT>) return launch_nb<QT, M, 7>(w, x, m, y, st, epi, norm);
+            [[fallthrough]];
+        case 8:
+            // the byte codes at one token, k 12289 .. 16384: four blocks a lane a half
+            if constexpr (M == 1 && kByteCodes<QT>)
+                if (epi != kEpiSwiglu && !norm.gamma) return launch_ks<QT, M, 4, 512>(w, x, m, y, st, epi, norm);
+            break;
         default: break;
     }
     return hipErrorInvalidValue;
@@ -886,11 +893,11 @@ hipError_t launch_m(const QWeight& w, const float* x, int64_t m, float* y, hipSt
 // two chunks of NB blocks per lane need (NB = ceil(KB / 64)): Q4_0 up to
 // NB = 7 at one row (K = 14336), 4 at two, 2 at four; byte-code payloads are twice
 // as wide, so one wave a row stops at NB = 4 at one row.  The k split over wave
-// pairs (three blocks a lane a half) takes NB = 5, 6 (K = 12288) for the byte codes
-// at one row and for every type at two.  M * KB <= 768 also bounds the x records in LDS
+// pairs takes the byte codes at one row up to NB = 8 (K = 16384; three or four
+// blocks a lane a half) and every type at two rows up to NB = 6 (K = 12288).  M * KB <= 768 also bounds the x records in LDS
 // (60 KiB).
 int64_t gemv_max_kb(int64_t m, int qtype) {
-    if (m <= 1) return byte_codes(qtype) ? 384 : 448;
+    if (m <= 1) return byte_codes(qtype) ? 512 : 448;
     if (m <= 2) return 384;
     return 128;
 }

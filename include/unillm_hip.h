@@ -68,6 +68,10 @@ extern "C" {
 
 /* Kernel path for unillm_hip_qmatmul_path (AUTO is what qmatmul uses). */
 #define UNILLM_PATH_AUTO 0
+/* GEMV, m <= 4, k up to: m = 1 14336 (Q4_0, Q4_K) or 16384 (Q8_0, Q5_0, Q5_K, Q6_K);
+ * m = 2 12288; m = 3, 4 4096.  Past k 8192 (byte codes at m = 1, every type at
+ * m = 2) and past k 2048 at m = 3, 4 (not Q6_K), k is split over the two waves of a
+ * pair.  Larger k takes the batched decode under UNILLM_PATH_AUTO. */
 #define UNILLM_PATH_GEMV 1         /* fused dequant + GEMV (VALU int8 dot), m <= 4 */
 #define UNILLM_PATH_DECODE_MFMA 2  /* batched decode, f16 MFMA, fp32 accumulate */
 #define UNILLM_PATH_PREFILL_MFMA 3 /* prefill, LDS-staged f16 MFMA (x rows scaled by powers of two), fp32 accumulate */
